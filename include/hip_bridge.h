@@ -1,0 +1,217 @@
+/*
+ * hip_bridge -- C-ABI of ziglm's fused per-layer ops on AMD Instinct MI355X (gfx950).
+ *
+ * Drop-in replacement for ziglm's src/cuda_bridge.h (reference: simonproyt/ziglm). Every
+ * entry point with a reference counterpart cites the declaration it replaces as
+ * "replaces cuda_bridge.h:LINE" (or cuda_bridge.cu:LINE / cuda.zig:LINE where the
+ * reference declares it only there). Entry points marked "new" have no counterpart: they
+ * carry the bf16-activation and fused variants and the per-row position/slot addressing.
+ *
+ * Conventions (as the reference):
+ *   - plain pointers and sizes only; the caller owns every device buffer (hip_malloc),
+ *     the bridge borrows pointers and keeps no global state on the op path;
+ *   - runtime calls return int: 0 = success, otherwise a hipError_t value;
+ *   - ops return void, are stream-ordered on `stream` (NULL = the null stream), never
+ *     allocate or synchronise (so they can be captured into a hipGraph), and return early
+ *     without launching when a size is <= 0;
+ *   - unsupported qtype / dtype / shape: no launch (the reference silently no-ops); the
+ *     reason is recorded for hip_bridge_last_error();
+ *   - in-place aliasing is allowed where the reference relies on it (noted per op).
+ * Numerics follow ziglm's CPU path (src/math.zig, src/quant.zig), not its CUDA kernels:
+ *   - gathers are bit-exact: out = (f32(q) * d) * scale, one rounding;
+ *   - RMSNorm: inv = 1/sqrt(mean + eps) (IEEE sqrt and divide), out = (x*inv)*(1+w);
+ *   - RoPE angles: theta = f32(pos)*freq_scale / D_i with D_i = f32(pow(base, f32(2i)/f32(r)))
+ *     evaluated on the host in double precision, cos/sin evaluated in double precision;
+ *   - bf16 activations: upconvert, compute in f32, round to nearest even once.
+ */
+#ifndef HIP_BRIDGE_H
+#define HIP_BRIDGE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* HipStream_t;    /* replaces CudaStream_t    (cuda_bridge.h:10) */
+typedef void* HipGraph_t;     /* replaces CudaGraph_t     (cuda_bridge.h:11) */
+typedef void* HipGraphExec_t; /* replaces CudaGraphExec_t (cuda_bridge.h:12) */
+typedef void* HipEvent_t;     /* new: event handle for stream timing */
+
+/* Activation / table element types: GGML type ids (reference types.zig:4-31). */
+#define HIP_BRIDGE_F32 0
+#define HIP_BRIDGE_F16 1
+#define HIP_BRIDGE_Q4_0 2
+#define HIP_BRIDGE_Q8_0 8
+#define HIP_BRIDGE_Q6_K 14
+#define HIP_BRIDGE_BF16 30
+
+/* hip_bridge_last_error() codes (positive values are hipError_t launch errors). */
+#define HIP_BRIDGE_OK 0
+#define HIP_BRIDGE_EINVAL (-1)       /* bad argument (NULL buffer, bad size); no launch */
+#define HIP_BRIDGE_EUNSUPPORTED (-2) /* qtype / dtype / shape not supported; no launch */
+
+/* ---------------------------------------------------------------------------------- */
+/* Device & memory management (replaces cuda_bridge.h:15-25)                          */
+/* ---------------------------------------------------------------------------------- */
+int hip_device_get_info(int device_id, char* name, size_t name_len, size_t* total_vram_bytes); /* cuda_bridge.h:15 */
+int hip_malloc(void** ptr, size_t bytes);                                            /* cuda_bridge.h:16 */
+int hip_free(void* ptr);                                                             /* cuda_bridge.h:17 */
+int hip_malloc_host(void** ptr, size_t bytes);                                       /* cuda_bridge.h:18 */
+int hip_free_host(void* ptr);                                                        /* cuda_bridge.h:19 */
+int hip_memcpy_h2d(void* dst, const void* src, size_t bytes, HipStream_t stream);    /* cuda_bridge.h:20 */
+int hip_memcpy_d2h(void* dst, const void* src, size_t bytes, HipStream_t stream);    /* cuda_bridge.h:21 */
+int hip_memcpy_d2d(void* dst, const void* src, size_t bytes, HipStream_t stream);    /* cuda_bridge.h:22 */
+int hip_stream_create(HipStream_t* stream);                                          /* cuda_bridge.h:23 */
+int hip_stream_destroy(HipStream_t stream);                                          /* cuda_bridge.h:24 */
+int hip_stream_sync(HipStream_t stream);                                             /* cuda_bridge.h:25 */
+
+/* ---------------------------------------------------------------------------------- */
+/* Graph management (replaces cuda_bridge.h:28-33)                                    */
+/* ---------------------------------------------------------------------------------- */
+int hip_graph_begin_capture(HipStream_t stream);                      /* cuda_bridge.h:28 */
+int hip_graph_end_capture(HipStream_t stream, HipGraph_t* graph_out); /* cuda_bridge.h:29 */
+int hip_graph_instantiate(HipGraphExec_t* exec_out, HipGraph_t graph);/* cuda_bridge.h:30 */
+int hip_graph_launch(HipGraphExec_t exec, HipStream_t stream);        /* cuda_bridge.h:31 */
+int hip_graph_destroy(HipGraph_t graph);                              /* cuda_bridge.h:32 */
+int hip_graph_exec_destroy(HipGraphExec_t exec);                      /* cuda_bridge.h:33 */
+
+/* ---------------------------------------------------------------------------------- */
+/* New runtime helpers: events (timing), fill, error reporting                         */
+/* ---------------------------------------------------------------------------------- */
+int hip_event_create(HipEvent_t* event);
+int hip_event_destroy(HipEvent_t event);
+int hip_event_record(HipEvent_t event, HipStream_t stream);
+int hip_event_sync(HipEvent_t event);
+int hip_event_elapsed_ms(float* ms, HipEvent_t start, HipEvent_t stop);
+/* Byte fill by a kernel (not hipMemsetAsync, so it is safe inside a captured graph). */
+int hip_fill_u8(void* ptr, unsigned char value, size_t bytes, HipStream_t stream);
+/* Last recorded op error on this host thread (HIP_BRIDGE_* or hipError_t); reading it
+ * clears it. */
+int hip_bridge_last_error(void);
+const char* hip_bridge_error_string(int code);
+/* Build identification string (architecture, compile flags). */
+const char* hip_bridge_version(void);
+
+/* ---------------------------------------------------------------------------------- */
+/* Embedding gather + dequant + scale (replaces cuda_bridge.h:53-54)                    */
+/* qtype in {F32, F16, Q4_0, Q8_0, Q6_K, BF16}; row r of the table starts at           */
+/* r * row_bytes(qtype, dim). out[t][i] = dequant(table[ids[t]])[i] * scale, bit-exact  */
+/* to quant.zig + model.zig:494-503.                                                   */
+/* ---------------------------------------------------------------------------------- */
+void hip_embed_lookup(const void* emb_weights, int qtype, int token_id, float* out, int dim,
+                      float scale, HipStream_t stream);                      /* cuda_bridge.h:53 */
+void hip_embed_lookup_batch(const void* emb_weights, int qtype, const int* token_ids, float* out,
+                            int n_tokens, int dim, float scale, HipStream_t stream); /* cuda_bridge.h:54 */
+/* new: 64-bit sizes, bounds-checked ids (ids outside [0, n_rows) give a zero row),
+ * f32 or bf16 output (out_dtype). */
+void hip_embed_gather(const void* table, int qtype, int64_t n_rows, const int32_t* ids,
+                      int out_dtype, void* out, int64_t n_tokens, int dim, float scale,
+                      HipStream_t stream);
+
+/* ---------------------------------------------------------------------------------- */
+/* RMSNorm family, f32 (replaces cuda_bridge.h:55-58, cuda_bridge.cu:2058)             */
+/* weight may be NULL (scale 1, reference's no-scale norm); use_unit_offset: (1+w).     */
+/* ---------------------------------------------------------------------------------- */
+void hip_rmsnorm(const float* x, const float* weight, float* out, int n, float eps,
+                 int use_unit_offset, HipStream_t stream);                   /* cuda_bridge.h:55 */
+/* count rows of head_dim; weight shared by all rows; x == out allowed. */
+void hip_rmsnorm_batched(float* x, const float* weight, float* out, int head_dim, int count,
+                         float eps, int use_unit_offset, HipStream_t stream); /* cuda_bridge.h:56 */
+/* x += residual (written back), out = norm(x); out may alias residual. */
+void hip_add_rmsnorm(float* x, const float* residual, const float* weight, float* out, int n,
+                     float eps, int use_unit_offset, HipStream_t stream);     /* cuda_bridge.h:57 */
+void hip_add_rmsnorm_batched(float* x, const float* residual, const float* weight, float* out,
+                             int n, int batch_size, float eps, int use_unit_offset,
+                             HipStream_t stream);                            /* cuda_bridge.h:58 */
+/* x += norm(in). */
+void hip_rmsnorm_add(float* x, const float* in, const float* weight, int n, float eps,
+                     int use_unit_offset, HipStream_t stream); /* cuda_bridge.cu:2058, cuda.zig:49 */
+
+/* new: dtype-generic row variants (dtype HIP_BRIDGE_F32 or HIP_BRIDGE_BF16 for x, residual,
+ * out; weights always f32), `rows` rows of n. Semantics as the f32 ops above. */
+void hip_rmsnorm_rows(int dtype, const void* x, const float* weight, void* out, int64_t rows,
+                      int n, float eps, int use_unit_offset, HipStream_t stream);
+void hip_add_rmsnorm_rows(int dtype, void* x, const void* residual, const float* weight,
+                          void* out, int64_t rows, int n, float eps, int use_unit_offset,
+                          HipStream_t stream);
+void hip_rmsnorm_add_rows(int dtype, void* x, const void* in, const float* weight,
+                          int64_t rows, int n, float eps, int use_unit_offset,
+                          HipStream_t stream);
+/* new, fused: xb' = norm(xb; w1); x += xb'; out = norm(x; w2). This is the reference's
+ * post-attention norm + addRmsNorm pair (cuda_model.zig:930-942) and also the post-FFN
+ * rmsnormAdd followed by the next layer's input norm (cuda_model.zig:962-967, 840-845).
+ * out may alias xb. */
+void hip_rmsnorm_add_rmsnorm(int dtype, void* x, const void* xb, const float* w1,
+                             const float* w2, void* out, int64_t rows, int n, float eps,
+                             int use_unit_offset, HipStream_t stream);
+
+/* ---------------------------------------------------------------------------------- */
+/* RoPE, half-split (ziglm RoPEType.normal), f32, in place (replaces cuda_bridge.h:59-61) */
+/* q or k may be NULL. rotary_dim 0 or > head_dim means head_dim.                       */
+/* ---------------------------------------------------------------------------------- */
+void hip_rope(float* q, float* k, int pos, int num_heads, int num_kv_heads, int head_dim,
+              int rotary_dim, float freq_base, HipStream_t stream);          /* cuda_bridge.h:59 */
+void hip_rope_ind(float* q, float* k, const int* d_pos, int num_heads, int num_kv_heads,
+                  int head_dim, int rotary_dim, float freq_base, HipStream_t stream); /* cuda_bridge.h:60 */
+/* token b of batch_size at position pos + b */
+void hip_rope_batched(float* q, float* k, int pos, int batch_size, int num_heads,
+                      int num_kv_heads, int head_dim, int rotary_dim, float freq_base,
+                      HipStream_t stream);                                   /* cuda_bridge.h:61 */
+
+/* ---------------------------------------------------------------------------------- */
+/* KV-cache append, f32, cache layout [layer][max_seq][max_kv_dim] (cuda_bridge.h:71-112) */
+/* Rows with pos outside [0, max_seq) are skipped.                                      */
+/* ---------------------------------------------------------------------------------- */
+void hip_kv_cache_put(float* k_cache, float* v_cache, const float* k, const float* v,
+                      int layer_idx, int pos, int max_seq, int n_kv_heads, int head_dim,
+                      int max_kv_dim, HipStream_t stream);                    /* cuda_bridge.h:71-83 */
+void hip_kv_cache_put_ind(float* k_cache, float* v_cache, const float* k, const float* v,
+                          int layer_idx, const int* d_pos, int max_seq, int n_kv_heads,
+                          int head_dim, int max_kv_dim, HipStream_t stream);  /* cuda_bridge.h:85-97 */
+void hip_kv_cache_put_batched(float* k_cache, float* v_cache, const float* k, const float* v,
+                              int layer_idx, int pos, int batch_size, int max_seq,
+                              int n_kv_heads, int head_dim, int max_kv_dim,
+                              HipStream_t stream);                           /* cuda_bridge.h:99-112 */
+
+/* ---------------------------------------------------------------------------------- */
+/* new, fused attention prologue: per-head Q RMSNorm -> RoPE -> Q written in place;     */
+/* per-head K RMSNorm -> RoPE -> written to the K cache; V (optionally Gemma-4 no-scale */
+/* norm, v_norm=1) -> written to the V cache. Replaces the reference sequence           */
+/* rmsNormBatched(Q), rmsNormBatched(K), [rmsNormBatched(V, NULL)], rope(K),            */
+/* kvCachePut, rope(Q) (cuda_model.zig:643-662, 901-920, 1268-1327) with one launch.    */
+/*   q: [n_tokens][num_heads][head_dim], k, v: [n_tokens][num_kv_heads][head_dim],      */
+/*   dtype HIP_BRIDGE_F32 or HIP_BRIDGE_BF16 (activations and caches);                  */
+/*   q_norm_w / k_norm_w: f32[head_dim] or NULL (no norm); q may be NULL (K/V only);     */
+/*   position of token t: d_pos ? d_pos[t] : pos_base + t;                              */
+/*   cache row of token t: d_slot ? d_slot[t] : layer_idx*max_seq + position;           */
+/*   rows outside [0, cache_rows) are not written; element (t, h, j) of K goes to        */
+/*   k_cache[row*max_kv_dim + h*head_dim + j].                                          */
+/* ---------------------------------------------------------------------------------- */
+void hip_qk_norm_rope_kv(int dtype, void* q, const void* k, const void* v,
+                         const float* q_norm_w, const float* k_norm_w, int v_norm,
+                         void* k_cache, void* v_cache, int64_t cache_rows, int layer_idx,
+                         int max_seq, int max_kv_dim, const int32_t* d_pos, int pos_base,
+                         const int64_t* d_slot, int n_tokens, int num_heads, int num_kv_heads,
+                         int head_dim, int rotary_dim, float freq_base, float freq_scale,
+                         float eps, int use_unit_offset, HipStream_t stream);
+
+/* ---------------------------------------------------------------------------------- */
+/* Activations & elementwise (replaces cuda_bridge.h:64, 66-68)                         */
+/* ---------------------------------------------------------------------------------- */
+/* out = gelu_tanh(gate) * up; out may alias gate or up. */
+void hip_geglu(const float* gate, const float* up, float* out, int n, HipStream_t stream); /* cuda_bridge.h:64 */
+void hip_add(float* x, const float* residual, int n, HipStream_t stream);              /* cuda_bridge.h:66 */
+void hip_scale(float* x, float scale, int n, HipStream_t stream);                      /* cuda_bridge.h:67 */
+/* x = cap * tanh(x / cap), in place. */
+void hip_tanh_softcap(float* x, float cap, int n, HipStream_t stream);                 /* cuda_bridge.h:68 */
+/* new: dtype-generic, 64-bit sizes. */
+void hip_geglu_ex(int dtype, const void* gate, const void* up, void* out, int64_t n,
+                  HipStream_t stream);
+void hip_tanh_softcap_ex(int dtype, void* x, float cap, int64_t n, HipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* HIP_BRIDGE_H */

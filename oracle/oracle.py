@@ -1,0 +1,277 @@
+"""ctypes front end of the CPU oracle (oracle/ziglm_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg, never by the product package. Arrays are numpy; bf16 tensors are
+numpy uint16 bit patterns.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+
+F32, F16, Q4_0, Q8_0, Q6_K, BF16 = 0, 1, 2, 8, 14, 30
+
+_fp = ctypes.POINTER(ctypes.c_float)
+_u16p = ctypes.POINTER(ctypes.c_uint16)
+_u8p = ctypes.POINTER(ctypes.c_uint8)
+_i32p = ctypes.POINTER(ctypes.c_int32)
+_i64p = ctypes.POINTER(ctypes.c_int64)
+_vp = ctypes.c_void_p
+_sz = ctypes.c_size_t
+_f = ctypes.c_float
+_i = ctypes.c_int
+
+_SIGS = {
+    "zo_f16_to_f32": (ctypes.c_float, [ctypes.c_uint16]),
+    "zo_bf16_to_f32": (ctypes.c_float, [ctypes.c_uint16]),
+    "zo_f32_to_bf16": (ctypes.c_uint16, [ctypes.c_float]),
+    "zo_bf16_to_f32_n": (None, [_u16p, _fp, _sz]),
+    "zo_f32_to_bf16_n": (None, [_fp, _u16p, _sz]),
+    "zo_row_bytes": (_sz, [_i, _sz]),
+    "zo_dequantize_row": (_i, [_i, _u8p, _fp, _sz]),
+    "zo_embed_gather": (_i, [_u8p, _i, _i32p, _sz, _sz, _f, _fp]),
+    "zo_rms_norm": (None, [_fp, _fp, _fp, _sz, _f, _i]),
+    "zo_rms_norm_no_scale": (None, [_fp, _fp, _sz, _f]),
+    "zo_add": (None, [_fp, _fp, _sz]),
+    "zo_add_rms_norm": (None, [_fp, _fp, _fp, _fp, _sz, _f, _i]),
+    "zo_rms_norm_add": (None, [_fp, _fp, _fp, _sz, _f, _i]),
+    "zo_rope_denominator": (ctypes.c_float, [_f, _sz, _sz]),
+    "zo_rope_cos_sin": (None, [_f, _f, _fp, _fp]),
+    "zo_apply_rope": (None, [_fp, _fp, _sz, _sz, _sz, _sz, _sz, _f, _f, _i]),
+    "zo_kv_cache_put": (None, [_fp, _fp, _fp, _fp, _sz, _sz, _sz, _sz, _sz, _sz]),
+    "zo_qk_norm_rope_kv_token": (
+        None, [_fp, _fp, _fp, _fp, _fp, _i, _sz, _sz, _sz, _sz, _sz, _f, _f, _f, _i]),
+    "zo_expm1f": (ctypes.c_float, [_f]),
+    "zo_tanhf": (ctypes.c_float, [_f]),
+    "zo_gelu": (ctypes.c_float, [_f]),
+    "zo_geglu": (None, [_fp, _fp, _fp, _sz]),
+    "zo_softcap": (None, [_fp, _f, _sz]),
+    "zo_add_rms_norm_bf16": (None, [_u16p, _u16p, _fp, _u16p, _sz, _sz, _f, _i]),
+    "zo_rms_norm_bf16": (None, [_u16p, _fp, _u16p, _sz, _sz, _f, _i]),
+    "zo_rms_norm_add_rms_norm_bf16": (None, [_u16p, _u16p, _fp, _fp, _sz, _sz, _f, _i]),
+    "zo_rms_norm_add_rms_norm": (None, [_fp, _fp, _fp, _fp, _sz, _sz, _f, _i]),
+    "zo_geglu_bf16": (None, [_u16p, _u16p, _u16p, _sz]),
+    "zo_qk_norm_rope_kv": (
+        None,
+        [_i, _vp, _vp, _vp, _fp, _fp, _i, _vp, _vp, _sz, _sz, _sz, _i32p, ctypes.c_int64, _i64p,
+         _sz, _sz, _sz, _sz, _sz, _f, _f, _f, _i]),
+}
+
+
+class Oracle:
+    """Typed handle on one build of the oracle library."""
+
+    def __init__(self, simd=False):
+        name = "liboracle_simd.so" if simd else "liboracle.so"
+        path = os.path.join(_HERE, name)
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} missing: run `make -C oracle` (or __graft_entry__.build())")
+        self.lib = ctypes.CDLL(path)
+        for fn, (res, args) in _SIGS.items():
+            f = getattr(self.lib, fn)
+            f.restype = res
+            f.argtypes = args
+
+    # -- pointer helpers -------------------------------------------------------------
+    @staticmethod
+    def _p(a, ptype):
+        if a is None:
+            return None
+        assert a.flags["C_CONTIGUOUS"], "oracle arrays must be C-contiguous"
+        return a.ctypes.data_as(ptype)
+
+    def fp(self, a):
+        if a is not None:
+            assert a.dtype == np.float32
+        return self._p(a, _fp)
+
+    def u16(self, a):
+        if a is not None:
+            assert a.dtype == np.uint16
+        return self._p(a, _u16p)
+
+    # -- ops -------------------------------------------------------------------------
+    def f32_to_bf16(self, x):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        out = np.empty(x.shape, np.uint16)
+        self.lib.zo_f32_to_bf16_n(self.fp(x), self.u16(out), x.size)
+        return out
+
+    def bf16_to_f32(self, u):
+        u = np.ascontiguousarray(u, dtype=np.uint16)
+        out = np.empty(u.shape, np.float32)
+        self.lib.zo_bf16_to_f32_n(self.u16(u), self.fp(out), u.size)
+        return out
+
+    def row_bytes(self, qtype, n):
+        return self.lib.zo_row_bytes(qtype, n)
+
+    def dequantize_row(self, qtype, row, n):
+        row = np.ascontiguousarray(row, dtype=np.uint8)
+        out = np.empty(n, np.float32)
+        rc = self.lib.zo_dequantize_row(qtype, self._p(row, _u8p), self.fp(out), n)
+        if rc != 0:
+            raise ValueError(f"unsupported qtype {qtype}")
+        return out
+
+    def embed_gather(self, table, qtype, ids, dim, scale):
+        table = np.ascontiguousarray(table, dtype=np.uint8)
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        out = np.empty((ids.size, dim), np.float32)
+        rc = self.lib.zo_embed_gather(self._p(table, _u8p), qtype, self._p(ids, _i32p), ids.size,
+                                      dim, scale, self.fp(out))
+        if rc != 0:
+            raise ValueError(f"unsupported qtype {qtype}")
+        return out
+
+    def rms_norm(self, x, w, eps, unit_offset=True):
+        """Row-wise math.rmsNorm over the last axis (w=None -> rmsNormNoScale)."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        n = x.shape[-1]
+        out = np.empty_like(x)
+        xr, orr = x.reshape(-1, n), out.reshape(-1, n)
+        for r in range(xr.shape[0]):
+            if w is None:
+                self.lib.zo_rms_norm_no_scale(self.fp(xr[r]), self.fp(orr[r]), n, eps)
+            else:
+                self.lib.zo_rms_norm(self.fp(xr[r]), self.fp(w), self.fp(orr[r]), n, eps,
+                                     int(unit_offset))
+        return out
+
+    def add_rms_norm(self, x, r, w, eps, unit_offset=True):
+        """Returns (x + r, rmsNorm(x + r)) row-wise (model.zig:714-723)."""
+        x = np.array(x, dtype=np.float32, copy=True, order="C")
+        r = np.ascontiguousarray(r, dtype=np.float32)
+        n = x.shape[-1]
+        out = np.empty_like(x)
+        xr, rr, orr = x.reshape(-1, n), r.reshape(-1, n), out.reshape(-1, n)
+        for i in range(xr.shape[0]):
+            self.lib.zo_add_rms_norm(self.fp(xr[i]), self.fp(rr[i]), self.fp(w), self.fp(orr[i]),
+                                     n, eps, int(unit_offset))
+        return x, out
+
+    def rms_norm_add(self, x, inp, w, eps, unit_offset=True):
+        """Returns x + rmsNorm(inp) row-wise (model.zig:748-755)."""
+        x = np.array(x, dtype=np.float32, copy=True, order="C")
+        inp = np.ascontiguousarray(inp, dtype=np.float32)
+        n = x.shape[-1]
+        xr, ir = x.reshape(-1, n), inp.reshape(-1, n)
+        for i in range(xr.shape[0]):
+            self.lib.zo_rms_norm_add(self.fp(xr[i]), self.fp(ir[i]), self.fp(w), n, eps,
+                                     int(unit_offset))
+        return x
+
+    def rms_norm_add_rms_norm(self, x, xb, w1, w2, eps, unit_offset=True):
+        """Returns (x + norm1(xb), norm2(x + norm1(xb))) row-wise; f32 or bf16 (uint16)."""
+        n = x.shape[-1]
+        rows = x.size // n
+        if x.dtype == np.uint16:
+            x = np.array(x, copy=True, order="C")
+            xb = np.array(xb, copy=True, order="C")
+            self.lib.zo_rms_norm_add_rms_norm_bf16(self.u16(x), self.u16(xb), self.fp(w1),
+                                                   self.fp(w2), rows, n, eps, int(unit_offset))
+        else:
+            x = np.array(x, dtype=np.float32, copy=True, order="C")
+            xb = np.array(xb, dtype=np.float32, copy=True, order="C")
+            self.lib.zo_rms_norm_add_rms_norm(self.fp(x), self.fp(xb), self.fp(w1), self.fp(w2),
+                                              rows, n, eps, int(unit_offset))
+        return x, xb
+
+    def add_rms_norm_bf16(self, x, r, w, eps, unit_offset=True):
+        x = np.array(x, dtype=np.uint16, copy=True, order="C")
+        r = np.ascontiguousarray(r, dtype=np.uint16)
+        n = x.shape[-1]
+        out = np.empty_like(x)
+        self.lib.zo_add_rms_norm_bf16(self.u16(x), self.u16(r), self.fp(w), self.u16(out),
+                                      x.size // n, n, eps, int(unit_offset))
+        return x, out
+
+    def rms_norm_bf16(self, x, w, eps, unit_offset=True):
+        x = np.ascontiguousarray(x, dtype=np.uint16)
+        n = x.shape[-1]
+        out = np.empty_like(x)
+        self.lib.zo_rms_norm_bf16(self.u16(x), self.fp(w), self.u16(out), x.size // n, n, eps,
+                                  int(unit_offset))
+        return out
+
+    def rope_denominator(self, base, i, eff):
+        return self.lib.zo_rope_denominator(base, i, eff)
+
+    def rope_cos_sin(self, pos_f, denom):
+        c, s = ctypes.c_float(), ctypes.c_float()
+        self.lib.zo_rope_cos_sin(pos_f, denom, ctypes.byref(c), ctypes.byref(s))
+        return c.value, s.value
+
+    def apply_rope(self, q, k, pos, head_size, rotary_dim, n_heads, n_kv_heads, base,
+                   freq_scale=1.0, neox=False):
+        q = None if q is None else np.array(q, dtype=np.float32, copy=True, order="C")
+        k = None if k is None else np.array(k, dtype=np.float32, copy=True, order="C")
+        self.lib.zo_apply_rope(self.fp(q), self.fp(k), pos, head_size, rotary_dim, n_heads,
+                               n_kv_heads, base, freq_scale, int(neox))
+        return q, k
+
+    def kv_cache_put(self, k_cache, v_cache, k, v, layer, pos, max_seq, n_kv, hd, max_kv_dim):
+        self.lib.zo_kv_cache_put(self.fp(k_cache), self.fp(v_cache), self.fp(k), self.fp(v),
+                                 layer, pos, max_seq, n_kv, hd, max_kv_dim)
+
+    def qk_norm_rope_kv(self, q, k, v, wq, wk, k_cache, v_cache, *, v_norm=False, layer=0,
+                        max_seq, max_kv_dim, pos=None, pos_base=0, slots=None, n_heads,
+                        n_kv_heads, head_dim, rotary_dim=0, base=10000.0, freq_scale=1.0,
+                        eps=1e-6, unit_offset=True):
+        """Token-batched fused op; returns the new q. k_cache/v_cache are updated in place."""
+        dtype = 1 if q.dtype == np.uint16 else 0
+        q = np.array(q, copy=True, order="C")
+        k = np.ascontiguousarray(k)
+        v = np.ascontiguousarray(v)
+        n_tokens = q.size // (n_heads * head_dim)
+        pos_a = None if pos is None else np.ascontiguousarray(pos, dtype=np.int32)
+        slot_a = None if slots is None else np.ascontiguousarray(slots, dtype=np.int64)
+        self.lib.zo_qk_norm_rope_kv(
+            dtype, q.ctypes.data, k.ctypes.data, v.ctypes.data, self.fp(wq), self.fp(wk),
+            int(v_norm), k_cache.ctypes.data, v_cache.ctypes.data, layer, max_seq, max_kv_dim,
+            self._p(pos_a, _i32p), pos_base, self._p(slot_a, _i64p), n_tokens, n_heads,
+            n_kv_heads, head_dim, rotary_dim, base, freq_scale, eps, int(unit_offset))
+        return q
+
+    def tanhf(self, x):
+        return self.lib.zo_tanhf(x)
+
+    def expm1f(self, x):
+        return self.lib.zo_expm1f(x)
+
+    def gelu(self, x):
+        return self.lib.zo_gelu(x)
+
+    def geglu(self, gate, up):
+        if gate.dtype == np.uint16:
+            g = np.ascontiguousarray(gate)
+            u = np.ascontiguousarray(up, dtype=np.uint16)
+            out = np.empty_like(g)
+            self.lib.zo_geglu_bf16(self.u16(g), self.u16(u), self.u16(out), g.size)
+            return out
+        g = np.ascontiguousarray(gate, dtype=np.float32)
+        u = np.ascontiguousarray(up, dtype=np.float32)
+        out = np.empty_like(g)
+        self.lib.zo_geglu(self.fp(g), self.fp(u), self.fp(out), g.size)
+        return out
+
+    def softcap(self, x, cap):
+        x = np.array(x, dtype=np.float32, copy=True, order="C")
+        self.lib.zo_softcap(self.fp(x), cap, x.size)
+        return x
+
+    def tanh_array(self, x):
+        """Elementwise zo_tanhf over an array (via soft-cap with cap 1, which is exact:
+        1*tanh(x/1) == tanh(x))."""
+        return self.softcap(x, 1.0)
+
+
+_cache = {}
+
+
+def get(simd=False):
+    if simd not in _cache:
+        _cache[simd] = Oracle(simd)
+    return _cache[simd]

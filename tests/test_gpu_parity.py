@@ -1,0 +1,427 @@
+"""GPU parity: every hip_bridge entry point against the CPU oracle on seeded inputs.
+
+All calls go through the C-ABI (ziglm_amd.device.HipDevice -> libhip_bridge.so).
+Tolerances:
+  gathers, KV copies, residual add/scale ....... bit-exact
+  f32 norm / RoPE / GeGLU / soft-cap ............ 1e-5 relative; RoPE outputs relative to
+      the norm of their rotation pair (a rotated coordinate can cancel to ~0); GeGLU adds
+      the reference's own cancellation bound in 1 + tanh(z): |x*up| * 2^-23
+  bf16 outputs .................................. 1 bf16 ulp, with the same floors
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from tol import assert_bf16, assert_bitexact, assert_rel
+from ziglm_amd import bridge as B
+from ziglm_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+SQRT = {2560: np.float32(np.sqrt(np.float32(2560))), 5376: np.float32(np.sqrt(np.float32(5376)))}
+
+
+def f16_table(seed, rows, cols):
+    return synth.f16_bits(synth.normal_f32(seed, "f16tab", (rows, cols), 0, 0.5)).view(np.uint8).reshape(rows, cols * 2)
+
+
+def f32_table(seed, rows, cols):
+    return synth.normal_f32(seed, "f32tab", (rows, cols)).view(np.uint8).reshape(rows, cols * 4)
+
+
+def q6k_table(seed, rows, cols):
+    nsb = cols // 256
+    raw = synth.uniform_int(seed, "q6k", (rows, nsb, 210), 0, 255).astype(np.uint8)
+    d = synth.f16_bits(synth.uniform_f32(seed, "q6k.d", (rows, nsb), 1e-3, 2e-2))
+    raw[:, :, 208:210] = d.reshape(rows, nsb, 1).view(np.uint8).reshape(rows, nsb, 2)
+    return raw.reshape(rows, nsb * 210)
+
+
+def make_table(qtype, seed, rows, cols):
+    return {
+        B.Q8_0: synth.q8_0_table, B.Q4_0: synth.q4_0_table, B.BF16: synth.bf16_table,
+        B.F16: f16_table, B.F32: f32_table, B.Q6_K: q6k_table,
+    }[qtype](seed, rows, cols)
+
+
+# ---------------------------------------------------------------------------------------
+# Embedding gather
+# ---------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("out_dtype", [B.F32, B.BF16])
+@pytest.mark.parametrize("qtype,dim", [(B.Q8_0, 2560), (B.Q4_0, 2560), (B.BF16, 2560), (B.F16, 2560),
+                                       (B.F32, 2560), (B.Q6_K, 2560), (B.Q8_0, 96), (B.Q4_0, 160),
+                                       (B.BF16, 2562), (B.F32, 100)])
+def test_embed_gather_bitexact(dev, oracle, qtype, dim, out_dtype):
+    vocab = 700
+    table = make_table(qtype, 2, vocab, dim)
+    ids = synth.gather_ids(2, 320, vocab, n_repeat=20)
+    bad = np.array([-1, vocab, vocab + 77, -5], np.int32)
+    all_ids = np.concatenate([ids, bad])
+    scale = np.float32(np.sqrt(np.float32(dim)))
+    ref = oracle.embed_gather(table, qtype, ids, dim, scale)
+    ref = np.concatenate([ref, np.zeros((bad.size, dim), np.float32)])
+    d_tab, d_ids = dev.from_numpy(table), dev.from_numpy(all_ids)
+    es = 4 if out_dtype == B.F32 else 2
+    d_out = dev.alloc(all_ids.size * dim * es)
+    d_out.fill(0xAB)
+    dev.embedGather(d_tab, qtype, vocab, d_ids, out_dtype, d_out, all_ids.size, dim, scale)
+    if out_dtype == B.F32:
+        got = d_out.to_numpy((all_ids.size, dim), np.float32)
+        assert_bitexact(got, ref, f"gather qtype={qtype} dim={dim}")
+    else:
+        got = d_out.to_numpy((all_ids.size, dim), np.uint16)
+        assert_bitexact(got, oracle.f32_to_bf16(ref), f"gather bf16-out qtype={qtype} dim={dim}")
+
+
+@pytest.mark.parametrize("qtype", [B.Q8_0, B.Q4_0, B.BF16, B.Q6_K])
+def test_embed_lookup_mirrors(dev, oracle, qtype):
+    vocab, dim = 300, 2560
+    table = make_table(qtype, 5, vocab, dim)
+    scale = SQRT[dim]
+    ids = np.array([0, 299, 7, 7, 150], np.int32)
+    ref = oracle.embed_gather(table, qtype, ids, dim, scale)
+    d_tab = dev.from_numpy(table)
+    d_out = dev.alloc(ids.size * dim * 4)
+    dev.embedLookupBatch(d_tab, qtype, dev.from_numpy(ids), d_out, ids.size, dim, scale)
+    assert_bitexact(d_out.to_numpy((ids.size, dim), np.float32), ref, "embedLookupBatch")
+    d_one = dev.alloc(dim * 4)
+    dev.embedLookup(d_tab, qtype, 299, d_one, dim, scale)
+    assert_bitexact(d_one.to_numpy((dim,), np.float32), ref[1], "embedLookup")
+
+
+def test_gather_unsupported_qtype_is_noop(dev):
+    d_tab = dev.alloc(1024)
+    d_ids = dev.from_numpy(np.zeros(1, np.int32))
+    d_out = dev.alloc(256 * 4)
+    d_out.fill(0x11)
+    dev.strict = False
+    try:
+        dev.embedLookupBatch(d_tab, 12, d_ids, d_out, 1, 256, 1.0)  # Q4_K: not supported
+        assert dev.b.last_error() == B.EUNSUPPORTED
+    finally:
+        dev.strict = True
+    assert np.all(d_out.to_numpy((1024,), np.uint8) == 0x11)
+
+
+# ---------------------------------------------------------------------------------------
+# RMSNorm family
+# ---------------------------------------------------------------------------------------
+
+EPS = np.float32(1e-6)
+
+
+@pytest.mark.parametrize("n", [2560, 5376, 256, 2561, 16384])
+@pytest.mark.parametrize("uo", [True, False])
+def test_rmsnorm_f32(dev, oracle, n, uo):
+    x = synth.normal_f32(0, "x", (n,))
+    w = synth.normal_f32(0, "w", (n,), 0, 0.1)
+    ref = oracle.rms_norm(x, w, EPS, uo)
+    d_x, d_w, d_o = dev.from_numpy(x), dev.from_numpy(w), dev.alloc(n * 4)
+    dev.rmsNorm(d_x, d_w, d_o, n, EPS, uo)
+    assert_rel(d_o.to_numpy((n,), np.float32), ref, 1e-5, what=f"rmsNorm n={n}")
+    dev.rmsNorm(d_x, None, d_o, n, EPS, uo)  # no weight: rmsNormNoScale
+    assert_rel(d_o.to_numpy((n,), np.float32), oracle.rms_norm(x, None, EPS), 1e-5, what="rmsNorm w=NULL")
+
+
+def test_rmsnorm_batched_inplace(dev, oracle):
+    q = synth.normal_f32(0, "q", (8, 256))
+    wq = synth.normal_f32(0, "wq", (256,), 0, 0.1)
+    d_q, d_w = dev.from_numpy(q), dev.from_numpy(wq)
+    dev.rmsNormBatched(d_q, d_w, d_q, 256, 8, EPS, True)
+    assert_rel(d_q.to_numpy((8, 256), np.float32), oracle.rms_norm(q, wq, EPS, True), 1e-5)
+
+
+@pytest.mark.parametrize("batch", [1, 64])
+def test_add_rmsnorm_out_aliases_residual(dev, oracle, batch):
+    n = 2560
+    x = synth.normal_f32(1, "x", (batch, n))
+    r = synth.normal_f32(1, "r", (batch, n))
+    w = synth.normal_f32(1, "w", (n,), 0, 0.1)
+    x_ref, out_ref = oracle.add_rms_norm(x, r, w, EPS, True)
+    d_x, d_r, d_w = dev.from_numpy(x), dev.from_numpy(r), dev.from_numpy(w)
+    if batch == 1:
+        dev.addRmsNorm(d_x, d_r, d_w, d_r, n, EPS, True)  # out = residual, as cuda_model.zig:935
+    else:
+        dev.addRmsNormBatched(d_x, d_r, d_w, d_r, n, batch, EPS, True)
+    assert_bitexact(d_x.to_numpy((batch, n), np.float32), x_ref, "x += r")
+    assert_rel(d_r.to_numpy((batch, n), np.float32), out_ref, 1e-5, what="norm(x+r)")
+
+
+def test_rmsnorm_add(dev, oracle):
+    n = 2560
+    x = synth.normal_f32(2, "x", (n,))
+    inp = synth.normal_f32(2, "in", (n,))
+    w = synth.normal_f32(2, "w", (n,), 0, 0.1)
+    ref = oracle.rms_norm_add(x, inp, w, EPS, True)
+    d_x = dev.from_numpy(x)
+    dev.rmsnormAdd(d_x, dev.from_numpy(inp), dev.from_numpy(w), n, EPS, True)
+    # x + norm(in): relative to the larger of the two summands (the sum can cancel)
+    floor = 1e-5 * np.abs(x)
+    assert_rel(d_x.to_numpy((n,), np.float32), ref, 1e-5, floor=floor, what="rmsnormAdd")
+
+
+@pytest.mark.parametrize("n,rows", [(2560, 64), (5376, 16), (2568, 8), (12000, 4)])
+def test_bf16_rows(dev, oracle, n, rows):
+    x = synth.normal_bf16(3, "x", (rows, n))
+    r = synth.normal_bf16(3, "r", (rows, n))
+    w = synth.normal_f32(3, "w", (n,), 0, 0.1)
+    x_ref, out_ref = oracle.add_rms_norm_bf16(x, r, w, EPS, True)
+    d_x, d_r, d_w, d_o = dev.from_numpy(x), dev.from_numpy(r), dev.from_numpy(w), dev.alloc(x.nbytes)
+    dev.addRmsNormRows(B.BF16, d_x, d_r, d_w, d_o, rows, n, EPS, True)
+    assert_bitexact(d_x.to_numpy(x.shape, np.uint16), x_ref, "bf16 x+r")
+    assert_bf16(d_o.to_numpy(x.shape, np.uint16), out_ref, 1, what="bf16 add+norm")
+    # plain norm rows
+    d_o2 = dev.alloc(x.nbytes)
+    dev.rmsNormRows(B.BF16, dev.from_numpy(x), d_w, d_o2, rows, n, EPS, True)
+    assert_bf16(d_o2.to_numpy(x.shape, np.uint16), oracle.rms_norm_bf16(x, w, EPS, True), 1, what="bf16 norm")
+
+
+@pytest.mark.parametrize("dtype,n,rows", [(B.F32, 2560, 8), (B.BF16, 2560, 64), (B.BF16, 5376, 8),
+                                          (B.F32, 2561, 3)])
+def test_rmsnorm_add_rmsnorm(dev, oracle, dtype, n, rows):
+    if dtype == B.F32:
+        x = synth.normal_f32(4, "x", (rows, n))
+        xb = synth.normal_f32(4, "xb", (rows, n))
+    else:
+        x = synth.normal_bf16(4, "x", (rows, n))
+        xb = synth.normal_bf16(4, "xb", (rows, n))
+    w1 = synth.normal_f32(4, "w1", (n,), 0, 0.1)
+    w2 = synth.normal_f32(4, "w2", (n,), 0, 0.1)
+    x_ref, out_ref = oracle.rms_norm_add_rms_norm(x, xb, w1, w2, EPS, True)
+    d_x, d_xb = dev.from_numpy(x), dev.from_numpy(xb)
+    dev.rmsNormAddRmsNorm(dtype, d_x, d_xb, dev.from_numpy(w1), dev.from_numpy(w2), d_xb, rows, n, EPS, True)
+    gx, go = d_x.to_numpy(x.shape, x.dtype), d_xb.to_numpy(x.shape, x.dtype)
+    # s = x + a, a = norm1(xb): an ulp-level difference in a moves s by ~1e-7*|a| even where
+    # the sum cancels, so s is checked relative to its summands, and norm2(s) = s*inv2*(1+w2)
+    # relative to (|x| + |a|)*inv2*|1+w2|.
+    f = O.get().bf16_to_f32
+    xf = (x if dtype == B.F32 else f(x)).astype(np.float64)
+    a = oracle.rms_norm(xb if dtype == B.F32 else f(xb), w1, EPS, True).astype(np.float64)
+    s = xf + a
+    inv2 = 1.0 / np.sqrt(np.mean(s * s, axis=-1, keepdims=True) + float(EPS))
+    floor_x = 1e-5 * (np.abs(xf) + np.abs(a))
+    floor_o = 1e-5 * (np.abs(xf) + np.abs(a)) * inv2 * np.abs(1.0 + w2.astype(np.float64))
+    if dtype == B.F32:
+        assert_rel(gx, x_ref, 1e-5, floor=floor_x, what="x + norm1(xb)")
+        assert_rel(go, out_ref, 1e-5, floor=floor_o, what="norm2(x)")
+    else:
+        assert_bf16(gx, x_ref, 1, floor=floor_x, what="bf16 x + norm1(xb)")
+        assert_bf16(go, out_ref, 1, floor=floor_o, what="bf16 norm2(x)")
+
+
+# ---------------------------------------------------------------------------------------
+# QK-norm + RoPE + KV append
+# ---------------------------------------------------------------------------------------
+
+def pair_floor(ref, D, rot, rtol=1e-5):
+    """rtol * |(r_i, r_{i+half})| for rotated coordinates, 0 elsewhere; ref [..., D]."""
+    r = np.asarray(ref, np.float64)
+    eff = D if (rot == 0 or rot > D) else rot
+    h = eff // 2
+    f = np.zeros_like(r)
+    pn = np.sqrt(r[..., :h] ** 2 + r[..., h:2 * h] ** 2)
+    f[..., :h] = rtol * pn
+    f[..., h:2 * h] = rtol * pn
+    return f
+
+
+def qk_case(dev, oracle, dtype, T, nh, nkv, D, rot, base, positions, slots=None, v_norm=False,
+            max_seq=4096, use_pos_array=True, layer=0, seed=7):
+    gen = synth.normal_bf16 if dtype == B.BF16 else synth.normal_f32
+    q = gen(seed, "q", (T, nh, D))
+    k = gen(seed, "k", (T, nkv, D))
+    v = gen(seed, "v", (T, nkv, D))
+    wq = synth.normal_f32(seed, "wq", (D,), 0, 0.1)
+    wk = synth.normal_f32(seed, "wk", (D,), 0, 0.1)
+    max_kv_dim = nkv * D
+    n_layers = layer + 1
+    cache_rows = n_layers * max_seq if slots is None else int(np.max(slots)) + 1
+    cdt = np.uint16 if dtype == B.BF16 else np.float32
+    kc = np.zeros((cache_rows, max_kv_dim), cdt)
+    vc = np.zeros((cache_rows, max_kv_dim), cdt)
+    pos = np.asarray(positions, np.int32)
+    q_ref = oracle.qk_norm_rope_kv(q, k, v, wq, wk, kc, vc, v_norm=v_norm, layer=layer,
+                                   max_seq=max_seq, max_kv_dim=max_kv_dim, pos=pos,
+                                   slots=slots, n_heads=nh, n_kv_heads=nkv, head_dim=D,
+                                   rotary_dim=rot, base=base, eps=EPS)
+    d_q, d_k, d_v = dev.from_numpy(q), dev.from_numpy(k), dev.from_numpy(v)
+    d_kc, d_vc = dev.alloc(kc.nbytes), dev.alloc(vc.nbytes)
+    d_kc.fill(0)
+    d_vc.fill(0)
+    d_pos = dev.from_numpy(pos) if use_pos_array else None
+    d_slot = dev.from_numpy(np.asarray(slots, np.int64)) if slots is not None else None
+    pos_base = int(pos[0]) if not use_pos_array else 0
+    dev.qkNormRopeKv(dtype, d_q, d_k, d_v, dev.from_numpy(wq), dev.from_numpy(wk), v_norm, d_kc, d_vc,
+                     cache_rows, layer, max_seq, max_kv_dim, d_pos, pos_base, d_slot, T, nh, nkv, D,
+                     rot, base, 1.0, EPS, True)
+    gq = d_q.to_numpy(q.shape, cdt)
+    gk = d_kc.to_numpy(kc.shape, cdt)
+    gv = d_vc.to_numpy(vc.shape, cdt)
+    kref = kc.reshape(cache_rows, nkv, D)
+    if dtype == B.F32:
+        assert_rel(gq, q_ref, 1e-5, floor=pair_floor(q_ref, D, rot), what="Q norm+rope")
+        assert_rel(gk.reshape(cache_rows, nkv, D), kref, 1e-5, floor=pair_floor(kref, D, rot), what="K cache")
+        assert_rel(gv, vc, 1e-5, what="V cache")
+        if not v_norm:
+            assert_bitexact(gv, vc, "V cache copy")
+    else:
+        f = O.get().bf16_to_f32
+        assert_bf16(gq, q_ref, 1, floor=pair_floor(f(q_ref), D, rot), what="bf16 Q")
+        assert_bf16(gk.reshape(cache_rows, nkv, D), kref, 1, floor=pair_floor(f(kref), D, rot), what="bf16 K cache")
+        if v_norm:
+            assert_bf16(gv, vc, 1, what="bf16 V cache")
+        else:
+            assert_bitexact(gv, vc, "bf16 V cache copy")
+
+
+def test_qk_c1_decode_f32(dev, oracle):
+    qk_case(dev, oracle, B.F32, 1, 8, 4, 256, 0, 10000.0, [1234])
+
+
+def test_qk_c1_decode_f32_by_value_pos(dev, oracle):
+    qk_case(dev, oracle, B.F32, 1, 8, 4, 256, 0, 10000.0, [1234], use_pos_array=False)
+
+
+def test_qk_prefill_bf16_d256(dev, oracle):
+    qk_case(dev, oracle, B.BF16, 64, 8, 4, 256, 0, 10000.0, np.arange(1000, 1064), max_seq=4096)
+
+
+@pytest.mark.parametrize("base", [10000.0, 1e6])
+def test_qk_prefill_bf16_d128(dev, oracle, base):
+    qk_case(dev, oracle, B.BF16, 24, 32, 16, 128, 0, base, np.arange(8000, 8024), max_seq=8192, layer=1)
+
+
+def test_qk_batched_decode_slots_f32(dev, oracle):
+    B_ = 8
+    pos = synth.uniform_int(4, "pos", (B_,), 0, 32767).astype(np.int32)
+    slots = np.arange(B_, dtype=np.int64) * 32768 + pos
+    qk_case(dev, oracle, B.F32, B_, 8, 4, 256, 0, 10000.0, pos, slots=slots, max_seq=32768)
+
+
+def test_qk_v_norm_d64(dev, oracle):
+    qk_case(dev, oracle, B.F32, 5, 4, 2, 64, 0, 10000.0, np.arange(5), v_norm=True)
+
+
+@pytest.mark.parametrize("D,rot", [(256, 128), (512, 128), (96, 0)])
+def test_qk_generic_path(dev, oracle, D, rot):
+    qk_case(dev, oracle, B.F32, 3, 4, 2, D, rot, 1e6, [3, 900, 4095])
+    qk_case(dev, oracle, B.BF16, 3, 4, 2, D, rot, 1e6, [3, 900, 4095])
+
+
+def test_rope_mirrors(dev, oracle):
+    nh, nkv, D = 8, 4, 256
+    q = synth.normal_f32(9, "q", (nh, D))
+    k = synth.normal_f32(9, "k", (nkv, D))
+    qr, kr = oracle.apply_rope(q, k, 1234, D, 0, nh, nkv, 10000.0)
+    d_q, d_k = dev.from_numpy(q), dev.from_numpy(k)
+    dev.rope(None, d_k, 1234, 0, nkv, D, 0, 10000.0)  # K first, as cuda_model.zig:658
+    dev.rope(d_q, None, 1234, nh, 0, D, 0, 10000.0)
+    assert_rel(d_q.to_numpy(q.shape, np.float32), qr, 1e-5, floor=pair_floor(qr, D, 0))
+    assert_rel(d_k.to_numpy(k.shape, np.float32), kr, 1e-5, floor=pair_floor(kr, D, 0))
+    # device-side position
+    d_q2 = dev.from_numpy(q)
+    dev.ropeInd(d_q2, None, dev.from_numpy(np.array([1234], np.int32)), nh, 0, D, 0, 10000.0)
+    assert_rel(d_q2.to_numpy(q.shape, np.float32), qr, 1e-5, floor=pair_floor(qr, D, 0))
+    # batched: token b at pos + b
+    Bt = 5
+    qb = synth.normal_f32(9, "qb", (Bt, nh, D))
+    d_qb = dev.from_numpy(qb)
+    dev.ropeBatched(d_qb, None, 100, Bt, nh, 0, D, 0, 10000.0)
+    ref = np.stack([oracle.apply_rope(qb[b], None, 100 + b, D, 0, nh, 0, 10000.0)[0] for b in range(Bt)])
+    assert_rel(d_qb.to_numpy(qb.shape, np.float32), ref, 1e-5, floor=pair_floor(ref, D, 0))
+
+
+def test_kv_cache_put_mirrors(dev, oracle):
+    nkv, D, max_seq, layers = 4, 256, 64, 3
+    max_kv_dim = nkv * D + 64  # padded rows, as the reference's max_kv_dim allows
+    kc = np.zeros((layers * max_seq, max_kv_dim), np.float32)
+    vc = np.zeros_like(kc)
+    d_kc, d_vc = dev.alloc(kc.nbytes), dev.alloc(vc.nbytes)
+    d_kc.fill(0)
+    d_vc.fill(0)
+    k = synth.normal_f32(10, "k", (6, nkv, D))
+    v = synth.normal_f32(10, "v", (6, nkv, D))
+    d_k, d_v = dev.from_numpy(k), dev.from_numpy(v)
+    dev.kvCachePut(d_kc, d_vc, d_k, d_v, 1, 17, max_seq, nkv, D, max_kv_dim)
+    oracle.kv_cache_put(kc, vc, k[0], v[0], 1, 17, max_seq, nkv, D, max_kv_dim)
+    dev.kvCachePutInd(d_kc, d_vc, d_k.at(k[0].nbytes), d_v.at(v[0].nbytes), 2,
+                      dev.from_numpy(np.array([63], np.int32)), max_seq, nkv, D, max_kv_dim)
+    oracle.kv_cache_put(kc, vc, np.ascontiguousarray(k[1]), np.ascontiguousarray(v[1]), 2, 63, max_seq, nkv, D, max_kv_dim)
+    dev.kvCachePutBatched(d_kc, d_vc, d_k.at(2 * k[0].nbytes), d_v.at(2 * v[0].nbytes), 0, 60, 4,
+                          max_seq, nkv, D, max_kv_dim)  # rows 60..63 (the 4th at 63 is the last slot)
+    for b in range(4):
+        oracle.kv_cache_put(kc, vc, np.ascontiguousarray(k[2 + b]), np.ascontiguousarray(v[2 + b]), 0,
+                            60 + b, max_seq, nkv, D, max_kv_dim)
+    assert_bitexact(d_kc.to_numpy(kc.shape, np.float32), kc, "K cache")
+    assert_bitexact(d_vc.to_numpy(vc.shape, np.float32), vc, "V cache")
+    # out-of-range position: skipped, cache untouched
+    dev.kvCachePut(d_kc, d_vc, d_k, d_v, 0, max_seq, max_seq, nkv, D, max_kv_dim)
+    assert_bitexact(d_kc.to_numpy(kc.shape, np.float32), kc, "K cache after pos=max_seq")
+
+
+# ---------------------------------------------------------------------------------------
+# GeGLU, soft-cap, add, scale
+# ---------------------------------------------------------------------------------------
+
+EXTREMES = np.array([0.0, -0.0, 1e-30, -1e-30, 1e-4, -1e-4, 0.5, -0.5, 3.0, -3.0, 5.0, -5.0, 9.0,
+                     -9.0, 20.0, -20.0, 60.0, -60.0, 1e4, -1e4], np.float32)
+
+
+def geglu_floor(g, u):
+    return np.abs(np.asarray(g, np.float64) * np.asarray(u, np.float64)) * 2.0 ** -23
+
+
+@pytest.mark.parametrize("n", [10240, 10240 + 3, 7])
+def test_geglu_f32(dev, oracle, n):
+    g = synth.normal_f32(0, "gate", (n,))
+    u = synth.normal_f32(0, "up", (n,))
+    g[: min(n, EXTREMES.size)] = EXTREMES[: min(n, EXTREMES.size)]
+    ref = oracle.geglu(g, u)
+    d_g, d_u, d_o = dev.from_numpy(g), dev.from_numpy(u), dev.alloc(g.nbytes)
+    dev.geglu(d_g, d_u, d_o, n)
+    assert_rel(d_o.to_numpy((n,), np.float32), ref, 1e-5, floor=geglu_floor(g, u), what="geglu f32")
+    dev.geglu(d_g, d_u, d_g, n)  # out aliases gate (math.zig geglu in place, model.zig:736-738)
+    assert_rel(d_g.to_numpy((n,), np.float32), ref, 1e-5, floor=geglu_floor(g, u), what="geglu in place")
+
+
+@pytest.mark.parametrize("n", [64 * 10240, 4096 + 5])
+def test_geglu_bf16(dev, oracle, n):
+    g = synth.normal_bf16(1, "gate", (n,))
+    u = synth.normal_bf16(1, "up", (n,))
+    g[:EXTREMES.size] = synth.f32_to_bf16(EXTREMES)
+    ref = oracle.geglu(g, u)
+    d_o = dev.alloc(g.nbytes)
+    dev.gegluEx(B.BF16, dev.from_numpy(g), dev.from_numpy(u), d_o, n)
+    f = O.get().bf16_to_f32
+    assert_bf16(d_o.to_numpy((n,), np.uint16), ref, 1, floor=geglu_floor(f(g), f(u)), what="geglu bf16")
+
+
+@pytest.mark.parametrize("cap,n,sigma", [(50.0, 8 * 1235, 20.0), (30.0, 4 * 262144, 15.0), (30.0, 1001, 100.0)])
+def test_softcap_f32(dev, oracle, cap, n, sigma):
+    x = synth.normal_f32(4, "logits", (n,), 0, sigma)
+    x[:EXTREMES.size] = EXTREMES
+    ref = oracle.softcap(x, cap)
+    d_x = dev.from_numpy(x)
+    dev.tanhSoftcap(d_x, cap, n)
+    assert_rel(d_x.to_numpy((n,), np.float32), ref, 1e-5, what=f"softcap cap={cap}")
+
+
+def test_softcap_bf16(dev, oracle):
+    n = 3 * 4096 + 1
+    x = synth.normal_bf16(4, "s", (n,), 0, 20)
+    ref = oracle.f32_to_bf16(oracle.softcap(oracle.bf16_to_f32(x), 50.0))
+    d_x = dev.from_numpy(x)
+    dev.tanhSoftcapEx(B.BF16, d_x, 50.0, n)
+    assert_bf16(d_x.to_numpy((n,), np.uint16), ref, 1, what="softcap bf16")
+
+
+def test_add_scale_mirrors(dev):
+    n = 2560 + 1
+    x = synth.normal_f32(5, "x", (n,))
+    r = synth.normal_f32(5, "r", (n,))
+    d_x = dev.from_numpy(x)
+    dev.add(d_x, dev.from_numpy(r), n)
+    assert_bitexact(d_x.to_numpy((n,), np.float32), (x + r).astype(np.float32), "add")
+    dev.scale(d_x, np.float32(0.37), n)
+    assert_bitexact(d_x.to_numpy((n,), np.float32), ((x + r) * np.float32(0.37)).astype(np.float32), "scale")

@@ -1,0 +1,133 @@
+"""ctypes binding of libhip_bridge.so: one typed Python callable per C-ABI entry point of
+include/hip_bridge.h.
+
+This is the Python side of the drop-in boundary (the Zig host binds the same symbols with
+`extern "c"` declarations). There is no fallback: if the library is missing or a symbol is
+absent, loading raises.
+"""
+import ctypes
+import os
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG, "libhip_bridge.so")
+
+F32, F16, Q4_0, Q8_0, Q6_K, BF16 = 0, 1, 2, 8, 14, 30
+OK, EINVAL, EUNSUPPORTED = 0, -1, -2
+
+_v = ctypes.c_void_p
+_i = ctypes.c_int
+_i64 = ctypes.c_int64
+_f = ctypes.c_float
+_sz = ctypes.c_size_t
+_pv = ctypes.POINTER(ctypes.c_void_p)
+
+# name -> (restype, argtypes), in header order.
+SIGNATURES = {
+    # runtime (cuda_bridge.h:15-33)
+    "hip_device_get_info": (_i, [_i, ctypes.c_char_p, _sz, ctypes.POINTER(_sz)]),
+    "hip_malloc": (_i, [_pv, _sz]),
+    "hip_free": (_i, [_v]),
+    "hip_malloc_host": (_i, [_pv, _sz]),
+    "hip_free_host": (_i, [_v]),
+    "hip_memcpy_h2d": (_i, [_v, _v, _sz, _v]),
+    "hip_memcpy_d2h": (_i, [_v, _v, _sz, _v]),
+    "hip_memcpy_d2d": (_i, [_v, _v, _sz, _v]),
+    "hip_stream_create": (_i, [_pv]),
+    "hip_stream_destroy": (_i, [_v]),
+    "hip_stream_sync": (_i, [_v]),
+    "hip_graph_begin_capture": (_i, [_v]),
+    "hip_graph_end_capture": (_i, [_v, _pv]),
+    "hip_graph_instantiate": (_i, [_pv, _v]),
+    "hip_graph_launch": (_i, [_v, _v]),
+    "hip_graph_destroy": (_i, [_v]),
+    "hip_graph_exec_destroy": (_i, [_v]),
+    # new runtime helpers
+    "hip_event_create": (_i, [_pv]),
+    "hip_event_destroy": (_i, [_v]),
+    "hip_event_record": (_i, [_v, _v]),
+    "hip_event_sync": (_i, [_v]),
+    "hip_event_elapsed_ms": (_i, [ctypes.POINTER(_f), _v, _v]),
+    "hip_fill_u8": (_i, [_v, ctypes.c_ubyte, _sz, _v]),
+    "hip_bridge_last_error": (_i, []),
+    "hip_bridge_error_string": (ctypes.c_char_p, [_i]),
+    "hip_bridge_version": (ctypes.c_char_p, []),
+    # gather (cuda_bridge.h:53-54 + new)
+    "hip_embed_lookup": (None, [_v, _i, _i, _v, _i, _f, _v]),
+    "hip_embed_lookup_batch": (None, [_v, _i, _v, _v, _i, _i, _f, _v]),
+    "hip_embed_gather": (None, [_v, _i, _i64, _v, _i, _v, _i64, _i, _f, _v]),
+    # norms (cuda_bridge.h:55-58, cuda_bridge.cu:2058 + new)
+    "hip_rmsnorm": (None, [_v, _v, _v, _i, _f, _i, _v]),
+    "hip_rmsnorm_batched": (None, [_v, _v, _v, _i, _i, _f, _i, _v]),
+    "hip_add_rmsnorm": (None, [_v, _v, _v, _v, _i, _f, _i, _v]),
+    "hip_add_rmsnorm_batched": (None, [_v, _v, _v, _v, _i, _i, _f, _i, _v]),
+    "hip_rmsnorm_add": (None, [_v, _v, _v, _i, _f, _i, _v]),
+    "hip_rmsnorm_rows": (None, [_i, _v, _v, _v, _i64, _i, _f, _i, _v]),
+    "hip_add_rmsnorm_rows": (None, [_i, _v, _v, _v, _v, _i64, _i, _f, _i, _v]),
+    "hip_rmsnorm_add_rows": (None, [_i, _v, _v, _v, _i64, _i, _f, _i, _v]),
+    "hip_rmsnorm_add_rmsnorm": (None, [_i, _v, _v, _v, _v, _v, _i64, _i, _f, _i, _v]),
+    # RoPE (cuda_bridge.h:59-61)
+    "hip_rope": (None, [_v, _v, _i, _i, _i, _i, _i, _f, _v]),
+    "hip_rope_ind": (None, [_v, _v, _v, _i, _i, _i, _i, _f, _v]),
+    "hip_rope_batched": (None, [_v, _v, _i, _i, _i, _i, _i, _i, _f, _v]),
+    # KV append (cuda_bridge.h:71-112)
+    "hip_kv_cache_put": (None, [_v, _v, _v, _v, _i, _i, _i, _i, _i, _i, _v]),
+    "hip_kv_cache_put_ind": (None, [_v, _v, _v, _v, _i, _v, _i, _i, _i, _i, _v]),
+    "hip_kv_cache_put_batched": (None, [_v, _v, _v, _v, _i, _i, _i, _i, _i, _i, _i, _v]),
+    # fused attention prologue (new)
+    "hip_qk_norm_rope_kv": (
+        None,
+        [_i, _v, _v, _v, _v, _v, _i, _v, _v, _i64, _i, _i, _i, _v, _i, _v, _i, _i, _i, _i, _i,
+         _f, _f, _f, _i, _v]),
+    # elementwise (cuda_bridge.h:64, 66-68 + new)
+    "hip_geglu": (None, [_v, _v, _v, _i, _v]),
+    "hip_add": (None, [_v, _v, _i, _v]),
+    "hip_scale": (None, [_v, _f, _i, _v]),
+    "hip_tanh_softcap": (None, [_v, _f, _i, _v]),
+    "hip_geglu_ex": (None, [_i, _v, _v, _v, _i64, _v]),
+    "hip_tanh_softcap_ex": (None, [_i, _v, _f, _i64, _v]),
+}
+
+
+class HipError(RuntimeError):
+    pass
+
+
+class Bridge:
+    """Loaded libhip_bridge.so with typed entry points as attributes."""
+
+    def __init__(self, path=LIB_PATH):
+        if not os.path.exists(path):
+            raise FileNotFoundError(
+                f"{path} not built: run `python -m ziglm_amd.build` (or __graft_entry__.build())")
+        self.path = path
+        self.lib = ctypes.CDLL(path)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(self.lib, name)  # AttributeError if the symbol is missing
+            fn.restype = res
+            fn.argtypes = args
+            setattr(self, name, fn)
+
+    def version(self):
+        return self.hip_bridge_version().decode()
+
+    def check(self, rc, what="hip call"):
+        if rc != 0:
+            raise HipError(f"{what} failed: {rc} ({self.hip_bridge_error_string(rc).decode()})")
+
+    def last_error(self):
+        return self.hip_bridge_last_error()
+
+    def raise_last_error(self, what="op"):
+        e = self.hip_bridge_last_error()
+        if e != 0:
+            raise HipError(f"{what}: {e} ({self.hip_bridge_error_string(e).decode()})")
+
+
+_bridge = None
+
+
+def load():
+    global _bridge
+    if _bridge is None:
+        _bridge = Bridge()
+    return _bridge

@@ -1,0 +1,169 @@
+// Elementwise ops: GeGLU (replaces cuda_bridge.cu:2247-2269), tanh soft-cap (2319-2330),
+// residual add and scale (2293-2317).
+//
+// Streaming layout: each thread owns U consecutive-by-wave 128-bit chunks
+// (chunk = (block*U + u)*256 + thread), so every load/store instruction of a wave covers
+// 1 KiB of contiguous memory; all loads of a thread are issued before any math. Elements
+// that do not fill a whole chunk (n % E) are done by a scalar tail in the first threads.
+//
+// GeGLU: out = gelu_tanh(gate) * up (math.zig:1119-1130) with the logistic form of GELU
+// (zl_common.h gelu_fast). Soft-cap: x = cap * tanh(x / cap) (model.zig:805-810) with the
+// IEEE quotient x/cap (div_by_uniform) and tanh_fast.
+#include "zl_common.h"
+#include "zl_host.h"
+
+namespace zl {
+
+constexpr int kEwThreads = 256;
+constexpr int kEwUnroll = 2;
+
+enum EwOp { EW_GEGLU = 0, EW_SOFTCAP = 1, EW_ADD = 2, EW_SCALE = 3 };
+
+struct EwArgs {
+    const void* a;  // gate | x | x
+    const void* b;  // up   | -  | residual
+    void* out;
+    int64_t n;
+    float p0, p1;   // softcap: cap, 1/cap; scale: factor
+};
+
+template <int OP>
+__device__ __forceinline__ float ew1(float a, float b, const EwArgs& args) {
+    if constexpr (OP == EW_GEGLU) return gelu_fast(a) * b;
+    else if constexpr (OP == EW_SOFTCAP) return args.p0 * tanh_fast(div_by_uniform(a, args.p0, args.p1));
+    else if constexpr (OP == EW_ADD) return a + b;
+    else return a * args.p0;
+}
+
+template <typename T, int OP>
+__global__ __launch_bounds__(kEwThreads) void k_ew(EwArgs args) {
+    using C = Chunk<T>;
+    constexpr int E = C::E;
+    constexpr bool kTwo = OP == EW_GEGLU || OP == EW_ADD;
+    const int64_t nch = args.n / E;
+    const T* A = (const T*)args.a;
+    const T* B = (const T*)args.b;
+    T* O = (T*)args.out;
+    u32x4 ra[kEwUnroll], rb[kEwUnroll];
+    int64_t idx[kEwUnroll];
+#pragma unroll
+    for (int u = 0; u < kEwUnroll; ++u) {
+        idx[u] = ((int64_t)blockIdx.x * kEwUnroll + u) * kEwThreads + threadIdx.x;
+        if (idx[u] < nch) {
+            ra[u] = ld16(A + idx[u] * E);
+            if constexpr (kTwo) rb[u] = ld16(B + idx[u] * E);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < kEwUnroll; ++u) {
+        if (idx[u] < nch) {
+            float x[E], y[E];
+            C::unpack(ra[u], x);
+            if constexpr (kTwo) C::unpack(rb[u], y);
+#pragma unroll
+            for (int j = 0; j < E; ++j) x[j] = ew1<OP>(x[j], kTwo ? y[j] : 0.0f, args);
+            st16(O + idx[u] * E, C::pack(x));
+        }
+    }
+    // scalar tail
+    const int64_t tail0 = nch * E;
+    const int64_t ti = tail0 + (int64_t)blockIdx.x * kEwThreads + threadIdx.x;
+    if (blockIdx.x == 0 && ti < args.n) {
+        float x, y = 0.0f;
+        if constexpr (sizeof(T) == 4) {
+            x = ((const float*)A)[ti];
+            if constexpr (kTwo) y = ((const float*)B)[ti];
+        } else {
+            x = bf16_lo(((const uint16_t*)A)[ti]);
+            if constexpr (kTwo) y = bf16_lo(((const uint16_t*)B)[ti]);
+        }
+        const float r = ew1<OP>(x, y, args);
+        if constexpr (sizeof(T) == 4) ((float*)O)[ti] = r;
+        else ((uint16_t*)O)[ti] = (uint16_t)(pack_bf16x2(r, 0.0f) & 0xffffu);
+    }
+}
+
+// Unaligned buffers: one element per thread.
+template <typename T, int OP>
+__global__ __launch_bounds__(kEwThreads) void k_ew_scalar(EwArgs args) {
+    constexpr bool kTwo = OP == EW_GEGLU || OP == EW_ADD;
+    const int64_t i = (int64_t)blockIdx.x * kEwThreads + threadIdx.x;
+    if (i >= args.n) return;
+    float x, y = 0.0f;
+    if constexpr (sizeof(T) == 4) {
+        x = ((const float*)args.a)[i];
+        if constexpr (kTwo) y = ((const float*)args.b)[i];
+    } else {
+        x = bf16_lo(((const uint16_t*)args.a)[i]);
+        if constexpr (kTwo) y = bf16_lo(((const uint16_t*)args.b)[i]);
+    }
+    const float r = ew1<OP>(x, y, args);
+    if constexpr (sizeof(T) == 4) ((float*)args.out)[i] = r;
+    else ((uint16_t*)args.out)[i] = (uint16_t)(pack_bf16x2(r, 0.0f) & 0xffffu);
+}
+
+template <typename T, int OP>
+static void launch_ew_t(const EwArgs& a, hipStream_t s) {
+    constexpr int E = Chunk<T>::E;
+    constexpr bool kTwo = OP == EW_GEGLU || OP == EW_ADD;
+    const bool vec = aligned16(a.a) && aligned16(a.out) && (!kTwo || aligned16(a.b));
+    if (vec) {
+        const int64_t nch = a.n / E;
+        int64_t grid = cdiv(nch, (int64_t)kEwThreads * kEwUnroll);
+        if (grid < 1) grid = 1;  // the tail still needs block 0
+        k_ew<T, OP><<<(unsigned)grid, kEwThreads, 0, s>>>(a);
+    } else {
+        k_ew_scalar<T, OP><<<(unsigned)cdiv(a.n, kEwThreads), kEwThreads, 0, s>>>(a);
+    }
+    check_launch();
+}
+
+template <int OP>
+static void launch_ew(int dtype, const EwArgs& a, hipStream_t s) {
+    if (a.n <= 0) return;
+    if (!a.a || !a.out || ((OP == EW_GEGLU || OP == EW_ADD) && !a.b)) {
+        set_error(HIP_BRIDGE_EINVAL);
+        return;
+    }
+    if (dtype == HIP_BRIDGE_F32) launch_ew_t<float, OP>(a, s);
+    else if (dtype == HIP_BRIDGE_BF16) launch_ew_t<uint16_t, OP>(a, s);
+    else set_error(HIP_BRIDGE_EUNSUPPORTED);
+}
+
+}  // namespace zl
+
+using namespace zl;
+
+extern "C" {
+
+void hip_geglu_ex(int dtype, const void* gate, const void* up, void* out, int64_t n,
+                  HipStream_t stream) {
+    EwArgs a{gate, up, out, n, 0.0f, 0.0f};
+    launch_ew<EW_GEGLU>(dtype, a, stream_of(stream));
+}
+
+void hip_tanh_softcap_ex(int dtype, void* x, float cap, int64_t n, HipStream_t stream) {
+    // 1/cap rounded once (IEEE f32 divide on the host) for the correctly rounded quotient.
+    EwArgs a{x, nullptr, x, n, cap, 1.0f / cap};
+    launch_ew<EW_SOFTCAP>(dtype, a, stream_of(stream));
+}
+
+void hip_geglu(const float* gate, const float* up, float* out, int n, HipStream_t stream) {
+    hip_geglu_ex(HIP_BRIDGE_F32, gate, up, out, n, stream);
+}
+
+void hip_tanh_softcap(float* x, float cap, int n, HipStream_t stream) {
+    hip_tanh_softcap_ex(HIP_BRIDGE_F32, x, cap, n, stream);
+}
+
+void hip_add(float* x, const float* residual, int n, HipStream_t stream) {
+    EwArgs a{x, residual, x, n, 0.0f, 0.0f};
+    launch_ew<EW_ADD>(HIP_BRIDGE_F32, a, stream_of(stream));
+}
+
+void hip_scale(float* x, float scale, int n, HipStream_t stream) {
+    EwArgs a{x, nullptr, x, n, scale, 0.0f};
+    launch_ew<EW_SCALE>(HIP_BRIDGE_F32, a, stream_of(stream));
+}
+
+}  // extern "C"

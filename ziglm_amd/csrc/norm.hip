@@ -1,0 +1,326 @@
+// RMSNorm family (replaces cuda_bridge.cu:1451-1553, 1942-2068) with ziglm's CPU numerics
+// (math.zig:850-988): sum of squares in f32, mean = sum/n, inv = 1.0/sqrt(mean + eps) with
+// IEEE sqrt and divide, out = (x*inv)*(1+w) | (x*inv)*w | x*inv (weight NULL).
+//
+// Modes (one kernel family, one wave per row):
+//   NORM           out = norm(x)                                   (rmsNorm, rmsNormBatched)
+//   ADD_NORM       s = x + r; x = s; out = norm(s)                 (addRmsNorm, model.zig:714-723)
+//   NORM_ADD       x = x + norm(r)                                 (rmsnormAdd, model.zig:748-755)
+//   NORM_ADD_NORM  s = x + norm(r; w1); x = s; out = norm(s; w2)   (post-attn norm + add +
+//                  pre-FFN norm, cuda_model.zig:930-942; post-FFN norm + add + next input norm)
+// The whole row lives in registers: each lane loads chunks lane, lane+64, ... with 128-bit
+// loads, so x and r are read from HBM once and x/out written once. The row statistics are
+// a wave64 butterfly sum. Weights (f32, shared by all rows) come from L2.
+// Rows that are not 16-byte aligned, or longer than 24 chunks per lane (f32 > 6144,
+// bf16 > 12288 elements), use a block-per-row kernel that re-reads the row from L2.
+// Aliasing: out may alias r (the reference calls addRmsNorm(x, xb, w, out=xb)) or x in
+// NORM mode; every lane reads its chunks before writing the same chunks.
+#include "zl_common.h"
+#include "zl_host.h"
+
+namespace zl {
+
+enum NormMode { M_NORM = 0, M_ADD_NORM = 1, M_NORM_ADD = 2, M_NORM_ADD_NORM = 3 };
+
+struct NormArgs {
+    void* x;          // NORM: input (read only); otherwise the residual stream (updated)
+    const void* r;    // ADD_NORM: residual; NORM_ADD: input to normalise; NORM_ADD_NORM: xb
+    const float* w1;  // weight of the first norm (NULL: no scale)
+    const float* w2;  // weight of the second norm (NORM_ADD_NORM only)
+    void* out;
+    int64_t rows;
+    int n;
+    float eps;
+    int uo;           // use_unit_offset: scale by (1 + w)
+};
+
+// (v * inv) * wf with wf = 1 + w, w, or absent.
+__device__ __forceinline__ float apply_w(float v, float inv, const float* w, int i, int uo, bool has_w) {
+    const float y = v * inv;
+    if (!has_w) return y;
+    const float wi = w[i];
+    return uo ? y * (1.0f + wi) : y * wi;
+}
+
+template <typename T, int NC, int MODE>
+__global__ __launch_bounds__(256) void k_norm_rows(NormArgs a) {
+    using C = Chunk<T>;
+    constexpr int E = C::E;
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= a.rows) return;
+    const int n = a.n;
+    const int nch = n / E;
+    T* xrow = (T*)a.x + row * n;
+    const T* rrow = (const T*)a.r + row * n;
+    T* orow = (T*)a.out + row * n;
+    const bool has_w1 = a.w1 != nullptr;
+    const bool has_w2 = a.w2 != nullptr;
+
+    u32x4 rx[NC], rr[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int idx = lane + c * kWave;
+        if (idx < nch) {
+            rx[c] = ld16(xrow + (int64_t)idx * E);
+            if constexpr (MODE != M_NORM) rr[c] = ld16(rrow + (int64_t)idx * E);
+        }
+    }
+
+    // v: the vector normalised first.
+    float v[NC][E];
+    float ss = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int idx = lane + c * kWave;
+        if (idx < nch) {
+            if constexpr (MODE == M_NORM) {
+                C::unpack(rx[c], v[c]);
+            } else if constexpr (MODE == M_ADD_NORM) {
+                float xv[E], rv[E];
+                C::unpack(rx[c], xv);
+                C::unpack(rr[c], rv);
+#pragma unroll
+                for (int j = 0; j < E; ++j) v[c][j] = xv[j] + rv[j];
+            } else {
+                C::unpack(rr[c], v[c]);
+            }
+#pragma unroll
+            for (int j = 0; j < E; ++j) ss = fmaf(v[c][j], v[c][j], ss);
+        }
+    }
+    ss = group_sum<kWave>(ss);
+    const float inv = rms_inv(ss, n, a.eps);
+
+    if constexpr (MODE == M_NORM || MODE == M_ADD_NORM) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const int idx = lane + c * kWave;
+            if (idx < nch) {
+                float y[E];
+#pragma unroll
+                for (int j = 0; j < E; ++j) y[j] = apply_w(v[c][j], inv, a.w1, idx * E + j, a.uo, has_w1);
+                if constexpr (MODE == M_ADD_NORM) st16(xrow + (int64_t)idx * E, C::pack(v[c]));
+                st16(orow + (int64_t)idx * E, C::pack(y));
+            }
+        }
+    } else if constexpr (MODE == M_NORM_ADD) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const int idx = lane + c * kWave;
+            if (idx < nch) {
+                float xv[E];
+                C::unpack(rx[c], xv);
+#pragma unroll
+                for (int j = 0; j < E; ++j) xv[j] = xv[j] + apply_w(v[c][j], inv, a.w1, idx * E + j, a.uo, has_w1);
+                st16(xrow + (int64_t)idx * E, C::pack(xv));
+            }
+        }
+    } else {  // M_NORM_ADD_NORM
+        float ss2 = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const int idx = lane + c * kWave;
+            if (idx < nch) {
+                float xv[E];
+                C::unpack(rx[c], xv);
+#pragma unroll
+                for (int j = 0; j < E; ++j) {
+                    v[c][j] = xv[j] + apply_w(v[c][j], inv, a.w1, idx * E + j, a.uo, has_w1);
+                    ss2 = fmaf(v[c][j], v[c][j], ss2);
+                }
+            }
+        }
+        ss2 = group_sum<kWave>(ss2);
+        const float inv2 = rms_inv(ss2, n, a.eps);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const int idx = lane + c * kWave;
+            if (idx < nch) {
+                float y[E];
+#pragma unroll
+                for (int j = 0; j < E; ++j) y[j] = apply_w(v[c][j], inv2, a.w2, idx * E + j, a.uo, has_w2);
+                st16(xrow + (int64_t)idx * E, C::pack(v[c]));
+                st16(orow + (int64_t)idx * E, C::pack(y));
+            }
+        }
+    }
+}
+
+// ---- block-per-row fallback: any n, any alignment ------------------------------------------
+
+template <typename T>
+__device__ __forceinline__ float ld1(const T* p, int64_t i);
+template <>
+__device__ __forceinline__ float ld1<float>(const float* p, int64_t i) { return p[i]; }
+template <>
+__device__ __forceinline__ float ld1<uint16_t>(const uint16_t* p, int64_t i) { return bf16_lo(p[i]); }
+
+template <typename T>
+__device__ __forceinline__ void st1(T* p, int64_t i, float v);
+template <>
+__device__ __forceinline__ void st1<float>(float* p, int64_t i, float v) { p[i] = v; }
+template <>
+__device__ __forceinline__ void st1<uint16_t>(uint16_t* p, int64_t i, float v) {
+    p[i] = (uint16_t)(pack_bf16x2(v, 0.0f) & 0xffffu);
+}
+
+__device__ __forceinline__ float block_sum256(float v, float* red) {
+    v = group_sum<kWave>(v);
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) red[wave] = v;
+    __syncthreads();
+    const float t = (red[0] + red[1]) + (red[2] + red[3]);
+    __syncthreads();
+    return t;
+}
+
+template <typename T, int MODE>
+__global__ __launch_bounds__(256) void k_norm_rows_generic(NormArgs a) {
+    __shared__ float red[4];
+    const int64_t row = blockIdx.x;
+    const int n = a.n;
+    T* xrow = (T*)a.x + row * n;
+    const T* rrow = (const T*)a.r + row * n;
+    T* orow = (T*)a.out + row * n;
+    const bool has_w1 = a.w1 != nullptr;
+    const bool has_w2 = a.w2 != nullptr;
+
+    auto first = [&](int i) -> float {
+        if constexpr (MODE == M_NORM) return ld1(xrow, i);
+        else if constexpr (MODE == M_ADD_NORM) return ld1(xrow, i) + ld1(rrow, i);
+        else return ld1(rrow, i);
+    };
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < n; i += 256) {
+        const float v = first(i);
+        ss = fmaf(v, v, ss);
+    }
+    const float inv = rms_inv(block_sum256(ss, red), n, a.eps);
+
+    if constexpr (MODE == M_NORM || MODE == M_ADD_NORM) {
+        for (int i = threadIdx.x; i < n; i += 256) {
+            const float v = first(i);
+            const float y = apply_w(v, inv, a.w1, i, a.uo, has_w1);
+            if constexpr (MODE == M_ADD_NORM) st1(xrow, i, v);
+            st1(orow, i, y);
+        }
+    } else if constexpr (MODE == M_NORM_ADD) {
+        for (int i = threadIdx.x; i < n; i += 256) {
+            const float v = first(i);
+            st1(xrow, i, ld1(xrow, i) + apply_w(v, inv, a.w1, i, a.uo, has_w1));
+        }
+    } else {
+        // Pass 2 computes s = x + norm1(xb) for the second statistic; pass 3 recomputes s
+        // with the same f32 operations (x is only overwritten in pass 3).
+        float ss2 = 0.0f;
+        for (int i = threadIdx.x; i < n; i += 256) {
+            const float s = ld1(xrow, i) + apply_w(first(i), inv, a.w1, i, a.uo, has_w1);
+            ss2 = fmaf(s, s, ss2);
+        }
+        const float inv2 = rms_inv(block_sum256(ss2, red), n, a.eps);
+        for (int i = threadIdx.x; i < n; i += 256) {
+            const float s = ld1(xrow, i) + apply_w(first(i), inv, a.w1, i, a.uo, has_w1);
+            st1(xrow, i, s);
+            st1(orow, i, apply_w(s, inv2, a.w2, i, a.uo, has_w2));
+        }
+    }
+}
+
+template <typename T, int MODE>
+static void launch_t(const NormArgs& a, hipStream_t s) {
+    constexpr int E = Chunk<T>::E;
+    const int nch = a.n / E;
+    const int per_lane = (int)cdiv(nch, kWave);
+    const bool vec = a.n % E == 0 && aligned16(a.x) && (MODE == M_NORM || aligned16(a.r)) &&
+                     (MODE == M_NORM_ADD || aligned16(a.out)) && per_lane <= 24;
+    if (vec) {
+        const unsigned grid = (unsigned)cdiv(a.rows, 4);
+        if (per_lane <= 2) k_norm_rows<T, 2, MODE><<<grid, 256, 0, s>>>(a);
+        else if (per_lane <= 6) k_norm_rows<T, 6, MODE><<<grid, 256, 0, s>>>(a);
+        else if (per_lane <= 12) k_norm_rows<T, 12, MODE><<<grid, 256, 0, s>>>(a);
+        else k_norm_rows<T, 24, MODE><<<grid, 256, 0, s>>>(a);
+    } else {
+        k_norm_rows_generic<T, MODE><<<(unsigned)a.rows, 256, 0, s>>>(a);
+    }
+    check_launch();
+}
+
+template <int MODE>
+static void launch_norm(int dtype, const NormArgs& a, hipStream_t s) {
+    if (a.rows <= 0 || a.n <= 0) return;
+    if (!a.x || (MODE != M_NORM && !a.r) || (MODE != M_NORM_ADD && !a.out)) {
+        set_error(HIP_BRIDGE_EINVAL);
+        return;
+    }
+    if (a.rows > 0x7fffffffLL) {
+        set_error(HIP_BRIDGE_EUNSUPPORTED);
+        return;
+    }
+    if (dtype == HIP_BRIDGE_F32) launch_t<float, MODE>(a, s);
+    else if (dtype == HIP_BRIDGE_BF16) launch_t<uint16_t, MODE>(a, s);
+    else set_error(HIP_BRIDGE_EUNSUPPORTED);
+}
+
+}  // namespace zl
+
+using namespace zl;
+
+extern "C" {
+
+void hip_rmsnorm_rows(int dtype, const void* x, const float* weight, void* out, int64_t rows,
+                      int n, float eps, int use_unit_offset, HipStream_t stream) {
+    NormArgs a{const_cast<void*>(x), nullptr, weight, nullptr, out, rows, n, eps, use_unit_offset};
+    launch_norm<M_NORM>(dtype, a, stream_of(stream));
+}
+
+void hip_add_rmsnorm_rows(int dtype, void* x, const void* residual, const float* weight,
+                          void* out, int64_t rows, int n, float eps, int use_unit_offset,
+                          HipStream_t stream) {
+    NormArgs a{x, residual, weight, nullptr, out, rows, n, eps, use_unit_offset};
+    launch_norm<M_ADD_NORM>(dtype, a, stream_of(stream));
+}
+
+void hip_rmsnorm_add_rows(int dtype, void* x, const void* in, const float* weight, int64_t rows,
+                          int n, float eps, int use_unit_offset, HipStream_t stream) {
+    NormArgs a{x, in, weight, nullptr, nullptr, rows, n, eps, use_unit_offset};
+    launch_norm<M_NORM_ADD>(dtype, a, stream_of(stream));
+}
+
+void hip_rmsnorm_add_rmsnorm(int dtype, void* x, const void* xb, const float* w1,
+                             const float* w2, void* out, int64_t rows, int n, float eps,
+                             int use_unit_offset, HipStream_t stream) {
+    NormArgs a{x, xb, w1, w2, out, rows, n, eps, use_unit_offset};
+    launch_norm<M_NORM_ADD_NORM>(dtype, a, stream_of(stream));
+}
+
+// ---- reference-ABI f32 entry points -------------------------------------------------------
+
+void hip_rmsnorm(const float* x, const float* weight, float* out, int n, float eps,
+                 int use_unit_offset, HipStream_t stream) {
+    hip_rmsnorm_rows(HIP_BRIDGE_F32, x, weight, out, 1, n, eps, use_unit_offset, stream);
+}
+
+void hip_rmsnorm_batched(float* x, const float* weight, float* out, int head_dim, int count,
+                         float eps, int use_unit_offset, HipStream_t stream) {
+    hip_rmsnorm_rows(HIP_BRIDGE_F32, x, weight, out, count, head_dim, eps, use_unit_offset, stream);
+}
+
+void hip_add_rmsnorm(float* x, const float* residual, const float* weight, float* out, int n,
+                     float eps, int use_unit_offset, HipStream_t stream) {
+    hip_add_rmsnorm_rows(HIP_BRIDGE_F32, x, residual, weight, out, 1, n, eps, use_unit_offset, stream);
+}
+
+void hip_add_rmsnorm_batched(float* x, const float* residual, const float* weight, float* out,
+                             int n, int batch_size, float eps, int use_unit_offset,
+                             HipStream_t stream) {
+    hip_add_rmsnorm_rows(HIP_BRIDGE_F32, x, residual, weight, out, batch_size, n, eps,
+                         use_unit_offset, stream);
+}
+
+void hip_rmsnorm_add(float* x, const float* in, const float* weight, int n, float eps,
+                     int use_unit_offset, HipStream_t stream) {
+    hip_rmsnorm_add_rows(HIP_BRIDGE_F32, x, in, weight, 1, n, eps, use_unit_offset, stream);
+}
+
+}  // extern "C"

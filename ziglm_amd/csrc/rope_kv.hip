@@ -1,0 +1,499 @@
+// Fused attention prologue: per-head RMSNorm of Q and K (and the Gemma-4 no-scale norm of
+// V), half-split RoPE, and the KV-cache append, in one launch. Replaces cuda_bridge.cu
+// k_rmsnorm_batched (1504-1553) x3, k_rope{,_ind,_batched} (2070-2245) and
+// k_kv_cache_put{,_ind,_batched} (2336-2460), which in the reference are six launches and
+// five extra HBM round trips of Q and K.
+//
+// Numerics follow ziglm's CPU path:
+//   norm  math.zig:850-988 (inv = 1.0/sqrt(mean + eps), (x*inv)*(1+w));
+//   RoPE  math.zig:1019-1078 .normal: pairs (i, i + r/2); theta = (f32(pos)*freq_scale)/D_i;
+//         D_i = f32(pow(f64 base, f64(f32(2i)/f32(r)))) is computed on the host by the same
+//         expression as the oracle and passed in the kernel arguments; cos/sin are the f32
+//         roundings of the double-precision cos/sin of theta; the rotation is
+//         v0*c - v1*s, v0*s + v1*c with no FMA;
+//   KV    kv_cache_put (cuda_bridge.cu:2349; kv_cache.zig:63-85): row-contiguous copy.
+//
+// Fast path (rotary_dim == head_dim in {64, 128, 256}, 16-byte aligned buffers): one
+// workgroup per token, LH = head_dim/(2E) lanes per head (E = elements per 128-bit chunk)
+// and 64/LH heads per wave. Lane l of a head holds chunk l (elements [lE, lE+E)) and chunk
+// l + LH (the same offsets + head_dim/2), so every RoPE pair is inside one lane; the norm
+// statistic is an LH-lane butterfly. The token's cos/sin table (head_dim/2 entries) is
+// computed once in LDS while the first head's loads are in flight.
+// Generic path (partial rotary, other head sizes up to 512, any alignment): one wave per
+// head, head staged in LDS.
+#include <math.h>
+#include <string.h>
+
+#include "zl_common.h"
+#include "zl_host.h"
+
+namespace zl {
+
+constexpr int kMaxHalf = 256;  // head_dim <= 512
+
+struct RopeTab {
+    float denom[kMaxHalf];
+};
+
+struct QkArgs {
+    void* q;
+    const void* k;
+    const void* v;
+    const float* wq;
+    const float* wk;
+    void* kdst;
+    void* vdst;
+    int64_t cache_rows;     // rows available in kdst/vdst (0: not checked)
+    int64_t row_stride;     // elements between destination rows
+    const int32_t* pos;     // device positions (pos_mode 1, 2)
+    int pos_mode;           // 0: pos_base + t; 1: pos[t]; 2: pos[0] + t
+    int pos_base;
+    const int64_t* slot;    // device cache rows (slot_mode 1)
+    int slot_mode;          // 0: layer_base + position, position in [0, max_seq); 1: slot[t]; 2: row t
+    int64_t layer_base;
+    int max_seq;
+    int n_tokens, nh, nkv, D, half;
+    int do_qnorm, do_knorm, v_norm, do_rope, uo;
+    float freq_scale, eps;
+};
+
+__device__ __forceinline__ int token_pos(const QkArgs& a, int t) {
+    return a.pos_mode == 0 ? a.pos_base + t : a.pos_mode == 1 ? a.pos[t] : a.pos[0] + t;
+}
+
+// Destination row of token t in kdst/vdst, or -1 when it must not be written.
+__device__ __forceinline__ int64_t token_row(const QkArgs& a, int t, int p) {
+    int64_t row;
+    if (a.slot_mode == 0) {
+        if (p < 0 || p >= a.max_seq) return -1;
+        row = a.layer_base + p;
+    } else if (a.slot_mode == 1) {
+        row = a.slot[t];
+    } else {
+        return t;
+    }
+    if (row < 0 || (a.cache_rows > 0 && row >= a.cache_rows)) return -1;
+    return row;
+}
+
+// cos/sin of theta_i = pos_f / D_i for i < half, into LDS.
+__device__ __forceinline__ void fill_cos_sin(const RopeTab& tab, float pos_f, int half, float* s_cos,
+                                             float* s_sin) {
+    for (int i = threadIdx.x; i < half; i += blockDim.x) {
+        const float theta = pos_f / tab.denom[i];
+        double s, c;
+        sincos((double)theta, &s, &c);
+        s_cos[i] = (float)c;
+        s_sin[i] = (float)s;
+    }
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void k_qk_fused(QkArgs a, RopeTab tab) {
+    using C = Chunk<T>;
+    constexpr int E = C::E;
+    constexpr int HALF = D / 2;
+    constexpr int LH = HALF / E;  // lanes per head
+    constexpr int G = kWave / LH; // heads per wave
+    static_assert(LH >= 1 && LH <= kWave && (LH & (LH - 1)) == 0, "bad head layout");
+    __shared__ float s_cos[HALF], s_sin[HALF];
+
+    const int t = blockIdx.x;
+    const int lane = threadIdx.x & 63;
+    const int hl = lane & (LH - 1);
+    const int gslot = (threadIdx.x >> 6) * G + lane / LH;
+    constexpr int kSlots = 4 * G;
+    const int nq = a.q ? a.nh : 0;
+    const int HR = a.nh + 2 * a.nkv;
+    const int p = token_pos(a, t);
+    const int64_t row = token_row(a, t, p);
+
+    // Head rows: [0, nh) Q, [nh, nh+nkv) K, [nh+nkv, nh+2nkv) V.
+    auto src_of = [&](int hr) -> const T* {
+        if (hr < a.nh) return (const T*)a.q + ((int64_t)t * a.nh + hr) * D;
+        if (hr < a.nh + a.nkv) return (const T*)a.k + ((int64_t)t * a.nkv + (hr - a.nh)) * D;
+        return (const T*)a.v + ((int64_t)t * a.nkv + (hr - a.nh - a.nkv)) * D;
+    };
+    auto active = [&](int hr) -> bool {
+        if (hr < a.nh) return nq > 0;
+        if (hr < a.nh + a.nkv) return a.k != nullptr && row >= 0;
+        return a.v != nullptr && row >= 0;
+    };
+
+    // Prefetch the first head row, then build the cos/sin table while it is in flight.
+    u32x4 ra = {0, 0, 0, 0}, rb = {0, 0, 0, 0};
+    if (gslot < HR && active(gslot)) {
+        const T* src = src_of(gslot);
+        ra = ld16(src + hl * E);
+        rb = ld16(src + HALF + hl * E);
+    }
+    if (a.do_rope) fill_cos_sin(tab, (float)p * a.freq_scale, HALF, s_cos, s_sin);
+    __syncthreads();
+
+    for (int hr = gslot; hr < HR; hr += kSlots) {
+        if (!active(hr)) continue;
+        if (hr != gslot) {
+            const T* src = src_of(hr);
+            ra = ld16(src + hl * E);
+            rb = ld16(src + HALF + hl * E);
+        }
+        const int kind = hr < a.nh ? 0 : hr < a.nh + a.nkv ? 1 : 2;  // Q, K, V
+        float x0[E], x1[E];
+        C::unpack(ra, x0);
+        C::unpack(rb, x1);
+        const bool norm = kind == 0 ? a.do_qnorm : kind == 1 ? a.do_knorm : a.v_norm;
+        if (norm) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int j = 0; j < E; ++j) {
+                ss = fmaf(x0[j], x0[j], ss);
+                ss = fmaf(x1[j], x1[j], ss);
+            }
+            ss = group_sum<LH>(ss);
+            const float inv = rms_inv(ss, D, a.eps);
+            const float* w = kind == 0 ? a.wq : kind == 1 ? a.wk : nullptr;
+            if (w) {
+                const int i0 = hl * E;
+#pragma unroll
+                for (int j = 0; j < E; ++j) {
+                    const float w0 = w[i0 + j], w1 = w[HALF + i0 + j];
+                    x0[j] = a.uo ? (x0[j] * inv) * (1.0f + w0) : (x0[j] * inv) * w0;
+                    x1[j] = a.uo ? (x1[j] * inv) * (1.0f + w1) : (x1[j] * inv) * w1;
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < E; ++j) {
+                    x0[j] = x0[j] * inv;
+                    x1[j] = x1[j] * inv;
+                }
+            }
+        }
+        if (a.do_rope && kind != 2) {
+#pragma unroll
+            for (int j = 0; j < E; ++j) {
+                const float c = s_cos[hl * E + j], s = s_sin[hl * E + j];
+                const float v0 = x0[j], v1 = x1[j];
+                x0[j] = v0 * c - v1 * s;
+                x1[j] = v0 * s + v1 * c;
+            }
+        }
+        T* dst;
+        if (kind == 0) dst = (T*)a.q + ((int64_t)t * a.nh + hr) * D;
+        else if (kind == 1) dst = (T*)a.kdst + row * a.row_stride + (int64_t)(hr - a.nh) * D;
+        else dst = (T*)a.vdst + row * a.row_stride + (int64_t)(hr - a.nh - a.nkv) * D;
+        st16(dst + hl * E, C::pack(x0));
+        st16(dst + HALF + hl * E, C::pack(x1));
+    }
+}
+
+// ---- generic path ----------------------------------------------------------------------
+
+template <typename T>
+__device__ __forceinline__ float gld(const T* p, int64_t i);
+template <>
+__device__ __forceinline__ float gld<float>(const float* p, int64_t i) { return p[i]; }
+template <>
+__device__ __forceinline__ float gld<uint16_t>(const uint16_t* p, int64_t i) { return bf16_lo(p[i]); }
+template <typename T>
+__device__ __forceinline__ void gst(T* p, int64_t i, float v);
+template <>
+__device__ __forceinline__ void gst<float>(float* p, int64_t i, float v) { p[i] = v; }
+template <>
+__device__ __forceinline__ void gst<uint16_t>(uint16_t* p, int64_t i, float v) {
+    p[i] = (uint16_t)(pack_bf16x2(v, 0.0f) & 0xffffu);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void k_qk_generic(QkArgs a, RopeTab tab) {
+    __shared__ float s_cos[kMaxHalf], s_sin[kMaxHalf];
+    __shared__ float s_head[4][2 * kMaxHalf];
+    const int t = blockIdx.x;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int D = a.D, half = a.half;
+    const int HR = a.nh + 2 * a.nkv;
+    const int p = token_pos(a, t);
+    const int64_t row = token_row(a, t, p);
+    if (a.do_rope) fill_cos_sin(tab, (float)p * a.freq_scale, half, s_cos, s_sin);
+    __syncthreads();
+    float* buf = s_head[wave];
+    const int rounds = (HR + 3) / 4;
+    for (int rd = 0; rd < rounds; ++rd) {
+        const int hr = rd * 4 + wave;
+        int kind = -1;
+        const T* src = nullptr;
+        T* dst = nullptr;
+        if (hr < a.nh) {
+            if (a.q) {
+                kind = 0;
+                src = (const T*)a.q + ((int64_t)t * a.nh + hr) * D;
+                dst = (T*)a.q + ((int64_t)t * a.nh + hr) * D;
+            }
+        } else if (hr < a.nh + a.nkv) {
+            if (a.k && row >= 0) {
+                kind = 1;
+                src = (const T*)a.k + ((int64_t)t * a.nkv + (hr - a.nh)) * D;
+                dst = (T*)a.kdst + row * a.row_stride + (int64_t)(hr - a.nh) * D;
+            }
+        } else if (hr < HR) {
+            if (a.v && row >= 0) {
+                kind = 2;
+                src = (const T*)a.v + ((int64_t)t * a.nkv + (hr - a.nh - a.nkv)) * D;
+                dst = (T*)a.vdst + row * a.row_stride + (int64_t)(hr - a.nh - a.nkv) * D;
+            }
+        }
+        float ss = 0.0f;
+        if (kind >= 0) {
+            for (int i = lane; i < D; i += kWave) {
+                const float x = gld(src, i);
+                buf[i] = x;
+                ss = fmaf(x, x, ss);
+            }
+        }
+        ss = group_sum<kWave>(ss);
+        __syncthreads();
+        if (kind >= 0) {
+            const bool norm = kind == 0 ? a.do_qnorm : kind == 1 ? a.do_knorm : a.v_norm;
+            if (norm) {
+                const float inv = rms_inv(ss, D, a.eps);
+                const float* w = kind == 0 ? a.wq : kind == 1 ? a.wk : nullptr;
+                for (int i = lane; i < D; i += kWave) {
+                    const float y = buf[i] * inv;
+                    buf[i] = w ? (a.uo ? y * (1.0f + w[i]) : y * w[i]) : y;
+                }
+            }
+        }
+        __syncthreads();
+        if (kind >= 0 && kind != 2 && a.do_rope) {
+            for (int i = lane; i < half; i += kWave) {
+                const float c = s_cos[i], s = s_sin[i];
+                const float v0 = buf[i], v1 = buf[i + half];
+                buf[i] = v0 * c - v1 * s;
+                buf[i + half] = v0 * s + v1 * c;
+            }
+        }
+        __syncthreads();
+        if (kind >= 0)
+            for (int i = lane; i < D; i += kWave) gst(dst, i, buf[i]);
+        __syncthreads();
+    }
+}
+
+// ---- host side -------------------------------------------------------------------------
+
+// D_i = f32(pow(f64 base, f64(f32(2i)/f32(eff)))): the same expression as the oracle's
+// zo_rope_denominator. A few (base, eff) tables are cached per host thread.
+static const RopeTab& rope_table(float base, int eff) {
+    struct Entry {
+        float base;
+        int eff;
+        RopeTab tab;
+    };
+    static thread_local Entry cache[4];
+    static thread_local int used = 0, next = 0;
+    for (int i = 0; i < used; ++i)
+        if (cache[i].eff == eff && memcmp(&cache[i].base, &base, sizeof(float)) == 0) return cache[i].tab;
+    Entry& e = cache[next];
+    next = (next + 1) % 4;
+    if (used < 4) ++used;
+    e.base = base;
+    e.eff = eff;
+    memset(&e.tab, 0, sizeof(e.tab));
+    for (int i = 0; i < eff / 2 && i < kMaxHalf; ++i) {
+        const float ex = (float)(2 * i) / (float)eff;
+        e.tab.denom[i] = (float)pow((double)base, (double)ex);
+    }
+    return e.tab;
+}
+
+template <typename T>
+static void launch_qk_t(const QkArgs& a, const RopeTab& tab, hipStream_t s) {
+    constexpr int E = Chunk<T>::E;
+    const bool fast = a.half * 2 == a.D && (a.D == 64 || a.D == 128 || a.D == 256) &&
+                      (a.D / 2) % E == 0 && aligned16(a.q) && aligned16(a.k) && aligned16(a.v) &&
+                      aligned16(a.kdst) && aligned16(a.vdst) && a.row_stride % E == 0;
+    const unsigned grid = (unsigned)a.n_tokens;
+    if (fast) {
+        if (a.D == 64) k_qk_fused<T, 64><<<grid, 256, 0, s>>>(a, tab);
+        else if (a.D == 128) k_qk_fused<T, 128><<<grid, 256, 0, s>>>(a, tab);
+        else k_qk_fused<T, 256><<<grid, 256, 0, s>>>(a, tab);
+    } else {
+        k_qk_generic<T><<<grid, 256, 0, s>>>(a, tab);
+    }
+    check_launch();
+}
+
+static void launch_qk(int dtype, QkArgs& a, float base, int rotary_dim, hipStream_t s) {
+    if (a.n_tokens <= 0 || a.D <= 0) return;
+    if (a.D > 2 * kMaxHalf || (a.D & 1) || a.nh < 0 || a.nkv < 0) {
+        set_error(HIP_BRIDGE_EUNSUPPORTED);
+        return;
+    }
+    const int eff = (rotary_dim <= 0 || rotary_dim > a.D) ? a.D : rotary_dim;
+    a.half = eff / 2;
+    if ((a.k && !a.kdst) || (a.v && !a.vdst) || (a.pos_mode != 0 && !a.pos) ||
+        (a.slot_mode == 1 && !a.slot)) {
+        set_error(HIP_BRIDGE_EINVAL);
+        return;
+    }
+    static const RopeTab zero_tab = {};
+    const RopeTab& tab = a.do_rope ? rope_table(base, eff) : zero_tab;
+    if (dtype == HIP_BRIDGE_F32) launch_qk_t<float>(a, tab, s);
+    else if (dtype == HIP_BRIDGE_BF16) launch_qk_t<uint16_t>(a, tab, s);
+    else set_error(HIP_BRIDGE_EUNSUPPORTED);
+}
+
+static QkArgs base_args() {
+    QkArgs a;
+    memset(&a, 0, sizeof(a));
+    a.freq_scale = 1.0f;
+    return a;
+}
+
+}  // namespace zl
+
+using namespace zl;
+
+extern "C" {
+
+void hip_qk_norm_rope_kv(int dtype, void* q, const void* k, const void* v,
+                         const float* q_norm_w, const float* k_norm_w, int v_norm,
+                         void* k_cache, void* v_cache, int64_t cache_rows, int layer_idx,
+                         int max_seq, int max_kv_dim, const int32_t* d_pos, int pos_base,
+                         const int64_t* d_slot, int n_tokens, int num_heads, int num_kv_heads,
+                         int head_dim, int rotary_dim, float freq_base, float freq_scale,
+                         float eps, int use_unit_offset, HipStream_t stream) {
+    QkArgs a = base_args();
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.wq = q_norm_w;
+    a.wk = k_norm_w;
+    a.kdst = k_cache;
+    a.vdst = v_cache;
+    a.cache_rows = cache_rows;
+    a.row_stride = max_kv_dim;
+    a.pos = d_pos;
+    a.pos_mode = d_pos ? 1 : 0;
+    a.pos_base = pos_base;
+    a.slot = d_slot;
+    a.slot_mode = d_slot ? 1 : 0;
+    a.layer_base = (int64_t)layer_idx * max_seq;
+    a.max_seq = max_seq;
+    a.n_tokens = n_tokens;
+    a.nh = q ? num_heads : 0;
+    a.nkv = num_kv_heads;
+    a.D = head_dim;
+    a.do_qnorm = q_norm_w != nullptr;
+    a.do_knorm = k_norm_w != nullptr;
+    a.v_norm = v_norm;
+    a.do_rope = 1;
+    a.uo = use_unit_offset;
+    a.freq_scale = freq_scale;
+    a.eps = eps;
+    if (max_kv_dim < num_kv_heads * head_dim) {
+        set_error(HIP_BRIDGE_EINVAL);
+        return;
+    }
+    launch_qk(dtype, a, freq_base, rotary_dim, stream_of(stream));
+}
+
+// ---- reference-ABI RoPE (in place, f32) ------------------------------------------------
+
+static void rope_common(float* q, float* k, const int* d_pos, int pos, int batch, int nh,
+                        int nkv, int head_dim, int rotary_dim, float base, HipStream_t stream) {
+    if (batch <= 0) return;
+    QkArgs a = base_args();
+    a.q = q;
+    a.k = k;
+    a.kdst = k;
+    a.row_stride = (int64_t)nkv * head_dim;
+    a.pos = d_pos;
+    a.pos_mode = d_pos ? 2 : 0;
+    a.pos_base = pos;
+    a.slot_mode = 2;
+    a.n_tokens = batch;
+    a.nh = q ? nh : 0;
+    a.nkv = k ? nkv : 0;
+    a.D = head_dim;
+    a.do_rope = 1;
+    launch_qk(HIP_BRIDGE_F32, a, base, rotary_dim, stream_of(stream));
+}
+
+void hip_rope(float* q, float* k, int pos, int num_heads, int num_kv_heads, int head_dim,
+              int rotary_dim, float freq_base, HipStream_t stream) {
+    rope_common(q, k, nullptr, pos, 1, num_heads, num_kv_heads, head_dim, rotary_dim, freq_base, stream);
+}
+
+void hip_rope_ind(float* q, float* k, const int* d_pos, int num_heads, int num_kv_heads,
+                  int head_dim, int rotary_dim, float freq_base, HipStream_t stream) {
+    if (!d_pos) {
+        set_error(HIP_BRIDGE_EINVAL);
+        return;
+    }
+    rope_common(q, k, d_pos, 0, 1, num_heads, num_kv_heads, head_dim, rotary_dim, freq_base, stream);
+}
+
+void hip_rope_batched(float* q, float* k, int pos, int batch_size, int num_heads,
+                      int num_kv_heads, int head_dim, int rotary_dim, float freq_base,
+                      HipStream_t stream) {
+    rope_common(q, k, nullptr, pos, batch_size, num_heads, num_kv_heads, head_dim, rotary_dim,
+                freq_base, stream);
+}
+
+// ---- reference-ABI KV append (f32) -----------------------------------------------------
+
+static void kv_put_common(float* kc, float* vc, const float* k, const float* v, int layer,
+                          const int* d_pos, int pos, int batch, int max_seq, int nkv,
+                          int head_dim, int max_kv_dim, HipStream_t stream) {
+    if (batch <= 0 || nkv <= 0 || head_dim <= 0) return;
+    if (!kc || !vc || !k || !v || max_kv_dim < nkv * head_dim) {
+        set_error(HIP_BRIDGE_EINVAL);
+        return;
+    }
+    QkArgs a = base_args();
+    a.k = k;
+    a.v = v;
+    a.kdst = kc;
+    a.vdst = vc;
+    a.row_stride = max_kv_dim;
+    a.pos = d_pos;
+    a.pos_mode = d_pos ? 2 : 0;
+    a.pos_base = pos;
+    a.slot_mode = 0;
+    a.layer_base = (int64_t)layer * max_seq;
+    a.max_seq = max_seq;
+    a.n_tokens = batch;
+    a.nh = 0;
+    a.nkv = nkv;
+    a.D = head_dim;
+    a.do_rope = 0;
+    launch_qk(HIP_BRIDGE_F32, a, 0.0f, 0, stream_of(stream));
+}
+
+void hip_kv_cache_put(float* k_cache, float* v_cache, const float* k, const float* v,
+                      int layer_idx, int pos, int max_seq, int n_kv_heads, int head_dim,
+                      int max_kv_dim, HipStream_t stream) {
+    kv_put_common(k_cache, v_cache, k, v, layer_idx, nullptr, pos, 1, max_seq, n_kv_heads,
+                  head_dim, max_kv_dim, stream);
+}
+
+void hip_kv_cache_put_ind(float* k_cache, float* v_cache, const float* k, const float* v,
+                          int layer_idx, const int* d_pos, int max_seq, int n_kv_heads,
+                          int head_dim, int max_kv_dim, HipStream_t stream) {
+    if (!d_pos) {
+        set_error(HIP_BRIDGE_EINVAL);
+        return;
+    }
+    kv_put_common(k_cache, v_cache, k, v, layer_idx, d_pos, 0, 1, max_seq, n_kv_heads, head_dim,
+                  max_kv_dim, stream);
+}
+
+void hip_kv_cache_put_batched(float* k_cache, float* v_cache, const float* k, const float* v,
+                              int layer_idx, int pos, int batch_size, int max_seq,
+                              int n_kv_heads, int head_dim, int max_kv_dim,
+                              HipStream_t stream) {
+    kv_put_common(k_cache, v_cache, k, v, layer_idx, nullptr, pos, batch_size, max_seq,
+                  n_kv_heads, head_dim, max_kv_dim, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,141 @@
+// Device helpers shared by the hip_bridge kernels (gfx950, wave64).
+//
+// All sources are compiled with -ffp-contract=off: a*b+c is never fused implicitly, so the
+// f32 expressions that mirror ziglm's CPU arithmetic round exactly as written. Where a
+// kernel wants an FMA (sums of squares, polynomial evaluation) it calls fmaf explicitly.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace zl {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+
+// ---- bf16 <-> f32 ------------------------------------------------------------------
+// bf16 is stored as uint16 bit patterns; a 32-bit word holds elements (2j, 2j+1) in its
+// (low, high) halves (little endian).
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// Round-to-nearest-even of two f32 values to bf16 (v_cvt_pk_bf16_f32 on gfx950). For every
+// non-NaN input this equals ziglm's quant.f32ToBf16 ((bits + 0x7FFF + lsb) >> 16); NaN inputs
+// stay NaN here, where the reference formula can carry a NaN payload into +-Inf.
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+    f32x2 v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+
+// ---- 16-byte chunk <-> f32 lanes ---------------------------------------------------
+// A "chunk" is one 128-bit load: 4 f32 or 8 bf16 elements.
+template <typename T> struct Chunk;
+template <> struct Chunk<float> {
+    static constexpr int E = 4;
+    __device__ static __forceinline__ void unpack(const u32x4& r, float* v) {
+        v[0] = __uint_as_float(r.x);
+        v[1] = __uint_as_float(r.y);
+        v[2] = __uint_as_float(r.z);
+        v[3] = __uint_as_float(r.w);
+    }
+    __device__ static __forceinline__ u32x4 pack(const float* v) {
+        u32x4 r;
+        r.x = __float_as_uint(v[0]);
+        r.y = __float_as_uint(v[1]);
+        r.z = __float_as_uint(v[2]);
+        r.w = __float_as_uint(v[3]);
+        return r;
+    }
+};
+template <> struct Chunk<uint16_t> {
+    static constexpr int E = 8;
+    __device__ static __forceinline__ void unpack(const u32x4& r, float* v) {
+        v[0] = bf16_lo(r.x);
+        v[1] = bf16_hi(r.x);
+        v[2] = bf16_lo(r.y);
+        v[3] = bf16_hi(r.y);
+        v[4] = bf16_lo(r.z);
+        v[5] = bf16_hi(r.z);
+        v[6] = bf16_lo(r.w);
+        v[7] = bf16_hi(r.w);
+    }
+    __device__ static __forceinline__ u32x4 pack(const float* v) {
+        u32x4 r;
+        r.x = pack_bf16x2(v[0], v[1]);
+        r.y = pack_bf16x2(v[2], v[3]);
+        r.z = pack_bf16x2(v[4], v[5]);
+        r.w = pack_bf16x2(v[6], v[7]);
+        return r;
+    }
+};
+
+__device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ void st16(void* p, const u32x4& v) { *reinterpret_cast<u32x4*>(p) = v; }
+__device__ __forceinline__ f32x4 ldf4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
+
+// ---- lane-group reductions -----------------------------------------------------------
+// Sum over aligned groups of G lanes (G a power of two <= 64); every lane of a group gets
+// the group total.
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int o = 1; o < G; o <<= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+
+// ---- RMSNorm scalar: inv = 1.0 / sqrt(mean + eps) (math.zig:894-895) --------------------
+// sqrtf and '/' are the correctly rounded IEEE operations under hipcc's defaults
+// (-fhip-fp32-correctly-rounded-divide-sqrt), the same as Zig's @sqrt and '/'.
+__device__ __forceinline__ float rms_inv(float sum_sq, int n, float eps) {
+    float mean = sum_sq / (float)n;
+    return 1.0f / sqrtf(mean + eps);
+}
+
+// ---- tanh / GELU / soft-cap ------------------------------------------------------------
+// Kernel tanh (a fast formulation, not the oracle's musl algorithm; both are accurate to a
+// few ulp, so they agree within the tolerances the tests state):
+//   |x| < 0.625: tanh(x) = x - x^3 q(x^2), q a degree-4 polynomial fitted (Lawson-weighted
+//                least squares in relative error) on [0, 0.625]; <= 0.7 ulp in f32.
+//   otherwise:   1 - 2/(exp(2|x|) + 1) with the hardware exp2 and reciprocal (a few ulp),
+//                sign restored; exp2 overflows to +inf for |x| > 44, giving exactly +-1.
+__device__ __forceinline__ float tanh_fast(float x) {
+    const float ax = fabsf(x);
+    const float x2 = x * x;
+    float q = fmaf(x2, 0.005704984534531832f, -0.02063908614218235f);
+    q = fmaf(x2, q, 0.05373971536755562f);
+    q = fmaf(x2, q, -0.13331441581249237f);
+    q = fmaf(x2, q, 0.3333328068256378f);
+    const float small = fmaf(-x * x2, q, x);
+    const float e = __builtin_amdgcn_exp2f(ax * 2.885390043258667f);  // exp(2|x|)
+    const float big = 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
+    return ax < 0.625f ? small : copysignf(big, x);
+}
+
+// GELU, tanh approximation (math.zig:1119-1123), in the algebraically equal logistic form
+//   0.5 x (1 + tanh(z)) = x / (1 + exp(-2z)),  z = 0.7978845608 (x + 0.044715 x^3),
+// with -2z*log2(e) = x (A + B x^2), A = -2*0.7978845608*log2(e), B = 0.044715*A.
+// No cancellation: relative error a few ulp everywhere. The reference's own 1 + tanh(z)
+// loses up to ~2^-23 absolute for z << 0, which is what the tests' absolute floor covers.
+// x -> -inf: exp2 -> +inf, rcp -> 0, result -0 (the reference gives 0.5x*0 = -0 too).
+__device__ __forceinline__ float gelu_fast(float x) {
+    const float x2 = x * x;
+    const float y = x * fmaf(x2, -0.10294324159622192f, -2.302208185195923f);
+    const float e = __builtin_amdgcn_exp2f(y);
+    return x * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+// Correctly rounded x / b for a divisor b shared by all lanes, given rb = RN(1/b) computed on
+// the host: q0 = x*rb, r = x - b*q0 (exact by FMA), q = q0 + r*rb (Markstein's correction;
+// valid when no intermediate over/underflows, which holds for |x| < 2^100 and
+// 2^-100 < |b| < 2^100). Equals the IEEE quotient the reference computes.
+__device__ __forceinline__ float div_by_uniform(float x, float b, float rb) {
+    const float q0 = x * rb;
+    const float r = fmaf(-b, q0, x);
+    return fmaf(r, rb, q0);
+}
+
+}  // namespace zl

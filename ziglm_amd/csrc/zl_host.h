@@ -1,0 +1,27 @@
+// Host-side helpers shared by the hip_bridge translation units: error recording, launch
+// checks, grid sizing. Not part of the C-ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/hip_bridge.h"
+
+namespace zl {
+
+// Record an op error for hip_bridge_last_error() (thread-local, first error wins until read).
+void set_error(int code);
+
+// After a launch: record hipGetLastError() if the launch failed.
+inline void check_launch() {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) set_error((int)e);
+}
+
+inline hipStream_t stream_of(HipStream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace zl

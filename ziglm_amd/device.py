@@ -1,0 +1,270 @@
+"""Host-side operator interface over the hip_bridge C-ABI.
+
+`HipDevice` mirrors ziglm's `CudaDevice` (src/cuda.zig:227-751): same method names,
+argument order and meaning, one stream created at init, ops enqueued on it and returning
+nothing. `DeviceBuffer` mirrors `CudaBuffer` (cuda.zig:187-225). The fused and bf16 entry
+points that the reference lacks are added under new names. The parity tests drive the
+kernels through this class exactly as cuda_model.zig drives CudaDevice.
+
+Pointer arguments accept a DeviceBuffer, a raw device address (int) or None.
+With strict=True (the default) every op checks hip_bridge_last_error() and raises
+HipError on an argument error; the reference ignores errors, so strict=False restores that.
+"""
+import ctypes
+
+import numpy as np
+
+from . import bridge as _b
+
+
+def _ptr(p):
+    if p is None:
+        return None
+    if isinstance(p, DeviceBuffer):
+        return p.ptr
+    return int(p)
+
+
+class DeviceBuffer:
+    """Device allocation (cuda.zig:187-225 CudaBuffer): upload / copyFrom / download / deinit."""
+
+    def __init__(self, dev, size_bytes, ptr=None, owner=True):
+        self.dev = dev
+        self.size_bytes = int(size_bytes)
+        self.owner = owner
+        if ptr is None:
+            p = ctypes.c_void_p()
+            dev.b.check(dev.b.hip_malloc(ctypes.byref(p), max(1, self.size_bytes)), "hip_malloc")
+            ptr = p.value
+        self.ptr = ptr
+
+    def at(self, offset_bytes):
+        """Non-owning view at a byte offset."""
+        return DeviceBuffer(self.dev, self.size_bytes - offset_bytes, self.ptr + offset_bytes, owner=False)
+
+    def upload(self, host, stream=None):
+        host = np.ascontiguousarray(host)
+        n = min(self.size_bytes, host.nbytes)
+        if n:
+            self.dev.b.check(self.dev.b.hip_memcpy_h2d(self.ptr, host.ctypes.data, n, stream), "upload")
+
+    def copy_from(self, other, copy_len, stream=None):
+        if copy_len:
+            self.dev.b.check(self.dev.b.hip_memcpy_d2d(self.ptr, _ptr(other), copy_len, stream), "copyFrom")
+
+    def download(self, host, stream=None):
+        n = min(self.size_bytes, host.nbytes)
+        if n:
+            self.dev.b.check(self.dev.b.hip_memcpy_d2h(host.ctypes.data, self.ptr, n, stream), "download")
+        return host
+
+    def to_numpy(self, shape, dtype):
+        out = np.empty(shape, dtype)
+        assert out.nbytes <= self.size_bytes
+        self.dev.sync()
+        return self.download(out)
+
+    def fill(self, value=0, stream=None):
+        self.dev.b.check(self.dev.b.hip_fill_u8(self.ptr, value, self.size_bytes, stream), "fill")
+
+    def deinit(self):
+        if self.owner and self.ptr:
+            self.dev.b.hip_free(self.ptr)
+        self.ptr = None
+
+    def __del__(self):
+        try:
+            self.deinit()
+        except Exception:
+            pass
+
+
+class HipDevice:
+    """Mirror of ziglm's CudaDevice over libhip_bridge.so (cuda.zig:227-751)."""
+
+    def __init__(self, strict=True):
+        self.b = _b.load()
+        name = ctypes.create_string_buffer(256)
+        vram = ctypes.c_size_t()
+        if self.b.hip_device_get_info(0, name, 256, ctypes.byref(vram)) != 0:
+            raise _b.HipError("CudaDeviceNotFound equivalent: no HIP device 0")
+        s = ctypes.c_void_p()
+        self.b.check(self.b.hip_stream_create(ctypes.byref(s)), "hip_stream_create")
+        self.stream = s.value
+        self.name = name.value.decode(errors="replace")
+        self.total_vram_bytes = vram.value
+        self.strict = strict
+
+    # -- memory ------------------------------------------------------------------------
+    def alloc(self, size_bytes):
+        return DeviceBuffer(self, size_bytes)
+
+    def from_numpy(self, arr):
+        arr = np.ascontiguousarray(arr)
+        buf = DeviceBuffer(self, arr.nbytes)
+        buf.upload(arr)
+        return buf
+
+    def sync(self):
+        self.b.check(self.b.hip_stream_sync(self.stream), "hip_stream_sync")
+
+    def deinit(self):
+        if self.stream:
+            self.b.hip_stream_destroy(self.stream)
+            self.stream = None
+
+    def _done(self, what):
+        if self.strict:
+            self.b.raise_last_error(what)
+
+    # -- embeddings (cuda.zig:358-380) --------------------------------------------------
+    def embedLookup(self, d_weights, qtype, token_id, d_out, dim, scale_factor):
+        self.b.hip_embed_lookup(_ptr(d_weights), qtype, token_id, _ptr(d_out), dim, scale_factor, self.stream)
+        self._done("embedLookup")
+
+    def embedLookupBatch(self, d_weights, qtype, d_token_ids, d_out, n_tokens, dim, scale_factor):
+        self.b.hip_embed_lookup_batch(_ptr(d_weights), qtype, _ptr(d_token_ids), _ptr(d_out),
+                                      n_tokens, dim, scale_factor, self.stream)
+        self._done("embedLookupBatch")
+
+    def embedGather(self, d_table, qtype, n_rows, d_ids, out_dtype, d_out, n_tokens, dim, scale):
+        """new: bounds-checked gather, f32 or bf16 output."""
+        self.b.hip_embed_gather(_ptr(d_table), qtype, n_rows, _ptr(d_ids), out_dtype, _ptr(d_out),
+                                n_tokens, dim, scale, self.stream)
+        self._done("embedGather")
+
+    # -- norms (cuda.zig:383-445) --------------------------------------------------------
+    def rmsNorm(self, d_x, d_weight, d_out, n, eps, use_unit_offset):
+        self.b.hip_rmsnorm(_ptr(d_x), _ptr(d_weight), _ptr(d_out), n, eps, int(use_unit_offset), self.stream)
+        self._done("rmsNorm")
+
+    def rmsNormBatched(self, d_x, d_weight, d_out, head_dim, count, eps, use_unit_offset):
+        self.b.hip_rmsnorm_batched(_ptr(d_x), _ptr(d_weight), _ptr(d_out), head_dim, count, eps,
+                                   int(use_unit_offset), self.stream)
+        self._done("rmsNormBatched")
+
+    def rmsnormAdd(self, d_x, d_in, d_weight, n, eps, use_unit_offset):
+        self.b.hip_rmsnorm_add(_ptr(d_x), _ptr(d_in), _ptr(d_weight), n, eps, int(use_unit_offset), self.stream)
+        self._done("rmsnormAdd")
+
+    def addRmsNorm(self, d_x, d_residual, d_weight, d_out, n, eps, use_unit_offset):
+        self.b.hip_add_rmsnorm(_ptr(d_x), _ptr(d_residual), _ptr(d_weight), _ptr(d_out), n, eps,
+                               int(use_unit_offset), self.stream)
+        self._done("addRmsNorm")
+
+    def addRmsNormBatched(self, d_x, d_residual, d_weight, d_out, n, batch_size, eps, use_unit_offset):
+        self.b.hip_add_rmsnorm_batched(_ptr(d_x), _ptr(d_residual), _ptr(d_weight), _ptr(d_out), n,
+                                       batch_size, eps, int(use_unit_offset), self.stream)
+        self._done("addRmsNormBatched")
+
+    # new dtype-generic row ops
+    def rmsNormRows(self, dtype, d_x, d_weight, d_out, rows, n, eps, use_unit_offset):
+        self.b.hip_rmsnorm_rows(dtype, _ptr(d_x), _ptr(d_weight), _ptr(d_out), rows, n, eps,
+                                int(use_unit_offset), self.stream)
+        self._done("rmsNormRows")
+
+    def addRmsNormRows(self, dtype, d_x, d_residual, d_weight, d_out, rows, n, eps, use_unit_offset):
+        self.b.hip_add_rmsnorm_rows(dtype, _ptr(d_x), _ptr(d_residual), _ptr(d_weight), _ptr(d_out),
+                                    rows, n, eps, int(use_unit_offset), self.stream)
+        self._done("addRmsNormRows")
+
+    def rmsnormAddRows(self, dtype, d_x, d_in, d_weight, rows, n, eps, use_unit_offset):
+        self.b.hip_rmsnorm_add_rows(dtype, _ptr(d_x), _ptr(d_in), _ptr(d_weight), rows, n, eps,
+                                    int(use_unit_offset), self.stream)
+        self._done("rmsnormAddRows")
+
+    def rmsNormAddRmsNorm(self, dtype, d_x, d_xb, d_w1, d_w2, d_out, rows, n, eps, use_unit_offset):
+        self.b.hip_rmsnorm_add_rmsnorm(dtype, _ptr(d_x), _ptr(d_xb), _ptr(d_w1), _ptr(d_w2),
+                                       _ptr(d_out), rows, n, eps, int(use_unit_offset), self.stream)
+        self._done("rmsNormAddRmsNorm")
+
+    # -- RoPE (cuda.zig:447-488) ---------------------------------------------------------
+    def rope(self, d_q, d_k, pos, num_heads, num_kv_heads, head_dim, rotary_dim, freq_base):
+        self.b.hip_rope(_ptr(d_q), _ptr(d_k), pos, num_heads, num_kv_heads, head_dim, rotary_dim,
+                        freq_base, self.stream)
+        self._done("rope")
+
+    def ropeInd(self, d_q, d_k, d_pos, num_heads, num_kv_heads, head_dim, rotary_dim, freq_base):
+        self.b.hip_rope_ind(_ptr(d_q), _ptr(d_k), _ptr(d_pos), num_heads, num_kv_heads, head_dim,
+                            rotary_dim, freq_base, self.stream)
+        self._done("ropeInd")
+
+    def ropeBatched(self, d_q, d_k, pos, batch_size, num_heads, num_kv_heads, head_dim, rotary_dim,
+                    freq_base):
+        self.b.hip_rope_batched(_ptr(d_q), _ptr(d_k), pos, batch_size, num_heads, num_kv_heads,
+                                head_dim, rotary_dim, freq_base, self.stream)
+        self._done("ropeBatched")
+
+    # -- KV cache (cuda.zig:490-574) -----------------------------------------------------
+    def kvCachePut(self, d_k_cache, d_v_cache, d_k, d_v, layer_idx, pos, max_seq, n_kv_heads,
+                   head_dim, max_kv_dim):
+        self.b.hip_kv_cache_put(_ptr(d_k_cache), _ptr(d_v_cache), _ptr(d_k), _ptr(d_v), layer_idx,
+                                pos, max_seq, n_kv_heads, head_dim, max_kv_dim, self.stream)
+        self._done("kvCachePut")
+
+    def kvCachePutInd(self, d_k_cache, d_v_cache, d_k, d_v, layer_idx, d_pos, max_seq, n_kv_heads,
+                      head_dim, max_kv_dim):
+        self.b.hip_kv_cache_put_ind(_ptr(d_k_cache), _ptr(d_v_cache), _ptr(d_k), _ptr(d_v),
+                                    layer_idx, _ptr(d_pos), max_seq, n_kv_heads, head_dim,
+                                    max_kv_dim, self.stream)
+        self._done("kvCachePutInd")
+
+    def kvCachePutBatched(self, d_k_cache, d_v_cache, d_k, d_v, layer_idx, pos, batch_size,
+                          max_seq, n_kv_heads, head_dim, max_kv_dim):
+        self.b.hip_kv_cache_put_batched(_ptr(d_k_cache), _ptr(d_v_cache), _ptr(d_k), _ptr(d_v),
+                                        layer_idx, pos, batch_size, max_seq, n_kv_heads, head_dim,
+                                        max_kv_dim, self.stream)
+        self._done("kvCachePutBatched")
+
+    # new: fused QK-norm + RoPE + KV append
+    def qkNormRopeKv(self, dtype, d_q, d_k, d_v, d_q_norm_w, d_k_norm_w, v_norm, d_k_cache,
+                     d_v_cache, cache_rows, layer_idx, max_seq, max_kv_dim, d_pos, pos_base,
+                     d_slot, n_tokens, num_heads, num_kv_heads, head_dim, rotary_dim, freq_base,
+                     freq_scale, eps, use_unit_offset):
+        self.b.hip_qk_norm_rope_kv(dtype, _ptr(d_q), _ptr(d_k), _ptr(d_v), _ptr(d_q_norm_w),
+                                   _ptr(d_k_norm_w), int(v_norm), _ptr(d_k_cache), _ptr(d_v_cache),
+                                   cache_rows, layer_idx, max_seq, max_kv_dim, _ptr(d_pos), pos_base,
+                                   _ptr(d_slot), n_tokens, num_heads, num_kv_heads, head_dim,
+                                   rotary_dim, freq_base, freq_scale, eps, int(use_unit_offset),
+                                   self.stream)
+        self._done("qkNormRopeKv")
+
+    # -- activations & elementwise (cuda.zig:686-750) -------------------------------------
+    def geglu(self, d_gate, d_up, d_out, n):
+        self.b.hip_geglu(_ptr(d_gate), _ptr(d_up), _ptr(d_out), n, self.stream)
+        self._done("geglu")
+
+    def gegluEx(self, dtype, d_gate, d_up, d_out, n):
+        self.b.hip_geglu_ex(dtype, _ptr(d_gate), _ptr(d_up), _ptr(d_out), n, self.stream)
+        self._done("gegluEx")
+
+    def add(self, d_x, d_res, n):
+        self.b.hip_add(_ptr(d_x), _ptr(d_res), n, self.stream)
+        self._done("add")
+
+    def scale(self, d_x, s, n):
+        self.b.hip_scale(_ptr(d_x), s, n, self.stream)
+        self._done("scale")
+
+    def tanhSoftcap(self, d_x, cap, n):
+        self.b.hip_tanh_softcap(_ptr(d_x), cap, n, self.stream)
+        self._done("tanhSoftcap")
+
+    def tanhSoftcapEx(self, dtype, d_x, cap, n):
+        self.b.hip_tanh_softcap_ex(dtype, _ptr(d_x), cap, n, self.stream)
+        self._done("tanhSoftcapEx")
+
+    # -- timing ----------------------------------------------------------------------------
+    def event(self):
+        e = ctypes.c_void_p()
+        self.b.check(self.b.hip_event_create(ctypes.byref(e)), "hip_event_create")
+        return e.value
+
+    def record(self, ev):
+        self.b.check(self.b.hip_event_record(ev, self.stream), "hip_event_record")
+
+    def elapsed_ms(self, start, stop):
+        self.b.check(self.b.hip_event_sync(stop), "hip_event_sync")
+        ms = ctypes.c_float()
+        self.b.check(self.b.hip_event_elapsed_ms(ctypes.byref(ms), start, stop), "hip_event_elapsed_ms")
+        return ms.value
