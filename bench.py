@@ -1,0 +1,468 @@
+#!/usr/bin/env python3
+"""bench.py -- ziglm's fused per-layer ops on one MI355X (gfx950).
+
+Headline workload ("c2"): Gemma-4B-shaped 2048-token prefill,
+bf16 activations with f32 arithmetic. One step = one pass of the per-layer fused chain
+(ziglm_amd/layer.py): input RMSNorm, QK-norm+RoPE+KV append, post-attn norm+add+pre-FFN
+norm, GeGLU, post-FFN norm+add. `value` is the chain's algorithmic bytes / time (GB/s).
+
+Measurement rules:
+  * inputs are resident in HBM before the timed region; the timed K steps are captured in
+    one hipGraph and replayed between two HIP events on the op stream;
+  * every step uses its own buffer set, and the sets together exceed the 256 MB Infinity
+    Cache several times, so each op streams from HBM rather than from the last step;
+  * per-op numbers come from graphs of one op alone over the same rotation ("isolated");
+  * the roofline object is the dominant kernel (GeGLU at c2): algorithmic bytes per launch
+    / average launch time over its timed region; `traffic` is the HBM bytes per launch
+    measured with rocprofv3 FETCH_SIZE/WRITE_SIZE (profiles/), or null;
+  * cpu_baseline: the oracle's -O3 x86-64-v3 build (restating ziglm's CPU path), one
+    thread, on a bounded prefix of the same chain.
+Secondary configs (c1 decode, c3 gather, c4 27B shapes, c5 batched decode) are reported
+under "configs" unless --quick.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
+       python bench.py --only OP [--config c2|c4] --steps K   (profiling: one op only)
+"""
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from ziglm_amd import bridge as B  # noqa: E402
+from ziglm_amd import layer as LY  # noqa: E402
+from ziglm_amd import synth  # noqa: E402
+from ziglm_amd.device import HipDevice  # noqa: E402
+
+PEAK_HBM_GBS = 8000.0  # MI355X HBM3E peak
+MALL_BYTES = 256 << 20
+METRIC = "fused-op HBM GB/s (% of MI355X peak) + µs per Gemma layer, decode & 2k prefill"
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------------------------------
+# graph capture + timing
+# ---------------------------------------------------------------------------------------
+
+class Graph:
+    """hipGraph of whatever `body()` enqueues on dev.stream."""
+
+    def __init__(self, dev, body):
+        self.dev, b = dev, dev.b
+        b.check(b.hip_graph_begin_capture(dev.stream), "begin_capture")
+        try:
+            body()
+        finally:
+            g = ctypes.c_void_p()
+            b.check(b.hip_graph_end_capture(dev.stream, ctypes.byref(g)), "end_capture")
+        ex = ctypes.c_void_p()
+        b.check(b.hip_graph_instantiate(ctypes.byref(ex), g), "instantiate")
+        self.graph, self.exec = g.value, ex.value
+
+    def launch(self):
+        self.dev.b.check(self.dev.b.hip_graph_launch(self.exec, self.dev.stream), "graph_launch")
+
+    def destroy(self):
+        self.dev.b.hip_graph_exec_destroy(self.exec)
+        self.dev.b.hip_graph_destroy(self.graph)
+
+
+def time_graph_ms(dev, g, reps=1):
+    e0, e1 = dev.event(), dev.event()
+    dev.record(e0)
+    for _ in range(reps):
+        g.launch()
+    dev.record(e1)
+    ms = dev.elapsed_ms(e0, e1) / reps
+    dev.b.hip_event_destroy(e0)
+    dev.b.hip_event_destroy(e1)
+    return ms
+
+
+def time_launches_us(dev, fn, sets, n_launch, warm=1):
+    """Average microseconds per launch of fn(dev, set) over a graph of n_launch launches
+    cycling through `sets`."""
+    def body():
+        for i in range(n_launch):
+            fn(dev, sets[i % len(sets)])
+    g = Graph(dev, body)
+    for _ in range(warm):
+        g.launch()
+    dev.sync()
+    ms = time_graph_ms(dev, g)
+    g.destroy()
+    return ms * 1000.0 / n_launch
+
+
+# ---------------------------------------------------------------------------------------
+# data
+# ---------------------------------------------------------------------------------------
+
+_POOLS = {}
+
+
+def pool(dtype, seed=1):
+    """Seeded 4M-element N(0,1) pool (bf16 or f32 bytes) tiled into large buffers."""
+    key = (dtype, seed)
+    if key not in _POOLS:
+        n = 1 << 22
+        a = synth.normal_bf16(seed, "pool", (n,)) if dtype == B.BF16 else synth.normal_f32(seed, "pool", (n,))
+        _POOLS[key] = a.view(np.uint8)
+    return _POOLS[key]
+
+
+def fill_tiled(buf, src):
+    """Fill device buffer `buf` by tiling host bytes `src` (H2D once, then D2D doubling)."""
+    n = buf.size_bytes
+    first = min(n, src.nbytes)
+    buf.upload(src[:first])
+    done = first
+    while done < n:
+        c = min(done, n - done)
+        buf.at(done).copy_from(buf, c)
+        done += c
+
+
+def make_sets(dev, shape, T, dtype, min_total=3 * MALL_BYTES, max_sets=8, cache_rows=None, pos0=0):
+    """Buffer sets for the rotation; set 0 seeded, others copies."""
+    L0 = LY.LayerBuffers(dev, shape, T, dtype, cache_rows=cache_rows)
+    per = sum(b.size_bytes for b in (L0.x, L0.xb, L0.ao, L0.fo, L0.q, L0.k, L0.v, L0.gate, L0.up, L0.act))
+    nsets = int(min(max_sets, max(2, math.ceil(min_total / per))))
+    p = pool(dtype)
+    for name in ("x", "xb", "ao", "fo", "q", "k", "v", "gate", "up", "act"):
+        fill_tiled(getattr(L0, name), p)
+    for k in L0.w:
+        L0.w[k].upload(synth.normal_f32(1, "w_" + k, (shape.H,), 0, 0.1))
+    L0.wq.upload(synth.normal_f32(1, "wq", (shape.D,), 0, 0.1))
+    L0.wk.upload(synth.normal_f32(1, "wk", (shape.D,), 0, 0.1))
+    L0.pos.upload(np.arange(pos0, pos0 + T, dtype=np.int32))
+    L0.kc.fill(0)
+    L0.vc.fill(0)
+    sets = [L0]
+    for _ in range(nsets - 1):
+        L = LY.LayerBuffers(dev, shape, T, dtype, cache_rows=cache_rows)
+        L.copy_from(L0)
+        L.kc.fill(0)
+        L.vc.fill(0)
+        sets.append(L)
+    dev.sync()
+    return sets, per
+
+
+def free_sets(sets):
+    from ziglm_amd.device import DeviceBuffer
+    for L in sets:
+        for v in list(vars(L).values()):
+            if isinstance(v, DeviceBuffer):
+                v.deinit()
+        for v in L.w.values():
+            v.deinit()
+
+
+# ---------------------------------------------------------------------------------------
+# prefill chain configs (c2, c4)
+# ---------------------------------------------------------------------------------------
+
+def bench_prefill(dev, shape, T, dtype, steps, warmup, ops_launches=40):
+    es = 4 if dtype == B.F32 else 2
+    sets, per = make_sets(dev, shape, T, dtype)
+    log(f"{shape.name} T={T}: {len(sets)} buffer sets x {per / 1e6:.0f} MB")
+    nb = LY.op_bytes(shape, T, es)
+    ops = {}
+    for name in ("input_norm", "add_rmsnorm", "qk_norm_rope_kv", "norm_add_norm", "geglu", "norm_add",
+                 "norm_add_norm_next"):
+        us = time_launches_us(dev, LY.OPS[name], sets, max(ops_launches, len(sets) * 4))
+        ops[name] = {"us": round(us, 3), "bytes": nb[name], "GBps": round(nb[name] / us / 1e3, 1),
+                     "frac_peak": round(nb[name] / us / 1e3 / PEAK_HBM_GBS, 4)}
+        log(f"  {name:20s} {us:9.2f} us  {nb[name] / us / 1e3:8.1f} GB/s")
+
+    def steps_graph(n):
+        def body():
+            for i in range(n):
+                LY.run_chain(dev, sets[i % len(sets)])
+        return Graph(dev, body)
+
+    gw = steps_graph(max(1, warmup))
+    gw.launch()
+    dev.sync()
+    gw.destroy()
+    g = steps_graph(steps)
+    dev.sync()
+    ms = time_graph_ms(dev, g)  # exactly `steps` chain passes between the two events
+    g.destroy()
+    chain_b = LY.chain_bytes(shape, T, es)
+    fused_b = LY.chain_bytes(shape, T, es, fused=True)
+
+    gf = Graph(dev, lambda: [LY.run_chain(dev, sets[i % len(sets)], fused=True) for i in range(steps)])
+    gf.launch()
+    dev.sync()
+    ms_f = time_graph_ms(dev, gf)
+    gf.destroy()
+    isolated = sum(ops[k]["us"] for k in LY.CHAIN)
+    res = {
+        "T": T, "shape": shape.name, "io_dtype": "bf16" if dtype == B.BF16 else "f32",
+        "ms_per_step": ms / steps,
+        "chain_bytes": chain_b,
+        "chain_GBps": chain_b / (ms / steps) / 1e6,
+        "us_per_layer": round(ms / steps * 1000, 2),
+        "us_per_layer_isolated_sum": round(isolated, 2),
+        "us_per_layer_fused_4op": round(ms_f / steps * 1000, 2),
+        "fused_chain_bytes": fused_b,
+        "ops": ops,
+        "buffer_sets": len(sets),
+    }
+    free_sets(sets)
+    return res
+
+
+# ---------------------------------------------------------------------------------------
+# c1 / c5: decode (f32)
+# ---------------------------------------------------------------------------------------
+
+def bench_decode(dev, B_, pos_seed=4, n_launch=200):
+    """Batched decode on Gemma-4B shapes, f32, each sequence at its own position
+    (~U[0,32767]) with a per-sequence KV cache of 32768 rows; per-op and per-layer us,
+    plus final RMSNorm + soft-cap 30*tanh(z/30) on f32[B x 262144] logits."""
+    s = LY.GEMMA_4B
+    max_seq = 32768
+    L = LY.LayerBuffers(dev, s, B_, B.F32, cache_rows=B_ * max_seq)
+    p = pool(B.F32)
+    for name in ("x", "xb", "ao", "fo", "q", "k", "v", "gate", "up", "act"):
+        fill_tiled(getattr(L, name), p)
+    for k in L.w:
+        L.w[k].upload(synth.normal_f32(4, "w_" + k, (s.H,), 0, 0.1))
+    L.wq.upload(synth.normal_f32(4, "wq", (s.D,), 0, 0.1))
+    L.wk.upload(synth.normal_f32(4, "wk", (s.D,), 0, 0.1))
+    pos = synth.uniform_int(pos_seed, "pos", (B_,), 0, max_seq - 1).astype(np.int32)
+    slots = np.arange(B_, dtype=np.int64) * max_seq + pos
+    L.pos.upload(pos)
+    d_slot = dev.from_numpy(slots)
+
+    def qk(dev_, L_):
+        dev_.qkNormRopeKv(B.F32, L_.q, L_.k, L_.v, L_.wq, L_.wk, 0, L_.kc, L_.vc, L_.cache_rows, 0,
+                          max_seq, s.nkv * s.D, L_.pos, 0, d_slot, L_.T, s.nh, s.nkv, s.D, 0, s.theta,
+                          1.0, s.eps, s.uo)
+
+    fns = {"input_norm": LY.op_input_norm, "qk_norm_rope_kv": qk, "norm_add_norm": LY.op_norm_add_norm,
+           "geglu": LY.op_geglu, "norm_add": LY.op_norm_add}
+    nb = LY.op_bytes(s, B_, 4)
+    nb["qk_norm_rope_kv"] += 8 * B_  # slot table
+    ops = {}
+    for name, fn in fns.items():
+        us = time_launches_us(dev, fn, [L], n_launch)
+        ops[name] = {"us": round(us, 3), "GBps": round(nb[name] / us / 1e3, 2)}
+    chain_us = time_launches_us(dev, lambda d, L_: [fns[k](d, L_) for k in LY.CHAIN], [L], n_launch // 5)
+    # final norm + soft-cap on the logits
+    V = 262144
+    logits = dev.alloc(B_ * V * 4)
+    fill_tiled(logits, (synth.normal_f32(4, "logits", (1 << 20,), 0, 15.0)).view(np.uint8))
+    nbuf = max(1, min(8, math.ceil(3 * MALL_BYTES / logits.size_bytes)))
+    bufs = [logits] + [dev.alloc(logits.size_bytes) for _ in range(nbuf - 1)]
+    for bb in bufs[1:]:
+        bb.copy_from(logits, logits.size_bytes)
+    us_cap = time_launches_us(dev, lambda d, buf: d.tanhSoftcap(buf, 30.0, B_ * V), bufs, max(16, 2 * nbuf))
+    us_fnorm = time_launches_us(dev, LY.op_input_norm, [L], n_launch)
+    for bb in bufs:
+        bb.deinit()
+    free_sets([L])
+    cap_bytes = 2 * 4 * B_ * V
+    return {"B": B_, "us_per_layer": round(chain_us, 2), "ops": ops,
+            "final_norm_us": round(us_fnorm, 3),
+            "softcap": {"us": round(us_cap, 2), "bytes": cap_bytes,
+                        "GBps": round(cap_bytes / us_cap / 1e3, 1),
+                        "frac_peak": round(cap_bytes / us_cap / 1e3 / PEAK_HBM_GBS, 4)}}
+
+
+# ---------------------------------------------------------------------------------------
+# c3: embedding gather
+# ---------------------------------------------------------------------------------------
+
+def bench_gather(dev, vocab=262144, dim=2560, n_tok=4096, n_rep=64):
+    out = {}
+    scale = np.float32(np.sqrt(np.float32(dim)))
+    nsets = 8
+    id_sets = [dev.from_numpy(synth.gather_ids(2 + i, n_tok, vocab, n_repeat=n_rep)) for i in range(nsets)]
+    outs = [dev.alloc(n_tok * dim * 4) for _ in range(nsets)]
+    for qt, name, rb in ((B.Q8_0, "q8_0", dim // 32 * 34), (B.Q4_0, "q4_0", dim // 32 * 18),
+                         (B.BF16, "bf16", dim * 2)):
+        tab = dev.alloc(vocab * rb)
+        if qt == B.BF16:
+            fill_tiled(tab, pool(B.BF16))
+        else:  # 64 seeded rows tiled over the vocabulary (finite block scales)
+            row = (synth.q8_0_table if qt == B.Q8_0 else synth.q4_0_table)(2, 64, dim)
+            fill_tiled(tab, row.reshape(-1))
+
+        def g(dev_, i, tab=tab, qt=qt):
+            dev_.embedGather(tab, qt, vocab, id_sets[i], B.F32, outs[i], n_tok, dim, scale)
+        sets = list(range(nsets))
+        us = time_launches_us(dev, g, sets, 4 * nsets)
+        nbytes = n_tok * (rb + dim * 4) + 4 * n_tok
+        out[name] = {"us": round(us, 2), "bytes": nbytes, "GBps": round(nbytes / us / 1e3, 1),
+                     "frac_peak": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4)}
+        log(f"  gather {name}: {us:.2f} us {nbytes / us / 1e3:.0f} GB/s")
+        tab.deinit()
+    for o in outs + id_sets:
+        o.deinit()
+    return out
+
+
+# ---------------------------------------------------------------------------------------
+# CPU baseline (oracle, -O3 -march=x86-64-v3, one thread)
+# ---------------------------------------------------------------------------------------
+
+def cpu_baseline(shape, T_full, target_s=12.0):
+    from oracle import oracle as O
+    o = O.get(simd=True)
+    s = shape
+
+    def run(T):
+        x = synth.normal_bf16(1, "x", (T, s.H))
+        ao = synth.normal_bf16(1, "ao", (T, s.H))
+        fo = synth.normal_bf16(1, "fo", (T, s.H))
+        q = synth.normal_bf16(1, "q", (T, s.nh, s.D))
+        k = synth.normal_bf16(1, "k", (T, s.nkv, s.D))
+        v = synth.normal_bf16(1, "v", (T, s.nkv, s.D))
+        gate = synth.normal_bf16(1, "gate", (T, s.I))
+        up = synth.normal_bf16(1, "up", (T, s.I))
+        w = {k_: synth.normal_f32(1, "w_" + k_, (s.H,), 0, 0.1) for k_ in ("in", "post_attn", "pre_ffn", "post_ffn")}
+        wq = synth.normal_f32(1, "wq", (s.D,), 0, 0.1)
+        wk = synth.normal_f32(1, "wk", (s.D,), 0, 0.1)
+        kc = np.zeros((s.max_seq, s.nkv * s.D), np.uint16)
+        vc = np.zeros_like(kc)
+        pos = np.arange(T, dtype=np.int32)
+        t0 = time.perf_counter()
+        o.rms_norm_bf16(x, w["in"], s.eps, True)
+        o.qk_norm_rope_kv(q, k, v, wq, wk, kc, vc, max_seq=s.max_seq, max_kv_dim=s.nkv * s.D, pos=pos,
+                          n_heads=s.nh, n_kv_heads=s.nkv, head_dim=s.D, base=s.theta, eps=s.eps)
+        x2, _ = o.rms_norm_add_rms_norm(x, ao, w["post_attn"], w["pre_ffn"], s.eps, True)
+        o.geglu(gate, up)
+        o.rms_norm_add(x2, fo, w["post_ffn"], s.eps, True)
+        return time.perf_counter() - t0
+
+    t_small = run(8)
+    T = int(min(T_full, max(8, 8 * target_s / max(t_small, 1e-6))))
+    t = run(T)
+    nbytes = LY.chain_bytes(shape, T, 2)
+    return {"value": round(nbytes / t / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"c2 per-layer chain over the first {T} of {T_full} tokens ({t:.1f} s), "
+                      f"oracle -O3 -march=x86-64-v3, one thread",
+            "us_per_token": round(t / T * 1e6, 1)}
+
+
+# ---------------------------------------------------------------------------------------
+
+def host_cpu():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def load_traffic():
+    p = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(p):
+        with open(p) as f:
+            return json.load(f)
+    return {}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--quick", action="store_true", help="headline config only")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", default=None, help="run one op only (profiling)")
+    ap.add_argument("--config", default="c2", choices=["c2", "c4"])
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {a.gpus} is not supported in this build "
+              f"(the fused per-layer ops need no inter-GPU exchange; see DESIGN.md on sharding)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    dev = HipDevice()
+    log(f"device {dev.name} {dev.total_vram_bytes / 2**30:.0f} GiB, {dev.b.version()}")
+    shape, T = (LY.GEMMA_4B, 2048) if a.config == "c2" else (LY.GEMMA_27B, 8192)
+
+    if a.only:
+        sets, _ = make_sets(dev, shape, T, B.BF16)
+        us = time_launches_us(dev, LY.OPS[a.only], sets, a.steps)
+        nb = LY.op_bytes(shape, T, 2)[a.only]
+        print(json.dumps({"op": a.only, "config": a.config, "us": us, "bytes": nb, "GBps": nb / us / 1e3}))
+        return
+
+    t_start = time.time()
+    c2 = bench_prefill(dev, shape, T, B.BF16, a.steps, a.warmup)
+    gl = c2["ops"]["geglu"]
+    traffic = load_traffic().get("geglu_c2")
+    result = {
+        "metric": METRIC,
+        "value": round(c2["chain_GBps"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(c2["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded SplitMix64/Box-Muller pool, bf16 storage)",
+        "config": {"workload": f"{a.config}: {shape.name}-shaped {T}-token prefill, per-layer fused chain "
+                               f"(input norm, QK-norm+RoPE+KV, norm+add+norm, GeGLU, norm+add)",
+                   "tokens": T, "hidden": shape.H, "heads": f"{shape.nh}/{shape.nkv}x{shape.D}",
+                   "intermediate": shape.I, "io_dtype": "bf16", "parallelism": "single GPU"},
+        "frac_peak": round(c2["chain_GBps"] / PEAK_HBM_GBS, 4),
+        "us_per_layer": c2["us_per_layer"],
+        "us_per_layer_isolated_sum": c2["us_per_layer_isolated_sum"],
+        "us_per_layer_fused_4op": c2["us_per_layer_fused_4op"],
+        "roofline": {"bound": "hbm", "achieved": gl["GBps"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gl["GBps"] / PEAK_HBM_GBS, 4),
+                     "traffic": traffic,
+                     "kernel": "k_ew<bf16,GEGLU> (GeGLU, c2 [2048x10240])",
+                     "bytes_per_launch": gl["bytes"], "us_per_launch": gl["us"]},
+        "ops": c2["ops"],
+    }
+    if not a.quick:
+        cfgs = {}
+        log("c3 gather")
+        cfgs["c3_gather"] = bench_gather(dev)
+        log("c4 27B prefill")
+        c4 = bench_prefill(dev, LY.GEMMA_27B, 8192, B.BF16, max(4, a.steps // 4), 2)
+        cfgs["c4_prefill"] = {k: c4[k] for k in ("us_per_layer", "us_per_layer_isolated_sum",
+                                                 "us_per_layer_fused_4op", "chain_GBps", "ops")}
+        cfgs["c4_prefill"]["chain_GBps"] = round(cfgs["c4_prefill"]["chain_GBps"], 1)
+        log("c1/c5 decode")
+        cfgs["c5_decode"] = {}
+        for b_ in (1, 8, 64, 256):
+            cfgs["c5_decode"][f"B{b_}"] = bench_decode(dev, b_)
+            log(f"  B={b_}: {cfgs['c5_decode'][f'B{b_}']['us_per_layer']} us/layer")
+        result["configs"] = cfgs
+    if not a.no_cpu:
+        log("cpu baseline")
+        cb = cpu_baseline(shape, T)
+        cb["host_cpu"] = host_cpu()
+        cb["nproc"] = os.cpu_count()
+        result["cpu_baseline"] = cb
+    result["wall_s"] = round(time.time() - t_start, 1)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -52,6 +52,7 @@ _SIGS = {
     "zo_rms_norm_bf16": (None, [_u16p, _fp, _u16p, _sz, _sz, _f, _i]),
     "zo_rms_norm_add_rms_norm_bf16": (None, [_u16p, _u16p, _fp, _fp, _sz, _sz, _f, _i]),
     "zo_rms_norm_add_rms_norm": (None, [_fp, _fp, _fp, _fp, _sz, _sz, _f, _i]),
+    "zo_rms_norm_add_bf16": (None, [_u16p, _u16p, _fp, _sz, _sz, _f, _i]),
     "zo_geglu_bf16": (None, [_u16p, _u16p, _u16p, _sz]),
     "zo_qk_norm_rope_kv": (
         None,
@@ -153,7 +154,14 @@ class Oracle:
         return x, out
 
     def rms_norm_add(self, x, inp, w, eps, unit_offset=True):
-        """Returns x + rmsNorm(inp) row-wise (model.zig:748-755)."""
+        """Returns x + rmsNorm(inp) row-wise (model.zig:748-755); f32 or bf16 (uint16)."""
+        if x.dtype == np.uint16:
+            x = np.array(x, copy=True, order="C")
+            inp = np.ascontiguousarray(inp, dtype=np.uint16)
+            n = x.shape[-1]
+            self.lib.zo_rms_norm_add_bf16(self.u16(x), self.u16(inp), self.fp(w), x.size // n, n,
+                                          eps, int(unit_offset))
+            return x
         x = np.array(x, dtype=np.float32, copy=True, order="C")
         inp = np.ascontiguousarray(inp, dtype=np.float32)
         n = x.shape[-1]

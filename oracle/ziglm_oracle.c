@@ -592,6 +592,20 @@ void zo_rms_norm_add_rms_norm_bf16(uint16_t* x, uint16_t* xb, const float* w1, c
     free(bf);
 }
 
+void zo_rms_norm_add_bf16(uint16_t* x, const uint16_t* in, const float* w, size_t rows, size_t n,
+                          float eps, int uo) {
+    float* xf = (float*)malloc(n * sizeof(float));
+    float* bf = (float*)malloc(n * sizeof(float));
+    for (size_t row = 0; row < rows; ++row) {
+        zo_bf16_to_f32_n(x + row * n, xf, n);
+        zo_bf16_to_f32_n(in + row * n, bf, n);
+        zo_rms_norm_add(xf, bf, w, n, eps, uo);
+        zo_f32_to_bf16_n(xf, x + row * n, n);
+    }
+    free(xf);
+    free(bf);
+}
+
 void zo_geglu_bf16(const uint16_t* gate, const uint16_t* up, uint16_t* out, size_t n) {
     for (size_t i = 0; i < n; ++i)
         out[i] = zo_f32_to_bf16(zo_gelu(zo_bf16_to_f32(gate[i])) * zo_bf16_to_f32(up[i]));

@@ -84,6 +84,8 @@ void zo_rms_norm_add_rms_norm_bf16(uint16_t* x, uint16_t* xb, const float* w1, c
                                    size_t rows, size_t n, float eps, int unit_offset);
 void zo_rms_norm_add_rms_norm(float* x, float* xb, const float* w1, const float* w2, size_t rows,
                               size_t n, float eps, int unit_offset);
+void zo_rms_norm_add_bf16(uint16_t* x, const uint16_t* in, const float* w, size_t rows, size_t n,
+                          float eps, int unit_offset);
 void zo_geglu_bf16(const uint16_t* gate, const uint16_t* up, uint16_t* out, size_t n);
 
 /* Token-batched fused QK-norm + RoPE + KV append, f32 or bf16 (dtype: 0 f32, 1 bf16).

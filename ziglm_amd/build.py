@@ -58,18 +58,27 @@ def compile_one(src, extra=()):
     return obj, out
 
 
-def build_bridge(verbose=False, jobs=None):
+def build_bridge(verbose=False, jobs=None, out=LIB, defines=()):
+    """Compile all sources and link `out`; `defines` are extra -D flags (variants)."""
     os.makedirs(BUILD, exist_ok=True)
     jobs = jobs or min(len(SOURCES), os.cpu_count() or 4)
+    extra = tuple(f"-D{d}" for d in defines)
+    tag = "_".join(d.replace("=", "") for d in defines)
+
+    def one(src):
+        obj = os.path.join(BUILD, os.path.splitext(src)[0] + (f".{tag}" if tag else "") + ".o")
+        cmd = [HIPCC, *HIP_FLAGS, *extra, "-c", os.path.join(CSRC, src), "-o", obj]
+        return obj, _run(cmd)
+
     with cf.ThreadPoolExecutor(jobs) as ex:
-        results = list(ex.map(compile_one, SOURCES))
-    for obj, out in results:
-        if out and verbose:
-            print(out)
-    tmp = LIB + ".tmp"
+        results = list(ex.map(one, SOURCES))
+    for obj, msg in results:
+        if msg and verbose:
+            print(msg)
+    tmp = out + ".tmp"
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *[o for o, _ in results]])
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, out)
+    return out
 
 
 def build_oracle():

@@ -50,8 +50,8 @@ __global__ __launch_bounds__(kEwThreads) void k_ew(EwArgs args) {
     for (int u = 0; u < kEwUnroll; ++u) {
         idx[u] = ((int64_t)blockIdx.x * kEwUnroll + u) * kEwThreads + threadIdx.x;
         if (idx[u] < nch) {
-            ra[u] = ld16(A + idx[u] * E);
-            if constexpr (kTwo) rb[u] = ld16(B + idx[u] * E);
+            ra[u] = lds16(A + idx[u] * E);
+            if constexpr (kTwo) rb[u] = lds16(B + idx[u] * E);
         }
     }
 #pragma unroll
@@ -62,7 +62,7 @@ __global__ __launch_bounds__(kEwThreads) void k_ew(EwArgs args) {
             if constexpr (kTwo) C::unpack(rb[u], y);
 #pragma unroll
             for (int j = 0; j < E; ++j) x[j] = ew1<OP>(x[j], kTwo ? y[j] : 0.0f, args);
-            st16(O + idx[u] * E, C::pack(x));
+            sts16(O + idx[u] * E, C::pack(x));
         }
     }
     // scalar tail

@@ -32,12 +32,12 @@ template <typename OutT>
 __device__ __forceinline__ void store8(OutT* orow, int64_t e, const float* v);
 template <>
 __device__ __forceinline__ void store8<float>(float* orow, int64_t e, const float* v) {
-    st16(orow + e, Chunk<float>::pack(v));
-    st16(orow + e + 4, Chunk<float>::pack(v + 4));
+    sts16(orow + e, Chunk<float>::pack(v));
+    sts16(orow + e + 4, Chunk<float>::pack(v + 4));
 }
 template <>
 __device__ __forceinline__ void store8<uint16_t>(uint16_t* orow, int64_t e, const float* v) {
-    st16(orow + e, Chunk<uint16_t>::pack(v));
+    sts16(orow + e, Chunk<uint16_t>::pack(v));
 }
 
 // Dequantise elements [e, e+8) of a row staged at `row` in LDS, multiplied by `scale`.
@@ -129,7 +129,7 @@ __global__ __launch_bounds__(256) void k_gather_blocks(const unsigned char* __re
         if (id >= 0 && id < n_rows) {
             const unsigned char* grow = table + id * (int64_t)row_bytes;
             if (vec16) {
-                for (int i = lane; i < (row_bytes >> 4); i += kWave) st16(srow + 16 * i, ld16(grow + 16 * i));
+                for (int i = lane; i < (row_bytes >> 4); i += kWave) st16(srow + 16 * i, lds16(grow + 16 * i));
             } else {
                 for (int i = lane; i < row_bytes; i += kWave) srow[i] = grow[i];
             }
@@ -171,7 +171,7 @@ __global__ __launch_bounds__(256) void k_gather_dense(const unsigned char* __res
     for (int c = lane; c < dim / EPC; c += kWave) {
         float v[8];
         if (valid) {
-            const u32x4 r = ld16(grow + 16 * c);
+            const u32x4 r = lds16(grow + 16 * c);
             if constexpr (QT == HIP_BRIDGE_F32) {
                 Chunk<float>::unpack(r, v);
             } else if constexpr (QT == HIP_BRIDGE_BF16) {
@@ -192,7 +192,7 @@ __global__ __launch_bounds__(256) void k_gather_dense(const unsigned char* __res
         }
         if constexpr (EPC == 4) {
             if constexpr (sizeof(OutT) == 4) {
-                st16(orow + 4 * c, Chunk<float>::pack(v));
+                sts16(orow + 4 * c, Chunk<float>::pack(v));
             } else {
                 uint32_t* o32 = reinterpret_cast<uint32_t*>(orow + 4 * c);
                 o32[0] = pack_bf16x2(v[0], v[1]);

@@ -2,17 +2,20 @@
 // (math.zig:850-988): sum of squares in f32, mean = sum/n, inv = 1.0/sqrt(mean + eps) with
 // IEEE sqrt and divide, out = (x*inv)*(1+w) | (x*inv)*w | x*inv (weight NULL).
 //
-// Modes (one kernel family, one wave per row):
+// Modes (one kernel family):
 //   NORM           out = norm(x)                                   (rmsNorm, rmsNormBatched)
 //   ADD_NORM       s = x + r; x = s; out = norm(s)                 (addRmsNorm, model.zig:714-723)
 //   NORM_ADD       x = x + norm(r)                                 (rmsnormAdd, model.zig:748-755)
 //   NORM_ADD_NORM  s = x + norm(r; w1); x = s; out = norm(s; w2)   (post-attn norm + add +
 //                  pre-FFN norm, cuda_model.zig:930-942; post-FFN norm + add + next input norm)
-// The whole row lives in registers: each lane loads chunks lane, lane+64, ... with 128-bit
-// loads, so x and r are read from HBM once and x/out written once. The row statistics are
-// a wave64 butterfly sum. Weights (f32, shared by all rows) come from L2.
-// Rows that are not 16-byte aligned, or longer than 24 chunks per lane (f32 > 6144,
-// bf16 > 12288 elements), use a block-per-row kernel that re-reads the row from L2.
+// The whole row lives in registers: rows of >= 256 chunks (128-bit loads) get a 256-thread
+// block (4 waves; wave butterfly sums, then a 4-float LDS exchange), shorter rows one wave
+// each; a lane owns chunks g, g+64W, ... so x and r are read from HBM once and x/out
+// written once, with every load of the row issued before the first use. The weights (f32,
+// shared by all rows, L2-resident) are loaded as 128-bit vectors up front and turned into
+// per-element factors (1+w), w or 1. Rows that are not 16-byte aligned, or longer than 16
+// chunks per lane (f32 > 16384, bf16 > 32768 elements), use a block-per-row kernel that
+// re-reads the row from L2.
 // Aliasing: out may alias r (the reference calls addRmsNorm(x, xb, w, out=xb)) or x in
 // NORM mode; every lane reads its chunks before writing the same chunks.
 #include "zl_common.h"
@@ -42,13 +45,38 @@ __device__ __forceinline__ float apply_w(float v, float inv, const float* w, int
     return uo ? y * (1.0f + wi) : y * wi;
 }
 
-template <typename T, int NC, int MODE>
+// Sum over the W waves of a row: wave butterfly, then (W > 1) partials through LDS, added
+// in wave order. `slot` is this row's W-float LDS area.
+template <int W>
+__device__ __forceinline__ float row_sum(float v, float* slot) {
+    v = group_sum<kWave>(v);
+    if constexpr (W == 1) {
+        return v;
+    } else {
+        const int wave = (threadIdx.x >> 6) % W;
+        if ((threadIdx.x & 63) == 0) slot[wave] = v;
+        __syncthreads();
+        float t = slot[0];
+#pragma unroll
+        for (int i = 1; i < W; ++i) t += slot[i];
+        __syncthreads();
+        return t;
+    }
+}
+
+// W waves per row (W in {1, 4}), 256 threads per block, 4/W rows per block. Lane g of a row
+// (g in [0, 64W)) owns chunks g, g + 64W, ... (NC of them at most).
+template <typename T, int NC, int MODE, int W>
 __global__ __launch_bounds__(256) void k_norm_rows(NormArgs a) {
     using C = Chunk<T>;
     constexpr int E = C::E;
-    const int lane = threadIdx.x & 63;
-    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= a.rows) return;
+    constexpr int RPB = 4 / W;  // rows per block
+    constexpr int STRIDE = kWave * W;
+    __shared__ float s_red[4];
+    const int rib = (threadIdx.x >> 6) / W;  // row within block
+    const int g = threadIdx.x - rib * STRIDE;
+    const int64_t row = (int64_t)blockIdx.x * RPB + rib;
+    const bool row_ok = row < a.rows;
     const int n = a.n;
     const int nch = n / E;
     T* xrow = (T*)a.x + row * n;
@@ -56,15 +84,23 @@ __global__ __launch_bounds__(256) void k_norm_rows(NormArgs a) {
     T* orow = (T*)a.out + row * n;
     const bool has_w1 = a.w1 != nullptr;
     const bool has_w2 = a.w2 != nullptr;
+    float* slot = s_red + rib * W;
 
+    // Issue every HBM load of the row, then the (L2-resident) weights.
     u32x4 rx[NC], rr[NC];
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-        const int idx = lane + c * kWave;
-        if (idx < nch) {
-            rx[c] = ld16(xrow + (int64_t)idx * E);
-            if constexpr (MODE != M_NORM) rr[c] = ld16(rrow + (int64_t)idx * E);
+        const int idx = g + c * STRIDE;
+        if (row_ok && idx < nch) {
+            rx[c] = lds16(xrow + (int64_t)idx * E);
+            if constexpr (MODE != M_NORM) rr[c] = lds16(rrow + (int64_t)idx * E);
         }
+    }
+    float f1[NC][E];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int idx = g + c * STRIDE;
+        if (row_ok && idx < nch) load_factors<E>(a.w1, (int64_t)idx * E, has_w1, a.uo, f1[c]);
     }
 
     // v: the vector normalised first.
@@ -72,8 +108,8 @@ __global__ __launch_bounds__(256) void k_norm_rows(NormArgs a) {
     float ss = 0.0f;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-        const int idx = lane + c * kWave;
-        if (idx < nch) {
+        const int idx = g + c * STRIDE;
+        if (row_ok && idx < nch) {
             if constexpr (MODE == M_NORM) {
                 C::unpack(rx[c], v[c]);
             } else if constexpr (MODE == M_ADD_NORM) {
@@ -89,59 +125,65 @@ __global__ __launch_bounds__(256) void k_norm_rows(NormArgs a) {
             for (int j = 0; j < E; ++j) ss = fmaf(v[c][j], v[c][j], ss);
         }
     }
-    ss = group_sum<kWave>(ss);
+    ss = row_sum<W>(ss, slot);
     const float inv = rms_inv(ss, n, a.eps);
 
     if constexpr (MODE == M_NORM || MODE == M_ADD_NORM) {
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
-            const int idx = lane + c * kWave;
-            if (idx < nch) {
+            const int idx = g + c * STRIDE;
+            if (row_ok && idx < nch) {
                 float y[E];
 #pragma unroll
-                for (int j = 0; j < E; ++j) y[j] = apply_w(v[c][j], inv, a.w1, idx * E + j, a.uo, has_w1);
-                if constexpr (MODE == M_ADD_NORM) st16(xrow + (int64_t)idx * E, C::pack(v[c]));
-                st16(orow + (int64_t)idx * E, C::pack(y));
+                for (int j = 0; j < E; ++j) y[j] = (v[c][j] * inv) * f1[c][j];
+                if constexpr (MODE == M_ADD_NORM) sts16(xrow + (int64_t)idx * E, C::pack(v[c]));
+                sts16(orow + (int64_t)idx * E, C::pack(y));
             }
         }
     } else if constexpr (MODE == M_NORM_ADD) {
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
-            const int idx = lane + c * kWave;
-            if (idx < nch) {
+            const int idx = g + c * STRIDE;
+            if (row_ok && idx < nch) {
                 float xv[E];
                 C::unpack(rx[c], xv);
 #pragma unroll
-                for (int j = 0; j < E; ++j) xv[j] = xv[j] + apply_w(v[c][j], inv, a.w1, idx * E + j, a.uo, has_w1);
-                st16(xrow + (int64_t)idx * E, C::pack(xv));
+                for (int j = 0; j < E; ++j) xv[j] = xv[j] + (v[c][j] * inv) * f1[c][j];
+                sts16(xrow + (int64_t)idx * E, C::pack(xv));
             }
         }
     } else {  // M_NORM_ADD_NORM
+        float f2[NC][E];
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const int idx = g + c * STRIDE;
+            if (row_ok && idx < nch) load_factors<E>(a.w2, (int64_t)idx * E, has_w2, a.uo, f2[c]);
+        }
         float ss2 = 0.0f;
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
-            const int idx = lane + c * kWave;
-            if (idx < nch) {
+            const int idx = g + c * STRIDE;
+            if (row_ok && idx < nch) {
                 float xv[E];
                 C::unpack(rx[c], xv);
 #pragma unroll
                 for (int j = 0; j < E; ++j) {
-                    v[c][j] = xv[j] + apply_w(v[c][j], inv, a.w1, idx * E + j, a.uo, has_w1);
+                    v[c][j] = xv[j] + (v[c][j] * inv) * f1[c][j];
                     ss2 = fmaf(v[c][j], v[c][j], ss2);
                 }
             }
         }
-        ss2 = group_sum<kWave>(ss2);
+        ss2 = row_sum<W>(ss2, slot);
         const float inv2 = rms_inv(ss2, n, a.eps);
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
-            const int idx = lane + c * kWave;
-            if (idx < nch) {
+            const int idx = g + c * STRIDE;
+            if (row_ok && idx < nch) {
                 float y[E];
 #pragma unroll
-                for (int j = 0; j < E; ++j) y[j] = apply_w(v[c][j], inv2, a.w2, idx * E + j, a.uo, has_w2);
-                st16(xrow + (int64_t)idx * E, C::pack(v[c]));
-                st16(orow + (int64_t)idx * E, C::pack(y));
+                for (int j = 0; j < E; ++j) y[j] = (v[c][j] * inv2) * f2[c][j];
+                sts16(xrow + (int64_t)idx * E, C::pack(v[c]));
+                sts16(orow + (int64_t)idx * E, C::pack(y));
             }
         }
     }
@@ -227,19 +269,32 @@ __global__ __launch_bounds__(256) void k_norm_rows_generic(NormArgs a) {
     }
 }
 
+template <typename T, int MODE, int W>
+static void launch_w(const NormArgs& a, int per_lane, hipStream_t s) {
+    const unsigned grid = (unsigned)cdiv(a.rows, 4 / W);
+    if (per_lane <= 1) k_norm_rows<T, 1, MODE, W><<<grid, 256, 0, s>>>(a);
+    else if (per_lane <= 2) k_norm_rows<T, 2, MODE, W><<<grid, 256, 0, s>>>(a);
+    else if (per_lane <= 4 || W == 1) k_norm_rows<T, 4, MODE, W><<<grid, 256, 0, s>>>(a);
+    else if constexpr (W == 4) {
+        if (per_lane <= 8) k_norm_rows<T, 8, MODE, W><<<grid, 256, 0, s>>>(a);
+        else k_norm_rows<T, 16, MODE, W><<<grid, 256, 0, s>>>(a);
+    }
+}
+
+// Rows of at least 256 chunks get a whole 256-thread block (4 waves, LDS cross-wave sum);
+// shorter rows (per-head norms) get one wave each, four rows per block.
 template <typename T, int MODE>
 static void launch_t(const NormArgs& a, hipStream_t s) {
     constexpr int E = Chunk<T>::E;
     const int nch = a.n / E;
-    const int per_lane = (int)cdiv(nch, kWave);
+    const int W = nch >= 256 ? 4 : 1;
+    const int per_lane = (int)cdiv(nch, kWave * W);
     const bool vec = a.n % E == 0 && aligned16(a.x) && (MODE == M_NORM || aligned16(a.r)) &&
-                     (MODE == M_NORM_ADD || aligned16(a.out)) && per_lane <= 24;
+                     (MODE == M_NORM_ADD || aligned16(a.out)) && aligned16(a.w1) &&
+                     (MODE != M_NORM_ADD_NORM || aligned16(a.w2)) && per_lane <= 16;
     if (vec) {
-        const unsigned grid = (unsigned)cdiv(a.rows, 4);
-        if (per_lane <= 2) k_norm_rows<T, 2, MODE><<<grid, 256, 0, s>>>(a);
-        else if (per_lane <= 6) k_norm_rows<T, 6, MODE><<<grid, 256, 0, s>>>(a);
-        else if (per_lane <= 12) k_norm_rows<T, 12, MODE><<<grid, 256, 0, s>>>(a);
-        else k_norm_rows<T, 24, MODE><<<grid, 256, 0, s>>>(a);
+        if (W == 4) launch_w<T, MODE, 4>(a, per_lane, s);
+        else launch_w<T, MODE, 1>(a, per_lane, s);
     } else {
         k_norm_rows_generic<T, MODE><<<(unsigned)a.rows, 256, 0, s>>>(a);
     }

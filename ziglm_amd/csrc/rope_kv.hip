@@ -124,9 +124,16 @@ __global__ __launch_bounds__(256) void k_qk_fused(QkArgs a, RopeTab tab) {
     u32x4 ra = {0, 0, 0, 0}, rb = {0, 0, 0, 0};
     if (gslot < HR && active(gslot)) {
         const T* src = src_of(gslot);
-        ra = ld16(src + hl * E);
-        rb = ld16(src + HALF + hl * E);
+        ra = lds16(src + hl * E);
+        rb = lds16(src + HALF + hl * E);
     }
+    // This lane's norm factors ((1+w), w or 1) for Q and K: fixed offsets hl*E and
+    // HALF + hl*E in every head, so they are loaded once.
+    float fq0[E], fq1[E], fk0[E], fk1[E];
+    load_factors<E>(a.wq, hl * E, a.wq != nullptr, a.uo, fq0);
+    load_factors<E>(a.wq, HALF + hl * E, a.wq != nullptr, a.uo, fq1);
+    load_factors<E>(a.wk, hl * E, a.wk != nullptr, a.uo, fk0);
+    load_factors<E>(a.wk, HALF + hl * E, a.wk != nullptr, a.uo, fk1);
     if (a.do_rope) fill_cos_sin(tab, (float)p * a.freq_scale, HALF, s_cos, s_sin);
     __syncthreads();
 
@@ -134,8 +141,8 @@ __global__ __launch_bounds__(256) void k_qk_fused(QkArgs a, RopeTab tab) {
         if (!active(hr)) continue;
         if (hr != gslot) {
             const T* src = src_of(hr);
-            ra = ld16(src + hl * E);
-            rb = ld16(src + HALF + hl * E);
+            ra = lds16(src + hl * E);
+            rb = lds16(src + HALF + hl * E);
         }
         const int kind = hr < a.nh ? 0 : hr < a.nh + a.nkv ? 1 : 2;  // Q, K, V
         float x0[E], x1[E];
@@ -151,20 +158,19 @@ __global__ __launch_bounds__(256) void k_qk_fused(QkArgs a, RopeTab tab) {
             }
             ss = group_sum<LH>(ss);
             const float inv = rms_inv(ss, D, a.eps);
-            const float* w = kind == 0 ? a.wq : kind == 1 ? a.wk : nullptr;
-            if (w) {
-                const int i0 = hl * E;
-#pragma unroll
-                for (int j = 0; j < E; ++j) {
-                    const float w0 = w[i0 + j], w1 = w[HALF + i0 + j];
-                    x0[j] = a.uo ? (x0[j] * inv) * (1.0f + w0) : (x0[j] * inv) * w0;
-                    x1[j] = a.uo ? (x1[j] * inv) * (1.0f + w1) : (x1[j] * inv) * w1;
-                }
-            } else {
+            if (kind == 2) {  // Gemma-4 V: no-scale norm
 #pragma unroll
                 for (int j = 0; j < E; ++j) {
                     x0[j] = x0[j] * inv;
                     x1[j] = x1[j] * inv;
+                }
+            } else {
+                const float* f0 = kind == 0 ? fq0 : fk0;
+                const float* f1 = kind == 0 ? fq1 : fk1;
+#pragma unroll
+                for (int j = 0; j < E; ++j) {
+                    x0[j] = (x0[j] * inv) * f0[j];
+                    x1[j] = (x1[j] * inv) * f1[j];
                 }
             }
         }
@@ -181,8 +187,8 @@ __global__ __launch_bounds__(256) void k_qk_fused(QkArgs a, RopeTab tab) {
         if (kind == 0) dst = (T*)a.q + ((int64_t)t * a.nh + hr) * D;
         else if (kind == 1) dst = (T*)a.kdst + row * a.row_stride + (int64_t)(hr - a.nh) * D;
         else dst = (T*)a.vdst + row * a.row_stride + (int64_t)(hr - a.nh - a.nkv) * D;
-        st16(dst + hl * E, C::pack(x0));
-        st16(dst + HALF + hl * E, C::pack(x1));
+        sts16(dst + hl * E, C::pack(x0));
+        sts16(dst + HALF + hl * E, C::pack(x1));
     }
 }
 
@@ -310,7 +316,8 @@ static void launch_qk_t(const QkArgs& a, const RopeTab& tab, hipStream_t s) {
     constexpr int E = Chunk<T>::E;
     const bool fast = a.half * 2 == a.D && (a.D == 64 || a.D == 128 || a.D == 256) &&
                       (a.D / 2) % E == 0 && aligned16(a.q) && aligned16(a.k) && aligned16(a.v) &&
-                      aligned16(a.kdst) && aligned16(a.vdst) && a.row_stride % E == 0;
+                      aligned16(a.kdst) && aligned16(a.vdst) && aligned16(a.wq) && aligned16(a.wk) &&
+                      a.row_stride % E == 0;
     const unsigned grid = (unsigned)a.n_tokens;
     if (fast) {
         if (a.D == 64) k_qk_fused<T, 64><<<grid, 256, 0, s>>>(a, tab);

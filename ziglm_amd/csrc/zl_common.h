@@ -75,6 +75,27 @@ template <> struct Chunk<uint16_t> {
 
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 __device__ __forceinline__ void st16(void* p, const u32x4& v) { *reinterpret_cast<u32x4*>(p) = v; }
+
+// Streaming (single-use) activations: nontemporal 128-bit loads and stores (the "nt" cache
+// policy: no retention in L2 for data read or written exactly once). Measured on MI355X
+// for GeGLU-shaped traffic: +8% bandwidth at 126 MB, +7% at 1 GB.
+#ifndef ZL_STREAM_NT
+#define ZL_STREAM_NT 1
+#endif
+__device__ __forceinline__ u32x4 lds16(const void* p) {
+#if ZL_STREAM_NT
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+#else
+    return *reinterpret_cast<const u32x4*>(p);
+#endif
+}
+__device__ __forceinline__ void sts16(void* p, const u32x4& v) {
+#if ZL_STREAM_NT
+    __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+#else
+    *reinterpret_cast<u32x4*>(p) = v;
+#endif
+}
 __device__ __forceinline__ f32x4 ldf4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
 
 // ---- lane-group reductions -----------------------------------------------------------
@@ -93,6 +114,29 @@ __device__ __forceinline__ float group_sum(float v) {
 __device__ __forceinline__ float rms_inv(float sum_sq, int n, float eps) {
     float mean = sum_sq / (float)n;
     return 1.0f / sqrtf(mean + eps);
+}
+
+// Per-element factor of one chunk: 1 + w, w, or 1 when there is no weight. Multiplying by
+// 1.0 is exact, so (x*inv)*1 equals the reference's no-scale x*inv bit for bit.
+template <int E>
+__device__ __forceinline__ void load_factors(const float* w, int64_t e0, bool has_w, int uo, float* f) {
+    if (has_w) {
+#pragma unroll
+        for (int q = 0; q < E / 4; ++q) {
+            const f32x4 v = ldf4(w + e0 + 4 * q);
+            f[4 * q + 0] = v.x;
+            f[4 * q + 1] = v.y;
+            f[4 * q + 2] = v.z;
+            f[4 * q + 3] = v.w;
+        }
+        if (uo) {
+#pragma unroll
+            for (int j = 0; j < E; ++j) f[j] = 1.0f + f[j];
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < E; ++j) f[j] = 1.0f;
+    }
 }
 
 // ---- tanh / GELU / soft-cap ------------------------------------------------------------

@@ -27,27 +27,52 @@ def stream_seed(config_seed, name):
     return ((int(config_seed) << 32) ^ zlib.crc32(name.encode())) & 0xFFFFFFFFFFFFFFFF
 
 
+_CHUNK = 1 << 20
+
+
 def splitmix64(seed, n, offset=0):
-    """n consecutive SplitMix64 outputs of stream `seed` starting at element `offset`."""
-    with np.errstate(over="ignore"):
-        i = np.arange(offset + 1, offset + n + 1, dtype=np.uint64)
-        z = np.uint64(seed) + i * _GOLD
-        z = (z ^ (z >> np.uint64(30))) * _M1
-        z = (z ^ (z >> np.uint64(27))) * _M2
-        return z ^ (z >> np.uint64(31))
+    """n consecutive SplitMix64 outputs of stream `seed` starting at element `offset`.
+    Computed in place over 1M-element chunks (fresh large arrays are slow to fault in)."""
+    out = np.empty(n, np.uint64)
+    tmp = np.empty(min(n, _CHUNK), np.uint64)
+    s = np.uint64(seed)
+    for c0 in range(0, n, _CHUNK):
+        m = min(_CHUNK, n - c0)
+        z, t = out[c0:c0 + m], tmp[:m]
+        z[:] = np.arange(offset + c0 + 1, offset + c0 + m + 1, dtype=np.uint64)
+        np.multiply(z, _GOLD, out=z)
+        np.add(z, s, out=z)
+        np.right_shift(z, np.uint64(30), out=t)
+        np.bitwise_xor(z, t, out=z)
+        np.multiply(z, _M1, out=z)
+        np.right_shift(z, np.uint64(27), out=t)
+        np.bitwise_xor(z, t, out=z)
+        np.multiply(z, _M2, out=z)
+        np.right_shift(z, np.uint64(31), out=t)
+        np.bitwise_xor(z, t, out=z)
+    return out
 
 
 def uniform(seed, n):
     """float64 uniforms in [0, 1)."""
-    return (splitmix64(seed, n) >> np.uint64(11)).astype(np.float64) * (2.0 ** -53)
+    z = splitmix64(seed, n)
+    np.right_shift(z, np.uint64(11), out=z)
+    u = z.astype(np.float64)
+    u *= 2.0 ** -53
+    return u
 
 
 def normal_f32(config_seed, name, shape, mu=0.0, sigma=1.0):
     n = int(np.prod(shape))
     u = uniform(stream_seed(config_seed, name), 2 * n)
-    u1, u2 = u[0::2], u[1::2]
-    z = np.sqrt(-2.0 * np.log1p(-u1)) * np.cos(2.0 * np.pi * u2)
-    return (mu + sigma * z).astype(np.float32).reshape(shape)
+    out = np.empty(n, np.float32)
+    for c0 in range(0, n, _CHUNK):
+        m = min(_CHUNK, n - c0)
+        u1 = u[2 * c0:2 * (c0 + m):2]
+        u2 = u[2 * c0 + 1:2 * (c0 + m):2]
+        z = np.sqrt(-2.0 * np.log1p(-u1)) * np.cos(2.0 * np.pi * u2)
+        out[c0:c0 + m] = mu + sigma * z
+    return out.reshape(shape)
 
 
 def uniform_f32(config_seed, name, shape, lo, hi):
@@ -59,9 +84,11 @@ def uniform_f32(config_seed, name, shape, lo, hi):
 def uniform_int(config_seed, name, shape, lo, hi):
     """Integers uniform in [lo, hi] (inclusive), by multiply-shift of the top 32 bits."""
     n = int(np.prod(shape))
-    z = splitmix64(stream_seed(config_seed, name), n) >> np.uint64(32)
-    span = np.uint64(hi - lo + 1)
-    return (np.int64(lo) + ((z * span) >> np.uint64(32)).astype(np.int64)).reshape(shape)
+    z = splitmix64(stream_seed(config_seed, name), n)
+    np.right_shift(z, np.uint64(32), out=z)
+    np.multiply(z, np.uint64(hi - lo + 1), out=z)
+    np.right_shift(z, np.uint64(32), out=z)
+    return (np.int64(lo) + z.astype(np.int64)).reshape(shape)
 
 
 def f32_to_bf16(x):
