@@ -425,3 +425,26 @@ def test_add_scale_mirrors(dev):
     assert_bitexact(d_x.to_numpy((n,), np.float32), (x + r).astype(np.float32), "add")
     dev.scale(d_x, np.float32(0.37), n)
     assert_bitexact(d_x.to_numpy((n,), np.float32), ((x + r) * np.float32(0.37)).astype(np.float32), "scale")
+
+
+@pytest.mark.parametrize("base", [10000.0, 1e6])
+@pytest.mark.parametrize("D", [256, 128, 64])
+def test_rope_angles_bitexact(dev, oracle, base, D):
+    """RoPE alone (no norm): the angle recipe (denominator, IEEE divide, f64 cos/sin rounded
+    to f32) and the no-FMA rotation are shared with the oracle, so the outputs are expected
+    bit-identical; any difference must be a single-ulp cos/sin rounding tie (< 1e-4 of
+    elements) and within the 1e-5 pair-norm tolerance."""
+    nh, nkv = 4, 2
+    positions = [0, 1, 2, 17, 100, 1234, 2047, 4095, 8191, 16383, 32767]
+    q = synth.normal_f32(11, "q", (len(positions), nh, D))
+    k = synth.normal_f32(11, "k", (len(positions), nkv, D))
+    qr = np.stack([oracle.apply_rope(q[i], k[i], p, D, 0, nh, nkv, base)[0] for i, p in enumerate(positions)])
+    kr = np.stack([oracle.apply_rope(q[i], k[i], p, D, 0, nh, nkv, base)[1] for i, p in enumerate(positions)])
+    d_q, d_k = dev.from_numpy(q), dev.from_numpy(k)
+    for i, p in enumerate(positions):
+        dev.rope(d_q.at(i * nh * D * 4), d_k.at(i * nkv * D * 4), p, nh, nkv, D, 0, base)
+    gq, gk = d_q.to_numpy(q.shape, np.float32), d_k.to_numpy(k.shape, np.float32)
+    for g, r, name in ((gq, qr, "Q"), (gk, kr, "K")):
+        assert_rel(g, r, 1e-5, floor=pair_floor(r, D, 0), what=f"rope {name}")
+        diff = np.count_nonzero(g.view(np.uint32) != r.view(np.uint32))
+        assert diff <= max(1, g.size // 10000), f"rope {name}: {diff} of {g.size} not bit-identical"

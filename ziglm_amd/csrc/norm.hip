@@ -8,10 +8,10 @@
 //   NORM_ADD       x = x + norm(r)                                 (rmsnormAdd, model.zig:748-755)
 //   NORM_ADD_NORM  s = x + norm(r; w1); x = s; out = norm(s; w2)   (post-attn norm + add +
 //                  pre-FFN norm, cuda_model.zig:930-942; post-FFN norm + add + next input norm)
-// The whole row lives in registers: rows of >= 256 chunks (128-bit loads) get a 256-thread
-// block (4 waves; wave butterfly sums, then a 4-float LDS exchange), shorter rows one wave
-// each; a lane owns chunks g, g+64W, ... so x and r are read from HBM once and x/out
-// written once, with every load of the row issued before the first use. The weights (f32,
+// The whole row lives in registers: W = 1, 2 or 4 waves per row (wave reductions by
+// DPP/permlane, then a W-float LDS exchange); a lane owns chunks g, g+64W, ... so x and r
+// are read from HBM once and x/out written once, with every load of the row issued before
+// the first use. The weights (f32,
 // shared by all rows, L2-resident) are loaded as 128-bit vectors up front and turned into
 // per-element factors (1+w), w or 1. Rows that are not 16-byte aligned, or longer than 16
 // chunks per lane (f32 > 16384, bf16 > 32768 elements), use a block-per-row kernel that
@@ -45,8 +45,9 @@ __device__ __forceinline__ float apply_w(float v, float inv, const float* w, int
     return uo ? y * (1.0f + wi) : y * wi;
 }
 
-// Sum over the W waves of a row: wave butterfly, then (W > 1) partials through LDS, added
-// in wave order. `slot` is this row's W-float LDS area.
+// Sum over the W waves of a row: wave reduction, then (W > 1) the W partials through LDS,
+// added in wave order. Each reduction of a kernel uses its own LDS slot, so one barrier per
+// reduction suffices (no slot is rewritten while another wave may still read it).
 template <int W>
 __device__ __forceinline__ float row_sum(float v, float* slot) {
     v = group_sum<kWave>(v);
@@ -59,12 +60,11 @@ __device__ __forceinline__ float row_sum(float v, float* slot) {
         float t = slot[0];
 #pragma unroll
         for (int i = 1; i < W; ++i) t += slot[i];
-        __syncthreads();
         return t;
     }
 }
 
-// W waves per row (W in {1, 4}), 256 threads per block, 4/W rows per block. Lane g of a row
+// W waves per row (W in {1, 2, 4}), 256 threads per block, 4/W rows per block. Lane g of a row
 // (g in [0, 64W)) owns chunks g, g + 64W, ... (NC of them at most).
 template <typename T, int NC, int MODE, int W>
 __global__ __launch_bounds__(256) void k_norm_rows(NormArgs a) {
@@ -72,7 +72,7 @@ __global__ __launch_bounds__(256) void k_norm_rows(NormArgs a) {
     constexpr int E = C::E;
     constexpr int RPB = 4 / W;  // rows per block
     constexpr int STRIDE = kWave * W;
-    __shared__ float s_red[4];
+    __shared__ float s_red[2][4];
     const int rib = (threadIdx.x >> 6) / W;  // row within block
     const int g = threadIdx.x - rib * STRIDE;
     const int64_t row = (int64_t)blockIdx.x * RPB + rib;
@@ -84,7 +84,8 @@ __global__ __launch_bounds__(256) void k_norm_rows(NormArgs a) {
     T* orow = (T*)a.out + row * n;
     const bool has_w1 = a.w1 != nullptr;
     const bool has_w2 = a.w2 != nullptr;
-    float* slot = s_red + rib * W;
+    float* slot1 = s_red[0] + rib * W;
+    float* slot2 = s_red[1] + rib * W;
 
     // Issue every HBM load of the row, then the (L2-resident) weights.
     u32x4 rx[NC], rr[NC];
@@ -100,7 +101,15 @@ __global__ __launch_bounds__(256) void k_norm_rows(NormArgs a) {
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
         const int idx = g + c * STRIDE;
-        if (row_ok && idx < nch) load_factors<E>(a.w1, (int64_t)idx * E, has_w1, a.uo, f1[c]);
+        if (row_ok && idx < nch) load_w<E>(a.w1, (int64_t)idx * E, has_w1, f1[c]);
+    }
+    float f2[MODE == M_NORM_ADD_NORM ? NC : 1][E];
+    if constexpr (MODE == M_NORM_ADD_NORM) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const int idx = g + c * STRIDE;
+            if (row_ok && idx < nch) load_w<E>(a.w2, (int64_t)idx * E, has_w2, f2[c]);
+        }
     }
 
     // v: the vector normalised first.
@@ -125,7 +134,7 @@ __global__ __launch_bounds__(256) void k_norm_rows(NormArgs a) {
             for (int j = 0; j < E; ++j) ss = fmaf(v[c][j], v[c][j], ss);
         }
     }
-    ss = row_sum<W>(ss, slot);
+    ss = row_sum<W>(ss, slot1);
     const float inv = rms_inv(ss, n, a.eps);
 
     if constexpr (MODE == M_NORM || MODE == M_ADD_NORM) {
@@ -135,7 +144,7 @@ __global__ __launch_bounds__(256) void k_norm_rows(NormArgs a) {
             if (row_ok && idx < nch) {
                 float y[E];
 #pragma unroll
-                for (int j = 0; j < E; ++j) y[j] = (v[c][j] * inv) * f1[c][j];
+                for (int j = 0; j < E; ++j) y[j] = (v[c][j] * inv) * w_factor(f1[c][j], has_w1, a.uo);
                 if constexpr (MODE == M_ADD_NORM) sts16(xrow + (int64_t)idx * E, C::pack(v[c]));
                 sts16(orow + (int64_t)idx * E, C::pack(y));
             }
@@ -148,17 +157,11 @@ __global__ __launch_bounds__(256) void k_norm_rows(NormArgs a) {
                 float xv[E];
                 C::unpack(rx[c], xv);
 #pragma unroll
-                for (int j = 0; j < E; ++j) xv[j] = xv[j] + (v[c][j] * inv) * f1[c][j];
+                for (int j = 0; j < E; ++j) xv[j] = xv[j] + (v[c][j] * inv) * w_factor(f1[c][j], has_w1, a.uo);
                 sts16(xrow + (int64_t)idx * E, C::pack(xv));
             }
         }
     } else {  // M_NORM_ADD_NORM
-        float f2[NC][E];
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-            const int idx = g + c * STRIDE;
-            if (row_ok && idx < nch) load_factors<E>(a.w2, (int64_t)idx * E, has_w2, a.uo, f2[c]);
-        }
         float ss2 = 0.0f;
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
@@ -168,12 +171,12 @@ __global__ __launch_bounds__(256) void k_norm_rows(NormArgs a) {
                 C::unpack(rx[c], xv);
 #pragma unroll
                 for (int j = 0; j < E; ++j) {
-                    v[c][j] = xv[j] + (v[c][j] * inv) * f1[c][j];
+                    v[c][j] = xv[j] + (v[c][j] * inv) * w_factor(f1[c][j], has_w1, a.uo);
                     ss2 = fmaf(v[c][j], v[c][j], ss2);
                 }
             }
         }
-        ss2 = row_sum<W>(ss2, slot);
+        ss2 = row_sum<W>(ss2, slot2);
         const float inv2 = rms_inv(ss2, n, a.eps);
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
@@ -181,7 +184,7 @@ __global__ __launch_bounds__(256) void k_norm_rows(NormArgs a) {
             if (row_ok && idx < nch) {
                 float y[E];
 #pragma unroll
-                for (int j = 0; j < E; ++j) y[j] = (v[c][j] * inv2) * f2[c][j];
+                for (int j = 0; j < E; ++j) y[j] = (v[c][j] * inv2) * w_factor(f2[c][j], has_w2, a.uo);
                 sts16(xrow + (int64_t)idx * E, C::pack(v[c]));
                 sts16(orow + (int64_t)idx * E, C::pack(y));
             }
@@ -274,26 +277,36 @@ static void launch_w(const NormArgs& a, int per_lane, hipStream_t s) {
     const unsigned grid = (unsigned)cdiv(a.rows, 4 / W);
     if (per_lane <= 1) k_norm_rows<T, 1, MODE, W><<<grid, 256, 0, s>>>(a);
     else if (per_lane <= 2) k_norm_rows<T, 2, MODE, W><<<grid, 256, 0, s>>>(a);
-    else if (per_lane <= 4 || W == 1) k_norm_rows<T, 4, MODE, W><<<grid, 256, 0, s>>>(a);
-    else if constexpr (W == 4) {
-        if (per_lane <= 8) k_norm_rows<T, 8, MODE, W><<<grid, 256, 0, s>>>(a);
-        else k_norm_rows<T, 16, MODE, W><<<grid, 256, 0, s>>>(a);
-    }
+    else if (per_lane <= 4) k_norm_rows<T, 4, MODE, W><<<grid, 256, 0, s>>>(a);
+    else if (per_lane <= 8) k_norm_rows<T, 8, MODE, W><<<grid, 256, 0, s>>>(a);
+    else if constexpr (W == 4) k_norm_rows<T, 16, MODE, W><<<grid, 256, 0, s>>>(a);
 }
 
-// Rows of at least 256 chunks get a whole 256-thread block (4 waves, LDS cross-wave sum);
-// shorter rows (per-head norms) get one wave each, four rows per block.
+// Waves per row: the fewest (1, 2 or 4) that keep a row within 4 chunks (128-bit loads)
+// per lane, so a row lives in registers with few cross-wave reductions; rows longer than
+// 4 chunks per lane at 4 waves take up to 16. NORM_ADD_NORM (two reductions) takes one
+// wave per row up to 8 chunks per lane: measured at 2048 x 2560 bf16 this keeps every row
+// resident at once (8.8 us against 11.4 us with 2 or 4 waves per row, which need a second
+// round of blocks at their occupancy). ZL_NORM_WAVES_PER_ROW forces a value.
+#ifndef ZL_NORM_WAVES_PER_ROW
+#define ZL_NORM_WAVES_PER_ROW 0
+#endif
 template <typename T, int MODE>
 static void launch_t(const NormArgs& a, hipStream_t s) {
     constexpr int E = Chunk<T>::E;
     const int nch = a.n / E;
-    const int W = nch >= 256 ? 4 : 1;
+    int W = ZL_NORM_WAVES_PER_ROW;
+    if (W == 0) {
+        if (MODE == M_NORM_ADD_NORM && nch <= 8 * kWave) W = 1;
+        else W = nch <= 4 * kWave ? 1 : nch <= 8 * kWave ? 2 : 4;
+    }
     const int per_lane = (int)cdiv(nch, kWave * W);
     const bool vec = a.n % E == 0 && aligned16(a.x) && (MODE == M_NORM || aligned16(a.r)) &&
                      (MODE == M_NORM_ADD || aligned16(a.out)) && aligned16(a.w1) &&
-                     (MODE != M_NORM_ADD_NORM || aligned16(a.w2)) && per_lane <= 16;
+                     (MODE != M_NORM_ADD_NORM || aligned16(a.w2)) && per_lane <= (W == 4 ? 16 : 8);
     if (vec) {
         if (W == 4) launch_w<T, MODE, 4>(a, per_lane, s);
+        else if (W == 2) launch_w<T, MODE, 2>(a, per_lane, s);
         else launch_w<T, MODE, 1>(a, per_lane, s);
     } else {
         k_norm_rows_generic<T, MODE><<<(unsigned)a.rows, 256, 0, s>>>(a);

@@ -18,7 +18,8 @@
 // and 64/LH heads per wave. Lane l of a head holds chunk l (elements [lE, lE+E)) and chunk
 // l + LH (the same offsets + head_dim/2), so every RoPE pair is inside one lane; the norm
 // statistic is an LH-lane butterfly. The token's cos/sin table (head_dim/2 entries) is
-// computed once in LDS while the first head's loads are in flight.
+// computed once in LDS while the first head's loads are in flight; its denominators are
+// evaluated per lane (rope_denom), so that phase has no memory operand to wait for.
 // Generic path (partial rotary, other head sizes up to 512, any alignment): one wave per
 // head, head staged in LDS.
 #include <math.h>
@@ -34,6 +35,16 @@ constexpr int kMaxHalf = 256;  // head_dim <= 512
 struct RopeTab {
     float denom[kMaxHalf];
 };
+
+// D_i = f32(base^(f32(2i)/f32(eff))) evaluated in double precision as exp2(e_i * log2(base)),
+// with log2(base) computed once on the host (double). The double result is within ~1e-15
+// relative of the exact power, so its f32 rounding equals the oracle's f32(pow(base, e_i))
+// except within ~1e-15 of an f32 rounding tie (tests/test_gpu_parity.py checks RoPE outputs
+// bit for bit). Computed per lane, no memory access.
+__device__ __forceinline__ float rope_denom(int i, int eff, double log2_base) {
+    const float e = (float)(2 * i) / (float)eff;
+    return (float)exp2((double)e * log2_base);
+}
 
 struct QkArgs {
     void* q;
@@ -55,6 +66,7 @@ struct QkArgs {
     int n_tokens, nh, nkv, D, half;
     int do_qnorm, do_knorm, v_norm, do_rope, uo;
     float freq_scale, eps;
+    double log2_base;
 };
 
 __device__ __forceinline__ int token_pos(const QkArgs& a, int t) {
@@ -89,7 +101,7 @@ __device__ __forceinline__ void fill_cos_sin(const RopeTab& tab, float pos_f, in
 }
 
 template <typename T, int D>
-__global__ __launch_bounds__(256) void k_qk_fused(QkArgs a, RopeTab tab) {
+__global__ __launch_bounds__(256) void k_qk_fused(QkArgs a) {
     using C = Chunk<T>;
     constexpr int E = C::E;
     constexpr int HALF = D / 2;
@@ -97,6 +109,7 @@ __global__ __launch_bounds__(256) void k_qk_fused(QkArgs a, RopeTab tab) {
     constexpr int G = kWave / LH; // heads per wave
     static_assert(LH >= 1 && LH <= kWave && (LH & (LH - 1)) == 0, "bad head layout");
     __shared__ float s_cos[HALF], s_sin[HALF];
+    __shared__ __attribute__((aligned(16))) float s_wq[D], s_wk[D];
 
     const int t = blockIdx.x;
     const int lane = threadIdx.x & 63;
@@ -120,21 +133,38 @@ __global__ __launch_bounds__(256) void k_qk_fused(QkArgs a, RopeTab tab) {
         return a.v != nullptr && row >= 0;
     };
 
-    // Prefetch the first head row, then build the cos/sin table while it is in flight.
+    // Issue the first head row's HBM loads and the weights, then evaluate the token's
+    // cos/sin table (no memory operands) while they are in flight.
+    const int ti = threadIdx.x;
     u32x4 ra = {0, 0, 0, 0}, rb = {0, 0, 0, 0};
     if (gslot < HR && active(gslot)) {
         const T* src = src_of(gslot);
         ra = lds16(src + hl * E);
         rb = lds16(src + HALF + hl * E);
     }
-    // This lane's norm factors ((1+w), w or 1) for Q and K: fixed offsets hl*E and
-    // HALF + hl*E in every head, so they are loaded once.
-    float fq0[E], fq1[E], fk0[E], fk1[E];
-    load_factors<E>(a.wq, hl * E, a.wq != nullptr, a.uo, fq0);
-    load_factors<E>(a.wq, HALF + hl * E, a.wq != nullptr, a.uo, fq1);
-    load_factors<E>(a.wk, hl * E, a.wk != nullptr, a.uo, fk0);
-    load_factors<E>(a.wk, HALF + hl * E, a.wk != nullptr, a.uo, fk1);
-    if (a.do_rope) fill_cos_sin(tab, (float)p * a.freq_scale, HALF, s_cos, s_sin);
+    // The norm weights go to LDS (read there per head, not held in registers): one f32x4
+    // per thread (threads [0, D/4) stage wq, [D/4, D/2) stage wk; D <= 256 fits 256 threads).
+    const bool has_wq = a.wq != nullptr, has_wk = a.wk != nullptr;
+    f32x4 wstage = {1.0f, 1.0f, 1.0f, 1.0f};
+    const int wi = ti < D / 4 ? ti : ti - D / 4;  // thread -> float4 index in its vector
+    const bool stage_q = ti < D / 4, stage_k = ti >= D / 4 && ti < D / 2;
+    if ((stage_q && has_wq) || (stage_k && has_wk)) wstage = ldf4((stage_q ? a.wq : a.wk) + 4 * wi);
+    if (a.do_rope && ti < HALF) {
+        const float theta = ((float)p * a.freq_scale) / rope_denom(ti, D, a.log2_base);
+        double sn, cs;
+        sincos((double)theta, &sn, &cs);
+        s_cos[ti] = (float)cs;
+        s_sin[ti] = (float)sn;
+    }
+    if (stage_q || stage_k) {
+        const bool hw = stage_q ? has_wq : has_wk;
+        f32x4 f;
+        f.x = w_factor(wstage.x, hw, a.uo);
+        f.y = w_factor(wstage.y, hw, a.uo);
+        f.z = w_factor(wstage.z, hw, a.uo);
+        f.w = w_factor(wstage.w, hw, a.uo);
+        *reinterpret_cast<f32x4*>((stage_q ? s_wq : s_wk) + 4 * wi) = f;
+    }
     __syncthreads();
 
     for (int hr = gslot; hr < HR; hr += kSlots) {
@@ -165,12 +195,11 @@ __global__ __launch_bounds__(256) void k_qk_fused(QkArgs a, RopeTab tab) {
                     x1[j] = x1[j] * inv;
                 }
             } else {
-                const float* f0 = kind == 0 ? fq0 : fk0;
-                const float* f1 = kind == 0 ? fq1 : fk1;
+                const float* sw = kind == 0 ? s_wq : s_wk;  // factors (1+w), w or 1
 #pragma unroll
                 for (int j = 0; j < E; ++j) {
-                    x0[j] = (x0[j] * inv) * f0[j];
-                    x1[j] = (x1[j] * inv) * f1[j];
+                    x0[j] = (x0[j] * inv) * sw[hl * E + j];
+                    x1[j] = (x1[j] * inv) * sw[HALF + hl * E + j];
                 }
             }
         }
@@ -320,9 +349,9 @@ static void launch_qk_t(const QkArgs& a, const RopeTab& tab, hipStream_t s) {
                       a.row_stride % E == 0;
     const unsigned grid = (unsigned)a.n_tokens;
     if (fast) {
-        if (a.D == 64) k_qk_fused<T, 64><<<grid, 256, 0, s>>>(a, tab);
-        else if (a.D == 128) k_qk_fused<T, 128><<<grid, 256, 0, s>>>(a, tab);
-        else k_qk_fused<T, 256><<<grid, 256, 0, s>>>(a, tab);
+        if (a.D == 64) k_qk_fused<T, 64><<<grid, 256, 0, s>>>(a);
+        else if (a.D == 128) k_qk_fused<T, 128><<<grid, 256, 0, s>>>(a);
+        else k_qk_fused<T, 256><<<grid, 256, 0, s>>>(a);
     } else {
         k_qk_generic<T><<<grid, 256, 0, s>>>(a, tab);
     }
@@ -344,6 +373,7 @@ static void launch_qk(int dtype, QkArgs& a, float base, int rotary_dim, hipStrea
     }
     static const RopeTab zero_tab = {};
     const RopeTab& tab = a.do_rope ? rope_table(base, eff) : zero_tab;
+    a.log2_base = log2((double)base);
     if (dtype == HIP_BRIDGE_F32) launch_qk_t<float>(a, tab, s);
     else if (dtype == HIP_BRIDGE_BF16) launch_qk_t<uint16_t>(a, tab, s);
     else set_error(HIP_BRIDGE_EUNSUPPORTED);

@@ -100,11 +100,35 @@ __device__ __forceinline__ f32x4 ldf4(const float* p) { return *reinterpret_cast
 
 // ---- lane-group reductions -----------------------------------------------------------
 // Sum over aligned groups of G lanes (G a power of two <= 64); every lane of a group gets
-// the group total.
+// the bit-identical group total (each step adds a pair in the same order on both sides).
+// Within a 16-lane row: DPP quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror, row_mirror.
+// Across rows: gfx950 v_permlane16_swap / v_permlane32_swap, whose two results are this
+// lane's row (half) and its partner's, so their sum is the pair total. The second operand
+// goes through an identity DPP move first: the compiler folds swap(x, x) into (x, x), which
+// is wrong for these partial-row swaps.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
 template <int G>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int o = 1; o < G; o <<= 1) v += __shfl_xor(v, o, kWave);
+    static_assert(G >= 1 && G <= 64 && (G & (G - 1)) == 0, "group size");
+    if constexpr (G >= 2) v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]
+    if constexpr (G >= 4) v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]
+    if constexpr (G >= 8) v += dpp<0x141>(v);  // row_half_mirror
+    if constexpr (G >= 16) v += dpp<0x140>(v); // row_mirror
+    if constexpr (G >= 32) {
+        const unsigned a = __builtin_bit_cast(unsigned, v);
+        const unsigned b = __builtin_bit_cast(unsigned, dpp<0xE4>(v));  // identity move
+        const auto p = __builtin_amdgcn_permlane16_swap(a, b, false, false);
+        v = __builtin_bit_cast(float, (unsigned)p[0]) + __builtin_bit_cast(float, (unsigned)p[1]);
+    }
+    if constexpr (G >= 64) {
+        const unsigned a = __builtin_bit_cast(unsigned, v);
+        const unsigned b = __builtin_bit_cast(unsigned, dpp<0xE4>(v));
+        const auto p = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+        v = __builtin_bit_cast(float, (unsigned)p[0]) + __builtin_bit_cast(float, (unsigned)p[1]);
+    }
     return v;
 }
 
@@ -116,10 +140,12 @@ __device__ __forceinline__ float rms_inv(float sum_sq, int n, float eps) {
     return 1.0f / sqrtf(mean + eps);
 }
 
-// Per-element factor of one chunk: 1 + w, w, or 1 when there is no weight. Multiplying by
-// 1.0 is exact, so (x*inv)*1 equals the reference's no-scale x*inv bit for bit.
+// Norm weights: raw 128-bit loads issued early (load_w), turned into the per-element factor
+// 1 + w, w, or 1 (no weight) only where used (w_factor), so that no wait on the weight loads
+// sits between the activation loads and independent work. Multiplying by 1.0 is exact, so
+// (x*inv)*1 equals the reference's no-scale x*inv bit for bit.
 template <int E>
-__device__ __forceinline__ void load_factors(const float* w, int64_t e0, bool has_w, int uo, float* f) {
+__device__ __forceinline__ void load_w(const float* w, int64_t e0, bool has_w, float* f) {
     if (has_w) {
 #pragma unroll
         for (int q = 0; q < E / 4; ++q) {
@@ -129,14 +155,10 @@ __device__ __forceinline__ void load_factors(const float* w, int64_t e0, bool ha
             f[4 * q + 2] = v.z;
             f[4 * q + 3] = v.w;
         }
-        if (uo) {
-#pragma unroll
-            for (int j = 0; j < E; ++j) f[j] = 1.0f + f[j];
-        }
-    } else {
-#pragma unroll
-        for (int j = 0; j < E; ++j) f[j] = 1.0f;
     }
+}
+__device__ __forceinline__ float w_factor(float w, bool has_w, int uo) {
+    return has_w ? (uo ? 1.0f + w : w) : 1.0f;
 }
 
 // ---- tanh / GELU / soft-cap ------------------------------------------------------------
