@@ -25,7 +25,7 @@
  *       test math.zig:1171-1177); agreement with Zig's std.math.pow / @cos / @sin bits is
  *       parity unpinned
  *   tanh / expm1 / gelu / soft-cap .................................. pinned to the
- *       mathematics (<= 2 ulp of f64 tanh/expm1 over dense sweeps, odd symmetry,
+ *       mathematics (<= 2.5 ulp of f64 tanh, <= 1 ulp expm1 over dense sweeps, odd symmetry,
  *       saturation); agreement with Zig's std.math.tanh bits is parity unpinned
  */
 #include "ziglm_oracle.h"

@@ -1,0 +1,533 @@
+"""Pins the CPU oracle (oracle/ziglm_oracle.c) before it is trusted as the checker.
+
+The reference (Zig) cannot be compiled here, and its tests hold no golden vectors for this
+path, so each oracle function is checked against
+  * the reference's own unit tests for the path, restated: math.zig:1149-1160 (RMSNorm),
+    math.zig:1171-1177 (RoPE), quant.zig:655-660 (bf16), quant.zig:662-694 (Q8_0/Q4_0
+    round trips), types.zig:375-381 (block sizes), kv_cache.zig:101-118 (put);
+  * what the mathematics fixes: exhaustive f16/bf16 sweeps, single-rounding products
+    computed exactly in float64, f64 RMSNorm / RoPE / tanh / expm1 / GELU, closed forms
+    (constant rows, pos 0 identity, angle of pair 0 = pos, norm preservation, odd
+    symmetry, saturation), known-answer blocks built by hand from the GGUF layout;
+  * agreement of the -O2 checker build with the -O3 x86-64-v3 baseline build, bit for bit.
+Parity at the bit level with Zig's own std.math.pow / @cos / @sin / std.math.tanh and
+@reduce lane order stays unpinned (no Zig toolchain); the tolerances above it are what the
+GPU tests rely on.
+"""
+import os
+import subprocess
+import tempfile
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from ziglm_amd import synth
+
+EPS = np.float32(1e-6)
+
+
+@pytest.fixture(scope="module")
+def o():
+    return O.get()
+
+
+@pytest.fixture(scope="module")
+def osimd():
+    return O.get(simd=True)
+
+
+def ulp32(x):
+    return np.spacing(np.abs(np.asarray(x, np.float32))).astype(np.float64)
+
+
+# ---------------------------------------------------------------------------------------
+# conversions
+# ---------------------------------------------------------------------------------------
+
+def test_f16_to_f32_exhaustive(o):
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    ref = h.view(np.float16).astype(np.float32)
+    got = np.array([o.lib.zo_f16_to_f32(int(v)) for v in h], np.float32)
+    fin = np.isfinite(ref)
+    assert np.array_equal(got[fin].view(np.uint32), ref[fin].view(np.uint32))
+    assert np.all(np.isnan(got[np.isnan(ref)])) and np.array_equal(got[np.isinf(ref)], ref[np.isinf(ref)])
+
+
+def test_bf16_to_f32_exhaustive(o):
+    u = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = o.bf16_to_f32(u)
+    assert np.array_equal(got.view(np.uint32), u.astype(np.uint32) << 16)
+
+
+def rne_bf16_f64(x):
+    """Independent RNE f32 -> bf16 through float64: pick the nearer of the two bf16
+    neighbours, ties to the even mantissa."""
+    x = np.asarray(x, np.float32)
+    b = x.view(np.uint32)
+    lo = (b & 0xFFFF0000).astype(np.uint32)
+    hi = lo + 0x10000
+    xl = lo.view(np.float32).astype(np.float64)
+    xh = hi.astype(np.uint32).view(np.float32).astype(np.float64)
+    xv = x.astype(np.float64)
+    dl, dh = np.abs(xv - xl), np.abs(xh - xv)
+    pick_hi = (dh < dl) | ((dh == dl) & (((lo >> 16) & 1) == 1))
+    return np.where(pick_hi, hi >> 16, lo >> 16).astype(np.uint16)
+
+
+def test_f32_to_bf16_rne(o):
+    rng = np.random.default_rng(0)
+    bits = rng.integers(0, 0x7F7F0000, 2_000_000, dtype=np.uint32)
+    bits |= rng.integers(0, 2, bits.size, dtype=np.uint32) << 31
+    ties = (rng.integers(0, 0x7F7F, 20000, dtype=np.uint32) << 16) | 0x8000
+    x = np.concatenate([bits, ties, np.array([0, 0x80000000, 1, 0x8000, 0x18000, 0x7F7FFFFF, 0x7F800000,
+                                               0xFF800000, 0x00800000, 0x007FFFFF], np.uint32)]).view(np.float32)
+    got = o.f32_to_bf16(x)
+    fin = np.isfinite(x) & (np.abs(x) < np.float32(3.3e38))
+    assert np.array_equal(got[fin], rne_bf16_f64(x[fin]))
+    assert got[x.view(np.uint32) == 0x7F7FFFFF][0] == 0x7F80  # max float rounds up to +inf
+    assert np.array_equal(got, synth.f32_to_bf16(x))  # the generator's numpy restatement
+
+
+def test_bf16_roundtrip_pi_quant_zig_655(o):
+    """quant.zig:655-660: bf16 round trip of pi within 1%."""
+    v = o.lib.zo_bf16_to_f32(o.lib.zo_f32_to_bf16(np.float32(np.pi)))
+    assert abs(v - np.pi) / np.pi < 0.01
+
+
+# ---------------------------------------------------------------------------------------
+# quant blocks and gather
+# ---------------------------------------------------------------------------------------
+
+def test_block_sizes_types_zig_375(o):
+    assert o.row_bytes(O.Q4_0, 32) == 18
+    assert o.row_bytes(O.Q8_0, 32) == 34
+    assert o.row_bytes(O.Q6_K, 256) == 210
+    assert o.row_bytes(O.BF16, 2560) == 5120 and o.row_bytes(O.Q8_0, 2560) == 2720 and o.row_bytes(O.Q4_0, 2560) == 1440
+
+
+def test_q8_0_known_answer(o):
+    blk = np.zeros(34, np.uint8)
+    blk[0:2] = np.array([np.float16(0.5)]).view(np.uint8)
+    qs = np.arange(-16, 16, dtype=np.int8)
+    qs[0], qs[31] = -127, 127
+    blk[2:] = qs.view(np.uint8)
+    assert np.array_equal(o.dequantize_row(O.Q8_0, blk, 32), qs.astype(np.float32) * np.float32(0.5))
+
+
+def test_q4_0_known_answer(o):
+    blk = np.zeros(18, np.uint8)
+    blk[0:2] = np.array([np.float16(0.25)]).view(np.uint8)
+    blk[2] = 0x1F   # element 0 = low nibble 0xF - 8 = 7; element 16 = high nibble 1 - 8 = -7
+    blk[3] = 0x80   # element 1 = 0 - 8 = -8; element 17 = 8 - 8 = 0
+    out = o.dequantize_row(O.Q4_0, blk, 32)
+    assert out[0] == 7 * 0.25 and out[16] == -7 * 0.25 and out[1] == -8 * 0.25 and out[17] == 0.0
+    assert np.all(out[[i for i in range(32) if i not in (0, 1, 16, 17)]] == -8 * 0.25)
+
+
+def q6k_numpy(sb):
+    """GGUF Q6_K super-block (ql[128] qh[64] scales[16] d) dequantised with whole-array
+    numpy indexing: y[n*128 + g*32 + l] for half n, group g (q1..q4) and l in 0..31."""
+    ql, qh = sb[:128].astype(np.int32), sb[128:192].astype(np.int32)
+    sc = sb[192:208].view(np.int8).astype(np.float32)
+    d = np.float32(sb[208:210].view(np.float16)[0])
+    y = np.empty(256, np.float32)
+    l = np.arange(32)
+    for n in range(2):
+        a, a32, h = ql[n * 64 + l], ql[n * 64 + l + 32], qh[n * 32 + l]
+        qs = [(a & 15) | ((h & 3) << 4), (a32 & 15) | (((h >> 2) & 3) << 4),
+              (a >> 4) | (((h >> 4) & 3) << 4), (a32 >> 4) | (((h >> 6) & 3) << 4)]
+        for g in range(4):
+            s = sc[n * 8 + l // 16 + 2 * g]
+            y[n * 128 + g * 32 + l] = (d * s).astype(np.float32) * (qs[g] - 32).astype(np.float32)
+    return y
+
+
+def test_q6_k_matches_layout(o):
+    rng = np.random.default_rng(3)
+    for _ in range(20):
+        sb = rng.integers(0, 256, 210, dtype=np.uint8)
+        sb[208:210] = np.array([np.float16(rng.uniform(1e-3, 2e-2))]).view(np.uint8)
+        assert np.array_equal(o.dequantize_row(O.Q6_K, sb, 256).view(np.uint32), q6k_numpy(sb).view(np.uint32))
+
+
+@pytest.mark.parametrize("qtype", [O.Q8_0, O.Q4_0, O.BF16, O.F16])
+def test_gather_single_rounding(o, qtype):
+    """out = fl(q*d*scale) with q*d exact: one IEEE rounding of the exact product (the CUDA
+    kernels' q*(d*scale) rounds twice and fails this for some elements)."""
+    dim, vocab = 2560, 40
+    if qtype == O.Q8_0:
+        tab = synth.q8_0_table(2, vocab, dim)
+    elif qtype == O.Q4_0:
+        tab = synth.q4_0_table(2, vocab, dim)
+    elif qtype == O.BF16:
+        tab = synth.bf16_table(2, vocab, dim)
+    else:
+        tab = synth.f16_bits(synth.normal_f32(2, "f16", (vocab, dim), 0, 0.5)).view(np.uint8).reshape(vocab, -1)
+    ids = np.array([3, 0, 39, 3, 17], np.int32)
+    scale = np.float32(np.sqrt(np.float32(dim)))
+    got = o.embed_gather(tab, qtype, ids, dim, scale)
+    raw = np.stack([o.dequantize_row(qtype, tab[i], dim) for i in ids]).astype(np.float64)
+    exact = (raw * np.float64(scale)).astype(np.float32)  # raw = q*d exactly; one rounding here
+    assert np.array_equal(got.view(np.uint32), exact.view(np.uint32))
+    if qtype in (O.Q8_0, O.Q4_0):
+        # independent check of raw: q * d from the block bytes
+        nb = dim // 32
+        bs = 34 if qtype == O.Q8_0 else 18
+        blk = tab[ids].reshape(len(ids), nb, bs)
+        d = blk[:, :, 0:2].copy().view(np.float16).astype(np.float64).reshape(len(ids), nb, 1)
+        if qtype == O.Q8_0:
+            q = blk[:, :, 2:].view(np.int8).astype(np.float64)
+        else:
+            b = blk[:, :, 2:].astype(np.int32)
+            q = np.concatenate([(b & 15) - 8, (b >> 4) - 8], axis=2).astype(np.float64)
+        assert np.array_equal((q * d).reshape(len(ids), dim), raw)
+
+
+def quantize_q8_0(x):
+    """quant.zig:55-71 restated: d = amax/127, q = round(x/d) clamped to int8."""
+    blocks = x.reshape(-1, 32)
+    amax = np.abs(blocks).max(1).astype(np.float32)
+    d = (amax / np.float32(127.0)).astype(np.float32)
+    idd = np.where(d != 0, np.float32(1.0) / np.where(d != 0, d, 1), 0).astype(np.float32)
+    q = np.clip(np.round(blocks * idd[:, None]), -128, 127).astype(np.int8)  # ties: see below
+    out = np.empty((blocks.shape[0], 34), np.uint8)
+    out[:, 0:2] = d.astype(np.float16).reshape(-1, 1).view(np.uint8)
+    out[:, 2:] = q.view(np.uint8)
+    return out.reshape(-1)
+
+
+def quantize_q4_0(x):
+    """quant.zig:89-117 restated: d = -max/8 (max = the value of largest |x|),
+    nibble = clamp(round(x/d) + 8, 0, 15), element i low nibble, i+16 high nibble."""
+    blocks = x.reshape(-1, 32)
+    idx = np.abs(blocks).argmax(1)
+    mx = blocks[np.arange(blocks.shape[0]), idx]
+    d = (-mx / np.float32(8.0)).astype(np.float32)
+    idd = np.where(d != 0, np.float32(1.0) / np.where(d != 0, d, 1), 0).astype(np.float32)
+    v = np.clip(np.round(blocks * idd[:, None]) + 8, 0, 15).astype(np.uint8)
+    out = np.empty((blocks.shape[0], 18), np.uint8)
+    out[:, 0:2] = d.astype(np.float16).reshape(-1, 1).view(np.uint8)
+    out[:, 2:] = (v[:, :16] & 15) | ((v[:, 16:] & 15) << 4)
+    return out.reshape(-1)
+
+
+def test_q8_0_q4_0_roundtrip_quant_zig_662(o):
+    """quant.zig:662-694: quantize -> dequantize within 0.05 (Q8_0) / 0.5 (Q4_0) absolute
+    on the test's ramp input (i*0.1 - 1.6)."""
+    x = (np.arange(32, dtype=np.float32) * np.float32(0.1) - np.float32(1.6)).astype(np.float32)
+    assert np.max(np.abs(o.dequantize_row(O.Q8_0, quantize_q8_0(x), 32) - x)) < 0.05
+    assert np.max(np.abs(o.dequantize_row(O.Q4_0, quantize_q4_0(x), 32) - x)) < 0.5
+
+
+# ---------------------------------------------------------------------------------------
+# RMSNorm
+# ---------------------------------------------------------------------------------------
+
+def rms_f64(x, w, eps, uo):
+    x = np.asarray(x, np.float64)
+    inv = 1.0 / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + float(eps))
+    return x * inv * ((1.0 + w) if uo else w) if w is not None else x * inv
+
+
+@pytest.mark.parametrize("n", [1, 7, 8, 9, 31, 32, 33, 40, 256, 2560, 2561, 5376])
+@pytest.mark.parametrize("uo", [True, False])
+def test_rmsnorm_vs_f64(o, n, uo):
+    x = synth.normal_f32(0, f"x{n}", (3, n))
+    w = synth.normal_f32(0, f"w{n}", (n,), 0, 0.1)
+    got = o.rms_norm(x, w, EPS, uo).astype(np.float64)
+    ref = rms_f64(x, w.astype(np.float64), EPS, uo)
+    assert np.all(np.abs(got - ref) <= 1e-6 * np.abs(ref) + 1e-30)
+    got0 = o.rms_norm(x, None, EPS).astype(np.float64)
+    assert np.all(np.abs(got0 - rms_f64(x, None, EPS, False)) <= 1e-6 * np.abs(got0) + 1e-30)
+
+
+def test_rmsnorm_constant_row_closed_form(o):
+    for c in (0.5, -3.0, 1e-3, 17.0):
+        x = np.full(2560, c, np.float32)
+        w = synth.normal_f32(0, "w", (2560,), 0, 0.1)
+        got = o.rms_norm(x, w, EPS, True).astype(np.float64)
+        ref = c / np.sqrt(c * c + float(EPS)) * (1.0 + w.astype(np.float64))
+        assert np.all(np.abs(got - ref) <= 4e-7 * np.abs(ref))
+
+
+def test_rmsnorm_math_zig_1149():
+    """math.zig:1149-1160: x = [1,2,3,4], w = 1, eps 1e-5, no unit offset: RMS(out) ~ 1."""
+    o = O.get()
+    out = o.rms_norm(np.array([1, 2, 3, 4], np.float32), np.ones(4, np.float32), np.float32(1e-5), False)
+    assert abs(np.sqrt(np.mean(out.astype(np.float64) ** 2)) - 1.0) < 1e-4
+
+
+def test_rmsnorm_in_place_and_add_variants(o):
+    n = 2560
+    x = synth.normal_f32(5, "x", (n,))
+    r = synth.normal_f32(5, "r", (n,))
+    w = synth.normal_f32(5, "w", (n,), 0, 0.1)
+    s, out = o.add_rms_norm(x, r, w, EPS)
+    assert np.array_equal(s, (x + r).astype(np.float32))
+    assert np.array_equal(out, o.rms_norm(s, w, EPS))
+    xn = o.rms_norm_add(x, r, w, EPS)
+    assert np.array_equal(xn, (x + o.rms_norm(r, w, EPS)).astype(np.float32))
+    w2 = synth.normal_f32(5, "w2", (n,), 0, 0.1)
+    x2, out2 = o.rms_norm_add_rms_norm(x, r, w, w2, EPS)
+    assert np.array_equal(x2, (x + o.rms_norm(r, w, EPS)).astype(np.float32))
+    assert np.array_equal(out2, o.rms_norm(x2, w2, EPS))
+
+
+def test_bf16_wrappers_are_upconvert_op_round(o):
+    rows, n = 3, 2560
+    x = synth.normal_bf16(6, "x", (rows, n))
+    r = synth.normal_bf16(6, "r", (rows, n))
+    w = synth.normal_f32(6, "w", (n,), 0, 0.1)
+    f = o.bf16_to_f32
+    xs, out = o.add_rms_norm_bf16(x, r, w, EPS)
+    s32, o32 = o.add_rms_norm(f(x), f(r), w, EPS)
+    assert np.array_equal(xs, o.f32_to_bf16(s32)) and np.array_equal(out, o.f32_to_bf16(o32))
+    assert np.array_equal(o.rms_norm_bf16(x, w, EPS), o.f32_to_bf16(o.rms_norm(f(x), w, EPS)))
+    assert np.array_equal(o.geglu(x, r), o.f32_to_bf16(o.geglu(f(x), f(r))))
+
+
+# ---------------------------------------------------------------------------------------
+# RoPE
+# ---------------------------------------------------------------------------------------
+
+def test_rope_denominators_correctly_rounded(o):
+    for base in (10000.0, 1e6):
+        for eff in (64, 128, 256, 512):
+            for i in range(eff // 2):
+                e = np.float32(2 * i) / np.float32(eff)
+                exact = float(base) ** float(e)
+                dv = o.rope_denominator(base, i, eff)
+                assert abs(dv - exact) <= 0.5 * float(np.spacing(np.float32(exact)))
+
+
+def test_rope_pos0_identity_and_layout(o):
+    q = synth.normal_f32(7, "q", (8, 256))
+    k = synth.normal_f32(7, "k", (4, 256))
+    q0, k0 = o.apply_rope(q, k, 0, 256, 0, 8, 4, 10000.0)
+    assert np.array_equal(q0, q) and np.array_equal(k0, k)
+    # half-split (.normal) pairs (i, i + d/2); the interleaved (.neox) variant pairs (2i, 2i+1)
+    h = np.array([[1, 0, 0, 0]], np.float32)
+    p = 3
+    qn, _ = o.apply_rope(h, None, p, 4, 0, 1, 0, 10000.0)
+    qx, _ = o.apply_rope(h, None, p, 4, 0, 1, 0, 10000.0, neox=True)
+    assert np.allclose(qn[0], [np.cos(p), 0, np.sin(p), 0], atol=1e-7)
+    assert np.allclose(qx[0], [np.cos(p), np.sin(p), 0, 0], atol=1e-7)
+
+
+def test_rope_math_zig_1171():
+    """math.zig:1171-1177: RoPE at pos 1 changes q (head 4, rotary 4, .normal)."""
+    o = O.get()
+    q, _ = o.apply_rope(np.array([1, 0, 0, 1], np.float32), np.array([1, 0, 0, 1], np.float32), 1, 4, 4, 1, 1, 10000.0)
+    assert q[0] != 1.0 or q[1] != 0.0
+
+
+@pytest.mark.parametrize("pos", [1, 7, 33, 64])
+def test_rope_vs_f64(o, pos):
+    """Against RoPE in float64 with f64 angles pos/base^(2i/r): the f32 angle's rounding
+    (|theta| * 2^-24) bounds the difference at these small positions."""
+    D, nh = 256, 8
+    q = synth.normal_f32(8, "q", (nh, D))
+    got, _ = o.apply_rope(q, None, pos, D, 0, nh, 0, 10000.0)
+    i = np.arange(D // 2)
+    th = pos / 10000.0 ** (2.0 * i / D)
+    c, s = np.cos(th), np.sin(th)
+    v0, v1 = q[:, :D // 2].astype(np.float64), q[:, D // 2:].astype(np.float64)
+    ref = np.concatenate([v0 * c - v1 * s, v0 * s + v1 * c], axis=1)
+    pn = np.sqrt(v0 ** 2 + v1 ** 2)
+    tol = np.concatenate([pn, pn], axis=1) * (pos * 2.0 ** -23 + 1e-6)
+    assert np.all(np.abs(got - ref) <= tol)
+
+
+@pytest.mark.parametrize("pos", [1234, 2047, 8191, 32767])
+def test_rope_large_pos_norm_and_own_angle(o, pos):
+    """At large positions the f32 angle is the recipe's defining rounding: check the rotation
+    is exactly by theta_i = f32(pos)/D_i (f64 trig of that f32 angle) and preserves norms."""
+    D, nh, base = 128, 4, 1e6
+    q = synth.normal_f32(9, "q", (nh, D))
+    got, _ = o.apply_rope(q, None, pos, D, 0, nh, 0, base)
+    th = np.array([np.float32(np.float32(pos) / np.float32(o.rope_denominator(base, i, D))) for i in range(D // 2)],
+                  np.float64)
+    c = np.cos(th).astype(np.float32).astype(np.float64)
+    s = np.sin(th).astype(np.float32).astype(np.float64)
+    v0, v1 = q[:, :D // 2].astype(np.float64), q[:, D // 2:].astype(np.float64)
+    ref = np.concatenate([v0 * c - v1 * s, v0 * s + v1 * c], axis=1)
+    pn = np.sqrt(v0 ** 2 + v1 ** 2)
+    assert np.all(np.abs(got - ref) <= np.concatenate([pn, pn], axis=1) * 3e-7)
+    gn = np.sqrt(got[:, :D // 2].astype(np.float64) ** 2 + got[:, D // 2:].astype(np.float64) ** 2)
+    assert np.all(np.abs(gn - pn) <= 1e-6 * pn)
+
+
+def test_rope_partial_rotary_leaves_tail(o):
+    D, r = 512, 128
+    q = synth.normal_f32(10, "q", (2, D))
+    got, _ = o.apply_rope(q, None, 500, D, r, 2, 0, 1e6)
+    assert np.array_equal(got[:, r:], q[:, r:])
+    assert not np.array_equal(got[:, :r], q[:, :r])
+    # rotated part equals full RoPE of a head of size r
+    sub, _ = o.apply_rope(np.ascontiguousarray(q[:, :r]), None, 500, r, 0, 2, 0, 1e6)
+    assert np.array_equal(got[:, :r], sub)
+
+
+def test_qk_norm_rope_kv_composition(o):
+    """The fused oracle = per-head norms (model.zig:562-567, 628-640), then RoPE on Q and K,
+    then the KV put of K (rotated) and V (normalised when v_norm)."""
+    nh, nkv, D, pos = 8, 4, 256, 1234
+    q = synth.normal_f32(11, "q", (1, nh, D))
+    k = synth.normal_f32(11, "k", (1, nkv, D))
+    v = synth.normal_f32(11, "v", (1, nkv, D))
+    wq = synth.normal_f32(11, "wq", (D,), 0, 0.1)
+    wk = synth.normal_f32(11, "wk", (D,), 0, 0.1)
+    kc = np.zeros((4096, nkv * D), np.float32)
+    vc = np.zeros_like(kc)
+    qo = o.qk_norm_rope_kv(q, k, v, wq, wk, kc, vc, v_norm=True, max_seq=4096, max_kv_dim=nkv * D,
+                           pos=np.array([pos], np.int32), n_heads=nh, n_kv_heads=nkv, head_dim=D, base=10000.0,
+                           eps=EPS)
+    qn = o.rms_norm(q[0], wq, EPS)
+    kn = o.rms_norm(k[0], wk, EPS)
+    qr, kr = o.apply_rope(qn, kn, pos, D, 0, nh, nkv, 10000.0)
+    assert np.array_equal(qo[0], qr)
+    assert np.array_equal(kc[pos].reshape(nkv, D), kr)
+    assert np.array_equal(vc[pos].reshape(nkv, D), o.rms_norm(v[0], None, EPS))
+    assert np.count_nonzero(kc) == kr.size - np.count_nonzero(kr == 0)
+
+
+def test_kv_cache_put_kv_cache_zig_101(o):
+    """kv_cache.zig:101-118: put at (layer 0, pos 5), read head 0 back (42 / 99)."""
+    nkv, hd, max_seq, layers = 4, 8, 16, 2
+    k = np.ones(nkv * hd, np.float32)
+    v = np.full(nkv * hd, 2.0, np.float32)
+    k[0], v[0] = 42.0, 99.0
+    kc = np.zeros((layers * max_seq, nkv * hd), np.float32)
+    vc = np.zeros_like(kc)
+    o.kv_cache_put(kc, vc, k, v, 0, 5, max_seq, nkv, hd, nkv * hd)
+    assert kc[5, 0] == 42.0 and vc[5, 0] == 99.0
+    assert np.array_equal(kc[5], k) and np.count_nonzero(kc) == k.size
+    o.kv_cache_put(kc, vc, k, v, 1, 15, max_seq, nkv, hd, nkv * hd)
+    assert np.array_equal(vc[max_seq + 15], v)
+
+
+# ---------------------------------------------------------------------------------------
+# tanh family
+# ---------------------------------------------------------------------------------------
+
+def sweep():
+    a = np.concatenate([np.linspace(-20, 20, 400001), np.geomspace(1e-30, 30, 200000),
+                        -np.geomspace(1e-30, 30, 200000), [0.2554, 0.5493, 9.0, 9.01, 10.0, 10.5, 88.0]])
+    return a.astype(np.float32)
+
+
+def test_expm1_vs_f64(o):
+    x = np.concatenate([np.linspace(-20, 88.7, 20001), np.geomspace(1e-20, 1, 5000), -np.geomspace(1e-20, 1, 5000)]).astype(np.float32)
+    got = np.array([o.expm1f(float(v)) for v in x], np.float32)
+    ref = np.expm1(x.astype(np.float64))
+    assert np.all(np.abs(got - ref) <= 1.0 * ulp32(ref) + 1e-45)
+
+
+def test_tanh_vs_f64_and_symmetry(o):
+    x = sweep()
+    t = o.tanh_array(x)
+    ref = np.tanh(x.astype(np.float64))
+    assert np.all(np.abs(t - ref) <= 2.5 * ulp32(ref) + 1e-45)  # musl tanhf: ~2.04 ulp max near |x| = 0.24
+    assert np.array_equal(o.tanh_array(-x).view(np.uint32), (-t).view(np.uint32))
+    assert o.tanhf(0.0) == 0.0 and o.tanhf(10.5) == 1.0 and o.tanhf(-30.0) == -1.0 and o.tanhf(9.5) == 1.0
+
+
+def test_gelu_vs_f64(o):
+    x = sweep()[::4]
+    g = np.array([o.gelu(float(v)) for v in x], np.float64)
+    xd = x.astype(np.float64)
+    ref = 0.5 * xd * (1.0 + np.tanh(0.7978845608 * (xd + 0.044715 * xd ** 3)))
+    # f32 evaluation: relative error of a few ulp, plus the cancellation of 1 + tanh(z) for
+    # z << 0 (one ulp of 1 in tanh is 2^-24 absolute in 1 + tanh)
+    assert np.all(np.abs(g - ref) <= 1e-6 * np.abs(ref) + np.abs(xd) * 2.0 ** -23)
+    assert o.gelu(0.0) == 0.0 and o.gelu(20.0) == 20.0 and o.gelu(-20.0) == 0.0
+
+
+def test_softcap_vs_f64(o):
+    for cap in (30.0, 50.0):
+        x = np.concatenate([synth.normal_f32(4, "s", (100000,), 0, 20), sweep()[::7] * 50]).astype(np.float32)
+        got = o.softcap(x, cap).astype(np.float64)
+        ref = cap * np.tanh(x.astype(np.float64) / cap)
+        assert np.all(np.abs(got - ref) <= 4.0 * ulp32(ref) + 1e-45)  # divide + tanh (2 ulp) + multiply
+        assert np.all(np.abs(got) <= cap)
+
+
+# ---------------------------------------------------------------------------------------
+# builds agree; generator pinned
+# ---------------------------------------------------------------------------------------
+
+def test_simd_build_bit_identical(o, osimd):
+    n = 2560
+    x = synth.normal_f32(12, "x", (4, n))
+    w = synth.normal_f32(12, "w", (n,), 0, 0.1)
+    assert np.array_equal(o.rms_norm(x, w, EPS), osimd.rms_norm(x, w, EPS))
+    assert np.array_equal(o.rms_norm(x, None, EPS), osimd.rms_norm(x, None, EPS))
+    g = synth.normal_f32(12, "g", (20000,))
+    u = synth.normal_f32(12, "u", (20000,))
+    assert np.array_equal(o.geglu(g, u).view(np.uint32), osimd.geglu(g, u).view(np.uint32))
+    assert np.array_equal(o.softcap(g * 30, 30.0).view(np.uint32), osimd.softcap(g * 30, 30.0).view(np.uint32))
+    q = synth.normal_f32(12, "q", (8, 256))
+    assert np.array_equal(o.apply_rope(q, None, 777, 256, 0, 8, 0, 1e4)[0], osimd.apply_rope(q, None, 777, 256, 0, 8, 0, 1e4)[0])
+    tab = synth.q4_0_table(12, 16, 2560)
+    ids = np.arange(16, dtype=np.int32)
+    assert np.array_equal(o.embed_gather(tab, O.Q4_0, ids, 2560, 50.5), osimd.embed_gather(tab, O.Q4_0, ids, 2560, 50.5))
+
+
+def test_splitmix64_published_sequence():
+    """SplitMix64 from state 0: the published reference outputs."""
+    z = synth.splitmix64(0, 3)
+    assert [int(v) for v in z] == [0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4, 0x06C45D188009454F]
+
+
+def test_generator_distribution():
+    x = synth.normal_f32(1, "x", (1 << 20,)).astype(np.float64)
+    assert abs(x.mean()) < 5e-3 and abs(x.std() - 1.0) < 5e-3
+    ids = synth.gather_ids(2, 4096, 262144)
+    assert ids.size == 4096 and ids.min() >= 0 and ids.max() < 262144
+    assert len(np.unique(ids)) <= 4096 - 64 + 1 and np.all(np.isin(ids[-64:], ids[:-64]))
+
+
+# ---------------------------------------------------------------------------------------
+# the kernels' correctly rounded division by a uniform divisor (soft-cap x/cap)
+# ---------------------------------------------------------------------------------------
+
+MARKSTEIN_C = r"""
+#include <math.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+static float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+int main(void) {
+    const float caps[] = {30.0f, 50.0f, 1.0f, 3.0f, 0.5f, 7.0f, 1e-3f, 123.456f, 15.0f, 1e4f};
+    uint64_t s = 88172645463325252ull, bad = 0, n = 0;
+    for (int c = 0; c < 10; ++c) {
+        const float b = caps[c], rb = 1.0f / b;
+        for (int i = 0; i < 2000000; ++i) {
+            s ^= s << 13; s ^= s >> 7; s ^= s << 17;
+            uint32_t e = 0x20000000u + (uint32_t)((s >> 32) % 0x3F000000u);  /* |x| in ~[2^-63, 2^63] */
+            float x = u2f((e & 0x7FFFFFFFu) | ((uint32_t)(s & 1) << 31));
+            float q0 = x * rb;
+            float r = fmaf(-b, q0, x);
+            float q = fmaf(r, rb, q0);
+            float ref = x / b;
+            n++;
+            if (memcmp(&q, &ref, 4) != 0) bad++;
+        }
+    }
+    printf("%llu %llu\n", (unsigned long long)bad, (unsigned long long)n);
+    return 0;
+}
+"""
+
+
+def test_markstein_uniform_division_is_ieee():
+    """div_by_uniform (zl_common.h): q0 = x*rb, r = fma(-b, q0, x), q = fma(r, rb, q0) with
+    rb = RN(1/b) reproduces IEEE x/b; checked here in C with libm's correctly rounded fmaf
+    over 20M random x for the soft-cap divisors."""
+    with tempfile.TemporaryDirectory() as d:
+        src, exe = os.path.join(d, "m.c"), os.path.join(d, "m")
+        open(src, "w").write(MARKSTEIN_C)
+        subprocess.run(["gcc", "-O2", "-ffp-contract=off", "-fno-fast-math", src, "-o", exe, "-lm"], check=True)
+        bad, n = map(int, subprocess.run([exe], capture_output=True, text=True, check=True).stdout.split())
+    assert n == 20_000_000 and bad == 0
