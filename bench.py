@@ -387,7 +387,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="headline config only")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default=None, help="run one op only (profiling)")
+    ap.add_argument("--only", default=None, help="run one op only (profiling); 'copy' = hipMemcpy "
+                    "device-to-device of the GeGLU output size (counter calibration)")
+    ap.add_argument("--eager", action="store_true", help="with --only: launch eagerly, no graph")
     ap.add_argument("--config", default="c2", choices=["c2", "c4"])
     a = ap.parse_args()
     if a.gpus != 1:
@@ -402,9 +404,29 @@ def main():
 
     if a.only:
         sets, _ = make_sets(dev, shape, T, B.BF16)
-        us = time_launches_us(dev, LY.OPS[a.only], sets, a.steps)
-        nb = LY.op_bytes(shape, T, 2)[a.only]
-        print(json.dumps({"op": a.only, "config": a.config, "us": us, "bytes": nb, "GBps": nb / us / 1e3}))
+        if a.only == "copy":
+            nb = sets[0].act.size_bytes
+
+            def fn(d, L):
+                d.b.check(d.b.hip_memcpy_d2d(L.act.ptr, L.gate.ptr, nb, d.stream), "copy")
+            traffic = 2 * nb
+        else:
+            fn = LY.OPS[a.only]
+            traffic = LY.op_bytes(shape, T, 2)[a.only]
+        if a.eager:
+            e0, e1 = dev.event(), dev.event()
+            for i in range(len(sets)):
+                fn(dev, sets[i])
+            dev.sync()
+            dev.record(e0)
+            for i in range(a.steps):
+                fn(dev, sets[i % len(sets)])
+            dev.record(e1)
+            us = dev.elapsed_ms(e0, e1) * 1000.0 / a.steps
+        else:
+            us = time_launches_us(dev, fn, sets, a.steps)
+        print(json.dumps({"op": a.only, "config": a.config, "us": us, "bytes": traffic, "GBps": traffic / us / 1e3,
+                          "eager": a.eager}))
         return
 
     t_start = time.time()
