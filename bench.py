@@ -320,43 +320,72 @@ def bench_gather(dev, vocab=262144, dim=2560, n_tok=4096, n_rep=64):
 # CPU baseline (oracle, -O3 -march=x86-64-v3, one thread)
 # ---------------------------------------------------------------------------------------
 
-def cpu_baseline(shape, T_full, target_s=12.0):
+def pool_threads(cpus):
+    """ziglm's default worker count (thread_pool.zig:26-35): half the CPUs from 16 up, 8 above
+    8, else all of them."""
+    return cpus // 2 if cpus >= 16 else 8 if cpus > 8 else max(1, cpus)
+
+
+def cpu_baseline(shape, T, target_s=10.0, parallel_s=3.0):
+    """The oracle's SIMD build timed on the host over the c2 chain: the whole 2048-token chain
+    repeated for about `target_s` seconds on one thread (ziglm's CPU ops are single-threaded,
+    one token at a time), plus a token-parallel run over ziglm's default pool size as an upper
+    bound."""
+    from concurrent.futures import ThreadPoolExecutor
     from oracle import oracle as O
     o = O.get(simd=True)
     s = shape
+    x = synth.normal_bf16(1, "x", (T, s.H))
+    ao = synth.normal_bf16(1, "ao", (T, s.H))
+    fo = synth.normal_bf16(1, "fo", (T, s.H))
+    q = synth.normal_bf16(1, "q", (T, s.nh, s.D))
+    k = synth.normal_bf16(1, "k", (T, s.nkv, s.D))
+    v = synth.normal_bf16(1, "v", (T, s.nkv, s.D))
+    gate = synth.normal_bf16(1, "gate", (T, s.I))
+    up = synth.normal_bf16(1, "up", (T, s.I))
+    w = {k_: synth.normal_f32(1, "w_" + k_, (s.H,), 0, 0.1) for k_ in ("in", "post_attn", "pre_ffn", "post_ffn")}
+    wq = synth.normal_f32(1, "wq", (s.D,), 0, 0.1)
+    wk = synth.normal_f32(1, "wk", (s.D,), 0, 0.1)
+    kc = np.zeros((s.max_seq, s.nkv * s.D), np.uint16)
+    vc = np.zeros_like(kc)
+    pos = np.arange(T, dtype=np.int32)
 
-    def run(T):
-        x = synth.normal_bf16(1, "x", (T, s.H))
-        ao = synth.normal_bf16(1, "ao", (T, s.H))
-        fo = synth.normal_bf16(1, "fo", (T, s.H))
-        q = synth.normal_bf16(1, "q", (T, s.nh, s.D))
-        k = synth.normal_bf16(1, "k", (T, s.nkv, s.D))
-        v = synth.normal_bf16(1, "v", (T, s.nkv, s.D))
-        gate = synth.normal_bf16(1, "gate", (T, s.I))
-        up = synth.normal_bf16(1, "up", (T, s.I))
-        w = {k_: synth.normal_f32(1, "w_" + k_, (s.H,), 0, 0.1) for k_ in ("in", "post_attn", "pre_ffn", "post_ffn")}
-        wq = synth.normal_f32(1, "wq", (s.D,), 0, 0.1)
-        wk = synth.normal_f32(1, "wk", (s.D,), 0, 0.1)
-        kc = np.zeros((s.max_seq, s.nkv * s.D), np.uint16)
-        vc = np.zeros_like(kc)
-        pos = np.arange(T, dtype=np.int32)
-        t0 = time.perf_counter()
-        o.rms_norm_bf16(x, w["in"], s.eps, True)
-        o.qk_norm_rope_kv(q, k, v, wq, wk, kc, vc, max_seq=s.max_seq, max_kv_dim=s.nkv * s.D, pos=pos,
-                          n_heads=s.nh, n_kv_heads=s.nkv, head_dim=s.D, base=s.theta, eps=s.eps)
-        x2, _ = o.rms_norm_add_rms_norm(x, ao, w["post_attn"], w["pre_ffn"], s.eps, True)
-        o.geglu(gate, up)
-        o.rms_norm_add(x2, fo, w["post_ffn"], s.eps, True)
-        return time.perf_counter() - t0
+    def chain(a, b):
+        o.rms_norm_bf16(x[a:b], w["in"], s.eps, True)
+        o.qk_norm_rope_kv(q[a:b], k[a:b], v[a:b], wq, wk, kc, vc, max_seq=s.max_seq,
+                          max_kv_dim=s.nkv * s.D, pos=pos[a:b], n_heads=s.nh, n_kv_heads=s.nkv,
+                          head_dim=s.D, base=s.theta, eps=s.eps)
+        x2, _ = o.rms_norm_add_rms_norm(x[a:b], ao[a:b], w["post_attn"], w["pre_ffn"], s.eps, True)
+        o.geglu(gate[a:b], up[a:b])
+        o.rms_norm_add(x2, fo[a:b], w["post_ffn"], s.eps, True)
 
-    t_small = run(8)
-    T = int(min(T_full, max(8, 8 * target_s / max(t_small, 1e-6))))
-    t = run(T)
+    def timed(fn, budget):
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            reps += 1
+            t = time.perf_counter() - t0
+            if t >= budget:
+                return reps, t
+
     nbytes = LY.chain_bytes(shape, T, 2)
-    return {"value": round(nbytes / t / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"c2 per-layer chain over the first {T} of {T_full} tokens ({t:.1f} s), "
+    reps, t = timed(lambda: chain(0, T), target_s)
+    cpus = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    nt = pool_threads(cpus)
+    edges = [T * i // nt for i in range(nt + 1)]
+    with ThreadPoolExecutor(nt) as ex:
+        def par():
+            for f in [ex.submit(chain, edges[i], edges[i + 1]) for i in range(nt)]:
+                f.result()
+        par()
+        preps, pt = timed(par, parallel_s)
+    return {"value": round(reps * nbytes / t / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"c2 per-layer chain, all {T} tokens, repeated {reps}x ({t:.1f} s), "
                       f"oracle -O3 -march=x86-64-v3, one thread",
-            "us_per_token": round(t / T * 1e6, 1)}
+            "us_per_token": round(t / (reps * T) * 1e6, 1),
+            "token_parallel_upper_bound": {
+                "value": round(preps * nbytes / pt / 1e9, 4), "unit": "GB/s", "threads": nt,
+                "sample": f"same chain split over {nt} threads by token ({preps}x, {pt:.1f} s)"}}
 
 
 # ---------------------------------------------------------------------------------------

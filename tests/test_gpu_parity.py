@@ -51,7 +51,10 @@ def make_table(qtype, seed, rows, cols):
 @pytest.mark.parametrize("out_dtype", [B.F32, B.BF16])
 @pytest.mark.parametrize("qtype,dim", [(B.Q8_0, 2560), (B.Q4_0, 2560), (B.BF16, 2560), (B.F16, 2560),
                                        (B.F32, 2560), (B.Q6_K, 2560), (B.Q8_0, 96), (B.Q4_0, 160),
-                                       (B.BF16, 2562), (B.F32, 100)])
+                                       (B.BF16, 2562), (B.F32, 100),
+                                       # partial last segment / byte-staged rows
+                                       (B.Q8_0, 5376), (B.Q4_0, 5376), (B.Q6_K, 5376),
+                                       (B.BF16, 5376), (B.Q8_0, 800), (B.F16, 1000)])
 def test_embed_gather_bitexact(dev, oracle, qtype, dim, out_dtype):
     vocab = 700
     table = make_table(qtype, 2, vocab, dim)

@@ -5,13 +5,15 @@
 // output is one IEEE rounding and the result is bit-exact; Q6_K keeps the CPU's
 // ((d * scale_j) * q) * scale order.
 //
-// Layout: one wave per output row, four rows per workgroup. Block formats (Q8_0 34 B,
-// Q4_0 18 B, Q6_K 210 B per block) are not 16-byte aligned per block, but whole rows are
-// (2720 / 1440 B at 2560 columns), so a wave first copies its row into LDS with 128-bit
-// loads (byte loads when the row is not 16-byte aligned), then each lane dequantises groups of
+// Layout: one wave per segment of consecutive outputs of one row (512 outputs; 2048 for
+// Q6_K), four independent waves per workgroup (no block barrier). Block formats (Q8_0 34 B,
+// Q4_0 18 B, Q6_K 210 B per block) are not 16-byte aligned per block, but segments of 16
+// (Q8_0/Q4_0) or 8 (Q6_K) blocks are (544 / 288 / 1680 B), and so are whole rows at the
+// usual widths (2720 / 1440 B at 2560 columns). A wave copies its segment into LDS with
+// 128-bit loads (byte loads when the row is not 16-byte aligned), then each lane dequantises
 // 8 consecutive outputs from LDS and writes them with 128-bit stores: one HBM read of the
-// row, one HBM write of the output, and the per-block scale read once per group.
-// Dense types (F32, F16, BF16) skip LDS: each lane converts one 16-byte chunk.
+// row, one HBM write of the output, the per-block scale read once per 8 outputs.
+// Dense types (F32, F16, BF16) skip LDS: each lane converts 8 consecutive elements.
 #include "zl_common.h"
 #include "zl_host.h"
 
@@ -110,39 +112,76 @@ __host__ __device__ constexpr int block_elems() {
     return QT == HIP_BRIDGE_Q6_K ? 256 : 32;
 }
 
-// Block formats: one wave per row, row staged in LDS.
+// Work split: one wave per segment of kSegElems[QT] consecutive outputs of one row
+// (n_tokens * ceil(dim / seg) waves, four per workgroup, independent of each other), so a
+// 2048-4096-token gather puts tens of thousands of waves in flight instead of one per row.
+// Segments hold whole blocks and start at multiples of 16 bytes within the row.
+template <int QT>
+__host__ __device__ constexpr int seg_elems() {
+    return QT == HIP_BRIDGE_Q6_K ? 2048 : 512;  // Q8_0 544 B, Q4_0 288 B, Q6_K 1680 B
+}
+
+// Block formats: the segment's bytes are staged in LDS, then dequantised 8 outputs per lane.
 template <int QT, typename OutT>
 __global__ __launch_bounds__(256) void k_gather_blocks(const unsigned char* __restrict__ table,
                                                        const int32_t* __restrict__ ids,
                                                        OutT* __restrict__ out, int64_t n_rows,
                                                        int64_t n_tokens, int dim, float scale,
-                                                       int row_bytes, int lds_stride, int vec16,
+                                                       int row_bytes, int nseg, int vec16,
                                                        int64_t single_id) {
-    extern __shared__ __attribute__((aligned(16))) unsigned char s_rows[];
+    constexpr int SEG = seg_elems<QT>();
+    constexpr int SEG_BYTES = SEG / block_elems<QT>() * (int)block_bytes<QT>();
+    constexpr int LDS_STRIDE = (SEG_BYTES + 15) & ~15;
+    static_assert(SEG_BYTES % 16 == 0, "segments must start 16-byte aligned");
+    __shared__ __attribute__((aligned(16))) unsigned char s_seg[kGatherWaves * LDS_STRIDE];
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
-    const int64_t t = (int64_t)blockIdx.x * kGatherWaves + wave;
-    unsigned char* srow = s_rows + wave * lds_stride;
+    const int64_t wg = (int64_t)blockIdx.x * kGatherWaves + wave;
+    const int64_t t = wg / nseg;
+    const int sg = (int)(wg - t * nseg);
+    unsigned char* sseg = s_seg + wave * LDS_STRIDE;
+    const int e0 = sg * SEG;
+    const int e1 = dim - e0 < SEG ? dim : e0 + SEG;
     int64_t id = -1;
     if (t < n_tokens) {
         id = ids ? (int64_t)ids[t] : single_id;
         if (id >= 0 && id < n_rows) {
-            const unsigned char* grow = table + id * (int64_t)row_bytes;
+            const int b0 = sg * SEG_BYTES;
+            const int b1 = (e1 / block_elems<QT>()) * (int)block_bytes<QT>();
+            const unsigned char* gseg = table + id * (int64_t)row_bytes + b0;
             if (vec16) {
-                for (int i = lane; i < (row_bytes >> 4); i += kWave) st16(srow + 16 * i, lds16(grow + 16 * i));
+                // row_bytes % 16 == 0: the rounded-up last chunk stays inside the row
+                const int n16 = (b1 - b0 + 15) >> 4;
+                constexpr int UN = (SEG_BYTES / 16 + kWave - 1) / kWave;
+                u32x4 tmp[UN];
+#pragma unroll
+                for (int u = 0; u < UN; ++u) {
+                    const int i = lane + kWave * u;
+                    if (i < n16) tmp[u] = lds16(gseg + 16 * i);
+                }
+#pragma unroll
+                for (int u = 0; u < UN; ++u) {
+                    const int i = lane + kWave * u;
+                    if (i < n16) st16(sseg + 16 * i, tmp[u]);
+                }
             } else {
-                for (int i = lane; i < row_bytes; i += kWave) srow[i] = grow[i];
+                for (int i = lane; i < b1 - b0; i += kWave) sseg[i] = gseg[i];
             }
         }
     }
-    __syncthreads();
+    // Each wave reads only the segment it staged: a wave-scope fence + barrier (LDS writes
+    // complete and ordered before the reads) instead of a block barrier, so the four waves of
+    // a workgroup do not wait for each other's HBM latency.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     if (t >= n_tokens) return;
     OutT* orow = out + t * (int64_t)dim;
     const bool valid = id >= 0 && id < n_rows;
-    for (int e = lane * 8; e < dim; e += kWave * 8) {
+    for (int e = e0 + lane * 8; e < e1; e += kWave * 8) {
         float v[8];
         if (valid) {
-            dequant8<QT>(srow, e, scale, v);
+            dequant8<QT>(sseg, e - e0, scale, v);
         } else {
 #pragma unroll
             for (int j = 0; j < 8; ++j) v[j] = 0.0f;
@@ -151,57 +190,48 @@ __global__ __launch_bounds__(256) void k_gather_blocks(const unsigned char* __re
     }
 }
 
-// Dense types: each lane converts 16-byte chunks of the row (4 f32, or 8 f16/bf16).
+// Dense types: one wave per 512-output segment, each lane converts 8 consecutive elements
+// (one 16-byte load of f16/bf16, two of f32).
 template <int QT, typename OutT>
 __global__ __launch_bounds__(256) void k_gather_dense(const unsigned char* __restrict__ table,
                                                       const int32_t* __restrict__ ids,
                                                       OutT* __restrict__ out, int64_t n_rows,
                                                       int64_t n_tokens, int dim, float scale,
-                                                      int64_t single_id) {
-    constexpr int EPC = QT == HIP_BRIDGE_F32 ? 4 : 8;  // elements per 16-byte chunk
+                                                      int nseg, int64_t single_id) {
+    constexpr int ES = QT == HIP_BRIDGE_F32 ? 4 : 2;
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
-    const int64_t t = (int64_t)blockIdx.x * kGatherWaves + wave;
+    const int64_t wg = (int64_t)blockIdx.x * kGatherWaves + wave;
+    const int64_t t = wg / nseg;
     if (t >= n_tokens) return;
+    const int e = (int)(wg - t * nseg) * 512 + lane * 8;
+    if (e >= dim) return;
     const int64_t id = ids ? (int64_t)ids[t] : single_id;
-    const bool valid = id >= 0 && id < n_rows;
-    const int64_t rb = (int64_t)dim * (QT == HIP_BRIDGE_F32 ? 4 : 2);
-    const unsigned char* grow = table + (valid ? id : 0) * rb;
-    OutT* orow = out + t * (int64_t)dim;
-    for (int c = lane; c < dim / EPC; c += kWave) {
-        float v[8];
-        if (valid) {
-            const u32x4 r = lds16(grow + 16 * c);
-            if constexpr (QT == HIP_BRIDGE_F32) {
-                Chunk<float>::unpack(r, v);
-            } else if constexpr (QT == HIP_BRIDGE_BF16) {
-                Chunk<uint16_t>::unpack(r, v);
-            } else {
-                const uint32_t w[4] = {r.x, r.y, r.z, r.w};
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    v[2 * j] = f16_bits_to_f32(w[j] & 0xffff);
-                    v[2 * j + 1] = f16_bits_to_f32(w[j] >> 16);
-                }
-            }
-#pragma unroll
-            for (int j = 0; j < EPC; ++j) v[j] = v[j] * scale;
+    float v[8];
+    if (id >= 0 && id < n_rows) {
+        const unsigned char* p = table + (id * (int64_t)dim + e) * ES;
+        if constexpr (QT == HIP_BRIDGE_F32) {
+            const u32x4 r0 = lds16(p), r1 = lds16(p + 16);
+            Chunk<float>::unpack(r0, v);
+            Chunk<float>::unpack(r1, v + 4);
+        } else if constexpr (QT == HIP_BRIDGE_BF16) {
+            Chunk<uint16_t>::unpack(lds16(p), v);
         } else {
+            const u32x4 r = lds16(p);
+            const uint32_t w[4] = {r.x, r.y, r.z, r.w};
 #pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = 0.0f;
-        }
-        if constexpr (EPC == 4) {
-            if constexpr (sizeof(OutT) == 4) {
-                sts16(orow + 4 * c, Chunk<float>::pack(v));
-            } else {
-                uint32_t* o32 = reinterpret_cast<uint32_t*>(orow + 4 * c);
-                o32[0] = pack_bf16x2(v[0], v[1]);
-                o32[1] = pack_bf16x2(v[2], v[3]);
+            for (int j = 0; j < 4; ++j) {
+                v[2 * j] = f16_bits_to_f32(w[j] & 0xffff);
+                v[2 * j + 1] = f16_bits_to_f32(w[j] >> 16);
             }
-        } else {
-            store8<OutT>(orow, (int64_t)EPC * c, v);
         }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = v[j] * scale;
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = 0.0f;
     }
+    store8<OutT>(out + t * (int64_t)dim, e, v);
 }
 
 // Any dense row layout / alignment: one thread per output element (scalar loads).
@@ -251,31 +281,39 @@ template <int QT, typename OutT>
 static void launch_blocks(const void* table, const int32_t* ids, int64_t single_id, void* out,
                           int64_t n_rows, int64_t n_tokens, int dim, float scale, hipStream_t s) {
     const int64_t rb = row_bytes_of(QT, dim);
-    const int stride = (int)((rb + 15) & ~(int64_t)15);
-    const size_t lds = (size_t)stride * kGatherWaves;
-    if (lds > 160 * 1024) {
+    const int vec16 = (rb % 16 == 0) && aligned16(table);
+    const int nseg = (int)cdiv(dim, seg_elems<QT>());
+    const int64_t grid = cdiv(n_tokens * nseg, kGatherWaves);
+    if (grid > INT32_MAX) {
         set_error(HIP_BRIDGE_EUNSUPPORTED);
         return;
     }
-    const int vec16 = (rb % 16 == 0) && aligned16(table);
-    const int64_t grid = cdiv(n_tokens, kGatherWaves);
-    k_gather_blocks<QT, OutT><<<(unsigned)grid, 256, lds, s>>>(
+    k_gather_blocks<QT, OutT><<<(unsigned)grid, 256, 0, s>>>(
         (const unsigned char*)table, ids, (OutT*)out, n_rows, n_tokens, dim, scale, (int)rb,
-        stride, vec16, single_id);
+        nseg, vec16, single_id);
     check_launch();
 }
 
 template <int QT, typename OutT>
 static void launch_dense(const void* table, const int32_t* ids, int64_t single_id, void* out,
                          int64_t n_rows, int64_t n_tokens, int dim, float scale, hipStream_t s) {
-    const int epc = QT == HIP_BRIDGE_F32 ? 4 : 8;
-    const bool vec = dim % 8 == 0 && aligned16(table) && aligned16(out) && dim % epc == 0;
+    const bool vec = dim % 8 == 0 && aligned16(table) && aligned16(out);
     if (vec) {
-        const int64_t grid = cdiv(n_tokens, kGatherWaves);
+        const int nseg = (int)cdiv(dim, 512);
+        const int64_t grid = cdiv(n_tokens * nseg, kGatherWaves);
+        if (grid > INT32_MAX) {
+            set_error(HIP_BRIDGE_EUNSUPPORTED);
+            return;
+        }
         k_gather_dense<QT, OutT><<<(unsigned)grid, 256, 0, s>>>(
-            (const unsigned char*)table, ids, (OutT*)out, n_rows, n_tokens, dim, scale, single_id);
+            (const unsigned char*)table, ids, (OutT*)out, n_rows, n_tokens, dim, scale, nseg,
+            single_id);
     } else {
         const int64_t grid = cdiv(n_tokens * (int64_t)dim, 256);
+        if (grid > INT32_MAX) {
+            set_error(HIP_BRIDGE_EUNSUPPORTED);
+            return;
+        }
         k_gather_dense_scalar<QT, OutT><<<(unsigned)grid, 256, 0, s>>>(
             (const unsigned char*)table, ids, (OutT*)out, n_rows, n_tokens, dim, scale, single_id);
     }
