@@ -77,6 +77,29 @@ def test_embed_gather_bitexact(dev, oracle, qtype, dim, out_dtype):
         assert_bitexact(got, oracle.f32_to_bf16(ref), f"gather bf16-out qtype={qtype} dim={dim}")
 
 
+@pytest.mark.parametrize("qtype,offset", [(B.Q8_0, 1), (B.Q4_0, 1), (B.Q8_0, 2), (B.Q4_0, 6),
+                                          (B.BF16, 2), (B.F16, 6), (B.F32, 4), (B.Q6_K, 8)])
+@pytest.mark.parametrize("out_dtype", [B.F32, B.BF16])
+def test_embed_gather_misaligned_table(dev, oracle, qtype, offset, out_dtype):
+    """Tables at an odd or non-16-byte address take the byte-staged / scalar paths."""
+    vocab, dim = 90, 2560
+    table = make_table(qtype, 3, vocab, dim)
+    ids = synth.gather_ids(3, 64, vocab, n_repeat=8)
+    scale = SQRT[dim]
+    ref = oracle.embed_gather(table, qtype, ids, dim, scale)
+    d_raw = dev.alloc(table.nbytes + 16)
+    d_tab = d_raw.at(offset)
+    d_tab.upload(table.reshape(-1))
+    es = 4 if out_dtype == B.F32 else 2
+    d_out = dev.alloc(ids.size * dim * es)
+    dev.embedGather(d_tab, qtype, vocab, dev.from_numpy(ids), out_dtype, d_out, ids.size, dim, scale)
+    if out_dtype == B.F32:
+        assert_bitexact(d_out.to_numpy((ids.size, dim), np.float32), ref, f"qtype={qtype} +{offset}")
+    else:
+        assert_bitexact(d_out.to_numpy((ids.size, dim), np.uint16), oracle.f32_to_bf16(ref),
+                        f"bf16-out qtype={qtype} +{offset}")
+
+
 @pytest.mark.parametrize("qtype", [B.Q8_0, B.Q4_0, B.BF16, B.Q6_K])
 def test_embed_lookup_mirrors(dev, oracle, qtype):
     vocab, dim = 300, 2560

@@ -5,15 +5,18 @@
 // output is one IEEE rounding and the result is bit-exact; Q6_K keeps the CPU's
 // ((d * scale_j) * q) * scale order.
 //
-// Layout: one wave per segment of consecutive outputs of one row (512 outputs; 2048 for
-// Q6_K), four independent waves per workgroup (no block barrier). Block formats (Q8_0 34 B,
-// Q4_0 18 B, Q6_K 210 B per block) are not 16-byte aligned per block, but segments of 16
-// (Q8_0/Q4_0) or 8 (Q6_K) blocks are (544 / 288 / 1680 B), and so are whole rows at the
-// usual widths (2720 / 1440 B at 2560 columns). A wave copies its segment into LDS with
-// 128-bit loads (byte loads when the row is not 16-byte aligned), then each lane dequantises
-// 8 consecutive outputs from LDS and writes them with 128-bit stores: one HBM read of the
-// row, one HBM write of the output, the per-block scale read once per 8 outputs.
-// Dense types (F32, F16, BF16) skip LDS: each lane converts 8 consecutive elements.
+// Layout: one wave per segment of 512 consecutive outputs of one row (2048 for Q6_K), four
+// independent waves per workgroup (no block barrier): a 4096-token gather is ~20k waves.
+// Every lane produces 16 bytes of output per step (4 f32 or 8 bf16), so each store
+// instruction of a wave writes 1 KB of whole, contiguous cache lines.
+// Q8_0 / Q4_0 (34 / 18 B blocks, 2-byte aligned): each lane loads the f16 scale and the
+// quant bytes behind its outputs straight from global memory with 16-bit loads, all issued
+// before the first use; the lanes of a wave read a contiguous span of the row, so the
+// loads coalesce into that span's cache lines (measured on MI355X at 4096 x 2560: 9.4 us
+// against 12.9 us for staging the row through LDS first).
+// Q6_K (210 B super-blocks): the segment (8 super-blocks) is staged in LDS, then decoded.
+// Dense types (F32, F16, BF16): each lane converts the elements behind its 16-byte stores,
+// all loads issued before the first store.
 #include "zl_common.h"
 #include "zl_host.h"
 
@@ -29,77 +32,68 @@ __device__ __forceinline__ uint32_t lds_u16(const unsigned char* p) {
     return *reinterpret_cast<const uint16_t*>(p);
 }
 
-// Writes 8 consecutive outputs starting at element e of row `orow`.
+// Outputs per lane per step: one 16-byte store (4 f32 or 8 bf16), so each store instruction
+// of a wave writes 64 x 16 B of contiguous, whole cache lines.
 template <typename OutT>
-__device__ __forceinline__ void store8(OutT* orow, int64_t e, const float* v);
-template <>
-__device__ __forceinline__ void store8<float>(float* orow, int64_t e, const float* v) {
-    sts16(orow + e, Chunk<float>::pack(v));
-    sts16(orow + e + 4, Chunk<float>::pack(v + 4));
-}
-template <>
-__device__ __forceinline__ void store8<uint16_t>(uint16_t* orow, int64_t e, const float* v) {
-    sts16(orow + e, Chunk<uint16_t>::pack(v));
+__host__ __device__ constexpr int out_epl() {
+    return 16 / (int)sizeof(OutT);
 }
 
-// Dequantise elements [e, e+8) of a row staged at `row` in LDS, multiplied by `scale`.
-template <int QT>
-__device__ __forceinline__ void dequant8(const unsigned char* row, int e, float scale, float* v);
+template <typename OutT>
+__device__ __forceinline__ void store16(OutT* p, const float* v) {
+    sts16(p, Chunk<OutT>::pack(v));
+}
 
-template <>
-__device__ __forceinline__ void dequant8<HIP_BRIDGE_Q8_0>(const unsigned char* row, int e, float scale,
-                                                    float* v) {
-    const unsigned char* blk = row + (e >> 5) * 34;
-    const float d = f16_bits_to_f32(lds_u16(blk));
-    const unsigned char* qs = blk + 2 + (e & 31);
+// Dequantise elements [e, e+N) (N = 4 or 8, e a multiple of N) of a block row staged at
+// `row` in LDS, multiplied by `scale`.
+template <int QT, int N>
+__device__ __forceinline__ void dequant(const unsigned char* row, int e, float scale, float* v) {
+    if constexpr (QT == HIP_BRIDGE_Q8_0) {
+        const unsigned char* blk = row + (e >> 5) * 34;
+        const float d = f16_bits_to_f32(lds_u16(blk));
+        const unsigned char* qs = blk + 2 + (e & 31);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint32_t w = lds_u16(qs + 2 * j);
-        v[2 * j] = ((float)(int8_t)(w & 0xff) * d) * scale;
-        v[2 * j + 1] = ((float)(int8_t)(w >> 8) * d) * scale;
-    }
-}
-
-template <>
-__device__ __forceinline__ void dequant8<HIP_BRIDGE_Q4_0>(const unsigned char* row, int e, float scale,
-                                                    float* v) {
-    const unsigned char* blk = row + (e >> 5) * 18;
-    const float d = f16_bits_to_f32(lds_u16(blk));
-    const int o = e & 31;
-    const unsigned char* qs = blk + 2 + (o & 15);
-    const int shift = o < 16 ? 0 : 4;  // low nibbles -> elements 0..15, high -> 16..31
+        for (int j = 0; j < N / 2; ++j) {
+            const uint32_t w = lds_u16(qs + 2 * j);
+            v[2 * j] = ((float)(int8_t)(w & 0xff) * d) * scale;
+            v[2 * j + 1] = ((float)(int8_t)(w >> 8) * d) * scale;
+        }
+    } else if constexpr (QT == HIP_BRIDGE_Q4_0) {
+        const unsigned char* blk = row + (e >> 5) * 18;
+        const float d = f16_bits_to_f32(lds_u16(blk));
+        const int o = e & 31;
+        const unsigned char* qs = blk + 2 + (o & 15);
+        const int shift = o < 16 ? 0 : 4;  // low nibbles -> elements 0..15, high -> 16..31
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint32_t w = lds_u16(qs + 2 * j);
-        const int q0 = (int)((w >> shift) & 0xf) - 8;
-        const int q1 = (int)((w >> (8 + shift)) & 0xf) - 8;
-        v[2 * j] = ((float)q0 * d) * scale;
-        v[2 * j + 1] = ((float)q1 * d) * scale;
-    }
-}
-
-template <>
-__device__ __forceinline__ void dequant8<HIP_BRIDGE_Q6_K>(const unsigned char* row, int e, float scale,
-                                                    float* v) {
-    // Super-block of 256: ql[128] qh[64] scales[16] (int8) d (f16) = 210 B (types.zig:187-192).
-    const unsigned char* sb = row + (e >> 8) * 210;
-    const float d = f16_bits_to_f32(lds_u16(sb + 208));
-    const int w = e & 255;
-    const int half = w >> 7;        // n in quant.zig:359
-    const int grp = (w & 127) >> 5; // which of q1..q4
-    const int l0 = w & 31;          // 8 consecutive l, same is = l/16
-    const unsigned char* ql = sb + half * 64 + l0 + ((grp & 1) ? 32 : 0);
-    const unsigned char* qh = sb + 128 + half * 32 + l0;
-    const int8_t sc = (int8_t)sb[192 + half * 8 + (l0 >> 4) + 2 * grp];
-    const float dsc = d * (float)sc;  // exact (11-bit x 8-bit)
-    const int nshift = (grp & 2) ? 4 : 0;
-    const int hshift = 2 * grp;
+        for (int j = 0; j < N / 2; ++j) {
+            const uint32_t w = lds_u16(qs + 2 * j);
+            const int q0 = (int)((w >> shift) & 0xf) - 8;
+            const int q1 = (int)((w >> (8 + shift)) & 0xf) - 8;
+            v[2 * j] = ((float)q0 * d) * scale;
+            v[2 * j + 1] = ((float)q1 * d) * scale;
+        }
+    } else {
+        // Q6_K super-block of 256: ql[128] qh[64] scales[16] (int8) d (f16) = 210 B
+        // (types.zig:187-192); element order as quant.zig:357-385.
+        const unsigned char* sb = row + (e >> 8) * 210;
+        const float d = f16_bits_to_f32(lds_u16(sb + 208));
+        const int w = e & 255;
+        const int half = w >> 7;        // n in quant.zig:359
+        const int grp = (w & 127) >> 5; // which of q1..q4
+        const int l0 = w & 31;          // N consecutive l, same is = l/16
+        const unsigned char* ql = sb + half * 64 + l0 + ((grp & 1) ? 32 : 0);
+        const unsigned char* qh = sb + 128 + half * 32 + l0;
+        const int8_t sc = (int8_t)sb[192 + half * 8 + (l0 >> 4) + 2 * grp];
+        const float dsc = d * (float)sc;  // exact (11-bit x 8-bit)
+        const int nshift = (grp & 2) ? 4 : 0;
+        const int hshift = 2 * grp;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int lo = (ql[j] >> nshift) & 0xf;
-        const int hi = (qh[j] >> hshift) & 3;
-        const int q = (lo | (hi << 4)) - 32;
-        v[j] = (dsc * (float)q) * scale;
+        for (int j = 0; j < N; ++j) {
+            const int lo = (ql[j] >> nshift) & 0xf;
+            const int hi = (qh[j] >> hshift) & 3;
+            const int q = (lo | (hi << 4)) - 32;
+            v[j] = (dsc * (float)q) * scale;
+        }
     }
 }
 
@@ -112,16 +106,82 @@ __host__ __device__ constexpr int block_elems() {
     return QT == HIP_BRIDGE_Q6_K ? 256 : 32;
 }
 
-// Work split: one wave per segment of kSegElems[QT] consecutive outputs of one row
-// (n_tokens * ceil(dim / seg) waves, four per workgroup, independent of each other), so a
-// 2048-4096-token gather puts tens of thousands of waves in flight instead of one per row.
-// Segments hold whole blocks and start at multiples of 16 bytes within the row.
 template <int QT>
 __host__ __device__ constexpr int seg_elems() {
-    return QT == HIP_BRIDGE_Q6_K ? 2048 : 512;  // Q8_0 544 B, Q4_0 288 B, Q6_K 1680 B
+    return QT == HIP_BRIDGE_Q6_K ? 2048 : 512;
 }
 
-// Block formats: the segment's bytes are staged in LDS, then dequantised 8 outputs per lane.
+__device__ __forceinline__ uint32_t ldg_u16(const unsigned char* p) {
+    return *reinterpret_cast<const uint16_t*>(p);
+}
+
+// Q8_0 / Q4_0: one wave per 512 outputs, direct 16-bit global loads (the table only needs
+// 2-byte alignment: blocks are 34 / 18 B).
+template <int QT, typename OutT>
+__global__ __launch_bounds__(256) void k_gather_q(const unsigned char* __restrict__ table,
+                                                  const int32_t* __restrict__ ids,
+                                                  OutT* __restrict__ out, int64_t n_rows,
+                                                  int64_t n_tokens, int dim, float scale, int nseg,
+                                                  int64_t single_id) {
+    constexpr int N = out_epl<OutT>();  // outputs per lane per step
+    constexpr int K = 512 / (kWave * N);  // steps per wave
+    constexpr int BB = (int)block_bytes<QT>();
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int64_t wg = (int64_t)blockIdx.x * kGatherWaves + wave;
+    const int64_t t = wg / nseg;
+    if (t >= n_tokens) return;
+    const int e0 = (int)(wg - t * nseg) * 512;
+    const int64_t id = ids ? (int64_t)ids[t] : single_id;
+    const bool valid = id >= 0 && id < n_rows;
+    const unsigned char* grow = table + (valid ? id : 0) * (int64_t)(dim / 32) * BB;
+    uint32_t dq[K], w[K][N / 2];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int e = e0 + lane * N + kWave * N * k;
+        if (valid && e < dim) {
+            const unsigned char* blk = grow + (e >> 5) * BB;
+            dq[k] = ldg_u16(blk);
+            // Q8_0: bytes 2 + (e & 31) ..; Q4_0: nibble bytes 2 + (e & 15) .. (low nibbles
+            // hold elements 0..15 of the block, high nibbles 16..31)
+            const unsigned char* qs = blk + 2 + (QT == HIP_BRIDGE_Q8_0 ? (e & 31) : (e & 15));
+#pragma unroll
+            for (int j = 0; j < N / 2; ++j) w[k][j] = ldg_u16(qs + 2 * j);
+        }
+    }
+    OutT* orow = out + t * (int64_t)dim;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int e = e0 + lane * N + kWave * N * k;
+        if (e >= dim) break;
+        float v[N];
+        if (valid) {
+            const float d = f16_bits_to_f32(dq[k]);
+            const int shift = (e & 31) < 16 ? 0 : 4;
+#pragma unroll
+            for (int j = 0; j < N / 2; ++j) {
+                int q0, q1;
+                if constexpr (QT == HIP_BRIDGE_Q8_0) {
+                    q0 = (int8_t)(w[k][j] & 0xff);
+                    q1 = (int8_t)(w[k][j] >> 8);
+                } else {
+                    q0 = (int)((w[k][j] >> shift) & 0xf) - 8;
+                    q1 = (int)((w[k][j] >> (8 + shift)) & 0xf) - 8;
+                }
+                v[2 * j] = ((float)q0 * d) * scale;
+                v[2 * j + 1] = ((float)q1 * d) * scale;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < N; ++j) v[j] = 0.0f;
+        }
+        store16<OutT>(orow + e, v);
+    }
+}
+
+// Q6_K, and Q8_0 / Q4_0 tables at an odd address: the segment's bytes are staged in LDS
+// (128-bit loads when the row is 16-byte aligned, byte loads otherwise), then decoded.
+// Segments hold whole blocks and start at multiples of 16 bytes within the row.
 template <int QT, typename OutT>
 __global__ __launch_bounds__(256) void k_gather_blocks(const unsigned char* __restrict__ table,
                                                        const int32_t* __restrict__ ids,
@@ -157,7 +217,7 @@ __global__ __launch_bounds__(256) void k_gather_blocks(const unsigned char* __re
 #pragma unroll
                 for (int u = 0; u < UN; ++u) {
                     const int i = lane + kWave * u;
-                    if (i < n16) tmp[u] = lds16(gseg + 16 * i);
+                    if (i < n16) tmp[u] = ld16(gseg + 16 * i);
                 }
 #pragma unroll
                 for (int u = 0; u < UN; ++u) {
@@ -178,60 +238,99 @@ __global__ __launch_bounds__(256) void k_gather_blocks(const unsigned char* __re
     if (t >= n_tokens) return;
     OutT* orow = out + t * (int64_t)dim;
     const bool valid = id >= 0 && id < n_rows;
-    for (int e = e0 + lane * 8; e < e1; e += kWave * 8) {
-        float v[8];
+    constexpr int N = out_epl<OutT>();
+    for (int e = e0 + lane * N; e < e1; e += kWave * N) {
+        float v[N];
         if (valid) {
-            dequant8<QT>(sseg, e - e0, scale, v);
+            dequant<QT, N>(sseg, e - e0, scale, v);
         } else {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = 0.0f;
+            for (int j = 0; j < N; ++j) v[j] = 0.0f;
         }
-        store8<OutT>(orow, e, v);
+        store16<OutT>(orow + e, v);
     }
 }
 
-// Dense types: one wave per 512-output segment, each lane converts 8 consecutive elements
-// (one 16-byte load of f16/bf16, two of f32).
+// Dense types: one wave per 512-output segment; per step each lane converts the N inputs
+// behind one 16-byte output store (f32 -> f32: 16 B loads; 16-bit -> f32: 8 B; 16-bit ->
+// bf16: 16 B; f32 -> bf16: 2 x 16 B), every load and store instruction contiguous across
+// the wave, all of a lane's loads issued before its first store.
+template <int QT, int N>
+struct DenseIn {
+    static constexpr int ES = QT == HIP_BRIDGE_F32 ? 4 : 2;
+    static constexpr int WORDS = N * ES / 4;  // 32-bit words behind N outputs
+    uint32_t w[WORDS];
+    __device__ __forceinline__ void load(const unsigned char* p) {
+        // plain (cached) loads: for rows at random addresses they measured faster than
+        // nontemporal ones (BF16 -> f32 at 4096 x 2560: 11.4 against 13.3 us)
+        if constexpr (WORDS == 2) {
+            const u32x2 r = *reinterpret_cast<const u32x2*>(p);
+            w[0] = r.x;
+            w[1] = r.y;
+        } else {
+#pragma unroll
+            for (int c = 0; c < WORDS / 4; ++c) {
+                const u32x4 r = ld16(p + 16 * c);
+                w[4 * c] = r.x;
+                w[4 * c + 1] = r.y;
+                w[4 * c + 2] = r.z;
+                w[4 * c + 3] = r.w;
+            }
+        }
+    }
+    __device__ __forceinline__ void convert(float scale, float* v) const {
+#pragma unroll
+        for (int j = 0; j < N; ++j) {
+            float x;
+            if constexpr (QT == HIP_BRIDGE_F32) {
+                x = __uint_as_float(w[j]);
+            } else {
+                const uint32_t h = (j & 1) ? w[j >> 1] >> 16 : w[j >> 1] & 0xffff;
+                x = QT == HIP_BRIDGE_BF16 ? __uint_as_float(h << 16) : f16_bits_to_f32(h);
+            }
+            v[j] = x * scale;
+        }
+    }
+};
+
 template <int QT, typename OutT>
 __global__ __launch_bounds__(256) void k_gather_dense(const unsigned char* __restrict__ table,
                                                       const int32_t* __restrict__ ids,
                                                       OutT* __restrict__ out, int64_t n_rows,
                                                       int64_t n_tokens, int dim, float scale,
                                                       int nseg, int64_t single_id) {
-    constexpr int ES = QT == HIP_BRIDGE_F32 ? 4 : 2;
+    constexpr int N = out_epl<OutT>();
+    constexpr int K = 512 / (kWave * N);
+    using In = DenseIn<QT, N>;
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
     const int64_t wg = (int64_t)blockIdx.x * kGatherWaves + wave;
     const int64_t t = wg / nseg;
     if (t >= n_tokens) return;
-    const int e = (int)(wg - t * nseg) * 512 + lane * 8;
-    if (e >= dim) return;
+    const int e0 = (int)(wg - t * nseg) * 512;
     const int64_t id = ids ? (int64_t)ids[t] : single_id;
-    float v[8];
-    if (id >= 0 && id < n_rows) {
-        const unsigned char* p = table + (id * (int64_t)dim + e) * ES;
-        if constexpr (QT == HIP_BRIDGE_F32) {
-            const u32x4 r0 = lds16(p), r1 = lds16(p + 16);
-            Chunk<float>::unpack(r0, v);
-            Chunk<float>::unpack(r1, v + 4);
-        } else if constexpr (QT == HIP_BRIDGE_BF16) {
-            Chunk<uint16_t>::unpack(lds16(p), v);
-        } else {
-            const u32x4 r = lds16(p);
-            const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+    const bool valid = id >= 0 && id < n_rows;
+    const unsigned char* grow = table + (valid ? id : 0) * (int64_t)dim * In::ES;
+    In in[K];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                v[2 * j] = f16_bits_to_f32(w[j] & 0xffff);
-                v[2 * j + 1] = f16_bits_to_f32(w[j] >> 16);
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = v[j] * scale;
-    } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = 0.0f;
+    for (int k = 0; k < K; ++k) {
+        const int e = e0 + lane * N + kWave * N * k;
+        if (valid && e < dim) in[k].load(grow + (int64_t)e * In::ES);
     }
-    store8<OutT>(out + t * (int64_t)dim, e, v);
+    OutT* orow = out + t * (int64_t)dim;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int e = e0 + lane * N + kWave * N * k;
+        if (e >= dim) break;
+        float v[N];
+        if (valid) {
+            in[k].convert(scale, v);
+        } else {
+#pragma unroll
+            for (int j = 0; j < N; ++j) v[j] = 0.0f;
+        }
+        store16<OutT>(orow + e, v);
+    }
 }
 
 // Any dense row layout / alignment: one thread per output element (scalar loads).
@@ -295,6 +394,20 @@ static void launch_blocks(const void* table, const int32_t* ids, int64_t single_
 }
 
 template <int QT, typename OutT>
+static void launch_q(const void* table, const int32_t* ids, int64_t single_id, void* out,
+                     int64_t n_rows, int64_t n_tokens, int dim, float scale, hipStream_t s) {
+    const int nseg = (int)cdiv(dim, 512);
+    const int64_t grid = cdiv(n_tokens * nseg, kGatherWaves);
+    if (grid > INT32_MAX) {
+        set_error(HIP_BRIDGE_EUNSUPPORTED);
+        return;
+    }
+    k_gather_q<QT, OutT><<<(unsigned)grid, 256, 0, s>>>((const unsigned char*)table, ids, (OutT*)out,
+                                                        n_rows, n_tokens, dim, scale, nseg, single_id);
+    check_launch();
+}
+
+template <int QT, typename OutT>
 static void launch_dense(const void* table, const int32_t* ids, int64_t single_id, void* out,
                          int64_t n_rows, int64_t n_tokens, int dim, float scale, hipStream_t s) {
     const bool vec = dim % 8 == 0 && aligned16(table) && aligned16(out);
@@ -326,12 +439,15 @@ static void gather(const void* table, int qtype, int64_t n_rows, const int32_t* 
                    hipStream_t s) {
     const int out_es = (int)sizeof(OutT);
     const bool block_ok = dim % 8 == 0 && aligned16(out) && ((int64_t)dim * out_es) % 16 == 0;
+    const bool even = (reinterpret_cast<uintptr_t>(table) & 1u) == 0;
     switch (qtype) {
         case HIP_BRIDGE_Q8_0:
             if (!block_ok) break;
+            if (even) return launch_q<HIP_BRIDGE_Q8_0, OutT>(table, ids, single_id, out, n_rows, n_tokens, dim, scale, s);
             return launch_blocks<HIP_BRIDGE_Q8_0, OutT>(table, ids, single_id, out, n_rows, n_tokens, dim, scale, s);
         case HIP_BRIDGE_Q4_0:
             if (!block_ok) break;
+            if (even) return launch_q<HIP_BRIDGE_Q4_0, OutT>(table, ids, single_id, out, n_rows, n_tokens, dim, scale, s);
             return launch_blocks<HIP_BRIDGE_Q4_0, OutT>(table, ids, single_id, out, n_rows, n_tokens, dim, scale, s);
         case HIP_BRIDGE_Q6_K:
             if (!block_ok) break;
