@@ -236,6 +236,56 @@ def test_rmsnorm_add_rmsnorm(dev, oracle, dtype, n, rows):
         assert_bf16(go, out_ref, 1, floor=floor_o, what="bf16 norm2(x)")
 
 
+@pytest.mark.parametrize("dtype,n,rows", [(B.BF16, 2560, 4097), (B.BF16, 5376, 2049), (B.F32, 2560, 2049),
+                                          (B.BF16, 1024, 777), (B.F32, 5376, 512)])
+def test_norm_modes_many_rows(dev, oracle, dtype, n, rows):
+    """Prefill-sized row counts. rows * waves-per-row >= 8192 takes two rows per lane group
+    (the odd counts leave the last group's second row out of range); the last two cases
+    take one row per group."""
+    f = O.get().bf16_to_f32
+    bf = dtype == B.BF16
+    gen = synth.normal_bf16 if bf else synth.normal_f32
+    up = (lambda a: f(a).astype(np.float64)) if bf else (lambda a: a.astype(np.float64))
+    x = gen(9, "x", (rows, n))
+    r = gen(9, "r", (rows, n))
+    w1 = synth.normal_f32(9, "w1", (n,), 0, 0.1)
+    w2 = synth.normal_f32(9, "w2", (n,), 0, 0.1)
+    npdt = x.dtype
+
+    def check(got, ref, what, floor=0.0):
+        if bf:
+            assert_bf16(got, ref, 1, floor=floor, what=what)
+        else:
+            assert_rel(got, ref, 1e-5, floor=floor, what=what)
+
+    # NORM
+    d_o = dev.alloc(x.nbytes)
+    dev.rmsNormRows(dtype, dev.from_numpy(x), dev.from_numpy(w1), d_o, rows, n, EPS, True)
+    ref = oracle.rms_norm_bf16(x, w1, EPS, True) if bf else oracle.rms_norm(x, w1, EPS, True)
+    check(d_o.to_numpy(x.shape, npdt), ref, "norm")
+    # ADD_NORM
+    d_x, d_o = dev.from_numpy(x), dev.alloc(x.nbytes)
+    dev.addRmsNormRows(dtype, d_x, dev.from_numpy(r), dev.from_numpy(w1), d_o, rows, n, EPS, True)
+    x_ref, o_ref = (oracle.add_rms_norm_bf16 if bf else oracle.add_rms_norm)(x, r, w1, EPS, True)
+    assert_bitexact(d_x.to_numpy(x.shape, npdt), x_ref, "x + r")
+    check(d_o.to_numpy(x.shape, npdt), o_ref, "norm(x + r)")
+    # NORM_ADD: x + norm(r), relative to its summands
+    a = oracle.rms_norm(up(r).astype(np.float32), w1, EPS, True).astype(np.float64)
+    floor = 1e-5 * (np.abs(up(x)) + np.abs(a))
+    d_x = dev.from_numpy(x)
+    dev.rmsnormAddRows(dtype, d_x, dev.from_numpy(r), dev.from_numpy(w1), rows, n, EPS, True)
+    check(d_x.to_numpy(x.shape, npdt), oracle.rms_norm_add(x, r, w1, EPS, True), "x + norm(r)", floor)
+    # NORM_ADD_NORM
+    d_x, d_r = dev.from_numpy(x), dev.from_numpy(r)
+    dev.rmsNormAddRmsNorm(dtype, d_x, d_r, dev.from_numpy(w1), dev.from_numpy(w2), d_r, rows, n, EPS, True)
+    x_ref, o_ref = oracle.rms_norm_add_rms_norm(x, r, w1, w2, EPS, True)
+    s_ = up(x) + a
+    inv2 = 1.0 / np.sqrt(np.mean(s_ * s_, axis=-1, keepdims=True) + float(EPS))
+    check(d_x.to_numpy(x.shape, npdt), x_ref, "x + norm1(r)", floor)
+    check(d_r.to_numpy(x.shape, npdt), o_ref, "norm2(x + norm1(r))",
+          floor * inv2 * np.abs(1.0 + w2.astype(np.float64)))
+
+
 # ---------------------------------------------------------------------------------------
 # QK-norm + RoPE + KV append
 # ---------------------------------------------------------------------------------------

@@ -64,129 +64,145 @@ __device__ __forceinline__ float row_sum(float v, float* slot) {
     }
 }
 
-// W waves per row (W in {1, 2, 4}), 256 threads per block, 4/W rows per block. Lane g of a row
-// (g in [0, 64W)) owns chunks g, g + 64W, ... (NC of them at most).
-template <typename T, int NC, int MODE, int W>
+// W waves per row group (W in {1, 2, 4}), 256 threads per block, 4/W row groups per block,
+// R consecutive rows per group (R in {1, 2}). Lane g of a group (g in [0, 64W)) owns chunks
+// g, g + 64W, ... (NC of them at most) of each of its R rows, so it loads the weights of
+// those chunks once for R rows: the weights are f32 while bf16 rows are 2 bytes an element,
+// and at one row per lane their reads through the L1/L2 path cost up to 14% of the kernel
+// (8192 x 5376 bf16, measured). All rows' HBM loads are issued first; row r+1's loads are
+// in flight while row r is reduced and stored.
+template <typename T, int NC, int MODE, int W, int R>
 __global__ __launch_bounds__(256) void k_norm_rows(NormArgs a) {
     using C = Chunk<T>;
     constexpr int E = C::E;
-    constexpr int RPB = 4 / W;  // rows per block
+    constexpr int GPB = 4 / W;  // row groups per block
     constexpr int STRIDE = kWave * W;
-    __shared__ float s_red[2][4];
-    const int rib = (threadIdx.x >> 6) / W;  // row within block
+    // one slot set per (row, reduction): no slot is rewritten while a wave may still read it
+    __shared__ float s_red[2 * R][4];
+    const int rib = (threadIdx.x >> 6) / W;  // group within block
     const int g = threadIdx.x - rib * STRIDE;
-    const int64_t row = (int64_t)blockIdx.x * RPB + rib;
-    const bool row_ok = row < a.rows;
+    const int64_t row0 = ((int64_t)blockIdx.x * GPB + rib) * R;
     const int n = a.n;
     const int nch = n / E;
-    T* xrow = (T*)a.x + row * n;
-    const T* rrow = (const T*)a.r + row * n;
-    T* orow = (T*)a.out + row * n;
     const bool has_w1 = a.w1 != nullptr;
     const bool has_w2 = a.w2 != nullptr;
-    float* slot1 = s_red[0] + rib * W;
-    float* slot2 = s_red[1] + rib * W;
 
-    // Issue every HBM load of the row, then the (L2-resident) weights.
-    u32x4 rx[NC], rr[NC];
+    // Issue every HBM load of the group's rows, then the (L2-resident) weights.
+    u32x4 rx[R][NC], rr[R][NC];
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
-        const int idx = g + c * STRIDE;
-        if (row_ok && idx < nch) {
-            rx[c] = lds16(xrow + (int64_t)idx * E);
-            if constexpr (MODE != M_NORM) rr[c] = lds16(rrow + (int64_t)idx * E);
+    for (int r = 0; r < R; ++r) {
+        const int64_t row = row0 + r;
+        const T* xrow = (const T*)a.x + row * n;
+        const T* rrow = (const T*)a.r + row * n;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const int idx = g + c * STRIDE;
+            if (row < a.rows && idx < nch) {
+                rx[r][c] = lds16(xrow + (int64_t)idx * E);
+                if constexpr (MODE != M_NORM) rr[r][c] = lds16(rrow + (int64_t)idx * E);
+            }
         }
     }
     float f1[NC][E];
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
         const int idx = g + c * STRIDE;
-        if (row_ok && idx < nch) load_w<E>(a.w1, (int64_t)idx * E, has_w1, f1[c]);
+        if (idx < nch) load_w<E>(a.w1, (int64_t)idx * E, has_w1, f1[c]);
     }
     float f2[MODE == M_NORM_ADD_NORM ? NC : 1][E];
     if constexpr (MODE == M_NORM_ADD_NORM) {
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
             const int idx = g + c * STRIDE;
-            if (row_ok && idx < nch) load_w<E>(a.w2, (int64_t)idx * E, has_w2, f2[c]);
+            if (idx < nch) load_w<E>(a.w2, (int64_t)idx * E, has_w2, f2[c]);
         }
     }
 
-    // v: the vector normalised first.
-    float v[NC][E];
-    float ss = 0.0f;
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
-        const int idx = g + c * STRIDE;
-        if (row_ok && idx < nch) {
-            if constexpr (MODE == M_NORM) {
-                C::unpack(rx[c], v[c]);
-            } else if constexpr (MODE == M_ADD_NORM) {
-                float xv[E], rv[E];
-                C::unpack(rx[c], xv);
-                C::unpack(rr[c], rv);
-#pragma unroll
-                for (int j = 0; j < E; ++j) v[c][j] = xv[j] + rv[j];
-            } else {
-                C::unpack(rr[c], v[c]);
-            }
-#pragma unroll
-            for (int j = 0; j < E; ++j) ss = fmaf(v[c][j], v[c][j], ss);
-        }
-    }
-    ss = row_sum<W>(ss, slot1);
-    const float inv = rms_inv(ss, n, a.eps);
+    for (int r = 0; r < R; ++r) {
+        const int64_t row = row0 + r;
+        const bool row_ok = row < a.rows;
+        T* xrow = (T*)a.x + row * n;
+        T* orow = (T*)a.out + row * n;
+        float* slot1 = s_red[2 * r] + rib * W;
+        float* slot2 = s_red[2 * r + 1] + rib * W;
 
-    if constexpr (MODE == M_NORM || MODE == M_ADD_NORM) {
+        // v: the vector normalised first.
+        float v[NC][E];
+        float ss = 0.0f;
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
             const int idx = g + c * STRIDE;
             if (row_ok && idx < nch) {
-                float y[E];
+                if constexpr (MODE == M_NORM) {
+                    C::unpack(rx[r][c], v[c]);
+                } else if constexpr (MODE == M_ADD_NORM) {
+                    float xv[E], rv[E];
+                    C::unpack(rx[r][c], xv);
+                    C::unpack(rr[r][c], rv);
 #pragma unroll
-                for (int j = 0; j < E; ++j) y[j] = (v[c][j] * inv) * w_factor(f1[c][j], has_w1, a.uo);
-                if constexpr (MODE == M_ADD_NORM) sts16(xrow + (int64_t)idx * E, C::pack(v[c]));
-                sts16(orow + (int64_t)idx * E, C::pack(y));
+                    for (int j = 0; j < E; ++j) v[c][j] = xv[j] + rv[j];
+                } else {
+                    C::unpack(rr[r][c], v[c]);
+                }
+#pragma unroll
+                for (int j = 0; j < E; ++j) ss = fmaf(v[c][j], v[c][j], ss);
             }
         }
-    } else if constexpr (MODE == M_NORM_ADD) {
+        ss = row_sum<W>(ss, slot1);
+        const float inv = rms_inv(ss, n, a.eps);
+
+        if constexpr (MODE == M_NORM || MODE == M_ADD_NORM) {
 #pragma unroll
-        for (int c = 0; c < NC; ++c) {
-            const int idx = g + c * STRIDE;
-            if (row_ok && idx < nch) {
-                float xv[E];
-                C::unpack(rx[c], xv);
+            for (int c = 0; c < NC; ++c) {
+                const int idx = g + c * STRIDE;
+                if (row_ok && idx < nch) {
+                    float y[E];
 #pragma unroll
-                for (int j = 0; j < E; ++j) xv[j] = xv[j] + (v[c][j] * inv) * w_factor(f1[c][j], has_w1, a.uo);
-                sts16(xrow + (int64_t)idx * E, C::pack(xv));
-            }
-        }
-    } else {  // M_NORM_ADD_NORM
-        float ss2 = 0.0f;
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-            const int idx = g + c * STRIDE;
-            if (row_ok && idx < nch) {
-                float xv[E];
-                C::unpack(rx[c], xv);
-#pragma unroll
-                for (int j = 0; j < E; ++j) {
-                    v[c][j] = xv[j] + (v[c][j] * inv) * w_factor(f1[c][j], has_w1, a.uo);
-                    ss2 = fmaf(v[c][j], v[c][j], ss2);
+                    for (int j = 0; j < E; ++j) y[j] = (v[c][j] * inv) * w_factor(f1[c][j], has_w1, a.uo);
+                    if constexpr (MODE == M_ADD_NORM) sts16(xrow + (int64_t)idx * E, C::pack(v[c]));
+                    sts16(orow + (int64_t)idx * E, C::pack(y));
                 }
             }
-        }
-        ss2 = row_sum<W>(ss2, slot2);
-        const float inv2 = rms_inv(ss2, n, a.eps);
+        } else if constexpr (MODE == M_NORM_ADD) {
 #pragma unroll
-        for (int c = 0; c < NC; ++c) {
-            const int idx = g + c * STRIDE;
-            if (row_ok && idx < nch) {
-                float y[E];
+            for (int c = 0; c < NC; ++c) {
+                const int idx = g + c * STRIDE;
+                if (row_ok && idx < nch) {
+                    float xv[E];
+                    C::unpack(rx[r][c], xv);
 #pragma unroll
-                for (int j = 0; j < E; ++j) y[j] = (v[c][j] * inv2) * w_factor(f2[c][j], has_w2, a.uo);
-                sts16(xrow + (int64_t)idx * E, C::pack(v[c]));
-                sts16(orow + (int64_t)idx * E, C::pack(y));
+                    for (int j = 0; j < E; ++j) xv[j] = xv[j] + (v[c][j] * inv) * w_factor(f1[c][j], has_w1, a.uo);
+                    sts16(xrow + (int64_t)idx * E, C::pack(xv));
+                }
+            }
+        } else {  // M_NORM_ADD_NORM
+            float ss2 = 0.0f;
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                const int idx = g + c * STRIDE;
+                if (row_ok && idx < nch) {
+                    float xv[E];
+                    C::unpack(rx[r][c], xv);
+#pragma unroll
+                    for (int j = 0; j < E; ++j) {
+                        v[c][j] = xv[j] + (v[c][j] * inv) * w_factor(f1[c][j], has_w1, a.uo);
+                        ss2 = fmaf(v[c][j], v[c][j], ss2);
+                    }
+                }
+            }
+            ss2 = row_sum<W>(ss2, slot2);
+            const float inv2 = rms_inv(ss2, n, a.eps);
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                const int idx = g + c * STRIDE;
+                if (row_ok && idx < nch) {
+                    float y[E];
+#pragma unroll
+                    for (int j = 0; j < E; ++j) y[j] = (v[c][j] * inv2) * w_factor(f2[c][j], has_w2, a.uo);
+                    sts16(xrow + (int64_t)idx * E, C::pack(v[c]));
+                    sts16(orow + (int64_t)idx * E, C::pack(y));
+                }
             }
         }
     }
@@ -273,23 +289,37 @@ __global__ __launch_bounds__(256) void k_norm_rows_generic(NormArgs a) {
 }
 
 template <typename T, int MODE, int W>
-static void launch_w(const NormArgs& a, int per_lane, hipStream_t s) {
-    const unsigned grid = (unsigned)cdiv(a.rows, 4 / W);
-    if (per_lane <= 1) k_norm_rows<T, 1, MODE, W><<<grid, 256, 0, s>>>(a);
-    else if (per_lane <= 2) k_norm_rows<T, 2, MODE, W><<<grid, 256, 0, s>>>(a);
-    else if (per_lane <= 4) k_norm_rows<T, 4, MODE, W><<<grid, 256, 0, s>>>(a);
-    else if (per_lane <= 8) k_norm_rows<T, 8, MODE, W><<<grid, 256, 0, s>>>(a);
-    else if constexpr (W == 4) k_norm_rows<T, 16, MODE, W><<<grid, 256, 0, s>>>(a);
+static void launch_w(const NormArgs& a, int per_lane, int R, hipStream_t s) {
+    const unsigned grid = (unsigned)cdiv(a.rows, (int64_t)(4 / W) * R);
+    // NC = chunks per lane, fitted to the row (the register footprint, and so the occupancy,
+    // grows with NC); two rows per lane group up to 4 chunks per lane
+    if (R == 2 && per_lane <= 4) {
+        if (per_lane <= 1) k_norm_rows<T, 1, MODE, W, 2><<<grid, 256, 0, s>>>(a);
+        else if (per_lane <= 2) k_norm_rows<T, 2, MODE, W, 2><<<grid, 256, 0, s>>>(a);
+        else if (per_lane <= 3) k_norm_rows<T, 3, MODE, W, 2><<<grid, 256, 0, s>>>(a);
+        else k_norm_rows<T, 4, MODE, W, 2><<<grid, 256, 0, s>>>(a);
+        return;
+    }
+    const unsigned grid1 = (unsigned)cdiv(a.rows, 4 / W);
+    if (per_lane <= 1) k_norm_rows<T, 1, MODE, W, 1><<<grid1, 256, 0, s>>>(a);
+    else if (per_lane <= 2) k_norm_rows<T, 2, MODE, W, 1><<<grid1, 256, 0, s>>>(a);
+    else if (per_lane <= 3) k_norm_rows<T, 3, MODE, W, 1><<<grid1, 256, 0, s>>>(a);
+    else if (per_lane <= 4) k_norm_rows<T, 4, MODE, W, 1><<<grid1, 256, 0, s>>>(a);
+    else if (per_lane <= 6) k_norm_rows<T, 6, MODE, W, 1><<<grid1, 256, 0, s>>>(a);
+    else if (per_lane <= 8) k_norm_rows<T, 8, MODE, W, 1><<<grid1, 256, 0, s>>>(a);
+    else if constexpr (W == 4) k_norm_rows<T, 16, MODE, W, 1><<<grid1, 256, 0, s>>>(a);
 }
 
 // Waves per row: the fewest (1, 2 or 4) that keep a row within 4 chunks (128-bit loads)
-// per lane, so a row lives in registers with few cross-wave reductions; rows longer than
-// 4 chunks per lane at 4 waves take up to 16. NORM_ADD_NORM (two reductions) takes one
-// wave per row up to 8 chunks per lane: measured at 2048 x 2560 bf16 this keeps every row
-// resident at once (8.8 us against 11.4 us with 2 or 4 waves per row, which need a second
-// round of blocks at their occupancy). ZL_NORM_WAVES_PER_ROW forces a value.
+// per lane (3 for NORM_ADD_NORM, which also holds the second weight vector), so a row lives
+// in registers with few cross-wave reductions and every row of a 2048-token prefill is
+// resident at once; rows longer than that at 4 waves take up to 16 chunks per lane.
+// ZL_NORM_WAVES_PER_ROW and ZL_NORM_ROWS_PER_GROUP force values.
 #ifndef ZL_NORM_WAVES_PER_ROW
 #define ZL_NORM_WAVES_PER_ROW 0
+#endif
+#ifndef ZL_NORM_ROWS_PER_GROUP
+#define ZL_NORM_ROWS_PER_GROUP 0
 #endif
 template <typename T, int MODE>
 static void launch_t(const NormArgs& a, hipStream_t s) {
@@ -297,17 +327,21 @@ static void launch_t(const NormArgs& a, hipStream_t s) {
     const int nch = a.n / E;
     int W = ZL_NORM_WAVES_PER_ROW;
     if (W == 0) {
-        if (MODE == M_NORM_ADD_NORM && nch <= 8 * kWave) W = 1;
-        else W = nch <= 4 * kWave ? 1 : nch <= 8 * kWave ? 2 : 4;
+        const int fit = MODE == M_NORM_ADD_NORM ? 3 : 4;
+        W = nch <= fit * kWave ? 1 : nch <= 2 * fit * kWave ? 2 : 4;
     }
     const int per_lane = (int)cdiv(nch, kWave * W);
+    // Two rows per lane group once the launch has several rounds of waves (measured: 8192 x
+    // 5376 bf16, 4 waves per row, 5-8% faster for every mode); below that, one row each keeps
+    // more waves per SIMD in flight (2048 x 2560 bf16, 2 waves per row: 2-5% faster).
+    const int R = ZL_NORM_ROWS_PER_GROUP ? ZL_NORM_ROWS_PER_GROUP : a.rows * W >= 8192 ? 2 : 1;
     const bool vec = a.n % E == 0 && aligned16(a.x) && (MODE == M_NORM || aligned16(a.r)) &&
                      (MODE == M_NORM_ADD || aligned16(a.out)) && aligned16(a.w1) &&
                      (MODE != M_NORM_ADD_NORM || aligned16(a.w2)) && per_lane <= (W == 4 ? 16 : 8);
     if (vec) {
-        if (W == 4) launch_w<T, MODE, 4>(a, per_lane, s);
-        else if (W == 2) launch_w<T, MODE, 2>(a, per_lane, s);
-        else launch_w<T, MODE, 1>(a, per_lane, s);
+        if (W == 4) launch_w<T, MODE, 4>(a, per_lane, R, s);
+        else if (W == 2) launch_w<T, MODE, 2>(a, per_lane, R, s);
+        else launch_w<T, MODE, 1>(a, per_lane, R, s);
     } else {
         k_norm_rows_generic<T, MODE><<<(unsigned)a.rows, 256, 0, s>>>(a);
     }
