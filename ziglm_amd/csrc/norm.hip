@@ -71,11 +71,19 @@ __device__ __forceinline__ float row_sum(float v, float* slot) {
 // and at one row per lane their reads through the L1/L2 path cost up to 14% of the kernel
 // (8192 x 5376 bf16, measured). All rows' HBM loads are issued first; row r+1's loads are
 // in flight while row r is reduced and stored.
+#ifndef ZL_NORM_GROUPS_PER_BLOCK
+#define ZL_NORM_GROUPS_PER_BLOCK 0
+#endif
+template <int W>
+__host__ __device__ constexpr int norm_gpb() {
+    return ZL_NORM_GROUPS_PER_BLOCK ? ZL_NORM_GROUPS_PER_BLOCK : 4 / W;
+}
+
 template <typename T, int NC, int MODE, int W, int R>
 __global__ __launch_bounds__(256) void k_norm_rows(NormArgs a) {
     using C = Chunk<T>;
     constexpr int E = C::E;
-    constexpr int GPB = 4 / W;  // row groups per block
+    constexpr int GPB = norm_gpb<W>();  // row groups per block
     constexpr int STRIDE = kWave * W;
     // one slot set per (row, reduction): no slot is rewritten while a wave may still read it
     __shared__ float s_red[2 * R][4];
@@ -290,24 +298,26 @@ __global__ __launch_bounds__(256) void k_norm_rows_generic(NormArgs a) {
 
 template <typename T, int MODE, int W>
 static void launch_w(const NormArgs& a, int per_lane, int R, hipStream_t s) {
-    const unsigned grid = (unsigned)cdiv(a.rows, (int64_t)(4 / W) * R);
+    constexpr int GPB = norm_gpb<W>();
+    constexpr int NT = 64 * W * GPB;
+    const unsigned grid = (unsigned)cdiv(a.rows, (int64_t)GPB * R);
     // NC = chunks per lane, fitted to the row (the register footprint, and so the occupancy,
     // grows with NC); two rows per lane group up to 4 chunks per lane
     if (R == 2 && per_lane <= 4) {
-        if (per_lane <= 1) k_norm_rows<T, 1, MODE, W, 2><<<grid, 256, 0, s>>>(a);
-        else if (per_lane <= 2) k_norm_rows<T, 2, MODE, W, 2><<<grid, 256, 0, s>>>(a);
-        else if (per_lane <= 3) k_norm_rows<T, 3, MODE, W, 2><<<grid, 256, 0, s>>>(a);
-        else k_norm_rows<T, 4, MODE, W, 2><<<grid, 256, 0, s>>>(a);
+        if (per_lane <= 1) k_norm_rows<T, 1, MODE, W, 2><<<grid, NT, 0, s>>>(a);
+        else if (per_lane <= 2) k_norm_rows<T, 2, MODE, W, 2><<<grid, NT, 0, s>>>(a);
+        else if (per_lane <= 3) k_norm_rows<T, 3, MODE, W, 2><<<grid, NT, 0, s>>>(a);
+        else k_norm_rows<T, 4, MODE, W, 2><<<grid, NT, 0, s>>>(a);
         return;
     }
-    const unsigned grid1 = (unsigned)cdiv(a.rows, 4 / W);
-    if (per_lane <= 1) k_norm_rows<T, 1, MODE, W, 1><<<grid1, 256, 0, s>>>(a);
-    else if (per_lane <= 2) k_norm_rows<T, 2, MODE, W, 1><<<grid1, 256, 0, s>>>(a);
-    else if (per_lane <= 3) k_norm_rows<T, 3, MODE, W, 1><<<grid1, 256, 0, s>>>(a);
-    else if (per_lane <= 4) k_norm_rows<T, 4, MODE, W, 1><<<grid1, 256, 0, s>>>(a);
-    else if (per_lane <= 6) k_norm_rows<T, 6, MODE, W, 1><<<grid1, 256, 0, s>>>(a);
-    else if (per_lane <= 8) k_norm_rows<T, 8, MODE, W, 1><<<grid1, 256, 0, s>>>(a);
-    else if constexpr (W == 4) k_norm_rows<T, 16, MODE, W, 1><<<grid1, 256, 0, s>>>(a);
+    const unsigned grid1 = (unsigned)cdiv(a.rows, GPB);
+    if (per_lane <= 1) k_norm_rows<T, 1, MODE, W, 1><<<grid1, NT, 0, s>>>(a);
+    else if (per_lane <= 2) k_norm_rows<T, 2, MODE, W, 1><<<grid1, NT, 0, s>>>(a);
+    else if (per_lane <= 3) k_norm_rows<T, 3, MODE, W, 1><<<grid1, NT, 0, s>>>(a);
+    else if (per_lane <= 4) k_norm_rows<T, 4, MODE, W, 1><<<grid1, NT, 0, s>>>(a);
+    else if (per_lane <= 6) k_norm_rows<T, 6, MODE, W, 1><<<grid1, NT, 0, s>>>(a);
+    else if (per_lane <= 8) k_norm_rows<T, 8, MODE, W, 1><<<grid1, NT, 0, s>>>(a);
+    else if constexpr (W == 4) k_norm_rows<T, 16, MODE, W, 1><<<grid1, NT, 0, s>>>(a);
 }
 
 // Waves per row: the fewest (1, 2 or 4) that keep a row within 4 chunks (128-bit loads)
