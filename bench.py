@@ -287,32 +287,40 @@ def bench_decode(dev, B_, pos_seed=4, n_launch=200):
 # c3: embedding gather
 # ---------------------------------------------------------------------------------------
 
-def bench_gather(dev, vocab=262144, dim=2560, n_tok=4096, n_rep=64):
-    out = {}
+GATHER_QTYPES = {"q8_0": B.Q8_0, "q4_0": B.Q4_0, "bf16": B.BF16}
+
+
+def gather_case(dev, name, vocab=262144, dim=2560, n_tok=4096, n_rep=64, nsets=8):
+    """c3: a [vocab x dim] table of `name` rows, `nsets` id lists (4032 uniform + 64 repeated
+    ids) and f32 outputs; returns (launch fn, sets, algorithmic bytes, buffers to free)."""
+    qt = GATHER_QTYPES[name]
+    rb = {"q8_0": dim // 32 * 34, "q4_0": dim // 32 * 18, "bf16": dim * 2}[name]
     scale = np.float32(np.sqrt(np.float32(dim)))
-    nsets = 8
     id_sets = [dev.from_numpy(synth.gather_ids(2 + i, n_tok, vocab, n_repeat=n_rep)) for i in range(nsets)]
     outs = [dev.alloc(n_tok * dim * 4) for _ in range(nsets)]
-    for qt, name, rb in ((B.Q8_0, "q8_0", dim // 32 * 34), (B.Q4_0, "q4_0", dim // 32 * 18),
-                         (B.BF16, "bf16", dim * 2)):
-        tab = dev.alloc(vocab * rb)
-        if qt == B.BF16:
-            fill_tiled(tab, pool(B.BF16))
-        else:  # 64 seeded rows tiled over the vocabulary (finite block scales)
-            row = (synth.q8_0_table if qt == B.Q8_0 else synth.q4_0_table)(2, 64, dim)
-            fill_tiled(tab, row.reshape(-1))
+    tab = dev.alloc(vocab * rb)
+    if qt == B.BF16:
+        fill_tiled(tab, pool(B.BF16))
+    else:  # 64 seeded rows tiled over the vocabulary (finite block scales)
+        row = (synth.q8_0_table if qt == B.Q8_0 else synth.q4_0_table)(2, 64, dim)
+        fill_tiled(tab, row.reshape(-1))
 
-        def g(dev_, i, tab=tab, qt=qt):
-            dev_.embedGather(tab, qt, vocab, id_sets[i], B.F32, outs[i], n_tok, dim, scale)
-        sets = list(range(nsets))
-        us = time_launches_us(dev, g, sets, 4 * nsets)
-        nbytes = n_tok * (rb + dim * 4) + 4 * n_tok
+    def g(dev_, i):
+        dev_.embedGather(tab, qt, vocab, id_sets[i], B.F32, outs[i], n_tok, dim, scale)
+    nbytes = n_tok * (rb + dim * 4) + 4 * n_tok
+    return g, list(range(nsets)), nbytes, [tab] + outs + id_sets
+
+
+def bench_gather(dev):
+    out = {}
+    for name in GATHER_QTYPES:
+        g, sets, nbytes, bufs = gather_case(dev, name)
+        us = time_launches_us(dev, g, sets, 4 * len(sets))
         out[name] = {"us": round(us, 2), "bytes": nbytes, "GBps": round(nbytes / us / 1e3, 1),
                      "frac_peak": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4)}
         log(f"  gather {name}: {us:.2f} us {nbytes / us / 1e3:.0f} GB/s")
-        tab.deinit()
-    for o in outs + id_sets:
-        o.deinit()
+        for b_ in bufs:
+            b_.deinit()
     return out
 
 
@@ -416,7 +424,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="headline config only")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default=None, help="run one op only (profiling); 'copy' = hipMemcpy "
+    ap.add_argument("--only", default=None, help="run one op only (profiling): a chain op, "
+                    "gather_q8_0 / gather_q4_0 / gather_bf16 (c3), or 'copy' = hipMemcpy "
                     "device-to-device of the GeGLU output size (counter calibration)")
     ap.add_argument("--eager", action="store_true", help="with --only: launch eagerly, no graph")
     ap.add_argument("--config", default="c2", choices=["c2", "c4"])
@@ -432,14 +441,17 @@ def main():
     shape, T = (LY.GEMMA_4B, 2048) if a.config == "c2" else (LY.GEMMA_27B, 8192)
 
     if a.only:
-        sets, _ = make_sets(dev, shape, T, B.BF16)
-        if a.only == "copy":
+        if a.only.startswith("gather_"):
+            fn, sets, traffic, _ = gather_case(dev, a.only[len("gather_"):])
+        elif a.only == "copy":
+            sets, _ = make_sets(dev, shape, T, B.BF16)
             nb = sets[0].act.size_bytes
 
             def fn(d, L):
                 d.b.check(d.b.hip_memcpy_d2d(L.act.ptr, L.gate.ptr, nb, d.stream), "copy")
             traffic = 2 * nb
         else:
+            sets, _ = make_sets(dev, shape, T, B.BF16)
             fn = LY.OPS[a.only]
             traffic = LY.op_bytes(shape, T, 2)[a.only]
         if a.eager:
@@ -490,10 +502,18 @@ def main():
                      "bytes_per_launch": gl["bytes"], "us_per_launch": gl["us"]},
         "ops": c2["ops"],
     }
+    # measured HBM bytes per launch (rocprofv3, copy-calibrated) where a profile exists
+    tr = load_traffic()
+    for k, v in result["ops"].items():
+        if f"{k}_c2" in tr:
+            v["traffic"] = tr[f"{k}_c2"]
     if not a.quick:
         cfgs = {}
         log("c3 gather")
         cfgs["c3_gather"] = bench_gather(dev)
+        for k, v in cfgs["c3_gather"].items():
+            if f"gather_{k}_c3" in tr:
+                v["traffic"] = tr[f"gather_{k}_c3"]
         log("c4 27B prefill")
         c4 = bench_prefill(dev, LY.GEMMA_27B, 8192, B.BF16, max(4, a.steps // 4), 2)
         cfgs["c4_prefill"] = {k: c4[k] for k in ("us_per_layer", "us_per_layer_isolated_sum",
