@@ -254,7 +254,7 @@ def bench_decode(dev, B_, pos_seed=4, n_launch=200):
                           1.0, s.eps, s.uo)
 
     fns = {"input_norm": LY.op_input_norm, "qk_norm_rope_kv": qk, "norm_add_norm": LY.op_norm_add_norm,
-           "geglu": LY.op_geglu, "norm_add": LY.op_norm_add}
+           "geglu": LY.op_geglu, "norm_add": LY.op_norm_add, "norm_add_norm_next": LY.OPS["norm_add_norm_next"]}
     nb = LY.op_bytes(s, B_, 4)
     nb["qk_norm_rope_kv"] += 8 * B_  # slot table
     ops = {}
@@ -262,6 +262,7 @@ def bench_decode(dev, B_, pos_seed=4, n_launch=200):
         us = time_launches_us(dev, fn, [L], n_launch)
         ops[name] = {"us": round(us, 3), "GBps": round(nb[name] / us / 1e3, 2)}
     chain_us = time_launches_us(dev, lambda d, L_: [fns[k](d, L_) for k in LY.CHAIN], [L], n_launch // 5)
+    fused_us = time_launches_us(dev, lambda d, L_: [fns[k](d, L_) for k in LY.CHAIN_FUSED], [L], n_launch // 4)
     # final norm + soft-cap on the logits
     V = 262144
     logits = dev.alloc(B_ * V * 4)
@@ -276,7 +277,7 @@ def bench_decode(dev, B_, pos_seed=4, n_launch=200):
         bb.deinit()
     free_sets([L])
     cap_bytes = 2 * 4 * B_ * V
-    return {"B": B_, "us_per_layer": round(chain_us, 2), "ops": ops,
+    return {"B": B_, "us_per_layer": round(chain_us, 2), "us_per_layer_fused_4op": round(fused_us, 2), "ops": ops,
             "final_norm_us": round(us_fnorm, 3),
             "softcap": {"us": round(us_cap, 2), "bytes": cap_bytes,
                         "GBps": round(cap_bytes / us_cap / 1e3, 1),
@@ -432,7 +433,8 @@ def main():
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {a.gpus} is not supported in this build "
-              f"(the fused per-layer ops need no inter-GPU exchange; see DESIGN.md on sharding)",
+              f"(the fused per-layer ops are independent per token and per head, so more GPUs "
+              f"each run them on their own token or head shard)",
               file=sys.stderr)
         sys.exit(2)
 
@@ -523,7 +525,8 @@ def main():
         cfgs["c5_decode"] = {}
         for b_ in (1, 8, 64, 256):
             cfgs["c5_decode"][f"B{b_}"] = bench_decode(dev, b_)
-            log(f"  B={b_}: {cfgs['c5_decode'][f'B{b_}']['us_per_layer']} us/layer")
+            log(f"  B={b_}: {cfgs['c5_decode'][f'B{b_}']['us_per_layer']} us/layer, "
+                f"{cfgs['c5_decode'][f'B{b_}']['us_per_layer_fused_4op']} fused")
         result["configs"] = cfgs
     if not a.no_cpu:
         log("cpu baseline")
