@@ -198,6 +198,45 @@ void hip_qk_norm_rope_kv(int dtype, void* q, const void* k, const void* v,
                          float eps, int use_unit_offset, HipStream_t stream);
 
 /* ---------------------------------------------------------------------------------- */
+/* GEMV / small-batch GEMM, f32 activations (replaces cuda_bridge.h:36-50)              */
+/* y[r] = sum_c W[r][c] * x[c]; W: rows x cols in GGML layout (Q4_0, Q8_0: cols % 32    */
+/* == 0, rows of (cols/32)*18 or *34 bytes; F16/BF16/F32 rows of cols elements).        */
+/* Arithmetic is ziglm's CPU definition (math.zig:25-330, 652-846): exact dequantisation */
+/* and f32 sums with x kept in f32 (no Q8_1 activation quantisation as in the CUDA       */
+/* kernels); the summation order differs from the CPU's.                                 */
+/* ---------------------------------------------------------------------------------- */
+void hip_gemv_q4_0(const void* weights, const float* x, float* y, int rows, int cols,
+                   HipStream_t stream);                                     /* cuda_bridge.h:36 */
+void hip_gemv_q8_0(const void* weights, const float* x, float* y, int rows, int cols,
+                   HipStream_t stream);                                     /* cuda_bridge.h:37 */
+void hip_gemv_f16(const void* weights, const float* x, float* y, int rows, int cols,
+                  HipStream_t stream);                                      /* cuda_bridge.h:40 */
+void hip_gemv_bf16(const void* weights, const float* x, float* y, int rows, int cols,
+                   HipStream_t stream);                                     /* cuda_bridge.h:41 */
+void hip_gemv_f32(const float* weights, const float* x, float* y, int rows, int cols,
+                  HipStream_t stream);                       /* cuda_bridge.cu:1151, cuda.zig:39 */
+/* qtype dispatch; unsupported types (Q4_K, Q6_K, ...) are a no-op + EUNSUPPORTED (the
+ * reference treats every unknown type as F32). */
+void hip_gemv(int qtype, const void* weights, const float* x, float* y, int rows, int cols,
+              HipStream_t stream);                                          /* cuda_bridge.h:42 */
+/* act_out[r] = gelu_tanh(gate_r . x) * (up_r . x) */
+void hip_gemv_geglu_q4_0(const void* gate_w, const void* up_w, const float* x, float* act_out,
+                         int rows, int cols, HipStream_t stream);           /* cuda_bridge.h:43 */
+/* three products over one x in one launch; any of the row counts may be 0 */
+void hip_gemv_qkv_q4_0(const void* q_w, const void* k_w, const void* v_w, const float* x,
+                       float* q_out, float* k_out, float* v_out, int q_rows, int k_rows,
+                       int v_rows, int cols, HipStream_t stream);            /* cuda_bridge.h:44 */
+/* Y[b*rows + r] = W[r] . X[b*cols ...], b < batch_size (batch 1 is the GEMV). */
+void hip_gemm_q4_0(const void* weights, const float* x, float* y, int batch_size, int rows,
+                   int cols, HipStream_t stream);                           /* cuda_bridge.h:47 */
+void hip_gemm_q8_0(const void* weights, const float* x, float* y, int batch_size, int rows,
+                   int cols, HipStream_t stream);                           /* cuda_bridge.h:48 */
+void hip_gemm_f16(const void* weights, const float* x, float* y, int batch_size, int rows,
+                  int cols, HipStream_t stream);                            /* cuda_bridge.h:49 */
+void hip_gemm(int qtype, const void* weights, const float* x, float* y, int batch_size,
+              int rows, int cols, HipStream_t stream);                      /* cuda_bridge.h:50 */
+
+/* ---------------------------------------------------------------------------------- */
 /* Activations & elementwise (replaces cuda_bridge.h:64, 66-68)                         */
 /* ---------------------------------------------------------------------------------- */
 /* out = gelu_tanh(gate) * up; out may alias gate or up. */

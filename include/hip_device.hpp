@@ -78,6 +78,30 @@ public:
 
     void sync() const { check(hip_stream_sync(stream), "hip_stream_sync"); }
 
+    // cuda.zig:281-356
+    void gemv(GGMLType qtype, const void* d_weights, const float* d_x, float* d_y, size_t rows,
+              size_t cols) const {
+        hip_gemv((int)qtype, d_weights, d_x, d_y, (int)rows, (int)cols, stream);
+    }
+    void gemvGegluQ4_0(const void* d_gate_w, const void* d_up_w, const float* d_x, float* d_act_out,
+                       size_t rows, size_t cols) const {
+        hip_gemv_geglu_q4_0(d_gate_w, d_up_w, d_x, d_act_out, (int)rows, (int)cols, stream);
+    }
+    void gemvQkvQ4_0(const void* d_q_w, const void* d_k_w, const void* d_v_w, const float* d_x, float* d_q_out,
+                     float* d_k_out, float* d_v_out, size_t q_rows, size_t k_rows, size_t v_rows,
+                     size_t cols) const {
+        hip_gemv_qkv_q4_0(d_q_w, d_k_w, d_v_w, d_x, d_q_out, d_k_out, d_v_out, (int)q_rows, (int)k_rows,
+                          (int)v_rows, (int)cols, stream);
+    }
+    void gemmQ4_0(const void* d_weights, const float* d_x, float* d_y, size_t batch_size, size_t rows,
+                  size_t cols) const {
+        hip_gemm_q4_0(d_weights, d_x, d_y, (int)batch_size, (int)rows, (int)cols, stream);
+    }
+    void gemm(GGMLType qtype, const void* d_weights, const float* d_x, float* d_y, size_t batch_size,
+              size_t rows, size_t cols) const {
+        hip_gemm((int)qtype, d_weights, d_x, d_y, (int)batch_size, (int)rows, (int)cols, stream);
+    }
+
     // cuda.zig:358-380
     void embedLookup(const void* d_weights, GGMLType qtype, uint32_t token_id, float* d_out, size_t dim,
                      float scale_factor) const {

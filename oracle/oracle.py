@@ -54,6 +54,12 @@ _SIGS = {
     "zo_rms_norm_add_rms_norm": (None, [_fp, _fp, _fp, _fp, _sz, _sz, _f, _i]),
     "zo_rms_norm_add_bf16": (None, [_u16p, _u16p, _fp, _sz, _sz, _f, _i]),
     "zo_geglu_bf16": (None, [_u16p, _u16p, _u16p, _sz]),
+    "zo_dot_f32": (ctypes.c_float, [_fp, _fp, _sz]),
+    "zo_dot_q8_0": (ctypes.c_float, [_u8p, _fp, _sz]),
+    "zo_dot_q4_0": (ctypes.c_float, [_u8p, _fp, _sz]),
+    "zo_dot_row": (ctypes.c_float, [_i, _u8p, _fp, _sz]),
+    "zo_gemv": (_i, [_i, _u8p, _fp, _fp, _sz, _sz]),
+    "zo_gemm": (_i, [_i, _u8p, _fp, _fp, _sz, _sz, _sz]),
     "zo_qk_norm_rope_kv": (
         None,
         [_i, _vp, _vp, _vp, _fp, _fp, _i, _vp, _vp, _sz, _sz, _sz, _i32p, ctypes.c_int64, _i64p,
@@ -126,6 +132,33 @@ class Oracle:
         if rc != 0:
             raise ValueError(f"unsupported qtype {qtype}")
         return out
+
+    def dot_row(self, qtype, row, x):
+        """math.dotRow over one weight row (bytes) and f32 x."""
+        row = np.ascontiguousarray(row, dtype=np.uint8)
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        return float(self.lib.zo_dot_row(qtype, self._p(row, _u8p), self.fp(x), x.size))
+
+    def gemv(self, qtype, w, x):
+        """math.gemv: w is [rows, row_bytes] uint8 (or [rows, cols] f32 for F32), x f32[cols]."""
+        x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+        w = np.ascontiguousarray(w).view(np.uint8).reshape(w.shape[0], -1)
+        y = np.empty(w.shape[0], np.float32)
+        if self.lib.zo_gemv(qtype, self._p(w, _u8p), self.fp(x), self.fp(y), w.shape[0], x.size) != 0:
+            raise ValueError(f"unsupported qtype {qtype}")
+        return y
+
+    def gemm(self, qtype, w, x):
+        """math.gemm: x f32[batch, cols] -> y f32[batch, rows] (batch 1 is gemv)."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        x2 = x.reshape(-1, x.shape[-1])
+        w = np.ascontiguousarray(w).view(np.uint8).reshape(w.shape[0], -1)
+        y = np.empty((x2.shape[0], w.shape[0]), np.float32)
+        rc = self.lib.zo_gemm(qtype, self._p(w, _u8p), self.fp(x2), self.fp(y), x2.shape[0], w.shape[0],
+                              x2.shape[1])
+        if rc != 0:
+            raise ValueError(f"unsupported qtype {qtype}")
+        return y
 
     def rms_norm(self, x, w, eps, unit_offset=True):
         """Row-wise math.rmsNorm over the last axis (w=None -> rmsNormNoScale)."""

@@ -99,6 +99,17 @@ void zo_qk_norm_rope_kv(int dtype, void* q, const void* k, const void* v, const 
                         size_t n_kv_heads, size_t head_dim, size_t rotary_dim, float freq_base,
                         float freq_scale, float eps, int unit_offset);
 
+/* ---- dot products, GEMV, GEMM (math.zig:25-330, 652-846; ziglm_oracle_gemv.c) ---- */
+float zo_dot_f32(const float* a, const float* b, size_t n);
+float zo_dot_q8_0(const uint8_t* row, const float* x, size_t n);
+float zo_dot_q4_0(const uint8_t* row, const float* x, size_t n);
+float zo_dot_row(int qtype, const uint8_t* row, const float* x, size_t cols);
+/* y[r] = dotRow(W[r], x), rows of zo_row_bytes(qtype, cols) bytes. */
+int zo_gemv(int qtype, const uint8_t* w, const float* x, float* y, size_t rows, size_t cols);
+/* Y[b*rows + r] for X[b*cols + c]; batch 1 is zo_gemv. */
+int zo_gemm(int qtype, const uint8_t* w, const float* x, float* y, size_t batch, size_t rows,
+            size_t cols);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,159 @@
+"""Pins the oracle's dot products, GEMV and GEMM (oracle/ziglm_oracle_gemv.c, restating
+math.zig:25-330 and 652-846) before they are trusted as the checker for the HIP GEMV.
+
+* Closed form: with integer-valued weights, activations and power-of-two block scales every
+  partial sum is an integer below 2^24, so each f32 sum is exact whatever its order and the
+  result must equal the exact integer dot product bit for bit. A dropped or repeated block,
+  a wrong nibble order (low nibbles are elements 0..15), a missing -8 offset, a wrong sign
+  or scale index, or a lost 8-element tail fails this.
+* float64: random rows agree with the exact dot product of the dequantised row within
+  2^-20 * sum |w_i x_i| (f32 summation error of a few thousand terms).
+* Structure: gemv is dotRow per row; gemm with batch 1 is gemv; gemm with batch > 1 is the
+  dequantise-then-dotF32F32 definition (math.zig:780-806).
+Unpinned at the last bit: @reduce(.Add)'s lane order.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from ziglm_amd import synth
+
+QTYPES = [O.Q4_0, O.Q8_0, O.BF16, O.F16, O.F32]
+
+
+@pytest.fixture(scope="module")
+def o():
+    return O.get()
+
+
+def f16_bytes(v):
+    """Little-endian bytes of the f16 value v."""
+    return np.array([v], np.float16).view(np.uint8)
+
+
+def int_matrix(qtype, rows, cols, seed, scale_pow=0):
+    """Integer-valued weights in `qtype` layout, their exact float64 values, and scale 2^p."""
+    rng = np.random.default_rng(seed)
+    d = np.float64(2.0 ** scale_pow)
+    if qtype == O.Q8_0:
+        q = rng.integers(-127, 128, (rows, cols))
+        raw = np.zeros((rows, cols // 32, 34), np.uint8)
+        raw[:, :, 0:2] = f16_bytes(d)
+        raw[:, :, 2:] = q.reshape(rows, cols // 32, 32).astype(np.int8).view(np.uint8)
+        return raw.reshape(rows, -1), q * d
+    if qtype == O.Q4_0:
+        q = rng.integers(0, 16, (rows, cols))
+        qb = q.reshape(rows, cols // 32, 32)
+        raw = np.zeros((rows, cols // 32, 18), np.uint8)
+        raw[:, :, 0:2] = f16_bytes(d)
+        raw[:, :, 2:] = (qb[:, :, :16] | (qb[:, :, 16:] << 4)).astype(np.uint8)
+        return raw.reshape(rows, -1), (q - 8) * d
+    w = rng.integers(-100, 101, (rows, cols)).astype(np.float64) * d
+    if qtype == O.F32:
+        return w.astype(np.float32).view(np.uint8).reshape(rows, -1), w
+    if qtype == O.F16:
+        return w.astype(np.float16).view(np.uint8).reshape(rows, -1), w
+    bits = (w.astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)  # exact: small ints
+    return bits.view(np.uint8).reshape(rows, -1), w
+
+
+def random_matrix(qtype, rows, cols, seed):
+    """Synthetic weights in `qtype` layout and their dequantised float64 values."""
+    if qtype == O.Q8_0:
+        raw = synth.q8_0_table(seed, rows, cols)
+    elif qtype == O.Q4_0:
+        raw = synth.q4_0_table(seed, rows, cols)
+    elif qtype == O.BF16:
+        raw = synth.bf16_table(seed, rows, cols)
+    elif qtype == O.F16:
+        raw = synth.f16_bits(synth.normal_f32(seed, "w16", (rows, cols), 0, 0.05)).view(np.uint8).reshape(rows, -1)
+    else:
+        raw = synth.normal_f32(seed, "w32", (rows, cols), 0, 0.05).view(np.uint8).reshape(rows, -1)
+    o = O.get()
+    deq = np.empty((rows, cols), np.float32)
+    for r in range(rows):
+        deq[r] = o.embed_gather(raw, qtype, np.array([r], np.int32), cols, np.float32(1.0))[0]
+    return raw, deq.astype(np.float64)
+
+
+def bound(wd, x):
+    """2^-20 * sum |w_i x_i| per output (rows of wd against each x)."""
+    return np.abs(x).astype(np.float64) @ np.abs(wd).T * 2.0 ** -20
+
+
+@pytest.mark.parametrize("qtype", QTYPES)
+@pytest.mark.parametrize("cols", [32, 64, 96, 2560, 264])
+def test_dot_integer_closed_form(o, qtype, cols):
+    if qtype in (O.Q4_0, O.Q8_0) and cols % 32:
+        pytest.skip("block types need cols % 32 == 0")
+    for p in (0, -1, 3):
+        raw, wd = int_matrix(qtype, 5, cols, seed=cols + p + 100 * qtype, scale_pow=p)
+        x = np.random.default_rng(cols).integers(-3, 4, cols).astype(np.float32)
+        exact = wd @ x.astype(np.float64)
+        assert np.all(np.abs(exact) < 2 ** 24)
+        y = o.gemv(qtype, raw, x)
+        np.testing.assert_array_equal(y, exact.astype(np.float32), err_msg=f"qtype={qtype} cols={cols} 2^{p}")
+
+
+def test_dot_f32_tails(o):
+    """dotF32F32's 32-, 8- and scalar-tail loops (n = 37 = 32 + 0*8 + 5, 45 = 32 + 8 + 5)."""
+    for n in (5, 8, 37, 45, 77):
+        a = np.arange(1, n + 1, dtype=np.float32)
+        b = (np.arange(n, dtype=np.float32) % 7) - 3
+        got = o.lib.zo_dot_f32(o.fp(a), o.fp(b), n)
+        assert got == float(np.dot(a.astype(np.float64), b.astype(np.float64))), n
+
+
+def test_q4_0_nibble_order_single_element(o):
+    """One nonzero weight at a time: element e of block 1 is the low nibble of byte e
+    (e < 16) or the high nibble of byte e - 16, offset by -8."""
+    cols = 64
+    x = np.arange(1, cols + 1, dtype=np.float32)
+    for e in (0, 5, 15, 16, 21, 31):
+        blk = np.zeros((2, 18), np.uint8)
+        blk[:, 0:2] = f16_bytes(1.0)
+        blk[:, 2:] = 0x88  # every nibble 8 -> weight 0
+        byte = e % 16
+        blk[1, 2 + byte] = 0xC8 if e >= 16 else 0x8C  # that nibble 12 -> weight 4
+        y = o.dot_row(O.Q4_0, blk.reshape(-1), x)
+        assert y == 4.0 * x[32 + e], (e, y)
+
+
+def test_q8_0_sign_and_scale(o):
+    cols = 64
+    blk = np.zeros((2, 34), np.uint8)
+    blk[0, 0:2] = f16_bytes(0.25)
+    blk[1, 0:2] = f16_bytes(-2.0)
+    blk[0, 2 + 3] = np.uint8(np.int8(-5).view(np.uint8))
+    blk[1, 2 + 30] = 7
+    x = np.arange(cols, dtype=np.float32) + 1
+    assert o.dot_row(O.Q8_0, blk.reshape(-1), x) == np.float32(-5 * 0.25 * 4 + 7 * -2.0 * 63)
+
+
+@pytest.mark.parametrize("qtype", QTYPES)
+def test_gemv_vs_f64(o, qtype):
+    rows, cols = 48, 2560
+    raw, wd = random_matrix(qtype, rows, cols, seed=11)
+    x = synth.normal_f32(11, "x", (cols,))
+    y = o.gemv(qtype, raw, x).astype(np.float64)
+    exact = wd @ x.astype(np.float64)
+    assert np.all(np.abs(y - exact) <= bound(wd, x)), np.max(np.abs(y - exact) / bound(wd, x))
+    for r in (0, 17, rows - 1):
+        assert o.dot_row(qtype, raw[r], x) == y[r]
+
+
+@pytest.mark.parametrize("qtype", QTYPES)
+def test_gemm_definition(o, qtype):
+    rows, cols, batch = 24, 512, 3
+    raw, wd = random_matrix(qtype, rows, cols, seed=12)
+    X = synth.normal_f32(12, "X", (batch, cols))
+    Y = o.gemm(qtype, raw, X)
+    np.testing.assert_array_equal(o.gemm(qtype, raw, X[:1])[0], o.gemv(qtype, raw, X[0]))
+    exact = X.astype(np.float64) @ wd.T
+    assert np.all(np.abs(Y - exact) <= bound(wd, X)), "gemm vs f64"
+    # batch > 1 uses dequantise + dotF32F32 (math.zig:780-806)
+    wf = wd.astype(np.float32)
+    for b in range(batch):
+        for r in (0, rows - 1):
+            ref = o.lib.zo_dot_f32(o.fp(np.ascontiguousarray(wf[r])), o.fp(np.ascontiguousarray(X[b])), cols)
+            assert Y[b, r] == np.float32(ref)

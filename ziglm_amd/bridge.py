@@ -84,6 +84,19 @@ SIGNATURES = {
     "hip_add": (None, [_v, _v, _i, _v]),
     "hip_scale": (None, [_v, _f, _i, _v]),
     "hip_tanh_softcap": (None, [_v, _f, _i, _v]),
+    # GEMV / GEMM (cuda_bridge.h:36-50)
+    "hip_gemv_q4_0": (None, [_v, _v, _v, _i, _i, _v]),
+    "hip_gemv_q8_0": (None, [_v, _v, _v, _i, _i, _v]),
+    "hip_gemv_f16": (None, [_v, _v, _v, _i, _i, _v]),
+    "hip_gemv_bf16": (None, [_v, _v, _v, _i, _i, _v]),
+    "hip_gemv_f32": (None, [_v, _v, _v, _i, _i, _v]),
+    "hip_gemv": (None, [_i, _v, _v, _v, _i, _i, _v]),
+    "hip_gemv_geglu_q4_0": (None, [_v, _v, _v, _v, _i, _i, _v]),
+    "hip_gemv_qkv_q4_0": (None, [_v, _v, _v, _v, _v, _v, _v, _i, _i, _i, _i, _v]),
+    "hip_gemm_q4_0": (None, [_v, _v, _v, _i, _i, _i, _v]),
+    "hip_gemm_q8_0": (None, [_v, _v, _v, _i, _i, _i, _v]),
+    "hip_gemm_f16": (None, [_v, _v, _v, _i, _i, _i, _v]),
+    "hip_gemm": (None, [_i, _v, _v, _v, _i, _i, _i, _v]),
     "hip_geglu_ex": (None, [_i, _v, _v, _v, _i64, _v]),
     "hip_tanh_softcap_ex": (None, [_i, _v, _f, _i64, _v]),
 }

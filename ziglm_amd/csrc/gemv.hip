@@ -1,0 +1,475 @@
+// Quantised / float matrix-vector and small-batch matrix-matrix products for decode
+// (replaces cuda_bridge.cu:255-605 and 1021-1445: cuda_gemv_*, cuda_gemv_geglu_q4_0,
+// cuda_gemv_qkv_q4_0, cuda_gemm_*).
+//
+// Numerics follow ziglm's CPU path (math.zig:25-330, 652-846), not the CUDA kernels: the
+// activations stay f32 (the CUDA kernels quantise them to Q8_1 first), every weight is
+// dequantised exactly ((q - 8) * d, q * d, f16/bf16 -> f32) and the products are summed in
+// f32. The summation order differs from the CPU's (lanes, then waves), so results agree
+// with the CPU within the f32 rounding of a dot product, not bit for bit.
+//
+// Layout. y[b][r] = sum_c W[r][c] * x[b][c], W rows of row_bytes(qtype, cols) bytes. One
+// 256-thread workgroup owns RPW consecutive rows and a tile of NB tokens; its 256 threads
+// split the row into 8-column groups (thread i takes groups i, i + 256, ...), so each
+// element of x is read once per workgroup and applied to all RPW rows from registers: f32 x
+// is ~7x the bytes of a Q4_0 row, and this reuse keeps its L1/L2 traffic below the weight
+// stream. Per group a lane loads, for Q8_0 / Q4_0, the block's f16 scale and 8 / 4 bytes of
+// quants with 16-bit loads (blocks are 34 / 18 B, 2-byte aligned; the lanes of a wave read
+// one contiguous span of the row), for BF16 / F16 one 16-byte chunk, for F32 two. Partial
+// sums are reduced within the wave (DPP / permlane) and across the 4 waves through LDS.
+// Fused forms: GeGLU pairs each gate row with its up row and writes gelu(g) * u (the
+// elementwise kernels' gelu_fast); QKV treats the three matrices as one row space.
+#include "zl_common.h"
+#include "zl_host.h"
+
+namespace zl {
+
+constexpr int kGemvThreads = 256;
+constexpr int kGemvWaves = kGemvThreads / kWave;
+
+enum GemvMode { GV_PLAIN = 0, GV_GEGLU = 1 };
+
+struct GemvSeg {
+    const unsigned char* w;
+    float* y;
+    int rows;
+};
+
+struct GemvArgs {
+    GemvSeg seg[3];             // one matrix, or Q/K/V sharing cols
+    int nseg;
+    int total_rows;
+    const unsigned char* w_up;  // GeGLU: up rows, paired with seg[0]'s gate rows
+    const float* x;             // [batch][cols]
+    int cols;
+    int64_t row_bytes;
+    int batch;
+};
+
+__device__ __forceinline__ uint32_t ldw16(const unsigned char* p) {
+    return *reinterpret_cast<const uint16_t*>(p);
+}
+__device__ __forceinline__ float h2f(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+// Raw weight bytes behind one 8-column group of one row.
+template <int QT>
+struct WGroup {
+    uint32_t v[QT == HIP_BRIDGE_F32 ? 8 : 4];
+    __device__ __forceinline__ void load(const unsigned char* row, int g) {
+        if constexpr (QT == HIP_BRIDGE_Q4_0) {
+            const unsigned char* blk = row + (g >> 2) * 18;
+            v[0] = ldw16(blk);                       // d
+            const unsigned char* qs = blk + 2 + (g & 3) * 4;
+            v[1] = ldw16(qs) | (ldw16(qs + 2) << 16);  // 4 bytes: 4 low + 4 high nibbles
+        } else if constexpr (QT == HIP_BRIDGE_Q8_0) {
+            const unsigned char* blk = row + (g >> 2) * 34;
+            v[0] = ldw16(blk);
+            const unsigned char* qs = blk + 2 + (g & 3) * 8;
+            v[1] = ldw16(qs) | (ldw16(qs + 2) << 16);
+            v[2] = ldw16(qs + 4) | (ldw16(qs + 6) << 16);
+        } else if constexpr (QT == HIP_BRIDGE_F32) {
+            const u32x4 a = ld16(row + 32 * (size_t)g), b = ld16(row + 32 * (size_t)g + 16);
+            v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+            v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+        } else {  // F16, BF16
+            const u32x4 a = ld16(row + 16 * (size_t)g);
+            v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        }
+    }
+    // sum_j w_j * x_j over the group's 8 columns; xa / xb are the x values of columns
+    // [8g, 8g+4) and [8g+4, 8g+8), or for Q4_0 of [32b+o, +4) and [32b+16+o, +4).
+    __device__ __forceinline__ float dot(const f32x4& xa, const f32x4& xb) const {
+        const float a[4] = {xa.x, xa.y, xa.z, xa.w};
+        const float b[4] = {xb.x, xb.y, xb.z, xb.w};
+        float s = 0.0f;
+        if constexpr (QT == HIP_BRIDGE_Q4_0) {
+            float t = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t byte = (v[1] >> (8 * k)) & 0xff;
+                t = fmaf((float)((int)(byte & 0xf) - 8), a[k], t);
+                t = fmaf((float)((int)(byte >> 4) - 8), b[k], t);
+            }
+            s = t * h2f(v[0]);
+        } else if constexpr (QT == HIP_BRIDGE_Q8_0) {
+            float t = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                t = fmaf((float)(int8_t)((v[1] >> (8 * k)) & 0xff), a[k], t);
+                t = fmaf((float)(int8_t)((v[2] >> (8 * k)) & 0xff), b[k], t);
+            }
+            s = t * h2f(v[0]);
+        } else if constexpr (QT == HIP_BRIDGE_F32) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                s = fmaf(__uint_as_float(v[k]), a[k], s);
+                s = fmaf(__uint_as_float(v[4 + k]), b[k], s);
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                float w0, w1, w2, w3;
+                if constexpr (QT == HIP_BRIDGE_BF16) {
+                    w0 = bf16_lo(v[k]); w1 = bf16_hi(v[k]);
+                    w2 = bf16_lo(v[2 + k]); w3 = bf16_hi(v[2 + k]);
+                } else {
+                    w0 = h2f(v[k] & 0xffff); w1 = h2f(v[k] >> 16);
+                    w2 = h2f(v[2 + k] & 0xffff); w3 = h2f(v[2 + k] >> 16);
+                }
+                s = fmaf(w0, a[2 * k], s);
+                s = fmaf(w1, a[2 * k + 1], s);
+                s = fmaf(w2, b[2 * k], s);
+                s = fmaf(w3, b[2 * k + 1], s);
+            }
+        }
+        return s;
+    }
+};
+
+// Column offsets of the two 4-float x vectors a group multiplies.
+template <int QT>
+__device__ __forceinline__ void group_cols(int g, int& ca, int& cb) {
+    if constexpr (QT == HIP_BRIDGE_Q4_0) {
+        ca = (g >> 2) * 32 + (g & 3) * 4;  // low nibbles: elements o..o+3 of the block
+        cb = ca + 16;                      // high nibbles: elements 16+o..16+o+3
+    } else {
+        ca = 8 * g;
+        cb = ca + 4;
+    }
+}
+
+template <int QT, int RPW, int NB, int MODE>
+__global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvArgs a) {
+    constexpr int NM = MODE == GV_GEGLU ? 2 : 1;  // matrices per row (gate, up)
+    constexpr int NACC = RPW * NB * NM;
+    __shared__ float s_part[kGemvWaves][NACC];
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    const int row0 = blockIdx.x * RPW;
+    const int G = a.cols / 8;
+
+    // Row pointers. Rows past the end read the workgroup's first row (always in range:
+    // the grid has cdiv(total_rows, RPW) workgroups) and are never written.
+    const unsigned char* wrow[RPW][NM];
+    float* yrow[RPW];
+    int ystride[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        const bool ok = row0 + r < a.total_rows;
+        int R = ok ? row0 + r : row0;
+        int s = 0;
+        if (a.nseg > 1 && R >= a.seg[0].rows) {
+            R -= a.seg[0].rows;
+            s = 1;
+            if (a.nseg > 2 && R >= a.seg[1].rows) {
+                R -= a.seg[1].rows;
+                s = 2;
+            }
+        }
+        wrow[r][0] = a.seg[s].w + (int64_t)R * a.row_bytes;
+        if constexpr (NM == 2) wrow[r][1] = a.w_up + (int64_t)R * a.row_bytes;
+        yrow[r] = ok ? a.seg[s].y + R : nullptr;
+        ystride[r] = a.seg[s].rows;
+    }
+
+    for (int b0 = 0; b0 < a.batch; b0 += NB) {
+        float acc[RPW][NM][NB];
+#pragma unroll
+        for (int r = 0; r < RPW; ++r)
+#pragma unroll
+            for (int m = 0; m < NM; ++m)
+#pragma unroll
+                for (int b = 0; b < NB; ++b) acc[r][m][b] = 0.0f;
+
+#pragma unroll 2
+        for (int g = tid; g < G; g += kGemvThreads) {
+            WGroup<QT> wg[RPW][NM];
+#pragma unroll
+            for (int r = 0; r < RPW; ++r)
+#pragma unroll
+                for (int m = 0; m < NM; ++m) wg[r][m].load(wrow[r][m], g);
+            int ca, cb;
+            group_cols<QT>(g, ca, cb);
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                const int bt = b0 + b < a.batch ? b0 + b : a.batch - 1;
+                const float* xr = a.x + (int64_t)bt * a.cols;
+                const f32x4 xa = ldf4(xr + ca), xb = ldf4(xr + cb);
+#pragma unroll
+                for (int r = 0; r < RPW; ++r)
+#pragma unroll
+                    for (int m = 0; m < NM; ++m) acc[r][m][b] += wg[r][m].dot(xa, xb);
+            }
+        }
+
+        // wave sums, then the 4 wave partials in order through LDS
+#pragma unroll
+        for (int r = 0; r < RPW; ++r)
+#pragma unroll
+            for (int m = 0; m < NM; ++m)
+#pragma unroll
+                for (int b = 0; b < NB; ++b) {
+                    const float v = group_sum<kWave>(acc[r][m][b]);
+                    if (lane == 0) s_part[wave][(r * NM + m) * NB + b] = v;
+                }
+        __syncthreads();
+        if (tid < RPW * NB) {
+            const int r = tid / NB, b = tid % NB;
+            float tot[NM];
+#pragma unroll
+            for (int m = 0; m < NM; ++m) {
+                const int i = (r * NM + m) * NB + b;
+                tot[m] = (s_part[0][i] + s_part[1][i]) + (s_part[2][i] + s_part[3][i]);
+            }
+            float* yr = nullptr;
+            int ys = 0;
+#pragma unroll
+            for (int rr = 0; rr < RPW; ++rr)
+                if (rr == r) {  // select without indexing the register arrays at run time
+                    yr = yrow[rr];
+                    ys = ystride[rr];
+                }
+            if (yr && b0 + b < a.batch) {
+                float out = tot[0];
+                if constexpr (MODE == GV_GEGLU) out = gelu_fast(tot[0]) * tot[1];
+                yr[(int64_t)(b0 + b) * ys] = out;
+            }
+        }
+        __syncthreads();  // s_part is rewritten by the next token tile
+    }
+}
+
+// Any alignment / column count: one workgroup per row, scalar dequantisation per element.
+template <int QT>
+__device__ __forceinline__ float w_elem(const unsigned char* row, int c) {
+    if constexpr (QT == HIP_BRIDGE_Q4_0) {
+        const unsigned char* blk = row + (c >> 5) * 18;
+        const int o = c & 31;
+        const int byte = blk[2 + (o & 15)];
+        const int q = (o < 16 ? (byte & 0xf) : (byte >> 4)) - 8;
+        return (float)q * h2f((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+    } else if constexpr (QT == HIP_BRIDGE_Q8_0) {
+        const unsigned char* blk = row + (c >> 5) * 34;
+        return (float)(int8_t)blk[2 + (c & 31)] * h2f((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+    } else if constexpr (QT == HIP_BRIDGE_F32) {
+        const unsigned char* p = row + 4 * (size_t)c;
+        return __uint_as_float((uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) |
+                               ((uint32_t)p[3] << 24));
+    } else {
+        const unsigned char* p = row + 2 * (size_t)c;
+        const uint32_t h = (uint32_t)p[0] | ((uint32_t)p[1] << 8);
+        return QT == HIP_BRIDGE_BF16 ? bf16_lo(h) : h2f(h);
+    }
+}
+
+template <int QT, int MODE>
+__global__ __launch_bounds__(kGemvThreads) void k_gemv_scalar(GemvArgs a) {
+    __shared__ float s_red[2][kGemvWaves];
+    int R = blockIdx.x;
+    int s = 0;
+    if (a.nseg > 1 && R >= a.seg[0].rows) {
+        R -= a.seg[0].rows;
+        s = 1;
+        if (a.nseg > 2 && R >= a.seg[1].rows) {
+            R -= a.seg[1].rows;
+            s = 2;
+        }
+    }
+    const unsigned char* wr = a.seg[s].w + (int64_t)R * a.row_bytes;
+    const unsigned char* ur = MODE == GV_GEGLU ? a.w_up + (int64_t)R * a.row_bytes : nullptr;
+    for (int b = 0; b < a.batch; ++b) {
+        const float* xr = a.x + (int64_t)b * a.cols;
+        float sg = 0.0f, su = 0.0f;
+        for (int c = threadIdx.x; c < a.cols; c += kGemvThreads) {
+            sg = fmaf(w_elem<QT>(wr, c), xr[c], sg);
+            if constexpr (MODE == GV_GEGLU) su = fmaf(w_elem<QT>(ur, c), xr[c], su);
+        }
+        sg = group_sum<kWave>(sg);
+        su = group_sum<kWave>(su);
+        const int wave = threadIdx.x >> 6;
+        if ((threadIdx.x & 63) == 0) {
+            s_red[0][wave] = sg;
+            s_red[1][wave] = su;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            const float g = (s_red[0][0] + s_red[0][1]) + (s_red[0][2] + s_red[0][3]);
+            float out = g;
+            if constexpr (MODE == GV_GEGLU) {
+                const float u = (s_red[1][0] + s_red[1][1]) + (s_red[1][2] + s_red[1][3]);
+                out = gelu_fast(g) * u;
+            }
+            a.seg[s].y[(int64_t)b * a.seg[s].rows + R] = out;
+        }
+        __syncthreads();
+    }
+}
+
+static int64_t gemv_row_bytes(int qtype, int cols) {
+    switch (qtype) {
+        case HIP_BRIDGE_F32: return (int64_t)cols * 4;
+        case HIP_BRIDGE_F16:
+        case HIP_BRIDGE_BF16: return (int64_t)cols * 2;
+        case HIP_BRIDGE_Q8_0: return cols % 32 ? -1 : (int64_t)(cols / 32) * 34;
+        case HIP_BRIDGE_Q4_0: return cols % 32 ? -1 : (int64_t)(cols / 32) * 18;
+        default: return -1;
+    }
+}
+
+template <int QT, int MODE>
+static void launch_vec(const GemvArgs& a, hipStream_t s) {
+    // Rows per workgroup: x is reused across them from registers (8 for one token); a
+    // token tile of NB shares each weight load across NB tokens.
+    if (a.batch == 1) {
+        constexpr int RPW = MODE == GV_GEGLU ? 4 : 8;
+        k_gemv<QT, RPW, 1, MODE><<<(unsigned)cdiv(a.total_rows, RPW), kGemvThreads, 0, s>>>(a);
+    } else if (a.batch == 2) {
+        constexpr int RPW = MODE == GV_GEGLU ? 2 : 4;
+        k_gemv<QT, RPW, 2, MODE><<<(unsigned)cdiv(a.total_rows, RPW), kGemvThreads, 0, s>>>(a);
+    } else {
+        constexpr int RPW = MODE == GV_GEGLU ? 1 : 2;
+        k_gemv<QT, RPW, 4, MODE><<<(unsigned)cdiv(a.total_rows, RPW), kGemvThreads, 0, s>>>(a);
+    }
+}
+
+template <int MODE>
+static void launch_gemv(int qtype, GemvArgs& a, hipStream_t s) {
+    if (a.total_rows <= 0 || a.cols <= 0 || a.batch <= 0) return;
+    a.row_bytes = gemv_row_bytes(qtype, a.cols);
+    if (a.row_bytes < 0) {
+        set_error(HIP_BRIDGE_EUNSUPPORTED);
+        return;
+    }
+    if (!a.x || (MODE == GV_GEGLU && !a.w_up)) {
+        set_error(HIP_BRIDGE_EINVAL);
+        return;
+    }
+    // Vector path: x 16-byte aligned, cols % 8 == 0; Q4_0 / Q8_0 rows 2-byte aligned (16-bit
+    // loads), dense rows 16-byte aligned (cols % 8 == 0 makes every row so).
+    const bool blocks = qtype == HIP_BRIDGE_Q4_0 || qtype == HIP_BRIDGE_Q8_0;
+    auto w_ok = [&](const void* w) {
+        const uintptr_t p = reinterpret_cast<uintptr_t>(w);
+        return blocks ? (p & 1u) == 0 : (p & 15u) == 0;
+    };
+    bool ok = a.cols % 8 == 0 && aligned16(a.x);
+    for (int i = 0; i < a.nseg; ++i) {
+        if (a.seg[i].rows <= 0) continue;
+        if (!a.seg[i].w || !a.seg[i].y) {
+            set_error(HIP_BRIDGE_EINVAL);
+            return;
+        }
+        ok = ok && w_ok(a.seg[i].w);
+    }
+    if (MODE == GV_GEGLU) ok = ok && w_ok(a.w_up);
+    if (ok) {
+        switch (qtype) {
+            case HIP_BRIDGE_Q4_0: launch_vec<HIP_BRIDGE_Q4_0, MODE>(a, s); break;
+            case HIP_BRIDGE_Q8_0: launch_vec<HIP_BRIDGE_Q8_0, MODE>(a, s); break;
+            case HIP_BRIDGE_F16: launch_vec<HIP_BRIDGE_F16, MODE>(a, s); break;
+            case HIP_BRIDGE_BF16: launch_vec<HIP_BRIDGE_BF16, MODE>(a, s); break;
+            default: launch_vec<HIP_BRIDGE_F32, MODE>(a, s); break;
+        }
+    } else {
+        const unsigned grid = (unsigned)a.total_rows;
+        switch (qtype) {
+            case HIP_BRIDGE_Q4_0: k_gemv_scalar<HIP_BRIDGE_Q4_0, MODE><<<grid, kGemvThreads, 0, s>>>(a); break;
+            case HIP_BRIDGE_Q8_0: k_gemv_scalar<HIP_BRIDGE_Q8_0, MODE><<<grid, kGemvThreads, 0, s>>>(a); break;
+            case HIP_BRIDGE_F16: k_gemv_scalar<HIP_BRIDGE_F16, MODE><<<grid, kGemvThreads, 0, s>>>(a); break;
+            case HIP_BRIDGE_BF16: k_gemv_scalar<HIP_BRIDGE_BF16, MODE><<<grid, kGemvThreads, 0, s>>>(a); break;
+            default: k_gemv_scalar<HIP_BRIDGE_F32, MODE><<<grid, kGemvThreads, 0, s>>>(a); break;
+        }
+    }
+    check_launch();
+}
+
+static GemvArgs one_matrix(const void* w, const float* x, float* y, int rows, int cols, int batch) {
+    GemvArgs a{};
+    a.seg[0] = GemvSeg{(const unsigned char*)w, y, rows};
+    a.nseg = 1;
+    a.total_rows = rows;
+    a.x = x;
+    a.cols = cols;
+    a.batch = batch;
+    return a;
+}
+
+}  // namespace zl
+
+using namespace zl;
+
+extern "C" {
+
+void hip_gemm(int qtype, const void* weights, const float* x, float* y, int batch_size, int rows,
+              int cols, HipStream_t stream) {
+    if (batch_size <= 0 || rows <= 0 || cols <= 0) return;
+    GemvArgs a = one_matrix(weights, x, y, rows, cols, batch_size);
+    launch_gemv<GV_PLAIN>(qtype, a, stream_of(stream));
+}
+
+void hip_gemv(int qtype, const void* weights, const float* x, float* y, int rows, int cols,
+              HipStream_t stream) {
+    hip_gemm(qtype, weights, x, y, 1, rows, cols, stream);
+}
+
+void hip_gemv_q4_0(const void* weights, const float* x, float* y, int rows, int cols, HipStream_t stream) {
+    hip_gemm(HIP_BRIDGE_Q4_0, weights, x, y, 1, rows, cols, stream);
+}
+void hip_gemv_q8_0(const void* weights, const float* x, float* y, int rows, int cols, HipStream_t stream) {
+    hip_gemm(HIP_BRIDGE_Q8_0, weights, x, y, 1, rows, cols, stream);
+}
+void hip_gemv_f16(const void* weights, const float* x, float* y, int rows, int cols, HipStream_t stream) {
+    hip_gemm(HIP_BRIDGE_F16, weights, x, y, 1, rows, cols, stream);
+}
+void hip_gemv_bf16(const void* weights, const float* x, float* y, int rows, int cols, HipStream_t stream) {
+    hip_gemm(HIP_BRIDGE_BF16, weights, x, y, 1, rows, cols, stream);
+}
+void hip_gemv_f32(const float* weights, const float* x, float* y, int rows, int cols, HipStream_t stream) {
+    hip_gemm(HIP_BRIDGE_F32, weights, x, y, 1, rows, cols, stream);
+}
+
+void hip_gemm_q4_0(const void* weights, const float* x, float* y, int batch_size, int rows, int cols,
+                   HipStream_t stream) {
+    hip_gemm(HIP_BRIDGE_Q4_0, weights, x, y, batch_size, rows, cols, stream);
+}
+void hip_gemm_q8_0(const void* weights, const float* x, float* y, int batch_size, int rows, int cols,
+                   HipStream_t stream) {
+    hip_gemm(HIP_BRIDGE_Q8_0, weights, x, y, batch_size, rows, cols, stream);
+}
+void hip_gemm_f16(const void* weights, const float* x, float* y, int batch_size, int rows, int cols,
+                  HipStream_t stream) {
+    hip_gemm(HIP_BRIDGE_F16, weights, x, y, batch_size, rows, cols, stream);
+}
+
+void hip_gemv_geglu_q4_0(const void* gate_w, const void* up_w, const float* x, float* act_out, int rows,
+                         int cols, HipStream_t stream) {
+    if (rows <= 0 || cols <= 0) return;
+    GemvArgs a = one_matrix(gate_w, x, act_out, rows, cols, 1);
+    a.w_up = (const unsigned char*)up_w;
+    launch_gemv<GV_GEGLU>(HIP_BRIDGE_Q4_0, a, stream_of(stream));
+}
+
+void hip_gemv_qkv_q4_0(const void* q_w, const void* k_w, const void* v_w, const float* x, float* q_out,
+                       float* k_out, float* v_out, int q_rows, int k_rows, int v_rows, int cols,
+                       HipStream_t stream) {
+    if (q_rows < 0 || k_rows < 0 || v_rows < 0) {
+        set_error(HIP_BRIDGE_EINVAL);
+        return;
+    }
+    const int total = q_rows + k_rows + v_rows;
+    if (total <= 0 || cols <= 0) return;
+    GemvArgs a{};
+    a.seg[0] = GemvSeg{(const unsigned char*)q_w, q_out, q_rows};
+    a.seg[1] = GemvSeg{(const unsigned char*)k_w, k_out, k_rows};
+    a.seg[2] = GemvSeg{(const unsigned char*)v_w, v_out, v_rows};
+    a.nseg = 3;
+    a.total_rows = total;
+    a.x = x;
+    a.cols = cols;
+    a.batch = 1;
+    launch_gemv<GV_PLAIN>(HIP_BRIDGE_Q4_0, a, stream_of(stream));
+}
+
+}  // extern "C"

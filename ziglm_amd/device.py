@@ -234,6 +234,29 @@ class HipDevice:
         self.b.hip_geglu(_ptr(d_gate), _ptr(d_up), _ptr(d_out), n, self.stream)
         self._done("geglu")
 
+    # -- GEMV / GEMM (cuda.zig:281-356) ----------------------------------------------------
+    def gemv(self, qtype, d_weights, d_x, d_y, rows, cols):
+        self.b.hip_gemv(int(qtype), _ptr(d_weights), _ptr(d_x), _ptr(d_y), rows, cols, self.stream)
+        self._done("gemv")
+
+    def gemvGegluQ4_0(self, d_gate_w, d_up_w, d_x, d_act_out, rows, cols):
+        self.b.hip_gemv_geglu_q4_0(_ptr(d_gate_w), _ptr(d_up_w), _ptr(d_x), _ptr(d_act_out), rows, cols,
+                                   self.stream)
+        self._done("gemvGegluQ4_0")
+
+    def gemvQkvQ4_0(self, d_q_w, d_k_w, d_v_w, d_x, d_q_out, d_k_out, d_v_out, q_rows, k_rows, v_rows, cols):
+        self.b.hip_gemv_qkv_q4_0(_ptr(d_q_w), _ptr(d_k_w), _ptr(d_v_w), _ptr(d_x), _ptr(d_q_out),
+                                 _ptr(d_k_out), _ptr(d_v_out), q_rows, k_rows, v_rows, cols, self.stream)
+        self._done("gemvQkvQ4_0")
+
+    def gemmQ4_0(self, d_weights, d_x, d_y, batch_size, rows, cols):
+        self.b.hip_gemm_q4_0(_ptr(d_weights), _ptr(d_x), _ptr(d_y), batch_size, rows, cols, self.stream)
+        self._done("gemmQ4_0")
+
+    def gemm(self, qtype, d_weights, d_x, d_y, batch_size, rows, cols):
+        self.b.hip_gemm(int(qtype), _ptr(d_weights), _ptr(d_x), _ptr(d_y), batch_size, rows, cols, self.stream)
+        self._done("gemm")
+
     def gegluEx(self, dtype, d_gate, d_up, d_out, n):
         self.b.hip_geglu_ex(dtype, _ptr(d_gate), _ptr(d_up), _ptr(d_out), n, self.stream)
         self._done("gegluEx")
