@@ -326,6 +326,79 @@ def bench_gather(dev):
 
 
 # ---------------------------------------------------------------------------------------
+# GEMV (decode projections, Gemma-4B shapes, f32 activations)
+# ---------------------------------------------------------------------------------------
+
+def weight_rows(qtype, rows, cols, seed=5):
+    """Synthetic weight bytes [rows x row_bytes]: 64 seeded rows tiled (finite scales)."""
+    if qtype == B.Q4_0:
+        base = synth.q4_0_table(seed, 64, cols)
+    elif qtype == B.Q8_0:
+        base = synth.q8_0_table(seed, 64, cols)
+    else:
+        base = synth.bf16_table(seed, 64, cols)
+    return base
+
+
+def gemv_case(dev, name, qtype, shapes, fn, batch=1):
+    """shapes: list of (rows, cols) matrices the launch reads; fn(dev, mats, x, ys) launches.
+    Weight copies rotate so the working set exceeds the Infinity Cache several times."""
+    rb = [row_bytes(qtype, c) * r for r, c in shapes]
+    per = sum(rb)
+    ncopy = max(2, min(64, math.ceil(3 * MALL_BYTES / per)))
+    sets = []
+    for i in range(ncopy):
+        mats = []
+        for (r, c), nb in zip(shapes, rb):
+            m = dev.alloc(nb)
+            fill_tiled(m, weight_rows(qtype, r, c).reshape(-1))
+            mats.append(m)
+        sets.append(mats)
+    cols = shapes[0][1]
+    x = dev.from_numpy(synth.normal_f32(5, "x", (batch, cols)))
+    ys = [dev.alloc(batch * r * 4) for r, _ in shapes]
+    us = time_launches_us(dev, lambda d, mats: fn(d, mats, x, ys), sets, max(32, 2 * ncopy))
+    nbytes = per + batch * 4 * (cols + sum(r for r, _ in shapes))
+    for mats in sets:
+        for m in mats:
+            m.deinit()
+    for b_ in ys + [x]:
+        b_.deinit()
+    return {"us": round(us, 2), "bytes": nbytes, "GBps": round(nbytes / us / 1e3, 1),
+            "frac_peak": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4)}
+
+
+def row_bytes(qtype, cols):
+    return {B.Q4_0: cols // 32 * 18, B.Q8_0: cols // 32 * 34, B.BF16: cols * 2, B.F16: cols * 2,
+            B.F32: cols * 4}[qtype]
+
+
+def bench_gemv(dev):
+    s = LY.GEMMA_4B
+    H, I, q_rows, kv_rows, V = s.H, s.I, s.nh * s.D, s.nkv * s.D, 262144
+    out = {}
+
+    def plain(qt, rows, cols, batch=1):
+        return lambda d, m, x, ys: d.gemm(qt, m[0], x, ys[0], batch, rows, cols)
+    cases = [
+        ("qkv_q4_0", B.Q4_0, [(q_rows, H), (kv_rows, H), (kv_rows, H)],
+         lambda d, m, x, ys: d.gemvQkvQ4_0(m[0], m[1], m[2], x, ys[0], ys[1], ys[2], q_rows, kv_rows, kv_rows, H), 1),
+        ("o_proj_q4_0", B.Q4_0, [(H, q_rows)], plain(B.Q4_0, H, q_rows), 1),
+        ("gate_up_geglu_q4_0", B.Q4_0, [(I, H), (I, H)],
+         lambda d, m, x, ys: d.gemvGegluQ4_0(m[0], m[1], x, ys[0], I, H), 1),
+        ("down_q4_0", B.Q4_0, [(H, I)], plain(B.Q4_0, H, I), 1),
+        ("lm_head_q4_0", B.Q4_0, [(V, H)], plain(B.Q4_0, V, H), 1),
+        ("lm_head_q8_0", B.Q8_0, [(V, H)], plain(B.Q8_0, V, H), 1),
+        ("lm_head_bf16", B.BF16, [(V, H)], plain(B.BF16, V, H), 1),
+        ("gate_q4_0_b8", B.Q4_0, [(I, H)], plain(B.Q4_0, I, H, 8), 8),
+    ]
+    for name, qt, shapes, fn, batch in cases:
+        out[name] = gemv_case(dev, name, qt, shapes, fn, batch)
+        log(f"  gemv {name:22s} {out[name]['us']:8.2f} us {out[name]['GBps']:8.1f} GB/s")
+    return out
+
+
+# ---------------------------------------------------------------------------------------
 # CPU baseline (oracle, -O3 -march=x86-64-v3, one thread)
 # ---------------------------------------------------------------------------------------
 
@@ -445,6 +518,10 @@ def main():
     if a.only:
         if a.only.startswith("gather_"):
             fn, sets, traffic, _ = gather_case(dev, a.only[len("gather_"):])
+        elif a.only == "gemv":
+            log("gemv (decode projections)")
+            print(json.dumps(bench_gemv(dev)))
+            return
         elif a.only == "copy":
             sets, _ = make_sets(dev, shape, T, B.BF16)
             nb = sets[0].act.size_bytes
@@ -521,6 +598,8 @@ def main():
         cfgs["c4_prefill"] = {k: c4[k] for k in ("us_per_layer", "us_per_layer_isolated_sum",
                                                  "us_per_layer_fused_4op", "chain_GBps", "ops")}
         cfgs["c4_prefill"]["chain_GBps"] = round(cfgs["c4_prefill"]["chain_GBps"], 1)
+        log("gemv (decode projections)")
+        cfgs["gemv_decode"] = bench_gemv(dev)
         log("c1/c5 decode")
         cfgs["c5_decode"] = {}
         for b_ in (1, 8, 64, 256):

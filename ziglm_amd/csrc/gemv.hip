@@ -46,6 +46,15 @@ struct GemvArgs {
     int batch;
 };
 
+// v & m, opaque to the optimiser: it would otherwise split the byte-wise mask into one
+// shift-and-mask per element, where the byte conversions below take v_cvt_f32_ubyte0..3
+// straight from the masked word (1 instead of 2 instructions per element).
+__device__ __forceinline__ uint32_t mask_bytes(uint32_t v, uint32_t m) {
+    uint32_t r;
+    asm("v_and_b32 %0, %1, %2" : "=v"(r) : "s"(m), "v"(v));
+    return r;
+}
+
 __device__ __forceinline__ uint32_t ldw16(const unsigned char* p) {
     return *reinterpret_cast<const uint16_t*>(p);
 }
@@ -57,74 +66,85 @@ __device__ __forceinline__ float h2f(uint32_t h) {
 template <int QT>
 struct WGroup {
     uint32_t v[QT == HIP_BRIDGE_F32 ? 8 : 4];
-    __device__ __forceinline__ void load(const unsigned char* row, int g) {
+    // row: the row's base (uniform across the workgroup); g: the lane's group. Offsets are
+    // unsigned 32-bit so each load is a scalar base plus a 32-bit vector offset, shared by
+    // all rows (no per-row 64-bit address arithmetic).
+    __device__ __forceinline__ void load(const unsigned char* row, uint32_t g) {
         if constexpr (QT == HIP_BRIDGE_Q4_0) {
-            const unsigned char* blk = row + (g >> 2) * 18;
-            v[0] = ldw16(blk);                       // d
-            const unsigned char* qs = blk + 2 + (g & 3) * 4;
-            v[1] = ldw16(qs) | (ldw16(qs + 2) << 16);  // 4 bytes: 4 low + 4 high nibbles
+            const uint32_t blk = (g >> 2) * 18u;
+            v[0] = ldw16(row + blk);                       // d
+            const uint32_t qs = blk + 2u + (g & 3u) * 4u;
+            v[1] = ldw16(row + qs) | (ldw16(row + (qs + 2u)) << 16);  // 4 low + 4 high nibbles
         } else if constexpr (QT == HIP_BRIDGE_Q8_0) {
-            const unsigned char* blk = row + (g >> 2) * 34;
-            v[0] = ldw16(blk);
-            const unsigned char* qs = blk + 2 + (g & 3) * 8;
-            v[1] = ldw16(qs) | (ldw16(qs + 2) << 16);
-            v[2] = ldw16(qs + 4) | (ldw16(qs + 6) << 16);
+            const uint32_t blk = (g >> 2) * 34u;
+            v[0] = ldw16(row + blk);
+            const uint32_t qs = blk + 2u + (g & 3u) * 8u;
+            v[1] = ldw16(row + qs) | (ldw16(row + (qs + 2u)) << 16);
+            v[2] = ldw16(row + (qs + 4u)) | (ldw16(row + (qs + 6u)) << 16);
         } else if constexpr (QT == HIP_BRIDGE_F32) {
-            const u32x4 a = ld16(row + 32 * (size_t)g), b = ld16(row + 32 * (size_t)g + 16);
+            const u32x4 a = ld16(row + 32u * g), b = ld16(row + (32u * g + 16u));
             v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
             v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
         } else {  // F16, BF16
-            const u32x4 a = ld16(row + 16 * (size_t)g);
+            const u32x4 a = ld16(row + 16u * g);
             v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
         }
     }
     // sum_j w_j * x_j over the group's 8 columns; xa / xb are the x values of columns
-    // [8g, 8g+4) and [8g+4, 8g+8), or for Q4_0 of [32b+o, +4) and [32b+16+o, +4).
-    __device__ __forceinline__ float dot(const f32x4& xa, const f32x4& xb) const {
+    // [8g, 8g+4) and [8g+4, 8g+8), or for Q4_0 of [32b+o, +4) and [32b+16+o, +4); sx is
+    // their sum. Block types take the CPU's form (math.zig:304-305): with u_j the stored
+    // unsigned byte / nibble, q_j = u_j - k (k = 8 for Q4_0 nibbles; Q8_0 bytes are read
+    // as u = q ^ 0x80, k = 128), d * (sum u_j x_j - k * sum x_j) -- each u_j converted by
+    // one v_cvt_f32_ubyteN, sum x_j shared by every row of the workgroup.
+    __device__ __forceinline__ float dot(const f32x4& xa, const f32x4& xb, float sx) const {
         const float a[4] = {xa.x, xa.y, xa.z, xa.w};
         const float b[4] = {xb.x, xb.y, xb.z, xb.w};
-        float s = 0.0f;
-        if constexpr (QT == HIP_BRIDGE_Q4_0) {
+        if constexpr (QT == HIP_BRIDGE_Q4_0 || QT == HIP_BRIDGE_Q8_0) {
+            uint32_t ua, ub;
+            float k;
+            if constexpr (QT == HIP_BRIDGE_Q4_0) {
+                ua = mask_bytes(v[1], 0x0f0f0f0fu);       // low nibbles: columns [32b+o, +4)
+                ub = mask_bytes(v[1] >> 4, 0x0f0f0f0fu);  // high nibbles: [32b+16+o, +4)
+                k = 8.0f;
+            } else {
+                ua = v[1] ^ 0x80808080u;
+                ub = v[2] ^ 0x80808080u;
+                k = 128.0f;
+            }
             float t = 0.0f;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const uint32_t byte = (v[1] >> (8 * k)) & 0xff;
-                t = fmaf((float)((int)(byte & 0xf) - 8), a[k], t);
-                t = fmaf((float)((int)(byte >> 4) - 8), b[k], t);
+            for (int j = 0; j < 4; ++j) {
+                t = fmaf((float)((ua >> (8 * j)) & 0xff), a[j], t);
+                t = fmaf((float)((ub >> (8 * j)) & 0xff), b[j], t);
             }
-            s = t * h2f(v[0]);
-        } else if constexpr (QT == HIP_BRIDGE_Q8_0) {
-            float t = 0.0f;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                t = fmaf((float)(int8_t)((v[1] >> (8 * k)) & 0xff), a[k], t);
-                t = fmaf((float)(int8_t)((v[2] >> (8 * k)) & 0xff), b[k], t);
-            }
-            s = t * h2f(v[0]);
+            return h2f(v[0]) * fmaf(-k, sx, t);
         } else if constexpr (QT == HIP_BRIDGE_F32) {
+            float s = 0.0f;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                s = fmaf(__uint_as_float(v[k]), a[k], s);
-                s = fmaf(__uint_as_float(v[4 + k]), b[k], s);
+            for (int j = 0; j < 4; ++j) {
+                s = fmaf(__uint_as_float(v[j]), a[j], s);
+                s = fmaf(__uint_as_float(v[4 + j]), b[j], s);
             }
+            return s;
         } else {
+            float s = 0.0f;
 #pragma unroll
-            for (int k = 0; k < 2; ++k) {
+            for (int j = 0; j < 2; ++j) {
                 float w0, w1, w2, w3;
                 if constexpr (QT == HIP_BRIDGE_BF16) {
-                    w0 = bf16_lo(v[k]); w1 = bf16_hi(v[k]);
-                    w2 = bf16_lo(v[2 + k]); w3 = bf16_hi(v[2 + k]);
+                    w0 = bf16_lo(v[j]); w1 = bf16_hi(v[j]);
+                    w2 = bf16_lo(v[2 + j]); w3 = bf16_hi(v[2 + j]);
                 } else {
-                    w0 = h2f(v[k] & 0xffff); w1 = h2f(v[k] >> 16);
-                    w2 = h2f(v[2 + k] & 0xffff); w3 = h2f(v[2 + k] >> 16);
+                    w0 = h2f(v[j] & 0xffff); w1 = h2f(v[j] >> 16);
+                    w2 = h2f(v[2 + j] & 0xffff); w3 = h2f(v[2 + j] >> 16);
                 }
-                s = fmaf(w0, a[2 * k], s);
-                s = fmaf(w1, a[2 * k + 1], s);
-                s = fmaf(w2, b[2 * k], s);
-                s = fmaf(w3, b[2 * k + 1], s);
+                s = fmaf(w0, a[2 * j], s);
+                s = fmaf(w1, a[2 * j + 1], s);
+                s = fmaf(w2, b[2 * j], s);
+                s = fmaf(w3, b[2 * j + 1], s);
             }
+            return s;
         }
-        return s;
     }
 };
 
@@ -184,13 +204,62 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvArgs a) {
 #pragma unroll
                 for (int b = 0; b < NB; ++b) acc[r][m][b] = 0.0f;
 
+        // Q8_0 / dense: double-buffered, the next group's weights and x are in flight while
+        // the current group is multiplied. Q4_0 (4.5 bytes per group and row) measured faster
+        // single-buffered with more rows per workgroup (LM head 262144 x 2560: 141 against
+        // 180 us; Q8_0: 187 against 209 us double- against single-buffered).
+        if constexpr (QT != HIP_BRIDGE_Q4_0) {
+        const float* xt[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) xt[b] = a.x + (int64_t)(b0 + b < a.batch ? b0 + b : a.batch - 1) * a.cols;
+        WGroup<QT> cur[RPW][NM], nxt[RPW][NM];
+        f32x4 cxa[NB], cxb[NB], nxa[NB], nxb[NB];
+        auto fetch = [&](int g, WGroup<QT> (&w)[RPW][NM], f32x4 (&xa)[NB], f32x4 (&xb)[NB]) {
+#pragma unroll
+            for (int r = 0; r < RPW; ++r)
+#pragma unroll
+                for (int m = 0; m < NM; ++m) w[r][m].load(wrow[r][m], (uint32_t)g);
+            int ca, cb;
+            group_cols<QT>(g, ca, cb);
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                xa[b] = ldf4(xt[b] + ca);
+                xb[b] = ldf4(xt[b] + cb);
+            }
+        };
+        int g = tid;
+        if (g < G) fetch(g, cur, cxa, cxb);
+        for (; g < G; g += kGemvThreads) {
+            const int gn = g + kGemvThreads;
+            if (gn < G) fetch(gn, nxt, nxa, nxb);
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                const f32x4 xa = cxa[b], xb = cxb[b];
+                const float sx = ((xa.x + xa.y) + (xa.z + xa.w)) + ((xb.x + xb.y) + (xb.z + xb.w));
+#pragma unroll
+                for (int r = 0; r < RPW; ++r)
+#pragma unroll
+                    for (int m = 0; m < NM; ++m) acc[r][m][b] += cur[r][m].dot(xa, xb, sx);
+            }
+#pragma unroll
+            for (int r = 0; r < RPW; ++r)
+#pragma unroll
+                for (int m = 0; m < NM; ++m) cur[r][m] = nxt[r][m];
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                cxa[b] = nxa[b];
+                cxb[b] = nxb[b];
+            }
+        }
+
+        } else {
 #pragma unroll 2
         for (int g = tid; g < G; g += kGemvThreads) {
             WGroup<QT> wg[RPW][NM];
 #pragma unroll
             for (int r = 0; r < RPW; ++r)
 #pragma unroll
-                for (int m = 0; m < NM; ++m) wg[r][m].load(wrow[r][m], g);
+                for (int m = 0; m < NM; ++m) wg[r][m].load(wrow[r][m], (uint32_t)g);
             int ca, cb;
             group_cols<QT>(g, ca, cb);
 #pragma unroll
@@ -198,11 +267,13 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvArgs a) {
                 const int bt = b0 + b < a.batch ? b0 + b : a.batch - 1;
                 const float* xr = a.x + (int64_t)bt * a.cols;
                 const f32x4 xa = ldf4(xr + ca), xb = ldf4(xr + cb);
+                const float sx = ((xa.x + xa.y) + (xa.z + xa.w)) + ((xb.x + xb.y) + (xb.z + xb.w));
 #pragma unroll
                 for (int r = 0; r < RPW; ++r)
 #pragma unroll
-                    for (int m = 0; m < NM; ++m) acc[r][m][b] += wg[r][m].dot(xa, xb);
+                    for (int m = 0; m < NM; ++m) acc[r][m][b] += wg[r][m].dot(xa, xb, sx);
             }
+        }
         }
 
         // wave sums, then the 4 wave partials in order through LDS
@@ -319,19 +390,26 @@ static int64_t gemv_row_bytes(int qtype, int cols) {
     }
 }
 
+// Rows per workgroup (x is reused across them from registers) against workgroup count:
+// measured on Gemma-4B decode shapes, small matrices (1024-4096 rows) want 2 rows and more
+// workgroups, large ones 4, Q4_0 (the most x per weight byte) 8 from 16384 rows. GeGLU
+// reads two matrices per row and takes half as many rows.
 template <int QT, int MODE>
 static void launch_vec(const GemvArgs& a, hipStream_t s) {
-    // Rows per workgroup: x is reused across them from registers (8 for one token); a
-    // token tile of NB shares each weight load across NB tokens.
+    constexpr int H = MODE == GV_GEGLU ? 2 : 1;
+    const unsigned g8 = (unsigned)cdiv(a.total_rows, 8 / H), g4 = (unsigned)cdiv(a.total_rows, 4 / H),
+                   g2 = (unsigned)cdiv(a.total_rows, 2 / H);
     if (a.batch == 1) {
-        constexpr int RPW = MODE == GV_GEGLU ? 4 : 8;
-        k_gemv<QT, RPW, 1, MODE><<<(unsigned)cdiv(a.total_rows, RPW), kGemvThreads, 0, s>>>(a);
+        if (QT == HIP_BRIDGE_Q4_0 && a.total_rows >= 16384)
+            k_gemv<QT, 8 / H, 1, MODE><<<g8, kGemvThreads, 0, s>>>(a);
+        else if (a.total_rows >= 8192)
+            k_gemv<QT, 4 / H, 1, MODE><<<g4, kGemvThreads, 0, s>>>(a);
+        else
+            k_gemv<QT, 2 / H, 1, MODE><<<g2, kGemvThreads, 0, s>>>(a);
     } else if (a.batch == 2) {
-        constexpr int RPW = MODE == GV_GEGLU ? 2 : 4;
-        k_gemv<QT, RPW, 2, MODE><<<(unsigned)cdiv(a.total_rows, RPW), kGemvThreads, 0, s>>>(a);
+        k_gemv<QT, 4 / H, 2, MODE><<<g4, kGemvThreads, 0, s>>>(a);
     } else {
-        constexpr int RPW = MODE == GV_GEGLU ? 1 : 2;
-        k_gemv<QT, RPW, 4, MODE><<<(unsigned)cdiv(a.total_rows, RPW), kGemvThreads, 0, s>>>(a);
+        k_gemv<QT, 2 / H, 4, MODE><<<g2, kGemvThreads, 0, s>>>(a);
     }
 }
 
