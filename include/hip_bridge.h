@@ -237,6 +237,43 @@ void hip_gemm(int qtype, const void* weights, const float* x, float* y, int batc
               int rows, int cols, HipStream_t stream);                      /* cuda_bridge.h:50 */
 
 /* ---------------------------------------------------------------------------------- */
+/* Decode attention, f32 q/out (replaces cuda_bridge.h:115-168)                         */
+/* Query token b at position p attends to positions [max(0, p+1-window), p] (window 0: */
+/* all): score = (q_h . k_t) * attn_scale, softcap * tanh(score / softcap) when         */
+/* softcap > 0, softmax, out_h = sum_t w_t v_t; kv head of query head h is              */
+/* h / (n_heads / n_kv_heads) (1, 2 or 4 query heads per kv head; head_dim 64/128/256). */
+/* Key of (position t, kv head j) at k_cache[(row0 + t) * row_stride + j * head_dim].   */
+/* ---------------------------------------------------------------------------------- */
+/* reference layout, f32 cache: row0 = donor_layer * max_seq, row_stride = max_kv_dim */
+void hip_attention_forward(const float* q, const float* k_cache, const float* v_cache, float* out,
+                           int donor_layer, int pos, int max_seq, int n_heads, int n_kv_heads,
+                           int head_dim, int max_kv_dim, float attn_scale, float softcap,
+                           int sliding_window, HipStream_t stream);        /* cuda_bridge.h:115-131 */
+void hip_attention_forward_ind(const float* q, const float* k_cache, const float* v_cache,
+                               float* out, int donor_layer, const int* d_pos, int max_seq,
+                               int n_heads, int n_kv_heads, int head_dim, int max_kv_dim,
+                               float attn_scale, float softcap, int sliding_window,
+                               HipStream_t stream);                        /* cuda_bridge.h:133-149 */
+/* token b of batch_size at position pos + b (causal chunk of one sequence) */
+void hip_attention_batched(const float* q, const float* k_cache, const float* v_cache, float* out,
+                           int donor_layer, int pos, int batch_size, int max_seq, int n_heads,
+                           int n_kv_heads, int head_dim, int max_kv_dim, float attn_scale,
+                           float softcap, int sliding_window, HipStream_t stream); /* cuda_bridge.h:151-168 */
+/* new: batched decode with per-token positions (d_pos ? d_pos[b] : pos_base + b) and cache
+ * row bases (d_row_base ? d_row_base[b] : row_base), f32 or bf16 caches (kv_dtype), cache
+ * bounds (cache_rows > 0; positions must also be < max_len; tokens outside give zeros) and
+ * a split over the sequence when the caller passes a workspace of at least
+ * hip_attention_workspace_bytes(...) bytes (16-byte aligned); with none it runs unsplit. */
+size_t hip_attention_workspace_bytes(int batch, int n_heads, int n_kv_heads, int head_dim,
+                                     int max_len, int sliding_window);
+void hip_attention_decode(int kv_dtype, const float* q, const void* k_cache, const void* v_cache,
+                          float* out, int64_t cache_rows, int64_t row_stride,
+                          const int64_t* d_row_base, int64_t row_base, const int32_t* d_pos,
+                          int pos_base, int max_len, int batch, int n_heads, int n_kv_heads,
+                          int head_dim, float attn_scale, float softcap, int sliding_window,
+                          void* workspace, size_t workspace_bytes, HipStream_t stream);
+
+/* ---------------------------------------------------------------------------------- */
 /* Activations & elementwise (replaces cuda_bridge.h:64, 66-68)                         */
 /* ---------------------------------------------------------------------------------- */
 /* out = gelu_tanh(gate) * up; out may alias gate or up. */

@@ -172,6 +172,32 @@ public:
                                  (int)max_seq, (int)n_kv_heads, (int)head_dim, (int)max_kv_dim, stream);
     }
 
+    // cuda.zig:576-684
+    void attentionForward(const float* d_q, const float* d_k_cache, const float* d_v_cache, float* d_out,
+                          size_t donor_layer, size_t pos, size_t max_seq, size_t n_heads, size_t n_kv_heads,
+                          size_t head_dim, size_t max_kv_dim, float attn_scale, float softcap,
+                          size_t sliding_window) const {
+        hip_attention_forward(d_q, d_k_cache, d_v_cache, d_out, (int)donor_layer, (int)pos, (int)max_seq,
+                              (int)n_heads, (int)n_kv_heads, (int)head_dim, (int)max_kv_dim, attn_scale, softcap,
+                              (int)sliding_window, stream);
+    }
+    void attentionForwardInd(const float* d_q, const float* d_k_cache, const float* d_v_cache, float* d_out,
+                             size_t donor_layer, const int* d_pos, size_t max_seq, size_t n_heads,
+                             size_t n_kv_heads, size_t head_dim, size_t max_kv_dim, float attn_scale,
+                             float softcap, size_t sliding_window) const {
+        hip_attention_forward_ind(d_q, d_k_cache, d_v_cache, d_out, (int)donor_layer, d_pos, (int)max_seq,
+                                  (int)n_heads, (int)n_kv_heads, (int)head_dim, (int)max_kv_dim, attn_scale,
+                                  softcap, (int)sliding_window, stream);
+    }
+    void attentionBatched(const float* d_q, const float* d_k_cache, const float* d_v_cache, float* d_out,
+                          size_t donor_layer, size_t pos, size_t batch_size, size_t max_seq, size_t n_heads,
+                          size_t n_kv_heads, size_t head_dim, size_t max_kv_dim, float attn_scale, float softcap,
+                          size_t sliding_window) const {
+        hip_attention_batched(d_q, d_k_cache, d_v_cache, d_out, (int)donor_layer, (int)pos, (int)batch_size,
+                              (int)max_seq, (int)n_heads, (int)n_kv_heads, (int)head_dim, (int)max_kv_dim,
+                              attn_scale, softcap, (int)sliding_window, stream);
+    }
+
     // cuda.zig:686-750
     void geglu(const float* d_gate, const float* d_up, float* d_out, size_t n) const {
         hip_geglu(d_gate, d_up, d_out, (int)n, stream);

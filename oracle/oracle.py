@@ -60,6 +60,7 @@ _SIGS = {
     "zo_dot_row": (ctypes.c_float, [_i, _u8p, _fp, _sz]),
     "zo_gemv": (_i, [_i, _u8p, _fp, _fp, _sz, _sz]),
     "zo_gemm": (_i, [_i, _u8p, _fp, _fp, _sz, _sz, _sz]),
+    "zo_attention_token": (_i, [_fp, _vp, _vp, _i, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _f, _f, _fp]),
     "zo_qk_norm_rope_kv": (
         None,
         [_i, _vp, _vp, _vp, _fp, _fp, _i, _vp, _vp, _sz, _sz, _sz, _i32p, ctypes.c_int64, _i64p,
@@ -159,6 +160,22 @@ class Oracle:
         if rc != 0:
             raise ValueError(f"unsupported qtype {qtype}")
         return y
+
+    def attention(self, q, kc, vc, row0, pos, n_heads, n_kv_heads, head_dim, scale, softcap=0.0,
+                  window=0):
+        """One query token (q f32[n_heads*head_dim]) over cache rows row0+start .. row0+pos
+        of kc / vc ([rows, row_stride] f32 or bf16 uint16)."""
+        q = np.ascontiguousarray(q, dtype=np.float32).reshape(-1)
+        kc = np.ascontiguousarray(kc)
+        vc = np.ascontiguousarray(vc)
+        kvd = 1 if kc.dtype == np.uint16 else 0
+        out = np.empty(n_heads * head_dim, np.float32)
+        rc = self.lib.zo_attention_token(self.fp(q), kc.ctypes.data, vc.ctypes.data, kvd, row0, kc.shape[-1],
+                                         pos, window, n_heads, n_kv_heads, head_dim, scale, softcap,
+                                         self.fp(out))
+        if rc != 0:
+            raise MemoryError("oracle attention")
+        return out
 
     def rms_norm(self, x, w, eps, unit_offset=True):
         """Row-wise math.rmsNorm over the last axis (w=None -> rmsNormNoScale)."""

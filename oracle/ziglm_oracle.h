@@ -110,6 +110,11 @@ int zo_gemv(int qtype, const uint8_t* w, const float* x, float* y, size_t rows, 
 int zo_gemm(int qtype, const uint8_t* w, const float* x, float* y, size_t batch, size_t rows,
             size_t cols);
 
+/* ---- decode attention, one query token (model.zig:658-700; ziglm_oracle_gemv.c) ---- */
+int zo_attention_token(const float* q, const void* k_cache, const void* v_cache, int kv_dtype,
+                       size_t row0, size_t row_stride, size_t pos, size_t window, size_t n_heads,
+                       size_t n_kv_heads, size_t head_dim, float scale, float softcap, float* out);
+
 #ifdef __cplusplus
 }
 #endif

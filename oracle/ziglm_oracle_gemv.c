@@ -1,6 +1,6 @@
 /*
- * ziglm CPU oracle, part 2: dot products, GEMV and GEMM (reference: simonproyt/ziglm,
- * src/math.zig:25-330, 652-846). TEST INFRASTRUCTURE ONLY (see ziglm_oracle.h): the
+ * ziglm CPU oracle, part 2: dot products, GEMV, GEMM and decode attention (reference:
+ * simonproyt/ziglm, src/math.zig:25-330, 652-846, 1088-1106; src/model.zig:658-700). TEST INFRASTRUCTURE ONLY (see ziglm_oracle.h): the
  * checker for the HIP GEMV kernels; nothing in the product library uses it.
  *
  * Zig's @Vector(8|16, f32) arithmetic is restated with GCC vector extensions, built with
@@ -18,6 +18,7 @@
  */
 #include "ziglm_oracle.h"
 
+#include <math.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -207,4 +208,72 @@ int zo_gemm(int qtype, const uint8_t* w, const float* x, float* y, size_t batch,
     }
     free(tmp);
     return rc;
+}
+
+/* ------------------------------------------------------------------------------------ */
+/* Decode attention (model.zig:658-700, math.zig:1088-1106)                                */
+/* ------------------------------------------------------------------------------------ */
+
+/* math.zig:1088-1106 softmax: max, exp(v - max) (Zig @exp f32; restated with expf),
+ * sequential sum, inv = 1/sum, v *= inv. Parity unpinned at the bit level for exp. */
+static void softmax_f32(float* x, size_t n) {
+    if (n == 0) return;
+    float m = x[0];
+    for (size_t i = 1; i < n; ++i)
+        if (x[i] > m) m = x[i];
+    float sum = 0.0f;
+    for (size_t i = 0; i < n; ++i) {
+        const float e = expf(x[i] - m);
+        x[i] = e;
+        sum += e;
+    }
+    const float inv = 1.0f / sum;
+    for (size_t i = 0; i < n; ++i) x[i] *= inv;
+}
+
+/* One query token, all heads (model.zig:658-700): for head h with kv head h / (nh/nkv),
+ * score_t = dotF32F32(q_h, k_t) * scale, soft-capped cap*tanh(s/cap) when cap > 0, over
+ * t in [start, pos] (start = pos+1-window when window > 0 and pos+1 > window); softmax;
+ * out_h = sum_t w_t v_t accumulated in t order (8-wide vectors, no contraction).
+ * K/V rows: key of position t, kv head j at kc[(row0 + t) * row_stride + j*d] (the logical
+ * cache layout); kv_dtype 0 f32, 1 bf16 (upconverted exactly). */
+int zo_attention_token(const float* q, const void* kc, const void* vc, int kv_dtype, size_t row0,
+                       size_t row_stride, size_t pos, size_t window, size_t n_heads,
+                       size_t n_kv_heads, size_t d, float scale, float softcap, float* out) {
+    const size_t seq = pos + 1;
+    const size_t start = (window > 0 && seq > window) ? seq - window : 0;
+    const size_t n = seq - start;
+    const size_t group = n_kv_heads ? n_heads / n_kv_heads : 1;
+    float* scores = (float*)malloc(n * sizeof(float));
+    float* kv = (float*)malloc(d * sizeof(float));
+    if (!scores || !kv) {
+        free(scores);
+        free(kv);
+        return -1;
+    }
+    for (size_t h = 0; h < n_heads; ++h) {
+        const size_t kh = h / group;
+        const float* qh = q + h * d;
+        for (size_t t = start; t < seq; ++t) {
+            const size_t off = (row0 + t) * row_stride + kh * d;
+            if (kv_dtype == 0) memcpy(kv, (const float*)kc + off, d * sizeof(float));
+            else for (size_t i = 0; i < d; ++i) kv[i] = bf16f(((const uint16_t*)kc)[off + i]);
+            float s = zo_dot_f32(qh, kv, d) * scale;
+            if (softcap > 0.0f) s = softcap * zo_tanhf(s / softcap);
+            scores[t - start] = s;
+        }
+        softmax_f32(scores, n);
+        float* oh = out + h * d;
+        memset(oh, 0, d * sizeof(float));
+        for (size_t t = start; t < seq; ++t) {
+            const size_t off = (row0 + t) * row_stride + kh * d;
+            if (kv_dtype == 0) memcpy(kv, (const float*)vc + off, d * sizeof(float));
+            else for (size_t i = 0; i < d; ++i) kv[i] = bf16f(((const uint16_t*)vc)[off + i]);
+            const float w = scores[t - start];
+            for (size_t i = 0; i < d; ++i) oh[i] = oh[i] + w * kv[i];
+        }
+    }
+    free(scores);
+    free(kv);
+    return 0;
 }

@@ -1,0 +1,137 @@
+"""Decode attention on the GPU (model.zig:658-700) against float64 with the f32 bound of
+attn_ref.py, and against the oracle's CPU restatement with twice that bound.
+
+Covers: head sizes 64/128/256, 1/2/4 query heads per kv head, soft-cap, sliding window,
+f32 and bf16 caches, per-token positions and per-sequence cache rows (positions up to 32767),
+the split-over-positions path (workspace) and the unsplit one, the reference-ABI mirrors
+(single token, device position, causal chunk), and tokens whose cache rows are out of range
+(zero output)."""
+import numpy as np
+import pytest
+
+from attn_ref import attention_f64
+from oracle import oracle as O
+from ziglm_amd import bridge as B
+from ziglm_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def check(got, q, kc_f32, vc_f32, row0, pos, nh, nkv, d, scale, softcap, window, what, oracle=None, kc=None, vc=None):
+    ref, tol = attention_f64(q, kc_f32, vc_f32, row0, pos, nh, nkv, d, scale, softcap, window)
+    err = np.abs(np.asarray(got, np.float64) - ref)
+    assert np.all(err <= tol), f"{what}: max err/tol {float(np.max(err / tol)):.3g}"
+    if oracle is not None:
+        o = oracle.attention(q, kc if kc is not None else kc_f32, vc if vc is not None else vc_f32, row0, pos,
+                             nh, nkv, d, scale, softcap, window).astype(np.float64)
+        assert np.all(np.abs(o - ref) <= tol), f"{what}: oracle outside the bound"
+
+
+@pytest.mark.parametrize("kv_dtype", [B.F32, B.BF16])
+@pytest.mark.parametrize("nh,nkv,d", [(8, 4, 256), (4, 4, 128), (8, 2, 64), (16, 4, 128)])
+@pytest.mark.parametrize("softcap,window", [(0.0, 0), (50.0, 0), (0.0, 300)])
+@pytest.mark.parametrize("split", [False, True])
+def test_attention_decode_per_sequence(dev, oracle, kv_dtype, nh, nkv, d, softcap, window, split):
+    B_, cap = 3, 2048                     # 3 sequences, 2048 cache rows each
+    positions = np.array([0, 1234, 2047], np.int32)
+    rows = B_ * cap
+    kc = synth.normal_f32(11, "kc", (rows, nkv * d))
+    vc = synth.normal_f32(11, "vc", (rows, nkv * d))
+    if kv_dtype == B.BF16:
+        kc_dev, vc_dev = oracle.f32_to_bf16(kc), oracle.f32_to_bf16(vc)
+        kc, vc = oracle.bf16_to_f32(kc_dev), oracle.bf16_to_f32(vc_dev)
+    else:
+        kc_dev, vc_dev = kc, vc
+    q = synth.normal_f32(11, "q", (B_, nh * d), 0, 0.3)
+    scale = float(np.float32(1.0 / np.sqrt(d)))
+    row_base = np.arange(B_, dtype=np.int64) * cap
+    d_out = dev.alloc(B_ * nh * d * 4)
+    ws_bytes = dev.attentionWorkspaceBytes(B_, nh, nkv, d, cap, window) if split else 0
+    d_ws = dev.alloc(ws_bytes) if ws_bytes else None
+    if split:
+        assert ws_bytes > 0
+    dev.attentionDecode(kv_dtype, dev.from_numpy(q), dev.from_numpy(kc_dev), dev.from_numpy(vc_dev), d_out, rows,
+                        nkv * d, dev.from_numpy(row_base), 0, dev.from_numpy(positions), 0, cap, B_, nh, nkv, d,
+                        scale, softcap, window, d_ws, ws_bytes)
+    got = d_out.to_numpy((B_, nh * d), np.float32)
+    for b in range(B_):
+        check(got[b], q[b], kc, vc, int(row_base[b]), int(positions[b]), nh, nkv, d, scale, softcap, window,
+              f"seq {b} pos {positions[b]}", oracle if b == 1 else None, kc_dev, vc_dev)
+
+
+def test_attention_decode_long_context(dev, oracle):
+    """Positions up to 32767 in per-sequence caches (the c5 layout), bf16, split."""
+    nh, nkv, d, cap = 8, 4, 256, 32768
+    positions = np.array([32767, 5], np.int32)
+    rows = 2 * cap
+    kc16 = oracle.f32_to_bf16(synth.normal_f32(12, "kc", (rows, nkv * d)))
+    vc16 = oracle.f32_to_bf16(synth.normal_f32(12, "vc", (rows, nkv * d)))
+    q = synth.normal_f32(12, "q", (2, nh * d), 0, 0.3)
+    ws = dev.attentionWorkspaceBytes(2, nh, nkv, d, cap)
+    d_out = dev.alloc(2 * nh * d * 4)
+    dev.attentionDecode(B.BF16, dev.from_numpy(q), dev.from_numpy(kc16), dev.from_numpy(vc16), d_out, rows, nkv * d,
+                        dev.from_numpy(np.array([0, cap], np.int64)), 0, dev.from_numpy(positions), 0, cap, 2, nh, nkv,
+                        d, 1.0 / 16, 0.0, 0, dev.alloc(ws), ws)
+    got = d_out.to_numpy((2, nh * d), np.float32)
+    kc, vc = oracle.bf16_to_f32(kc16), oracle.bf16_to_f32(vc16)
+    check(got[0], q[0], kc, vc, 0, 32767, nh, nkv, d, 1.0 / 16, 0.0, 0, "pos 32767")
+    check(got[1], q[1], kc, vc, cap, 5, nh, nkv, d, 1.0 / 16, 0.0, 0, "pos 5")
+
+
+def test_attention_reference_mirrors(dev, oracle):
+    nh, nkv, d, max_seq, layer = 8, 4, 256, 512, 1
+    max_kv_dim = nkv * d + 64                      # padded rows
+    kc = synth.normal_f32(13, "kc", (2 * max_seq, max_kv_dim))
+    vc = synth.normal_f32(13, "vc", (2 * max_seq, max_kv_dim))
+    d_kc, d_vc = dev.from_numpy(kc), dev.from_numpy(vc)
+    scale = 1.0 / 16
+    # single token by value and through a device position
+    q = synth.normal_f32(13, "q", (nh * d,), 0, 0.3)
+    d_q, d_out = dev.from_numpy(q), dev.alloc(nh * d * 4)
+    for pos in (0, 300, 511):
+        dev.attentionForward(d_q, d_kc, d_vc, d_out, layer, pos, max_seq, nh, nkv, d, max_kv_dim, scale, 30.0, 0)
+        check(d_out.to_numpy((nh * d,), np.float32), q, kc, vc, layer * max_seq, pos, nh, nkv, d, scale, 30.0, 0,
+              f"forward pos {pos}", oracle)
+        dev.attentionForwardInd(d_q, d_kc, d_vc, d_out, layer, dev.from_numpy(np.array([pos], np.int32)), max_seq,
+                                nh, nkv, d, max_kv_dim, scale, 0.0, 128)
+        check(d_out.to_numpy((nh * d,), np.float32), q, kc, vc, layer * max_seq, pos, nh, nkv, d, scale, 0.0, 128,
+              f"forward_ind pos {pos}")
+    # causal chunk: token b at position pos + b
+    T, pos = 5, 100
+    qb = synth.normal_f32(14, "q", (T, nh * d), 0, 0.3)
+    d_outb = dev.alloc(T * nh * d * 4)
+    dev.attentionBatched(dev.from_numpy(qb), d_kc, d_vc, d_outb, layer, pos, T, max_seq, nh, nkv, d, max_kv_dim,
+                         scale, 0.0, 0)
+    got = d_outb.to_numpy((T, nh * d), np.float32)
+    for b in range(T):
+        check(got[b], qb[b], kc, vc, layer * max_seq, pos + b, nh, nkv, d, scale, 0.0, 0, f"batched token {b}")
+
+
+def test_attention_out_of_range_rows_give_zeros(dev):
+    nh, nkv, d, cap = 4, 2, 128, 64
+    kc = synth.normal_f32(15, "kc", (2 * cap, nkv * d))
+    q = synth.normal_f32(15, "q", (3, nh * d))
+    d_out = dev.alloc(3 * nh * d * 4)
+    d_out.fill(0x7f)
+    # token 0: position beyond max_len; token 1: row past the cache; token 2: valid
+    pos = np.array([cap, cap - 1, 3], np.int32)
+    base = np.array([0, cap + 8, 0], np.int64)
+    dev.attentionDecode(B.F32, dev.from_numpy(q), dev.from_numpy(kc), dev.from_numpy(kc), d_out, 2 * cap, nkv * d,
+                        dev.from_numpy(base), 0, dev.from_numpy(pos), 0, cap, 3, nh, nkv, d, 0.1, 0.0, 0)
+    got = d_out.to_numpy((3, nh * d), np.float32)
+    assert np.all(got[0] == 0) and np.all(got[1] == 0)
+    ref, tol = attention_f64(q[2], kc, kc, 0, 3, nh, nkv, d, 0.1)
+    assert np.all(np.abs(got[2] - ref) <= tol)
+
+
+def test_attention_unsupported_group_is_noop(dev):
+    d_buf = dev.alloc(1 << 16)
+    d_out = dev.alloc(16 * 64 * 4)
+    d_out.fill(0x11)
+    dev.strict = False
+    try:
+        dev.attentionForward(d_buf, d_buf, d_buf, d_out, 0, 3, 16, 16, 2, 64, 128, 1.0, 0.0, 0)  # 8 q per kv head
+        assert dev.b.last_error() == B.EUNSUPPORTED
+    finally:
+        dev.strict = True
+    assert np.all(d_out.to_numpy((16 * 64 * 4,), np.uint8) == 0x11)

@@ -157,3 +157,45 @@ def test_gemm_definition(o, qtype):
         for r in (0, rows - 1):
             ref = o.lib.zo_dot_f32(o.fp(np.ascontiguousarray(wf[r])), o.fp(np.ascontiguousarray(X[b])), cols)
             assert Y[b, r] == np.float32(ref)
+
+
+# ---------------------------------------------------------------------------------------
+# Decode attention (model.zig:658-700, math.softmax math.zig:1088-1106)
+# ---------------------------------------------------------------------------------------
+
+from attn_ref import attention_f64  # noqa: E402
+
+
+@pytest.mark.parametrize("nh,nkv,d", [(8, 4, 256), (4, 4, 128), (8, 2, 64)])
+@pytest.mark.parametrize("softcap,window", [(0.0, 0), (50.0, 0), (0.0, 40)])
+def test_attention_vs_f64(o, nh, nkv, d, softcap, window):
+    rows, pos, row0 = 300, 250, 20
+    kc = synth.normal_f32(7, "kc", (rows, nkv * d))
+    vc = synth.normal_f32(7, "vc", (rows, nkv * d))
+    q = synth.normal_f32(7, "q", (nh * d,), 0, 0.25)
+    scale = float(np.float32(1.0 / np.sqrt(d)))
+    got = o.attention(q, kc, vc, row0, pos, nh, nkv, d, scale, softcap, window).astype(np.float64)
+    ref, tol = attention_f64(q, kc, vc, row0, pos, nh, nkv, d, scale, softcap, window)
+    assert np.all(np.abs(got - ref) <= tol), float(np.max(np.abs(got - ref) / tol))
+
+
+def test_attention_closed_forms(o):
+    nh, nkv, d = 8, 4, 128
+    kc = synth.normal_f32(8, "kc", (64, nkv * d))
+    vc = synth.normal_f32(8, "vc", (64, nkv * d))
+    q = synth.normal_f32(8, "q", (nh * d,))
+    # one position (pos 0, or a window of 1): weight exactly 1, out = v of that position
+    for pos, window in ((0, 0), (37, 1)):
+        out = o.attention(q, kc, vc, 0, pos, nh, nkv, d, 0.1, 0.0, window).reshape(nh, d)
+        for h in range(nh):
+            np.testing.assert_array_equal(out[h], vc[pos, (h // 2) * d:(h // 2 + 1) * d])
+    # q = 0: equal scores, out = the mean of v over [0, pos]
+    out = o.attention(np.zeros(nh * d, np.float32), kc, vc, 0, 19, nh, nkv, d, 0.1).reshape(nh, d)
+    mean = vc[:20].astype(np.float64).mean(axis=0)
+    for h in range(nh):
+        np.testing.assert_allclose(out[h], mean[(h // 2) * d:(h // 2 + 1) * d], rtol=0, atol=2e-6)
+    # bf16 cache = the same attention over the upconverted values
+    kb, vb = o.f32_to_bf16(kc), o.f32_to_bf16(vc)
+    a = o.attention(q, kb, vb, 0, 40, nh, nkv, d, 0.1)
+    b = o.attention(q, o.bf16_to_f32(kb), o.bf16_to_f32(vb), 0, 40, nh, nkv, d, 0.1)
+    np.testing.assert_array_equal(a, b)

@@ -97,6 +97,13 @@ SIGNATURES = {
     "hip_gemm_q8_0": (None, [_v, _v, _v, _i, _i, _i, _v]),
     "hip_gemm_f16": (None, [_v, _v, _v, _i, _i, _i, _v]),
     "hip_gemm": (None, [_i, _v, _v, _v, _i, _i, _i, _v]),
+    # decode attention (cuda_bridge.h:115-168)
+    "hip_attention_forward": (None, [_v, _v, _v, _v, _i, _i, _i, _i, _i, _i, _i, _f, _f, _i, _v]),
+    "hip_attention_forward_ind": (None, [_v, _v, _v, _v, _i, _v, _i, _i, _i, _i, _i, _f, _f, _i, _v]),
+    "hip_attention_batched": (None, [_v, _v, _v, _v, _i, _i, _i, _i, _i, _i, _i, _i, _f, _f, _i, _v]),
+    "hip_attention_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i]),
+    "hip_attention_decode": (None, [_i, _v, _v, _v, _v, _i64, _i64, _v, _i64, _v, _i, _i, _i, _i, _i, _i,
+                                    _f, _f, _i, _v, _sz, _v]),
     "hip_geglu_ex": (None, [_i, _v, _v, _v, _i64, _v]),
     "hip_tanh_softcap_ex": (None, [_i, _v, _f, _i64, _v]),
 }

@@ -1,0 +1,348 @@
+// Decode attention over the KV cache with soft-capped scores, sliding window and GQA
+// (replaces cuda_bridge.cu:2466-2879: cuda_attention_forward, _ind, _batched; CPU
+// definition model.zig:658-700 with math.softmax, math.zig:1088-1106).
+//
+// Query token b (of `batch`) at position p_b attends to positions [start_b, p_b], start_b =
+// p_b + 1 - window when a window is set and exceeded: score_t = (q_h . k_t) * scale, then
+// cap * tanh(score / cap) when cap > 0, softmax over t, out_h = sum_t w_t v_t; query head h
+// reads kv head h / (n_heads / n_kv_heads).
+//
+// Layout (flash-decoding). One workgroup per (token b, kv head, split s) covers `chunk`
+// consecutive positions. Lanes come in groups of LT = D/8 (8 elements of a head row per
+// lane), one group per position, so a wave works on 64/LT positions at a time and the K/V row
+// loads of a position are one contiguous span; all G = n_heads/n_kv_heads query heads of the
+// kv head reuse each loaded K and V row. Each lane group keeps an online softmax state per
+// query head (running max m, sum l, accumulator a = sum exp(s - m) v); the groups and waves
+// are merged through LDS. With one split the workgroup writes out = a / l; otherwise it
+// writes (m, l, a) to the caller's workspace and a second kernel merges the splits.
+// Arithmetic: f32 throughout, exp via exp2; results agree with the CPU's (which exponentiates
+// after a full max pass and normalises the weights before the weighted sum) within the f32
+// rounding of the scores, not bit for bit.
+#include <algorithm>
+
+#include "zl_common.h"
+#include "zl_host.h"
+
+namespace zl {
+
+constexpr int kAttnThreads = 256;
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct AttnArgs {
+    const float* q;           // [batch][n_heads][D]
+    const void* kc;           // cache rows of row_stride elements (f32 or bf16)
+    const void* vc;
+    float* out;               // [batch][n_heads][D]
+    float* ws;                // [batch][n_heads][nsplit][D + 2] partials (nsplit > 1)
+    const int32_t* pos;       // per-token positions, or null: pos_base + b
+    const int64_t* row_base;  // per-token cache row of position 0, or null: row0
+    int64_t row0;
+    int64_t cache_rows;       // > 0: rows outside [0, cache_rows) give a zero output
+    int64_t row_stride;
+    int pos_base;
+    int max_len;              // positions must be < max_len
+    int batch, nh, nkv, D;
+    int window;
+    int nsplit, chunk;
+    float scale, softcap, inv_cap;
+};
+
+// Position range of token b, or an empty range when its rows fall outside the cache.
+__device__ __forceinline__ void attn_range(const AttnArgs& a, int b, int& start, int& end, int64_t& rb) {
+    const int p = a.pos ? a.pos[b] : a.pos_base + b;
+    rb = a.row_base ? a.row_base[b] : a.row0;
+    start = 0;
+    end = 0;
+    if (p < 0 || p >= a.max_len || rb < 0) return;
+    if (a.cache_rows > 0 && rb + p >= a.cache_rows) return;
+    end = p + 1;
+    start = (a.window > 0 && end > a.window) ? end - a.window : 0;
+}
+
+template <typename KT>
+__device__ __forceinline__ void load8(const KT* row, float* v) {
+    if constexpr (sizeof(KT) == 4) {
+        const f32x4 x = ldf4((const float*)row), y = ldf4((const float*)row + 4);
+        v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+        v[4] = y.x; v[5] = y.y; v[6] = y.z; v[7] = y.w;
+    } else {
+        Chunk<uint16_t>::unpack(ld16(row), v);
+    }
+}
+
+template <typename KT, int D, int G>
+__global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
+    constexpr int LT = D / 8;                  // lanes per position
+    constexpr int SLOTS = kAttnThreads / LT;   // positions in flight per workgroup
+    // Per-slot states for the merge: m, l per query head, a per (head, element).
+    __shared__ float s_m[SLOTS][G], s_l[SLOTS][G];
+    __shared__ float s_a[SLOTS][G][D];
+    const int tid = threadIdx.x;
+    const int slot = tid / LT;
+    const int li = tid % LT;                   // 8-element slice of the head row
+    const int split = blockIdx.x % a.nsplit;
+    const int bk = blockIdx.x / a.nsplit;
+    const int kvh = bk % a.nkv;
+    const int b = bk / a.nkv;
+
+    int start, end;
+    int64_t rb;
+    attn_range(a, b, start, end, rb);
+    const int t0 = start + split * a.chunk;
+    const int t1 = min(end, t0 + a.chunk);
+
+    float q[G][8];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const float* qh = a.q + ((int64_t)b * a.nh + kvh * G + g) * D + li * 8;
+        const f32x4 x = ldf4(qh), y = ldf4(qh + 4);
+        q[g][0] = x.x; q[g][1] = x.y; q[g][2] = x.z; q[g][3] = x.w;
+        q[g][4] = y.x; q[g][5] = y.y; q[g][6] = y.z; q[g][7] = y.w;
+    }
+    float m[G], l[G], acc[G][8];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        m[g] = -INFINITY;
+        l[g] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[g][e] = 0.0f;
+    }
+
+    const KT* kbase = (const KT*)a.kc + kvh * D + li * 8;
+    const KT* vbase = (const KT*)a.vc + kvh * D + li * 8;
+    for (int t = t0 + slot; t < t1; t += SLOTS) {
+        const int64_t off = (rb + t) * a.row_stride;
+        float k[8], v[8];
+        load8<KT>(kbase + off, k);
+        load8<KT>(vbase + off, v);
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            float s = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) s = fmaf(q[g][e], k[e], s);
+            s = group_sum<LT>(s) * a.scale;
+            if (a.softcap > 0.0f) s = a.softcap * tanh_fast(div_by_uniform(s, a.softcap, a.inv_cap));
+            const float mn = fmaxf(m[g], s);
+            const float c = exp2f((m[g] - mn) * kLog2e);
+            const float p = exp2f((s - mn) * kLog2e);
+            l[g] = l[g] * c + p;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(p, v[e], acc[g][e] * c);
+            m[g] = mn;
+        }
+    }
+
+    // Merge the SLOTS states: every slot stores its state, then thread i merges element
+    // (g, e) = i over the slots in slot order, rescaling each by exp(m_slot - max).
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        if (li == 0) {
+            s_m[slot][g] = m[g];
+            s_l[slot][g] = l[g];
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s_a[slot][g][li * 8 + e] = acc[g][e];
+    }
+    __syncthreads();
+    for (int i = tid; i < G * D; i += kAttnThreads) {
+        const int g = i / D, e = i % D;
+        float M = -INFINITY;
+        for (int s = 0; s < SLOTS; ++s) M = fmaxf(M, s_m[s][g]);
+        float L = 0.0f, A = 0.0f;
+        if (M != -INFINITY) {
+            for (int s = 0; s < SLOTS; ++s) {
+                const float c = exp2f((s_m[s][g] - M) * kLog2e);
+                L = fmaf(s_l[s][g], c, L);
+                A = fmaf(s_a[s][g][e], c, A);
+            }
+        }
+        const int h = kvh * G + g;
+        if (a.nsplit == 1) {
+            a.out[((int64_t)b * a.nh + h) * D + e] = L > 0.0f ? A / L : 0.0f;
+        } else {
+            float* w = a.ws + (((int64_t)b * a.nh + h) * a.nsplit + split) * (D + 2);
+            w[2 + e] = A;
+            if (e == 0) {
+                w[0] = M;
+                w[1] = L;
+            }
+        }
+    }
+}
+
+// Merge the splits of (token b, head h): one workgroup, threads over the head's elements.
+__global__ __launch_bounds__(kAttnThreads) void k_attn_merge(AttnArgs a) {
+    const int bh = blockIdx.x;
+    const float* w = a.ws + (int64_t)bh * a.nsplit * (a.D + 2);
+    float M = -INFINITY;
+    for (int s = 0; s < a.nsplit; ++s) M = fmaxf(M, w[s * (a.D + 2)]);
+    for (int e = threadIdx.x; e < a.D; e += kAttnThreads) {
+        float L = 0.0f, A = 0.0f;
+        if (M != -INFINITY) {
+            for (int s = 0; s < a.nsplit; ++s) {
+                const float* ws = w + s * (a.D + 2);
+                const float c = exp2f((ws[0] - M) * kLog2e);
+                L = fmaf(ws[1], c, L);
+                A = fmaf(ws[2 + e], c, A);
+            }
+        }
+        a.out[(int64_t)bh * a.D + e] = L > 0.0f ? A / L : 0.0f;
+    }
+}
+
+template <typename KT, int D>
+static void launch_g(const AttnArgs& a, int G, hipStream_t s) {
+    const unsigned grid = (unsigned)((int64_t)a.batch * a.nkv * a.nsplit);
+    switch (G) {
+        case 1: k_attn<KT, D, 1><<<grid, kAttnThreads, 0, s>>>(a); break;
+        case 2: k_attn<KT, D, 2><<<grid, kAttnThreads, 0, s>>>(a); break;
+        default: k_attn<KT, D, 4><<<grid, kAttnThreads, 0, s>>>(a); break;
+    }
+}
+
+// Positions per split: enough splits that batch * n_kv_heads * splits fills the chip
+// (~2048 workgroups), at least 64 positions each.
+static void choose_split(AttnArgs& a, size_t ws_bytes) {
+    const int len = a.window > 0 ? std::min(a.window, a.max_len) : a.max_len;
+    const int64_t groups = (int64_t)a.batch * a.nkv;
+    int nsplit = (int)std::max<int64_t>(1, std::min<int64_t>(cdiv(len, 64), cdiv(2048, groups)));
+    const size_t need = (size_t)a.batch * a.nh * nsplit * (a.D + 2) * sizeof(float);
+    if (!a.ws || need > ws_bytes) nsplit = 1;
+    a.nsplit = nsplit;
+    a.chunk = (int)cdiv(len, nsplit);
+}
+
+static void launch_attn(int kv_dtype, AttnArgs& a, size_t ws_bytes, hipStream_t s) {
+    if (a.batch <= 0 || a.nh <= 0) return;
+    const int G = a.nkv > 0 ? a.nh / a.nkv : 0;
+    if (!a.q || !a.kc || !a.vc || !a.out || a.nkv <= 0 || a.nh % a.nkv != 0 || a.max_len <= 0) {
+        set_error(HIP_BRIDGE_EINVAL);
+        return;
+    }
+    // G <= 4: the merge buffer is 8 KB per query head of the group (static LDS <= 64 KB)
+    const bool shapes = (a.D == 64 || a.D == 128 || a.D == 256) && (G == 1 || G == 2 || G == 4) &&
+                        (int64_t)a.nkv * a.D <= a.row_stride;
+    const int es = kv_dtype == HIP_BRIDGE_BF16 ? 2 : 4;
+    const bool aligned = aligned16(a.q) && aligned16(a.kc) && aligned16(a.vc) && (a.row_stride * es) % 16 == 0;
+    if ((kv_dtype != HIP_BRIDGE_F32 && kv_dtype != HIP_BRIDGE_BF16) || !shapes || !aligned) {
+        set_error(HIP_BRIDGE_EUNSUPPORTED);
+        return;
+    }
+    a.inv_cap = a.softcap > 0.0f ? 1.0f / a.softcap : 0.0f;
+    choose_split(a, ws_bytes);
+    if ((int64_t)a.batch * a.nkv * a.nsplit > INT32_MAX) {
+        set_error(HIP_BRIDGE_EUNSUPPORTED);
+        return;
+    }
+    if (kv_dtype == HIP_BRIDGE_F32) {
+        if (a.D == 64) launch_g<float, 64>(a, G, s);
+        else if (a.D == 128) launch_g<float, 128>(a, G, s);
+        else launch_g<float, 256>(a, G, s);
+    } else {
+        if (a.D == 64) launch_g<uint16_t, 64>(a, G, s);
+        else if (a.D == 128) launch_g<uint16_t, 128>(a, G, s);
+        else launch_g<uint16_t, 256>(a, G, s);
+    }
+    if (a.nsplit > 1) k_attn_merge<<<(unsigned)((int64_t)a.batch * a.nh), kAttnThreads, 0, s>>>(a);
+    check_launch();
+}
+
+static AttnArgs base_attn(const float* q, const void* kc, const void* vc, float* out, int n_heads,
+                          int n_kv_heads, int head_dim, float scale, float softcap, int window) {
+    AttnArgs a{};
+    a.q = q;
+    a.kc = kc;
+    a.vc = vc;
+    a.out = out;
+    a.nh = n_heads;
+    a.nkv = n_kv_heads;
+    a.D = head_dim;
+    a.scale = scale;
+    a.softcap = softcap;
+    a.window = window;
+    return a;
+}
+
+}  // namespace zl
+
+using namespace zl;
+
+extern "C" {
+
+size_t hip_attention_workspace_bytes(int batch, int n_heads, int n_kv_heads, int head_dim, int max_len,
+                                     int sliding_window) {
+    if (batch <= 0 || n_heads <= 0 || n_kv_heads <= 0 || head_dim <= 0 || max_len <= 0) return 0;
+    AttnArgs a{};
+    a.batch = batch;
+    a.nh = n_heads;
+    a.nkv = n_kv_heads;
+    a.D = head_dim;
+    a.max_len = max_len;
+    a.window = sliding_window;
+    a.ws = reinterpret_cast<float*>(16);  // any non-null pointer: size for the unconstrained split
+    choose_split(a, SIZE_MAX);
+    return a.nsplit > 1 ? (size_t)batch * n_heads * a.nsplit * (head_dim + 2) * sizeof(float) : 0;
+}
+
+void hip_attention_decode(int kv_dtype, const float* q, const void* k_cache, const void* v_cache, float* out,
+                          int64_t cache_rows, int64_t row_stride, const int64_t* d_row_base, int64_t row_base,
+                          const int32_t* d_pos, int pos_base, int max_len, int batch, int n_heads,
+                          int n_kv_heads, int head_dim, float attn_scale, float softcap, int sliding_window,
+                          void* workspace, size_t workspace_bytes, HipStream_t stream) {
+    AttnArgs a = base_attn(q, k_cache, v_cache, out, n_heads, n_kv_heads, head_dim, attn_scale, softcap,
+                           sliding_window);
+    a.ws = (float*)workspace;
+    a.cache_rows = cache_rows;
+    a.row_stride = row_stride;
+    a.row_base = d_row_base;
+    a.row0 = row_base;
+    a.pos = d_pos;
+    a.pos_base = pos_base;
+    a.max_len = max_len;
+    a.batch = batch;
+    if (!aligned16(workspace)) a.ws = nullptr;
+    launch_attn(kv_dtype, a, workspace_bytes, stream_of(stream));
+}
+
+void hip_attention_forward(const float* q, const float* k_cache, const float* v_cache, float* out,
+                           int donor_layer, int pos, int max_seq, int n_heads, int n_kv_heads, int head_dim,
+                           int max_kv_dim, float attn_scale, float softcap, int sliding_window,
+                           HipStream_t stream) {
+    hip_attention_batched(q, k_cache, v_cache, out, donor_layer, pos, 1, max_seq, n_heads, n_kv_heads,
+                          head_dim, max_kv_dim, attn_scale, softcap, sliding_window, stream);
+}
+
+void hip_attention_forward_ind(const float* q, const float* k_cache, const float* v_cache, float* out,
+                               int donor_layer, const int* d_pos, int max_seq, int n_heads, int n_kv_heads,
+                               int head_dim, int max_kv_dim, float attn_scale, float softcap,
+                               int sliding_window, HipStream_t stream) {
+    if (!d_pos) {
+        set_error(HIP_BRIDGE_EINVAL);
+        return;
+    }
+    AttnArgs a = base_attn(q, k_cache, v_cache, out, n_heads, n_kv_heads, head_dim, attn_scale, softcap,
+                           sliding_window);
+    a.row0 = (int64_t)donor_layer * max_seq;
+    a.row_stride = max_kv_dim;
+    a.pos = d_pos;
+    a.max_len = max_seq;
+    a.batch = 1;
+    launch_attn(HIP_BRIDGE_F32, a, 0, stream_of(stream));
+}
+
+void hip_attention_batched(const float* q, const float* k_cache, const float* v_cache, float* out,
+                           int donor_layer, int pos, int batch_size, int max_seq, int n_heads, int n_kv_heads,
+                           int head_dim, int max_kv_dim, float attn_scale, float softcap, int sliding_window,
+                           HipStream_t stream) {
+    if (batch_size <= 0) return;
+    AttnArgs a = base_attn(q, k_cache, v_cache, out, n_heads, n_kv_heads, head_dim, attn_scale, softcap,
+                           sliding_window);
+    a.row0 = (int64_t)donor_layer * max_seq;
+    a.row_stride = max_kv_dim;
+    a.pos_base = pos;
+    a.max_len = max_seq;
+    a.batch = batch_size;
+    launch_attn(HIP_BRIDGE_F32, a, 0, stream_of(stream));
+}
+
+}  // extern "C"

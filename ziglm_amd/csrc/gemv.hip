@@ -253,7 +253,6 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvArgs a) {
         }
 
         } else {
-#pragma unroll 2
         for (int g = tid; g < G; g += kGemvThreads) {
             WGroup<QT> wg[RPW][NM];
 #pragma unroll

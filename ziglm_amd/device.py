@@ -257,6 +257,41 @@ class HipDevice:
         self.b.hip_gemm(int(qtype), _ptr(d_weights), _ptr(d_x), _ptr(d_y), batch_size, rows, cols, self.stream)
         self._done("gemm")
 
+    # -- decode attention (cuda.zig:576-684) ---------------------------------------------
+    def attentionForward(self, d_q, d_k_cache, d_v_cache, d_out, donor_layer, pos, max_seq, n_heads,
+                         n_kv_heads, head_dim, max_kv_dim, attn_scale, softcap, sliding_window):
+        self.b.hip_attention_forward(_ptr(d_q), _ptr(d_k_cache), _ptr(d_v_cache), _ptr(d_out), donor_layer, pos,
+                                     max_seq, n_heads, n_kv_heads, head_dim, max_kv_dim, attn_scale, softcap,
+                                     sliding_window, self.stream)
+        self._done("attentionForward")
+
+    def attentionForwardInd(self, d_q, d_k_cache, d_v_cache, d_out, donor_layer, d_pos, max_seq, n_heads,
+                            n_kv_heads, head_dim, max_kv_dim, attn_scale, softcap, sliding_window):
+        self.b.hip_attention_forward_ind(_ptr(d_q), _ptr(d_k_cache), _ptr(d_v_cache), _ptr(d_out), donor_layer,
+                                         _ptr(d_pos), max_seq, n_heads, n_kv_heads, head_dim, max_kv_dim,
+                                         attn_scale, softcap, sliding_window, self.stream)
+        self._done("attentionForwardInd")
+
+    def attentionBatched(self, d_q, d_k_cache, d_v_cache, d_out, donor_layer, pos, batch_size, max_seq,
+                         n_heads, n_kv_heads, head_dim, max_kv_dim, attn_scale, softcap, sliding_window):
+        self.b.hip_attention_batched(_ptr(d_q), _ptr(d_k_cache), _ptr(d_v_cache), _ptr(d_out), donor_layer, pos,
+                                     batch_size, max_seq, n_heads, n_kv_heads, head_dim, max_kv_dim, attn_scale,
+                                     softcap, sliding_window, self.stream)
+        self._done("attentionBatched")
+
+    def attentionWorkspaceBytes(self, batch, n_heads, n_kv_heads, head_dim, max_len, sliding_window=0):
+        return int(self.b.hip_attention_workspace_bytes(batch, n_heads, n_kv_heads, head_dim, max_len,
+                                                        sliding_window))
+
+    def attentionDecode(self, kv_dtype, d_q, d_k_cache, d_v_cache, d_out, cache_rows, row_stride, d_row_base,
+                        row_base, d_pos, pos_base, max_len, batch, n_heads, n_kv_heads, head_dim, attn_scale,
+                        softcap, sliding_window, d_workspace=None, workspace_bytes=0):
+        self.b.hip_attention_decode(int(kv_dtype), _ptr(d_q), _ptr(d_k_cache), _ptr(d_v_cache), _ptr(d_out),
+                                    cache_rows, row_stride, _ptr(d_row_base), row_base, _ptr(d_pos), pos_base,
+                                    max_len, batch, n_heads, n_kv_heads, head_dim, attn_scale, softcap,
+                                    sliding_window, _ptr(d_workspace), workspace_bytes, self.stream)
+        self._done("attentionDecode")
+
     def gegluEx(self, dtype, d_gate, d_up, d_out, n):
         self.b.hip_geglu_ex(dtype, _ptr(d_gate), _ptr(d_up), _ptr(d_out), n, self.stream)
         self._done("gegluEx")
