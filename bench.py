@@ -275,10 +275,25 @@ def bench_decode(dev, B_, pos_seed=4, n_launch=200):
     us_fnorm = time_launches_us(dev, LY.op_input_norm, [L], n_launch)
     for bb in bufs:
         bb.deinit()
+    # decode attention over each sequence's cache (positions as above, f32 cache, split)
+    row_base = dev.from_numpy(np.arange(B_, dtype=np.int64) * max_seq)
+    ws_bytes = dev.attentionWorkspaceBytes(B_, s.nh, s.nkv, s.D, max_seq)
+    d_ws = dev.alloc(max(ws_bytes, 16))
+    d_ao = dev.alloc(B_ * s.nh * s.D * 4)
+
+    def attn(d, L_):
+        d.attentionDecode(B.F32, L_.q, L_.kc, L_.vc, d_ao, L_.cache_rows, s.nkv * s.D, row_base, 0, L_.pos, 0,
+                          max_seq, B_, s.nh, s.nkv, s.D, 1.0, 0.0, 0, d_ws, ws_bytes)
+    us_attn = time_launches_us(dev, attn, [L], max(8, n_launch // 10))
+    attn_bytes = int((pos.astype(np.int64) + 1).sum()) * s.nkv * s.D * 4 * 2 + 2 * B_ * s.nh * s.D * 4
+    for bb in (row_base, d_ws, d_ao):
+        bb.deinit()
     free_sets([L])
     cap_bytes = 2 * 4 * B_ * V
     return {"B": B_, "us_per_layer": round(chain_us, 2), "us_per_layer_fused_4op": round(fused_us, 2), "ops": ops,
             "final_norm_us": round(us_fnorm, 3),
+            "attention": {"us": round(us_attn, 2), "bytes": attn_bytes, "GBps": round(attn_bytes / us_attn / 1e3, 1),
+                          "frac_peak": round(attn_bytes / us_attn / 1e3 / PEAK_HBM_GBS, 4)},
             "softcap": {"us": round(us_cap, 2), "bytes": cap_bytes,
                         "GBps": round(cap_bytes / us_cap / 1e3, 1),
                         "frac_peak": round(cap_bytes / us_cap / 1e3 / PEAK_HBM_GBS, 4)}}
@@ -604,8 +619,9 @@ def main():
         cfgs["c5_decode"] = {}
         for b_ in (1, 8, 64, 256):
             cfgs["c5_decode"][f"B{b_}"] = bench_decode(dev, b_)
-            log(f"  B={b_}: {cfgs['c5_decode'][f'B{b_}']['us_per_layer']} us/layer, "
-                f"{cfgs['c5_decode'][f'B{b_}']['us_per_layer_fused_4op']} fused")
+            c5b = cfgs['c5_decode'][f'B{b_}']
+            log(f"  B={b_}: {c5b['us_per_layer']} us/layer, {c5b['us_per_layer_fused_4op']} fused; "
+                f"attention {c5b['attention']['us']} us {c5b['attention']['GBps']} GB/s")
         result["configs"] = cfgs
     if not a.no_cpu:
         log("cpu baseline")

@@ -110,11 +110,24 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
 
     const KT* kbase = (const KT*)a.kc + kvh * D + li * 8;
     const KT* vbase = (const KT*)a.vc + kvh * D + li * 8;
-    for (int t = t0 + slot; t < t1; t += SLOTS) {
-        const int64_t off = (rb + t) * a.row_stride;
+    // Double-buffered: the next position's K/V rows are in flight during this one's math.
+    float kn[8], vn[8];
+    int t = t0 + slot;
+    if (t < t1) {
+        load8<KT>(kbase + (rb + t) * a.row_stride, kn);
+        load8<KT>(vbase + (rb + t) * a.row_stride, vn);
+    }
+    for (; t < t1; t += SLOTS) {
         float k[8], v[8];
-        load8<KT>(kbase + off, k);
-        load8<KT>(vbase + off, v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            k[e] = kn[e];
+            v[e] = vn[e];
+        }
+        if (t + SLOTS < t1) {
+            load8<KT>(kbase + (rb + t + SLOTS) * a.row_stride, kn);
+            load8<KT>(vbase + (rb + t + SLOTS) * a.row_stride, vn);
+        }
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             float s = 0.0f;
@@ -170,22 +183,40 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
     }
 }
 
-// Merge the splits of (token b, head h): one workgroup, threads over the head's elements.
+// Merge the splits of (token b, head h): one workgroup. The per-split factors
+// exp(m_s - M) and the total L are formed once in LDS, then each thread sums its elements
+// over the splits (8 split loads in flight per thread).
+constexpr int kMaxSplit = 1024;
 __global__ __launch_bounds__(kAttnThreads) void k_attn_merge(AttnArgs a) {
+    __shared__ float s_c[kMaxSplit];
+    __shared__ float s_red[kAttnThreads / kWave];
     const int bh = blockIdx.x;
+    const int tid = threadIdx.x;
     const float* w = a.ws + (int64_t)bh * a.nsplit * (a.D + 2);
-    float M = -INFINITY;
-    for (int s = 0; s < a.nsplit; ++s) M = fmaxf(M, w[s * (a.D + 2)]);
-    for (int e = threadIdx.x; e < a.D; e += kAttnThreads) {
-        float L = 0.0f, A = 0.0f;
-        if (M != -INFINITY) {
-            for (int s = 0; s < a.nsplit; ++s) {
-                const float* ws = w + s * (a.D + 2);
-                const float c = exp2f((ws[0] - M) * kLog2e);
-                L = fmaf(ws[1], c, L);
-                A = fmaf(ws[2 + e], c, A);
-            }
-        }
+    float mx = -INFINITY;
+    for (int s = tid; s < a.nsplit; s += kAttnThreads) mx = fmaxf(mx, w[(int64_t)s * (a.D + 2)]);
+    // block max (DPP within waves, then the 4 wave values)
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    if ((tid & 63) == 0) s_red[tid >> 6] = mx;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+    __syncthreads();
+    float lsum = 0.0f;
+    for (int s = tid; s < a.nsplit; s += kAttnThreads) {
+        const float* ws = w + (int64_t)s * (a.D + 2);
+        const float c = M == -INFINITY ? 0.0f : exp2f((ws[0] - M) * kLog2e);
+        s_c[s] = c;
+        lsum = fmaf(ws[1], c, lsum);
+    }
+    lsum = group_sum<kWave>(lsum);
+    if ((tid & 63) == 0) s_red[tid >> 6] = lsum;
+    __syncthreads();
+    const float L = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+    for (int e = tid; e < a.D; e += kAttnThreads) {
+        float A = 0.0f;
+#pragma unroll 8
+        for (int s = 0; s < a.nsplit; ++s) A = fmaf(w[(int64_t)s * (a.D + 2) + 2 + e], s_c[s], A);
         a.out[(int64_t)bh * a.D + e] = L > 0.0f ? A / L : 0.0f;
     }
 }
@@ -201,11 +232,14 @@ static void launch_g(const AttnArgs& a, int G, hipStream_t s) {
 }
 
 // Positions per split: enough splits that batch * n_kv_heads * splits fills the chip
-// (~2048 workgroups), at least 64 positions each.
+// (~2048 workgroups) and no split exceeds 1024 positions (sequences of a batch differ in
+// length: short splits keep the long ones from leaving a tail), at least 128 positions
+// each, at most kMaxSplit splits.
 static void choose_split(AttnArgs& a, size_t ws_bytes) {
     const int len = a.window > 0 ? std::min(a.window, a.max_len) : a.max_len;
     const int64_t groups = (int64_t)a.batch * a.nkv;
-    int nsplit = (int)std::max<int64_t>(1, std::min<int64_t>(cdiv(len, 64), cdiv(2048, groups)));
+    const int64_t want = std::max<int64_t>(cdiv(2048, groups), cdiv(len, 1024));
+    int nsplit = (int)std::max<int64_t>(1, std::min<int64_t>({cdiv(len, 128), want, (int64_t)kMaxSplit}));
     const size_t need = (size_t)a.batch * a.nh * nsplit * (a.D + 2) * sizeof(float);
     if (!a.ws || need > ws_bytes) nsplit = 1;
     a.nsplit = nsplit;
