@@ -38,6 +38,7 @@ sys.path.insert(0, ROOT)
 
 from ziglm_amd import bridge as B  # noqa: E402
 from ziglm_amd import layer as LY  # noqa: E402
+from ziglm_amd.device import Graph  # noqa: E402
 from ziglm_amd import synth  # noqa: E402
 from ziglm_amd.device import HipDevice  # noqa: E402
 
@@ -53,29 +54,6 @@ def log(*a):
 # ---------------------------------------------------------------------------------------
 # graph capture + timing
 # ---------------------------------------------------------------------------------------
-
-class Graph:
-    """hipGraph of whatever `body()` enqueues on dev.stream."""
-
-    def __init__(self, dev, body):
-        self.dev, b = dev, dev.b
-        b.check(b.hip_graph_begin_capture(dev.stream), "begin_capture")
-        try:
-            body()
-        finally:
-            g = ctypes.c_void_p()
-            b.check(b.hip_graph_end_capture(dev.stream, ctypes.byref(g)), "end_capture")
-        ex = ctypes.c_void_p()
-        b.check(b.hip_graph_instantiate(ctypes.byref(ex), g), "instantiate")
-        self.graph, self.exec = g.value, ex.value
-
-    def launch(self):
-        self.dev.b.check(self.dev.b.hip_graph_launch(self.exec, self.dev.stream), "graph_launch")
-
-    def destroy(self):
-        self.dev.b.hip_graph_exec_destroy(self.exec)
-        self.dev.b.hip_graph_destroy(self.graph)
-
 
 def time_graph_ms(dev, g, reps=1):
     e0, e1 = dev.event(), dev.event()

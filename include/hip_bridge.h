@@ -274,6 +274,14 @@ void hip_attention_decode(int kv_dtype, const float* q, const void* k_cache, con
                           void* workspace, size_t workspace_bytes, HipStream_t stream);
 
 /* ---------------------------------------------------------------------------------- */
+/* Greedy token selection (replaces cuda_bridge.h:175) with ziglm's CPU definition      */
+/* (sampler.zig:158-170): *out_idx = first index of the greatest logit in [1, n) (index 0, */
+/* the pad token, is never chosen; NaN never compares greater; n <= 1 gives 0).          */
+/* Partials live in device globals: calls on different streams must not overlap.        */
+/* ---------------------------------------------------------------------------------- */
+void hip_argmax(const float* logits, int n, unsigned int* out_idx, HipStream_t stream); /* cuda_bridge.h:175 */
+
+/* ---------------------------------------------------------------------------------- */
 /* Activations & elementwise (replaces cuda_bridge.h:64, 66-68)                         */
 /* ---------------------------------------------------------------------------------- */
 /* out = gelu_tanh(gate) * up; out may alias gate or up. */

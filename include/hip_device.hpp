@@ -198,6 +198,11 @@ public:
                               attn_scale, softcap, (int)sliding_window, stream);
     }
 
+    // cuda.zig:743-750
+    void argmax(const float* d_logits, size_t n, unsigned int* d_out_idx) const {
+        hip_argmax(d_logits, (int)n, d_out_idx, stream);
+    }
+
     // cuda.zig:686-750
     void geglu(const float* d_gate, const float* d_up, float* d_out, size_t n) const {
         hip_geglu(d_gate, d_up, d_out, (int)n, stream);

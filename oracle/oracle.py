@@ -60,6 +60,7 @@ _SIGS = {
     "zo_dot_row": (ctypes.c_float, [_i, _u8p, _fp, _sz]),
     "zo_gemv": (_i, [_i, _u8p, _fp, _fp, _sz, _sz]),
     "zo_gemm": (_i, [_i, _u8p, _fp, _fp, _sz, _sz, _sz]),
+    "zo_argmax": (ctypes.c_uint32, [_fp, _sz]),
     "zo_attention_token": (_i, [_fp, _vp, _vp, _i, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _f, _f, _fp]),
     "zo_qk_norm_rope_kv": (
         None,
@@ -160,6 +161,11 @@ class Oracle:
         if rc != 0:
             raise ValueError(f"unsupported qtype {qtype}")
         return y
+
+    def argmax(self, logits):
+        """sampler.sampleGreedy over one row of logits."""
+        x = np.ascontiguousarray(logits, dtype=np.float32).reshape(-1)
+        return int(self.lib.zo_argmax(self.fp(x), x.size))
 
     def attention(self, q, kc, vc, row0, pos, n_heads, n_kv_heads, head_dim, scale, softcap=0.0,
                   window=0):

@@ -115,6 +115,9 @@ int zo_attention_token(const float* q, const void* k_cache, const void* v_cache,
                        size_t row0, size_t row_stride, size_t pos, size_t window, size_t n_heads,
                        size_t n_kv_heads, size_t head_dim, float scale, float softcap, float* out);
 
+/* ---- greedy sampling (sampler.zig:158-170) ---- */
+uint32_t zo_argmax(const float* logits, size_t n);
+
 #ifdef __cplusplus
 }
 #endif

@@ -277,3 +277,20 @@ int zo_attention_token(const float* q, const void* kc, const void* vc, int kv_dt
     free(kv);
     return 0;
 }
+
+/* sampler.zig:158-170 sampleGreedy: index 0 (the pad token) is never chosen; the first
+ * index of the strictly greatest value from index 1 on; n <= 1 gives 0. NaN compares false,
+ * so a NaN at index 1 is kept and NaNs elsewhere are skipped. Pinned by the reference's own
+ * test (sampler.zig:173-177) and by brute force in the tests. */
+uint32_t zo_argmax(const float* logits, size_t n) {
+    if (n <= 1) return 0;
+    size_t best = 1;
+    float m = logits[1];
+    for (size_t i = 2; i < n; ++i) {
+        if (logits[i] > m) {
+            m = logits[i];
+            best = i;
+        }
+    }
+    return (uint32_t)best;
+}

@@ -199,3 +199,45 @@ def test_attention_closed_forms(o):
     a = o.attention(q, kb, vb, 0, 40, nh, nkv, d, 0.1)
     b = o.attention(q, o.bf16_to_f32(kb), o.bf16_to_f32(vb), 0, 40, nh, nkv, d, 0.1)
     np.testing.assert_array_equal(a, b)
+
+
+# ---------------------------------------------------------------------------------------
+# Greedy selection (sampler.zig:158-170)
+# ---------------------------------------------------------------------------------------
+
+def greedy_brute(x):
+    """First index i >= 1 of the strictly greatest value scanning from index 1 (Python)."""
+    if len(x) <= 1:
+        return 0
+    best, m = 1, x[1]
+    for i in range(2, len(x)):
+        if x[i] > m:
+            best, m = i, x[i]
+    return best
+
+
+def test_argmax_sampler_zig_173(o):
+    assert o.argmax(np.array([0.1, 2.5, 0.3, -1.0], np.float32)) == 1
+
+
+@pytest.mark.parametrize("case", ["random", "ties", "index0", "nan1", "nan_mid", "inf", "short"])
+def test_argmax_brute_force(o, case):
+    rng = np.random.default_rng(abs(hash(case)) % 1000)
+    x = rng.normal(0, 1, 5000).astype(np.float32)
+    if case == "ties":
+        x[[7, 3000, 4999]] = 9.0
+    elif case == "index0":
+        x[0] = 100.0
+    elif case == "nan1":
+        x[1] = np.nan
+    elif case == "nan_mid":
+        x[[5, 17, 4000]] = np.nan
+        x[4001] = 50.0
+    elif case == "inf":
+        x[:] = -np.inf
+        x[2500] = np.inf
+    elif case == "short":
+        for n in (0, 1, 2, 3):
+            assert o.argmax(x[:n]) == greedy_brute(list(x[:n]))
+        return
+    assert o.argmax(x) == greedy_brute(list(x))

@@ -97,6 +97,7 @@ SIGNATURES = {
     "hip_gemm_q8_0": (None, [_v, _v, _v, _i, _i, _i, _v]),
     "hip_gemm_f16": (None, [_v, _v, _v, _i, _i, _i, _v]),
     "hip_gemm": (None, [_i, _v, _v, _v, _i, _i, _i, _v]),
+    "hip_argmax": (None, [_v, _i, _v, _v]),
     # decode attention (cuda_bridge.h:115-168)
     "hip_attention_forward": (None, [_v, _v, _v, _v, _i, _i, _i, _i, _i, _i, _i, _f, _f, _i, _v]),
     "hip_attention_forward_ind": (None, [_v, _v, _v, _v, _i, _v, _i, _i, _i, _i, _i, _f, _f, _i, _v]),

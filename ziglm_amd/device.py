@@ -257,6 +257,11 @@ class HipDevice:
         self.b.hip_gemm(int(qtype), _ptr(d_weights), _ptr(d_x), _ptr(d_y), batch_size, rows, cols, self.stream)
         self._done("gemm")
 
+    # -- greedy token (cuda.zig:743-750) -------------------------------------------------
+    def argmax(self, d_logits, n, d_out_idx):
+        self.b.hip_argmax(_ptr(d_logits), n, _ptr(d_out_idx), self.stream)
+        self._done("argmax")
+
     # -- decode attention (cuda.zig:576-684) ---------------------------------------------
     def attentionForward(self, d_q, d_k_cache, d_v_cache, d_out, donor_layer, pos, max_seq, n_heads,
                          n_kv_heads, head_dim, max_kv_dim, attn_scale, softcap, sliding_window):
@@ -326,3 +331,27 @@ class HipDevice:
         ms = ctypes.c_float()
         self.b.check(self.b.hip_event_elapsed_ms(ctypes.byref(ms), start, stop), "hip_event_elapsed_ms")
         return ms.value
+
+
+class Graph:
+    """hipGraph of whatever `body()` enqueues on dev.stream (the reference's graph capture,
+    cuda_bridge.h:28-33): capture once, replay with launch()."""
+
+    def __init__(self, dev, body):
+        self.dev, b = dev, dev.b
+        b.check(b.hip_graph_begin_capture(dev.stream), "begin_capture")
+        try:
+            body()
+        finally:
+            g = ctypes.c_void_p()
+            b.check(b.hip_graph_end_capture(dev.stream, ctypes.byref(g)), "end_capture")
+        ex = ctypes.c_void_p()
+        b.check(b.hip_graph_instantiate(ctypes.byref(ex), g), "instantiate")
+        self.graph, self.exec = g.value, ex.value
+
+    def launch(self):
+        self.dev.b.check(self.dev.b.hip_graph_launch(self.exec, self.dev.stream), "graph_launch")
+
+    def destroy(self):
+        self.dev.b.hip_graph_exec_destroy(self.exec)
+        self.dev.b.hip_graph_destroy(self.graph)
