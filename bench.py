@@ -392,6 +392,37 @@ def bench_gemv(dev):
 
 
 # ---------------------------------------------------------------------------------------
+# Full decode step (34-layer Gemma-4B-shaped Q4_0 model, graph replay per token)
+# ---------------------------------------------------------------------------------------
+
+def bench_decode_step(dev, n_layers=34, pos0=1234, n_tokens=32):
+    from ziglm_amd.decode import DecodeModel
+    m = DecodeModel(dev, LY.GEMMA_4B, n_layers=n_layers, vocab=262144, max_seq=4096)
+    try:
+        m.set_token(2)
+        m.capture()
+        m.run(pos0 - 8, 8)  # warm-up; fills 8 cache rows
+        e0, e1 = dev.event(), dev.event()
+        dev.record(e0)
+        m.run(pos0, n_tokens)
+        dev.record(e1)
+        ms = dev.elapsed_ms(e0, e1)
+        s = LY.GEMMA_4B
+        H, I, qn, kn = s.H, s.I, s.nh * s.D, s.nkv * s.D
+        wbytes = n_layers * (qn + 2 * kn + 2 * I) * (H // 32 * 18) + n_layers * H * (qn // 32 * 18) \
+            + n_layers * H * (I // 32 * 18) + 262144 * (H // 32 * 18)
+        us = ms * 1000.0 / n_tokens
+        out = {"layers": n_layers, "pos": f"{pos0}..{pos0 + n_tokens - 1}", "us_per_token": round(us, 1),
+               "tokens_per_s": round(1e6 / us, 1), "us_per_layer": round(us / n_layers, 2),
+               "weight_bytes": wbytes, "weight_GBps": round(wbytes / us / 1e3, 1),
+               "note": "one hipGraph replay per token; Q4_0 weights, f32 activations, token fed back on device"}
+        log(f"  decode step: {us:.1f} us/token ({1e6 / us:.0f} tok/s), {us / n_layers:.2f} us/layer")
+        return out
+    finally:
+        m.free()
+
+
+# ---------------------------------------------------------------------------------------
 # CPU baseline (oracle, -O3 -march=x86-64-v3, one thread)
 # ---------------------------------------------------------------------------------------
 
@@ -511,6 +542,9 @@ def main():
     if a.only:
         if a.only.startswith("gather_"):
             fn, sets, traffic, _ = gather_case(dev, a.only[len("gather_"):])
+        elif a.only == "decode_step":
+            print(json.dumps(bench_decode_step(dev)))
+            return
         elif a.only == "gemv":
             log("gemv (decode projections)")
             print(json.dumps(bench_gemv(dev)))
@@ -593,6 +627,8 @@ def main():
         cfgs["c4_prefill"]["chain_GBps"] = round(cfgs["c4_prefill"]["chain_GBps"], 1)
         log("gemv (decode projections)")
         cfgs["gemv_decode"] = bench_gemv(dev)
+        log("decode step (34 layers, graph)")
+        cfgs["decode_step"] = bench_decode_step(dev)
         log("c1/c5 decode")
         cfgs["c5_decode"] = {}
         for b_ in (1, 8, 64, 256):

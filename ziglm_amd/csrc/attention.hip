@@ -110,38 +110,37 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
 
     const KT* kbase = (const KT*)a.kc + kvh * D + li * 8;
     const KT* vbase = (const KT*)a.vc + kvh * D + li * 8;
-    // Double-buffered: the next position's K/V rows are in flight during this one's math.
-    float kn[8], vn[8];
-    int t = t0 + slot;
-    if (t < t1) {
-        load8<KT>(kbase + (rb + t) * a.row_stride, kn);
-        load8<KT>(vbase + (rb + t) * a.row_stride, vn);
-    }
-    for (; t < t1; t += SLOTS) {
-        float k[8], v[8];
+    // Each lane group takes U positions per step (t, t + SLOTS, ...), all 2U row loads issued
+    // before any math, then folds them into its online softmax state in position order.
+    constexpr int U = 4;
+    for (int t = t0 + slot; t < t1; t += U * SLOTS) {
+        float k[U][8], v[U][8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            k[e] = kn[e];
-            v[e] = vn[e];
-        }
-        if (t + SLOTS < t1) {
-            load8<KT>(kbase + (rb + t + SLOTS) * a.row_stride, kn);
-            load8<KT>(vbase + (rb + t + SLOTS) * a.row_stride, vn);
+        for (int u = 0; u < U; ++u) {
+            const int tu = t + u * SLOTS;
+            if (tu < t1) {
+                load8<KT>(kbase + (rb + tu) * a.row_stride, k[u]);
+                load8<KT>(vbase + (rb + tu) * a.row_stride, v[u]);
+            }
         }
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            float s = 0.0f;
+        for (int u = 0; u < U; ++u) {
+            if (t + u * SLOTS >= t1) break;  // uniform within a lane group
 #pragma unroll
-            for (int e = 0; e < 8; ++e) s = fmaf(q[g][e], k[e], s);
-            s = group_sum<LT>(s) * a.scale;
-            if (a.softcap > 0.0f) s = a.softcap * tanh_fast(div_by_uniform(s, a.softcap, a.inv_cap));
-            const float mn = fmaxf(m[g], s);
-            const float c = exp2f((m[g] - mn) * kLog2e);
-            const float p = exp2f((s - mn) * kLog2e);
-            l[g] = l[g] * c + p;
+            for (int g = 0; g < G; ++g) {
+                float s = 0.0f;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(p, v[e], acc[g][e] * c);
-            m[g] = mn;
+                for (int e = 0; e < 8; ++e) s = fmaf(q[g][e], k[u][e], s);
+                s = group_sum<LT>(s) * a.scale;
+                if (a.softcap > 0.0f) s = a.softcap * tanh_fast(div_by_uniform(s, a.softcap, a.inv_cap));
+                const float mn = fmaxf(m[g], s);
+                const float c = exp2f((m[g] - mn) * kLog2e);
+                const float p = exp2f((s - mn) * kLog2e);
+                l[g] = l[g] * c + p;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(p, v[u][e], acc[g][e] * c);
+                m[g] = mn;
+            }
         }
     }
 
@@ -233,13 +232,14 @@ static void launch_g(const AttnArgs& a, int G, hipStream_t s) {
 
 // Positions per split: enough splits that batch * n_kv_heads * splits fills the chip
 // (~2048 workgroups) and no split exceeds 1024 positions (sequences of a batch differ in
-// length: short splits keep the long ones from leaving a tail), at least 128 positions
-// each, at most kMaxSplit splits.
+// length: short splits keep the long ones from leaving a tail), at least 64 positions each
+// (the actual lengths are on the device: a short context still spreads over several
+// workgroups), at most kMaxSplit splits.
 static void choose_split(AttnArgs& a, size_t ws_bytes) {
     const int len = a.window > 0 ? std::min(a.window, a.max_len) : a.max_len;
     const int64_t groups = (int64_t)a.batch * a.nkv;
     const int64_t want = std::max<int64_t>(cdiv(2048, groups), cdiv(len, 1024));
-    int nsplit = (int)std::max<int64_t>(1, std::min<int64_t>({cdiv(len, 128), want, (int64_t)kMaxSplit}));
+    int nsplit = (int)std::max<int64_t>(1, std::min<int64_t>({cdiv(len, 64), want, (int64_t)kMaxSplit}));
     const size_t need = (size_t)a.batch * a.nh * nsplit * (a.D + 2) * sizeof(float);
     if (!a.ws || need > ws_bytes) nsplit = 1;
     a.nsplit = nsplit;
