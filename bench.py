@@ -397,7 +397,7 @@ def bench_gemv(dev):
 
 def bench_decode_step(dev, n_layers=34, pos0=1234, n_tokens=32):
     from ziglm_amd.decode import DecodeModel
-    m = DecodeModel(dev, LY.GEMMA_4B, n_layers=n_layers, vocab=262144, max_seq=4096)
+    m = DecodeModel.synthetic(dev, LY.GEMMA_4B, n_layers=n_layers, vocab=262144, max_seq=4096)
     try:
         m.set_token(2)
         m.capture()
@@ -420,6 +420,61 @@ def bench_decode_step(dev, n_layers=34, pos0=1234, n_tokens=32):
         return out
     finally:
         m.free()
+
+
+# ---------------------------------------------------------------------------------------
+# GGUF file -> device tables -> graph decode (gemma-4-E2B-shaped synthetic file)
+# ---------------------------------------------------------------------------------------
+
+def bench_gguf_decode(dev, pos0=1234, n_tokens=64, path=None):
+    """Write the synthetic E2B-shaped Q4_0 GGUF (ziglm_amd/synth_gguf.py), open it (mmap),
+    load it into device tables (timed: the pinned-ring upload and norm conversion), then
+    time graph-replayed greedy decode steps at positions pos0.. (tokens/s)."""
+    import tempfile
+    from ziglm_amd import gguf as G
+    from ziglm_amd import synth_gguf as S
+    from ziglm_amd.decode import DecodeModel
+    from ziglm_amd.model import Model
+    cfg = S.E2B
+    t0 = time.time()
+    tmp = path or os.path.join(tempfile.gettempdir(), f"ziglm_amd_e2b_{os.getpid()}.gguf")
+    S.build(cfg).write(tmp)
+    t_write = time.time() - t0
+    try:
+        with G.GGUFFile.open(tmp) as f:
+            file_bytes = f.size
+            dev.sync()
+            t1 = time.time()
+            model = Model.from_gguf(dev, f)
+            t_load = time.time() - t1
+        dm = DecodeModel(dev, model, max_seq=4096, own_model=True)
+    finally:
+        if path is None:
+            os.unlink(tmp)
+    try:
+        dm.reset(2)
+        dm.capture()
+        dm.run(pos0 - 8, 8)  # warm-up
+        e0, e1 = dev.event(), dev.event()
+        dev.record(e0)
+        dm.run(pos0, n_tokens)
+        dev.record(e1)
+        us = dev.elapsed_ms(e0, e1) * 1000.0 / n_tokens
+        wb = S.weight_bytes(cfg)
+        out = {"model": "gemma-4-E2B-shaped synthetic GGUF (q4_0; 35 layers, 1536 hidden, 8/1 heads x 256|512, "
+                        "FFN 6144, PLE 35x256, 15 unshared KV layers)",
+               "file_bytes": file_bytes, "write_s": round(t_write, 2), "load_s": round(t_load, 3),
+               "load_GBps": round(file_bytes / t_load / 1e9, 2),
+               "pos": f"{pos0}..{pos0 + n_tokens - 1}", "us_per_token": round(us, 1),
+               "tokens_per_s": round(1e6 / us, 1), "weight_bytes_per_token": wb,
+               "weight_GBps": round(wb / us / 1e3, 1),
+               "reference_published": "101.0 tok/s generation, gemma-4-E2B q4_0, Quadro RTX 3000 "
+                                      "(benchmarks/benchmark_final.md:14; other hardware, real weights)"}
+        log(f"  gguf decode: load {t_load:.2f} s ({file_bytes / t_load / 1e9:.1f} GB/s), "
+            f"{us:.1f} us/token ({1e6 / us:.0f} tok/s, {wb / us / 1e3:.0f} GB/s of weights)")
+        return out
+    finally:
+        dm.free()
 
 
 # ---------------------------------------------------------------------------------------
@@ -523,8 +578,8 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline config only")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default=None, help="run one op only (profiling): a chain op, "
-                    "gather_q8_0 / gather_q4_0 / gather_bf16 (c3), or 'copy' = hipMemcpy "
-                    "device-to-device of the GeGLU output size (counter calibration)")
+                    "gather_q8_0 / gather_q4_0 / gather_bf16 (c3), gemv, decode_step, gguf_decode, "
+                    "or 'copy' = hipMemcpy device-to-device of the GeGLU output size (counter calibration)")
     ap.add_argument("--eager", action="store_true", help="with --only: launch eagerly, no graph")
     ap.add_argument("--config", default="c2", choices=["c2", "c4"])
     a = ap.parse_args()
@@ -544,6 +599,9 @@ def main():
             fn, sets, traffic, _ = gather_case(dev, a.only[len("gather_"):])
         elif a.only == "decode_step":
             print(json.dumps(bench_decode_step(dev)))
+            return
+        elif a.only == "gguf_decode":
+            print(json.dumps(bench_gguf_decode(dev)))
             return
         elif a.only == "gemv":
             log("gemv (decode projections)")
@@ -629,6 +687,8 @@ def main():
         cfgs["gemv_decode"] = bench_gemv(dev)
         log("decode step (34 layers, graph)")
         cfgs["decode_step"] = bench_decode_step(dev)
+        log("GGUF load + E2B-shaped decode")
+        cfgs["gguf_e2b_decode"] = bench_gguf_decode(dev)
         log("c1/c5 decode")
         cfgs["c5_decode"] = {}
         for b_ in (1, 8, 64, 256):

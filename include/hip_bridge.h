@@ -241,7 +241,8 @@ void hip_gemm(int qtype, const void* weights, const float* x, float* y, int batc
 /* Query token b at position p attends to positions [max(0, p+1-window), p] (window 0: */
 /* all): score = (q_h . k_t) * attn_scale, softcap * tanh(score / softcap) when         */
 /* softcap > 0, softmax, out_h = sum_t w_t v_t; kv head of query head h is              */
-/* h / (n_heads / n_kv_heads) (1, 2 or 4 query heads per kv head; head_dim 64/128/256). */
+/* h / (n_heads / n_kv_heads) (1, 2, 4 or 8 query heads per kv head;                    */
+/* head_dim 64, 128, 256 or 512).                                                       */
 /* Key of (position t, kv head j) at k_cache[(row0 + t) * row_stride + j * head_dim].   */
 /* ---------------------------------------------------------------------------------- */
 /* reference layout, f32 cache: row0 = donor_layer * max_seq, row_stride = max_kv_dim */

@@ -1,22 +1,28 @@
 """CPU-side checks of the C-ABI boundary (no GPU needed, no compute calls):
-every function declared in include/*.h is exported by libhip_bridge.so, the ctypes binding
-covers exactly those functions, and the library loads without initialising a device."""
+every function declared in include/*.h is exported by libhip_bridge.so, the ctypes bindings
+(ziglm_amd/bridge.py for hip_bridge.h, ziglm_amd/gguf.py for zl_gguf.h) cover exactly those
+functions, and the library loads without initialising a device."""
 import os
 import re
 import subprocess
 
 import pytest
 
-from ziglm_amd import bridge
+from ziglm_amd import bridge, gguf
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HDR = os.path.join(ROOT, "include", "hip_bridge.h")
+HEADERS = {"hip_bridge.h": "hip_", "zl_gguf.h": "zl_"}
 
 
-def declared_functions():
-    text = open(HDR).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(hip_\w+)\s*\(", text)))
+def declared_functions(header=None):
+    names = set()
+    for h, prefix in HEADERS.items():
+        if header and h != header:
+            continue
+        text = open(os.path.join(ROOT, "include", h)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names |= set(re.findall(r"\b(" + prefix + r"\w+)\s*\(", text))
+    return sorted(names)
 
 
 def test_header_parses():
@@ -30,13 +36,15 @@ def test_library_exports_every_declared_symbol():
         pytest.fail("libhip_bridge.so is not built (run __graft_entry__.build())")
     out = subprocess.run(["nm", "-D", "--defined-only", bridge.LIB_PATH], capture_output=True,
                          text=True, check=True).stdout
-    exported = set(re.findall(r"\bT (hip_\w+)$", out, flags=re.M))
+    exported = set(re.findall(r"\bT ((?:hip|zl)_\w+)$", out, flags=re.M))
     missing = [n for n in declared_functions() if n not in exported]
     assert not missing, f"declared but not exported: {missing}"
 
 
 def test_binding_matches_header():
-    assert sorted(bridge.SIGNATURES) == declared_functions()
+    assert sorted(bridge.SIGNATURES) == declared_functions("hip_bridge.h")
+    assert sorted(gguf.SIGNATURES) == declared_functions("zl_gguf.h")
+    gguf.lib()  # binds every zl_ symbol
 
 
 def test_library_loads_and_binds():

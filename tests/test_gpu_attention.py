@@ -1,7 +1,7 @@
 """Decode attention on the GPU (model.zig:658-700) against float64 with the f32 bound of
 attn_ref.py, and against the oracle's CPU restatement with twice that bound.
 
-Covers: head sizes 64/128/256, 1/2/4 query heads per kv head, soft-cap, sliding window,
+Covers: head sizes 64/128/256/512, 1/2/4/8 query heads per kv head, soft-cap, sliding window,
 f32 and bf16 caches, per-token positions and per-sequence cache rows (positions up to 32767),
 the split-over-positions path (workspace) and the unsplit one, the reference-ABI mirrors
 (single token, device position, causal chunk), and tokens whose cache rows are out of range
@@ -28,7 +28,8 @@ def check(got, q, kc_f32, vc_f32, row0, pos, nh, nkv, d, scale, softcap, window,
 
 
 @pytest.mark.parametrize("kv_dtype", [B.F32, B.BF16])
-@pytest.mark.parametrize("nh,nkv,d", [(8, 4, 256), (4, 4, 128), (8, 2, 64), (16, 4, 128)])
+@pytest.mark.parametrize("nh,nkv,d", [(8, 4, 256), (4, 4, 128), (8, 2, 64), (16, 4, 128), (8, 1, 256), (8, 1, 512),
+                                      (4, 2, 512)])
 @pytest.mark.parametrize("softcap,window", [(0.0, 0), (50.0, 0), (0.0, 300)])
 @pytest.mark.parametrize("split", [False, True])
 def test_attention_decode_per_sequence(dev, oracle, kv_dtype, nh, nkv, d, softcap, window, split):
@@ -126,12 +127,14 @@ def test_attention_out_of_range_rows_give_zeros(dev):
 
 def test_attention_unsupported_group_is_noop(dev):
     d_buf = dev.alloc(1 << 16)
-    d_out = dev.alloc(16 * 64 * 4)
+    d_out = dev.alloc(32 * 64 * 4)
     d_out.fill(0x11)
     dev.strict = False
     try:
-        dev.attentionForward(d_buf, d_buf, d_buf, d_out, 0, 3, 16, 16, 2, 64, 128, 1.0, 0.0, 0)  # 8 q per kv head
+        dev.attentionForward(d_buf, d_buf, d_buf, d_out, 0, 3, 16, 32, 2, 64, 128, 1.0, 0.0, 0)  # 16 q per kv head
+        assert dev.b.last_error() == B.EUNSUPPORTED
+        dev.attentionForward(d_buf, d_buf, d_buf, d_out, 0, 3, 16, 4, 2, 96, 192, 1.0, 0.0, 0)   # head_dim 96
         assert dev.b.last_error() == B.EUNSUPPORTED
     finally:
         dev.strict = True
-    assert np.all(d_out.to_numpy((16 * 64 * 4,), np.uint8) == 0x11)
+    assert np.all(d_out.to_numpy((32 * 64 * 4,), np.uint8) == 0x11)

@@ -72,7 +72,7 @@ def reset(m, token):
 
 def test_decode_graph_equals_eager(dev):
     """The captured step replays the eager step bit for bit, token fed back on the device."""
-    m = DecodeModel(dev, GEMMA_4B, n_layers=2, vocab=4096, max_seq=64)
+    m = DecodeModel.synthetic(dev, GEMMA_4B, n_layers=2, vocab=4096, max_seq=64)
     try:
         reset(m, 5)
         eager = []
@@ -101,7 +101,7 @@ def test_decode_step_vs_oracle(dev, oracle):
     sums differ in order), and the greedy token equal wherever the top-2 gap exceeds that."""
     s = GEMMA_4B
     L, V, max_seq, tok0 = 2, 4096, 16, 7
-    m = DecodeModel(dev, s, n_layers=L, vocab=V, max_seq=max_seq, host_weights=True)
+    m = DecodeModel.synthetic(dev, s, n_layers=L, vocab=V, max_seq=max_seq, host_weights=True)
     try:
         reset(m, tok0)
         h, eps = m.host, np.float32(s.eps)

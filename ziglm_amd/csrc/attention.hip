@@ -74,9 +74,11 @@ template <typename KT, int D, int G>
 __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
     constexpr int LT = D / 8;                  // lanes per position
     constexpr int SLOTS = kAttnThreads / LT;   // positions in flight per workgroup
-    // Per-slot states for the merge: m, l per query head, a per (head, element).
-    __shared__ float s_m[SLOTS][G], s_l[SLOTS][G];
-    __shared__ float s_a[SLOTS][G][D];
+    constexpr int GM = G < 4 ? G : 4;          // query heads merged per LDS pass
+    // Per-slot states for the merge: m, l per query head, a per (head, element); the G heads
+    // go through in passes of GM (LDS = SLOTS * GM * D * 4 <= 32 KB for every D).
+    __shared__ float s_m[SLOTS][GM], s_l[SLOTS][GM];
+    __shared__ float s_a[SLOTS][GM][D];
     const int tid = threadIdx.x;
     const int slot = tid / LT;
     const int li = tid % LT;                   // 8-element slice of the head row
@@ -147,36 +149,40 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
     // Merge the SLOTS states: every slot stores its state, then thread i merges element
     // (g, e) = i over the slots in slot order, rescaling each by exp(m_slot - max).
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        if (li == 0) {
-            s_m[slot][g] = m[g];
-            s_l[slot][g] = l[g];
-        }
+    for (int g0 = 0; g0 < G; g0 += GM) {
+        if (g0 > 0) __syncthreads();  // the previous pass has read the buffers
 #pragma unroll
-        for (int e = 0; e < 8; ++e) s_a[slot][g][li * 8 + e] = acc[g][e];
-    }
-    __syncthreads();
-    for (int i = tid; i < G * D; i += kAttnThreads) {
-        const int g = i / D, e = i % D;
-        float M = -INFINITY;
-        for (int s = 0; s < SLOTS; ++s) M = fmaxf(M, s_m[s][g]);
-        float L = 0.0f, A = 0.0f;
-        if (M != -INFINITY) {
-            for (int s = 0; s < SLOTS; ++s) {
-                const float c = exp2f((s_m[s][g] - M) * kLog2e);
-                L = fmaf(s_l[s][g], c, L);
-                A = fmaf(s_a[s][g][e], c, A);
+        for (int g = 0; g < GM; ++g) {
+            if (li == 0) {
+                s_m[slot][g] = m[g0 + g];
+                s_l[slot][g] = l[g0 + g];
             }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) s_a[slot][g][li * 8 + e] = acc[g0 + g][e];
         }
-        const int h = kvh * G + g;
-        if (a.nsplit == 1) {
-            a.out[((int64_t)b * a.nh + h) * D + e] = L > 0.0f ? A / L : 0.0f;
-        } else {
-            float* w = a.ws + (((int64_t)b * a.nh + h) * a.nsplit + split) * (D + 2);
-            w[2 + e] = A;
-            if (e == 0) {
-                w[0] = M;
-                w[1] = L;
+        __syncthreads();
+        for (int i = tid; i < GM * D; i += kAttnThreads) {
+            const int g = i / D, e = i % D;
+            float M = -INFINITY;
+            for (int s = 0; s < SLOTS; ++s) M = fmaxf(M, s_m[s][g]);
+            float L = 0.0f, A = 0.0f;
+            if (M != -INFINITY) {
+                for (int s = 0; s < SLOTS; ++s) {
+                    const float c = exp2f((s_m[s][g] - M) * kLog2e);
+                    L = fmaf(s_l[s][g], c, L);
+                    A = fmaf(s_a[s][g][e], c, A);
+                }
+            }
+            const int h = kvh * G + g0 + g;
+            if (a.nsplit == 1) {
+                a.out[((int64_t)b * a.nh + h) * D + e] = L > 0.0f ? A / L : 0.0f;
+            } else {
+                float* w = a.ws + (((int64_t)b * a.nh + h) * a.nsplit + split) * (D + 2);
+                w[2 + e] = A;
+                if (e == 0) {
+                    w[0] = M;
+                    w[1] = L;
+                }
             }
         }
     }
@@ -226,7 +232,8 @@ static void launch_g(const AttnArgs& a, int G, hipStream_t s) {
     switch (G) {
         case 1: k_attn<KT, D, 1><<<grid, kAttnThreads, 0, s>>>(a); break;
         case 2: k_attn<KT, D, 2><<<grid, kAttnThreads, 0, s>>>(a); break;
-        default: k_attn<KT, D, 4><<<grid, kAttnThreads, 0, s>>>(a); break;
+        case 4: k_attn<KT, D, 4><<<grid, kAttnThreads, 0, s>>>(a); break;
+        default: k_attn<KT, D, 8><<<grid, kAttnThreads, 0, s>>>(a); break;
     }
 }
 
@@ -253,9 +260,8 @@ static void launch_attn(int kv_dtype, AttnArgs& a, size_t ws_bytes, hipStream_t 
         set_error(HIP_BRIDGE_EINVAL);
         return;
     }
-    // G <= 4: the merge buffer is 8 KB per query head of the group (static LDS <= 64 KB)
-    const bool shapes = (a.D == 64 || a.D == 128 || a.D == 256) && (G == 1 || G == 2 || G == 4) &&
-                        (int64_t)a.nkv * a.D <= a.row_stride;
+    const bool shapes = (a.D == 64 || a.D == 128 || a.D == 256 || a.D == 512) &&
+                        (G == 1 || G == 2 || G == 4 || G == 8) && (int64_t)a.nkv * a.D <= a.row_stride;
     const int es = kv_dtype == HIP_BRIDGE_BF16 ? 2 : 4;
     const bool aligned = aligned16(a.q) && aligned16(a.kc) && aligned16(a.vc) && (a.row_stride * es) % 16 == 0;
     if ((kv_dtype != HIP_BRIDGE_F32 && kv_dtype != HIP_BRIDGE_BF16) || !shapes || !aligned) {
@@ -271,11 +277,13 @@ static void launch_attn(int kv_dtype, AttnArgs& a, size_t ws_bytes, hipStream_t 
     if (kv_dtype == HIP_BRIDGE_F32) {
         if (a.D == 64) launch_g<float, 64>(a, G, s);
         else if (a.D == 128) launch_g<float, 128>(a, G, s);
-        else launch_g<float, 256>(a, G, s);
+        else if (a.D == 256) launch_g<float, 256>(a, G, s);
+        else launch_g<float, 512>(a, G, s);
     } else {
         if (a.D == 64) launch_g<uint16_t, 64>(a, G, s);
         else if (a.D == 128) launch_g<uint16_t, 128>(a, G, s);
-        else launch_g<uint16_t, 256>(a, G, s);
+        else if (a.D == 256) launch_g<uint16_t, 256>(a, G, s);
+        else launch_g<uint16_t, 512>(a, G, s);
     }
     if (a.nsplit > 1) k_attn_merge<<<(unsigned)((int64_t)a.batch * a.nh), kAttnThreads, 0, s>>>(a);
     check_launch();
