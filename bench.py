@@ -426,10 +426,11 @@ def bench_decode_step(dev, n_layers=34, pos0=1234, n_tokens=32):
 # GGUF file -> device tables -> graph decode (gemma-4-E2B-shaped synthetic file)
 # ---------------------------------------------------------------------------------------
 
-def bench_gguf_decode(dev, pos0=1234, n_tokens=64, path=None):
+def bench_gguf_decode(dev, pos0=1234, n_tokens=64, path=None, graph=True):
     """Write the synthetic E2B-shaped Q4_0 GGUF (ziglm_amd/synth_gguf.py), open it (mmap),
     load it into device tables (timed: the pinned-ring upload and norm conversion), then
-    time graph-replayed greedy decode steps at positions pos0.. (tokens/s)."""
+    time graph-replayed greedy decode steps at positions pos0.. (tokens/s). graph=False
+    launches every step eagerly (for kernel traces; the time then includes host gaps)."""
     import tempfile
     from ziglm_amd import gguf as G
     from ziglm_amd import synth_gguf as S
@@ -453,12 +454,20 @@ def bench_gguf_decode(dev, pos0=1234, n_tokens=64, path=None):
             os.unlink(tmp)
     try:
         dm.reset(2)
-        dm.capture()
-        dm.run(pos0 - 8, 8)  # warm-up
         e0, e1 = dev.event(), dev.event()
-        dev.record(e0)
-        dm.run(pos0, n_tokens)
-        dev.record(e1)
+        if graph:
+            dm.capture()
+            dm.run(pos0 - 8, 8)  # warm-up
+            dev.record(e0)
+            dm.run(pos0, n_tokens)
+            dev.record(e1)
+        else:
+            for p in range(pos0 - 8, pos0):
+                dm.step(p, graph=False)
+            dev.record(e0)
+            for p in range(pos0, pos0 + n_tokens):
+                dm.step(p, graph=False)
+            dev.record(e1)
         us = dev.elapsed_ms(e0, e1) * 1000.0 / n_tokens
         wb = S.weight_bytes(cfg)
         out = {"model": "gemma-4-E2B-shaped synthetic GGUF (q4_0; 35 layers, 1536 hidden, 8/1 heads x 256|512, "
@@ -601,7 +610,7 @@ def main():
             print(json.dumps(bench_decode_step(dev)))
             return
         elif a.only == "gguf_decode":
-            print(json.dumps(bench_gguf_decode(dev)))
+            print(json.dumps(bench_gguf_decode(dev, graph=not a.eager)))
             return
         elif a.only == "gemv":
             log("gemv (decode projections)")

@@ -295,6 +295,8 @@ void hip_tanh_softcap(float* x, float cap, int n, HipStream_t stream);          
 void hip_geglu_ex(int dtype, const void* gate, const void* up, void* out, int64_t n,
                   HipStream_t stream);
 void hip_tanh_softcap_ex(int dtype, void* x, float cap, int64_t n, HipStream_t stream);
+/* new: out[i] = x[i] * scale (x == out allowed; scale 1 copies exactly). */
+void hip_scale_ex(int dtype, const void* x, float scale, void* out, int64_t n, HipStream_t stream);
 
 #ifdef __cplusplus
 }

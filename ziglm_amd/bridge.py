@@ -107,6 +107,7 @@ SIGNATURES = {
                                     _f, _f, _i, _v, _sz, _v]),
     "hip_geglu_ex": (None, [_i, _v, _v, _v, _i64, _v]),
     "hip_tanh_softcap_ex": (None, [_i, _v, _f, _i64, _v]),
+    "hip_scale_ex": (None, [_i, _v, _f, _v, _i64, _v]),
 }
 
 

@@ -7,11 +7,12 @@
 // cap * tanh(score / cap) when cap > 0, softmax over t, out_h = sum_t w_t v_t; query head h
 // reads kv head h / (n_heads / n_kv_heads).
 //
-// Layout (flash-decoding). One workgroup per (token b, kv head, split s) covers `chunk`
-// consecutive positions. Lanes come in groups of LT = D/8 (8 elements of a head row per
-// lane), one group per position, so a wave works on 64/LT positions at a time and the K/V row
-// loads of a position are one contiguous span; all G = n_heads/n_kv_heads query heads of the
-// kv head reuse each loaded K and V row. Each lane group keeps an online softmax state per
+// Layout (flash-decoding). One workgroup per (token b, kv head, head group, split s) covers
+// `chunk` consecutive positions for G query heads of the kv head (G = n_heads/n_kv_heads, or
+// a fraction of it when there are few kv-head groups, choose_heads). Lanes come in groups of
+// LT = D/8 (8 elements of a head row per lane), one group per position, so a wave works on
+// 64/LT positions at a time and the K/V row loads of a position are one contiguous span; the
+// workgroup's G query heads reuse each loaded K and V row. Each lane group keeps an online softmax state per
 // query head (running max m, sum l, accumulator a = sum exp(s - m) v); the groups and waves
 // are merged through LDS. With one split the workgroup writes out = a / l; otherwise it
 // writes (m, l, a) to the caller's workspace and a second kernel merges the splits.
@@ -44,6 +45,8 @@ struct AttnArgs {
     int batch, nh, nkv, D;
     int window;
     int nsplit, chunk;
+    int gq;                   // query heads per kv head (nh / nkv)
+    int hg;                   // workgroups per (token, kv head, split): each takes gq / hg heads
     float scale, softcap, inv_cap;
 };
 
@@ -83,9 +86,12 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
     const int slot = tid / LT;
     const int li = tid % LT;                   // 8-element slice of the head row
     const int split = blockIdx.x % a.nsplit;
-    const int bk = blockIdx.x / a.nsplit;
+    const int r = blockIdx.x / a.nsplit;
+    const int hgi = r % a.hg;
+    const int bk = r / a.hg;
     const int kvh = bk % a.nkv;
     const int b = bk / a.nkv;
+    const int h0 = kvh * a.gq + hgi * G;       // first query head of this workgroup
 
     int start, end;
     int64_t rb;
@@ -96,7 +102,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
     float q[G][8];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-        const float* qh = a.q + ((int64_t)b * a.nh + kvh * G + g) * D + li * 8;
+        const float* qh = a.q + ((int64_t)b * a.nh + h0 + g) * D + li * 8;
         const f32x4 x = ldf4(qh), y = ldf4(qh + 4);
         q[g][0] = x.x; q[g][1] = x.y; q[g][2] = x.z; q[g][3] = x.w;
         q[g][4] = y.x; q[g][5] = y.y; q[g][6] = y.z; q[g][7] = y.w;
@@ -173,7 +179,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
                     A = fmaf(s_a[s][g][e], c, A);
                 }
             }
-            const int h = kvh * G + g0 + g;
+            const int h = h0 + g0 + g;
             if (a.nsplit == 1) {
                 a.out[((int64_t)b * a.nh + h) * D + e] = L > 0.0f ? A / L : 0.0f;
             } else {
@@ -227,9 +233,9 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_merge(AttnArgs a) {
 }
 
 template <typename KT, int D>
-static void launch_g(const AttnArgs& a, int G, hipStream_t s) {
-    const unsigned grid = (unsigned)((int64_t)a.batch * a.nkv * a.nsplit);
-    switch (G) {
+static void launch_g(const AttnArgs& a, hipStream_t s) {
+    const unsigned grid = (unsigned)((int64_t)a.batch * a.nkv * a.hg * a.nsplit);
+    switch (a.gq / a.hg) {
         case 1: k_attn<KT, D, 1><<<grid, kAttnThreads, 0, s>>>(a); break;
         case 2: k_attn<KT, D, 2><<<grid, kAttnThreads, 0, s>>>(a); break;
         case 4: k_attn<KT, D, 4><<<grid, kAttnThreads, 0, s>>>(a); break;
@@ -237,14 +243,34 @@ static void launch_g(const AttnArgs& a, int G, hipStream_t s) {
     }
 }
 
-// Positions per split: enough splits that batch * n_kv_heads * splits fills the chip
-// (~2048 workgroups) and no split exceeds 1024 positions (sequences of a batch differ in
-// length: short splits keep the long ones from leaving a tail), at least 64 positions each
-// (the actual lengths are on the device: a short context still spreads over several
-// workgroups), at most kMaxSplit splits.
+// Query heads per workgroup. Each workgroup loads its positions' K/V rows once for all the
+// heads it takes, so with many (token, kv head) groups every workgroup takes all gq heads
+// of its kv head (fewest K/V reads); with few groups (single-token decode over a few kv
+// heads) every workgroup takes one head: the heads re-read the same rows (from L2 at
+// decode sizes) but each workgroup's serial chain is gq times shorter. Measured on MI355X,
+// one token at position 1234 (us per call, with the merge; 1 / 2 / 4 / 8 heads per
+// workgroup): 8/1 heads x 256, window 512: 7.4 / 8.8 / 11.7 / 18.1; 8/1 x 512, full
+// context: 16.7 / 18.2 / 24.2 / 35.8; 8/4 x 256: 7.4 / 8.8 (2 heads = all).
+#ifndef ZL_ATTN_GW
+#define ZL_ATTN_GW 0
+#endif
+constexpr int64_t kFewGroups = 16;
+static void choose_heads(AttnArgs& a) {
+    a.gq = a.nh / a.nkv;
+    int gw = a.gq;
+    if (ZL_ATTN_GW > 0) gw = std::min(a.gq, ZL_ATTN_GW);
+    else if ((int64_t)a.batch * a.nkv < kFewGroups) gw = 1;
+    a.hg = a.gq / gw;
+}
+
+// Positions per split: enough splits that batch * n_kv_heads * head groups * splits fills
+// the chip (~2048 workgroups) and no split exceeds 1024 positions (sequences of a batch
+// differ in length: short splits keep the long ones from leaving a tail), at least 64
+// positions each (the actual lengths are on the device: a short context still spreads over
+// several workgroups), at most kMaxSplit splits.
 static void choose_split(AttnArgs& a, size_t ws_bytes) {
     const int len = a.window > 0 ? std::min(a.window, a.max_len) : a.max_len;
-    const int64_t groups = (int64_t)a.batch * a.nkv;
+    const int64_t groups = (int64_t)a.batch * a.nkv * a.hg;
     const int64_t want = std::max<int64_t>(cdiv(2048, groups), cdiv(len, 1024));
     int nsplit = (int)std::max<int64_t>(1, std::min<int64_t>({cdiv(len, 64), want, (int64_t)kMaxSplit}));
     const size_t need = (size_t)a.batch * a.nh * nsplit * (a.D + 2) * sizeof(float);
@@ -269,21 +295,22 @@ static void launch_attn(int kv_dtype, AttnArgs& a, size_t ws_bytes, hipStream_t 
         return;
     }
     a.inv_cap = a.softcap > 0.0f ? 1.0f / a.softcap : 0.0f;
+    choose_heads(a);
     choose_split(a, ws_bytes);
-    if ((int64_t)a.batch * a.nkv * a.nsplit > INT32_MAX) {
+    if ((int64_t)a.batch * a.nkv * a.hg * a.nsplit > INT32_MAX) {
         set_error(HIP_BRIDGE_EUNSUPPORTED);
         return;
     }
     if (kv_dtype == HIP_BRIDGE_F32) {
-        if (a.D == 64) launch_g<float, 64>(a, G, s);
-        else if (a.D == 128) launch_g<float, 128>(a, G, s);
-        else if (a.D == 256) launch_g<float, 256>(a, G, s);
-        else launch_g<float, 512>(a, G, s);
+        if (a.D == 64) launch_g<float, 64>(a, s);
+        else if (a.D == 128) launch_g<float, 128>(a, s);
+        else if (a.D == 256) launch_g<float, 256>(a, s);
+        else launch_g<float, 512>(a, s);
     } else {
-        if (a.D == 64) launch_g<uint16_t, 64>(a, G, s);
-        else if (a.D == 128) launch_g<uint16_t, 128>(a, G, s);
-        else if (a.D == 256) launch_g<uint16_t, 256>(a, G, s);
-        else launch_g<uint16_t, 512>(a, G, s);
+        if (a.D == 64) launch_g<uint16_t, 64>(a, s);
+        else if (a.D == 128) launch_g<uint16_t, 128>(a, s);
+        else if (a.D == 256) launch_g<uint16_t, 256>(a, s);
+        else launch_g<uint16_t, 512>(a, s);
     }
     if (a.nsplit > 1) k_attn_merge<<<(unsigned)((int64_t)a.batch * a.nh), kAttnThreads, 0, s>>>(a);
     check_launch();
@@ -322,6 +349,8 @@ size_t hip_attention_workspace_bytes(int batch, int n_heads, int n_kv_heads, int
     a.max_len = max_len;
     a.window = sliding_window;
     a.ws = reinterpret_cast<float*>(16);  // any non-null pointer: size for the unconstrained split
+    if (n_heads % n_kv_heads != 0) return 0;
+    choose_heads(a);
     choose_split(a, SIZE_MAX);
     return a.nsplit > 1 ? (size_t)batch * n_heads * a.nsplit * (head_dim + 2) * sizeof(float) : 0;
 }

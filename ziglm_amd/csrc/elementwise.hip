@@ -1,5 +1,6 @@
 // Elementwise ops: GeGLU (replaces cuda_bridge.cu:2247-2269), tanh soft-cap (2319-2330),
-// residual add and scale (2293-2317).
+// residual add and scale (2293-2317), and an out-of-place scale (scale 1: a kernel copy,
+// which a captured graph replays like any other kernel).
 //
 // Streaming layout: one wave per workgroup, each thread owns U consecutive-by-wave 128-bit
 // chunks (chunk = (block*U + u)*64 + thread), so every load/store instruction of a wave
@@ -172,6 +173,11 @@ void hip_add(float* x, const float* residual, int n, HipStream_t stream) {
 void hip_scale(float* x, float scale, int n, HipStream_t stream) {
     EwArgs a{x, nullptr, x, n, scale, 0.0f};
     launch_ew<EW_SCALE>(HIP_BRIDGE_F32, a, stream_of(stream));
+}
+
+void hip_scale_ex(int dtype, const void* x, float scale, void* out, int64_t n, HipStream_t stream) {
+    EwArgs a{x, nullptr, out, n, scale, 0.0f};
+    launch_ew<EW_SCALE>(dtype, a, stream_of(stream));
 }
 
 }  // extern "C"

@@ -93,7 +93,7 @@ class DecodeModel:
         elif layer.input_layernorm is not None:
             self._norm(self.x, layer.input_layernorm, self.xb, m.dim)
         else:
-            self.xb.copy_from(self.x, 4 * m.dim, d.stream)
+            d.copyF32(self.x, self.xb, m.dim)
 
     def _ple_prologue(self):
         """model.zig:506-540 (token path)."""
@@ -103,8 +103,7 @@ class DecodeModel:
                       float(np.sqrt(np.float32(PLE_DIM))))
         if m.ple_proj is None:
             return
-        self.xb.copy_from(self.x, 4 * m.dim, d.stream)
-        d.scale(self.xb, float(np.float32(1.0) / np.sqrt(np.float32(m.dim))), m.dim)
+        d.scaleEx(B.F32, self.x, float(np.float32(1.0) / np.sqrt(np.float32(m.dim))), self.xb, m.dim)
         self._gemv(m.ple_proj, self.xb, self.ple_ctx)
         if m.ple_proj_norm is not None:
             d.rmsNormRows(B.F32, self.ple_ctx, m.ple_proj_norm, self.ple_ctx, self.L, PLE_DIM, m.eps, False)
@@ -195,7 +194,7 @@ class DecodeModel:
         if pf is not None:
             self._norm(self.x, pf, self.xb, H)
         else:
-            self.xb.copy_from(self.x, 4 * H, d.stream)
+            d.copyF32(self.x, self.xb, H)
 
     def _ffn_block(self, ly):
         m, d = self.model, self.dev

@@ -309,6 +309,14 @@ class HipDevice:
         self.b.hip_scale(_ptr(d_x), s, n, self.stream)
         self._done("scale")
 
+    def scaleEx(self, dtype, d_x, s, d_out, n):
+        self.b.hip_scale_ex(dtype, _ptr(d_x), s, _ptr(d_out), n, self.stream)
+        self._done("scaleEx")
+
+    def copyF32(self, d_src, d_dst, n):
+        """dst = src (n f32) by a kernel, so it records as a kernel node in a graph."""
+        self.scaleEx(_b.F32, d_src, 1.0, d_dst, n)
+
     def tanhSoftcap(self, d_x, cap, n):
         self.b.hip_tanh_softcap(_ptr(d_x), cap, n, self.stream)
         self._done("tanhSoftcap")
