@@ -395,9 +395,9 @@ def bench_gemv(dev):
 # Full decode step (34-layer Gemma-4B-shaped Q4_0 model, graph replay per token)
 # ---------------------------------------------------------------------------------------
 
-def bench_decode_step(dev, n_layers=34, pos0=1234, n_tokens=32):
+def bench_decode_step(dev, n_layers=34, pos0=1234, n_tokens=32, fused=True):
     from ziglm_amd.decode import DecodeModel
-    m = DecodeModel.synthetic(dev, LY.GEMMA_4B, n_layers=n_layers, vocab=262144, max_seq=4096)
+    m = DecodeModel.synthetic(dev, LY.GEMMA_4B, n_layers=n_layers, vocab=262144, max_seq=4096, fused=fused)
     try:
         m.set_token(2)
         m.capture()
@@ -426,7 +426,7 @@ def bench_decode_step(dev, n_layers=34, pos0=1234, n_tokens=32):
 # GGUF file -> device tables -> graph decode (gemma-4-E2B-shaped synthetic file)
 # ---------------------------------------------------------------------------------------
 
-def bench_gguf_decode(dev, pos0=1234, n_tokens=64, path=None, graph=True):
+def bench_gguf_decode(dev, pos0=1234, n_tokens=64, path=None, graph=True, fused=True):
     """Write the synthetic E2B-shaped Q4_0 GGUF (ziglm_amd/synth_gguf.py), open it (mmap),
     load it into device tables (timed: the pinned-ring upload and norm conversion), then
     time graph-replayed greedy decode steps at positions pos0.. (tokens/s). graph=False
@@ -448,7 +448,7 @@ def bench_gguf_decode(dev, pos0=1234, n_tokens=64, path=None, graph=True):
             t1 = time.time()
             model = Model.from_gguf(dev, f)
             t_load = time.time() - t1
-        dm = DecodeModel(dev, model, max_seq=4096, own_model=True)
+        dm = DecodeModel(dev, model, max_seq=4096, own_model=True, fused=fused)
     finally:
         if path is None:
             os.unlink(tmp)

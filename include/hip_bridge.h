@@ -226,6 +226,37 @@ void hip_gemv_geglu_q4_0(const void* gate_w, const void* up_w, const float* x, f
 void hip_gemv_qkv_q4_0(const void* q_w, const void* k_w, const void* v_w, const float* x,
                        float* q_out, float* k_out, float* v_out, int q_rows, int k_rows,
                        int v_rows, int cols, HipStream_t stream);            /* cuda_bridge.h:44 */
+/* new: GEMV with an input prologue (batch 1), so the norm / residual step before a product
+ * needs no launch of its own. Every workgroup builds the product's input v from x:
+ *   mode HIP_GEMV_PRO_NORM:  x1 = (x + [RMSNorm(r; r_weight, r_unit_offset)]) * scale
+ *                            (r NULL: x1 = x * scale; r_weight NULL: r added as is),
+ *                            v = RMSNorm(x1; weight, unit_offset) (weight NULL: v = x1);
+ *   mode HIP_GEMV_PRO_GEGLU: v = gelu_tanh(x) * r.
+ * Workgroup 0 stores x1 to x_out and v to xb_out when they are not NULL; neither may alias
+ * x or r (other workgroups are still reading them). RMSNorm is the norm kernels'
+ * arithmetic: inv = 1/sqrt(mean(v^2) + eps), (v * inv) * (1 + w) or (v * inv) * w.
+ * cols <= 16384, cols % 8 == 0, every vector 16-byte aligned; else EUNSUPPORTED. */
+#define HIP_GEMV_PRO_NORM 1
+#define HIP_GEMV_PRO_GEGLU 2
+typedef struct {
+    int mode;
+    const float* r;
+    const float* r_weight;
+    int r_unit_offset;
+    float scale;
+    float* x_out;
+    const float* weight;
+    int unit_offset;
+    float eps;
+    float* xb_out;
+} HipGemvPrologue;
+/* y = W . v, or with up_weights: y[r] = gelu_tanh(W_r . v) * (U_r . v); any GEMV qtype. */
+void hip_gemv_pro(int qtype, const void* weights, const void* up_weights, const float* x, float* y,
+                  int rows, int cols, const HipGemvPrologue* pro, HipStream_t stream);
+/* Q, K, V of one qtype over one v in one launch (hip_gemv_qkv_q4_0 for any qtype). */
+void hip_gemv_qkv_pro(int qtype, const void* q_w, const void* k_w, const void* v_w, const float* x,
+                      float* q_out, float* k_out, float* v_out, int q_rows, int k_rows, int v_rows,
+                      int cols, const HipGemvPrologue* pro, HipStream_t stream);
 /* Y[b*rows + r] = W[r] . X[b*cols ...], b < batch_size (batch 1 is the GEMV). */
 void hip_gemm_q4_0(const void* weights, const float* x, float* y, int batch_size, int rows,
                    int cols, HipStream_t stream);                           /* cuda_bridge.h:47 */

@@ -70,9 +70,13 @@ def reset(m, token):
     m.set_token(token)
 
 
-def test_decode_graph_equals_eager(dev):
+FUSE_SETS = [set(), {"qkv", "ffn", "ple", "head"}]
+
+
+@pytest.mark.parametrize("fused", FUSE_SETS, ids=["unfused", "prologues"])
+def test_decode_graph_equals_eager(dev, fused):
     """The captured step replays the eager step bit for bit, token fed back on the device."""
-    m = DecodeModel.synthetic(dev, GEMMA_4B, n_layers=2, vocab=4096, max_seq=64)
+    m = DecodeModel.synthetic(dev, GEMMA_4B, n_layers=2, vocab=4096, max_seq=64, fused=fused)
     try:
         reset(m, 5)
         eager = []
@@ -94,14 +98,15 @@ def test_decode_graph_equals_eager(dev):
         m.free()
 
 
-def test_decode_step_vs_oracle(dev, oracle):
+@pytest.mark.parametrize("fused", FUSE_SETS, ids=["unfused", "prologues"])
+def test_decode_step_vs_oracle(dev, oracle, fused):
     """Three decode steps of a 2-layer model against the oracle's composition of the same
     ops (same tokens fed to both). Each op is parity-tested on its own; this checks the
     wiring of the step. Logits within 2e-3 * (1 + |logit|) (a chain of ~25 f32 ops whose
     sums differ in order), and the greedy token equal wherever the top-2 gap exceeds that."""
     s = GEMMA_4B
     L, V, max_seq, tok0 = 2, 4096, 16, 7
-    m = DecodeModel.synthetic(dev, s, n_layers=L, vocab=V, max_seq=max_seq, host_weights=True)
+    m = DecodeModel.synthetic(dev, s, n_layers=L, vocab=V, max_seq=max_seq, host_weights=True, fused=fused)
     try:
         reset(m, tok0)
         h, eps = m.host, np.float32(s.eps)

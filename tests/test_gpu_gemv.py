@@ -16,6 +16,7 @@ from oracle import oracle as O
 from ziglm_amd import bridge as B
 from ziglm_amd import synth
 from test_oracle_gemv_cpu import bound, int_matrix, random_matrix
+from tol import assert_bitexact, assert_rel
 
 pytestmark = pytest.mark.gpu
 
@@ -135,3 +136,143 @@ def test_gemv_unsupported_qtype_is_noop(dev):
     finally:
         dev.strict = True
     assert np.all(d_y.to_numpy((64,), np.uint8) == 0x11)
+
+
+# ---------------------------------------------------------------------------------------
+# Input prologue (hip_gemv_pro / hip_gemv_qkv_pro)
+# ---------------------------------------------------------------------------------------
+
+def pro_ref(oracle, x, r=None, r_w=None, r_uo=False, scale=1.0, w=None, uo=False, eps=1e-6):
+    """The prologue as the reference's separate ops: x1 = (x + [norm](r)) * scale,
+    v = [norm](x1); returns (x1, v, y) with y the branch term added to x."""
+    x1 = x.astype(np.float32)
+    y = None
+    if r is not None:
+        y = r if r_w is None else oracle.rms_norm(r, r_w, eps, r_uo)
+        x1 = (x1 + y).astype(np.float32)
+    if scale != 1.0:
+        x1 = (x1 * np.float32(scale)).astype(np.float32)
+    v = x1 if w is None else oracle.rms_norm(x1, w, eps, uo)
+    return x1, v, y
+
+
+def check_pro_outputs(got_y, wd, v, got_v=None, got_x1=None, x1=None, y=None, what=""):
+    """v within 1e-5 relative (the norm kernels' bar); y = W v within twice the dot-product
+    bound plus the change a 1e-5-relative v can make (1e-5 * sum |w| |v|)."""
+    if got_v is not None:
+        assert_rel(got_v, v, 1e-5, what=f"{what} v")
+    if got_x1 is not None:
+        floor = 1e-5 * np.abs(y) if y is not None else 0.0
+        assert_rel(got_x1, x1, 2.0 ** -23, floor=floor, what=f"{what} x1")
+    ref = wd @ v.astype(np.float64)
+    tol = 2 * bound(wd, v[None])[0] + 1e-5 * (np.abs(wd) @ np.abs(v.astype(np.float64)))
+    err = np.abs(np.asarray(got_y, np.float64) - ref)
+    assert np.all(err <= tol), f"{what}: max err/tol {float(np.max(err / tol)):.3g}"
+
+
+PRO_CASES = {
+    "norm": dict(w=True, uo=True),
+    "add_raw_norm": dict(r="raw", w=True, uo=True),
+    "add_norm_norm": dict(r="norm", r_uo=True, w=True, uo=True, outs=True),
+    "add_norm_scale": dict(r="norm", r_uo=False, scale=0.75, outs=True),
+    "add_norm_norm_w": dict(r="norm", r_uo=False, w=True, uo=False, outs=True),
+}
+
+
+@pytest.mark.parametrize("qtype", QTYPES)
+@pytest.mark.parametrize("case", list(PRO_CASES))
+@pytest.mark.parametrize("rows,cols", [(1536, 2048), (37, 1536), (300, 256)])
+def test_gemv_prologue_norm(dev, oracle, qtype, case, rows, cols):
+    c = PRO_CASES[case]
+    raw, wd = random_matrix(qtype, rows, cols, seed=rows + cols)
+    x = synth.normal_f32(51, "x", (cols,), 0, 3.0)
+    r = synth.normal_f32(51, "r", (cols,), 0, 0.5) if "r" in c else None
+    r_w = synth.normal_f32(51, "rw", (cols,), 0, 0.1) if c.get("r") == "norm" else None
+    w = synth.normal_f32(51, "w", (cols,), 0, 0.1) if c.get("w") else None
+    x1, v, y = pro_ref(oracle, x, r, r_w, c.get("r_uo", False), c.get("scale", 1.0), w, c.get("uo", False))
+    d = {k: (dev.from_numpy(a) if a is not None else None) for k, a in dict(x=x, r=r, r_w=r_w, w=w).items()}
+    d_y, d_x1, d_v, d_w = dev.alloc(rows * 4), dev.alloc(cols * 4), dev.alloc(cols * 4), dev.from_numpy(raw.reshape(-1))
+    outs = c.get("outs", False)
+    pro = dev.prologue(B.PRO_NORM, r=d["r"], r_weight=d["r_w"], r_unit_offset=c.get("r_uo", False),
+                       scale=c.get("scale", 1.0), x_out=d_x1 if outs else None, weight=d["w"],
+                       unit_offset=c.get("uo", False), eps=1e-6, xb_out=d_v if outs else None)
+    dev.gemvPro(qtype, d_w, None, d["x"], d_y, rows, cols, pro)
+    got_y = d_y.to_numpy((rows,), np.float32)
+    if outs:
+        check_pro_outputs(got_y, wd, v, d_v.to_numpy((cols,), np.float32), d_x1.to_numpy((cols,), np.float32), x1,
+                          y, what=case)
+    else:
+        check_pro_outputs(got_y, wd, v, what=case)
+
+
+@pytest.mark.parametrize("qtype", [B.Q4_0, B.Q8_0, B.F32])
+def test_gemv_prologue_geglu_input(dev, oracle, qtype):
+    """v = gelu(x) * r (the per-layer-embedding projection's input)."""
+    rows, cols = 1536, 256
+    raw, wd = random_matrix(qtype, rows, cols, seed=77)
+    g = synth.normal_f32(52, "g", (cols,), 0, 2.0)
+    u = synth.normal_f32(52, "u", (cols,))
+    v = oracle.geglu(g, u)
+    d_y, d_v, d_u, d_g, d_w = dev.alloc(rows * 4), dev.alloc(cols * 4), dev.from_numpy(u), dev.from_numpy(g), \
+        dev.from_numpy(raw.reshape(-1))
+    pro = dev.prologue(B.PRO_GEGLU, r=d_u, xb_out=d_v)
+    dev.gemvPro(qtype, d_w, None, d_g, d_y, rows, cols, pro)
+    got_v = d_v.to_numpy((cols,), np.float32)
+    assert_rel(got_v, v, 1e-5, floor=np.abs(g.astype(np.float64) * u) * 2.0 ** -23, what="gelu(x)*r")
+    check_pro_outputs(d_y.to_numpy((rows,), np.float32), wd, v, what="geglu input")
+
+
+@pytest.mark.parametrize("qtype", [B.Q4_0, B.Q8_0, B.BF16])
+def test_gemv_prologue_geglu_matrices_and_qkv(dev, oracle, qtype):
+    """GeGLU pair and Q/K/V segments with a prologue: the same per-row arithmetic as the
+    single-matrix form over the same input (QKV bit for bit; GeGLU against gelu(g) * u of
+    the two single products, which it computes from the same sums)."""
+    cols, I = 1536, 1024
+    x = synth.normal_f32(53, "x", (cols,))
+    r = synth.normal_f32(53, "r", (cols,))
+    rw = synth.normal_f32(53, "rw", (cols,), 0, 0.1)
+    w = synth.normal_f32(53, "w", (cols,), 0, 0.1)
+    d_x, d_r, d_rw, d_w = (dev.from_numpy(a) for a in (x, r, rw, w))
+    pro = dev.prologue(B.PRO_NORM, r=d_r, r_weight=d_rw, r_unit_offset=True, weight=d_w, unit_offset=True)
+    mats = [random_matrix(qtype, n, cols, seed=90 + n) for n in (2048, 512, 512)]
+    d_m = [dev.from_numpy(m[0].reshape(-1)) for m in mats]
+    outs = [dev.alloc(n * 4) for n in (2048, 512, 512)]
+    dev.gemvQkvPro(qtype, *d_m, d_x, *outs, 2048, 512, 512, cols, pro)
+    for (raw, wd), dm, o, n in zip(mats, d_m, outs, (2048, 512, 512)):
+        single = dev.alloc(n * 4)
+        dev.gemvPro(qtype, dm, None, d_x, single, n, cols, pro)
+        assert_bitexact(o.to_numpy((n,), np.float32), single.to_numpy((n,), np.float32), "qkv segment")
+    _, v, _ = pro_ref(oracle, x, r, rw, True, 1.0, w, True)
+    check_pro_outputs(outs[0].to_numpy((2048,), np.float32), mats[0][1], v, what="qkv q")
+    gm, um = random_matrix(qtype, I, cols, seed=5), random_matrix(qtype, I, cols, seed=6)
+    d_act, d_g, d_u = dev.alloc(I * 4), dev.alloc(I * 4), dev.alloc(I * 4)
+    d_gm, d_um = dev.from_numpy(gm[0].reshape(-1)), dev.from_numpy(um[0].reshape(-1))
+    dev.gemvPro(qtype, d_gm, d_um, d_x, d_act, I, cols, pro)
+    dev.gemvPro(qtype, d_gm, None, d_x, d_g, I, cols, pro)
+    dev.gemvPro(qtype, d_um, None, d_x, d_u, I, cols, pro)
+    gg, uu = d_g.to_numpy((I,), np.float32), d_u.to_numpy((I,), np.float32)
+    dev.geglu(d_g, d_u, d_g, I)
+    assert_bitexact(d_act.to_numpy((I,), np.float32), d_g.to_numpy((I,), np.float32), "geglu pair")
+    check_pro_outputs(gg, gm[1], v, what="gate")
+    check_pro_outputs(uu, um[1], v, what="up")
+
+
+def test_gemv_prologue_rejects(dev):
+    w = dev.alloc(18 * 1024)
+    x = dev.alloc(4 * 20000)
+    y = dev.alloc(4 * 64)
+    y.fill(0x33)
+    dev.strict = False
+    try:
+        pro = dev.prologue(B.PRO_NORM, weight=x)
+        dev.gemvPro(B.Q4_0, w, None, x, y, 1, 16416, pro)                     # input beyond LDS
+        assert dev.b.last_error() == B.EUNSUPPORTED
+        dev.gemvPro(B.Q4_0, w, None, x, y, 4, 256, dev.prologue(B.PRO_NORM, weight=x, x_out=y.at(4)))  # misaligned
+        assert dev.b.last_error() == B.EUNSUPPORTED
+        dev.gemvPro(B.Q4_0, w, None, x, y, 4, 256, dev.prologue(B.PRO_GEGLU))    # GEGLU needs r
+        assert dev.b.last_error() == B.EINVAL
+        dev.gemvPro(B.Q4_0, w, None, x, y, 4, 256, dev.prologue(B.PRO_NORM, r_weight=x))  # r weight without r
+        assert dev.b.last_error() == B.EINVAL
+    finally:
+        dev.strict = True
+    assert np.all(y.to_numpy((256,), np.uint8) == 0x33)

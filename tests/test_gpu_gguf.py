@@ -36,7 +36,8 @@ GEMMA4 = S.GgufModelConfig(arch="gemma4", dim=256, n_layers=20, n_heads=8, n_kv_
                            norm_type=B.F16, no_kv_from=18, scalars={3: (B.BF16, 0.75), 7: (B.F32, 1.5)},
                            tile_rows=0)
 GEMMA2 = S.GgufModelConfig(arch="gemma2", dim=256, n_layers=3, n_heads=4, n_kv_heads=2, head_dim=128,
-                           global_every=0, inter=512, vocab=1024, ple=False, norm_type=B.BF16, tile_rows=0)
+                           global_every=0, inter=512, vocab=1024, ple=False, norm_type=B.BF16, tile_rows=0,
+                           types={"up": B.BF16})
 
 
 def gguf_bytes(cfg, seed=9):
@@ -171,12 +172,17 @@ def check_token(gtok, ref, tol, what):
         assert gtok == int(np.argmax(ref[1:])) + 1, what
 
 
+FUSE_SETS = [True, set(), {"qkv", "ffn", "ple", "head"}]
+FUSE_IDS = ["default", "unfused", "prologues"]
+
+
+@pytest.mark.parametrize("fused", FUSE_SETS, ids=FUSE_IDS)
 @pytest.mark.parametrize("cfg", [GEMMA4, GEMMA2], ids=["gemma4", "gemma2"])
-def test_decode_loaded_model_vs_oracle(dev, oracle, cfg):
+def test_decode_loaded_model_vs_oracle(dev, oracle, cfg, fused):
     data = gguf_bytes(cfg)
     ref = MR.RefModel(oracle, data, max_seq=32)
     with G.GGUFFile.from_buffer(data) as f:
-        dm = DecodeModel(dev, Model.from_gguf(dev, f), max_seq=32, own_model=True)
+        dm = DecodeModel(dev, Model.from_gguf(dev, f), max_seq=32, own_model=True, fused=fused)
     try:
         dm.reset(0)
         for pos, tok in enumerate([3, 17, 101, 250, 77, 1000]):
@@ -190,10 +196,11 @@ def test_decode_loaded_model_vs_oracle(dev, oracle, cfg):
         dm.free()
 
 
-def test_decode_loaded_graph_equals_eager(dev):
+@pytest.mark.parametrize("fused", FUSE_SETS, ids=FUSE_IDS)
+def test_decode_loaded_graph_equals_eager(dev, fused):
     data = gguf_bytes(GEMMA4)
     with G.GGUFFile.from_buffer(data) as f:
-        dm = DecodeModel(dev, Model.from_gguf(dev, f), max_seq=32, own_model=True)
+        dm = DecodeModel(dev, Model.from_gguf(dev, f), max_seq=32, own_model=True, fused=fused)
     try:
         dm.reset(5)
         eager = []

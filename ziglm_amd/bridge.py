@@ -22,6 +22,19 @@ _f = ctypes.c_float
 _sz = ctypes.c_size_t
 _pv = ctypes.POINTER(ctypes.c_void_p)
 
+PRO_NORM, PRO_GEGLU = 1, 2
+
+
+class GemvPrologue(ctypes.Structure):
+    """HipGemvPrologue (include/hip_bridge.h)."""
+    _fields_ = [("mode", ctypes.c_int), ("r", ctypes.c_void_p), ("r_weight", ctypes.c_void_p),
+                ("r_unit_offset", ctypes.c_int), ("scale", ctypes.c_float), ("x_out", ctypes.c_void_p),
+                ("weight", ctypes.c_void_p), ("unit_offset", ctypes.c_int), ("eps", ctypes.c_float),
+                ("xb_out", ctypes.c_void_p)]
+
+
+_ppro = ctypes.POINTER(GemvPrologue)
+
 # name -> (restype, argtypes), in header order.
 SIGNATURES = {
     # runtime (cuda_bridge.h:15-33)
@@ -93,6 +106,8 @@ SIGNATURES = {
     "hip_gemv": (None, [_i, _v, _v, _v, _i, _i, _v]),
     "hip_gemv_geglu_q4_0": (None, [_v, _v, _v, _v, _i, _i, _v]),
     "hip_gemv_qkv_q4_0": (None, [_v, _v, _v, _v, _v, _v, _v, _i, _i, _i, _i, _v]),
+    "hip_gemv_pro": (None, [_i, _v, _v, _v, _v, _i, _i, _ppro, _v]),
+    "hip_gemv_qkv_pro": (None, [_i, _v, _v, _v, _v, _v, _v, _v, _i, _i, _i, _i, _ppro, _v]),
     "hip_gemm_q4_0": (None, [_v, _v, _v, _i, _i, _i, _v]),
     "hip_gemm_q8_0": (None, [_v, _v, _v, _i, _i, _i, _v]),
     "hip_gemm_f16": (None, [_v, _v, _v, _i, _i, _i, _v]),

@@ -19,6 +19,8 @@
 // sums are reduced within the wave (DPP / permlane) and across the 4 waves through LDS.
 // Fused forms: GeGLU pairs each gate row with its up row and writes gelu(g) * u (the
 // elementwise kernels' gelu_fast); QKV treats the three matrices as one row space.
+#include <algorithm>
+
 #include "zl_common.h"
 #include "zl_host.h"
 
@@ -28,6 +30,31 @@ constexpr int kGemvThreads = 256;
 constexpr int kGemvWaves = kGemvThreads / kWave;
 
 enum GemvMode { GV_PLAIN = 0, GV_GEGLU = 1 };
+
+// Input prologue (HipGemvPrologue, batch 1): every workgroup builds the product's input
+// vector in LDS from x before the weight stream starts, so a norm / residual step needs no
+// launch of its own. NORM: x1 = (x + [RMSNorm](r)) * scale, input = [RMSNorm](x1), with
+// workgroup 0 writing x1 (x_out) and the input (xb_out) when asked; GEGLU: input =
+// gelu(x) * r. The statistics are recomputed per workgroup (a few KB read from L2).
+enum GemvProMode { GP_NONE = 0, GP_NORM = 1, GP_GEGLU = 2 };
+constexpr int kGemvProMaxCols = 16384;  // input vector in LDS: <= 64 KB
+#ifndef ZL_GEMV_PRO_GRID
+#define ZL_GEMV_PRO_GRID 1024
+#endif
+constexpr unsigned kGemvProGrid = ZL_GEMV_PRO_GRID;
+
+struct GemvPro {
+    int mode;
+    const float* r;
+    const float* r_w;
+    int r_uo;
+    float scale;
+    float* x_out;
+    const float* w;
+    int uo;
+    float eps;
+    float* xb_out;
+};
 
 struct GemvSeg {
     const unsigned char* w;
@@ -44,6 +71,7 @@ struct GemvArgs {
     int cols;
     int64_t row_bytes;
     int batch;
+    GemvPro pro;                // used by the PRO kernels only
 };
 
 // v & m, opaque to the optimiser: it would otherwise split the byte-wise mask into one
@@ -160,19 +188,112 @@ __device__ __forceinline__ void group_cols(int g, int& ca, int& cb) {
     }
 }
 
-template <int QT, int RPW, int NB, int MODE>
+// Sum over the workgroup (wave sums, then the 4 wave values in order); s_red[4] in LDS.
+__device__ __forceinline__ float gemv_block_sum(float v, float* s_red) {
+    v = group_sum<kWave>(v);
+    if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    const float t = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+    __syncthreads();  // s_red is reused by the next reduction
+    return t;
+}
+
+// Builds the input vector of a PRO product in s_x[0, cols) (cols % 4 == 0, 16-byte aligned
+// operands): see GemvProMode. The RMSNorm arithmetic is the norm kernels' (rms_inv, then
+// (v * inv) * (1 + w) or * w).
+__device__ void gemv_prologue(const GemvArgs& a, float* s_x, float* s_red) {
+    const GemvPro& p = a.pro;
+    const int n4 = a.cols / 4;
+    const int tid = threadIdx.x;
+    f32x4* sx4 = reinterpret_cast<f32x4*>(s_x);
+    if (p.mode == GP_GEGLU) {
+        for (int c = tid; c < n4; c += kGemvThreads) {
+            const f32x4 g = ldf4(a.x + 4 * c), u = ldf4(p.r + 4 * c);
+            f32x4 o;
+            o.x = gelu_fast(g.x) * u.x;
+            o.y = gelu_fast(g.y) * u.y;
+            o.z = gelu_fast(g.z) * u.z;
+            o.w = gelu_fast(g.w) * u.w;
+            sx4[c] = o;
+        }
+    } else {
+        float inv1 = 0.0f;
+        if (p.r && p.r_w) {
+            float ss = 0.0f;
+            for (int c = tid; c < n4; c += kGemvThreads) {
+                const f32x4 v = ldf4(p.r + 4 * c);
+                ss = fmaf(v.x, v.x, ss);
+                ss = fmaf(v.y, v.y, ss);
+                ss = fmaf(v.z, v.z, ss);
+                ss = fmaf(v.w, v.w, ss);
+            }
+            inv1 = rms_inv(gemv_block_sum(ss, s_red), a.cols, p.eps);
+        }
+        const bool wr = p.x_out && blockIdx.x == 0;
+        float ss = 0.0f;
+        for (int c = tid; c < n4; c += kGemvThreads) {
+            const f32x4 xv = ldf4(a.x + 4 * c);
+            float v[4] = {xv.x, xv.y, xv.z, xv.w};
+            if (p.r) {
+                const f32x4 rv = ldf4(p.r + 4 * c);
+                float y[4] = {rv.x, rv.y, rv.z, rv.w};
+                if (p.r_w) {
+                    const f32x4 wv = ldf4(p.r_w + 4 * c);
+                    const float w[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const float t = y[j] * inv1;
+                        y[j] = p.r_uo ? t * (1.0f + w[j]) : t * w[j];
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j) v[j] = v[j] + y[j];
+            }
+            if (p.scale != 1.0f) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) v[j] = v[j] * p.scale;
+            }
+            const f32x4 o = {v[0], v[1], v[2], v[3]};
+            if (wr) *reinterpret_cast<f32x4*>(p.x_out + 4 * c) = o;
+            sx4[c] = o;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) ss = fmaf(v[j], v[j], ss);
+        }
+        if (p.w) {
+            const float inv2 = rms_inv(gemv_block_sum(ss, s_red), a.cols, p.eps);
+            for (int c = tid; c < n4; c += kGemvThreads) {  // the elements this thread wrote
+                const f32x4 v = sx4[c], wv = ldf4(p.w + 4 * c);
+                f32x4 o;
+                o.x = p.uo ? (v.x * inv2) * (1.0f + wv.x) : (v.x * inv2) * wv.x;
+                o.y = p.uo ? (v.y * inv2) * (1.0f + wv.y) : (v.y * inv2) * wv.y;
+                o.z = p.uo ? (v.z * inv2) * (1.0f + wv.z) : (v.z * inv2) * wv.z;
+                o.w = p.uo ? (v.w * inv2) * (1.0f + wv.w) : (v.w * inv2) * wv.w;
+                sx4[c] = o;
+            }
+        }
+    }
+    if (p.xb_out && blockIdx.x == 0)
+        for (int c = tid; c < n4; c += kGemvThreads) *reinterpret_cast<f32x4*>(p.xb_out + 4 * c) = sx4[c];
+    __syncthreads();
+}
+
+template <int QT, int RPW, int NB, int MODE, bool PRO = false>
 __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvArgs a) {
     constexpr int NM = MODE == GV_GEGLU ? 2 : 1;  // matrices per row (gate, up)
     constexpr int NACC = RPW * NB * NM;
     __shared__ float s_part[kGemvWaves][NACC];
+    extern __shared__ float s_x[];  // PRO: the input vector, cols floats
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
     const int lane = tid & 63;
-    const int row0 = blockIdx.x * RPW;
     const int G = a.cols / 8;
+    if constexpr (PRO) gemv_prologue(a, s_x, &s_part[0][0]);
 
-    // Row pointers. Rows past the end read the workgroup's first row (always in range:
-    // the grid has cdiv(total_rows, RPW) workgroups) and are never written.
+    // Row blocks: one per workgroup, except PRO kernels, whose grid is capped (the prologue
+    // is paid once per workgroup) and which take every gridDim.x-th block.
+    for (int row0 = blockIdx.x * RPW;;) {
+    // Row pointers. Rows past the end read the block's first row (in range: row0 <
+    // total_rows) and are never written.
     const unsigned char* wrow[RPW][NM];
     float* yrow[RPW];
     int ystride[RPW];
@@ -211,7 +332,8 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvArgs a) {
         if constexpr (QT != HIP_BRIDGE_Q4_0) {
         const float* xt[NB];
 #pragma unroll
-        for (int b = 0; b < NB; ++b) xt[b] = a.x + (int64_t)(b0 + b < a.batch ? b0 + b : a.batch - 1) * a.cols;
+        for (int b = 0; b < NB; ++b)
+            xt[b] = PRO ? s_x : a.x + (int64_t)(b0 + b < a.batch ? b0 + b : a.batch - 1) * a.cols;
         WGroup<QT> cur[RPW][NM], nxt[RPW][NM];
         f32x4 cxa[NB], cxb[NB], nxa[NB], nxb[NB];
         auto fetch = [&](int g, WGroup<QT> (&w)[RPW][NM], f32x4 (&xa)[NB], f32x4 (&xb)[NB]) {
@@ -264,7 +386,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvArgs a) {
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
                 const int bt = b0 + b < a.batch ? b0 + b : a.batch - 1;
-                const float* xr = a.x + (int64_t)bt * a.cols;
+                const float* xr = PRO ? s_x : a.x + (int64_t)bt * a.cols;
                 const f32x4 xa = ldf4(xr + ca), xb = ldf4(xr + cb);
                 const float sx = ((xa.x + xa.y) + (xa.z + xa.w)) + ((xb.x + xb.y) + (xb.z + xb.w));
 #pragma unroll
@@ -309,6 +431,10 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvArgs a) {
             }
         }
         __syncthreads();  // s_part is rewritten by the next token tile
+    }
+    if constexpr (!PRO) break;
+    row0 += gridDim.x * RPW;
+    if (row0 >= a.total_rows) break;
     }
 }
 
@@ -393,12 +519,21 @@ static int64_t gemv_row_bytes(int qtype, int cols) {
 // measured on Gemma-4B decode shapes, small matrices (1024-4096 rows) want 2 rows and more
 // workgroups, large ones 4, Q4_0 (the most x per weight byte) 8 from 16384 rows. GeGLU
 // reads two matrices per row and takes half as many rows.
-template <int QT, int MODE>
+template <int QT, int MODE, bool PRO>
 static void launch_vec(const GemvArgs& a, hipStream_t s) {
     constexpr int H = MODE == GV_GEGLU ? 2 : 1;
     const unsigned g8 = (unsigned)cdiv(a.total_rows, 8 / H), g4 = (unsigned)cdiv(a.total_rows, 4 / H),
                    g2 = (unsigned)cdiv(a.total_rows, 2 / H);
-    if (a.batch == 1) {
+    if (PRO) {  // batch 1; the input vector in dynamic LDS; at most kGemvProGrid workgroups
+        const size_t lds = (size_t)a.cols * sizeof(float);
+        const unsigned cap = kGemvProGrid;
+        if (QT == HIP_BRIDGE_Q4_0 && a.total_rows >= 16384)
+            k_gemv<QT, 8 / H, 1, MODE, true><<<std::min(g8, cap), kGemvThreads, lds, s>>>(a);
+        else if (a.total_rows >= 8192)
+            k_gemv<QT, 4 / H, 1, MODE, true><<<std::min(g4, cap), kGemvThreads, lds, s>>>(a);
+        else
+            k_gemv<QT, 2 / H, 1, MODE, true><<<std::min(g2, cap), kGemvThreads, lds, s>>>(a);
+    } else if (a.batch == 1) {
         if (QT == HIP_BRIDGE_Q4_0 && a.total_rows >= 16384)
             k_gemv<QT, 8 / H, 1, MODE><<<g8, kGemvThreads, 0, s>>>(a);
         else if (a.total_rows >= 8192)
@@ -441,13 +576,35 @@ static void launch_gemv(int qtype, GemvArgs& a, hipStream_t s) {
         ok = ok && w_ok(a.seg[i].w);
     }
     if (MODE == GV_GEGLU) ok = ok && w_ok(a.w_up);
-    if (ok) {
+    const GemvPro& p = a.pro;
+    if (p.mode != GP_NONE) {
+        // prologue: batch 1, vector path, input vector within LDS, 16-byte aligned operands
+        const bool args = (p.mode == GP_NORM || p.mode == GP_GEGLU) && (p.mode != GP_GEGLU || p.r) &&
+                          (p.r || !p.r_w);
+        if (!args) {
+            set_error(HIP_BRIDGE_EINVAL);
+            return;
+        }
+        const bool pro_ok = ok && a.batch == 1 && a.cols <= kGemvProMaxCols && aligned16(p.r) &&
+                            aligned16(p.r_w) && aligned16(p.w) && aligned16(p.x_out) && aligned16(p.xb_out);
+        if (!pro_ok) {
+            set_error(HIP_BRIDGE_EUNSUPPORTED);
+            return;
+        }
         switch (qtype) {
-            case HIP_BRIDGE_Q4_0: launch_vec<HIP_BRIDGE_Q4_0, MODE>(a, s); break;
-            case HIP_BRIDGE_Q8_0: launch_vec<HIP_BRIDGE_Q8_0, MODE>(a, s); break;
-            case HIP_BRIDGE_F16: launch_vec<HIP_BRIDGE_F16, MODE>(a, s); break;
-            case HIP_BRIDGE_BF16: launch_vec<HIP_BRIDGE_BF16, MODE>(a, s); break;
-            default: launch_vec<HIP_BRIDGE_F32, MODE>(a, s); break;
+            case HIP_BRIDGE_Q4_0: launch_vec<HIP_BRIDGE_Q4_0, MODE, true>(a, s); break;
+            case HIP_BRIDGE_Q8_0: launch_vec<HIP_BRIDGE_Q8_0, MODE, true>(a, s); break;
+            case HIP_BRIDGE_F16: launch_vec<HIP_BRIDGE_F16, MODE, true>(a, s); break;
+            case HIP_BRIDGE_BF16: launch_vec<HIP_BRIDGE_BF16, MODE, true>(a, s); break;
+            default: launch_vec<HIP_BRIDGE_F32, MODE, true>(a, s); break;
+        }
+    } else if (ok) {
+        switch (qtype) {
+            case HIP_BRIDGE_Q4_0: launch_vec<HIP_BRIDGE_Q4_0, MODE, false>(a, s); break;
+            case HIP_BRIDGE_Q8_0: launch_vec<HIP_BRIDGE_Q8_0, MODE, false>(a, s); break;
+            case HIP_BRIDGE_F16: launch_vec<HIP_BRIDGE_F16, MODE, false>(a, s); break;
+            case HIP_BRIDGE_BF16: launch_vec<HIP_BRIDGE_BF16, MODE, false>(a, s); break;
+            default: launch_vec<HIP_BRIDGE_F32, MODE, false>(a, s); break;
         }
     } else {
         const unsigned grid = (unsigned)a.total_rows;
@@ -528,16 +685,15 @@ void hip_gemv_geglu_q4_0(const void* gate_w, const void* up_w, const float* x, f
     launch_gemv<GV_GEGLU>(HIP_BRIDGE_Q4_0, a, stream_of(stream));
 }
 
-void hip_gemv_qkv_q4_0(const void* q_w, const void* k_w, const void* v_w, const float* x, float* q_out,
-                       float* k_out, float* v_out, int q_rows, int k_rows, int v_rows, int cols,
-                       HipStream_t stream) {
+static bool qkv_args(GemvArgs& a, const void* q_w, const void* k_w, const void* v_w, const float* x,
+                     float* q_out, float* k_out, float* v_out, int q_rows, int k_rows, int v_rows, int cols) {
     if (q_rows < 0 || k_rows < 0 || v_rows < 0) {
         set_error(HIP_BRIDGE_EINVAL);
-        return;
+        return false;
     }
     const int total = q_rows + k_rows + v_rows;
-    if (total <= 0 || cols <= 0) return;
-    GemvArgs a{};
+    if (total <= 0 || cols <= 0) return false;
+    a = GemvArgs{};
     a.seg[0] = GemvSeg{(const unsigned char*)q_w, q_out, q_rows};
     a.seg[1] = GemvSeg{(const unsigned char*)k_w, k_out, k_rows};
     a.seg[2] = GemvSeg{(const unsigned char*)v_w, v_out, v_rows};
@@ -546,7 +702,51 @@ void hip_gemv_qkv_q4_0(const void* q_w, const void* k_w, const void* v_w, const 
     a.x = x;
     a.cols = cols;
     a.batch = 1;
-    launch_gemv<GV_PLAIN>(HIP_BRIDGE_Q4_0, a, stream_of(stream));
+    return true;
+}
+
+static void set_pro(GemvArgs& a, const HipGemvPrologue* pro) {
+    if (!pro) return;
+    a.pro.mode = pro->mode;
+    a.pro.r = pro->r;
+    a.pro.r_w = pro->r_weight;
+    a.pro.r_uo = pro->r_unit_offset;
+    a.pro.scale = pro->scale;
+    a.pro.x_out = pro->x_out;
+    a.pro.w = pro->weight;
+    a.pro.uo = pro->unit_offset;
+    a.pro.eps = pro->eps;
+    a.pro.xb_out = pro->xb_out;
+}
+
+void hip_gemv_qkv_q4_0(const void* q_w, const void* k_w, const void* v_w, const float* x, float* q_out,
+                       float* k_out, float* v_out, int q_rows, int k_rows, int v_rows, int cols,
+                       HipStream_t stream) {
+    GemvArgs a;
+    if (qkv_args(a, q_w, k_w, v_w, x, q_out, k_out, v_out, q_rows, k_rows, v_rows, cols))
+        launch_gemv<GV_PLAIN>(HIP_BRIDGE_Q4_0, a, stream_of(stream));
+}
+
+void hip_gemv_pro(int qtype, const void* weights, const void* up_weights, const float* x, float* y, int rows,
+                  int cols, const HipGemvPrologue* pro, HipStream_t stream) {
+    if (rows <= 0 || cols <= 0) return;
+    GemvArgs a = one_matrix(weights, x, y, rows, cols, 1);
+    set_pro(a, pro);
+    if (up_weights) {
+        a.w_up = (const unsigned char*)up_weights;
+        launch_gemv<GV_GEGLU>(qtype, a, stream_of(stream));
+    } else {
+        launch_gemv<GV_PLAIN>(qtype, a, stream_of(stream));
+    }
+}
+
+void hip_gemv_qkv_pro(int qtype, const void* q_w, const void* k_w, const void* v_w, const float* x, float* q_out,
+                      float* k_out, float* v_out, int q_rows, int k_rows, int v_rows, int cols,
+                      const HipGemvPrologue* pro, HipStream_t stream) {
+    GemvArgs a;
+    if (!qkv_args(a, q_w, k_w, v_w, x, q_out, k_out, v_out, q_rows, k_rows, v_rows, cols)) return;
+    set_pro(a, pro);
+    launch_gemv<GV_PLAIN>(qtype, a, stream_of(stream));
 }
 
 }  // extern "C"

@@ -21,8 +21,9 @@
 // computed once in LDS while the first head's loads are in flight; its denominators are
 // evaluated per lane (rope_denom), so that phase has no memory operand to wait for.
 // Generic path (partial rotary, other head sizes up to 512, any alignment): one wave per
-// head, head staged in LDS.
+// head row (Q, K or V head), head staged in LDS, four rows per workgroup.
 #include <math.h>
+#include <algorithm>
 #include <string.h>
 
 #include "zl_common.h"
@@ -251,9 +252,9 @@ __global__ __launch_bounds__(256) void k_qk_generic(QkArgs a, RopeTab tab) {
     if (a.do_rope) fill_cos_sin(tab, (float)p * a.freq_scale, half, s_cos, s_sin);
     __syncthreads();
     float* buf = s_head[wave];
-    const int rounds = (HR + 3) / 4;
-    for (int rd = 0; rd < rounds; ++rd) {
-        const int hr = rd * 4 + wave;
+    // Workgroup (t, y) takes head rows 4y .. 4y+3 of token t, one per wave.
+    {
+        const int hr = blockIdx.y * 4 + wave;
         int kind = -1;
         const T* src = nullptr;
         T* dst = nullptr;
@@ -353,7 +354,8 @@ static void launch_qk_t(const QkArgs& a, const RopeTab& tab, hipStream_t s) {
         else if (a.D == 128) k_qk_fused<T, 128><<<grid, 256, 0, s>>>(a);
         else k_qk_fused<T, 256><<<grid, 256, 0, s>>>(a);
     } else {
-        k_qk_generic<T><<<grid, 256, 0, s>>>(a, tab);
+        const dim3 g2(grid, (unsigned)std::max<int64_t>(1, cdiv(a.nh + 2 * a.nkv, 4)));  // 4 head rows per workgroup
+        k_qk_generic<T><<<g2, 256, 0, s>>>(a, tab);
     }
     check_launch();
 }

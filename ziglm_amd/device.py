@@ -249,6 +249,28 @@ class HipDevice:
                                  _ptr(d_k_out), _ptr(d_v_out), q_rows, k_rows, v_rows, cols, self.stream)
         self._done("gemvQkvQ4_0")
 
+    @staticmethod
+    def prologue(mode=_b.PRO_NORM, r=None, r_weight=None, r_unit_offset=False, scale=1.0, x_out=None,
+                 weight=None, unit_offset=False, eps=1e-6, xb_out=None):
+        """A HipGemvPrologue (see include/hip_bridge.h). It holds references to the buffers
+        it points at, so none is freed while the prologue can still be launched."""
+        pro = _b.GemvPrologue(int(mode), _ptr(r), _ptr(r_weight), int(r_unit_offset), float(scale), _ptr(x_out),
+                              _ptr(weight), int(unit_offset), float(eps), _ptr(xb_out))
+        pro._keep = (r, r_weight, x_out, weight, xb_out)
+        return pro
+
+    def gemvPro(self, qtype, d_weights, d_up_weights, d_x, d_y, rows, cols, pro):
+        self.b.hip_gemv_pro(int(qtype), _ptr(d_weights), _ptr(d_up_weights), _ptr(d_x), _ptr(d_y), rows, cols,
+                            ctypes.byref(pro) if pro is not None else None, self.stream)
+        self._done("gemvPro")
+
+    def gemvQkvPro(self, qtype, d_q_w, d_k_w, d_v_w, d_x, d_q_out, d_k_out, d_v_out, q_rows, k_rows, v_rows, cols,
+                   pro):
+        self.b.hip_gemv_qkv_pro(int(qtype), _ptr(d_q_w), _ptr(d_k_w), _ptr(d_v_w), _ptr(d_x), _ptr(d_q_out),
+                                _ptr(d_k_out), _ptr(d_v_out), q_rows, k_rows, v_rows, cols,
+                                ctypes.byref(pro) if pro is not None else None, self.stream)
+        self._done("gemvQkvPro")
+
     def gemmQ4_0(self, d_weights, d_x, d_y, batch_size, rows, cols):
         self.b.hip_gemm_q4_0(_ptr(d_weights), _ptr(d_x), _ptr(d_y), batch_size, rows, cols, self.stream)
         self._done("gemmQ4_0")
