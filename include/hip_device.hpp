@@ -101,6 +101,17 @@ public:
               size_t rows, size_t cols) const {
         hip_gemm((int)qtype, d_weights, d_x, d_y, (int)batch_size, (int)rows, (int)cols, stream);
     }
+    // new: products with an input prologue (norm / residual add / gelu(x) * r), batch 1
+    void gemvPro(GGMLType qtype, const void* d_weights, const void* d_up_weights, const float* d_x, float* d_y,
+                 size_t rows, size_t cols, const HipGemvPrologue* pro) const {
+        hip_gemv_pro((int)qtype, d_weights, d_up_weights, d_x, d_y, (int)rows, (int)cols, pro, stream);
+    }
+    void gemvQkvPro(GGMLType qtype, const void* d_q_w, const void* d_k_w, const void* d_v_w, const float* d_x,
+                    float* d_q_out, float* d_k_out, float* d_v_out, size_t q_rows, size_t k_rows, size_t v_rows,
+                    size_t cols, const HipGemvPrologue* pro) const {
+        hip_gemv_qkv_pro((int)qtype, d_q_w, d_k_w, d_v_w, d_x, d_q_out, d_k_out, d_v_out, (int)q_rows,
+                         (int)k_rows, (int)v_rows, (int)cols, pro, stream);
+    }
 
     // cuda.zig:358-380
     void embedLookup(const void* d_weights, GGMLType qtype, uint32_t token_id, float* d_out, size_t dim,
