@@ -328,6 +328,10 @@ def weight_rows(qtype, rows, cols, seed=5):
         base = synth.q4_0_table(seed, 64, cols)
     elif qtype == B.Q8_0:
         base = synth.q8_0_table(seed, 64, cols)
+    elif qtype == B.Q4_K:
+        base = synth.q4_k_table(seed, 64, cols)
+    elif qtype == B.Q6_K:
+        base = synth.q6_k_table(seed, 64, cols)
     else:
         base = synth.bf16_table(seed, 64, cols)
     return base
@@ -362,8 +366,8 @@ def gemv_case(dev, name, qtype, shapes, fn, batch=1):
 
 
 def row_bytes(qtype, cols):
-    return {B.Q4_0: cols // 32 * 18, B.Q8_0: cols // 32 * 34, B.BF16: cols * 2, B.F16: cols * 2,
-            B.F32: cols * 4}[qtype]
+    return {B.Q4_0: cols // 32 * 18, B.Q8_0: cols // 32 * 34, B.Q4_K: cols // 256 * 144, B.Q6_K: cols // 256 * 210,
+            B.BF16: cols * 2, B.F16: cols * 2, B.F32: cols * 4}[qtype]
 
 
 def bench_gemv(dev):
@@ -383,6 +387,9 @@ def bench_gemv(dev):
         ("lm_head_q4_0", B.Q4_0, [(V, H)], plain(B.Q4_0, V, H), 1),
         ("lm_head_q8_0", B.Q8_0, [(V, H)], plain(B.Q8_0, V, H), 1),
         ("lm_head_bf16", B.BF16, [(V, H)], plain(B.BF16, V, H), 1),
+        ("lm_head_q4_k", B.Q4_K, [(V, H)], plain(B.Q4_K, V, H), 1),
+        ("lm_head_q6_k", B.Q6_K, [(V, H)], plain(B.Q6_K, V, H), 1),
+        ("down_q4_k", B.Q4_K, [(H, I)], plain(B.Q4_K, H, I), 1),
         ("gate_q4_0_b8", B.Q4_0, [(I, H)], plain(B.Q4_0, I, H, 8), 8),
     ]
     for name, qt, shapes, fn, batch in cases:

@@ -44,6 +44,7 @@ typedef void* HipEvent_t;     /* new: event handle for stream timing */
 #define HIP_BRIDGE_F16 1
 #define HIP_BRIDGE_Q4_0 2
 #define HIP_BRIDGE_Q8_0 8
+#define HIP_BRIDGE_Q4_K 12
 #define HIP_BRIDGE_Q6_K 14
 #define HIP_BRIDGE_BF16 30
 

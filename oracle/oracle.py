@@ -11,7 +11,7 @@ import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 
-F32, F16, Q4_0, Q8_0, Q6_K, BF16 = 0, 1, 2, 8, 14, 30
+F32, F16, Q4_0, Q8_0, Q4_K, Q6_K, BF16 = 0, 1, 2, 8, 12, 14, 30
 
 _fp = ctypes.POINTER(ctypes.c_float)
 _u16p = ctypes.POINTER(ctypes.c_uint16)
@@ -57,6 +57,8 @@ _SIGS = {
     "zo_dot_f32": (ctypes.c_float, [_fp, _fp, _sz]),
     "zo_dot_q8_0": (ctypes.c_float, [_u8p, _fp, _sz]),
     "zo_dot_q4_0": (ctypes.c_float, [_u8p, _fp, _sz]),
+    "zo_dot_q4_k": (ctypes.c_float, [_u8p, _fp, _sz]),
+    "zo_dot_q6_k": (ctypes.c_float, [_u8p, _fp, _sz]),
     "zo_dot_row": (ctypes.c_float, [_i, _u8p, _fp, _sz]),
     "zo_gemv": (_i, [_i, _u8p, _fp, _fp, _sz, _sz]),
     "zo_gemm": (_i, [_i, _u8p, _fp, _fp, _sz, _sz, _sz]),

@@ -104,7 +104,8 @@ void zo_f32_to_bf16_n(const float* src, uint16_t* dst, size_t n) {
 
 static inline uint16_t rd16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
 
-/* types.zig:113-116 (Q4_0, 18 B), 141-144 (Q8_0, 34 B), 187-192 (Q6_K, 210 B), 320-330. */
+/* types.zig:113-116 (Q4_0, 18 B), 141-144 (Q8_0, 34 B), 170-175 (Q4_K, 144 B), 187-192 (Q6_K,
+ * 210 B), 320-330. */
 size_t zo_row_bytes(int qtype, size_t n) {
     switch (qtype) {
         case ZO_F32: return n * 4;
@@ -112,6 +113,7 @@ size_t zo_row_bytes(int qtype, size_t n) {
         case ZO_BF16: return n * 2;
         case ZO_Q8_0: return (n / 32) * 34;
         case ZO_Q4_0: return (n / 32) * 18;
+        case ZO_Q4_K: return (n / 256) * 144;
         case ZO_Q6_K: return (n / 256) * 210;
         default: return 0;
     }
@@ -121,6 +123,7 @@ size_t zo_row_bytes(int qtype, size_t n) {
  *   F32 memcpy (414-426); F16 @floatCast (427-443); BF16 bits<<16 (444-450);
  *   Q8_0 f32(qs[i]) * f32(d) (quant.zig:73-79);
  *   Q4_0 f32(i32(nibble)-8) * d, low nibbles -> 0..15, high -> 16..31 (quant.zig:119-130);
+ *   Q4_K f32(q) * (d * scale_j) - dmin * min_j (quant.zig:276-309);
  *   Q6_K d * f32(scale) * f32(q) (quant.zig:357-385).
  * Returns -1 for any other type (the reference zero-fills, quant.zig:603-605). */
 int zo_dequantize_row(int qtype, const uint8_t* src, float* dst, size_t n) {
@@ -151,6 +154,31 @@ int zo_dequantize_row(int qtype, const uint8_t* src, float* dst, size_t n) {
                     int v1 = (int)((qs >> 4) & 0x0F) - 8;
                     dst[b * 32 + i] = (float)v0 * d;
                     dst[b * 32 + i + 16] = (float)v1 * d;
+                }
+            }
+            return 0;
+        case ZO_Q4_K:
+            for (size_t b = 0; b < n / 256; ++b) {
+                const uint8_t* blk = src + b * 144;
+                const float d = zo_f16_to_f32(rd16(blk)), dmin = zo_f16_to_f32(rd16(blk + 2));
+                const uint8_t* sc = blk + 4;
+                uint8_t scales[8], mins[8];
+                for (int j = 0; j < 4; ++j) {
+                    scales[j] = sc[j] & 63;
+                    mins[j] = sc[j + 4] & 63;
+                    scales[j + 4] = (uint8_t)((sc[j + 8] & 0x0F) | ((sc[j] >> 6) << 4));
+                    mins[j + 4] = (uint8_t)((sc[j + 8] >> 4) | ((sc[j + 4] >> 6) << 4));
+                }
+                const uint8_t* qs = blk + 16;
+                float* y = dst + b * 256;
+                for (int j = 0; j < 4; ++j) {
+                    const float d0 = d * (float)scales[2 * j], m0 = dmin * (float)mins[2 * j];
+                    const float d1 = d * (float)scales[2 * j + 1], m1 = dmin * (float)mins[2 * j + 1];
+                    for (int l = 0; l < 32; ++l) {
+                        const uint8_t q = qs[32 * j + l];
+                        y[64 * j + l] = (float)(q & 0x0F) * d0 - m0;
+                        y[64 * j + 32 + l] = (float)((q >> 4) & 0x0F) * d1 - m1;
+                    }
                 }
             }
             return 0;

@@ -26,6 +26,7 @@ enum {
     ZO_F16 = 1,
     ZO_Q4_0 = 2,
     ZO_Q8_0 = 8,
+    ZO_Q4_K = 12,
     ZO_Q6_K = 14,
     ZO_BF16 = 30,
 };
@@ -103,6 +104,8 @@ void zo_qk_norm_rope_kv(int dtype, void* q, const void* k, const void* v, const 
 float zo_dot_f32(const float* a, const float* b, size_t n);
 float zo_dot_q8_0(const uint8_t* row, const float* x, size_t n);
 float zo_dot_q4_0(const uint8_t* row, const float* x, size_t n);
+float zo_dot_q4_k(const uint8_t* row, const float* x, size_t n);
+float zo_dot_q6_k(const uint8_t* row, const float* x, size_t n);
 float zo_dot_row(int qtype, const uint8_t* row, const float* x, size_t cols);
 /* y[r] = dotRow(W[r], x), rows of zo_row_bytes(qtype, cols) bytes. */
 int zo_gemv(int qtype, const uint8_t* w, const float* x, float* y, size_t rows, size_t cols);

@@ -1,6 +1,7 @@
 /*
  * ziglm CPU oracle, part 2: dot products, GEMV, GEMM and decode attention (reference:
- * simonproyt/ziglm, src/math.zig:25-330, 652-846, 1088-1106; src/model.zig:658-700). TEST INFRASTRUCTURE ONLY (see ziglm_oracle.h): the
+ * simonproyt/ziglm, src/math.zig:25-330, 440-496, 556-616, 652-846, 1088-1106;
+ * src/model.zig:658-700). TEST INFRASTRUCTURE ONLY (see ziglm_oracle.h): the
  * checker for the HIP GEMV kernels; nothing in the product library uses it.
  *
  * Zig's @Vector(8|16, f32) arithmetic is restated with GCC vector extensions, built with
@@ -154,6 +155,92 @@ float zo_dot_q4_0(const uint8_t* row, const float* x, size_t n) {
     return red16(s0 + s1);
 }
 
+/* Q4_K 6-bit scale / min unpacking of a 144-byte super-block (math.zig:453-458,
+ * quant.zig:285-290). */
+static void q4k_scales(const uint8_t* sc, uint8_t* scales, uint8_t* mins) {
+    for (int j = 0; j < 4; ++j) {
+        scales[j] = sc[j] & 63;
+        mins[j] = sc[j + 4] & 63;
+        scales[j + 4] = (uint8_t)((sc[j + 8] & 0x0F) | ((sc[j] >> 6) << 4));
+        mins[j + 4] = (uint8_t)((sc[j + 8] >> 4) | ((sc[j + 4] >> 6) << 4));
+    }
+}
+
+/* math.zig:440-496 dotQ4_KF32: 144-byte super-blocks {f16 d, f16 dmin, scales[12], qs[128]};
+ * 16-lane accumulator: total += (q0*(d*sc) - dmin*m) * b0 + (q1*(d*sc') - dmin*m') * b1. */
+float zo_dot_q4_k(const uint8_t* row, const float* x, size_t n) {
+    v16f total = {0};
+    for (size_t b = 0; b < n / 256; ++b) {
+        const uint8_t* blk = row + b * 144;
+        const float d = zo_f16_to_f32(rd16(blk)), dmin = zo_f16_to_f32(rd16(blk + 2));
+        uint8_t scales[8], mins[8];
+        q4k_scales(blk + 4, scales, mins);
+        const uint8_t* qs = blk + 16;
+        const float* xb = x + 256 * b;
+        for (int j = 0; j < 4; ++j) {
+            v16f vd0, vm0, vd1, vm1;
+            const float d0 = d * (float)scales[2 * j], m0 = dmin * (float)mins[2 * j];
+            const float d1 = d * (float)scales[2 * j + 1], m1 = dmin * (float)mins[2 * j + 1];
+            for (int k = 0; k < 16; ++k) {
+                vd0[k] = d0;
+                vm0[k] = m0;
+                vd1[k] = d1;
+                vm1[k] = m1;
+            }
+            for (int half = 0; half < 2; ++half) {
+                const int off = half * 16;
+                v16f q0, q1;
+                for (int k = 0; k < 16; ++k) {
+                    const uint8_t q = qs[32 * j + off + k];
+                    q0[k] = (float)(q & 0x0F);
+                    q1[k] = (float)(q >> 4);
+                }
+                const v16f b0 = ld16f(xb + 64 * j + off), b1 = ld16f(xb + 64 * j + 32 + off);
+                total += (q0 * vd0 - vm0) * b0 + (q1 * vd1 - vm1) * b1;
+            }
+        }
+    }
+    return red16(total);
+}
+
+/* math.zig:556-616 dotQ6_KF32: 210-byte super-blocks {ql[128], qh[64], int8 scales[16],
+ * f16 d}; total += ((q1*s1)*b1 + (q2*s2)*b2 + (q3*s3)*b3 + (q4*s4)*b4) * d. */
+float zo_dot_q6_k(const uint8_t* row, const float* x, size_t n) {
+    v16f total = {0};
+    for (size_t b = 0; b < n / 256; ++b) {
+        const uint8_t* blk = row + b * 210;
+        const uint8_t* ql = blk;
+        const uint8_t* qh = blk + 128;
+        const int8_t* sc = (const int8_t*)(blk + 192);
+        const float d = zo_f16_to_f32(rd16(blk + 208));
+        v16f vd;
+        for (int k = 0; k < 16; ++k) vd[k] = d;
+        const float* xb = x + 256 * b;
+        for (int nn = 0; nn < 2; ++nn) {
+            for (int chunk = 0; chunk < 2; ++chunk) {
+                const int l0 = chunk * 16, is = chunk;
+                v16f q1, q2, q3, q4, s1, s2, s3, s4;
+                for (int k = 0; k < 16; ++k) {
+                    const int l = l0 + k;
+                    const uint8_t a = ql[nn * 64 + l], a32 = ql[nn * 64 + l + 32], h = qh[nn * 32 + l];
+                    q1[k] = (float)((int)((a & 0x0F) | (((h >> 0) & 3) << 4)) - 32);
+                    q2[k] = (float)((int)((a32 & 0x0F) | (((h >> 2) & 3) << 4)) - 32);
+                    q3[k] = (float)((int)((a >> 4) | (((h >> 4) & 3) << 4)) - 32);
+                    q4[k] = (float)((int)((a32 >> 4) | (((h >> 6) & 3) << 4)) - 32);
+                    s1[k] = (float)sc[nn * 8 + is + 0];
+                    s2[k] = (float)sc[nn * 8 + is + 2];
+                    s3[k] = (float)sc[nn * 8 + is + 4];
+                    s4[k] = (float)sc[nn * 8 + is + 6];
+                }
+                const float* bp = xb + nn * 128 + l0;
+                const v16f b1 = ld16f(bp), b2 = ld16f(bp + 32), b3 = ld16f(bp + 64), b4 = ld16f(bp + 96);
+                total += (q1 * s1 * b1 + q2 * s2 * b2 + q3 * s3 * b3 + q4 * s4 * b4) * vd;
+            }
+        }
+    }
+    return red16(total);
+}
+
 /* math.zig:652-708 dotRow for the types the GPU GEMV supports. */
 float zo_dot_row(int qtype, const uint8_t* row, const float* x, size_t cols) {
     switch (qtype) {
@@ -172,6 +259,8 @@ float zo_dot_row(int qtype, const uint8_t* row, const float* x, size_t cols) {
         case ZO_BF16: return dot_half(row, x, cols, 1);
         case ZO_Q8_0: return zo_dot_q8_0(row, x, cols);
         case ZO_Q4_0: return zo_dot_q4_0(row, x, cols);
+        case ZO_Q4_K: return zo_dot_q4_k(row, x, cols);
+        case ZO_Q6_K: return zo_dot_q6_k(row, x, cols);
         default: return 0.0f;
     }
 }

@@ -20,7 +20,8 @@ from tol import assert_bitexact, assert_rel
 
 pytestmark = pytest.mark.gpu
 
-QTYPES = [B.Q4_0, B.Q8_0, B.BF16, B.F16, B.F32]
+QTYPES = [B.Q4_0, B.Q8_0, B.Q4_K, B.Q6_K, B.BF16, B.F16, B.F32]
+K_QUANTS = (B.Q4_K, B.Q6_K)
 
 
 def run_gemm(dev, qtype, raw, X, rows, cols, batch):
@@ -39,6 +40,8 @@ def run_gemm(dev, qtype, raw, X, rows, cols, batch):
 @pytest.mark.parametrize("rows,cols,batch", [(37, 2560, 1), (16, 96, 1), (9, 10240, 1), (11, 512, 2),
                                              (13, 2560, 3), (6, 256, 7)])
 def test_gemv_integer_bitexact(dev, qtype, rows, cols, batch):
+    if qtype in K_QUANTS and cols % 256:
+        pytest.skip("super-block types need cols % 256 == 0")
     raw, wd = int_matrix(qtype, rows, cols, seed=rows * cols + qtype, scale_pow=-1)
     X = np.random.default_rng(rows).integers(-3, 4, (batch, cols)).astype(np.float32)
     exact = X.astype(np.float64) @ wd.T
@@ -84,6 +87,14 @@ def test_gemv_mirrors_and_misaligned_paths(dev, oracle):
     d_wb.at(2).upload(rawb.reshape(-1))
     dev.gemv(B.BF16, d_wb.at(2), dev.from_numpy(xb), d_y, rows, 1000)
     assert np.all(np.abs(d_y.to_numpy((rows,), np.float32) - wdb @ xb.astype(np.float64)) <= bound(wdb, xb))
+    # K-quant rows below their load alignment (Q4_K: 4 bytes, Q6_K: 2 bytes): scalar kernel
+    d_xk = dev.from_numpy(x)
+    for qt, off in ((B.Q4_K, 2), (B.Q6_K, 1)):
+        rawk, wdk = random_matrix(qt, rows, cols, seed=5)
+        d_wk = dev.alloc(rawk.nbytes + 16)
+        d_wk.at(off).upload(rawk.reshape(-1))
+        dev.gemv(qt, d_wk.at(off), d_xk, d_y, rows, cols)
+        assert np.all(np.abs(d_y.to_numpy((rows,), np.float32) - wdk @ x.astype(np.float64)) <= bound(wdk, x)), qt
 
 
 @pytest.mark.parametrize("q_rows,k_rows,v_rows", [(2048, 1024, 1024), (13, 0, 6), (0, 5, 3)])
@@ -131,7 +142,7 @@ def test_gemv_unsupported_qtype_is_noop(dev):
     d_y.fill(0x11)
     dev.strict = False
     try:
-        dev.gemv(12, d_w, d_x, d_y, 4, 256)  # Q4_K: not supported here
+        dev.gemv(13, d_w, d_x, d_y, 4, 256)  # Q5_K: not supported here
         assert dev.b.last_error() == B.EUNSUPPORTED
     finally:
         dev.strict = True

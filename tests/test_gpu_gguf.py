@@ -38,6 +38,10 @@ GEMMA4 = S.GgufModelConfig(arch="gemma4", dim=256, n_layers=20, n_heads=8, n_kv_
 GEMMA2 = S.GgufModelConfig(arch="gemma2", dim=256, n_layers=3, n_heads=4, n_kv_heads=2, head_dim=128,
                            global_every=0, inter=512, vocab=1024, ple=False, norm_type=B.BF16, tile_rows=0,
                            types={"up": B.BF16})
+# a Q4_K_M-like mix: K-quant projections, Q6_K embedding / LM head and down projection
+GEMMA2K = S.GgufModelConfig(arch="gemma2", dim=512, n_layers=2, n_heads=4, n_kv_heads=2, head_dim=128,
+                            global_every=0, inter=1024, vocab=1024, ple=False, tile_rows=0, weight_type=B.Q4_K,
+                            types={"emb": B.Q6_K, "down": B.Q6_K, "v": B.Q6_K})
 
 
 def gguf_bytes(cfg, seed=9):
@@ -146,9 +150,9 @@ def test_loader_rejects_bad_tables(dev):
     with G.GGUFFile.from_buffer(w.tobytes()) as f:
         with pytest.raises(Exception, match="ffn_down"):
             Model.from_gguf(dev, f)
-    # a matrix type the GEMV kernels do not take
+    # a matrix type the GEMV kernels do not take (Q5_K)
     w = S.build(cfg)
-    w.infos = [(n, 12 if n == "blk.0.attn_q.weight" else t, s, d) for n, t, s, d in w.infos]
+    w.infos = [(n, 13 if n == "blk.0.attn_q.weight" else t, s, d) for n, t, s, d in w.infos]
     with G.GGUFFile.from_buffer(w.tobytes()) as f:
         with pytest.raises(Exception, match="attn_q"):
             Model.from_gguf(dev, f)
@@ -177,7 +181,7 @@ FUSE_IDS = ["default", "unfused", "prologues"]
 
 
 @pytest.mark.parametrize("fused", FUSE_SETS, ids=FUSE_IDS)
-@pytest.mark.parametrize("cfg", [GEMMA4, GEMMA2], ids=["gemma4", "gemma2"])
+@pytest.mark.parametrize("cfg", [GEMMA4, GEMMA2, GEMMA2K], ids=["gemma4", "gemma2", "gemma2_kquants"])
 def test_decode_loaded_model_vs_oracle(dev, oracle, cfg, fused):
     data = gguf_bytes(cfg)
     ref = MR.RefModel(oracle, data, max_seq=32)

@@ -30,17 +30,13 @@ def f32_table(seed, rows, cols):
 
 
 def q6k_table(seed, rows, cols):
-    nsb = cols // 256
-    raw = synth.uniform_int(seed, "q6k", (rows, nsb, 210), 0, 255).astype(np.uint8)
-    d = synth.f16_bits(synth.uniform_f32(seed, "q6k.d", (rows, nsb), 1e-3, 2e-2))
-    raw[:, :, 208:210] = d.reshape(rows, nsb, 1).view(np.uint8).reshape(rows, nsb, 2)
-    return raw.reshape(rows, nsb * 210)
+    return synth.q6_k_table(seed, rows, cols)
 
 
 def make_table(qtype, seed, rows, cols):
     return {
         B.Q8_0: synth.q8_0_table, B.Q4_0: synth.q4_0_table, B.BF16: synth.bf16_table,
-        B.F16: f16_table, B.F32: f32_table, B.Q6_K: q6k_table,
+        B.F16: f16_table, B.F32: f32_table, B.Q6_K: q6k_table, B.Q4_K: synth.q4_k_table,
     }[qtype](seed, rows, cols)
 
 
@@ -54,7 +50,8 @@ def make_table(qtype, seed, rows, cols):
                                        (B.BF16, 2562), (B.F32, 100),
                                        # partial last segment / byte-staged rows
                                        (B.Q8_0, 5376), (B.Q4_0, 5376), (B.Q6_K, 5376),
-                                       (B.BF16, 5376), (B.Q8_0, 800), (B.F16, 1000)])
+                                       (B.BF16, 5376), (B.Q8_0, 800), (B.F16, 1000),
+                                       (B.Q4_K, 2560), (B.Q4_K, 5376), (B.Q4_K, 256)])
 def test_embed_gather_bitexact(dev, oracle, qtype, dim, out_dtype):
     vocab = 700
     table = make_table(qtype, 2, vocab, dim)
@@ -78,7 +75,7 @@ def test_embed_gather_bitexact(dev, oracle, qtype, dim, out_dtype):
 
 
 @pytest.mark.parametrize("qtype,offset", [(B.Q8_0, 1), (B.Q4_0, 1), (B.Q8_0, 2), (B.Q4_0, 6),
-                                          (B.BF16, 2), (B.F16, 6), (B.F32, 4), (B.Q6_K, 8)])
+                                          (B.BF16, 2), (B.F16, 6), (B.F32, 4), (B.Q6_K, 8), (B.Q4_K, 1)])
 @pytest.mark.parametrize("out_dtype", [B.F32, B.BF16])
 def test_embed_gather_misaligned_table(dev, oracle, qtype, offset, out_dtype):
     """Tables at an odd or non-16-byte address take the byte-staged / scalar paths."""
@@ -100,7 +97,7 @@ def test_embed_gather_misaligned_table(dev, oracle, qtype, offset, out_dtype):
                         f"bf16-out qtype={qtype} +{offset}")
 
 
-@pytest.mark.parametrize("qtype", [B.Q8_0, B.Q4_0, B.BF16, B.Q6_K])
+@pytest.mark.parametrize("qtype", [B.Q8_0, B.Q4_0, B.BF16, B.Q6_K, B.Q4_K])
 def test_embed_lookup_mirrors(dev, oracle, qtype):
     vocab, dim = 300, 2560
     table = make_table(qtype, 5, vocab, dim)
@@ -123,7 +120,7 @@ def test_gather_unsupported_qtype_is_noop(dev):
     d_out.fill(0x11)
     dev.strict = False
     try:
-        dev.embedLookupBatch(d_tab, 12, d_ids, d_out, 1, 256, 1.0)  # Q4_K: not supported
+        dev.embedLookupBatch(d_tab, 13, d_ids, d_out, 1, 256, 1.0)  # Q5_K: not supported
         assert dev.b.last_error() == B.EUNSUPPORTED
     finally:
         dev.strict = True

@@ -18,7 +18,7 @@ import pytest
 from oracle import oracle as O
 from ziglm_amd import synth
 
-QTYPES = [O.Q4_0, O.Q8_0, O.BF16, O.F16, O.F32]
+QTYPES = [O.Q4_0, O.Q8_0, O.Q4_K, O.Q6_K, O.BF16, O.F16, O.F32]
 
 
 @pytest.fixture(scope="module")
@@ -48,6 +48,10 @@ def int_matrix(qtype, rows, cols, seed, scale_pow=0):
         raw[:, :, 0:2] = f16_bytes(d)
         raw[:, :, 2:] = (qb[:, :, :16] | (qb[:, :, 16:] << 4)).astype(np.uint8)
         return raw.reshape(rows, -1), (q - 8) * d
+    if qtype == O.Q4_K:
+        return q4_k_encode(rng, rows, cols, d)
+    if qtype == O.Q6_K:
+        return q6_k_encode(rng, rows, cols, d)
     w = rng.integers(-100, 101, (rows, cols)).astype(np.float64) * d
     if qtype == O.F32:
         return w.astype(np.float32).view(np.uint8).reshape(rows, -1), w
@@ -55,6 +59,65 @@ def int_matrix(qtype, rows, cols, seed, scale_pow=0):
         return w.astype(np.float16).view(np.uint8).reshape(rows, -1), w
     bits = (w.astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)  # exact: small ints
     return bits.view(np.uint8).reshape(rows, -1), w
+
+
+def q4_k_encode(rng, rows, cols, d):
+    """Q4_K rows from intended values, packed by the GGUF format description (not by
+    inverting the decoder): a 256-column super-block is {f16 d, f16 dmin, 12 scale bytes,
+    128 quant bytes}; column c of a super-block belongs to 32-column sub-block j = c // 32,
+    whose value is q * (d * sc_j) - dmin * m_j with 6-bit sc_j, m_j; the quant byte of c is
+    qs[32 (j // 2) + c % 32], low nibble for even j, high for odd j; sc_j, m_j for j < 4 are
+    the low 6 bits of bytes j and j + 4, for j >= 4 the low / high nibble of byte j + 4 with
+    their top 2 bits in bits 6-7 of bytes j - 4 / j. Scales and mins are kept small so every
+    integer sum stays exact in f32."""
+    nsb = cols // 256
+    q = rng.integers(0, 16, (rows, nsb, 8, 32))
+    sc = rng.integers(0, 8, (rows, nsb, 8))
+    sc[..., 4:] |= rng.integers(0, 2, (rows, nsb, 4)) << 4   # exercise the high bits of j >= 4
+    sc[..., 4:] = np.minimum(sc[..., 4:], 23)
+    mn = rng.integers(0, 8, (rows, nsb, 8))
+    mn[..., 4:] |= rng.integers(0, 2, (rows, nsb, 4)) << 4
+    mn[..., 4:] = np.minimum(mn[..., 4:], 23)
+    dmin = np.float64(d) / 2
+    raw = np.zeros((rows, nsb, 144), np.uint8)
+    raw[..., 0:2] = f16_bytes(d)
+    raw[..., 2:4] = f16_bytes(dmin)
+    b = np.zeros((rows, nsb, 12), np.int64)
+    for j in range(4):
+        b[..., j] = (sc[..., j] & 63) | ((sc[..., j + 4] >> 4) << 6)
+        b[..., j + 4] = (mn[..., j] & 63) | ((mn[..., j + 4] >> 4) << 6)
+        b[..., j + 8] = (sc[..., j + 4] & 15) | ((mn[..., j + 4] & 15) << 4)
+    raw[..., 4:16] = b.astype(np.uint8)
+    for jj in range(4):
+        raw[..., 16 + 32 * jj:48 + 32 * jj] = (q[:, :, 2 * jj] | (q[:, :, 2 * jj + 1] << 4)).astype(np.uint8)
+    val = q * (d * sc[..., None]) - dmin * mn[..., None]
+    return raw.reshape(rows, -1), val.reshape(rows, cols).astype(np.float64)
+
+
+def q6_k_encode(rng, rows, cols, d):
+    """Q6_K rows from intended values, packed by the format description: a 256-column
+    super-block is {ql[128], qh[64], int8 scales[16], f16 d}; column c has value
+    d * scales[c // 16] * (u - 32), u a 6-bit code whose low 4 bits sit in ql and top 2 bits in
+    qh: with h = c // 128, i = c % 128, l = i % 32 and quadrant k = i // 32, the low bits are
+    nibble (k // 2) of ql[64 h + 32 (k % 2) + l] and the top bits are bits 2k, 2k + 1 of
+    qh[32 h + l]."""
+    nsb = cols // 256
+    u = rng.integers(0, 64, (rows, nsb, 256))
+    sc = rng.integers(-8, 8, (rows, nsb, 16))
+    raw = np.zeros((rows, nsb, 210), np.uint8)
+    ql = np.zeros((rows, nsb, 128), np.int64)
+    qh = np.zeros((rows, nsb, 64), np.int64)
+    for c in range(256):
+        h, i = divmod(c, 128)
+        k, l = divmod(i, 32)
+        ql[..., 64 * h + 32 * (k % 2) + l] |= (u[..., c] & 15) << (4 * (k // 2))
+        qh[..., 32 * h + l] |= (u[..., c] >> 4) << (2 * k)
+    raw[..., 0:128] = ql.astype(np.uint8)
+    raw[..., 128:192] = qh.astype(np.uint8)
+    raw[..., 192:208] = sc.astype(np.int8).view(np.uint8)
+    raw[..., 208:210] = f16_bytes(d)
+    val = d * np.repeat(sc, 16, axis=-1) * (u - 32)
+    return raw.reshape(rows, -1), val.reshape(rows, cols).astype(np.float64)
 
 
 def random_matrix(qtype, rows, cols, seed):
@@ -65,6 +128,10 @@ def random_matrix(qtype, rows, cols, seed):
         raw = synth.q4_0_table(seed, rows, cols)
     elif qtype == O.BF16:
         raw = synth.bf16_table(seed, rows, cols)
+    elif qtype == O.Q4_K:
+        raw = synth.q4_k_table(seed, rows, cols)
+    elif qtype == O.Q6_K:
+        raw = synth.q6_k_table(seed, rows, cols)
     elif qtype == O.F16:
         raw = synth.f16_bits(synth.normal_f32(seed, "w16", (rows, cols), 0, 0.05)).view(np.uint8).reshape(rows, -1)
     else:
@@ -86,6 +153,8 @@ def bound(wd, x):
 def test_dot_integer_closed_form(o, qtype, cols):
     if qtype in (O.Q4_0, O.Q8_0) and cols % 32:
         pytest.skip("block types need cols % 32 == 0")
+    if qtype in (O.Q4_K, O.Q6_K) and cols % 256:
+        pytest.skip("super-block types need cols % 256 == 0")
     for p in (0, -1, 3):
         raw, wd = int_matrix(qtype, 5, cols, seed=cols + p + 100 * qtype, scale_pow=p)
         x = np.random.default_rng(cols).integers(-3, 4, cols).astype(np.float32)
@@ -117,6 +186,19 @@ def test_q4_0_nibble_order_single_element(o):
         blk[1, 2 + byte] = 0xC8 if e >= 16 else 0x8C  # that nibble 12 -> weight 4
         y = o.dot_row(O.Q4_0, blk.reshape(-1), x)
         assert y == 4.0 * x[32 + e], (e, y)
+
+
+def test_k_quant_dequant_matches_encoder(o):
+    """The dequantisation (quant.zig:276-309, 357-385) returns the values the format-level
+    encoders above intended, element for element (Q4_K: every scale / min byte position,
+    both nibbles; Q6_K: every quadrant, both qh bit pairs, signed scales)."""
+    rng = np.random.default_rng(5)
+    for qt, enc in ((O.Q4_K, q4_k_encode), (O.Q6_K, q6_k_encode)):
+        for d in (1.0, 0.5, 8.0):
+            raw, val = enc(rng, 3, 512, d)
+            for r in range(3):
+                got = o.dequantize_row(qt, raw[r], 512).astype(np.float64)
+                np.testing.assert_array_equal(got, val[r], err_msg=f"qtype {qt} d {d} row {r}")
 
 
 def test_q8_0_sign_and_scale(o):

@@ -12,7 +12,7 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 # HIP_BRIDGE_LIB selects another build of the same library (e.g. for A/B measurements).
 LIB_PATH = os.environ.get("HIP_BRIDGE_LIB") or os.path.join(PKG, "libhip_bridge.so")
 
-F32, F16, Q4_0, Q8_0, Q6_K, BF16 = 0, 1, 2, 8, 14, 30
+F32, F16, Q4_0, Q8_0, Q4_K, Q6_K, BF16 = 0, 1, 2, 8, 12, 14, 30
 OK, EINVAL, EUNSUPPORTED = 0, -1, -2
 
 _v = ctypes.c_void_p

@@ -254,12 +254,19 @@ static void launch_g(const AttnArgs& a, hipStream_t s) {
 #ifndef ZL_ATTN_GW
 #define ZL_ATTN_GW 0
 #endif
+// Only while the K/V rows the call can touch stay cache-resident (<= 32 MB: a 4096-position
+// f32 cache of 8 heads x 256, say); longer contexts re-read them from HBM per head group, so
+// every workgroup takes all heads (Gemma-4B heads at positions ~U[0, 32767], B = 1: 49.7 us
+// with all heads, 70.4 us with one head per workgroup).
 constexpr int64_t kFewGroups = 16;
-static void choose_heads(AttnArgs& a) {
+constexpr double kKvResidentBytes = 32.0 * (1 << 20);
+static void choose_heads(AttnArgs& a, int es) {
     a.gq = a.nh / a.nkv;
+    const int len = a.window > 0 ? std::min(a.window, a.max_len) : a.max_len;
+    const double kv = (double)a.batch * len * a.nkv * a.D * 2.0 * es;
     int gw = a.gq;
     if (ZL_ATTN_GW > 0) gw = std::min(a.gq, ZL_ATTN_GW);
-    else if ((int64_t)a.batch * a.nkv < kFewGroups) gw = 1;
+    else if ((int64_t)a.batch * a.nkv < kFewGroups && kv <= kKvResidentBytes) gw = 1;
     a.hg = a.gq / gw;
 }
 
@@ -295,7 +302,7 @@ static void launch_attn(int kv_dtype, AttnArgs& a, size_t ws_bytes, hipStream_t 
         return;
     }
     a.inv_cap = a.softcap > 0.0f ? 1.0f / a.softcap : 0.0f;
-    choose_heads(a);
+    choose_heads(a, kv_dtype == HIP_BRIDGE_BF16 ? 2 : 4);
     choose_split(a, ws_bytes);
     if ((int64_t)a.batch * a.nkv * a.hg * a.nsplit > INT32_MAX) {
         set_error(HIP_BRIDGE_EUNSUPPORTED);
@@ -350,9 +357,13 @@ size_t hip_attention_workspace_bytes(int batch, int n_heads, int n_kv_heads, int
     a.window = sliding_window;
     a.ws = reinterpret_cast<float*>(16);  // any non-null pointer: size for the unconstrained split
     if (n_heads % n_kv_heads != 0) return 0;
-    choose_heads(a);
-    choose_split(a, SIZE_MAX);
-    return a.nsplit > 1 ? (size_t)batch * n_heads * a.nsplit * (head_dim + 2) * sizeof(float) : 0;
+    size_t need = 0;
+    for (int es : {2, 4}) {  // the head grouping (and so the split) depends on the cache type
+        choose_heads(a, es);
+        choose_split(a, SIZE_MAX);
+        if (a.nsplit > 1) need = std::max(need, (size_t)batch * n_heads * a.nsplit * (head_dim + 2) * sizeof(float));
+    }
+    return need;
 }
 
 void hip_attention_decode(int kv_dtype, const float* q, const void* k_cache, const void* v_cache, float* out,

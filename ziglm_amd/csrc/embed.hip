@@ -3,9 +3,9 @@
 // Arithmetic is ziglm's CPU order (quant.zig:73-79, 119-130, 357-385, 413-512 and
 // model.zig:494-503): out = fl(fl(f32(q) * d) * scale). For Q8_0/Q4_0 q*d is exact, so every
 // output is one IEEE rounding and the result is bit-exact; Q6_K keeps the CPU's
-// ((d * scale_j) * q) * scale order.
+// ((d * scale_j) * q) * scale order and Q4_K its (q * (d * sc_j) - dmin * m_j) * scale.
 //
-// Layout: one wave per segment of 512 consecutive outputs of one row (2048 for Q6_K), four
+// Layout: one wave per segment of 512 consecutive outputs of one row (2048 for K-quants), four
 // independent waves per workgroup (no block barrier): a 4096-token gather is ~20k waves.
 // Every lane produces 16 bytes of output per step (4 f32 or 8 bf16), so each store
 // instruction of a wave writes 1 KB of whole, contiguous cache lines.
@@ -14,7 +14,8 @@
 // before the first use; the lanes of a wave read a contiguous span of the row, so the
 // loads coalesce into that span's cache lines (measured on MI355X at 4096 x 2560: 9.4 us
 // against 12.9 us for staging the row through LDS first).
-// Q6_K (210 B super-blocks): the segment (8 super-blocks) is staged in LDS, then decoded.
+// Q6_K / Q4_K (210 / 144 B super-blocks): the segment (8 super-blocks) is staged in LDS, then
+// decoded.
 // Dense types (F32, F16, BF16): each lane converts the elements behind its 16-byte stores,
 // all loads issued before the first store.
 #include "zl_common.h"
@@ -72,6 +73,32 @@ __device__ __forceinline__ void dequant(const unsigned char* row, int e, float s
             v[2 * j] = ((float)q0 * d) * scale;
             v[2 * j + 1] = ((float)q1 * d) * scale;
         }
+    } else if constexpr (QT == HIP_BRIDGE_Q4_K) {
+        // Q4_K super-block of 256: d, dmin (f16), scales[12] (packed 6-bit scales / mins),
+        // qs[128] = 144 B (types.zig:170-175); element order and arithmetic as
+        // quant.zig:276-309: f32(q) * (d * sc_j) - dmin * m_j, then * scale.
+        const unsigned char* sb = row + (e >> 8) * 144;
+        const float d = f16_bits_to_f32(lds_u16(sb)), dmin = f16_bits_to_f32(lds_u16(sb + 2));
+        const int w = e & 255;
+        const int jj = w >> 6;            // pair of 32-element sub-blocks sharing qs[32 jj ..]
+        const int hi = (w >> 5) & 1;      // high nibbles: the pair's second sub-block
+        const int j = 2 * jj + hi;        // sub-block 0..7
+        const unsigned char* sc = sb + 4;
+        int s6, m6;
+        if (j < 4) {
+            s6 = sc[j] & 63;
+            m6 = sc[j + 4] & 63;
+        } else {
+            s6 = (sc[j + 4] & 0x0F) | ((sc[j - 4] >> 6) << 4);
+            m6 = (sc[j + 4] >> 4) | ((sc[j] >> 6) << 4);
+        }
+        const float dj = d * (float)s6, mj = dmin * (float)m6;
+        const unsigned char* qs = sb + 16 + 32 * jj + (w & 31);
+#pragma unroll
+        for (int k = 0; k < N; ++k) {
+            const int q = hi ? (qs[k] >> 4) : (qs[k] & 0x0F);
+            v[k] = ((float)q * dj - mj) * scale;
+        }
     } else {
         // Q6_K super-block of 256: ql[128] qh[64] scales[16] (int8) d (f16) = 210 B
         // (types.zig:187-192); element order as quant.zig:357-385.
@@ -99,16 +126,16 @@ __device__ __forceinline__ void dequant(const unsigned char* row, int e, float s
 
 template <int QT>
 __host__ __device__ constexpr int64_t block_bytes() {
-    return QT == HIP_BRIDGE_Q8_0 ? 34 : QT == HIP_BRIDGE_Q4_0 ? 18 : 210;
+    return QT == HIP_BRIDGE_Q8_0 ? 34 : QT == HIP_BRIDGE_Q4_0 ? 18 : QT == HIP_BRIDGE_Q4_K ? 144 : 210;
 }
 template <int QT>
 __host__ __device__ constexpr int block_elems() {
-    return QT == HIP_BRIDGE_Q6_K ? 256 : 32;
+    return QT == HIP_BRIDGE_Q6_K || QT == HIP_BRIDGE_Q4_K ? 256 : 32;
 }
 
 template <int QT>
 __host__ __device__ constexpr int seg_elems() {
-    return QT == HIP_BRIDGE_Q6_K ? 2048 : 512;
+    return QT == HIP_BRIDGE_Q6_K || QT == HIP_BRIDGE_Q4_K ? 2048 : 512;
 }
 
 __device__ __forceinline__ uint32_t ldg_u16(const unsigned char* p) {
@@ -371,6 +398,7 @@ static int64_t row_bytes_of(int qtype, int dim) {
         case HIP_BRIDGE_BF16: return (int64_t)dim * 2;
         case HIP_BRIDGE_Q8_0: return dim % 32 ? -1 : (int64_t)(dim / 32) * 34;
         case HIP_BRIDGE_Q4_0: return dim % 32 ? -1 : (int64_t)(dim / 32) * 18;
+        case HIP_BRIDGE_Q4_K: return dim % 256 ? -1 : (int64_t)(dim / 256) * 144;
         case HIP_BRIDGE_Q6_K: return dim % 256 ? -1 : (int64_t)(dim / 256) * 210;
         default: return -1;
     }
@@ -452,6 +480,9 @@ static void gather(const void* table, int qtype, int64_t n_rows, const int32_t* 
         case HIP_BRIDGE_Q6_K:
             if (!block_ok) break;
             return launch_blocks<HIP_BRIDGE_Q6_K, OutT>(table, ids, single_id, out, n_rows, n_tokens, dim, scale, s);
+        case HIP_BRIDGE_Q4_K:
+            if (!block_ok) break;
+            return launch_blocks<HIP_BRIDGE_Q4_K, OutT>(table, ids, single_id, out, n_rows, n_tokens, dim, scale, s);
         case HIP_BRIDGE_F32:
             return launch_dense<HIP_BRIDGE_F32, OutT>(table, ids, single_id, out, n_rows, n_tokens, dim, scale, s);
         case HIP_BRIDGE_F16:

@@ -176,12 +176,110 @@ struct WGroup {
     }
 };
 
+__device__ __forceinline__ uint32_t ldw32(const unsigned char* p) {
+    return *reinterpret_cast<const uint32_t*>(p);
+}
+
+__device__ __forceinline__ float dot4u(uint32_t u, const f32x4& x) {
+    // sum_k byte_k(u) * x_k, each byte through v_cvt_f32_ubyteN
+    float t = (float)(u & 0xff) * x.x;
+    t = fmaf((float)((u >> 8) & 0xff), x.y, t);
+    t = fmaf((float)((u >> 16) & 0xff), x.z, t);
+    return fmaf((float)(u >> 24), x.w, t);
+}
+
+__device__ __forceinline__ float sum4(const f32x4& x) { return (x.x + x.y) + (x.z + x.w); }
+
+// Q4_K: 144-byte super-blocks {f16 d, f16 dmin, scales[12] (packed 6-bit scales and mins),
+// qs[128]} (types.zig:170-175), rows 4-byte aligned. Group g: super-block g/32; r = g%32,
+// jj = r/8 picks the 32-byte qs span shared by sub-blocks 2jj (low nibbles) and 2jj+1 (high
+// nibbles), o = 4*(r%8) the lane's 4 bytes, i.e. columns [64jj+o, +4) and [64jj+32+o, +4)
+// of the super-block (the same low/high split as Q4_0 blocks). Value of a nibble q of
+// sub-block j: q * (d * sc_j) - dmin * m_j (math.zig:440-496), summed here as
+// (d*sc_j) * sum(q x) - (dmin*m_j) * sum(x).
+template <>
+struct WGroup<HIP_BRIDGE_Q4_K> {
+    uint32_t dm, s0, s1, s2, q, jj;
+    __device__ __forceinline__ void load(const unsigned char* row, uint32_t g) {
+        const uint32_t base = (g >> 5) * 144u, r = g & 31u;
+        jj = r >> 3;
+        dm = ldw32(row + base);
+        s0 = ldw32(row + (base + 4u));
+        s1 = ldw32(row + (base + 8u));
+        s2 = ldw32(row + (base + 12u));
+        q = ldw32(row + (base + 16u + 32u * jj + 4u * (r & 7u)));
+    }
+    __device__ __forceinline__ float dot(const f32x4& xa, const f32x4& xb, float) const {
+        // scale / min bytes of sub-blocks 2jj and 2jj+1 (quant.zig:285-290): bytes t, t+1
+        // (t = 2 (jj & 1)) of the three scale words
+        const uint32_t sh = (jj & 1u) * 16u;
+        const uint32_t A = s0 >> sh, Bw = s1 >> sh, C = s2 >> sh;
+        uint32_t sc0, sc1, m0, m1;
+        if (jj < 2) {
+            sc0 = A & 63u;
+            sc1 = (A >> 8) & 63u;
+            m0 = Bw & 63u;
+            m1 = (Bw >> 8) & 63u;
+        } else {
+            sc0 = (C & 15u) | (((A >> 6) & 3u) << 4);
+            sc1 = ((C >> 8) & 15u) | (((A >> 14) & 3u) << 4);
+            m0 = ((C >> 4) & 15u) | (((Bw >> 6) & 3u) << 4);
+            m1 = ((C >> 12) & 15u) | (((Bw >> 14) & 3u) << 4);
+        }
+        const float d = h2f(dm & 0xffffu), dmin = h2f(dm >> 16);
+        const float d0 = d * (float)sc0, d1 = d * (float)sc1;
+        const float n0 = dmin * (float)m0, n1 = dmin * (float)m1;
+        const float ta = dot4u(mask_bytes(q, 0x0f0f0f0fu), xa);
+        const float tb = dot4u(mask_bytes(q >> 4, 0x0f0f0f0fu), xb);
+        return fmaf(d0, ta, -(n0 * sum4(xa))) + fmaf(d1, tb, -(n1 * sum4(xb)));
+    }
+};
+
+// Q6_K: 210-byte super-blocks {ql[128], qh[64], int8 scales[16], f16 d} (types.zig:187-192),
+// 2-byte aligned. Group g: super-block g/32; r = g%32: half n = r/16, rr = r%16, l0 =
+// 4*(rr/2), p = rr%2; columns [128n + 32p + l0, +4) (6-bit values from the low nibbles of
+// ql[64n + 32p + l0 ..] and qh bits 2p) and that + 64 (high nibbles, qh bits 4 + 2p), scales
+// 8n + l0/16 + 2p and + 4 (math.zig:556-616: d * sum over quadrants of scale * (u - 32) * x).
+template <>
+struct WGroup<HIP_BRIDGE_Q6_K> {
+    uint32_t ql, qh, sc, dd, p;
+    __device__ __forceinline__ void load(const unsigned char* row, uint32_t g) {
+        const uint32_t base = (g >> 5) * 210u, r = g & 31u, n = r >> 4, rr = r & 15u;
+        const uint32_t l0 = 4u * (rr >> 1);
+        p = rr & 1u;
+        const uint32_t oq = base + 64u * n + 32u * p + l0, oh = base + 128u + 32u * n + l0;
+        ql = ldw16(row + oq) | (ldw16(row + (oq + 2u)) << 16);
+        qh = ldw16(row + oh) | (ldw16(row + (oh + 2u)) << 16);
+        const uint32_t ia = base + 192u + 8u * n + (l0 >> 4) + 2u * p, ib = ia + 4u;
+        const uint32_t wa = ldw16(row + (ia & ~1u)), wb = ldw16(row + (ib & ~1u));
+        sc = ((wa >> (8u * (ia & 1u))) & 0xffu) | (((wb >> (8u * (ib & 1u))) & 0xffu) << 8);
+        dd = ldw16(row + (base + 208u));
+    }
+    __device__ __forceinline__ float dot(const f32x4& xa, const f32x4& xb, float) const {
+        const uint32_t ha = (qh >> (2u * p)) & 0x03030303u, hb = (qh >> (4u + 2u * p)) & 0x03030303u;
+        const uint32_t ua = mask_bytes(ql, 0x0f0f0f0fu) | (ha << 4);
+        const uint32_t ub = mask_bytes(ql >> 4, 0x0f0f0f0fu) | (hb << 4);
+        const float sa = (float)(int8_t)(sc & 0xffu), sb = (float)(int8_t)(sc >> 8);
+        const float ta = fmaf(-32.0f, sum4(xa), dot4u(ua, xa));
+        const float tb = fmaf(-32.0f, sum4(xb), dot4u(ub, xb));
+        return h2f(dd) * fmaf(sa, ta, sb * tb);
+    }
+};
+
 // Column offsets of the two 4-float x vectors a group multiplies.
 template <int QT>
 __device__ __forceinline__ void group_cols(int g, int& ca, int& cb) {
     if constexpr (QT == HIP_BRIDGE_Q4_0) {
         ca = (g >> 2) * 32 + (g & 3) * 4;  // low nibbles: elements o..o+3 of the block
         cb = ca + 16;                      // high nibbles: elements 16+o..16+o+3
+    } else if constexpr (QT == HIP_BRIDGE_Q4_K) {
+        const int r = g & 31;
+        ca = (g >> 5) * 256 + (r >> 3) * 64 + (r & 7) * 4;
+        cb = ca + 32;
+    } else if constexpr (QT == HIP_BRIDGE_Q6_K) {
+        const int r = g & 31, rr = r & 15;
+        ca = (g >> 5) * 256 + (r >> 4) * 128 + (rr & 1) * 32 + (rr >> 1) * 4;
+        cb = ca + 64;
     } else {
         ca = 8 * g;
         cb = ca + 4;
@@ -450,6 +548,24 @@ __device__ __forceinline__ float w_elem(const unsigned char* row, int c) {
     } else if constexpr (QT == HIP_BRIDGE_Q8_0) {
         const unsigned char* blk = row + (c >> 5) * 34;
         return (float)(int8_t)blk[2 + (c & 31)] * h2f((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+    } else if constexpr (QT == HIP_BRIDGE_Q4_K) {
+        const unsigned char* sb = row + (c >> 8) * 144;
+        const int w = c & 255, jj = w >> 6, hi = (w >> 5) & 1, j = 2 * jj + hi;
+        const unsigned char* sc = sb + 4;
+        const int s6 = j < 4 ? (sc[j] & 63) : ((sc[j + 4] & 0x0F) | ((sc[j - 4] >> 6) << 4));
+        const int m6 = j < 4 ? (sc[j + 4] & 63) : ((sc[j + 4] >> 4) | ((sc[j] >> 6) << 4));
+        const float d = h2f((uint32_t)sb[0] | ((uint32_t)sb[1] << 8));
+        const float dmin = h2f((uint32_t)sb[2] | ((uint32_t)sb[3] << 8));
+        const int byte = sb[16 + 32 * jj + (w & 31)];
+        return (float)(hi ? byte >> 4 : byte & 0x0F) * (d * (float)s6) - dmin * (float)m6;
+    } else if constexpr (QT == HIP_BRIDGE_Q6_K) {
+        const unsigned char* sb = row + (c >> 8) * 210;
+        const int w = c & 255, half = w >> 7, grp = (w & 127) >> 5, l = w & 31;
+        const int lo = (sb[half * 64 + l + ((grp & 1) ? 32 : 0)] >> ((grp & 2) ? 4 : 0)) & 0xf;
+        const int hi = (sb[128 + half * 32 + l] >> (2 * grp)) & 3;
+        const int8_t sc = (int8_t)sb[192 + half * 8 + (l >> 4) + 2 * grp];
+        const float d = h2f((uint32_t)sb[208] | ((uint32_t)sb[209] << 8));
+        return d * (float)sc * (float)((lo | (hi << 4)) - 32);
     } else if constexpr (QT == HIP_BRIDGE_F32) {
         const unsigned char* p = row + 4 * (size_t)c;
         return __uint_as_float((uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) |
@@ -511,6 +627,8 @@ static int64_t gemv_row_bytes(int qtype, int cols) {
         case HIP_BRIDGE_BF16: return (int64_t)cols * 2;
         case HIP_BRIDGE_Q8_0: return cols % 32 ? -1 : (int64_t)(cols / 32) * 34;
         case HIP_BRIDGE_Q4_0: return cols % 32 ? -1 : (int64_t)(cols / 32) * 18;
+        case HIP_BRIDGE_Q4_K: return cols % 256 ? -1 : (int64_t)(cols / 256) * 144;
+        case HIP_BRIDGE_Q6_K: return cols % 256 ? -1 : (int64_t)(cols / 256) * 210;
         default: return -1;
     }
 }
@@ -561,11 +679,12 @@ static void launch_gemv(int qtype, GemvArgs& a, hipStream_t s) {
     }
     // Vector path: x 16-byte aligned, cols % 8 == 0; Q4_0 / Q8_0 rows 2-byte aligned (16-bit
     // loads), dense rows 16-byte aligned (cols % 8 == 0 makes every row so).
-    const bool blocks = qtype == HIP_BRIDGE_Q4_0 || qtype == HIP_BRIDGE_Q8_0;
-    auto w_ok = [&](const void* w) {
-        const uintptr_t p = reinterpret_cast<uintptr_t>(w);
-        return blocks ? (p & 1u) == 0 : (p & 15u) == 0;
-    };
+    // weight alignment the vector loads need: 2 bytes for Q4_0 / Q8_0 / Q6_K blocks (16-bit
+    // loads), 4 for Q4_K (32-bit loads; 144-byte blocks), 16 for dense rows
+    const uintptr_t walign = qtype == HIP_BRIDGE_Q4_0 || qtype == HIP_BRIDGE_Q8_0 || qtype == HIP_BRIDGE_Q6_K ? 1u
+                             : qtype == HIP_BRIDGE_Q4_K                                                   ? 3u
+                                                                                                          : 15u;
+    auto w_ok = [&](const void* w) { return (reinterpret_cast<uintptr_t>(w) & walign) == 0; };
     bool ok = a.cols % 8 == 0 && aligned16(a.x);
     for (int i = 0; i < a.nseg; ++i) {
         if (a.seg[i].rows <= 0) continue;
@@ -594,6 +713,8 @@ static void launch_gemv(int qtype, GemvArgs& a, hipStream_t s) {
         switch (qtype) {
             case HIP_BRIDGE_Q4_0: launch_vec<HIP_BRIDGE_Q4_0, MODE, true>(a, s); break;
             case HIP_BRIDGE_Q8_0: launch_vec<HIP_BRIDGE_Q8_0, MODE, true>(a, s); break;
+            case HIP_BRIDGE_Q4_K: launch_vec<HIP_BRIDGE_Q4_K, MODE, true>(a, s); break;
+            case HIP_BRIDGE_Q6_K: launch_vec<HIP_BRIDGE_Q6_K, MODE, true>(a, s); break;
             case HIP_BRIDGE_F16: launch_vec<HIP_BRIDGE_F16, MODE, true>(a, s); break;
             case HIP_BRIDGE_BF16: launch_vec<HIP_BRIDGE_BF16, MODE, true>(a, s); break;
             default: launch_vec<HIP_BRIDGE_F32, MODE, true>(a, s); break;
@@ -602,6 +723,8 @@ static void launch_gemv(int qtype, GemvArgs& a, hipStream_t s) {
         switch (qtype) {
             case HIP_BRIDGE_Q4_0: launch_vec<HIP_BRIDGE_Q4_0, MODE, false>(a, s); break;
             case HIP_BRIDGE_Q8_0: launch_vec<HIP_BRIDGE_Q8_0, MODE, false>(a, s); break;
+            case HIP_BRIDGE_Q4_K: launch_vec<HIP_BRIDGE_Q4_K, MODE, false>(a, s); break;
+            case HIP_BRIDGE_Q6_K: launch_vec<HIP_BRIDGE_Q6_K, MODE, false>(a, s); break;
             case HIP_BRIDGE_F16: launch_vec<HIP_BRIDGE_F16, MODE, false>(a, s); break;
             case HIP_BRIDGE_BF16: launch_vec<HIP_BRIDGE_BF16, MODE, false>(a, s); break;
             default: launch_vec<HIP_BRIDGE_F32, MODE, false>(a, s); break;
@@ -611,6 +734,8 @@ static void launch_gemv(int qtype, GemvArgs& a, hipStream_t s) {
         switch (qtype) {
             case HIP_BRIDGE_Q4_0: k_gemv_scalar<HIP_BRIDGE_Q4_0, MODE><<<grid, kGemvThreads, 0, s>>>(a); break;
             case HIP_BRIDGE_Q8_0: k_gemv_scalar<HIP_BRIDGE_Q8_0, MODE><<<grid, kGemvThreads, 0, s>>>(a); break;
+            case HIP_BRIDGE_Q4_K: k_gemv_scalar<HIP_BRIDGE_Q4_K, MODE><<<grid, kGemvThreads, 0, s>>>(a); break;
+            case HIP_BRIDGE_Q6_K: k_gemv_scalar<HIP_BRIDGE_Q6_K, MODE><<<grid, kGemvThreads, 0, s>>>(a); break;
             case HIP_BRIDGE_F16: k_gemv_scalar<HIP_BRIDGE_F16, MODE><<<grid, kGemvThreads, 0, s>>>(a); break;
             case HIP_BRIDGE_BF16: k_gemv_scalar<HIP_BRIDGE_BF16, MODE><<<grid, kGemvThreads, 0, s>>>(a); break;
             default: k_gemv_scalar<HIP_BRIDGE_F32, MODE><<<grid, kGemvThreads, 0, s>>>(a); break;

@@ -28,9 +28,8 @@ form of model.zig:130-137 loadNorm. Weight matrices are uploaded as raw GGUF row
 
 Checks the reference does not make (they keep a kernel from reading past a table): every
 matrix must hold exactly rows x cols of its type, with the sizes the decode step uses, and
-have a type the GEMV kernels take (F32, F16, BF16, Q4_0, Q8_0); the embedding table also
-Q6_K when an output.weight serves as LM head. Violations raise ModelError naming the
-tensor.
+have a type the GEMV and gather kernels take (F32, F16, BF16, Q4_0, Q8_0, Q4_K, Q6_K).
+Violations raise ModelError naming the tensor.
 """
 import math
 from dataclasses import dataclass, field
@@ -41,8 +40,8 @@ from . import bridge as B
 from . import gguf as G
 from . import synth
 
-GEMV_TYPES = (B.F32, B.F16, B.BF16, B.Q4_0, B.Q8_0)
-GATHER_TYPES = (B.F32, B.F16, B.BF16, B.Q4_0, B.Q8_0, B.Q6_K)
+GEMV_TYPES = (B.F32, B.F16, B.BF16, B.Q4_0, B.Q8_0, B.Q4_K, B.Q6_K)
+GATHER_TYPES = GEMV_TYPES
 PLE_DIM = 256  # per-layer embedding width (model.zig:508)
 
 

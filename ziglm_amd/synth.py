@@ -139,6 +139,28 @@ def q4_0_table(config_seed, rows, cols, name="tok_embd_q4_0"):
     return blk.reshape(rows, nb * 18)
 
 
+def q6_k_table(config_seed, rows, cols, name="q6k"):
+    """Q6_K rows (types.zig:187-192): per 256-super-block random ql / qh / int8 scales and an
+    f16 d ~ U[1e-3, 2e-2]."""
+    nsb = cols // 256
+    raw = uniform_int(config_seed, name, (rows, nsb, 210), 0, 255).astype(np.uint8)
+    d = f16_bits(uniform_f32(config_seed, name + ".d", (rows, nsb), 1e-3, 2e-2))
+    raw[:, :, 208:210] = d.reshape(rows, nsb, 1).view(np.uint8).reshape(rows, nsb, 2)
+    return raw.reshape(rows, nsb * 210)
+
+
+def q4_k_table(config_seed, rows, cols, name="q4k"):
+    """Q4_K rows (types.zig:170-175): per 256-super-block f16 d ~ U[1e-3, 2e-2], f16 dmin ~
+    U[1e-3, 1e-2], random packed 6-bit scales / mins and nibbles."""
+    nsb = cols // 256
+    raw = uniform_int(config_seed, name, (rows, nsb, 144), 0, 255).astype(np.uint8)
+    d = f16_bits(uniform_f32(config_seed, name + ".d", (rows, nsb), 1e-3, 2e-2))
+    m = f16_bits(uniform_f32(config_seed, name + ".dmin", (rows, nsb), 1e-3, 1e-2))
+    raw[:, :, 0:2] = d.reshape(rows, nsb, 1).view(np.uint8).reshape(rows, nsb, 2)
+    raw[:, :, 2:4] = m.reshape(rows, nsb, 1).view(np.uint8).reshape(rows, nsb, 2)
+    return raw.reshape(rows, nsb * 144)
+
+
 def bf16_table(config_seed, rows, cols, name="tok_embd_bf16"):
     """BF16 rows ~ N(0, 0.02), as little-endian bytes."""
     return normal_bf16(config_seed, name, (rows, cols), 0.0, 0.02).view(np.uint8).reshape(rows, cols * 2)

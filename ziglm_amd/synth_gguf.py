@@ -58,6 +58,10 @@ def _matrix(cfg, seed, name, qtype, rows, cols):
         src = synth.q4_0_table(seed, n, cols, name)
     elif qtype == B.Q8_0:
         src = synth.q8_0_table(seed, n, cols, name)
+    elif qtype == B.Q4_K:
+        src = synth.q4_k_table(seed, n, cols, name)
+    elif qtype == B.Q6_K:
+        src = synth.q6_k_table(seed, n, cols, name)
     else:
         w = synth.normal_f32(seed, name, (n, cols), 0.0, 0.02)
         if qtype == B.F32:
