@@ -402,17 +402,26 @@ def bench_gemv(dev):
 # Full decode step (34-layer Gemma-4B-shaped Q4_0 model, graph replay per token)
 # ---------------------------------------------------------------------------------------
 
-def bench_decode_step(dev, n_layers=34, pos0=1234, n_tokens=32, fused=True):
+def bench_decode_step(dev, n_layers=34, pos0=1234, n_tokens=32, fused=True, graph=True):
+    """graph=False launches every step eagerly (for kernel traces; host gaps included)."""
     from ziglm_amd.decode import DecodeModel
     m = DecodeModel.synthetic(dev, LY.GEMMA_4B, n_layers=n_layers, vocab=262144, max_seq=4096, fused=fused)
     try:
         m.set_token(2)
-        m.capture()
-        m.run(pos0 - 8, 8)  # warm-up; fills 8 cache rows
         e0, e1 = dev.event(), dev.event()
-        dev.record(e0)
-        m.run(pos0, n_tokens)
-        dev.record(e1)
+        if graph:
+            m.capture()
+            m.run(pos0 - 8, 8)  # warm-up; fills 8 cache rows
+            dev.record(e0)
+            m.run(pos0, n_tokens)
+            dev.record(e1)
+        else:
+            for p in range(pos0 - 8, pos0):
+                m.step(p, graph=False)
+            dev.record(e0)
+            for p in range(pos0, pos0 + n_tokens):
+                m.step(p, graph=False)
+            dev.record(e1)
         ms = dev.elapsed_ms(e0, e1)
         s = LY.GEMMA_4B
         H, I, qn, kn = s.H, s.I, s.nh * s.D, s.nkv * s.D
@@ -614,7 +623,7 @@ def main():
         if a.only.startswith("gather_"):
             fn, sets, traffic, _ = gather_case(dev, a.only[len("gather_"):])
         elif a.only == "decode_step":
-            print(json.dumps(bench_decode_step(dev)))
+            print(json.dumps(bench_decode_step(dev, graph=not a.eager)))
             return
         elif a.only == "gguf_decode":
             print(json.dumps(bench_gguf_decode(dev, graph=not a.eager)))
