@@ -210,14 +210,18 @@ void hip_gemv_q4_0(const void* weights, const float* x, float* y, int rows, int 
                    HipStream_t stream);                                     /* cuda_bridge.h:36 */
 void hip_gemv_q8_0(const void* weights, const float* x, float* y, int rows, int cols,
                    HipStream_t stream);                                     /* cuda_bridge.h:37 */
+void hip_gemv_q4_k(const void* weights, const float* x, float* y, int rows, int cols,
+                   HipStream_t stream);                                     /* cuda_bridge.h:38 */
+void hip_gemv_q6_k(const void* weights, const float* x, float* y, int rows, int cols,
+                   HipStream_t stream);                                     /* cuda_bridge.h:39 */
 void hip_gemv_f16(const void* weights, const float* x, float* y, int rows, int cols,
                   HipStream_t stream);                                      /* cuda_bridge.h:40 */
 void hip_gemv_bf16(const void* weights, const float* x, float* y, int rows, int cols,
                    HipStream_t stream);                                     /* cuda_bridge.h:41 */
 void hip_gemv_f32(const float* weights, const float* x, float* y, int rows, int cols,
                   HipStream_t stream);                       /* cuda_bridge.cu:1151, cuda.zig:39 */
-/* qtype dispatch; unsupported types (Q4_K, Q6_K, ...) are a no-op + EUNSUPPORTED (the
- * reference treats every unknown type as F32). */
+/* qtype dispatch (F32, F16, BF16, Q4_0, Q8_0, Q4_K, Q6_K); other types are a no-op +
+ * EUNSUPPORTED (the reference treats every unknown type as F32). */
 void hip_gemv(int qtype, const void* weights, const float* x, float* y, int rows, int cols,
               HipStream_t stream);                                          /* cuda_bridge.h:42 */
 /* act_out[r] = gelu_tanh(gate_r . x) * (up_r . x) */

@@ -1,4 +1,5 @@
-"""GEMV / small-batch GEMM on the GPU against the oracle (math.zig:25-330, 652-846).
+"""GEMV / small-batch GEMM on the GPU against the oracle (math.zig:25-330, 440-616, 652-846).
+Shapes include LM-head-sized row counts (>= 65536 rows: the wave-owned-rows kernel).
 
 The kernels sum in a different order from ziglm's CPU code, so the checks are
   * bit-exact on integer-valued inputs (every partial sum is exact in f32, so any order
@@ -38,7 +39,7 @@ def run_gemm(dev, qtype, raw, X, rows, cols, batch):
 
 @pytest.mark.parametrize("qtype", QTYPES)
 @pytest.mark.parametrize("rows,cols,batch", [(37, 2560, 1), (16, 96, 1), (9, 10240, 1), (11, 512, 2),
-                                             (13, 2560, 3), (6, 256, 7)])
+                                             (13, 2560, 3), (6, 256, 7), (65601, 256, 1)])
 def test_gemv_integer_bitexact(dev, qtype, rows, cols, batch):
     if qtype in K_QUANTS and cols % 256:
         pytest.skip("super-block types need cols % 256 == 0")
@@ -51,7 +52,8 @@ def test_gemv_integer_bitexact(dev, qtype, rows, cols, batch):
 
 
 @pytest.mark.parametrize("qtype", QTYPES)
-@pytest.mark.parametrize("rows,cols,batch", [(64, 2560, 1), (40, 10240, 1), (24, 2560, 4), (7, 1024, 5)])
+@pytest.mark.parametrize("rows,cols,batch", [(64, 2560, 1), (40, 10240, 1), (24, 2560, 4), (7, 1024, 5),
+                                             (65540, 512, 1)])
 def test_gemv_vs_f64(dev, oracle, qtype, rows, cols, batch):
     raw, wd = random_matrix(qtype, rows, cols, seed=rows + cols)
     X = synth.normal_f32(rows, "X", (batch, cols))
@@ -87,8 +89,16 @@ def test_gemv_mirrors_and_misaligned_paths(dev, oracle):
     d_wb.at(2).upload(rawb.reshape(-1))
     dev.gemv(B.BF16, d_wb.at(2), dev.from_numpy(xb), d_y, rows, 1000)
     assert np.all(np.abs(d_y.to_numpy((rows,), np.float32) - wdb @ xb.astype(np.float64)) <= bound(wdb, xb))
-    # K-quant rows below their load alignment (Q4_K: 4 bytes, Q6_K: 2 bytes): scalar kernel
+    # K-quant reference-ABI mirrors (cuda_bridge.h:38-39) equal the qtype dispatch
     d_xk = dev.from_numpy(x)
+    for qt, fn in ((B.Q4_K, dev.b.hip_gemv_q4_k), (B.Q6_K, dev.b.hip_gemv_q6_k)):
+        rawk, _ = random_matrix(qt, rows, cols, seed=6)
+        d_wk = dev.from_numpy(rawk.reshape(-1))
+        fn(d_wk.ptr, d_xk.ptr, d_y.ptr, rows, cols, dev.stream)
+        y_m = d_y.to_numpy((rows,), np.float32)
+        dev.gemv(qt, d_wk, d_xk, d_y, rows, cols)
+        np.testing.assert_array_equal(y_m, d_y.to_numpy((rows,), np.float32))
+    # K-quant rows below their load alignment (Q4_K: 4 bytes, Q6_K: 2 bytes): scalar kernel
     for qt, off in ((B.Q4_K, 2), (B.Q6_K, 1)):
         rawk, wdk = random_matrix(qt, rows, cols, seed=5)
         d_wk = dev.alloc(rawk.nbytes + 16)

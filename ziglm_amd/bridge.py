@@ -100,6 +100,8 @@ SIGNATURES = {
     # GEMV / GEMM (cuda_bridge.h:36-50)
     "hip_gemv_q4_0": (None, [_v, _v, _v, _i, _i, _v]),
     "hip_gemv_q8_0": (None, [_v, _v, _v, _i, _i, _v]),
+    "hip_gemv_q4_k": (None, [_v, _v, _v, _i, _i, _v]),
+    "hip_gemv_q6_k": (None, [_v, _v, _v, _i, _i, _v]),
     "hip_gemv_f16": (None, [_v, _v, _v, _i, _i, _v]),
     "hip_gemv_bf16": (None, [_v, _v, _v, _i, _i, _v]),
     "hip_gemv_f32": (None, [_v, _v, _v, _i, _i, _v]),

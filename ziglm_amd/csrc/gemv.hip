@@ -42,6 +42,7 @@ constexpr int kGemvProMaxCols = 16384;  // input vector in LDS: <= 64 KB
 #define ZL_GEMV_PRO_GRID 1024
 #endif
 constexpr unsigned kGemvProGrid = ZL_GEMV_PRO_GRID;
+constexpr int kGemvWaveRowsMin = 65536;  // rows from which batch-1 products use k_gemv_w
 
 struct GemvPro {
     int mode;
@@ -536,6 +537,85 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvArgs a) {
     }
 }
 
+// Batch-1 products, wave-owned rows: each wave of the workgroup owns RW consecutive rows and
+// walks all G column groups of them with its 64 lanes (lane l takes groups l, l + 64, ...),
+// so a row's work is balanced over the lanes for any G that is a multiple of 64 (the
+// workgroup-wide split above leaves waves idle when G is not a multiple of 256: 2560 columns
+// are 320 groups), the row sums reduce within the wave (no LDS, no barrier), and the next
+// group's weights and x are loaded while the current group is multiplied.
+template <int QT, int RW, int MODE>
+__global__ __launch_bounds__(kGemvThreads) void k_gemv_w(GemvArgs a) {
+    constexpr int NM = MODE == GV_GEGLU ? 2 : 1;
+    const int lane = threadIdx.x & 63;
+    const int row0 = (blockIdx.x * kGemvWaves + (threadIdx.x >> 6)) * RW;
+    if (row0 >= a.total_rows) return;  // the whole wave
+    const int G = a.cols / 8;
+    const unsigned char* wrow[RW][NM];
+    float* yrow[RW];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+        const bool ok = row0 + r < a.total_rows;
+        int R = ok ? row0 + r : row0;
+        int sg = 0;
+        if (a.nseg > 1 && R >= a.seg[0].rows) {
+            R -= a.seg[0].rows;
+            sg = 1;
+            if (a.nseg > 2 && R >= a.seg[1].rows) {
+                R -= a.seg[1].rows;
+                sg = 2;
+            }
+        }
+        wrow[r][0] = a.seg[sg].w + (int64_t)R * a.row_bytes;
+        if constexpr (NM == 2) wrow[r][1] = a.w_up + (int64_t)R * a.row_bytes;
+        yrow[r] = ok ? a.seg[sg].y + R : nullptr;
+    }
+    float acc[RW][NM];
+#pragma unroll
+    for (int r = 0; r < RW; ++r)
+#pragma unroll
+        for (int m = 0; m < NM; ++m) acc[r][m] = 0.0f;
+    WGroup<QT> cur[RW][NM], nxt[RW][NM];
+    f32x4 cxa, cxb, nxa, nxb;
+    auto fetch = [&](int g, WGroup<QT> (&w)[RW][NM], f32x4& xa, f32x4& xb) {
+#pragma unroll
+        for (int r = 0; r < RW; ++r)
+#pragma unroll
+            for (int m = 0; m < NM; ++m) w[r][m].load(wrow[r][m], (uint32_t)g);
+        int ca, cb;
+        group_cols<QT>(g, ca, cb);
+        xa = ldf4(a.x + ca);
+        xb = ldf4(a.x + cb);
+    };
+    int g = lane;
+    if (g < G) fetch(g, cur, cxa, cxb);
+    for (; g < G; g += kWave) {
+        const int gn = g + kWave;
+        if (gn < G) fetch(gn, nxt, nxa, nxb);
+        const float sx = ((cxa.x + cxa.y) + (cxa.z + cxa.w)) + ((cxb.x + cxb.y) + (cxb.z + cxb.w));
+#pragma unroll
+        for (int r = 0; r < RW; ++r)
+#pragma unroll
+            for (int m = 0; m < NM; ++m) acc[r][m] += cur[r][m].dot(cxa, cxb, sx);
+#pragma unroll
+        for (int r = 0; r < RW; ++r)
+#pragma unroll
+            for (int m = 0; m < NM; ++m) cur[r][m] = nxt[r][m];
+        cxa = nxa;
+        cxb = nxb;
+    }
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+        float t[NM];
+#pragma unroll
+        for (int m = 0; m < NM; ++m) t[m] = group_sum<kWave>(acc[r][m]);
+        if (lane == 0 && yrow[r]) {
+            float out = t[0];
+            if constexpr (MODE == GV_GEGLU) out = gelu_fast(t[0]) * t[1];
+            *yrow[r] = out;
+        }
+    }
+}
+
 // Any alignment / column count: one workgroup per row, scalar dequantisation per element.
 template <int QT>
 __device__ __forceinline__ float w_elem(const unsigned char* row, int c) {
@@ -651,6 +731,13 @@ static void launch_vec(const GemvArgs& a, hipStream_t s) {
             k_gemv<QT, 4 / H, 1, MODE, true><<<std::min(g4, cap), kGemvThreads, lds, s>>>(a);
         else
             k_gemv<QT, 2 / H, 1, MODE, true><<<std::min(g2, cap), kGemvThreads, lds, s>>>(a);
+    } else if (MODE == GV_PLAIN && a.batch == 1 && a.total_rows >= kGemvWaveRowsMin &&
+               QT != HIP_BRIDGE_F16 && QT != HIP_BRIDGE_BF16 && QT != HIP_BRIDGE_F32) {
+        // LM-head-sized block-quantised products: wave-owned rows (measured, 262144 x 2560,
+        // us: Q4_K 226 -> 160 with 2 rows per wave, Q6_K 310 -> 194 with 4, Q8_0 185 -> 174
+        // and Q4_0 137 -> 133 with 8; smaller matrices and dense types are faster above)
+        constexpr int RW = QT == HIP_BRIDGE_Q4_K ? 2 : QT == HIP_BRIDGE_Q6_K ? 4 : 8;
+        k_gemv_w<QT, RW, MODE><<<(unsigned)cdiv(a.total_rows, (int64_t)RW * kGemvWaves), kGemvThreads, 0, s>>>(a);
     } else if (a.batch == 1) {
         if (QT == HIP_BRIDGE_Q4_0 && a.total_rows >= 16384)
             k_gemv<QT, 8 / H, 1, MODE><<<g8, kGemvThreads, 0, s>>>(a);
@@ -778,6 +865,12 @@ void hip_gemv_q4_0(const void* weights, const float* x, float* y, int rows, int 
 }
 void hip_gemv_q8_0(const void* weights, const float* x, float* y, int rows, int cols, HipStream_t stream) {
     hip_gemm(HIP_BRIDGE_Q8_0, weights, x, y, 1, rows, cols, stream);
+}
+void hip_gemv_q4_k(const void* weights, const float* x, float* y, int rows, int cols, HipStream_t stream) {
+    hip_gemm(HIP_BRIDGE_Q4_K, weights, x, y, 1, rows, cols, stream);
+}
+void hip_gemv_q6_k(const void* weights, const float* x, float* y, int rows, int cols, HipStream_t stream) {
+    hip_gemm(HIP_BRIDGE_Q6_K, weights, x, y, 1, rows, cols, stream);
 }
 void hip_gemv_f16(const void* weights, const float* x, float* y, int rows, int cols, HipStream_t stream) {
     hip_gemm(HIP_BRIDGE_F16, weights, x, y, 1, rows, cols, stream);
