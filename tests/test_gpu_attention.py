@@ -108,7 +108,10 @@ def test_attention_reference_mirrors(dev, oracle):
         check(got[b], qb[b], kc, vc, layer * max_seq, pos + b, nh, nkv, d, scale, 0.0, 0, f"batched token {b}")
 
 
-def test_attention_out_of_range_rows_give_zeros(dev):
+@pytest.mark.parametrize("split", [False, True])
+def test_attention_out_of_range_rows_give_zeros(dev, split):
+    """Out-of-range tokens write zeros from the attention kernel itself (one split) or from
+    the merge, which then reads none of their splits (workspace given)."""
     nh, nkv, d, cap = 4, 2, 128, 64
     kc = synth.normal_f32(15, "kc", (2 * cap, nkv * d))
     q = synth.normal_f32(15, "q", (3, nh * d))
@@ -117,8 +120,11 @@ def test_attention_out_of_range_rows_give_zeros(dev):
     # token 0: position beyond max_len; token 1: row past the cache; token 2: valid
     pos = np.array([cap, cap - 1, 3], np.int32)
     base = np.array([0, cap + 8, 0], np.int64)
+    ws = dev.attentionWorkspaceBytes(3, nh, nkv, d, cap) if split else 0
+    assert ws > 0 or not split
     dev.attentionDecode(B.F32, dev.from_numpy(q), dev.from_numpy(kc), dev.from_numpy(kc), d_out, 2 * cap, nkv * d,
-                        dev.from_numpy(base), 0, dev.from_numpy(pos), 0, cap, 3, nh, nkv, d, 0.1, 0.0, 0)
+                        dev.from_numpy(base), 0, dev.from_numpy(pos), 0, cap, 3, nh, nkv, d, 0.1, 0.0, 0,
+                        dev.alloc(ws) if ws else None, ws)
     got = d_out.to_numpy((3, nh * d), np.float32)
     assert np.all(got[0] == 0) and np.all(got[1] == 0)
     ref, tol = attention_f64(q[2], kc, kc, 0, 3, nh, nkv, d, 0.1)

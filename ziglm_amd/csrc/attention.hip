@@ -8,7 +8,8 @@
 // reads kv head h / (n_heads / n_kv_heads).
 //
 // Layout (flash-decoding). One workgroup per (token b, kv head, head group, split s) covers
-// `chunk` consecutive positions for G query heads of the kv head (G = n_heads/n_kv_heads, or
+// one chunk of consecutive positions (the sequence's own length cut into nsplit chunks,
+// split_chunk) for G query heads of the kv head (G = n_heads/n_kv_heads, or
 // a fraction of it when there are few kv-head groups, choose_heads). Lanes come in groups of
 // LT = D/8 (8 elements of a head row per lane), one group per position, so a wave works on
 // 64/LT positions at a time and the K/V row loads of a position are one contiguous span; the
@@ -44,7 +45,7 @@ struct AttnArgs {
     int max_len;              // positions must be < max_len
     int batch, nh, nkv, D;
     int window;
-    int nsplit, chunk;
+    int nsplit;               // splits per sequence (split_chunk)
     int gq;                   // query heads per kv head (nh / nkv)
     int hg;                   // workgroups per (token, kv head, split): each takes gq / hg heads
     float scale, softcap, inv_cap;
@@ -60,6 +61,24 @@ __device__ __forceinline__ void attn_range(const AttnArgs& a, int b, int& start,
     if (a.cache_rows > 0 && rb + p >= a.cache_rows) return;
     end = p + 1;
     start = (a.window > 0 && end > a.window) ? end - a.window : 0;
+}
+
+// Positions per split for a sequence of `len` positions: the sequence's own length is cut
+// into nsplit equal chunks (the host sized nsplit for the longest possible sequence), no
+// chunk shorter than kChunkMin, so a short context spreads over fewer splits and the rest
+// stay empty. Returns the number of non-empty splits in `used`. Measured on MI355X (us per
+// call with the merge; floor 32 / 64 / 128 / 256): Gemma-4B heads (8/4 x 256), one token at
+// position 27259 of a 32768-row cache: 47.6 / 45.7 / 50.0 / 43.6; the same at position 100:
+// 9.8 / 11.2 / 17.9 / 13.2; 8/1 x 512 at position 1234 of 4096: 12.2 / 13.1 / 15.1 / 22.3;
+// 8/1 x 256, window 512: 8.0 / 8.3 / 10.0 / 13.5.
+#ifndef ZL_ATTN_CHUNK_MIN
+#define ZL_ATTN_CHUNK_MIN 32
+#endif
+constexpr int kChunkMin = ZL_ATTN_CHUNK_MIN;
+__device__ __forceinline__ int split_chunk(const AttnArgs& a, int len, int& used) {
+    const int chunk = max((len + a.nsplit - 1) / a.nsplit, kChunkMin);
+    used = len > 0 ? min(a.nsplit, (len + chunk - 1) / chunk) : 0;
+    return chunk;
 }
 
 template <typename KT>
@@ -96,8 +115,13 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
     int start, end;
     int64_t rb;
     attn_range(a, b, start, end, rb);
-    const int t0 = start + split * a.chunk;
-    const int t1 = min(end, t0 + a.chunk);
+    int used;
+    const int chunk = split_chunk(a, end - start, used);
+    // Splits past the sequence's length hold nothing: the merge reads only the first `used`
+    // (block-uniform exit; with one split the workgroup still writes the zero output).
+    if (a.nsplit > 1 && split >= used) return;
+    const int t0 = start + split * chunk;
+    const int t1 = min(end, t0 + chunk);
 
     float q[G][8];
 #pragma unroll
@@ -194,41 +218,58 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
     }
 }
 
-// Merge the splits of (token b, head h): one workgroup. The per-split factors
-// exp(m_s - M) and the total L are formed once in LDS, then each thread sums its elements
-// over the splits (8 split loads in flight per thread).
+// Merge the splits of (token b, head h) over columns [64 y, 64 y + 64): one workgroup per
+// (b, h, y). The per-split factors exp(m_s - M) and the total L are formed in LDS over the
+// sequence's non-empty splits; then lane i of wave w sums column 64 y + i over splits
+// w, w + 4, ... (8 loads in flight), and the four waves' sums are added in wave order.
 constexpr int kMaxSplit = 1024;
+constexpr int kMergeCols = kWave;
 __global__ __launch_bounds__(kAttnThreads) void k_attn_merge(AttnArgs a) {
+    constexpr int NW = kAttnThreads / kWave;
     __shared__ float s_c[kMaxSplit];
-    __shared__ float s_red[kAttnThreads / kWave];
+    __shared__ float s_red[NW];
+    __shared__ float s_part[NW][kMergeCols];
     const int bh = blockIdx.x;
     const int tid = threadIdx.x;
+    const int lane = tid % kWave, wv = tid / kWave;
+    const int e = blockIdx.y * kMergeCols + lane;
+    int start, end, used;
+    int64_t rb;
+    attn_range(a, bh / a.nh, start, end, rb);
+    split_chunk(a, end - start, used);
+    float* out = a.out + (int64_t)bh * a.D;
+    if (used == 0) {
+        if (wv == 0) out[e] = 0.0f;
+        return;
+    }
     const float* w = a.ws + (int64_t)bh * a.nsplit * (a.D + 2);
     float mx = -INFINITY;
-    for (int s = tid; s < a.nsplit; s += kAttnThreads) mx = fmaxf(mx, w[(int64_t)s * (a.D + 2)]);
-    // block max (DPP within waves, then the 4 wave values)
+    for (int s = tid; s < used; s += kAttnThreads) mx = fmaxf(mx, w[(int64_t)s * (a.D + 2)]);
 #pragma unroll
     for (int o = 1; o < kWave; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-    if ((tid & 63) == 0) s_red[tid >> 6] = mx;
+    if (lane == 0) s_red[wv] = mx;
     __syncthreads();
     const float M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
     __syncthreads();
     float lsum = 0.0f;
-    for (int s = tid; s < a.nsplit; s += kAttnThreads) {
+    for (int s = tid; s < used; s += kAttnThreads) {
         const float* ws = w + (int64_t)s * (a.D + 2);
         const float c = M == -INFINITY ? 0.0f : exp2f((ws[0] - M) * kLog2e);
         s_c[s] = c;
         lsum = fmaf(ws[1], c, lsum);
     }
     lsum = group_sum<kWave>(lsum);
-    if ((tid & 63) == 0) s_red[tid >> 6] = lsum;
+    if (lane == 0) s_red[wv] = lsum;
     __syncthreads();
     const float L = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
-    for (int e = tid; e < a.D; e += kAttnThreads) {
-        float A = 0.0f;
+    float A = 0.0f;
 #pragma unroll 8
-        for (int s = 0; s < a.nsplit; ++s) A = fmaf(w[(int64_t)s * (a.D + 2) + 2 + e], s_c[s], A);
-        a.out[(int64_t)bh * a.D + e] = L > 0.0f ? A / L : 0.0f;
+    for (int s = wv; s < used; s += NW) A = fmaf(w[(int64_t)s * (a.D + 2) + 2 + e], s_c[s], A);
+    s_part[wv][lane] = A;
+    __syncthreads();
+    if (wv == 0) {
+        const float t = (s_part[0][lane] + s_part[1][lane]) + (s_part[2][lane] + s_part[3][lane]);
+        out[e] = L > 0.0f ? t / L : 0.0f;
     }
 }
 
@@ -256,8 +297,8 @@ static void launch_g(const AttnArgs& a, hipStream_t s) {
 #endif
 // Only while the K/V rows the call can touch stay cache-resident (<= 32 MB: a 4096-position
 // f32 cache of 8 heads x 256, say); longer contexts re-read them from HBM per head group, so
-// every workgroup takes all heads (Gemma-4B heads at positions ~U[0, 32767], B = 1: 49.7 us
-// with all heads, 70.4 us with one head per workgroup).
+// every workgroup takes all heads (Gemma-4B heads at a position ~U[0, 32767], B = 1: 49.7 us
+// with all heads, 70.4 us with one head per workgroup, before the per-sequence split).
 constexpr int64_t kFewGroups = 16;
 constexpr double kKvResidentBytes = 32.0 * (1 << 20);
 static void choose_heads(AttnArgs& a, int es) {
@@ -270,20 +311,19 @@ static void choose_heads(AttnArgs& a, int es) {
     a.hg = a.gq / gw;
 }
 
-// Positions per split: enough splits that batch * n_kv_heads * head groups * splits fills
-// the chip (~2048 workgroups) and no split exceeds 1024 positions (sequences of a batch
-// differ in length: short splits keep the long ones from leaving a tail), at least 64
-// positions each (the actual lengths are on the device: a short context still spreads over
-// several workgroups), at most kMaxSplit splits.
+// Splits per sequence: enough that batch * n_kv_heads * head groups * splits fills the chip
+// (~2048 workgroups) and no split exceeds 1024 positions of the longest possible sequence
+// (sequences of a batch differ in length: short splits keep the long ones from leaving a
+// tail), at most one per kChunkMin positions, at most kMaxSplit. The actual lengths are on
+// the device: each sequence cuts its own length into that many chunks (split_chunk).
 static void choose_split(AttnArgs& a, size_t ws_bytes) {
     const int len = a.window > 0 ? std::min(a.window, a.max_len) : a.max_len;
     const int64_t groups = (int64_t)a.batch * a.nkv * a.hg;
     const int64_t want = std::max<int64_t>(cdiv(2048, groups), cdiv(len, 1024));
-    int nsplit = (int)std::max<int64_t>(1, std::min<int64_t>({cdiv(len, 64), want, (int64_t)kMaxSplit}));
+    int nsplit = (int)std::max<int64_t>(1, std::min<int64_t>({cdiv(len, kChunkMin), want, (int64_t)kMaxSplit}));
     const size_t need = (size_t)a.batch * a.nh * nsplit * (a.D + 2) * sizeof(float);
     if (!a.ws || need > ws_bytes) nsplit = 1;
     a.nsplit = nsplit;
-    a.chunk = (int)cdiv(len, nsplit);
 }
 
 static void launch_attn(int kv_dtype, AttnArgs& a, size_t ws_bytes, hipStream_t s) {
@@ -319,7 +359,8 @@ static void launch_attn(int kv_dtype, AttnArgs& a, size_t ws_bytes, hipStream_t 
         else if (a.D == 256) launch_g<uint16_t, 256>(a, s);
         else launch_g<uint16_t, 512>(a, s);
     }
-    if (a.nsplit > 1) k_attn_merge<<<(unsigned)((int64_t)a.batch * a.nh), kAttnThreads, 0, s>>>(a);
+    if (a.nsplit > 1)
+        k_attn_merge<<<dim3((unsigned)((int64_t)a.batch * a.nh), (unsigned)(a.D / kMergeCols)), kAttnThreads, 0, s>>>(a);
     check_launch();
 }
 

@@ -87,6 +87,19 @@ __device__ __forceinline__ uint32_t mask_bytes(uint32_t v, uint32_t m) {
 __device__ __forceinline__ uint32_t ldw16(const unsigned char* p) {
     return *reinterpret_cast<const uint16_t*>(p);
 }
+// 32-bit load from a 2-byte aligned address (block quants sit at offset 2 of 18 / 34-byte
+// blocks): one global_load_dword, which gfx950 serves unaligned, addressed as the row's base
+// plus the lane's 32-bit offset.
+typedef uint32_t u32_align2 __attribute__((aligned(2)));
+__device__ __forceinline__ uint32_t ldw32_a2(const unsigned char* p) {
+    return *reinterpret_cast<const u32_align2*>(p);
+}
+// v, opaque to the optimiser: a lane offset it would otherwise split into separately
+// zero-extended terms (64-bit address adds per row) stays one 32-bit offset register.
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
 __device__ __forceinline__ float h2f(uint32_t h) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }
@@ -102,14 +115,14 @@ struct WGroup {
         if constexpr (QT == HIP_BRIDGE_Q4_0) {
             const uint32_t blk = (g >> 2) * 18u;
             v[0] = ldw16(row + blk);                       // d
-            const uint32_t qs = blk + 2u + (g & 3u) * 4u;
-            v[1] = ldw16(row + qs) | (ldw16(row + (qs + 2u)) << 16);  // 4 low + 4 high nibbles
+            const uint32_t qs = opaque(blk + 2u + (g & 3u) * 4u);
+            v[1] = ldw32_a2(row + qs);                     // 4 low + 4 high nibbles
         } else if constexpr (QT == HIP_BRIDGE_Q8_0) {
             const uint32_t blk = (g >> 2) * 34u;
             v[0] = ldw16(row + blk);
-            const uint32_t qs = blk + 2u + (g & 3u) * 8u;
-            v[1] = ldw16(row + qs) | (ldw16(row + (qs + 2u)) << 16);
-            v[2] = ldw16(row + (qs + 4u)) | (ldw16(row + (qs + 6u)) << 16);
+            const uint32_t qs = opaque(blk + 2u + (g & 3u) * 8u);
+            v[1] = ldw32_a2(row + qs);
+            v[2] = ldw32_a2(row + (qs + 4u));
         } else if constexpr (QT == HIP_BRIDGE_F32) {
             const u32x4 a = ld16(row + 32u * g), b = ld16(row + (32u * g + 16u));
             v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
@@ -547,7 +560,10 @@ template <int QT, int RW, int MODE>
 __global__ __launch_bounds__(kGemvThreads) void k_gemv_w(GemvArgs a) {
     constexpr int NM = MODE == GV_GEGLU ? 2 : 1;
     const int lane = threadIdx.x & 63;
-    const int row0 = (blockIdx.x * kGemvWaves + (threadIdx.x >> 6)) * RW;
+    // The wave index is uniform across the wave: read from the first lane, it makes the row
+    // pointers scalar (each load is a scalar base plus the lane's 32-bit offset).
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int row0 = (blockIdx.x * kGemvWaves + wv) * RW;
     if (row0 >= a.total_rows) return;  // the whole wave
     const int G = a.cols / 8;
     const unsigned char* wrow[RW][NM];
@@ -574,8 +590,6 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_w(GemvArgs a) {
     for (int r = 0; r < RW; ++r)
 #pragma unroll
         for (int m = 0; m < NM; ++m) acc[r][m] = 0.0f;
-    WGroup<QT> cur[RW][NM], nxt[RW][NM];
-    f32x4 cxa, cxb, nxa, nxb;
     auto fetch = [&](int g, WGroup<QT> (&w)[RW][NM], f32x4& xa, f32x4& xb) {
 #pragma unroll
         for (int r = 0; r < RW; ++r)
@@ -586,16 +600,21 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_w(GemvArgs a) {
         xa = ldf4(a.x + ca);
         xb = ldf4(a.x + cb);
     };
+    auto fold = [&](const WGroup<QT> (&w)[RW][NM], const f32x4& xa, const f32x4& xb) {
+        const float sx = ((xa.x + xa.y) + (xa.z + xa.w)) + ((xb.x + xb.y) + (xb.z + xb.w));
+#pragma unroll
+        for (int r = 0; r < RW; ++r)
+#pragma unroll
+            for (int m = 0; m < NM; ++m) acc[r][m] += w[r][m].dot(xa, xb, sx);
+    };
+    WGroup<QT> cur[RW][NM], nxt[RW][NM];
+    f32x4 cxa, cxb, nxa, nxb;
     int g = lane;
     if (g < G) fetch(g, cur, cxa, cxb);
     for (; g < G; g += kWave) {
         const int gn = g + kWave;
         if (gn < G) fetch(gn, nxt, nxa, nxb);
-        const float sx = ((cxa.x + cxa.y) + (cxa.z + cxa.w)) + ((cxb.x + cxb.y) + (cxb.z + cxb.w));
-#pragma unroll
-        for (int r = 0; r < RW; ++r)
-#pragma unroll
-            for (int m = 0; m < NM; ++m) acc[r][m] += cur[r][m].dot(cxa, cxb, sx);
+        fold(cur, cxa, cxb);
 #pragma unroll
         for (int r = 0; r < RW; ++r)
 #pragma unroll
@@ -734,8 +753,9 @@ static void launch_vec(const GemvArgs& a, hipStream_t s) {
     } else if (MODE == GV_PLAIN && a.batch == 1 && a.total_rows >= kGemvWaveRowsMin &&
                QT != HIP_BRIDGE_F16 && QT != HIP_BRIDGE_BF16 && QT != HIP_BRIDGE_F32) {
         // LM-head-sized block-quantised products: wave-owned rows (measured, 262144 x 2560,
-        // us: Q4_K 226 -> 160 with 2 rows per wave, Q6_K 310 -> 194 with 4, Q8_0 185 -> 174
-        // and Q4_0 137 -> 133 with 8; smaller matrices and dense types are faster above)
+        // us: Q4_K 226 -> 157 with 2 rows per wave, Q6_K 310 -> 177 with 4, Q8_0 185 -> 173
+        // and Q4_0 137 -> 113 with 8; smaller matrices, whose rows are long against their
+        // count, and dense types are faster above: 2560 x 10240 Q4_0 8.0 us above, 14.6 here)
         constexpr int RW = QT == HIP_BRIDGE_Q4_K ? 2 : QT == HIP_BRIDGE_Q6_K ? 4 : 8;
         k_gemv_w<QT, RW, MODE><<<(unsigned)cdiv(a.total_rows, (int64_t)RW * kGemvWaves), kGemvThreads, 0, s>>>(a);
     } else if (a.batch == 1) {
