@@ -219,13 +219,20 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
 }
 
 // Merge the splits of (token b, head h) over columns [64 y, 64 y + 64): one workgroup per
-// (b, h, y). The per-split factors exp(m_s - M) and the total L are formed in LDS over the
-// sequence's non-empty splits; then lane i of wave w sums column 64 y + i over splits
-// w, w + 4, ... (8 loads in flight), and the four waves' sums are added in wave order.
+// (b, h, y), over the sequence's non-empty splits. Every (m, l) pair and the first kMergePre
+// partials of each lane's column are loaded at once through range-checked loads (one memory
+// round trip before the first reduction); the per-split factors exp(m_s - M) and the total
+// L are formed in LDS, lane i of wave w sums column 64 y + i over splits w, w + 4, ... in
+// split order, and the four waves' sums are added in wave order.
 constexpr int kMaxSplit = 1024;
 constexpr int kMergeCols = kWave;
+constexpr int kMergePre = 8;
+__device__ __forceinline__ float bldf(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
 __global__ __launch_bounds__(kAttnThreads) void k_attn_merge(AttnArgs a) {
     constexpr int NW = kAttnThreads / kWave;
+    constexpr int PER = kMaxSplit / kAttnThreads;  // (m, l) pairs per thread
     __shared__ float s_c[kMaxSplit];
     __shared__ float s_red[NW];
     __shared__ float s_part[NW][kMergeCols];
@@ -243,8 +250,21 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_merge(AttnArgs a) {
         return;
     }
     const float* w = a.ws + (int64_t)bh * a.nsplit * (a.D + 2);
+    const uint32_t rowb = (uint32_t)(a.D + 2) * 4u;
+    const auto rs = buf_rsrc(w, (uint32_t)used * rowb);  // reads past split used - 1 give 0
+    float mv[PER], lv[PER], pre[kMergePre];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const uint32_t o = (uint32_t)(tid + k * kAttnThreads) * rowb;
+        mv[k] = bldf(rs, o);
+        lv[k] = bldf(rs, o + 4u);
+    }
+#pragma unroll
+    for (int k = 0; k < kMergePre; ++k) pre[k] = bldf(rs, (uint32_t)(wv + k * NW) * rowb + 8u + 4u * (uint32_t)e);
     float mx = -INFINITY;
-    for (int s = tid; s < used; s += kAttnThreads) mx = fmaxf(mx, w[(int64_t)s * (a.D + 2)]);
+#pragma unroll
+    for (int k = 0; k < PER; ++k)
+        if (tid + k * kAttnThreads < used) mx = fmaxf(mx, mv[k]);
 #pragma unroll
     for (int o = 1; o < kWave; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
     if (lane == 0) s_red[wv] = mx;
@@ -252,19 +272,25 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_merge(AttnArgs a) {
     const float M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
     __syncthreads();
     float lsum = 0.0f;
-    for (int s = tid; s < used; s += kAttnThreads) {
-        const float* ws = w + (int64_t)s * (a.D + 2);
-        const float c = M == -INFINITY ? 0.0f : exp2f((ws[0] - M) * kLog2e);
-        s_c[s] = c;
-        lsum = fmaf(ws[1], c, lsum);
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const int sp = tid + k * kAttnThreads;
+        if (sp < used) {
+            const float c = M == -INFINITY ? 0.0f : exp2f((mv[k] - M) * kLog2e);
+            s_c[sp] = c;
+            lsum = fmaf(lv[k], c, lsum);
+        }
     }
     lsum = group_sum<kWave>(lsum);
     if (lane == 0) s_red[wv] = lsum;
     __syncthreads();
     const float L = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
     float A = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kMergePre; ++k)
+        if (wv + k * NW < used) A = fmaf(pre[k], s_c[wv + k * NW], A);
 #pragma unroll 8
-    for (int s = wv; s < used; s += NW) A = fmaf(w[(int64_t)s * (a.D + 2) + 2 + e], s_c[s], A);
+    for (int sp = wv + kMergePre * NW; sp < used; sp += NW) A = fmaf(w[(int64_t)sp * (a.D + 2) + 2 + e], s_c[sp], A);
     s_part[wv][lane] = A;
     __syncthreads();
     if (wv == 0) {

@@ -312,13 +312,118 @@ __device__ __forceinline__ float gemv_block_sum(float v, float* s_red) {
 
 // Builds the input vector of a PRO product in s_x[0, cols) (cols % 4 == 0, 16-byte aligned
 // operands): see GemvProMode. The RMSNorm arithmetic is the norm kernels' (rms_inv, then
-// (v * inv) * (1 + w) or * w).
+// (v * inv) * (1 + w) or * w). Up to kProRegChunks 16-byte chunks per thread (cols <= 4096)
+// every operand is loaded at once through range-checked loads and kept in registers (one
+// memory round trip before the first reduction); wider inputs loop over the operands.
+constexpr int kProRegChunks = 4;
+__device__ __forceinline__ f32x4 norm_w4(const f32x4& v, float inv, const f32x4& w, int uo) {
+    f32x4 o;
+    o.x = uo ? (v.x * inv) * (1.0f + w.x) : (v.x * inv) * w.x;
+    o.y = uo ? (v.y * inv) * (1.0f + w.y) : (v.y * inv) * w.y;
+    o.z = uo ? (v.z * inv) * (1.0f + w.z) : (v.z * inv) * w.z;
+    o.w = uo ? (v.w * inv) * (1.0f + w.w) : (v.w * inv) * w.w;
+    return o;
+}
+__device__ __forceinline__ float sumsq4(const f32x4& v, float ss) {
+    ss = fmaf(v.x, v.x, ss);
+    ss = fmaf(v.y, v.y, ss);
+    ss = fmaf(v.z, v.z, ss);
+    return fmaf(v.w, v.w, ss);
+}
+// x1 = (x + [norm(r)]) * scale (the NORM prologue's first vector), from registers.
+__device__ __forceinline__ f32x4 pro_x1(const GemvPro& p, const f32x4& xv, const f32x4& rv, const f32x4& rwv,
+                                        float inv1) {
+    float v[4] = {xv.x, xv.y, xv.z, xv.w};
+    if (p.r) {
+        float y[4] = {rv.x, rv.y, rv.z, rv.w};
+        if (p.r_w) {
+            const float w[4] = {rwv.x, rwv.y, rwv.z, rwv.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float t = y[j] * inv1;
+                y[j] = p.r_uo ? t * (1.0f + w[j]) : t * w[j];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = v[j] + y[j];
+    }
+    if (p.scale != 1.0f) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = v[j] * p.scale;
+    }
+    return f32x4{v[0], v[1], v[2], v[3]};
+}
 __device__ void gemv_prologue(const GemvArgs& a, float* s_x, float* s_red) {
     const GemvPro& p = a.pro;
     const int n4 = a.cols / 4;
     const int tid = threadIdx.x;
     f32x4* sx4 = reinterpret_cast<f32x4*>(s_x);
-    if (p.mode == GP_GEGLU) {
+    const bool wr = p.x_out && blockIdx.x == 0;
+    if (n4 <= kProRegChunks * kGemvThreads) {
+        constexpr int K = kProRegChunks;
+        const uint32_t nb = (uint32_t)n4 * 16u;
+        const auto rs_x = buf_rsrc(a.x, nb);
+        const auto rs_r = buf_rsrc(p.r, p.r ? nb : 0u);
+        f32x4 xv[K], rv[K];
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            const uint32_t o = (uint32_t)(tid + k * kGemvThreads) * 16u;
+            xv[k] = bldf4(rs_x, o);
+            rv[k] = bldf4(rs_r, o);
+        }
+        if (p.mode == GP_GEGLU) {
+#pragma unroll
+            for (int k = 0; k < K; ++k) {
+                const int c = tid + k * kGemvThreads;
+                if (c < n4) {
+                    f32x4 o;
+                    o.x = gelu_fast(xv[k].x) * rv[k].x;
+                    o.y = gelu_fast(xv[k].y) * rv[k].y;
+                    o.z = gelu_fast(xv[k].z) * rv[k].z;
+                    o.w = gelu_fast(xv[k].w) * rv[k].w;
+                    sx4[c] = o;
+                }
+            }
+        } else {
+            const auto rs_rw = buf_rsrc(p.r_w, p.r && p.r_w ? nb : 0u);
+            const auto rs_w = buf_rsrc(p.w, p.w ? nb : 0u);
+            f32x4 rwv[K], wv[K];
+#pragma unroll
+            for (int k = 0; k < K; ++k) {
+                const uint32_t o = (uint32_t)(tid + k * kGemvThreads) * 16u;
+                rwv[k] = bldf4(rs_rw, o);
+                wv[k] = bldf4(rs_w, o);
+            }
+            float inv1 = 0.0f;
+            if (p.r && p.r_w) {
+                float ss = 0.0f;
+#pragma unroll
+                for (int k = 0; k < K; ++k)
+                    if (tid + k * kGemvThreads < n4) ss = sumsq4(rv[k], ss);
+                inv1 = rms_inv(gemv_block_sum(ss, s_red), a.cols, p.eps);
+            }
+            float ss = 0.0f;
+#pragma unroll
+            for (int k = 0; k < K; ++k) {
+                const int c = tid + k * kGemvThreads;
+                if (c < n4) {
+                    xv[k] = pro_x1(p, xv[k], rv[k], rwv[k], inv1);
+                    if (wr) *reinterpret_cast<f32x4*>(p.x_out + 4 * c) = xv[k];
+                    ss = sumsq4(xv[k], ss);
+                }
+            }
+            if (p.w) {
+                const float inv2 = rms_inv(gemv_block_sum(ss, s_red), a.cols, p.eps);
+#pragma unroll
+                for (int k = 0; k < K; ++k) xv[k] = norm_w4(xv[k], inv2, wv[k], p.uo);
+            }
+#pragma unroll
+            for (int k = 0; k < K; ++k) {
+                const int c = tid + k * kGemvThreads;
+                if (c < n4) sx4[c] = xv[k];
+            }
+        }
+    } else if (p.mode == GP_GEGLU) {
         for (int c = tid; c < n4; c += kGemvThreads) {
             const f32x4 g = ldf4(a.x + 4 * c), u = ldf4(p.r + 4 * c);
             f32x4 o;
@@ -332,56 +437,22 @@ __device__ void gemv_prologue(const GemvArgs& a, float* s_x, float* s_red) {
         float inv1 = 0.0f;
         if (p.r && p.r_w) {
             float ss = 0.0f;
-            for (int c = tid; c < n4; c += kGemvThreads) {
-                const f32x4 v = ldf4(p.r + 4 * c);
-                ss = fmaf(v.x, v.x, ss);
-                ss = fmaf(v.y, v.y, ss);
-                ss = fmaf(v.z, v.z, ss);
-                ss = fmaf(v.w, v.w, ss);
-            }
+            for (int c = tid; c < n4; c += kGemvThreads) ss = sumsq4(ldf4(p.r + 4 * c), ss);
             inv1 = rms_inv(gemv_block_sum(ss, s_red), a.cols, p.eps);
         }
-        const bool wr = p.x_out && blockIdx.x == 0;
         float ss = 0.0f;
+        const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
         for (int c = tid; c < n4; c += kGemvThreads) {
-            const f32x4 xv = ldf4(a.x + 4 * c);
-            float v[4] = {xv.x, xv.y, xv.z, xv.w};
-            if (p.r) {
-                const f32x4 rv = ldf4(p.r + 4 * c);
-                float y[4] = {rv.x, rv.y, rv.z, rv.w};
-                if (p.r_w) {
-                    const f32x4 wv = ldf4(p.r_w + 4 * c);
-                    const float w[4] = {wv.x, wv.y, wv.z, wv.w};
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const float t = y[j] * inv1;
-                        y[j] = p.r_uo ? t * (1.0f + w[j]) : t * w[j];
-                    }
-                }
-#pragma unroll
-                for (int j = 0; j < 4; ++j) v[j] = v[j] + y[j];
-            }
-            if (p.scale != 1.0f) {
-#pragma unroll
-                for (int j = 0; j < 4; ++j) v[j] = v[j] * p.scale;
-            }
-            const f32x4 o = {v[0], v[1], v[2], v[3]};
+            const f32x4 o = pro_x1(p, ldf4(a.x + 4 * c), p.r ? ldf4(p.r + 4 * c) : zero,
+                                   p.r && p.r_w ? ldf4(p.r_w + 4 * c) : zero, inv1);
             if (wr) *reinterpret_cast<f32x4*>(p.x_out + 4 * c) = o;
             sx4[c] = o;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) ss = fmaf(v[j], v[j], ss);
+            ss = sumsq4(o, ss);
         }
         if (p.w) {
             const float inv2 = rms_inv(gemv_block_sum(ss, s_red), a.cols, p.eps);
-            for (int c = tid; c < n4; c += kGemvThreads) {  // the elements this thread wrote
-                const f32x4 v = sx4[c], wv = ldf4(p.w + 4 * c);
-                f32x4 o;
-                o.x = p.uo ? (v.x * inv2) * (1.0f + wv.x) : (v.x * inv2) * wv.x;
-                o.y = p.uo ? (v.y * inv2) * (1.0f + wv.y) : (v.y * inv2) * wv.y;
-                o.z = p.uo ? (v.z * inv2) * (1.0f + wv.z) : (v.z * inv2) * wv.z;
-                o.w = p.uo ? (v.w * inv2) * (1.0f + wv.w) : (v.w * inv2) * wv.w;
-                sx4[c] = o;
-            }
+            for (int c = tid; c < n4; c += kGemvThreads)  // the elements this thread wrote
+                sx4[c] = norm_w4(sx4[c], inv2, ldf4(p.w + 4 * c), p.uo);
         }
     }
     if (p.xb_out && blockIdx.x == 0)

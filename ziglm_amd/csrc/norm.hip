@@ -79,7 +79,7 @@ __host__ __device__ constexpr int norm_gpb() {
     return ZL_NORM_GROUPS_PER_BLOCK ? ZL_NORM_GROUPS_PER_BLOCK : 4 / W;
 }
 
-template <typename T, int NC, int MODE, int W, int R>
+template <typename T, int NC, int MODE, int W, int R, bool WL>
 __global__ __launch_bounds__(256) void k_norm_rows(NormArgs a) {
     using C = Chunk<T>;
     constexpr int E = C::E;
@@ -87,7 +87,7 @@ __global__ __launch_bounds__(256) void k_norm_rows(NormArgs a) {
     constexpr int STRIDE = kWave * W;
     // one slot set per (row, reduction): no slot is rewritten while a wave may still read it
     __shared__ float s_red[2 * R][4];
-    const int rib = (threadIdx.x >> 6) / W;  // group within block
+    const int rib = __builtin_amdgcn_readfirstlane((threadIdx.x >> 6) / W);  // group within block (wave-uniform)
     const int g = threadIdx.x - rib * STRIDE;
     const int64_t row0 = ((int64_t)blockIdx.x * GPB + rib) * R;
     const int n = a.n;
@@ -95,36 +95,43 @@ __global__ __launch_bounds__(256) void k_norm_rows(NormArgs a) {
     const bool has_w1 = a.w1 != nullptr;
     const bool has_w2 = a.w2 != nullptr;
 
-    // Issue every HBM load of the group's rows, then the (L2-resident) weights.
+    // Issue every HBM load of the group's rows, then the (L2-resident) weights, all through
+    // range-checked buffer loads (bld16): chunks past a row's end, and rows past the
+    // tensor's, read as zeros with no branch, so every load is in flight before the first
+    // wait. Their slots are never used.
     u32x4 rx[R][NC], rr[R][NC];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const int64_t row = row0 + r;
-        const T* xrow = (const T*)a.x + row * n;
-        const T* rrow = (const T*)a.r + row * n;
+        const uint32_t bytes = row < a.rows ? (uint32_t)n * sizeof(T) : 0u;
+        const auto rsx = buf_rsrc((const T*)a.x + row * n, bytes);
+        const auto rsr = buf_rsrc((const T*)a.r + row * n, MODE != M_NORM ? bytes : 0u);
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
-            const int idx = g + c * STRIDE;
-            if (row < a.rows && idx < nch) {
-                rx[r][c] = lds16(xrow + (int64_t)idx * E);
-                if constexpr (MODE != M_NORM) rr[r][c] = lds16(rrow + (int64_t)idx * E);
-            }
+            const uint32_t off = (uint32_t)(g + c * STRIDE) * 16u;
+            rx[r][c] = bld16(rsx, off);
+            if constexpr (MODE != M_NORM) rr[r][c] = bld16(rsr, off);
         }
     }
+    // Weights: with the activations (WL false: latency-bound launches, one round trip in
+    // all) or once the first row's activations have arrived (WL true: launches with every
+    // row resident at once, where thousands of waves asking for the same weight lines in the
+    // same instant queue behind each other; measured on 2048 x 2560 bf16 rows, input norm
+    // 5.84 -> 4.62 us).
     float f1[NC][E];
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-        const int idx = g + c * STRIDE;
-        if (idx < nch) load_w<E>(a.w1, (int64_t)idx * E, has_w1, f1[c]);
-    }
     float f2[MODE == M_NORM_ADD_NORM ? NC : 1][E];
-    if constexpr (MODE == M_NORM_ADD_NORM) {
+    auto load_weights = [&]() {
+        const uint32_t wbytes = (uint32_t)n * 4u;
+        const auto rsw1 = buf_rsrc(a.w1, has_w1 ? wbytes : 0u);
 #pragma unroll
-        for (int c = 0; c < NC; ++c) {
-            const int idx = g + c * STRIDE;
-            if (idx < nch) load_w<E>(a.w2, (int64_t)idx * E, has_w2, f2[c]);
+        for (int c = 0; c < NC; ++c) load_wb<E>(rsw1, (uint32_t)(g + c * STRIDE) * E * 4u, f1[c]);
+        if constexpr (MODE == M_NORM_ADD_NORM) {
+            const auto rsw2 = buf_rsrc(a.w2, has_w2 ? wbytes : 0u);
+#pragma unroll
+            for (int c = 0; c < NC; ++c) load_wb<E>(rsw2, (uint32_t)(g + c * STRIDE) * E * 4u, f2[c]);
         }
-    }
+    };
+    if constexpr (!WL) load_weights();
 
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -156,6 +163,9 @@ __global__ __launch_bounds__(256) void k_norm_rows(NormArgs a) {
 #pragma unroll
                 for (int j = 0; j < E; ++j) ss = fmaf(v[c][j], v[c][j], ss);
             }
+        }
+        if constexpr (WL) {
+            if (r == 0) load_weights();
         }
         ss = row_sum<W>(ss, slot1);
         const float inv = rms_inv(ss, n, a.eps);
@@ -296,7 +306,7 @@ __global__ __launch_bounds__(256) void k_norm_rows_generic(NormArgs a) {
     }
 }
 
-template <typename T, int MODE, int W>
+template <typename T, int MODE, int W, bool WL>
 static void launch_w(const NormArgs& a, int per_lane, int R, hipStream_t s) {
     constexpr int GPB = norm_gpb<W>();
     constexpr int NT = 64 * W * GPB;
@@ -304,20 +314,25 @@ static void launch_w(const NormArgs& a, int per_lane, int R, hipStream_t s) {
     // NC = chunks per lane, fitted to the row (the register footprint, and so the occupancy,
     // grows with NC); two rows per lane group up to 4 chunks per lane
     if (R == 2 && per_lane <= 4) {
-        if (per_lane <= 1) k_norm_rows<T, 1, MODE, W, 2><<<grid, NT, 0, s>>>(a);
-        else if (per_lane <= 2) k_norm_rows<T, 2, MODE, W, 2><<<grid, NT, 0, s>>>(a);
-        else if (per_lane <= 3) k_norm_rows<T, 3, MODE, W, 2><<<grid, NT, 0, s>>>(a);
-        else k_norm_rows<T, 4, MODE, W, 2><<<grid, NT, 0, s>>>(a);
+        if (per_lane <= 1) k_norm_rows<T, 1, MODE, W, 2, WL><<<grid, NT, 0, s>>>(a);
+        else if (per_lane <= 2) k_norm_rows<T, 2, MODE, W, 2, WL><<<grid, NT, 0, s>>>(a);
+        else if (per_lane <= 3) k_norm_rows<T, 3, MODE, W, 2, WL><<<grid, NT, 0, s>>>(a);
+        else k_norm_rows<T, 4, MODE, W, 2, WL><<<grid, NT, 0, s>>>(a);
         return;
     }
     const unsigned grid1 = (unsigned)cdiv(a.rows, GPB);
-    if (per_lane <= 1) k_norm_rows<T, 1, MODE, W, 1><<<grid1, NT, 0, s>>>(a);
-    else if (per_lane <= 2) k_norm_rows<T, 2, MODE, W, 1><<<grid1, NT, 0, s>>>(a);
-    else if (per_lane <= 3) k_norm_rows<T, 3, MODE, W, 1><<<grid1, NT, 0, s>>>(a);
-    else if (per_lane <= 4) k_norm_rows<T, 4, MODE, W, 1><<<grid1, NT, 0, s>>>(a);
-    else if (per_lane <= 6) k_norm_rows<T, 6, MODE, W, 1><<<grid1, NT, 0, s>>>(a);
-    else if (per_lane <= 8) k_norm_rows<T, 8, MODE, W, 1><<<grid1, NT, 0, s>>>(a);
-    else if constexpr (W == 4) k_norm_rows<T, 16, MODE, W, 1><<<grid1, NT, 0, s>>>(a);
+    if (per_lane <= 1) k_norm_rows<T, 1, MODE, W, 1, WL><<<grid1, NT, 0, s>>>(a);
+    else if (per_lane <= 2) k_norm_rows<T, 2, MODE, W, 1, WL><<<grid1, NT, 0, s>>>(a);
+    else if (per_lane <= 3) k_norm_rows<T, 3, MODE, W, 1, WL><<<grid1, NT, 0, s>>>(a);
+    else if (per_lane <= 4) k_norm_rows<T, 4, MODE, W, 1, WL><<<grid1, NT, 0, s>>>(a);
+    else if (per_lane <= 6) k_norm_rows<T, 6, MODE, W, 1, WL><<<grid1, NT, 0, s>>>(a);
+    else if (per_lane <= 8) k_norm_rows<T, 8, MODE, W, 1, WL><<<grid1, NT, 0, s>>>(a);
+    else if constexpr (W == 4) k_norm_rows<T, 16, MODE, W, 1, WL><<<grid1, NT, 0, s>>>(a);
+}
+template <typename T, int MODE, int W>
+static void launch_wl(const NormArgs& a, int per_lane, int R, bool late, hipStream_t s) {
+    if (late) launch_w<T, MODE, W, true>(a, per_lane, R, s);
+    else launch_w<T, MODE, W, false>(a, per_lane, R, s);
 }
 
 // Waves per row: the fewest (1, 2 or 4) that keep a row within 4 chunks (128-bit loads)
@@ -341,17 +356,22 @@ static void launch_t(const NormArgs& a, hipStream_t s) {
         W = nch <= fit * kWave ? 1 : nch <= 2 * fit * kWave ? 2 : 4;
     }
     const int per_lane = (int)cdiv(nch, kWave * W);
-    // Two rows per lane group once the launch has several rounds of waves (measured: 8192 x
-    // 5376 bf16, 4 waves per row, 5-8% faster for every mode); below that, one row each keeps
-    // more waves per SIMD in flight (2048 x 2560 bf16, 2 waves per row: 2-5% faster).
-    const int R = ZL_NORM_ROWS_PER_GROUP ? ZL_NORM_ROWS_PER_GROUP : a.rows * W >= 8192 ? 2 : 1;
+    // Two rows per lane group (the second row's loads in flight while the first is reduced
+    // and stored) once the launch has several rounds of waves (8192 x 5376 bf16, 4 waves per
+    // row: 5-8% faster for every mode), and from 2048 waves for the modes with two input
+    // streams (2048 x 2560 bf16, 2 waves per row: residual add + norm 7.9 -> 7.2 us); the
+    // plain norm keeps one row each there (4.6 against 5.0 us).
+    const int64_t waves = a.rows * W;
+    const int R = ZL_NORM_ROWS_PER_GROUP ? ZL_NORM_ROWS_PER_GROUP
+                  : waves >= 8192 || (MODE != M_NORM && waves >= 2048) ? 2 : 1;
+    const bool late = waves >= 1024;  // weights after the first row's activations (k_norm_rows)
     const bool vec = a.n % E == 0 && aligned16(a.x) && (MODE == M_NORM || aligned16(a.r)) &&
                      (MODE == M_NORM_ADD || aligned16(a.out)) && aligned16(a.w1) &&
                      (MODE != M_NORM_ADD_NORM || aligned16(a.w2)) && per_lane <= (W == 4 ? 16 : 8);
     if (vec) {
-        if (W == 4) launch_w<T, MODE, 4>(a, per_lane, R, s);
-        else if (W == 2) launch_w<T, MODE, 2>(a, per_lane, R, s);
-        else launch_w<T, MODE, 1>(a, per_lane, R, s);
+        if (W == 4) launch_wl<T, MODE, 4>(a, per_lane, R, late, s);
+        else if (W == 2) launch_wl<T, MODE, 2>(a, per_lane, R, late, s);
+        else launch_wl<T, MODE, 1>(a, per_lane, R, late, s);
     } else {
         k_norm_rows_generic<T, MODE><<<(unsigned)a.rows, 256, 0, s>>>(a);
     }

@@ -99,6 +99,23 @@ __device__ __forceinline__ void sts16(void* p, const u32x4& v) {
 }
 __device__ __forceinline__ f32x4 ldf4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
 
+// Range-checked loads through a buffer resource over [base, base + bytes): a raw buffer load
+// at a byte offset past the end returns zeros and makes no memory access (CDNA buffer range
+// checking), so lanes whose chunk lies outside a row need no branch around their load. A
+// conditional load makes the compiler wait for it before the next one is issued (the value
+// is merged at the branch's end), one memory round trip per chunk; these keep every load of
+// a row in flight together. Word 3 of the resource is the gfx9-family raw-buffer format.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+// 16 bytes at `off`; nt: the streaming (nontemporal) policy of lds16.
+__device__ __forceinline__ u32x4 bld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, ZL_STREAM_NT ? 2 : 0));
+}
+__device__ __forceinline__ f32x4 bldf4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
 // ---- lane-group reductions -----------------------------------------------------------
 // Sum over aligned groups of G lanes (G a power of two <= 64); every lane of a group gets
 // the bit-identical group total (each step adds a pair in the same order on both sides).
@@ -156,6 +173,18 @@ __device__ __forceinline__ void load_w(const float* w, int64_t e0, bool has_w, f
             f[4 * q + 2] = v.z;
             f[4 * q + 3] = v.w;
         }
+    }
+}
+// The same from a range-checked resource (a weight-less resource reads zeros, unused).
+template <int E>
+__device__ __forceinline__ void load_wb(__amdgpu_buffer_rsrc_t r, uint32_t off, float* f) {
+#pragma unroll
+    for (int q = 0; q < E / 4; ++q) {
+        const f32x4 v = bldf4(r, off + 16u * q);
+        f[4 * q + 0] = v.x;
+        f[4 * q + 1] = v.y;
+        f[4 * q + 2] = v.z;
+        f[4 * q + 3] = v.w;
     }
 }
 __device__ __forceinline__ float w_factor(float w, bool has_w, int uo) {
