@@ -376,10 +376,28 @@ def test_qk_v_norm_d64(dev, oracle):
     qk_case(dev, oracle, B.F32, 5, 4, 2, 64, 0, 10000.0, np.arange(5), v_norm=True)
 
 
-@pytest.mark.parametrize("D,rot", [(256, 128), (512, 128), (96, 0)])
-def test_qk_generic_path(dev, oracle, D, rot):
+@pytest.mark.parametrize("D,rot", [(256, 128), (512, 128), (512, 0), (128, 64)])
+def test_qk_partial_rotary(dev, oracle, D, rot):
+    """Fused path with a rotary width below head_dim (lanes split into RoPE pairs and the
+    unrotated tail) and head_dim 512; one token (workgroups per pass of head rows) and a
+    few."""
+    qk_case(dev, oracle, B.F32, 1, 8, 1, D, rot, 1e6, [1234])
     qk_case(dev, oracle, B.F32, 3, 4, 2, D, rot, 1e6, [3, 900, 4095])
     qk_case(dev, oracle, B.BF16, 3, 4, 2, D, rot, 1e6, [3, 900, 4095])
+
+
+@pytest.mark.parametrize("D,rot", [(96, 0), (128, 24)])
+def test_qk_generic_path(dev, oracle, D, rot):
+    """Generic path: head_dim outside the fused set, or (bf16) a rotary half that is not a
+    whole number of 16-byte chunks."""
+    qk_case(dev, oracle, B.F32, 3, 4, 2, D, rot, 1e6, [3, 900, 4095])
+    qk_case(dev, oracle, B.BF16, 3, 4, 2, D, rot, 1e6, [3, 900, 4095])
+
+
+def test_qk_many_tokens_loop_over_head_rows(dev, oracle):
+    """More than 64 tokens: one workgroup per token takes its head rows in passes."""
+    qk_case(dev, oracle, B.BF16, 96, 32, 16, 128, 0, 1e6, np.arange(500, 596), max_seq=1024)
+    qk_case(dev, oracle, B.F32, 80, 8, 1, 512, 128, 1e6, np.arange(10, 90), max_seq=1024)
 
 
 def test_rope_mirrors(dev, oracle):

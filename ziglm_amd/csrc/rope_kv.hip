@@ -13,15 +13,18 @@
 //         v0*c - v1*s, v0*s + v1*c with no FMA;
 //   KV    kv_cache_put (cuda_bridge.cu:2349; kv_cache.zig:63-85): row-contiguous copy.
 //
-// Fast path (rotary_dim == head_dim in {64, 128, 256}, 16-byte aligned buffers): one
-// workgroup per token, LH = head_dim/(2E) lanes per head (E = elements per 128-bit chunk)
-// and 64/LH heads per wave. Lane l of a head holds chunk l (elements [lE, lE+E)) and chunk
-// l + LH (the same offsets + head_dim/2), so every RoPE pair is inside one lane; the norm
-// statistic is an LH-lane butterfly. The token's cos/sin table (head_dim/2 entries) is
-// computed once in LDS while the first head's loads are in flight; its denominators are
-// evaluated per lane (rope_denom), so that phase has no memory operand to wait for.
-// Generic path (partial rotary, other head sizes up to 512, any alignment): one wave per
-// head row (Q, K or V head), head staged in LDS, four rows per workgroup.
+// Fast path (head_dim in {64, 128, 256, 512}, rotary_dim/2 a multiple of E, 16-byte aligned
+// buffers): LH = head_dim/(2E) lanes per head (E = elements per 128-bit chunk), 64/LH heads
+// per wave, one workgroup per token (per token and pass of head rows when there are few
+// tokens). Each lane holds two chunks of a head row: with R = rotary_dim/(2E), lanes l < R
+// chunks l and l + R (elements i and i + rotary_dim/2, so every RoPE pair is inside one
+// lane), the others two adjacent chunks of the unrotated tail; with full rotary that is
+// chunk l and chunk l + LH. The norm statistic is an LH-lane butterfly. The token's cos/sin
+// table (rotary_dim/2 entries) is computed once in LDS while the first head's loads are in
+// flight; its denominators are evaluated per lane (rope_denom), so that phase has no memory
+// operand to wait for.
+// Generic path (other head sizes up to 512, any alignment): one wave per head row (Q, K or V
+// head), head staged in LDS, four rows per workgroup.
 #include <math.h>
 #include <algorithm>
 #include <string.h>
@@ -101,6 +104,12 @@ __device__ __forceinline__ void fill_cos_sin(const RopeTab& tab, float pos_f, in
     }
 }
 
+// Head rows one pass of a k_qk_fused workgroup takes (4 waves of 64 / LH heads).
+template <typename T, int D>
+__host__ __device__ constexpr int qk_slots() {
+    return 4 * (kWave / (D / 2 / Chunk<T>::E));
+}
+
 template <typename T, int D>
 __global__ __launch_bounds__(256) void k_qk_fused(QkArgs a) {
     using C = Chunk<T>;
@@ -115,8 +124,16 @@ __global__ __launch_bounds__(256) void k_qk_fused(QkArgs a) {
     const int t = blockIdx.x;
     const int lane = threadIdx.x & 63;
     const int hl = lane & (LH - 1);
-    const int gslot = (threadIdx.x >> 6) * G + lane / LH;
-    constexpr int kSlots = 4 * G;
+    constexpr int kSlots = qk_slots<T, D>();
+    // Workgroup (t, y) takes head rows y * kSlots + slot, + kSlots * gridDim.y, ...
+    const int gslot = blockIdx.y * kSlots + (threadIdx.x >> 6) * G + lane / LH;
+    const int hstep = kSlots * gridDim.y;
+    // The lane's two chunks of a head row (E elements each): with rotary width r = 2 * half,
+    // lanes [0, R) (R = half / E) hold the RoPE pair (hl, hl + R) -- elements i and i + half --
+    // and the others two adjacent chunks of the unrotated tail [r, D).
+    const int R = a.half / E;
+    const int c0 = hl < R ? hl : 2 * R + 2 * (hl - R);
+    const int c1 = hl < R ? hl + R : c0 + 1;
     const int nq = a.q ? a.nh : 0;
     const int HR = a.nh + 2 * a.nkv;
     const int p = token_pos(a, t);
@@ -140,8 +157,8 @@ __global__ __launch_bounds__(256) void k_qk_fused(QkArgs a) {
     u32x4 ra = {0, 0, 0, 0}, rb = {0, 0, 0, 0};
     if (gslot < HR && active(gslot)) {
         const T* src = src_of(gslot);
-        ra = lds16(src + hl * E);
-        rb = lds16(src + HALF + hl * E);
+        ra = lds16(src + c0 * E);
+        rb = lds16(src + c1 * E);
     }
     // The norm weights go to LDS (read there per head, not held in registers): one f32x4
     // per thread (threads [0, D/4) stage wq, [D/4, D/2) stage wk; D <= 256 fits 256 threads).
@@ -150,8 +167,8 @@ __global__ __launch_bounds__(256) void k_qk_fused(QkArgs a) {
     const int wi = ti < D / 4 ? ti : ti - D / 4;  // thread -> float4 index in its vector
     const bool stage_q = ti < D / 4, stage_k = ti >= D / 4 && ti < D / 2;
     if ((stage_q && has_wq) || (stage_k && has_wk)) wstage = ldf4((stage_q ? a.wq : a.wk) + 4 * wi);
-    if (a.do_rope && ti < HALF) {
-        const float theta = ((float)p * a.freq_scale) / rope_denom(ti, D, a.log2_base);
+    if (a.do_rope && ti < a.half) {
+        const float theta = ((float)p * a.freq_scale) / rope_denom(ti, 2 * a.half, a.log2_base);
         double sn, cs;
         sincos((double)theta, &sn, &cs);
         s_cos[ti] = (float)cs;
@@ -168,12 +185,12 @@ __global__ __launch_bounds__(256) void k_qk_fused(QkArgs a) {
     }
     __syncthreads();
 
-    for (int hr = gslot; hr < HR; hr += kSlots) {
+    for (int hr = gslot; hr < HR; hr += hstep) {
         if (!active(hr)) continue;
         if (hr != gslot) {
             const T* src = src_of(hr);
-            ra = lds16(src + hl * E);
-            rb = lds16(src + HALF + hl * E);
+            ra = lds16(src + c0 * E);
+            rb = lds16(src + c1 * E);
         }
         const int kind = hr < a.nh ? 0 : hr < a.nh + a.nkv ? 1 : 2;  // Q, K, V
         float x0[E], x1[E];
@@ -199,12 +216,12 @@ __global__ __launch_bounds__(256) void k_qk_fused(QkArgs a) {
                 const float* sw = kind == 0 ? s_wq : s_wk;  // factors (1+w), w or 1
 #pragma unroll
                 for (int j = 0; j < E; ++j) {
-                    x0[j] = (x0[j] * inv) * sw[hl * E + j];
-                    x1[j] = (x1[j] * inv) * sw[HALF + hl * E + j];
+                    x0[j] = (x0[j] * inv) * sw[c0 * E + j];
+                    x1[j] = (x1[j] * inv) * sw[c1 * E + j];
                 }
             }
         }
-        if (a.do_rope && kind != 2) {
+        if (a.do_rope && kind != 2 && hl < R) {
 #pragma unroll
             for (int j = 0; j < E; ++j) {
                 const float c = s_cos[hl * E + j], s = s_sin[hl * E + j];
@@ -217,8 +234,8 @@ __global__ __launch_bounds__(256) void k_qk_fused(QkArgs a) {
         if (kind == 0) dst = (T*)a.q + ((int64_t)t * a.nh + hr) * D;
         else if (kind == 1) dst = (T*)a.kdst + row * a.row_stride + (int64_t)(hr - a.nh) * D;
         else dst = (T*)a.vdst + row * a.row_stride + (int64_t)(hr - a.nh - a.nkv) * D;
-        sts16(dst + hl * E, C::pack(x0));
-        sts16(dst + HALF + hl * E, C::pack(x1));
+        sts16(dst + c0 * E, C::pack(x0));
+        sts16(dst + c1 * E, C::pack(x1));
     }
 }
 
@@ -344,15 +361,19 @@ static const RopeTab& rope_table(float base, int eff) {
 template <typename T>
 static void launch_qk_t(const QkArgs& a, const RopeTab& tab, hipStream_t s) {
     constexpr int E = Chunk<T>::E;
-    const bool fast = a.half * 2 == a.D && (a.D == 64 || a.D == 128 || a.D == 256) &&
-                      (a.D / 2) % E == 0 && aligned16(a.q) && aligned16(a.k) && aligned16(a.v) &&
-                      aligned16(a.kdst) && aligned16(a.vdst) && aligned16(a.wq) && aligned16(a.wk) &&
-                      a.row_stride % E == 0;
+    const bool fast = (a.D == 64 || a.D == 128 || a.D == 256 || a.D == 512) && a.half % E == 0 &&
+                      aligned16(a.q) && aligned16(a.k) && aligned16(a.v) && aligned16(a.kdst) &&
+                      aligned16(a.vdst) && aligned16(a.wq) && aligned16(a.wk) && a.row_stride % E == 0;
     const unsigned grid = (unsigned)a.n_tokens;
     if (fast) {
-        if (a.D == 64) k_qk_fused<T, 64><<<grid, 256, 0, s>>>(a);
-        else if (a.D == 128) k_qk_fused<T, 128><<<grid, 256, 0, s>>>(a);
-        else k_qk_fused<T, 256><<<grid, 256, 0, s>>>(a);
+        // Few tokens (decode): one workgroup per pass of head rows, so no workgroup loops
+        // (each pass would wait for its own loads); many tokens: the token's rows in turn.
+        const int HR = a.nh + 2 * a.nkv;
+        auto gy = [&](int slots) { return (unsigned)(a.n_tokens <= 64 ? std::max<int64_t>(1, cdiv(HR, slots)) : 1); };
+        if (a.D == 64) k_qk_fused<T, 64><<<dim3(grid, gy(qk_slots<T, 64>())), 256, 0, s>>>(a);
+        else if (a.D == 128) k_qk_fused<T, 128><<<dim3(grid, gy(qk_slots<T, 128>())), 256, 0, s>>>(a);
+        else if (a.D == 256) k_qk_fused<T, 256><<<dim3(grid, gy(qk_slots<T, 256>())), 256, 0, s>>>(a);
+        else k_qk_fused<T, 512><<<dim3(grid, gy(qk_slots<T, 512>())), 256, 0, s>>>(a);
     } else {
         const dim3 g2(grid, (unsigned)std::max<int64_t>(1, cdiv(a.nh + 2 * a.nkv, 4)));  // 4 head rows per workgroup
         k_qk_generic<T><<<g2, 256, 0, s>>>(a, tab);
