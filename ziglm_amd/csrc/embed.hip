@@ -10,14 +10,14 @@
 // Every lane produces 16 bytes of output per step (4 f32 or 8 bf16), so each store
 // instruction of a wave writes 1 KB of whole, contiguous cache lines.
 // Q8_0 / Q4_0 (34 / 18 B blocks, 2-byte aligned): each lane loads the f16 scale and the
-// quant bytes behind its outputs straight from global memory with 16-bit loads, all issued
-// before the first use; the lanes of a wave read a contiguous span of the row, so the
+// quant bytes behind its outputs straight from global memory with 16-bit loads; the lanes of a wave read a contiguous span of the row, so the
 // loads coalesce into that span's cache lines (measured on MI355X at 4096 x 2560: 9.4 us
 // against 12.9 us for staging the row through LDS first).
 // Q6_K / Q4_K (210 / 144 B super-blocks): the segment (8 super-blocks) is staged in LDS, then
 // decoded.
 // Dense types (F32, F16, BF16): each lane converts the elements behind its 16-byte stores,
-// all loads issued before the first store.
+// all loads (range-checked, so none waits behind another's bounds branch) issued before the
+// first store.
 #include "zl_common.h"
 #include "zl_host.h"
 
@@ -32,6 +32,7 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
 __device__ __forceinline__ uint32_t lds_u16(const unsigned char* p) {
     return *reinterpret_cast<const uint16_t*>(p);
 }
+
 
 // Outputs per lane per step: one 16-byte store (4 f32 or 8 bf16), so each store instruction
 // of a wave writes 64 x 16 B of contiguous, whole cache lines.
@@ -138,9 +139,6 @@ __host__ __device__ constexpr int seg_elems() {
     return QT == HIP_BRIDGE_Q6_K || QT == HIP_BRIDGE_Q4_K ? 2048 : 512;
 }
 
-__device__ __forceinline__ uint32_t ldg_u16(const unsigned char* p) {
-    return *reinterpret_cast<const uint16_t*>(p);
-}
 
 // Q8_0 / Q4_0: one wave per 512 outputs, direct 16-bit global loads (the table only needs
 // 2-byte alignment: blocks are 34 / 18 B).
@@ -161,6 +159,8 @@ __global__ __launch_bounds__(256) void k_gather_q(const unsigned char* __restric
     const int e0 = (int)(wg - t * nseg) * 512;
     const int64_t id = ids ? (int64_t)ids[t] : single_id;
     const bool valid = id >= 0 && id < n_rows;
+    // (Plain loads under the bounds condition: the range-checked form of these 16-bit loads
+    // measured slower here, Q4_0 at 4096 x 2560 9.4 against 9.9 us.)
     const unsigned char* grow = table + (valid ? id : 0) * (int64_t)(dim / 32) * BB;
     uint32_t dq[K], w[K][N / 2];
 #pragma unroll
@@ -168,12 +168,12 @@ __global__ __launch_bounds__(256) void k_gather_q(const unsigned char* __restric
         const int e = e0 + lane * N + kWave * N * k;
         if (valid && e < dim) {
             const unsigned char* blk = grow + (e >> 5) * BB;
-            dq[k] = ldg_u16(blk);
+            dq[k] = lds_u16(blk);
             // Q8_0: bytes 2 + (e & 31) ..; Q4_0: nibble bytes 2 + (e & 15) .. (low nibbles
             // hold elements 0..15 of the block, high nibbles 16..31)
             const unsigned char* qs = blk + 2 + (QT == HIP_BRIDGE_Q8_0 ? (e & 31) : (e & 15));
 #pragma unroll
-            for (int j = 0; j < N / 2; ++j) w[k][j] = ldg_u16(qs + 2 * j);
+            for (int j = 0; j < N / 2; ++j) w[k][j] = lds_u16(qs + 2 * j);
         }
     }
     OutT* orow = out + t * (int64_t)dim;
@@ -287,17 +287,18 @@ struct DenseIn {
     static constexpr int ES = QT == HIP_BRIDGE_F32 ? 4 : 2;
     static constexpr int WORDS = N * ES / 4;  // 32-bit words behind N outputs
     uint32_t w[WORDS];
-    __device__ __forceinline__ void load(const unsigned char* p) {
-        // plain (cached) loads: for rows at random addresses they measured faster than
-        // nontemporal ones (BF16 -> f32 at 4096 x 2560: 11.4 against 13.3 us)
+    // rs: the row's resource; off: byte offset of the first input (past the row: zeros).
+    // Plain (cached) loads: for rows at random addresses they measured faster than
+    // nontemporal ones (BF16 -> f32 at 4096 x 2560: 11.4 against 13.3 us).
+    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
         if constexpr (WORDS == 2) {
-            const u32x2 r = *reinterpret_cast<const u32x2*>(p);
+            const auto r = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0));
             w[0] = r.x;
             w[1] = r.y;
         } else {
 #pragma unroll
             for (int c = 0; c < WORDS / 4; ++c) {
-                const u32x4 r = ld16(p + 16 * c);
+                const auto r = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16u * c, 0, 0));
                 w[4 * c] = r.x;
                 w[4 * c + 1] = r.y;
                 w[4 * c + 2] = r.z;
@@ -337,13 +338,11 @@ __global__ __launch_bounds__(256) void k_gather_dense(const unsigned char* __res
     const int e0 = (int)(wg - t * nseg) * 512;
     const int64_t id = ids ? (int64_t)ids[t] : single_id;
     const bool valid = id >= 0 && id < n_rows;
-    const unsigned char* grow = table + (valid ? id : 0) * (int64_t)dim * In::ES;
+    const int64_t rbytes = (int64_t)dim * In::ES;
+    const auto rs = buf_rsrc(table + (valid ? id : 0) * rbytes, valid ? (uint32_t)rbytes : 0u);
     In in[K];
 #pragma unroll
-    for (int k = 0; k < K; ++k) {
-        const int e = e0 + lane * N + kWave * N * k;
-        if (valid && e < dim) in[k].load(grow + (int64_t)e * In::ES);
-    }
+    for (int k = 0; k < K; ++k) in[k].load(rs, (uint32_t)(e0 + lane * N + kWave * N * k) * In::ES);
     OutT* orow = out + t * (int64_t)dim;
 #pragma unroll
     for (int k = 0; k < K; ++k) {

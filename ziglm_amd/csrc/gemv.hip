@@ -43,6 +43,12 @@ constexpr int kGemvProMaxCols = 16384;  // input vector in LDS: <= 64 KB
 #endif
 constexpr unsigned kGemvProGrid = ZL_GEMV_PRO_GRID;
 constexpr int kGemvWaveRowsMin = 65536;  // rows from which batch-1 products use k_gemv_w
+// Tuning builds: a non-zero ZL_GEMV_FORCE sends every batch-1 product without prologue to
+// k_gemv with that many rows per workgroup (> 0) or, for block types, to k_gemv_w with -F
+// rows per wave (< 0); GeGLU products take half. 0 (the library) uses the rules below.
+#ifndef ZL_GEMV_FORCE
+#define ZL_GEMV_FORCE 0
+#endif
 
 struct GemvPro {
     int mode;
@@ -806,7 +812,9 @@ static int64_t gemv_row_bytes(int qtype, int cols) {
 // Rows per workgroup (x is reused across them from registers) against workgroup count:
 // measured on Gemma-4B decode shapes, small matrices (1024-4096 rows) want 2 rows and more
 // workgroups, large ones 4, Q4_0 (the most x per weight byte) 8 from 16384 rows. GeGLU
-// reads two matrices per row and takes half as many rows.
+// reads two matrices per row and takes half as many rows; Q4_0 GeGLU products take 4 row
+// pairs from 4096 pairs (gate-up 2 x 6144 x 1536: 7.6 -> 6.4 us; 2 x 10240 x 2560: 12.6 ->
+// 11.8 us).
 template <int QT, int MODE, bool PRO>
 static void launch_vec(const GemvArgs& a, hipStream_t s) {
     constexpr int H = MODE == GV_GEGLU ? 2 : 1;
@@ -821,6 +829,16 @@ static void launch_vec(const GemvArgs& a, hipStream_t s) {
             k_gemv<QT, 4 / H, 1, MODE, true><<<std::min(g4, cap), kGemvThreads, lds, s>>>(a);
         else
             k_gemv<QT, 2 / H, 1, MODE, true><<<std::min(g2, cap), kGemvThreads, lds, s>>>(a);
+    } else if (ZL_GEMV_FORCE != 0 && a.batch == 1) {  // tuning builds only (see the macro)
+        constexpr int F = ZL_GEMV_FORCE;
+        constexpr bool blockq = QT != HIP_BRIDGE_F16 && QT != HIP_BRIDGE_BF16 && QT != HIP_BRIDGE_F32;
+        if constexpr (F < 0 && blockq) {
+            constexpr int RW = std::max(1, -F / H);
+            k_gemv_w<QT, RW, MODE><<<(unsigned)cdiv(a.total_rows, (int64_t)RW * kGemvWaves), kGemvThreads, 0, s>>>(a);
+        } else {
+            constexpr int RP = F > 0 ? std::max(1, F / H) : 2 / H;
+            k_gemv<QT, RP, 1, MODE><<<(unsigned)cdiv(a.total_rows, RP), kGemvThreads, 0, s>>>(a);
+        }
     } else if (MODE == GV_PLAIN && a.batch == 1 && a.total_rows >= kGemvWaveRowsMin &&
                QT != HIP_BRIDGE_F16 && QT != HIP_BRIDGE_BF16 && QT != HIP_BRIDGE_F32) {
         // LM-head-sized block-quantised products: wave-owned rows (measured, 262144 x 2560,
@@ -830,7 +848,7 @@ static void launch_vec(const GemvArgs& a, hipStream_t s) {
         constexpr int RW = QT == HIP_BRIDGE_Q4_K ? 2 : QT == HIP_BRIDGE_Q6_K ? 4 : 8;
         k_gemv_w<QT, RW, MODE><<<(unsigned)cdiv(a.total_rows, (int64_t)RW * kGemvWaves), kGemvThreads, 0, s>>>(a);
     } else if (a.batch == 1) {
-        if (QT == HIP_BRIDGE_Q4_0 && a.total_rows >= 16384)
+        if (QT == HIP_BRIDGE_Q4_0 && (a.total_rows >= 16384 || (MODE == GV_GEGLU && a.total_rows >= 4096)))
             k_gemv<QT, 8 / H, 1, MODE><<<g8, kGemvThreads, 0, s>>>(a);
         else if (a.total_rows >= 8192)
             k_gemv<QT, 4 / H, 1, MODE><<<g4, kGemvThreads, 0, s>>>(a);
