@@ -476,34 +476,51 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvArgs a) {
     const int wave = tid >> 6;
     const int lane = tid & 63;
     const int G = a.cols / 8;
-    if constexpr (PRO) gemv_prologue(a, s_x, &s_part[0][0]);
+    // Row pointers of the block at row0. Rows past the end read the block's first row (in
+    // range: row0 < total_rows) and are never written.
+    auto rows_of = [&](int row0, const unsigned char* (&wrow)[RPW][NM], float* (&yrow)[RPW], int (&ystride)[RPW]) {
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+            const bool ok = row0 + r < a.total_rows;
+            int R = ok ? row0 + r : row0;
+            int s = 0;
+            if (a.nseg > 1 && R >= a.seg[0].rows) {
+                R -= a.seg[0].rows;
+                s = 1;
+                if (a.nseg > 2 && R >= a.seg[1].rows) {
+                    R -= a.seg[1].rows;
+                    s = 2;
+                }
+            }
+            wrow[r][0] = a.seg[s].w + (int64_t)R * a.row_bytes;
+            if constexpr (NM == 2) wrow[r][1] = a.w_up + (int64_t)R * a.row_bytes;
+            yrow[r] = ok ? a.seg[s].y + R : nullptr;
+            ystride[r] = a.seg[s].rows;
+        }
+    };
+    // PRO: the first row block's first column group of weights (group tid, clamped into the
+    // row) is loaded before the prologue, so its HBM latency overlaps the prologue's.
+    WGroup<QT> wpre[RPW][NM];
+    if constexpr (PRO) {
+        const unsigned char* w0[RPW][NM];
+        float* y0[RPW];
+        int s0[RPW];
+        rows_of(blockIdx.x * RPW, w0, y0, s0);
+#pragma unroll
+        for (int r = 0; r < RPW; ++r)
+#pragma unroll
+            for (int m = 0; m < NM; ++m) wpre[r][m].load(w0[r][m], (uint32_t)min(tid, G - 1));
+        gemv_prologue(a, s_x, &s_part[0][0]);
+    }
 
     // Row blocks: one per workgroup, except PRO kernels, whose grid is capped (the prologue
     // is paid once per workgroup) and which take every gridDim.x-th block.
     for (int row0 = blockIdx.x * RPW;;) {
-    // Row pointers. Rows past the end read the block's first row (in range: row0 <
-    // total_rows) and are never written.
+    const bool first = PRO && row0 == (int)blockIdx.x * RPW;  // wpre holds its group tid
     const unsigned char* wrow[RPW][NM];
     float* yrow[RPW];
     int ystride[RPW];
-#pragma unroll
-    for (int r = 0; r < RPW; ++r) {
-        const bool ok = row0 + r < a.total_rows;
-        int R = ok ? row0 + r : row0;
-        int s = 0;
-        if (a.nseg > 1 && R >= a.seg[0].rows) {
-            R -= a.seg[0].rows;
-            s = 1;
-            if (a.nseg > 2 && R >= a.seg[1].rows) {
-                R -= a.seg[1].rows;
-                s = 2;
-            }
-        }
-        wrow[r][0] = a.seg[s].w + (int64_t)R * a.row_bytes;
-        if constexpr (NM == 2) wrow[r][1] = a.w_up + (int64_t)R * a.row_bytes;
-        yrow[r] = ok ? a.seg[s].y + R : nullptr;
-        ystride[r] = a.seg[s].rows;
-    }
+    rows_of(row0, wrow, yrow, ystride);
 
     for (int b0 = 0; b0 < a.batch; b0 += NB) {
         float acc[RPW][NM][NB];
@@ -539,7 +556,20 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvArgs a) {
             }
         };
         int g = tid;
-        if (g < G) fetch(g, cur, cxa, cxb);
+        if (g < G) {
+            if (first) {  // weights prefetched before the prologue; x from LDS
+#pragma unroll
+                for (int r = 0; r < RPW; ++r)
+#pragma unroll
+                    for (int m = 0; m < NM; ++m) cur[r][m] = wpre[r][m];
+                int ca, cb;
+                group_cols<QT>(g, ca, cb);
+                cxa[0] = ldf4(s_x + ca);
+                cxb[0] = ldf4(s_x + cb);
+            } else {
+                fetch(g, cur, cxa, cxb);
+            }
+        }
         for (; g < G; g += kGemvThreads) {
             const int gn = g + kGemvThreads;
             if (gn < G) fetch(gn, nxt, nxa, nxb);
@@ -566,10 +596,17 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvArgs a) {
         } else {
         for (int g = tid; g < G; g += kGemvThreads) {
             WGroup<QT> wg[RPW][NM];
+            if (first && g == tid) {  // the group prefetched before the prologue
 #pragma unroll
-            for (int r = 0; r < RPW; ++r)
+                for (int r = 0; r < RPW; ++r)
 #pragma unroll
-                for (int m = 0; m < NM; ++m) wg[r][m].load(wrow[r][m], (uint32_t)g);
+                    for (int m = 0; m < NM; ++m) wg[r][m] = wpre[r][m];
+            } else {
+#pragma unroll
+                for (int r = 0; r < RPW; ++r)
+#pragma unroll
+                    for (int m = 0; m < NM; ++m) wg[r][m].load(wrow[r][m], (uint32_t)g);
+            }
             int ca, cb;
             group_cols<QT>(g, ca, cb);
 #pragma unroll
