@@ -202,8 +202,9 @@ PRO_CASES = {
 
 @pytest.mark.parametrize("qtype", QTYPES)
 @pytest.mark.parametrize("case", list(PRO_CASES))
-@pytest.mark.parametrize("rows,cols", [(1536, 2048), (37, 1536), (300, 256)])
+@pytest.mark.parametrize("rows,cols", [(1536, 2048), (37, 1536), (300, 256), (64, 6144)])
 def test_gemv_prologue_norm(dev, oracle, qtype, case, rows, cols):
+    """Input widths up to 4096 take the register prologue, 6144 the looping one."""
     c = PRO_CASES[case]
     raw, wd = random_matrix(qtype, rows, cols, seed=rows + cols)
     x = synth.normal_f32(51, "x", (cols,), 0, 3.0)
@@ -227,9 +228,10 @@ def test_gemv_prologue_norm(dev, oracle, qtype, case, rows, cols):
 
 
 @pytest.mark.parametrize("qtype", [B.Q4_0, B.Q8_0, B.F32])
-def test_gemv_prologue_geglu_input(dev, oracle, qtype):
-    """v = gelu(x) * r (the per-layer-embedding projection's input)."""
-    rows, cols = 1536, 256
+@pytest.mark.parametrize("rows,cols", [(1536, 256), (96, 6144)])
+def test_gemv_prologue_geglu_input(dev, oracle, qtype, rows, cols):
+    """v = gelu(x) * r (the per-layer-embedding projection's input), register and looping
+    prologues."""
     raw, wd = random_matrix(qtype, rows, cols, seed=77)
     g = synth.normal_f32(52, "g", (cols,), 0, 2.0)
     u = synth.normal_f32(52, "u", (cols,))
