@@ -364,7 +364,10 @@ static void launch_t(const NormArgs& a, hipStream_t s) {
     const int64_t waves = a.rows * W;
     const int R = ZL_NORM_ROWS_PER_GROUP ? ZL_NORM_ROWS_PER_GROUP
                   : waves >= 8192 || (MODE != M_NORM && waves >= 2048) ? 2 : 1;
-    const bool late = waves >= 1024;  // weights after the first row's activations (k_norm_rows)
+    // weights after the first row's activations (k_norm_rows), except for NORM_ADD, whose
+    // single weight vector measured faster with the activations (2048 x 2560 bf16: 7.15
+    // against 7.45 us)
+    const bool late = waves >= 1024 && MODE != M_NORM_ADD;
     const bool vec = a.n % E == 0 && aligned16(a.x) && (MODE == M_NORM || aligned16(a.r)) &&
                      (MODE == M_NORM_ADD || aligned16(a.out)) && aligned16(a.w1) &&
                      (MODE != M_NORM_ADD_NORM || aligned16(a.w2)) && per_lane <= (W == 4 ? 16 : 8);
