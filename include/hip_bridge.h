@@ -309,6 +309,25 @@ void hip_attention_decode(int kv_dtype, const float* q, const void* k_cache, con
                           int pos_base, int max_len, int batch, int n_heads, int n_kv_heads,
                           int head_dim, float attn_scale, float softcap, int sliding_window,
                           void* workspace, size_t workspace_bytes, HipStream_t stream);
+/* new: the same call with the decode step's QK-norm + RoPE + KV append folded in (no
+ * counterpart in the reference, which runs hip_qk_norm_rope_kv's three steps as separate
+ * launches before attention): q holds the raw query heads (read only; not rewritten), and
+ * each token's own K / V row is formed from the raw k, v [batch][n_kv_heads][head_dim]
+ * (norm with k_norm_w, RoPE, v no-scale norm when v_norm) and written to its cache row
+ * (row base + position), exactly what hip_qk_norm_rope_kv would write, while attention uses
+ * it directly. k = v = NULL: the layer reads rows written earlier (KV-shared layers); only
+ * q is normalised and rotated. Norm weights may be NULL (no norm). rotary_dim / 2 must be a
+ * multiple of 8 with rotary_dim / 16 a power of two (or rotary_dim 0 = head_dim such);
+ * other shapes report HIP_BRIDGE_EUNSUPPORTED. Same workspace rule as hip_attention_decode. */
+void hip_attention_decode_qk(int kv_dtype, const float* q, const float* k, const float* v,
+                             const float* q_norm_w, const float* k_norm_w, int v_norm,
+                             void* k_cache, void* v_cache, float* out, int64_t cache_rows,
+                             int64_t row_stride, const int64_t* d_row_base, int64_t row_base,
+                             const int32_t* d_pos, int pos_base, int max_len, int batch,
+                             int n_heads, int n_kv_heads, int head_dim, int rotary_dim,
+                             float freq_base, float freq_scale, float eps, int use_unit_offset,
+                             float attn_scale, float softcap, int sliding_window,
+                             void* workspace, size_t workspace_bytes, HipStream_t stream);
 
 /* ---------------------------------------------------------------------------------- */
 /* Greedy token selection (replaces cuda_bridge.h:175) with ziglm's CPU definition      */

@@ -10,6 +10,7 @@ import numpy as np
 import pytest
 
 from attn_ref import attention_f64
+from tol import assert_bf16, assert_bitexact, assert_rel
 from oracle import oracle as O
 from ziglm_amd import bridge as B
 from ziglm_amd import synth
@@ -144,3 +145,102 @@ def test_attention_unsupported_group_is_noop(dev):
     finally:
         dev.strict = True
     assert np.all(d_out.to_numpy((32 * 64 * 4,), np.uint8) == 0x11)
+
+
+QK_SHAPES = [(8, 4, 256, 0), (8, 1, 512, 128), (8, 1, 256, 0), (4, 2, 64, 0), (16, 4, 128, 64)]
+
+
+@pytest.mark.parametrize("kv_dtype", [B.F32, B.BF16])
+@pytest.mark.parametrize("nh,nkv,d,rot", QK_SHAPES)
+@pytest.mark.parametrize("own", [True, False], ids=["own_kv", "reads_only"])
+@pytest.mark.parametrize("split", [False, True])
+def test_attention_decode_qk(dev, oracle, kv_dtype, nh, nkv, d, rot, own, split):
+    """hip_attention_decode_qk against the oracle's QK-norm + RoPE + KV append followed by a
+    float64 attention over the updated cache: the written cache rows (f32 within 1e-5 of the
+    rotated pair's norm, bf16 within 1 ulp), the untouched rows bit for bit, and the outputs
+    within the f32 attention bound. own_kv: the token's K/V row is formed in the kernel;
+    reads_only (KV-shared layers): q only, the row is already in the cache."""
+    B_, cap = 3, 2048
+    positions = np.array([0, 777, 2047], np.int32)
+    window = 300 if (d == 256 and nkv == 1) else 0
+    softcap = 30.0 if d == 128 else 0.0
+    v_norm = nkv == 1
+    base = 1e6 if rot else 1e4
+    eps = np.float32(1e-6)
+    rows = B_ * cap
+    row_base = np.arange(B_, dtype=np.int64) * cap
+    slots = row_base + positions
+    kc = synth.normal_f32(21, "kc", (rows, nkv * d))
+    vc = synth.normal_f32(21, "vc", (rows, nkv * d))
+    if kv_dtype == B.BF16:
+        kc, vc = oracle.bf16_to_f32(oracle.f32_to_bf16(kc)), oracle.bf16_to_f32(oracle.f32_to_bf16(vc))
+    q = synth.normal_f32(21, "q", (B_, nh, d))
+    k = synth.normal_f32(21, "k", (B_, nkv, d))
+    v = synth.normal_f32(21, "v", (B_, nkv, d))
+    wq = synth.normal_f32(21, "wq", (d,), 0, 0.1)
+    wk = synth.normal_f32(21, "wk", (d,), 0, 0.1)
+    kc_ref, vc_ref = kc.copy(), vc.copy()
+    q_ref = oracle.qk_norm_rope_kv(q, k if own else np.zeros((B_, 0), np.float32),
+                                   v if own else np.zeros((B_, 0), np.float32), wq, wk if own else None,
+                                   kc_ref, vc_ref, v_norm=v_norm and own, max_seq=cap, max_kv_dim=nkv * d,
+                                   pos=positions, slots=slots, n_heads=nh, n_kv_heads=nkv if own else 0,
+                                   head_dim=d, rotary_dim=rot, base=base, eps=eps, unit_offset=True)
+    if kv_dtype == B.BF16:  # the cache holds the rows rounded to bf16
+        kc_att, vc_att = oracle.bf16_to_f32(oracle.f32_to_bf16(kc_ref)), oracle.bf16_to_f32(oracle.f32_to_bf16(vc_ref))
+        d_kc, d_vc = dev.from_numpy(oracle.f32_to_bf16(kc)), dev.from_numpy(oracle.f32_to_bf16(vc))
+    else:
+        kc_att, vc_att = kc_ref, vc_ref
+        d_kc, d_vc = dev.from_numpy(kc), dev.from_numpy(vc)
+    scale = float(np.float32(1.0 / np.sqrt(d)))
+    ws = dev.attentionWorkspaceBytes(B_, nh, nkv, d, cap, window) if split else 0
+    d_out = dev.alloc(B_ * nh * d * 4)
+    keep = []  # device buffers alive until the launch has run
+    keep += [dev.from_numpy(a) for a in (q, k, v, wq, wk, row_base, positions)]
+    d_q, d_k, d_v, d_wq, d_wk, d_rb, d_pos = keep
+    dev.attentionDecodeQk(kv_dtype, d_q, d_k if own else None, d_v if own else None, d_wq, d_wk if own else None,
+                          v_norm and own, d_kc, d_vc, d_out, rows, nkv * d, d_rb, 0, d_pos, 0, cap, B_, nh, nkv, d,
+                          rot, base, 1.0, float(eps), True, scale, softcap, window,
+                          dev.alloc(ws) if ws else None, ws)
+    got = d_out.to_numpy((B_, nh * d), np.float32)
+    cdt = np.uint16 if kv_dtype == B.BF16 else np.float32
+    gk = d_kc.to_numpy(kc.shape, cdt)
+    gv = d_vc.to_numpy(vc.shape, cdt)
+    others = np.setdiff1d(np.arange(rows), slots if own else [])
+    ref_k0 = oracle.f32_to_bf16(kc) if kv_dtype == B.BF16 else kc
+    ref_v0 = oracle.f32_to_bf16(vc) if kv_dtype == B.BF16 else vc
+    assert_bitexact(gk[others], ref_k0[others], "untouched K rows")
+    assert_bitexact(gv[others], ref_v0[others], "untouched V rows")
+    if own:
+        kr = kc_ref[slots].reshape(B_, nkv, d)
+        vr = vc_ref[slots].reshape(B_, nkv, d)
+        if kv_dtype == B.BF16:
+            assert_bf16(gk[slots].reshape(B_, nkv, d), oracle.f32_to_bf16(kr), 1, what="bf16 K row")
+            assert_bf16(gv[slots].reshape(B_, nkv, d), oracle.f32_to_bf16(vr), 1, what="bf16 V row")
+        else:
+            eff = d if rot == 0 else rot
+            h = eff // 2
+            pn = np.sqrt(kr[..., :h].astype(np.float64) ** 2 + kr[..., h:2 * h].astype(np.float64) ** 2)
+            floor = np.zeros(kr.shape)
+            floor[..., :h] = 1e-5 * pn
+            floor[..., h:2 * h] = 1e-5 * pn
+            assert_rel(gk[slots].reshape(B_, nkv, d), kr, 1e-5, floor=floor, what="K row")
+            assert_rel(gv[slots].reshape(B_, nkv, d), vr, 1e-5, what="V row")
+    for b in range(B_):
+        check(got[b], q_ref[b].reshape(-1), kc_att, vc_att, int(row_base[b]), int(positions[b]), nh, nkv, d, scale,
+              softcap, window, f"seq {b} pos {positions[b]}")
+
+
+def test_attention_decode_qk_unsupported_rotary(dev):
+    """A rotary half that is not a power-of-two number of 8-element lane slices is
+    reported, nothing launched."""
+    d_buf = dev.alloc(1 << 20)
+    d_out = dev.alloc(4 * 256 * 4)
+    d_out.fill(0x11)
+    dev.strict = False
+    try:
+        dev.attentionDecodeQk(B.F32, d_buf, d_buf, d_buf, None, None, False, d_buf, d_buf, d_out, 16, 256, None, 0,
+                              None, 3, 16, 1, 4, 1, 256, 96, 1e4, 1.0, 1e-6, True, 0.0625, 0.0, 0)
+        assert dev.b.last_error() == B.EUNSUPPORTED
+    finally:
+        dev.strict = True
+    assert np.all(d_out.to_numpy((4 * 256 * 4,), np.uint8) == 0x11)

@@ -70,10 +70,10 @@ def reset(m, token):
     m.set_token(token)
 
 
-FUSE_SETS = [set(), {"qkv", "ffn", "ple", "head"}]
+FUSE_SETS = [set(), {"qkv", "ffn", "ple", "head"}, {"attn"}]
 
 
-@pytest.mark.parametrize("fused", FUSE_SETS, ids=["unfused", "prologues"])
+@pytest.mark.parametrize("fused", FUSE_SETS, ids=["unfused", "prologues", "qk_attention"])
 def test_decode_graph_equals_eager(dev, fused):
     """The captured step replays the eager step bit for bit, token fed back on the device."""
     m = DecodeModel.synthetic(dev, GEMMA_4B, n_layers=2, vocab=4096, max_seq=64, fused=fused)
@@ -98,7 +98,7 @@ def test_decode_graph_equals_eager(dev, fused):
         m.free()
 
 
-@pytest.mark.parametrize("fused", FUSE_SETS, ids=["unfused", "prologues"])
+@pytest.mark.parametrize("fused", FUSE_SETS, ids=["unfused", "prologues", "qk_attention"])
 def test_decode_step_vs_oracle(dev, oracle, fused):
     """Three decode steps of a 2-layer model against the oracle's composition of the same
     ops (same tokens fed to both). Each op is parity-tested on its own; this checks the

@@ -176,8 +176,8 @@ def check_token(gtok, ref, tol, what):
         assert gtok == int(np.argmax(ref[1:])) + 1, what
 
 
-FUSE_SETS = [True, set(), {"qkv", "ffn", "ple", "head"}]
-FUSE_IDS = ["default", "unfused", "prologues"]
+FUSE_SETS = [True, set(), {"qkv", "ffn", "ple", "head"}, {"attn", "ple"}]
+FUSE_IDS = ["default", "unfused", "prologues", "qk_attention"]
 
 
 @pytest.mark.parametrize("fused", FUSE_SETS, ids=FUSE_IDS)

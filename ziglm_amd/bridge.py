@@ -122,6 +122,8 @@ SIGNATURES = {
     "hip_attention_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i]),
     "hip_attention_decode": (None, [_i, _v, _v, _v, _v, _i64, _i64, _v, _i64, _v, _i, _i, _i, _i, _i, _i,
                                     _f, _f, _i, _v, _sz, _v]),
+    "hip_attention_decode_qk": (None, [_i, _v, _v, _v, _v, _v, _i, _v, _v, _v, _i64, _i64, _v, _i64, _v, _i, _i,
+                                       _i, _i, _i, _i, _i, _f, _f, _f, _i, _f, _f, _i, _v, _sz, _v]),
     "hip_geglu_ex": (None, [_i, _v, _v, _v, _i64, _v]),
     "hip_tanh_softcap_ex": (None, [_i, _v, _f, _i64, _v]),
     "hip_scale_ex": (None, [_i, _v, _f, _v, _i64, _v]),

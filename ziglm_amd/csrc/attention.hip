@@ -20,6 +20,7 @@
 // Arithmetic: f32 throughout, exp via exp2; results agree with the CPU's (which exponentiates
 // after a full max pass and normalises the weights before the weighted sum) within the f32
 // rounding of the scores, not bit for bit.
+#include <math.h>
 #include <algorithm>
 
 #include "zl_common.h"
@@ -49,6 +50,16 @@ struct AttnArgs {
     int gq;                   // query heads per kv head (nh / nkv)
     int hg;                   // workgroups per (token, kv head, split): each takes gq / hg heads
     float scale, softcap, inv_cap;
+    // QK mode (k_attn<..., true>): the query heads arrive raw and are normalised and rotated
+    // here, and the token's own K/V row is formed from the raw projections (not read from the
+    // cache) and written to the cache by one workgroup per kv head.
+    const float* qk_k;        // raw K / V of the tokens [batch][nkv][D], or null: reads only
+    const float* qk_v;
+    const float* qk_wq;       // per-head norm weights [D], or null: no norm
+    const float* qk_wk;
+    int qk_vnorm, qk_uo, qk_half;  // V no-scale norm; (1 + w) weights; rotary_dim / 2 (0: none)
+    float qk_eps, qk_freq_scale;
+    double qk_log2_base;
 };
 
 // Position range of token b, or an empty range when its rows fall outside the cache.
@@ -92,7 +103,37 @@ __device__ __forceinline__ void load8(const KT* row, float* v) {
     }
 }
 
-template <typename KT, int D, int G>
+// QK mode: RMSNorm of a head row held as 8 elements per lane over LT lanes (the norm
+// kernels' arithmetic: inv = rms_inv(sum of squares), then (x * inv) * factor).
+template <int LT>
+__device__ __forceinline__ void qk_norm8(float* x, int D, float eps, const float* wf) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss = fmaf(x[e], x[e], ss);
+    const float inv = rms_inv(group_sum<LT>(ss), D, eps);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = (x[e] * inv) * wf[e];
+}
+// Half-split RoPE of a head row held as 8 elements per lane: element i < half pairs with
+// i + half, which lives hl = half / 8 lanes further (hl a power of two, so the partner is
+// lane ^ hl within the row's lane group); cos / sin of pair i come from the LDS table. The
+// rotation is the QK kernel's: v0*c - v1*s, v0*s + v1*c.
+__device__ __forceinline__ void qk_rope8(float* x, int li, int half, const float* s_cos, const float* s_sin) {
+    const int hl = half >> 3;
+    float y[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) y[e] = __shfl_xor(x[e], hl);
+    if (li < 2 * hl) {
+        const int base = (li & (hl - 1)) * 8;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float c = s_cos[base + e], sn = s_sin[base + e];
+            x[e] = li < hl ? x[e] * c - y[e] * sn : y[e] * sn + x[e] * c;
+        }
+    }
+}
+
+template <typename KT, int D, int G, bool QK>
 __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
     constexpr int LT = D / 8;                  // lanes per position
     constexpr int SLOTS = kAttnThreads / LT;   // positions in flight per workgroup
@@ -101,6 +142,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
     // go through in passes of GM (LDS = SLOTS * GM * D * 4 <= 32 KB for every D).
     __shared__ float s_m[SLOTS][GM], s_l[SLOTS][GM];
     __shared__ float s_a[SLOTS][GM][D];
+    __shared__ float s_cos[QK ? D / 2 : 1], s_sin[QK ? D / 2 : 1];
     const int tid = threadIdx.x;
     const int slot = tid / LT;
     const int li = tid % LT;                   // 8-element slice of the head row
@@ -122,7 +164,18 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
     if (a.nsplit > 1 && split >= used) return;
     const int t0 = start + split * chunk;
     const int t1 = min(end, t0 + chunk);
+    const int last = end - 1;  // the token's own position (end > 0 whenever any work is done)
 
+    if constexpr (QK) {
+        // cos / sin of the token's position for the rotary pairs, while the q loads fly
+        if (a.qk_half > 0 && tid < a.qk_half && end > 0) {
+            const float theta = ((float)last * a.qk_freq_scale) / rope_denom(tid, 2 * a.qk_half, a.qk_log2_base);
+            double sn, cs;
+            sincos((double)theta, &sn, &cs);
+            s_cos[tid] = (float)cs;
+            s_sin[tid] = (float)sn;
+        }
+    }
     float q[G][8];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
@@ -130,6 +183,28 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
         const f32x4 x = ldf4(qh), y = ldf4(qh + 4);
         q[g][0] = x.x; q[g][1] = x.y; q[g][2] = x.z; q[g][3] = x.w;
         q[g][4] = y.x; q[g][5] = y.y; q[g][6] = y.z; q[g][7] = y.w;
+    }
+    // QK mode: per-element norm factors (1 + w), w or 1 of this lane's slice
+    auto norm_factors = [&](const float* w, float* f) {
+        if (w) {
+            const f32x4 x = ldf4(w + li * 8), y = ldf4(w + li * 8 + 4);
+            const float v[8] = {x.x, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) f[e] = a.qk_uo ? 1.0f + v[e] : v[e];
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) f[e] = 1.0f;
+        }
+    };
+    if constexpr (QK) {
+        float fq[8];
+        norm_factors(a.qk_wq, fq);
+        __syncthreads();  // the cos / sin table
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            if (a.qk_wq) qk_norm8<LT>(q[g], D, a.qk_eps, fq);
+            if (a.qk_half > 0) qk_rope8(q[g], li, a.qk_half, s_cos, s_sin);
+        }
     }
     float m[G], l[G], acc[G][8];
 #pragma unroll
@@ -139,39 +214,93 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[g][e] = 0.0f;
     }
+    // Online softmax step of one position for this lane group (k, v: its 8-element slices).
+    auto fold = [&](const float* k, const float* v, bool take) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            float s = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) s = fmaf(q[g][e], k[e], s);
+            s = group_sum<LT>(s) * a.scale;
+            if (a.softcap > 0.0f) s = a.softcap * tanh_fast(div_by_uniform(s, a.softcap, a.inv_cap));
+            if (take) {
+                const float mn = fmaxf(m[g], s);
+                const float c = exp2f((m[g] - mn) * kLog2e);
+                const float p = exp2f((s - mn) * kLog2e);
+                l[g] = l[g] * c + p;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(p, v[e], acc[g][e] * c);
+                m[g] = mn;
+            }
+        }
+    };
 
     const KT* kbase = (const KT*)a.kc + kvh * D + li * 8;
     const KT* vbase = (const KT*)a.vc + kvh * D + li * 8;
+    // QK mode with new K/V: the token's own position is not read from the cache (its row is
+    // written below); the split holding it folds it in after the loop.
+    const bool own = QK && a.qk_k != nullptr;
+    const int tc = own ? min(t1, last) : t1;
     // Each lane group takes U positions per step (t, t + SLOTS, ...), all 2U row loads issued
     // before any math, then folds them into its online softmax state in position order.
     constexpr int U = 4;
-    for (int t = t0 + slot; t < t1; t += U * SLOTS) {
+    for (int t = t0 + slot; t < tc; t += U * SLOTS) {
         float k[U][8], v[U][8];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int tu = t + u * SLOTS;
-            if (tu < t1) {
+            if (tu < tc) {
                 load8<KT>(kbase + (rb + tu) * a.row_stride, k[u]);
                 load8<KT>(vbase + (rb + tu) * a.row_stride, v[u]);
             }
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            if (t + u * SLOTS >= t1) break;  // uniform within a lane group
+            if (t + u * SLOTS >= tc) break;  // uniform within a lane group
+            fold(k[u], v[u], true);
+        }
+    }
+    if constexpr (QK) {
+        if (own && t0 <= last && last < t1) {  // block-uniform: the split holding the token
+            // Every lane group forms the row (uniform code); slot 0 folds it in and, in the
+            // first head group's workgroup, writes it to the cache.
+            const float* kr = a.qk_k + ((int64_t)b * a.nkv + kvh) * D + li * 8;
+            const float* vr = a.qk_v + ((int64_t)b * a.nkv + kvh) * D + li * 8;
+            const f32x4 k0 = ldf4(kr), k1 = ldf4(kr + 4), v0 = ldf4(vr), v1 = ldf4(vr + 4);
+            float kn[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+            float vn[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+            float fk[8];
+            norm_factors(a.qk_wk, fk);
+            if (a.qk_wk) qk_norm8<LT>(kn, D, a.qk_eps, fk);
+            if (a.qk_vnorm) {
+                float one[8];
 #pragma unroll
-            for (int g = 0; g < G; ++g) {
-                float s = 0.0f;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) s = fmaf(q[g][e], k[u][e], s);
-                s = group_sum<LT>(s) * a.scale;
-                if (a.softcap > 0.0f) s = a.softcap * tanh_fast(div_by_uniform(s, a.softcap, a.inv_cap));
-                const float mn = fmaxf(m[g], s);
-                const float c = exp2f((m[g] - mn) * kLog2e);
-                const float p = exp2f((s - mn) * kLog2e);
-                l[g] = l[g] * c + p;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(p, v[u][e], acc[g][e] * c);
-                m[g] = mn;
+                for (int e = 0; e < 8; ++e) one[e] = 1.0f;
+                qk_norm8<LT>(vn, D, a.qk_eps, one);
+            }
+            if (a.qk_half > 0) qk_rope8(kn, li, a.qk_half, s_cos, s_sin);
+            // attention uses the row as the cache holds it (bf16 caches: rounded), as it would
+            // read it back
+            u32x4 kp{}, vp{};
+            if constexpr (sizeof(KT) == 2) {
+                kp = Chunk<uint16_t>::pack(kn);
+                vp = Chunk<uint16_t>::pack(vn);
+                Chunk<uint16_t>::unpack(kp, kn);
+                Chunk<uint16_t>::unpack(vp, vn);
+            }
+            fold(kn, vn, slot == 0);
+            if (hgi == 0 && slot == 0) {
+                KT* kd = (KT*)a.kc + (rb + last) * a.row_stride + kvh * D + li * 8;
+                KT* vd = (KT*)a.vc + (rb + last) * a.row_stride + kvh * D + li * 8;
+                if constexpr (sizeof(KT) == 4) {
+                    *reinterpret_cast<f32x4*>(kd) = f32x4{kn[0], kn[1], kn[2], kn[3]};
+                    *reinterpret_cast<f32x4*>(kd + 4) = f32x4{kn[4], kn[5], kn[6], kn[7]};
+                    *reinterpret_cast<f32x4*>(vd) = f32x4{vn[0], vn[1], vn[2], vn[3]};
+                    *reinterpret_cast<f32x4*>(vd + 4) = f32x4{vn[4], vn[5], vn[6], vn[7]};
+                } else {
+                    *reinterpret_cast<u32x4*>(kd) = kp;
+                    *reinterpret_cast<u32x4*>(vd) = vp;
+                }
             }
         }
     }
@@ -299,15 +428,20 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_merge(AttnArgs a) {
     }
 }
 
-template <typename KT, int D>
-static void launch_g(const AttnArgs& a, hipStream_t s) {
+template <typename KT, int D, bool QK>
+static void launch_gq(const AttnArgs& a, hipStream_t s) {
     const unsigned grid = (unsigned)((int64_t)a.batch * a.nkv * a.hg * a.nsplit);
     switch (a.gq / a.hg) {
-        case 1: k_attn<KT, D, 1><<<grid, kAttnThreads, 0, s>>>(a); break;
-        case 2: k_attn<KT, D, 2><<<grid, kAttnThreads, 0, s>>>(a); break;
-        case 4: k_attn<KT, D, 4><<<grid, kAttnThreads, 0, s>>>(a); break;
-        default: k_attn<KT, D, 8><<<grid, kAttnThreads, 0, s>>>(a); break;
+        case 1: k_attn<KT, D, 1, QK><<<grid, kAttnThreads, 0, s>>>(a); break;
+        case 2: k_attn<KT, D, 2, QK><<<grid, kAttnThreads, 0, s>>>(a); break;
+        case 4: k_attn<KT, D, 4, QK><<<grid, kAttnThreads, 0, s>>>(a); break;
+        default: k_attn<KT, D, 8, QK><<<grid, kAttnThreads, 0, s>>>(a); break;
     }
+}
+template <typename KT, int D>
+static void launch_g(const AttnArgs& a, bool qk, hipStream_t s) {
+    if (qk) launch_gq<KT, D, true>(a, s);
+    else launch_gq<KT, D, false>(a, s);
 }
 
 // Query heads per workgroup. Each workgroup loads its positions' K/V rows once for all the
@@ -352,7 +486,7 @@ static void choose_split(AttnArgs& a, size_t ws_bytes) {
     a.nsplit = nsplit;
 }
 
-static void launch_attn(int kv_dtype, AttnArgs& a, size_t ws_bytes, hipStream_t s) {
+static void launch_attn(int kv_dtype, AttnArgs& a, size_t ws_bytes, hipStream_t s, bool qk = false) {
     if (a.batch <= 0 || a.nh <= 0) return;
     const int G = a.nkv > 0 ? a.nh / a.nkv : 0;
     if (!a.q || !a.kc || !a.vc || !a.out || a.nkv <= 0 || a.nh % a.nkv != 0 || a.max_len <= 0) {
@@ -374,16 +508,28 @@ static void launch_attn(int kv_dtype, AttnArgs& a, size_t ws_bytes, hipStream_t 
         set_error(HIP_BRIDGE_EUNSUPPORTED);
         return;
     }
+    if (qk) {
+        // QK mode: the rotary pairs must be whole 8-element lane slices a power-of-two number
+        // of lanes apart; aligned raw K / V rows and norm weights
+        const int hl = a.qk_half / 8;
+        const bool rope_ok = a.qk_half == 0 || (a.qk_half % 8 == 0 && (hl & (hl - 1)) == 0 && 2 * a.qk_half <= a.D);
+        const bool qk_ok = rope_ok && aligned16(a.qk_k) && aligned16(a.qk_v) && aligned16(a.qk_wq) &&
+                           aligned16(a.qk_wk) && (!a.qk_k) == (!a.qk_v);
+        if (!qk_ok) {
+            set_error(HIP_BRIDGE_EUNSUPPORTED);
+            return;
+        }
+    }
     if (kv_dtype == HIP_BRIDGE_F32) {
-        if (a.D == 64) launch_g<float, 64>(a, s);
-        else if (a.D == 128) launch_g<float, 128>(a, s);
-        else if (a.D == 256) launch_g<float, 256>(a, s);
-        else launch_g<float, 512>(a, s);
+        if (a.D == 64) launch_g<float, 64>(a, qk, s);
+        else if (a.D == 128) launch_g<float, 128>(a, qk, s);
+        else if (a.D == 256) launch_g<float, 256>(a, qk, s);
+        else launch_g<float, 512>(a, qk, s);
     } else {
-        if (a.D == 64) launch_g<uint16_t, 64>(a, s);
-        else if (a.D == 128) launch_g<uint16_t, 128>(a, s);
-        else if (a.D == 256) launch_g<uint16_t, 256>(a, s);
-        else launch_g<uint16_t, 512>(a, s);
+        if (a.D == 64) launch_g<uint16_t, 64>(a, qk, s);
+        else if (a.D == 128) launch_g<uint16_t, 128>(a, qk, s);
+        else if (a.D == 256) launch_g<uint16_t, 256>(a, qk, s);
+        else launch_g<uint16_t, 512>(a, qk, s);
     }
     if (a.nsplit > 1)
         k_attn_merge<<<dim3((unsigned)((int64_t)a.batch * a.nh), (unsigned)(a.D / kMergeCols)), kAttnThreads, 0, s>>>(a);
@@ -451,6 +597,39 @@ void hip_attention_decode(int kv_dtype, const float* q, const void* k_cache, con
     a.batch = batch;
     if (!aligned16(workspace)) a.ws = nullptr;
     launch_attn(kv_dtype, a, workspace_bytes, stream_of(stream));
+}
+
+void hip_attention_decode_qk(int kv_dtype, const float* q, const float* k, const float* v,
+                             const float* q_norm_w, const float* k_norm_w, int v_norm, void* k_cache,
+                             void* v_cache, float* out, int64_t cache_rows, int64_t row_stride,
+                             const int64_t* d_row_base, int64_t row_base, const int32_t* d_pos, int pos_base,
+                             int max_len, int batch, int n_heads, int n_kv_heads, int head_dim, int rotary_dim,
+                             float freq_base, float freq_scale, float eps, int use_unit_offset, float attn_scale,
+                             float softcap, int sliding_window, void* workspace, size_t workspace_bytes,
+                             HipStream_t stream) {
+    AttnArgs a = base_attn(q, k_cache, v_cache, out, n_heads, n_kv_heads, head_dim, attn_scale, softcap,
+                           sliding_window);
+    a.ws = aligned16(workspace) ? (float*)workspace : nullptr;
+    a.cache_rows = cache_rows;
+    a.row_stride = row_stride;
+    a.row_base = d_row_base;
+    a.row0 = row_base;
+    a.pos = d_pos;
+    a.pos_base = pos_base;
+    a.max_len = max_len;
+    a.batch = batch;
+    a.qk_k = k;
+    a.qk_v = v;
+    a.qk_wq = q_norm_w;
+    a.qk_wk = k_norm_w;
+    a.qk_vnorm = v_norm;
+    a.qk_uo = use_unit_offset;
+    const int eff = (rotary_dim <= 0 || rotary_dim > head_dim) ? head_dim : rotary_dim;
+    a.qk_half = eff / 2;
+    a.qk_eps = eps;
+    a.qk_freq_scale = freq_scale;
+    a.qk_log2_base = log2((double)freq_base);
+    launch_attn(kv_dtype, a, workspace_bytes, stream_of(stream), true);
 }
 
 void hip_attention_forward(const float* q, const float* k_cache, const float* v_cache, float* out,

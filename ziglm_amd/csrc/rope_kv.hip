@@ -40,15 +40,6 @@ struct RopeTab {
     float denom[kMaxHalf];
 };
 
-// D_i = f32(base^(f32(2i)/f32(eff))) evaluated in double precision as exp2(e_i * log2(base)),
-// with log2(base) computed once on the host (double). The double result is within ~1e-15
-// relative of the exact power, so its f32 rounding equals the oracle's f32(pow(base, e_i))
-// except within ~1e-15 of an f32 rounding tie (tests/test_gpu_parity.py checks RoPE outputs
-// bit for bit). Computed per lane, no memory access.
-__device__ __forceinline__ float rope_denom(int i, int eff, double log2_base) {
-    const float e = (float)(2 * i) / (float)eff;
-    return (float)exp2((double)e * log2_base);
-}
 
 struct QkArgs {
     void* q;

@@ -191,6 +191,16 @@ __device__ __forceinline__ float w_factor(float w, bool has_w, int uo) {
     return has_w ? (uo ? 1.0f + w : w) : 1.0f;
 }
 
+// RoPE denominator D_i = f32(base^(f32(2i)/f32(eff))) evaluated in double precision as
+// exp2(e_i * log2(base)), with log2(base) computed once on the host (double). The double
+// result is within ~1e-15 relative of the exact power, so its f32 rounding equals the
+// oracle's f32(pow(base, e_i)) except within ~1e-15 of an f32 rounding tie (the GPU parity
+// tests check RoPE outputs bit for bit). Computed per lane, no memory access.
+__device__ __forceinline__ float rope_denom(int i, int eff, double log2_base) {
+    const float e = (float)(2 * i) / (float)eff;
+    return (float)exp2((double)e * log2_base);
+}
+
 // ---- tanh / GELU / soft-cap ------------------------------------------------------------
 // Kernel tanh (a fast formulation, not the oracle's musl algorithm; both are accurate to a
 // few ulp, so they agree within the tolerances the tests state):

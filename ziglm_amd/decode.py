@@ -11,8 +11,9 @@ Per step, with the token id and position in device buffers, in the CPU forward's
     xb = input RMSNorm(x) (or x)                                     (543-548)
     q[, k, v] = QKV projections (one launch when all three share a type) (555-558, 617-623)
     Q-norm, K-norm, Gemma-4 V no-scale norm, RoPE(pos), K/V append to layer l's rows
-      (one fused launch; a KV-shared layer only normalises and rotates Q) (560-656)
-    attn = decode attention over the rows of layer kv_layer          (658-700)
+      (a KV-shared layer only normalises and rotates Q) (560-656), then
+    attn = decode attention over the rows of layer kv_layer          (658-700):
+      one launch for both by default ("attn": hip_attention_decode_qk), else two
     x += post-attn-norm(O attn); xb = pre-FFN-norm(x)                 (702-727)
     act = GeGLU(gate xb, up xb) (in the GEMV when both share a type)   (729-744)
     x += post-FFN-norm(down act)                                      (746-755)
@@ -46,8 +47,8 @@ class DecodeModel:
         """Decode state (activations, f32 KV cache [layers][max_seq][max_kv_dim],
         attention workspace) for `model`; own_model: free the model with this object;
         fused: True for the default set of products that take their norms / residual adds
-        in a prologue (default_fuse), False for none, or a set of "qkv", "ffn", "ple",
-        "head"."""
+        in a prologue, and whether attention takes the QK-norm / RoPE / KV append
+        (default_fuse), False for none, or a set of "qkv", "ffn", "ple", "head", "attn"."""
         if model.activation != "geglu":
             raise NotImplementedError(f"{model.arch}: only the GeGLU (Gemma) feed-forward is built")
         missing = [f"blk.{l.index}" for l in model.layers
@@ -160,7 +161,8 @@ class DecodeModel:
         """Per layer: QKV, QK-norm / RoPE / KV append, attention, O, gate.up GeGLU, down
         [, PLE gate, PLE projection]; then the LM head, soft-cap and argmax. Each norm /
         residual add runs in the prologue of the product that consumes it when that product
-        is in self.fuse ("qkv", "ffn", "ple", "head"), else as its own launch (adjacent norms
+        is in self.fuse ("qkv", "ffn", "ple", "head"; "attn": QK work inside attention),
+        else as its own launch (adjacent norms
         fused: post-attention norm + add + pre-FFN norm; post-FFN norm + add + next input
         norm)."""
         m, d, F = self.model, self.dev, self.fuse
@@ -222,9 +224,20 @@ class DecodeModel:
         d.argmax(self.logits, self.V, self.token)
 
     def _attention_core(self, ly):
-        """QK-norm / RoPE / KV append, attention, O projection (q, k, v -> ao)."""
+        """QK-norm / RoPE / KV append, attention, O projection (q, k, v -> ao). With "attn"
+        in the fuse set (and a rotary width the fused kernel takes), one attention launch
+        normalises and rotates q and forms, uses and stores the token's K/V row."""
         m, d = self.model, self.dev
         shared = ly.kv_shared
+        if "attn" in self.fuse and qk_attention_ok(ly):
+            d.attentionDecodeQk(B.F32, self.q, None if shared else self.k, None if shared else self.v,
+                                ly.attn_q_norm, None if shared else ly.attn_k_norm, ly.v_norm and not shared,
+                                self.kc, self.vc, self.attn, self.cache_rows, self.kv_dim, None,
+                                ly.kv_layer * self.max_seq, self.pos, 0, self.max_seq, 1, ly.n_heads, ly.n_kv_heads,
+                                ly.head_dim, ly.rotary_dim, ly.rope_theta, m.rope_freq_scale, m.eps, m.unit_offset,
+                                ly.attn_scale, m.attn_softcap, ly.sliding_window, self.ws, self.ws_bytes)
+            self._gemv(ly.attn_output, self.attn, self.ao)
+            return
         d.qkNormRopeKv(B.F32, self.q, None if shared else self.k, None if shared else self.v, ly.attn_q_norm,
                        None if shared else ly.attn_k_norm, ly.v_norm and not shared, self.kc, self.vc,
                        self.cache_rows, ly.index, self.max_seq, self.kv_dim, self.pos, 0, None, 1, ly.n_heads,
@@ -294,6 +307,14 @@ class DecodeModel:
             self.model.free()
 
 
+def qk_attention_ok(ly):
+    """Whether the fused QK + attention kernel takes the layer's RoPE: rotary_dim / 2 a
+    multiple of 8 with rotary_dim / 16 a power of two."""
+    eff = ly.head_dim if (ly.rotary_dim <= 0 or ly.rotary_dim > ly.head_dim) else ly.rotary_dim
+    hl = eff // 2 // 8
+    return (eff // 2) % 8 == 0 and hl > 0 and (hl & (hl - 1)) == 0 and ly.head_dim in (64, 128, 256, 512)
+
+
 def default_fuse(model):
     """Products that take their norms in a prologue by default. Every workgroup of a
     prologue product recomputes the input (norm statistics included), so the prologue pays
@@ -301,8 +322,9 @@ def default_fuse(model):
     projection (whose prologue is gelu(gate) * ple, no statistics). Measured, graph decode
     step, us per token (E2B-shaped 35 x 1536 / Gemma-4B-shaped 34 x 2560): no prologues
     2103 / 2071; PLE 2065 / -; QKV 2114 / 2096; gate.up 2163 / 2168; LM head 2154 / 2097;
-    QKV + PLE 2048 / -; all 2140 / 2259."""
-    return {"ple"}
+    QKV + PLE 2048 / -; all 2140 / 2259. "attn" (QK-norm / RoPE / KV append inside the
+    attention launch, one launch fewer per layer): 1802 -> 1736 / 1895 -> 1846."""
+    return {"ple", "attn"}
 
 
 def cache_bytes(model, max_seq):

@@ -319,6 +319,18 @@ class HipDevice:
                                     sliding_window, _ptr(d_workspace), workspace_bytes, self.stream)
         self._done("attentionDecode")
 
+    def attentionDecodeQk(self, kv_dtype, d_q, d_k, d_v, d_q_norm_w, d_k_norm_w, v_norm, d_k_cache, d_v_cache,
+                          d_out, cache_rows, row_stride, d_row_base, row_base, d_pos, pos_base, max_len, batch,
+                          n_heads, n_kv_heads, head_dim, rotary_dim, freq_base, freq_scale, eps, use_unit_offset,
+                          attn_scale, softcap, sliding_window, d_workspace=None, workspace_bytes=0):
+        self.b.hip_attention_decode_qk(int(kv_dtype), _ptr(d_q), _ptr(d_k), _ptr(d_v), _ptr(d_q_norm_w),
+                                       _ptr(d_k_norm_w), int(bool(v_norm)), _ptr(d_k_cache), _ptr(d_v_cache),
+                                       _ptr(d_out), cache_rows, row_stride, _ptr(d_row_base), row_base, _ptr(d_pos),
+                                       pos_base, max_len, batch, n_heads, n_kv_heads, head_dim, rotary_dim,
+                                       freq_base, freq_scale, eps, int(bool(use_unit_offset)), attn_scale, softcap,
+                                       sliding_window, _ptr(d_workspace), workspace_bytes, self.stream)
+        self._done("attentionDecodeQk")
+
     def gegluEx(self, dtype, d_gate, d_up, d_out, n):
         self.b.hip_geglu_ex(dtype, _ptr(d_gate), _ptr(d_up), _ptr(d_out), n, self.stream)
         self._done("gegluEx")
