@@ -200,6 +200,32 @@ def test_decode_loaded_model_vs_oracle(dev, oracle, cfg, fused):
         dm.free()
 
 
+def test_decode_e2b_full_shape_vs_oracle(dev, oracle, tmp_path):
+    """The gemma-4-E2B-shaped model the benchmark decodes (35 layers, 1536 hidden, 8/1 heads
+    x 256 with a 512 window | 512 with rotary 128, FFN 6144, per-layer embeddings, 15
+    unshared KV layers, tied 262144-row LM head; Q4_0; the default fuse set, so the fused QK
+    attention and the prologue GEMVs run at their real shapes): three decode steps against
+    the oracle's forward pass over the same file."""
+    path = str(tmp_path / "e2b.gguf")
+    S.build(S.E2B, seed=11).write(path)  # streamed: 2.3 GB
+    with open(path, "rb") as fh:
+        data = fh.read()
+    ref = MR.RefModel(oracle, data, max_seq=16)
+    with G.GGUFFile.open(path) as f:
+        dm = DecodeModel(dev, Model.from_gguf(dev, f), max_seq=16, own_model=True)
+    try:
+        dm.reset(0)
+        for pos, tok in enumerate([2, 1234, 99999]):
+            dm.set_token(tok)
+            dm.step(pos, graph=False)
+            got = dm.logits.to_numpy((dm.V,), np.float32)
+            want = ref.forward(tok, pos)
+            tol = check_logits(got, want, f"e2b pos {pos}")
+            check_token(dm.read_token(), want.astype(np.float64), tol, f"e2b pos {pos}")
+    finally:
+        dm.free()
+
+
 @pytest.mark.parametrize("fused", FUSE_SETS, ids=FUSE_IDS)
 def test_decode_loaded_graph_equals_eager(dev, fused):
     data = gguf_bytes(GEMMA4)
