@@ -319,11 +319,12 @@ def default_fuse(model):
     """Products that take their norms in a prologue by default. Every workgroup of a
     prologue product recomputes the input (norm statistics included), so the prologue pays
     only where the product has few workgroups: the per-layer-embedding gate (256 rows) and
-    projection (whose prologue is gelu(gate) * ple, no statistics). Measured, graph decode
-    step, us per token (E2B-shaped 35 x 1536 / Gemma-4B-shaped 34 x 2560): no prologues
-    2103 / 2071; PLE 2065 / -; QKV 2114 / 2096; gate.up 2163 / 2168; LM head 2154 / 2097;
-    QKV + PLE 2048 / -; all 2140 / 2259. "attn" (QK-norm / RoPE / KV append inside the
-    attention launch, one launch fewer per layer): 1802 -> 1736 / 1895 -> 1846."""
+    projection (whose prologue is gelu(gate) * ple, no statistics). "attn" puts the QK-norm /
+    RoPE / KV append inside the attention launch (one launch fewer per layer). Measured,
+    graph decode step, us per token (E2B-shaped 35 x 1536 / Gemma-4B-shaped 34 x 2560), with
+    "attn" in every set: PLE 1737 / -; + QKV 1754 / 1886-1892; + gate.up 1867 / 2017-2025;
+    + LM head 1806-1812 / 1904-1909; + all three 1939-1942 / -; none of the three
+    - / 1849-1850. Before "attn": no prologues 2103 / 2071, PLE 2065 / -."""
     return {"ple", "attn"}
 
 
