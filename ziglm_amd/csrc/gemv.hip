@@ -114,30 +114,44 @@ __device__ __forceinline__ float h2f(uint32_t h) {
 template <int QT>
 struct WGroup {
     uint32_t v[QT == HIP_BRIDGE_F32 ? 8 : 4];
-    // row: the row's base (uniform across the workgroup); g: the lane's group. Offsets are
-    // unsigned 32-bit so each load is a scalar base plus a 32-bit vector offset, shared by
-    // all rows (no per-row 64-bit address arithmetic).
-    __device__ __forceinline__ void load(const unsigned char* row, uint32_t g) {
+    // The lane's byte offsets inside a row for group g: computed once per group and shared
+    // by all rows. Unsigned 32-bit, so each load is the row's (uniform) base plus a 32-bit
+    // vector offset (no per-row 64-bit address arithmetic).
+    struct Off {
+        uint32_t a, b;
+    };
+    __device__ __forceinline__ static Off off(uint32_t g) {
         if constexpr (QT == HIP_BRIDGE_Q4_0) {
-            const uint32_t blk = (g >> 2) * 18u;
-            v[0] = ldw16(row + blk);                       // d
-            const uint32_t qs = opaque(blk + 2u + (g & 3u) * 4u);
-            v[1] = ldw32_a2(row + qs);                     // 4 low + 4 high nibbles
+            const uint32_t blk = opaque((g >> 2) * 18u);
+            return {blk, opaque(blk + 2u + (g & 3u) * 4u)};  // d; 4 low + 4 high nibbles
         } else if constexpr (QT == HIP_BRIDGE_Q8_0) {
-            const uint32_t blk = (g >> 2) * 34u;
-            v[0] = ldw16(row + blk);
-            const uint32_t qs = opaque(blk + 2u + (g & 3u) * 8u);
-            v[1] = ldw32_a2(row + qs);
-            v[2] = ldw32_a2(row + (qs + 4u));
+            const uint32_t blk = opaque((g >> 2) * 34u);
+            return {blk, opaque(blk + 2u + (g & 3u) * 8u)};
         } else if constexpr (QT == HIP_BRIDGE_F32) {
-            const u32x4 a = ld16(row + 32u * g), b = ld16(row + (32u * g + 16u));
+            return {32u * g, 32u * g + 16u};
+        } else {  // F16, BF16
+            return {16u * g, 0u};
+        }
+    }
+    __device__ __forceinline__ void load(const unsigned char* row, const Off& o) {
+        if constexpr (QT == HIP_BRIDGE_Q4_0) {
+            v[0] = ldw16(row + o.a);
+            v[1] = ldw32_a2(row + o.b);
+        } else if constexpr (QT == HIP_BRIDGE_Q8_0) {
+            v[0] = ldw16(row + o.a);
+            v[1] = ldw32_a2(row + o.b);
+            v[2] = ldw32_a2(row + (o.b + 4u));
+        } else if constexpr (QT == HIP_BRIDGE_F32) {
+            const u32x4 a = ld16(row + o.a), b = ld16(row + o.b);
             v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
             v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-        } else {  // F16, BF16
-            const u32x4 a = ld16(row + 16u * g);
+        } else {
+            const u32x4 a = ld16(row + o.a);
             v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
         }
     }
+    // row: the row's base (uniform across the workgroup); g: the lane's group.
+    __device__ __forceinline__ void load(const unsigned char* row, uint32_t g) { load(row, off(g)); }
     // sum_j w_j * x_j over the group's 8 columns; xa / xb are the x values of columns
     // [8g, 8g+4) and [8g+4, 8g+8), or for Q4_0 of [32b+o, +4) and [32b+16+o, +4); sx is
     // their sum. Block types take the CPU's form (math.zig:304-305): with u_j the stored
@@ -159,23 +173,27 @@ struct WGroup {
                 ub = v[2] ^ 0x80808080u;
                 k = 128.0f;
             }
-            float t = 0.0f;
+            // The first term is a product, not an fma onto 0 (the same rounding; no zeroed
+            // register per row).
+            float t = (float)(ua & 0xff) * a[0];
+            t = fmaf((float)(ub & 0xff), b[0], t);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
+            for (int j = 1; j < 4; ++j) {
                 t = fmaf((float)((ua >> (8 * j)) & 0xff), a[j], t);
                 t = fmaf((float)((ub >> (8 * j)) & 0xff), b[j], t);
             }
             return h2f(v[0]) * fmaf(-k, sx, t);
         } else if constexpr (QT == HIP_BRIDGE_F32) {
-            float s = 0.0f;
+            float s = __uint_as_float(v[0]) * a[0];
+            s = fmaf(__uint_as_float(v[4]), b[0], s);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
+            for (int j = 1; j < 4; ++j) {
                 s = fmaf(__uint_as_float(v[j]), a[j], s);
                 s = fmaf(__uint_as_float(v[4 + j]), b[j], s);
             }
             return s;
         } else {
-            float s = 0.0f;
+            float s = -0.0f;  // x + -0 == x for every x: the first fma is a product
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 float w0, w1, w2, w3;
@@ -220,6 +238,11 @@ __device__ __forceinline__ float sum4(const f32x4& x) { return (x.x + x.y) + (x.
 template <>
 struct WGroup<HIP_BRIDGE_Q4_K> {
     uint32_t dm, s0, s1, s2, q, jj;
+    struct Off {
+        uint32_t g;
+    };
+    __device__ __forceinline__ static Off off(uint32_t g) { return {g}; }
+    __device__ __forceinline__ void load(const unsigned char* row, const Off& o) { load(row, o.g); }
     __device__ __forceinline__ void load(const unsigned char* row, uint32_t g) {
         const uint32_t base = (g >> 5) * 144u, r = g & 31u;
         jj = r >> 3;
@@ -262,24 +285,35 @@ struct WGroup<HIP_BRIDGE_Q4_K> {
 // 8n + l0/16 + 2p and + 4 (math.zig:556-616: d * sum over quadrants of scale * (u - 32) * x).
 template <>
 struct WGroup<HIP_BRIDGE_Q6_K> {
-    uint32_t ql, qh, sc, dd, p;
-    __device__ __forceinline__ void load(const unsigned char* row, uint32_t g) {
+    // The loaded words are kept as loaded and combined in dot(), so that nothing waits for
+    // a load before the next group's loads are issued.
+    uint32_t ql, qh, wa, wb, dd, p, sh;
+    struct Off {
+        uint32_t oq, oh, os, od, p, sh;
+    };
+    __device__ __forceinline__ static Off off(uint32_t g) {
         const uint32_t base = (g >> 5) * 210u, r = g & 31u, n = r >> 4, rr = r & 15u;
-        const uint32_t l0 = 4u * (rr >> 1);
-        p = rr & 1u;
-        const uint32_t oq = base + 64u * n + 32u * p + l0, oh = base + 128u + 32u * n + l0;
-        ql = ldw16(row + oq) | (ldw16(row + (oq + 2u)) << 16);
-        qh = ldw16(row + oh) | (ldw16(row + (oh + 2u)) << 16);
-        const uint32_t ia = base + 192u + 8u * n + (l0 >> 4) + 2u * p, ib = ia + 4u;
-        const uint32_t wa = ldw16(row + (ia & ~1u)), wb = ldw16(row + (ib & ~1u));
-        sc = ((wa >> (8u * (ia & 1u))) & 0xffu) | (((wb >> (8u * (ib & 1u))) & 0xffu) << 8);
-        dd = ldw16(row + (base + 208u));
+        const uint32_t l0 = 4u * (rr >> 1), p = rr & 1u;
+        // scale bytes ia = base + 192 + 8n + l0/16 + 2p and ia + 4: the 16-bit words at
+        // ia & ~1 and ia & ~1 + 4, byte l0/16 of each
+        return {opaque(base + 64u * n + 32u * p + l0), opaque(base + 128u + 32u * n + l0),
+                opaque(base + 192u + 8u * n + 2u * p), opaque(base + 208u), p, (l0 >> 1) & 8u};
     }
+    __device__ __forceinline__ void load(const unsigned char* row, const Off& o) {
+        ql = ldw32_a2(row + o.oq);
+        qh = ldw32_a2(row + o.oh);
+        wa = ldw16(row + o.os);
+        wb = ldw16(row + (o.os + 4u));
+        dd = ldw16(row + o.od);
+        p = o.p;
+        sh = o.sh;
+    }
+    __device__ __forceinline__ void load(const unsigned char* row, uint32_t g) { load(row, off(g)); }
     __device__ __forceinline__ float dot(const f32x4& xa, const f32x4& xb, float) const {
         const uint32_t ha = (qh >> (2u * p)) & 0x03030303u, hb = (qh >> (4u + 2u * p)) & 0x03030303u;
         const uint32_t ua = mask_bytes(ql, 0x0f0f0f0fu) | (ha << 4);
         const uint32_t ub = mask_bytes(ql >> 4, 0x0f0f0f0fu) | (hb << 4);
-        const float sa = (float)(int8_t)(sc & 0xffu), sb = (float)(int8_t)(sc >> 8);
+        const float sa = (float)(int8_t)(uint8_t)(wa >> sh), sb = (float)(int8_t)(uint8_t)(wb >> sh);
         const float ta = fmaf(-32.0f, sum4(xa), dot4u(ua, xa));
         const float tb = fmaf(-32.0f, sum4(xb), dot4u(ub, xb));
         return h2f(dd) * fmaf(sa, ta, sb * tb);
@@ -506,10 +540,11 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvArgs a) {
         float* y0[RPW];
         int s0[RPW];
         rows_of(blockIdx.x * RPW, w0, y0, s0);
+        const typename WGroup<QT>::Off o = WGroup<QT>::off((uint32_t)min(tid, G - 1));
 #pragma unroll
         for (int r = 0; r < RPW; ++r)
 #pragma unroll
-            for (int m = 0; m < NM; ++m) wpre[r][m].load(w0[r][m], (uint32_t)min(tid, G - 1));
+            for (int m = 0; m < NM; ++m) wpre[r][m].load(w0[r][m], o);
         gemv_prologue(a, s_x, &s_part[0][0]);
     }
 
@@ -543,10 +578,11 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvArgs a) {
         WGroup<QT> cur[RPW][NM], nxt[RPW][NM];
         f32x4 cxa[NB], cxb[NB], nxa[NB], nxb[NB];
         auto fetch = [&](int g, WGroup<QT> (&w)[RPW][NM], f32x4 (&xa)[NB], f32x4 (&xb)[NB]) {
+            const typename WGroup<QT>::Off o = WGroup<QT>::off((uint32_t)g);
 #pragma unroll
             for (int r = 0; r < RPW; ++r)
 #pragma unroll
-                for (int m = 0; m < NM; ++m) w[r][m].load(wrow[r][m], (uint32_t)g);
+                for (int m = 0; m < NM; ++m) w[r][m].load(wrow[r][m], o);
             int ca, cb;
             group_cols<QT>(g, ca, cb);
 #pragma unroll
@@ -602,10 +638,11 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvArgs a) {
 #pragma unroll
                     for (int m = 0; m < NM; ++m) wg[r][m] = wpre[r][m];
             } else {
+                const typename WGroup<QT>::Off o = WGroup<QT>::off((uint32_t)g);
 #pragma unroll
                 for (int r = 0; r < RPW; ++r)
 #pragma unroll
-                    for (int m = 0; m < NM; ++m) wg[r][m].load(wrow[r][m], (uint32_t)g);
+                    for (int m = 0; m < NM; ++m) wg[r][m].load(wrow[r][m], o);
             }
             int ca, cb;
             group_cols<QT>(g, ca, cb);
@@ -671,15 +708,15 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvArgs a) {
 // are 320 groups), the row sums reduce within the wave (no LDS, no barrier), and the next
 // group's weights and x are loaded while the current group is multiplied.
 template <int QT, int RW, int MODE>
-__global__ __launch_bounds__(kGemvThreads) void k_gemv_w(GemvArgs a) {
+__global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(QT == HIP_BRIDGE_Q4_0 && MODE == GV_PLAIN ? 7 : 1))) void k_gemv_w(GemvArgs a) {
     constexpr int NM = MODE == GV_GEGLU ? 2 : 1;
     const int lane = threadIdx.x & 63;
     // The wave index is uniform across the wave: read from the first lane, it makes the row
     // pointers scalar (each load is a scalar base plus the lane's 32-bit offset).
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int row0 = (blockIdx.x * kGemvWaves + wv) * RW;
-    if (row0 >= a.total_rows) return;  // the whole wave
     const int G = a.cols / 8;
+    if (row0 >= a.total_rows || G <= 0) return;  // the whole wave
     const unsigned char* wrow[RW][NM];
     float* yrow[RW];
 #pragma unroll
@@ -704,37 +741,57 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_w(GemvArgs a) {
     for (int r = 0; r < RW; ++r)
 #pragma unroll
         for (int m = 0; m < NM; ++m) acc[r][m] = 0.0f;
-    auto fetch = [&](int g, WGroup<QT> (&w)[RW][NM], f32x4& xa, f32x4& xb) {
+    // Step k takes group lane + 64k. The step count is the same for every lane, so all
+    // branches below are uniform: a lane past the last group loads the last group again
+    // (in bounds) and drops its products. (A load under a per-lane branch would make the
+    // compiler wait for it where the branch ends, i.e. before the step that needs it.)
+    const int n = (G + kWave - 1) / kWave;
+    auto fetch = [&](int k, WGroup<QT> (&w)[RW][NM], f32x4& xa, f32x4& xb) {
+        const int g = min(lane + kWave * k, G - 1);
+        const typename WGroup<QT>::Off o = WGroup<QT>::off((uint32_t)g);
 #pragma unroll
         for (int r = 0; r < RW; ++r)
 #pragma unroll
-            for (int m = 0; m < NM; ++m) w[r][m].load(wrow[r][m], (uint32_t)g);
+            for (int m = 0; m < NM; ++m) w[r][m].load(wrow[r][m], o);
         int ca, cb;
         group_cols<QT>(g, ca, cb);
         xa = ldf4(a.x + ca);
         xb = ldf4(a.x + cb);
     };
-    auto fold = [&](const WGroup<QT> (&w)[RW][NM], const f32x4& xa, const f32x4& xb) {
+    auto fold = [&](const WGroup<QT> (&w)[RW][NM], const f32x4& xa, const f32x4& xb, int k, bool last) {
         const float sx = ((xa.x + xa.y) + (xa.z + xa.w)) + ((xb.x + xb.y) + (xb.z + xb.w));
+        const bool ok = !last || lane + kWave * k < G;
 #pragma unroll
         for (int r = 0; r < RW; ++r)
 #pragma unroll
-            for (int m = 0; m < NM; ++m) acc[r][m] += w[r][m].dot(xa, xb, sx);
+            for (int m = 0; m < NM; ++m) {
+                const float d = w[r][m].dot(xa, xb, sx);
+                if (last) acc[r][m] = ok ? acc[r][m] + d : acc[r][m];
+                else acc[r][m] += d;
+            }
     };
-    WGroup<QT> cur[RW][NM], nxt[RW][NM];
-    f32x4 cxa, cxb, nxa, nxb;
-    int g = lane;
-    if (g < G) fetch(g, cur, cxa, cxb);
-    for (; g < G; g += kWave) {
-        const int gn = g + kWave;
-        if (gn < G) fetch(gn, nxt, nxa, nxb);
-        fold(cur, cxa, cxb);
-#pragma unroll
-        for (int r = 0; r < RW; ++r)
-#pragma unroll
-            for (int m = 0; m < NM; ++m) cur[r][m] = nxt[r][m];
-        cxa = nxa;
-        cxb = nxb;
+    // Two register sets in turn (no copy of the prefetched set per step). The scheduling
+    // barriers keep each step's loads ahead of the previous step's arithmetic: otherwise
+    // the scheduler hoists that arithmetic, and with it the wait for its operands, above
+    // the new loads, and every step waits a full memory round trip.
+    WGroup<QT> wa[RW][NM], wb[RW][NM];
+    f32x4 axa, axb, bxa, bxb;
+    fetch(0, wa, axa, axb);
+    for (int k = 0;; k += 2) {
+        if (k + 1 >= n) {
+            fold(wa, axa, axb, k, true);
+            break;
+        }
+        fetch(k + 1, wb, bxa, bxb);
+        __builtin_amdgcn_sched_barrier(0);
+        fold(wa, axa, axb, k, false);
+        if (k + 2 >= n) {
+            fold(wb, bxa, bxb, k + 1, true);
+            break;
+        }
+        fetch(k + 2, wa, axa, axb);
+        __builtin_amdgcn_sched_barrier(0);
+        fold(wb, bxa, bxb, k + 1, false);
     }
 #pragma unroll
     for (int r = 0; r < RW; ++r) {
@@ -878,12 +935,15 @@ static void launch_vec(const GemvArgs& a, hipStream_t s) {
         }
     } else if (MODE == GV_PLAIN && a.batch == 1 && a.total_rows >= kGemvWaveRowsMin &&
                QT != HIP_BRIDGE_F16 && QT != HIP_BRIDGE_BF16 && QT != HIP_BRIDGE_F32) {
+        // (k_gemv_w is instantiated for these cases only)
+        if constexpr (MODE == GV_PLAIN && QT != HIP_BRIDGE_F16 && QT != HIP_BRIDGE_BF16 && QT != HIP_BRIDGE_F32) {
         // LM-head-sized block-quantised products: wave-owned rows (measured, 262144 x 2560,
         // us: Q4_K 226 -> 157 with 2 rows per wave, Q6_K 310 -> 177 with 4, Q8_0 185 -> 173
         // and Q4_0 137 -> 113 with 8; smaller matrices, whose rows are long against their
         // count, and dense types are faster above: 2560 x 10240 Q4_0 8.0 us above, 14.6 here)
         constexpr int RW = QT == HIP_BRIDGE_Q4_K ? 2 : QT == HIP_BRIDGE_Q6_K ? 4 : 8;
         k_gemv_w<QT, RW, MODE><<<(unsigned)cdiv(a.total_rows, (int64_t)RW * kGemvWaves), kGemvThreads, 0, s>>>(a);
+        }
     } else if (a.batch == 1) {
         if (QT == HIP_BRIDGE_Q4_0 && (a.total_rows >= 16384 || (MODE == GV_GEGLU && a.total_rows >= 4096)))
             k_gemv<QT, 8 / H, 1, MODE><<<g8, kGemvThreads, 0, s>>>(a);
