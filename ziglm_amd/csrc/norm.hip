@@ -86,7 +86,7 @@ __global__ __launch_bounds__(256) void k_norm_rows(NormArgs a) {
     constexpr int GPB = norm_gpb<W>();  // row groups per block
     constexpr int STRIDE = kWave * W;
     // one slot set per (row, reduction): no slot is rewritten while a wave may still read it
-    __shared__ float s_red[2 * R][4];
+    __shared__ float s_red[2 * R][W * GPB];
     const int rib = __builtin_amdgcn_readfirstlane((threadIdx.x >> 6) / W);  // group within block (wave-uniform)
     const int g = threadIdx.x - rib * STRIDE;
     const int64_t row0 = ((int64_t)blockIdx.x * GPB + rib) * R;
