@@ -166,6 +166,30 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
     const int t1 = min(end, t0 + chunk);
     const int last = end - 1;  // the token's own position (end > 0 whenever any work is done)
 
+    const KT* kbase = (const KT*)a.kc + kvh * D + li * 8;
+    const KT* vbase = (const KT*)a.vc + kvh * D + li * 8;
+    // QK mode with new K/V: the token's own position is not read from the cache (its row is
+    // written below); the split holding it folds it in after the loop.
+    const bool own = QK && a.qk_k != nullptr;
+    const int tc = own ? min(t1, last) : t1;
+    // Each lane group takes U positions per step (t, t + SLOTS, ...), all 2U row loads issued
+    // before any math, then folds them into its online softmax state in position order. A
+    // position past the range loads the range's last row instead (in bounds, no per-lane
+    // branch) and is not folded. The first step's rows are requested here, before the query
+    // is loaded and (QK mode) normalised and rotated, which does not need them.
+    constexpr int U = 4;
+    const int nstep = t0 < tc ? (tc - t0 + U * SLOTS - 1) / (U * SLOTS) : 0;  // uniform
+    float k[U][8], v[U][8];
+    auto load_step = [&](int t) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int tu = min(t + u * SLOTS, tc - 1);
+            load8<KT>(kbase + (rb + tu) * a.row_stride, k[u]);
+            load8<KT>(vbase + (rb + tu) * a.row_stride, v[u]);
+        }
+    };
+    if (nstep > 0) load_step(t0 + slot);
+
     if constexpr (QK) {
         // cos / sin of the token's position for the rotary pairs, while the q loads fly
         if (a.qk_half > 0 && tid < a.qk_half && end > 0) {
@@ -235,25 +259,9 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
         }
     };
 
-    const KT* kbase = (const KT*)a.kc + kvh * D + li * 8;
-    const KT* vbase = (const KT*)a.vc + kvh * D + li * 8;
-    // QK mode with new K/V: the token's own position is not read from the cache (its row is
-    // written below); the split holding it folds it in after the loop.
-    const bool own = QK && a.qk_k != nullptr;
-    const int tc = own ? min(t1, last) : t1;
-    // Each lane group takes U positions per step (t, t + SLOTS, ...), all 2U row loads issued
-    // before any math, then folds them into its online softmax state in position order.
-    constexpr int U = 4;
-    for (int t = t0 + slot; t < tc; t += U * SLOTS) {
-        float k[U][8], v[U][8];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int tu = t + u * SLOTS;
-            if (tu < tc) {
-                load8<KT>(kbase + (rb + tu) * a.row_stride, k[u]);
-                load8<KT>(vbase + (rb + tu) * a.row_stride, v[u]);
-            }
-        }
+    for (int st = 0; st < nstep; ++st) {
+        const int t = t0 + slot + st * U * SLOTS;
+        if (st > 0) load_step(t);
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             if (t + u * SLOTS >= tc) break;  // uniform within a lane group
