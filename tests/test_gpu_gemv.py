@@ -1,5 +1,6 @@
 """GEMV / small-batch GEMM on the GPU against the oracle (math.zig:25-330, 440-616, 652-846).
-Shapes include LM-head-sized row counts (>= 65536 rows: the wave-owned-rows kernel).
+Shapes include LM-head-sized row counts (>= 65536 rows: the wave-owned-rows kernel), with
+one, two and three column steps per lane and a last step that only some lanes fill.
 
 The kernels sum in a different order from ziglm's CPU code, so the checks are
   * bit-exact on integer-valued inputs (every partial sum is exact in f32, so any order
@@ -39,7 +40,8 @@ def run_gemm(dev, qtype, raw, X, rows, cols, batch):
 
 @pytest.mark.parametrize("qtype", QTYPES)
 @pytest.mark.parametrize("rows,cols,batch", [(37, 2560, 1), (16, 96, 1), (9, 10240, 1), (11, 512, 2),
-                                             (13, 2560, 3), (6, 256, 7), (65601, 256, 1)])
+                                             (13, 2560, 3), (6, 256, 7), (65601, 256, 1), (65601, 768, 1),
+                                             (65537, 1280, 1)])
 def test_gemv_integer_bitexact(dev, qtype, rows, cols, batch):
     if qtype in K_QUANTS and cols % 256:
         pytest.skip("super-block types need cols % 256 == 0")
