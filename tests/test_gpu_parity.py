@@ -1,7 +1,7 @@
 """GPU parity: every hip_bridge entry point against the CPU oracle on seeded inputs.
 
 All calls go through the C-ABI (ziglm_amd.device.HipDevice -> libhip_bridge.so).
-Tolerances (BASELINE north star):
+Tolerances (BASELINE.json north_star):
   gathers, KV copies, residual add/scale ....... bit-exact
   f32 norm / RoPE / GeGLU / soft-cap ............ 1e-5 relative; RoPE outputs relative to
       the norm of their rotation pair (a rotated coordinate can cancel to ~0); GeGLU adds

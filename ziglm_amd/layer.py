@@ -123,7 +123,8 @@ def op_input_norm(dev, L):
 
 
 def op_add_rmsnorm(dev, L):
-    """R1 as BASELINE states it: x += r, out = norm(x) (r = attention output buffer)."""
+    """Residual add + RMSNorm as the BASELINE.json configs state it: x += r, out = norm(x)
+    (r = attention output buffer)."""
     s = L.shape
     dev.addRmsNormRows(L.dtype, L.x, L.ao, L.w["pre_ffn"], L.xb, L.T, s.H, s.eps, s.uo)
 
