@@ -43,6 +43,7 @@ constexpr int kGemvProMaxCols = 16384;  // input vector in LDS: <= 64 KB
 #endif
 constexpr unsigned kGemvProGrid = ZL_GEMV_PRO_GRID;
 constexpr int kGemvWaveRowsMin = 65536;  // rows from which batch-1 products use k_gemv_w
+constexpr int kGemvWaveColsMax = 16384;  // its x in LDS: at most 64 KB
 // Tuning builds: a non-zero ZL_GEMV_FORCE sends every batch-1 product without prologue to
 // k_gemv with that many rows per workgroup (> 0) or, for block types, to k_gemv_w with -F
 // rows per wave (< 0); GeGLU products take half. 0 (the library) uses the rules below.
@@ -708,7 +709,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvArgs a) {
 // are 320 groups), the row sums reduce within the wave (no LDS, no barrier), and the next
 // group's weights and x are loaded while the current group is multiplied.
 template <int QT, int RW, int MODE>
-__global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(QT == HIP_BRIDGE_Q4_0 && MODE == GV_PLAIN ? 7 : 1))) void k_gemv_w(GemvArgs a) {
+__global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(QT == HIP_BRIDGE_Q4_0 && MODE == GV_PLAIN ? 8 : 1))) void k_gemv_w(GemvArgs a) {
     constexpr int NM = MODE == GV_GEGLU ? 2 : 1;
     const int lane = threadIdx.x & 63;
     // The wave index is uniform across the wave: read from the first lane, it makes the row
@@ -716,7 +717,9 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(QT
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int row0 = (blockIdx.x * kGemvWaves + wv) * RW;
     const int G = a.cols / 8;
-    if (row0 >= a.total_rows || G <= 0) return;  // the whole wave
+    if (G <= 0) return;  // the whole grid
+    // Waves past the last row take part in staging x (below) and then leave.
+    const bool live = row0 < a.total_rows;
     const unsigned char* wrow[RW][NM];
     float* yrow[RW];
 #pragma unroll
@@ -746,19 +749,22 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(QT
     // (in bounds) and drops its products. (A load under a per-lane branch would make the
     // compiler wait for it where the branch ends, i.e. before the step that needs it.)
     const int n = (G + kWave - 1) / kWave;
-    auto fetch = [&](int k, WGroup<QT> (&w)[RW][NM], f32x4& xa, f32x4& xb) {
+    // x is staged once per workgroup in LDS and read there at each step (it is not held in
+    // registers across a step, which keeps the kernel at 8 waves per SIMD for Q4_0).
+    extern __shared__ __attribute__((aligned(16))) float s_xw[];
+    auto fetch = [&](int k, WGroup<QT> (&w)[RW][NM]) {
         const int g = min(lane + kWave * k, G - 1);
         const typename WGroup<QT>::Off o = WGroup<QT>::off((uint32_t)g);
 #pragma unroll
         for (int r = 0; r < RW; ++r)
 #pragma unroll
             for (int m = 0; m < NM; ++m) w[r][m].load(wrow[r][m], o);
-        int ca, cb;
-        group_cols<QT>(g, ca, cb);
-        xa = ldf4(a.x + ca);
-        xb = ldf4(a.x + cb);
     };
-    auto fold = [&](const WGroup<QT> (&w)[RW][NM], const f32x4& xa, const f32x4& xb, int k, bool last) {
+    auto fold = [&](const WGroup<QT> (&w)[RW][NM], int k, bool last) {
+        int ca, cb;
+        group_cols<QT>(min(lane + kWave * k, G - 1), ca, cb);
+        const f32x4 xa = *reinterpret_cast<const f32x4*>(s_xw + ca);
+        const f32x4 xb = *reinterpret_cast<const f32x4*>(s_xw + cb);
         const float sx = ((xa.x + xa.y) + (xa.z + xa.w)) + ((xb.x + xb.y) + (xb.z + xb.w));
         const bool ok = !last || lane + kWave * k < G;
 #pragma unroll
@@ -775,23 +781,26 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(QT
     // the scheduler hoists that arithmetic, and with it the wait for its operands, above
     // the new loads, and every step waits a full memory round trip.
     WGroup<QT> wa[RW][NM], wb[RW][NM];
-    f32x4 axa, axb, bxa, bxb;
-    fetch(0, wa, axa, axb);
+    if (live) fetch(0, wa);  // the first weights are in flight while x is staged
+    for (int i = threadIdx.x; i < a.cols / 4; i += kGemvThreads)
+        *reinterpret_cast<f32x4*>(s_xw + 4 * i) = ldf4(a.x + 4 * i);
+    __syncthreads();
+    if (!live) return;
     for (int k = 0;; k += 2) {
         if (k + 1 >= n) {
-            fold(wa, axa, axb, k, true);
+            fold(wa, k, true);
             break;
         }
-        fetch(k + 1, wb, bxa, bxb);
+        fetch(k + 1, wb);
         __builtin_amdgcn_sched_barrier(0);
-        fold(wa, axa, axb, k, false);
+        fold(wa, k, false);
         if (k + 2 >= n) {
-            fold(wb, bxa, bxb, k + 1, true);
+            fold(wb, k + 1, true);
             break;
         }
-        fetch(k + 2, wa, axa, axb);
+        fetch(k + 2, wa);
         __builtin_amdgcn_sched_barrier(0);
-        fold(wb, bxa, bxb, k + 1, false);
+        fold(wb, k + 1, false);
     }
 #pragma unroll
     for (int r = 0; r < RW; ++r) {
@@ -928,12 +937,12 @@ static void launch_vec(const GemvArgs& a, hipStream_t s) {
         constexpr bool blockq = QT != HIP_BRIDGE_F16 && QT != HIP_BRIDGE_BF16 && QT != HIP_BRIDGE_F32;
         if constexpr (F < 0 && blockq) {
             constexpr int RW = std::max(1, -F / H);
-            k_gemv_w<QT, RW, MODE><<<(unsigned)cdiv(a.total_rows, (int64_t)RW * kGemvWaves), kGemvThreads, 0, s>>>(a);
+            k_gemv_w<QT, RW, MODE><<<(unsigned)cdiv(a.total_rows, (int64_t)RW * kGemvWaves), kGemvThreads, (size_t)a.cols * 4, s>>>(a);
         } else {
             constexpr int RP = F > 0 ? std::max(1, F / H) : 2 / H;
             k_gemv<QT, RP, 1, MODE><<<(unsigned)cdiv(a.total_rows, RP), kGemvThreads, 0, s>>>(a);
         }
-    } else if (MODE == GV_PLAIN && a.batch == 1 && a.total_rows >= kGemvWaveRowsMin &&
+    } else if (MODE == GV_PLAIN && a.batch == 1 && a.total_rows >= kGemvWaveRowsMin && a.cols <= kGemvWaveColsMax &&
                QT != HIP_BRIDGE_F16 && QT != HIP_BRIDGE_BF16 && QT != HIP_BRIDGE_F32) {
         // (k_gemv_w is instantiated for these cases only)
         if constexpr (MODE == GV_PLAIN && QT != HIP_BRIDGE_F16 && QT != HIP_BRIDGE_BF16 && QT != HIP_BRIDGE_F32) {
@@ -942,7 +951,7 @@ static void launch_vec(const GemvArgs& a, hipStream_t s) {
         // and Q4_0 137 -> 113 with 8; smaller matrices, whose rows are long against their
         // count, and dense types are faster above: 2560 x 10240 Q4_0 8.0 us above, 14.6 here)
         constexpr int RW = QT == HIP_BRIDGE_Q4_K ? 2 : QT == HIP_BRIDGE_Q6_K ? 4 : 8;
-        k_gemv_w<QT, RW, MODE><<<(unsigned)cdiv(a.total_rows, (int64_t)RW * kGemvWaves), kGemvThreads, 0, s>>>(a);
+        k_gemv_w<QT, RW, MODE><<<(unsigned)cdiv(a.total_rows, (int64_t)RW * kGemvWaves), kGemvThreads, (size_t)a.cols * 4, s>>>(a);
         }
     } else if (a.batch == 1) {
         if (QT == HIP_BRIDGE_Q4_0 && (a.total_rows >= 16384 || (MODE == GV_GEGLU && a.total_rows >= 4096)))
