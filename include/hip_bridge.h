@@ -342,6 +342,9 @@ void hip_argmax(const float* logits, int n, unsigned int* out_idx, HipStream_t s
 /* ---------------------------------------------------------------------------------- */
 /* out = gelu_tanh(gate) * up; out may alias gate or up. */
 void hip_geglu(const float* gate, const float* up, float* out, int n, HipStream_t stream); /* cuda_bridge.h:64 */
+/* out = silu(gate) * up, silu(x) = x / (1 + exp(-x)) (math.zig:1108-1117); out may alias gate
+ * or up. */
+void hip_swiglu(const float* gate, const float* up, float* out, int n, HipStream_t stream); /* cuda_bridge.h:65 */
 void hip_add(float* x, const float* residual, int n, HipStream_t stream);              /* cuda_bridge.h:66 */
 void hip_scale(float* x, float scale, int n, HipStream_t stream);                      /* cuda_bridge.h:67 */
 /* x = cap * tanh(x / cap), in place. */
@@ -352,6 +355,19 @@ void hip_geglu_ex(int dtype, const void* gate, const void* up, void* out, int64_
 void hip_tanh_softcap_ex(int dtype, void* x, float cap, int64_t n, HipStream_t stream);
 /* new: out[i] = x[i] * scale (x == out allowed; scale 1 copies exactly). */
 void hip_scale_ex(int dtype, const void* x, float scale, void* out, int64_t n, HipStream_t stream);
+void hip_swiglu_ex(int dtype, const void* gate, const void* up, void* out, int64_t n,
+                   HipStream_t stream);
+
+/* ---------------------------------------------------------------------------------- */
+/* Per-layer embedding (Gemma-4 PLE) steps (replaces cuda_bridge.h:171-172)             */
+/* ---------------------------------------------------------------------------------- */
+/* ple_buf_out[i] = gelu_tanh(ple_gate_in[i]) * ple_slice[i] (model.zig:762-768). */
+void hip_ple_gate_gelu(const float* ple_gate_in, const float* ple_slice, float* ple_buf_out,
+                       int ple_dim, HipStream_t stream);                     /* cuda_bridge.h:171 */
+/* add_token_embd != 0: ctx_ple_buf[i] = (ctx_ple_buf[i] + ctx_scratch[i]) * f32(1/sqrt(2));
+ * else ctx_ple_buf[i] = ctx_scratch[i] (model.zig:525-535; n = n_layers * 256 per token). */
+void hip_ple_ctx_fuse(float* ctx_ple_buf, const float* ctx_scratch, int n, int add_token_embd,
+                      HipStream_t stream);                                   /* cuda_bridge.h:172 */
 
 #ifdef __cplusplus
 }

@@ -218,6 +218,16 @@ public:
     void geglu(const float* d_gate, const float* d_up, float* d_out, size_t n) const {
         hip_geglu(d_gate, d_up, d_out, (int)n, stream);
     }
+    void swiglu(const float* d_gate, const float* d_up, float* d_out, size_t n) const {
+        hip_swiglu(d_gate, d_up, d_out, (int)n, stream);
+    }
+    // cuda.zig:696-714
+    void pleGateGelu(const float* d_ple_gate, const float* d_ple_slice, float* d_ple_buf, size_t ple_dim) const {
+        hip_ple_gate_gelu(d_ple_gate, d_ple_slice, d_ple_buf, (int)ple_dim, stream);
+    }
+    void pleCtxFuse(float* d_ctx_ple_buf, const float* d_ctx_scratch, size_t n, bool add_token_embd) const {
+        hip_ple_ctx_fuse(d_ctx_ple_buf, d_ctx_scratch, (int)n, add_token_embd ? 1 : 0, stream);
+    }
     void add(float* d_x, const float* d_res, size_t n) const { hip_add(d_x, d_res, (int)n, stream); }
     void scale(float* d_x, float s, size_t n) const { hip_scale(d_x, s, (int)n, stream); }
     void tanhSoftcap(float* d_x, float cap, size_t n) const { hip_tanh_softcap(d_x, cap, (int)n, stream); }

@@ -145,18 +145,11 @@ class RefModel:
         if self.gemma:
             x = (x * np.float32(np.sqrt(np.float32(dim)))).astype(np.float32)
         ple = None
-        if self.ple is not None:
+        if self.ple is not None:  # model.zig:506-540 (token path)
             n = L * PLE_DIM
-            ple = o.dequantize_row(self.ple["type"], self.ple["raw"].reshape(self.V, -1)[token], n)
-            ple = (ple * np.float32(np.sqrt(np.float32(PLE_DIM)))).astype(np.float32)
-            if self.ple_proj is not None:
-                xb = (x * (np.float32(1.0) / np.sqrt(np.float32(dim)))).astype(np.float32)
-                ctx = self.gemv(self.mat(self.ple_proj, n), xb)
-                if self.ple_norm is not None:
-                    inv2 = np.float32(1.0) / np.sqrt(np.float32(2.0))
-                    for l in range(L):
-                        s = self.rms(ctx[l * PLE_DIM:(l + 1) * PLE_DIM], self.ple_norm, False)
-                        ple[l * PLE_DIM:(l + 1) * PLE_DIM] = (ple[l * PLE_DIM:(l + 1) * PLE_DIM] + s) * inv2
+            row = o.dequantize_row(self.ple["type"], self.ple["raw"].reshape(self.V, -1)[token], n)
+            pq, pw = self.mat(self.ple_proj, n) if self.ple_proj is not None else (None, None)
+            ple = o.ple_token_inputs(row, x, pq, pw, self.ple_norm, L, self.eps, ple_dim=PLE_DIM)
         for i, ly in enumerate(self.layers):
             hd, nh, nkv = ly["head_dim"], ly["n_heads"], ly["n_kv"]
             xb = self.rms(x, ly["in"]) if ly["in"] is not None else x.copy()
@@ -186,14 +179,9 @@ class RefModel:
             if ly["post_ffn"] is not None:
                 fo = self.rms(fo, ly["post_ffn"])
             x = (x + fo).astype(np.float32)
-            if ple is not None and ly["ple_gate"] is not None and ly["ple_proj"] is not None:
-                gate = self.gemv(ly["ple_gate"], x)
-                gl = np.array([o.gelu(float(g)) for g in gate], np.float32)
-                pb = (ple[i * PLE_DIM:(i + 1) * PLE_DIM] * gl).astype(np.float32)
-                d = self.gemv(ly["ple_proj"], pb)
-                if ly["post_ple"] is not None:
-                    d = self.rms(d, ly["post_ple"], False)
-                x = (x + d).astype(np.float32)
+            if ple is not None and ly["ple_gate"] is not None and ly["ple_proj"] is not None:  # 757-781
+                x = o.ple_inject(x, ple[i * PLE_DIM:(i + 1) * PLE_DIM], *ly["ple_gate"], *ly["ple_proj"],
+                                 ly["post_ple"], self.eps)
             if ly["scalar"] != 1.0:
                 x = (x * np.float32(ly["scalar"])).astype(np.float32)
         xb = self.rms(x, self.output_norm)

@@ -48,6 +48,11 @@ _SIGS = {
     "zo_gelu": (ctypes.c_float, [_f]),
     "zo_geglu": (None, [_fp, _fp, _fp, _sz]),
     "zo_softcap": (None, [_fp, _f, _sz]),
+    "zo_silu": (ctypes.c_float, [_f]),
+    "zo_swiglu": (None, [_fp, _fp, _fp, _sz]),
+    "zo_swiglu_bf16": (None, [_u16p, _u16p, _u16p, _sz]),
+    "zo_ple_gate_gelu": (None, [_fp, _fp, _fp, _sz]),
+    "zo_ple_ctx_fuse": (None, [_fp, _fp, _sz, _i]),
     "zo_add_rms_norm_bf16": (None, [_u16p, _u16p, _fp, _u16p, _sz, _sz, _f, _i]),
     "zo_rms_norm_bf16": (None, [_u16p, _fp, _u16p, _sz, _sz, _f, _i]),
     "zo_rms_norm_add_rms_norm_bf16": (None, [_u16p, _u16p, _fp, _fp, _sz, _sz, _f, _i]),
@@ -322,6 +327,73 @@ class Oracle:
         out = np.empty_like(g)
         self.lib.zo_geglu(self.fp(g), self.fp(u), self.fp(out), g.size)
         return out
+
+    def silu(self, x):
+        return self.lib.zo_silu(x)
+
+    def swiglu(self, gate, up):
+        """math.swiglu: silu(gate) * up; f32, or bf16 (uint16) rounded once."""
+        if gate.dtype == np.uint16:
+            g = np.ascontiguousarray(gate)
+            u = np.ascontiguousarray(up, dtype=np.uint16)
+            out = np.empty_like(g)
+            self.lib.zo_swiglu_bf16(self.u16(g), self.u16(u), self.u16(out), g.size)
+            return out
+        g = np.ascontiguousarray(gate, dtype=np.float32)
+        u = np.ascontiguousarray(up, dtype=np.float32)
+        out = np.empty_like(g)
+        self.lib.zo_swiglu(self.fp(g), self.fp(u), self.fp(out), g.size)
+        return out
+
+    def ple_gate_gelu(self, gate, ple_slice):
+        """model.zig:762-768: ple_slice * gelu(gate)."""
+        g = np.ascontiguousarray(gate, dtype=np.float32)
+        s_ = np.ascontiguousarray(ple_slice, dtype=np.float32)
+        out = np.empty_like(g)
+        self.lib.zo_ple_gate_gelu(self.fp(g), self.fp(s_), self.fp(out), g.size)
+        return out
+
+    def ple_ctx_fuse(self, ctx, scratch, add_token_embd=True):
+        """model.zig:525-535: (ctx + scratch) * f32(1/sqrt 2), or scratch (returns a copy)."""
+        c = np.array(ctx, dtype=np.float32, copy=True, order="C")
+        s_ = np.ascontiguousarray(scratch, dtype=np.float32)
+        self.lib.zo_ple_ctx_fuse(self.fp(c), self.fp(s_), c.size, int(bool(add_token_embd)))
+        return c
+
+    def ple_token_inputs(self, ple_row_f32, x, proj_qtype, proj_w, proj_norm, n_layers, eps,
+                         token_path=True, ple_dim=256):
+        """model.zig:506-540 after the row gather: ple = row * sqrt(256) (token path, else 0);
+        ctx = proj(x / sqrt(dim)); per layer l: ctx_l = rmsNorm(ctx_l; proj_norm) (no unit
+        offset) and ple_l = (ple_l + ctx_l) * f32(1/sqrt 2) (token path) or ctx_l.
+        ple_row_f32: the dequantized PLE row (n_layers * ple_dim), or None when not token_path."""
+        n = n_layers * ple_dim
+        if token_path:
+            ple = (np.asarray(ple_row_f32, np.float32) * np.float32(np.sqrt(np.float32(ple_dim)))).astype(np.float32)
+        else:
+            ple = np.zeros(n, np.float32)
+        if proj_w is None:
+            return ple
+        x = np.asarray(x, np.float32)
+        inv = np.float32(1.0) / np.sqrt(np.float32(x.size))
+        xb = (x * inv).astype(np.float32)
+        ctx = self.gemv(proj_qtype, proj_w, xb)
+        if proj_norm is None:
+            return ple
+        for l in range(n_layers):
+            sl = slice(l * ple_dim, (l + 1) * ple_dim)
+            ctx[sl] = self.rms_norm(ctx[sl], proj_norm, eps, unit_offset=False)
+            ple[sl] = self.ple_ctx_fuse(ple[sl], ctx[sl], token_path)
+        return ple
+
+    def ple_inject(self, x, ple_slice, gate_qtype, gate_w, proj_qtype, proj_w, post_norm, eps):
+        """model.zig:757-781 for one layer: gate = gelu(W_gate x); ple = slice * gate;
+        d = W_proj ple; d = rmsNorm(d; post_norm) (no unit offset) when present; returns x + d."""
+        gate = self.gemv(gate_qtype, gate_w, x)
+        pb = self.ple_gate_gelu(gate, ple_slice)
+        d = self.gemv(proj_qtype, proj_w, pb)
+        if post_norm is not None:
+            d = self.rms_norm(d, post_norm, eps, unit_offset=False)
+        return (np.asarray(x, np.float32) + d).astype(np.float32)
 
     def softcap(self, x, cap):
         x = np.array(x, dtype=np.float32, copy=True, order="C")

@@ -573,6 +573,33 @@ void zo_softcap(float* x, float cap, size_t n) {
     for (size_t i = 0; i < n; ++i) x[i] = cap * zo_tanhf(x[i] / cap);
 }
 
+/* math.zig:1108-1110: silu(x) = x / (1.0 + @exp(-x)). ziglm links libc (build.zig:76, 92),
+ * so Zig's @exp on f32 is the C library's expf: glibc's here, the same function ziglm's
+ * Linux build calls (its result is correctly rounded except in rare cases; pinned against
+ * the f64 exponential in tests/test_oracle_cpu.py). */
+float zo_silu(float x) {
+    return x / (1.0f + expf(-x));
+}
+
+/* math.zig:1112-1117: out[i] = silu(gate[i]) * up[i] (out may alias gate). */
+void zo_swiglu(const float* gate, const float* up, float* out, size_t n) {
+    for (size_t i = 0; i < n; ++i) out[i] = zo_silu(gate[i]) * up[i];
+}
+
+/* Per-layer embedding (PLE) injection, model.zig:762-768: gate = gelu(W_gate x) in place,
+ * then ple_buf[d] = ple_slice[d] * gate[d]. */
+void zo_ple_gate_gelu(const float* gate, const float* slice, float* out, size_t n) {
+    for (size_t i = 0; i < n; ++i) out[i] = slice[i] * zo_gelu(gate[i]);
+}
+
+/* PLE context fuse, model.zig:525-535 with the reference ABI's flag (cuda_bridge.cu:2908-2923):
+ * add_token_embd: ctx[d] = (ctx[d] + s[d]) * inv_sqrt_2, inv_sqrt_2 = f32(1/sqrt(2)) (the
+ * comptime `1.0 / @sqrt(2.0)` of model.zig:528 coerced to f32); else ctx[d] = s[d]. */
+void zo_ple_ctx_fuse(float* ctx, const float* s, size_t n, int add_token_embd) {
+    const float inv_sqrt_2 = 0.70710677f; /* 0x3F3504F3 */
+    for (size_t i = 0; i < n; ++i) ctx[i] = add_token_embd ? (ctx[i] + s[i]) * inv_sqrt_2 : s[i];
+}
+
 /* ------------------------------------------------------------------------------------ */
 /* bf16 activation variants: upconvert (quant.zig:30-33), f32 op, round (quant.zig:35-40)  */
 /* ------------------------------------------------------------------------------------ */
@@ -637,4 +664,10 @@ void zo_rms_norm_add_bf16(uint16_t* x, const uint16_t* in, const float* w, size_
 void zo_geglu_bf16(const uint16_t* gate, const uint16_t* up, uint16_t* out, size_t n) {
     for (size_t i = 0; i < n; ++i)
         out[i] = zo_f32_to_bf16(zo_gelu(zo_bf16_to_f32(gate[i])) * zo_bf16_to_f32(up[i]));
+}
+
+/* SwiGLU on bf16 activations: upconvert, math.zig:1112-1117 in f32, round once. */
+void zo_swiglu_bf16(const uint16_t* gate, const uint16_t* up, uint16_t* out, size_t n) {
+    for (size_t i = 0; i < n; ++i)
+        out[i] = zo_f32_to_bf16(zo_silu(zo_bf16_to_f32(gate[i])) * zo_bf16_to_f32(up[i]));
 }

@@ -75,6 +75,10 @@ float zo_tanhf(float x);
 float zo_gelu(float x);
 void zo_geglu(const float* gate, const float* up, float* out, size_t n);
 void zo_softcap(float* x, float cap, size_t n);
+float zo_silu(float x);
+void zo_swiglu(const float* gate, const float* up, float* out, size_t n);
+void zo_ple_gate_gelu(const float* gate, const float* slice, float* out, size_t n);
+void zo_ple_ctx_fuse(float* ctx, const float* s, size_t n, int add_token_embd);
 
 /* ---- bf16 activation variants: upconvert, run the f32 op, round once (quant.zig:30-40) ---- */
 void zo_add_rms_norm_bf16(uint16_t* x, const uint16_t* r, const float* w, uint16_t* out,
@@ -88,6 +92,7 @@ void zo_rms_norm_add_rms_norm(float* x, float* xb, const float* w1, const float*
 void zo_rms_norm_add_bf16(uint16_t* x, const uint16_t* in, const float* w, size_t rows, size_t n,
                           float eps, int unit_offset);
 void zo_geglu_bf16(const uint16_t* gate, const uint16_t* up, uint16_t* out, size_t n);
+void zo_swiglu_bf16(const uint16_t* gate, const uint16_t* up, uint16_t* out, size_t n);
 
 /* Token-batched fused QK-norm + RoPE + KV append, f32 or bf16 (dtype: 0 f32, 1 bf16).
  * q: [T][nh][d] updated in place; k, v: [T][nkv][d] read only; the rotated K and the

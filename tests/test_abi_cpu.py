@@ -1,7 +1,10 @@
 """CPU-side checks of the C-ABI boundary (no GPU needed, no compute calls):
-every function declared in include/*.h is exported by libhip_bridge.so, the ctypes bindings
-(ziglm_amd/bridge.py for hip_bridge.h, ziglm_amd/gguf.py for zl_gguf.h) cover exactly those
-functions, and the library loads without initialising a device."""
+every function declared in include/*.h is exported by libhip_bridge.so, every entry point of
+the reference ABI (cuda_bridge.h and cuda.zig's extern block) has its hip_ counterpart, the
+ctypes bindings (ziglm_amd/bridge.py for hip_bridge.h, ziglm_amd/gguf.py for zl_gguf.h) cover
+exactly those functions, the Zig binding (ziglm_amd/zig/hip.zig) declares every hip_bridge.h
+function with the header's argument count, and the library loads without initialising a
+device."""
 import os
 import re
 import subprocess
@@ -12,6 +15,26 @@ from ziglm_amd import bridge, gguf
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADERS = {"hip_bridge.h": "hip_", "zl_gguf.h": "zl_"}
+HIP_ZIG = os.path.join(ROOT, "ziglm_amd", "zig", "hip.zig")
+
+# The reference's C-ABI: every cuda_* function of src/cuda_bridge.h (lines 15-175) plus the
+# two that only cuda.zig's extern block declares (cuda_rmsnorm_add cuda.zig:49,
+# cuda_gemv_f32 cuda.zig:39). A drop-in library exports each under the hip_ prefix.
+REFERENCE_ABI = """
+cuda_device_get_info cuda_malloc cuda_free cuda_malloc_host cuda_free_host cuda_memcpy_h2d
+cuda_memcpy_d2h cuda_memcpy_d2d cuda_stream_create cuda_stream_destroy cuda_stream_sync
+cuda_graph_begin_capture cuda_graph_end_capture cuda_graph_instantiate cuda_graph_launch
+cuda_graph_destroy cuda_graph_exec_destroy
+cuda_gemv_q4_0 cuda_gemv_q8_0 cuda_gemv_q4_k cuda_gemv_q6_k cuda_gemv_f16 cuda_gemv_bf16 cuda_gemv
+cuda_gemv_geglu_q4_0 cuda_gemv_qkv_q4_0 cuda_gemm_q4_0 cuda_gemm_q8_0 cuda_gemm_f16 cuda_gemm
+cuda_embed_lookup cuda_embed_lookup_batch cuda_rmsnorm cuda_rmsnorm_batched cuda_add_rmsnorm
+cuda_add_rmsnorm_batched cuda_rope cuda_rope_ind cuda_rope_batched cuda_geglu cuda_swiglu cuda_add
+cuda_scale cuda_tanh_softcap cuda_kv_cache_put cuda_kv_cache_put_ind cuda_kv_cache_put_batched
+cuda_attention_forward cuda_attention_forward_ind cuda_attention_batched cuda_ple_gate_gelu
+cuda_ple_ctx_fuse cuda_argmax
+cuda_rmsnorm_add cuda_gemv_f32
+""".split()
+REF_SRC = "/root/reference/src"
 
 
 def declared_functions(header=None):
@@ -52,3 +75,63 @@ def test_library_loads_and_binds():
     assert "gfx950" in b.version()
     assert b.hip_bridge_last_error() == 0
     assert b.hip_bridge_error_string(-2).decode().startswith("unsupported")
+
+
+def _ref_names(path, pattern):
+    text = re.sub(r"/\*.*?\*/|//[^\n]*", "", open(path).read(), flags=re.S)
+    return set(re.findall(pattern, text))
+
+
+def test_reference_abi_list_matches_reference_sources():
+    """The committed name list against the reference's own files, where they exist (this
+    container only; the list above is what the other tests use)."""
+    h, z = os.path.join(REF_SRC, "cuda_bridge.h"), os.path.join(REF_SRC, "cuda.zig")
+    if not (os.path.exists(h) and os.path.exists(z)):
+        pytest.skip("reference sources not present")
+    names = _ref_names(h, r"\b(cuda_\w+)\s*\(") | _ref_names(z, r"extern \"c\" fn (cuda_\w+)")
+    assert names == set(REFERENCE_ABI)
+
+
+def test_every_reference_entry_point_has_a_hip_export():
+    declared = set(declared_functions("hip_bridge.h"))
+    missing = [n for n in REFERENCE_ABI if "hip_" + n[len("cuda_"):] not in declared]
+    assert not missing, f"reference entry points without a hip_ counterpart: {missing}"
+
+
+def _c_arg_counts():
+    text = open(os.path.join(ROOT, "include", "hip_bridge.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for m in re.finditer(r"\b(hip_\w+)\s*\(([^;{]*?)\)\s*;", text, flags=re.S):
+        args = m.group(2).strip()
+        out[m.group(1)] = 0 if args in ("", "void") else args.count(",") + 1
+    return out
+
+
+def test_zig_binding_declares_every_function():
+    """hip.zig's extern block: every hip_bridge.h function, with the same argument count."""
+    text = open(HIP_ZIG).read()
+    zig = {}
+    for m in re.finditer(r"pub extern \"c\" fn (hip_\w+)\((.*?)\)\s*[^;(]+;", text):
+        args = m.group(2).strip()
+        zig[m.group(1)] = 0 if not args else len([a for a in args.split(",") if a.strip()])
+    c = _c_arg_counts()
+    assert set(zig) == set(c), (sorted(set(c) - set(zig)), sorted(set(zig) - set(c)))
+    bad = {n: (zig[n], c[n]) for n in c if zig[n] != c[n]}
+    assert not bad, bad
+
+
+def test_zig_binding_has_every_cuda_device_method():
+    """HipDevice / HipBuffer offer every CudaDevice / CudaBuffer method the reference's callers
+    use (cuda.zig:187-751), and the aliases under the reference's names."""
+    text = open(HIP_ZIG).read()
+    methods = set(re.findall(r"pub (?:inline )?fn (\w+)\(", text))
+    need = """upload copyFrom download asF32 asConstF32 deinit init getName alloc sync gemv gemvGegluQ4_0
+    gemvQkvQ4_0 gemmQ4_0 gemm embedLookup embedLookupBatch rmsNorm rmsNormBatched rmsnormAdd addRmsNorm
+    addRmsNormBatched rope ropeInd ropeBatched kvCachePut kvCachePutInd kvCachePutBatched attentionForward
+    attentionForwardInd attentionBatched geglu pleGateGelu pleCtxFuse add scale tanhSoftcap argmax""".split()
+    assert not [m for m in need if m not in methods]
+    for alias in ("CudaDevice", "CudaBuffer", "CudaStream_t", "CudaGraph_t", "CudaGraphExec_t"):
+        assert re.search(r"pub const " + alias + r"\b", text), alias
+    for n in REFERENCE_ABI:
+        assert re.search(r"pub const " + n + r" = hip_", text), n

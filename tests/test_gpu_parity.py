@@ -507,6 +507,66 @@ def test_softcap_bf16(dev, oracle):
     assert_bf16(d_x.to_numpy((n,), np.uint16), ref, 1, what="softcap bf16")
 
 
+# SwiGLU: relative 1e-5; where exp(-gate) overflows in f32 (gate < -88.7) or the quotient
+# is subnormal, the CPU gives x / inf = -0 or a value below 2e-37, so the floor is
+# |up| * 1e-36.
+SILU_EXTREMES = np.array([-87.0, -88.5, -88.75, -89.0, -100.0, -1e4, 87.0, 88.8, 1e4, -1e-40, 1e-40,
+                          np.float32(1e-37), -16.6, 16.6], np.float32)
+
+
+@pytest.mark.parametrize("n", [10240, 10240 + 3, 7])
+def test_swiglu_f32(dev, oracle, n):
+    g = synth.normal_f32(6, "gate", (n,), 0, 4)
+    u = synth.normal_f32(6, "up", (n,))
+    ext = np.concatenate([EXTREMES, SILU_EXTREMES])
+    m = min(n, ext.size)
+    g[:m] = ext[:m]
+    ref = oracle.swiglu(g, u)
+    floor = np.abs(u.astype(np.float64)) * 1e-36
+    d_g, d_u, d_o = dev.from_numpy(g), dev.from_numpy(u), dev.alloc(g.nbytes)
+    dev.swiglu(d_g, d_u, d_o, n)
+    assert_rel(d_o.to_numpy((n,), np.float32), ref, 1e-5, floor=floor, what="swiglu f32")
+    dev.swiglu(d_g, d_u, d_u, n)  # out aliases up
+    assert_rel(d_u.to_numpy((n,), np.float32), ref, 1e-5, floor=floor, what="swiglu in place")
+
+
+@pytest.mark.parametrize("n", [64 * 10240, 4096 + 5])
+def test_swiglu_bf16(dev, oracle, n):
+    g = synth.normal_bf16(6, "gate", (n,), 0, 4)
+    u = synth.normal_bf16(6, "up", (n,))
+    g[:EXTREMES.size] = synth.f32_to_bf16(EXTREMES)
+    ref = oracle.swiglu(g, u)
+    d_o = dev.alloc(g.nbytes)
+    dev.swigluEx(B.BF16, dev.from_numpy(g), dev.from_numpy(u), d_o, n)
+    floor = np.abs(O.get().bf16_to_f32(u).astype(np.float64)) * 1e-36
+    assert_bf16(d_o.to_numpy((n,), np.uint16), ref, 1, floor=floor, what="swiglu bf16")
+
+
+@pytest.mark.parametrize("n", [256, 35 * 256, 35 * 256 * 8 + 3])
+def test_ple_gate_gelu(dev, oracle, n):
+    """cuda_ple_gate_gelu (cuda_bridge.h:171) against model.zig:762-768."""
+    g = synth.normal_f32(7, "pg", (n,), 0, 2)
+    sl = synth.normal_f32(7, "ps", (n,))
+    g[:EXTREMES.size] = EXTREMES
+    ref = oracle.ple_gate_gelu(g, sl)
+    d_o = dev.alloc(g.nbytes)
+    dev.pleGateGelu(dev.from_numpy(g), dev.from_numpy(sl), d_o, n)
+    assert_rel(d_o.to_numpy((n,), np.float32), ref, 1e-5, floor=geglu_floor(g, sl), what="ple gate gelu")
+
+
+@pytest.mark.parametrize("add", [True, False])
+@pytest.mark.parametrize("n", [35 * 256, 8 * 35 * 256 + 5, 3])
+def test_ple_ctx_fuse_bitexact(dev, oracle, n, add):
+    """cuda_ple_ctx_fuse (cuda_bridge.h:172) against model.zig:525-535: one rounding of the
+    sum, one of the product by f32(1/sqrt 2), so bit-exact."""
+    ctx = synth.normal_f32(8, "ctx", (n,), 0, 16)
+    s = synth.normal_f32(8, "scr", (n,))
+    ref = oracle.ple_ctx_fuse(ctx, s, add)
+    d_c = dev.from_numpy(ctx)
+    dev.pleCtxFuse(d_c, dev.from_numpy(s), n, add)
+    assert_bitexact(d_c.to_numpy((n,), np.float32), ref, f"ple ctx fuse add={add}")
+
+
 def test_add_scale_mirrors(dev):
     n = 2560 + 1
     x = synth.normal_f32(5, "x", (n,))

@@ -453,6 +453,102 @@ def test_softcap_vs_f64(o):
         assert np.all(np.abs(got) <= cap)
 
 
+def test_silu_vs_f64_and_identities(o):
+    # math.zig:1108-1110 with glibc's expf (the function ziglm's libc-linked build calls)
+    x = np.concatenate([sweep()[::3], np.linspace(-104, -80, 2001), np.linspace(80, 100, 201)]).astype(np.float32)
+    got = np.array([o.silu(float(v)) for v in x], np.float64)
+    xd = x.astype(np.float64)
+    with np.errstate(over="ignore"):
+        ref = xd / (1.0 + np.exp(-xd))
+    # expf (<= 0.502 ulp) + 1 + e + the division: a few ulp relative; exp(-x) overflowing in f32
+    # (x < -88.72) gives x / inf = -0 where f64 still has a value below 2e-37
+    fin = xd > -88.7
+    assert np.all(np.abs(got[fin] - ref[fin]) <= 3.0 * ulp32(ref[fin]) + 1e-45)
+    assert np.all(np.abs(got[~fin]) <= 1e-36)
+    # silu(x) - silu(-x) = x (sigma(x) + sigma(-x) = 1), silu(0) = 0, silu(x) -> x for x >> 0
+    m = np.abs(xd) < 80
+    neg = np.array([o.silu(float(-v)) for v in x[m]], np.float64)
+    assert np.all(np.abs((got[m] - neg) - xd[m]) <= 4.0 * ulp32(xd[m]) + 1e-45)
+    assert o.silu(0.0) == 0.0 and o.silu(30.0) == 30.0 and np.signbit(o.silu(-120.0))
+
+
+def test_swiglu_elementwise_and_bf16(o):
+    g = np.concatenate([synth.normal_f32(0, "gate", (10240,)), sweep()[::97]]).astype(np.float32)
+    u = synth.normal_f32(0, "up", (g.size,))
+    out = o.swiglu(g, u)
+    ref = np.array([o.silu(float(a)) for a in g], np.float32) * u
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+    gd, ud = g.astype(np.float64), u.astype(np.float64)
+    with np.errstate(over="ignore"):
+        r64 = gd / (1.0 + np.exp(-gd)) * ud
+    assert np.all(np.abs(out - r64) <= 4.0 * ulp32(r64) + 1e-36)
+    gb, ub = o.f32_to_bf16(g), o.f32_to_bf16(u)
+    outb = o.swiglu(gb, ub)
+    assert np.array_equal(outb, o.f32_to_bf16(o.swiglu(o.bf16_to_f32(gb), o.bf16_to_f32(ub))))
+
+
+def test_ple_gate_gelu_and_ctx_fuse(o):
+    gate = np.concatenate([synth.normal_f32(1, "pg", (256,)), sweep()[::1000]]).astype(np.float32)
+    sl = synth.normal_f32(1, "ps", (gate.size,))
+    got = o.ple_gate_gelu(gate, sl)
+    gl = np.array([o.gelu(float(v)) for v in gate], np.float32)
+    assert np.array_equal(got.view(np.uint32), (sl * gl).view(np.uint32))  # model.zig:765-768
+    assert np.array_equal(o.ple_gate_gelu(gate, np.ones_like(gate)), gl)
+    # the constant is f32(1/sqrt 2): (0 + 1) * c == c exactly
+    c = o.ple_ctx_fuse(np.zeros(4, np.float32), np.ones(4, np.float32))
+    assert np.all(c.view(np.uint32) == np.float32(1.0 / np.sqrt(2.0)).view(np.uint32)) and c[0] == np.float32(0.70710677)
+    a, b = synth.normal_f32(1, "ca", (4096,)), synth.normal_f32(1, "cb", (4096,))
+    f = o.ple_ctx_fuse(a, b).astype(np.float64)
+    r = (a.astype(np.float64) + b) / np.sqrt(2.0)
+    assert np.all(np.abs(f - r) <= 1.5 * ulp32(r) + 1e-45)  # one rounding of the sum, one of the product
+    assert np.array_equal(o.ple_ctx_fuse(a, b, add_token_embd=False), b)
+
+
+def _f64_ple_inputs(row, x, w, norm, L, eps):
+    ple = row.astype(np.float64) * 16.0
+    ctx = w @ (x.astype(np.float64) / np.sqrt(x.size))
+    for l in range(L):
+        s = ctx[l * 256:(l + 1) * 256]
+        s = s / np.sqrt(np.mean(s * s) + eps) * norm
+        ple[l * 256:(l + 1) * 256] = (ple[l * 256:(l + 1) * 256] + s) / np.sqrt(2.0)
+    return ple
+
+
+def test_ple_token_inputs_and_inject_vs_f64(o):
+    """model.zig:506-540 and 757-781 against a float64 restatement from the definitions;
+    planted mistakes (no sqrt(256) token scale, no 1/sqrt 2, unit-offset norm, a gelu on the
+    slice instead of the gate) move the result far outside the bound."""
+    L, dim, eps = 4, 192, 1e-6
+    row = synth.normal_f32(2, "row", (L * 256,), 0, 0.02)
+    x = synth.normal_f32(2, "x", (dim,), 0, 1)
+    w = synth.normal_f32(2, "w", (L * 256, dim), 0, 0.05)
+    norm = synth.normal_f32(2, "n", (256,), 1, 0.1)
+    got = o.ple_token_inputs(row, x, O.F32, w, norm, L, np.float32(eps))
+    ref = _f64_ple_inputs(row, x, w.astype(np.float64), norm, L, eps)
+    tol = 1e-5 * (np.abs(ref) + 1.0)
+    assert np.all(np.abs(got - ref) <= tol)
+    assert np.max(np.abs(_f64_ple_inputs(row / 16.0, x, w.astype(np.float64), norm, L, eps) - ref)) > 100 * tol.max()
+    bad = o.ple_token_inputs(row, x, O.F32, w, norm + 1.0, L, np.float32(eps))
+    assert np.max(np.abs(bad - ref)) > 100 * tol.max()
+    # inject
+    gw = synth.normal_f32(2, "gw", (256, dim), 0, 0.1)
+    pw = synth.normal_f32(2, "pw", (dim, 256), 0, 0.1)
+    post = synth.normal_f32(2, "post", (dim,), 1, 0.1)
+    sl = got[256:512]
+    xi = o.ple_inject(x, sl, O.F32, gw, O.F32, pw, post, np.float32(eps))
+    g64 = gw.astype(np.float64) @ x
+    gelu = 0.5 * g64 * (1 + np.tanh(0.7978845608 * (g64 + 0.044715 * g64 ** 3)))
+    d = pw.astype(np.float64) @ (sl.astype(np.float64) * gelu)
+    d = d / np.sqrt(np.mean(d * d) + eps) * post
+    r = x.astype(np.float64) + d
+    tol = 2e-5 * (np.abs(r) + 1.0)
+    assert np.all(np.abs(xi - r) <= tol)
+    s64 = sl.astype(np.float64)
+    d2 = pw.astype(np.float64) @ (0.5 * s64 * (1 + np.tanh(0.7978845608 * (s64 + 0.044715 * s64 ** 3))) * g64)
+    d2 = d2 / np.sqrt(np.mean(d2 * d2) + eps) * post
+    assert np.max(np.abs(x + d2 - r)) > 100 * tol.max()
+
+
 # ---------------------------------------------------------------------------------------
 # builds agree; generator pinned
 # ---------------------------------------------------------------------------------------
@@ -467,6 +563,7 @@ def test_simd_build_bit_identical(o, osimd):
     u = synth.normal_f32(12, "u", (20000,))
     assert np.array_equal(o.geglu(g, u).view(np.uint32), osimd.geglu(g, u).view(np.uint32))
     assert np.array_equal(o.softcap(g * 30, 30.0).view(np.uint32), osimd.softcap(g * 30, 30.0).view(np.uint32))
+    assert np.array_equal(o.swiglu(g, u).view(np.uint32), osimd.swiglu(g, u).view(np.uint32))
     q = synth.normal_f32(12, "q", (8, 256))
     assert np.array_equal(o.apply_rope(q, None, 777, 256, 0, 8, 0, 1e4)[0], osimd.apply_rope(q, None, 777, 256, 0, 8, 0, 1e4)[0])
     tab = synth.q4_0_table(12, 16, 2560)

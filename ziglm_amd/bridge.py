@@ -94,6 +94,7 @@ SIGNATURES = {
          _f, _f, _f, _i, _v]),
     # elementwise (cuda_bridge.h:64, 66-68 + new)
     "hip_geglu": (None, [_v, _v, _v, _i, _v]),
+    "hip_swiglu": (None, [_v, _v, _v, _i, _v]),
     "hip_add": (None, [_v, _v, _i, _v]),
     "hip_scale": (None, [_v, _f, _i, _v]),
     "hip_tanh_softcap": (None, [_v, _f, _i, _v]),
@@ -127,6 +128,10 @@ SIGNATURES = {
     "hip_geglu_ex": (None, [_i, _v, _v, _v, _i64, _v]),
     "hip_tanh_softcap_ex": (None, [_i, _v, _f, _i64, _v]),
     "hip_scale_ex": (None, [_i, _v, _f, _v, _i64, _v]),
+    "hip_swiglu_ex": (None, [_i, _v, _v, _v, _i64, _v]),
+    # per-layer embedding steps (cuda_bridge.h:171-172)
+    "hip_ple_gate_gelu": (None, [_v, _v, _v, _i, _v]),
+    "hip_ple_ctx_fuse": (None, [_v, _v, _i, _i, _v]),
 }
 
 

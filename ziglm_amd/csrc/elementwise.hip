@@ -1,5 +1,6 @@
-// Elementwise ops: GeGLU (replaces cuda_bridge.cu:2247-2269), tanh soft-cap (2319-2330),
-// residual add and scale (2293-2317), and an out-of-place scale (scale 1: a kernel copy,
+// Elementwise ops: GeGLU (replaces cuda_bridge.cu:2247-2269), SwiGLU (2275-2291), tanh
+// soft-cap (2319-2330), residual add and scale (2293-2317), the per-layer-embedding (PLE)
+// gate and context fuse (2885-2937), and an out-of-place scale (scale 1: a kernel copy,
 // which a captured graph replays like any other kernel).
 //
 // Streaming layout: one wave per workgroup, each thread owns U consecutive-by-wave 128-bit
@@ -10,8 +11,10 @@
 // and U = 1 take 20.2 / 155 us, against 22.1 / 169 us for 256 threads and U = 2.
 //
 // GeGLU: out = gelu_tanh(gate) * up (math.zig:1119-1130) with the logistic form of GELU
-// (zl_common.h gelu_fast). Soft-cap: x = cap * tanh(x / cap) (model.zig:805-810) with the
-// IEEE quotient x/cap (div_by_uniform) and tanh_fast.
+// (zl_common.h gelu_fast). SwiGLU: out = silu(gate) * up (math.zig:1108-1117, silu_fast).
+// Soft-cap: x = cap * tanh(x / cap) (model.zig:805-810) with the IEEE quotient x/cap
+// (div_by_uniform) and tanh_fast. PLE context fuse (model.zig:525-535): ctx = (ctx + s) * c
+// with c = f32(1/sqrt(2)), two roundings as the CPU's, or ctx = s.
 #include "zl_common.h"
 #include "zl_host.h"
 
@@ -26,14 +29,18 @@ namespace zl {
 constexpr int kEwThreads = ZL_EW_THREADS;
 constexpr int kEwUnroll = ZL_EW_UNROLL;
 
-enum EwOp { EW_GEGLU = 0, EW_SOFTCAP = 1, EW_ADD = 2, EW_SCALE = 3 };
+enum EwOp { EW_GEGLU = 0, EW_SOFTCAP = 1, EW_ADD = 2, EW_SCALE = 3, EW_SWIGLU = 4, EW_PLE_FUSE = 5 };
+
+// Ops with a second input stream.
+template <int OP>
+constexpr bool ew_two() { return OP == EW_GEGLU || OP == EW_ADD || OP == EW_SWIGLU || OP == EW_PLE_FUSE; }
 
 struct EwArgs {
     const void* a;  // gate | x | x
     const void* b;  // up   | -  | residual
     void* out;
     int64_t n;
-    float p0, p1;   // softcap: cap, 1/cap; scale: factor
+    float p0, p1;   // softcap: cap, 1/cap; scale: factor; PLE fuse: factor, 1 = add (0 = copy b)
 };
 
 template <int OP>
@@ -41,6 +48,8 @@ __device__ __forceinline__ float ew1(float a, float b, const EwArgs& args) {
     if constexpr (OP == EW_GEGLU) return gelu_fast(a) * b;
     else if constexpr (OP == EW_SOFTCAP) return args.p0 * tanh_fast(div_by_uniform(a, args.p0, args.p1));
     else if constexpr (OP == EW_ADD) return a + b;
+    else if constexpr (OP == EW_SWIGLU) return silu_fast(a) * b;
+    else if constexpr (OP == EW_PLE_FUSE) return args.p1 != 0.0f ? (a + b) * args.p0 : b;
     else return a * args.p0;
 }
 
@@ -48,7 +57,7 @@ template <typename T, int OP>
 __global__ __launch_bounds__(kEwThreads) void k_ew(EwArgs args) {
     using C = Chunk<T>;
     constexpr int E = C::E;
-    constexpr bool kTwo = OP == EW_GEGLU || OP == EW_ADD;
+    constexpr bool kTwo = ew_two<OP>();
     const int64_t nch = args.n / E;
     const T* A = (const T*)args.a;
     const T* B = (const T*)args.b;
@@ -95,7 +104,7 @@ __global__ __launch_bounds__(kEwThreads) void k_ew(EwArgs args) {
 // Unaligned buffers: one element per thread.
 template <typename T, int OP>
 __global__ __launch_bounds__(kEwThreads) void k_ew_scalar(EwArgs args) {
-    constexpr bool kTwo = OP == EW_GEGLU || OP == EW_ADD;
+    constexpr bool kTwo = ew_two<OP>();
     const int64_t i = (int64_t)blockIdx.x * kEwThreads + threadIdx.x;
     if (i >= args.n) return;
     float x, y = 0.0f;
@@ -114,7 +123,7 @@ __global__ __launch_bounds__(kEwThreads) void k_ew_scalar(EwArgs args) {
 template <typename T, int OP>
 static void launch_ew_t(const EwArgs& a, hipStream_t s) {
     constexpr int E = Chunk<T>::E;
-    constexpr bool kTwo = OP == EW_GEGLU || OP == EW_ADD;
+    constexpr bool kTwo = ew_two<OP>();
     const bool vec = aligned16(a.a) && aligned16(a.out) && (!kTwo || aligned16(a.b));
     if (vec) {
         const int64_t nch = a.n / E;
@@ -130,7 +139,7 @@ static void launch_ew_t(const EwArgs& a, hipStream_t s) {
 template <int OP>
 static void launch_ew(int dtype, const EwArgs& a, hipStream_t s) {
     if (a.n <= 0) return;
-    if (!a.a || !a.out || ((OP == EW_GEGLU || OP == EW_ADD) && !a.b)) {
+    if (!a.a || !a.out || (ew_two<OP>() && !a.b)) {
         set_error(HIP_BRIDGE_EINVAL);
         return;
     }
@@ -178,6 +187,31 @@ void hip_scale(float* x, float scale, int n, HipStream_t stream) {
 void hip_scale_ex(int dtype, const void* x, float scale, void* out, int64_t n, HipStream_t stream) {
     EwArgs a{x, nullptr, out, n, scale, 0.0f};
     launch_ew<EW_SCALE>(dtype, a, stream_of(stream));
+}
+
+void hip_swiglu_ex(int dtype, const void* gate, const void* up, void* out, int64_t n,
+                   HipStream_t stream) {
+    EwArgs a{gate, up, out, n, 0.0f, 0.0f};
+    launch_ew<EW_SWIGLU>(dtype, a, stream_of(stream));
+}
+
+void hip_swiglu(const float* gate, const float* up, float* out, int n, HipStream_t stream) {
+    hip_swiglu_ex(HIP_BRIDGE_F32, gate, up, out, n, stream);
+}
+
+// ple_buf = gelu_tanh(gate) * slice: the GeGLU kernel with the slice as the up operand
+// (model.zig:765-768 computes slice * gelu(gate); the product commutes exactly).
+void hip_ple_gate_gelu(const float* ple_gate_in, const float* ple_slice, float* ple_buf_out,
+                       int ple_dim, HipStream_t stream) {
+    hip_geglu_ex(HIP_BRIDGE_F32, ple_gate_in, ple_slice, ple_buf_out, ple_dim, stream);
+}
+
+void hip_ple_ctx_fuse(float* ctx_ple_buf, const float* ctx_scratch, int n, int add_token_embd,
+                      HipStream_t stream) {
+    // 1/sqrt(2) rounded to f32 (0x3F3504F3), the value of model.zig:528's
+    // `1.0 / @sqrt(2.0)` coerced to f32.
+    EwArgs a{ctx_ple_buf, ctx_scratch, ctx_ple_buf, n, 0.70710677f, add_token_embd ? 1.0f : 0.0f};
+    launch_ew<EW_PLE_FUSE>(HIP_BRIDGE_F32, a, stream_of(stream));
 }
 
 }  // extern "C"

@@ -234,6 +234,24 @@ __device__ __forceinline__ float gelu_fast(float x) {
     return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
+// SiLU x / (1 + exp(-x)) (math.zig:1108-1110). exp(-x) = 2^y with y = -x*log2(e): the
+// rounding error of y (FMA residual plus the low part of log2(e)) is folded back in to first
+// order, so the exponential is accurate to ~2 ulp for every |x| (a plain exp2 of the rounded
+// product loses up to |x|*2^-24 relative); the quotient is rcp plus one Newton step. exp(-x)
+// overflowing (x < -88.7) gives x / inf = -0, as the CPU's division does.
+__device__ __forceinline__ float silu_fast(float x) {
+    const float nx = -x;
+    const float y = nx * 1.44269502f;                                // RN(-x * log2 e)
+    const float dy = fmaf(nx, 1.44269502f, -y) + nx * 1.92596299e-8f;  // -x*log2(e) - y
+    const float e0 = __builtin_amdgcn_exp2f(y);
+    const float e = fmaf(e0, dy * 0.693147181f, e0);
+    const float d = 1.0f + e;
+    const float r = __builtin_amdgcn_rcpf(d);
+    const float q = x * r;
+    const float qc = fmaf(fmaf(-d, q, x), r, q);
+    return (__builtin_isinf(e0) || __builtin_isinf(e)) ? copysignf(0.0f, x) : qc;
+}
+
 // Correctly rounded x / b for a divisor b shared by all lanes, given rb = RN(1/b) computed on
 // the host: q0 = x*rb, r = x - b*q0 (exact by FMA), q = q0 + r*rb (Markstein's correction;
 // valid when no intermediate over/underflows, which holds for |x| < 2^100 and

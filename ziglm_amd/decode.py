@@ -113,8 +113,7 @@ class DecodeModel:
         self._gemv(m.ple_proj, self.xb, self.ple_ctx)
         if m.ple_proj_norm is not None:
             d.rmsNormRows(B.F32, self.ple_ctx, m.ple_proj_norm, self.ple_ctx, self.L, PLE_DIM, m.eps, False)
-            d.add(self.ple, self.ple_ctx, n)
-            d.scale(self.ple, float(np.float32(1.0) / np.sqrt(np.float32(2.0))), n)
+            d.pleCtxFuse(self.ple, self.ple_ctx, n, True)
 
     def step_ops(self):
         """Enqueue one decode step on dev.stream (token and position read from the device)."""
@@ -211,7 +210,7 @@ class DecodeModel:
                     d.gemvPro(t.qtype, t.buf, None, self.ple_gate, self.fo, t.rows, t.cols,
                               d.prologue(B.PRO_GEGLU, r=ple_l))
                 else:
-                    d.geglu(self.ple_gate, ple_l, self.ple_buf, PLE_DIM)
+                    d.pleGateGelu(self.ple_gate, ple_l, self.ple_buf, PLE_DIM)
                     self._gemv(t, self.ple_buf, self.fo)
                 pend = (self.fo, ly.post_per_layer_input_norm, False, 1.0)
             if ly.layer_scalar != 1.0:

@@ -234,6 +234,18 @@ class HipDevice:
         self.b.hip_geglu(_ptr(d_gate), _ptr(d_up), _ptr(d_out), n, self.stream)
         self._done("geglu")
 
+    def swiglu(self, d_gate, d_up, d_out, n):
+        self.b.hip_swiglu(_ptr(d_gate), _ptr(d_up), _ptr(d_out), n, self.stream)
+        self._done("swiglu")
+
+    def pleGateGelu(self, d_ple_gate, d_ple_slice, d_ple_buf, ple_dim):
+        self.b.hip_ple_gate_gelu(_ptr(d_ple_gate), _ptr(d_ple_slice), _ptr(d_ple_buf), ple_dim, self.stream)
+        self._done("pleGateGelu")
+
+    def pleCtxFuse(self, d_ctx_ple_buf, d_ctx_scratch, n, add_token_embd):
+        self.b.hip_ple_ctx_fuse(_ptr(d_ctx_ple_buf), _ptr(d_ctx_scratch), n, int(bool(add_token_embd)), self.stream)
+        self._done("pleCtxFuse")
+
     # -- GEMV / GEMM (cuda.zig:281-356) ----------------------------------------------------
     def gemv(self, qtype, d_weights, d_x, d_y, rows, cols):
         self.b.hip_gemv(int(qtype), _ptr(d_weights), _ptr(d_x), _ptr(d_y), rows, cols, self.stream)
@@ -346,6 +358,10 @@ class HipDevice:
     def scaleEx(self, dtype, d_x, s, d_out, n):
         self.b.hip_scale_ex(dtype, _ptr(d_x), s, _ptr(d_out), n, self.stream)
         self._done("scaleEx")
+
+    def swigluEx(self, dtype, d_gate, d_up, d_out, n):
+        self.b.hip_swiglu_ex(dtype, _ptr(d_gate), _ptr(d_up), _ptr(d_out), n, self.stream)
+        self._done("swigluEx")
 
     def copyF32(self, d_src, d_dst, n):
         """dst = src (n f32) by a kernel, so it records as a kernel node in a graph."""
