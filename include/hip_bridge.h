@@ -52,6 +52,8 @@ typedef void* HipEvent_t;     /* new: event handle for stream timing */
 #define HIP_BRIDGE_OK 0
 #define HIP_BRIDGE_EINVAL (-1)       /* bad argument (NULL buffer, bad size); no launch */
 #define HIP_BRIDGE_EUNSUPPORTED (-2) /* qtype / dtype / shape not supported; no launch */
+#define HIP_BRIDGE_ESCRATCH (-3)     /* call exceeds a no-allocation entry point's static
+                                        scratch; no launch */
 
 /* ---------------------------------------------------------------------------------- */
 /* Device & memory management (replaces cuda_bridge.h:15-25)                          */
@@ -309,6 +311,23 @@ void hip_attention_decode(int kv_dtype, const float* q, const void* k_cache, con
                           int pos_base, int max_len, int batch, int n_heads, int n_kv_heads,
                           int head_dim, float attn_scale, float softcap, int sliding_window,
                           void* workspace, size_t workspace_bytes, HipStream_t stream);
+/* new, no counterpart in the reference: hip_attention_decode for callers that cannot
+ * allocate (code under hipGraph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). The split partials live in a static 32 MiB device array of the library, one per
+ * GPU, instead of a workspace; the call allocates nothing. A call whose
+ * hip_attention_workspace_bytes(batch, n_heads, n_kv_heads, head_dim, max_len,
+ * sliding_window) exceeds 32 MiB is not launched and records HIP_BRIDGE_ESCRATCH (e.g. 256
+ * sequences of Gemma-4B heads over 32768 positions need 68 MB: use hip_attention_decode).
+ * Every call on one GPU shares that GPU's array: calls that overlap in time on one GPU
+ * (different streams, or host threads) race. Nothing in the array needs to start at zero
+ * (every partial the merge reads is written by the same call). The first call on a device
+ * looks up the array's device address (hipGetSymbolAddress); make it outside stream capture. */
+void hip_attention_decode_noalloc(int kv_dtype, const float* q, const void* k_cache, const void* v_cache,
+                                  float* out, int64_t cache_rows, int64_t row_stride,
+                                  const int64_t* d_row_base, int64_t row_base, const int32_t* d_pos,
+                                  int pos_base, int max_len, int batch, int n_heads, int n_kv_heads,
+                                  int head_dim, float attn_scale, float softcap, int sliding_window,
+                                  HipStream_t stream);
 /* new: the same call with the decode step's QK-norm + RoPE + KV append folded in (no
  * counterpart in the reference, which runs hip_qk_norm_rope_kv's three steps as separate
  * launches before attention): q holds the raw query heads (read only; not rewritten), and

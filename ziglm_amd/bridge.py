@@ -13,7 +13,7 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("HIP_BRIDGE_LIB") or os.path.join(PKG, "libhip_bridge.so")
 
 F32, F16, Q4_0, Q8_0, Q4_K, Q6_K, BF16 = 0, 1, 2, 8, 12, 14, 30
-OK, EINVAL, EUNSUPPORTED = 0, -1, -2
+OK, EINVAL, EUNSUPPORTED, ESCRATCH = 0, -1, -2, -3
 
 _v = ctypes.c_void_p
 _i = ctypes.c_int
@@ -123,6 +123,8 @@ SIGNATURES = {
     "hip_attention_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i]),
     "hip_attention_decode": (None, [_i, _v, _v, _v, _v, _i64, _i64, _v, _i64, _v, _i, _i, _i, _i, _i, _i,
                                     _f, _f, _i, _v, _sz, _v]),
+    "hip_attention_decode_noalloc": (None, [_i, _v, _v, _v, _v, _i64, _i64, _v, _i64, _v, _i, _i, _i, _i, _i, _i,
+                                            _f, _f, _i, _v]),
     "hip_attention_decode_qk": (None, [_i, _v, _v, _v, _v, _v, _i, _v, _v, _v, _i64, _i64, _v, _i64, _v, _i, _i,
                                        _i, _i, _i, _i, _i, _f, _f, _f, _i, _f, _f, _i, _v, _sz, _v]),
     "hip_geglu_ex": (None, [_i, _v, _v, _v, _i64, _v]),

@@ -22,6 +22,7 @@
 // rounding of the scores, not bit for bit.
 #include <math.h>
 #include <algorithm>
+#include <mutex>
 
 #include "zl_common.h"
 #include "zl_host.h"
@@ -560,6 +561,43 @@ static AttnArgs base_attn(const float* q, const void* kc, const void* vc, float*
     return a;
 }
 
+// ---- the no-allocation variant's scratch -------------------------------------------------
+// hip_attention_decode_noalloc keeps its split partials in this file-scope device array
+// instead of a caller workspace. Each GPU the library runs on holds its own copy, at its own
+// address, until the process ends. Host code never passes the array's name to a kernel (in
+// host code that name is a host-side stand-in, not a device address): the device address is
+// looked up once per device, with that device current, and cached.
+constexpr size_t kScratchBytes = size_t(32) << 20;
+constexpr int kScratchDevices = 64;
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kScratchDevices];
+
+// The current device's copy of `scratch`, or null (error recorded).
+static void* scratch_on_current_device() {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) {
+        set_error((int)e);
+        return nullptr;
+    }
+    if (dev < 0 || dev >= kScratchDevices) {
+        set_error(HIP_BRIDGE_EUNSUPPORTED);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            set_error(e != hipSuccess ? (int)e : HIP_BRIDGE_EINVAL);
+            return nullptr;
+        }
+        g_scratch_ptr[dev] = p;
+    }
+    return g_scratch_ptr[dev];
+}
+
 }  // namespace zl
 
 using namespace zl;
@@ -605,6 +643,25 @@ void hip_attention_decode(int kv_dtype, const float* q, const void* k_cache, con
     a.batch = batch;
     if (!aligned16(workspace)) a.ws = nullptr;
     launch_attn(kv_dtype, a, workspace_bytes, stream_of(stream));
+}
+
+void hip_attention_decode_noalloc(int kv_dtype, const float* q, const void* k_cache, const void* v_cache,
+                                  float* out, int64_t cache_rows, int64_t row_stride, const int64_t* d_row_base,
+                                  int64_t row_base, const int32_t* d_pos, int pos_base, int max_len, int batch,
+                                  int n_heads, int n_kv_heads, int head_dim, float attn_scale, float softcap,
+                                  int sliding_window, HipStream_t stream) {
+    // the split partials the workspace variant would ask for must fit the static scratch
+    const size_t need = hip_attention_workspace_bytes(batch, n_heads, n_kv_heads, head_dim, max_len,
+                                                      sliding_window);
+    if (need > kScratchBytes) {
+        set_error(HIP_BRIDGE_ESCRATCH);
+        return;
+    }
+    void* ws = need > 0 ? scratch_on_current_device() : nullptr;
+    if (need > 0 && !ws) return;  // error recorded
+    hip_attention_decode(kv_dtype, q, k_cache, v_cache, out, cache_rows, row_stride, d_row_base, row_base, d_pos,
+                         pos_base, max_len, batch, n_heads, n_kv_heads, head_dim, attn_scale, softcap,
+                         sliding_window, ws, ws ? kScratchBytes : 0, stream);
 }
 
 void hip_attention_decode_qk(int kv_dtype, const float* q, const float* k, const float* v,

@@ -190,6 +190,8 @@ const char* hip_bridge_error_string(int code) {
     if (code == HIP_BRIDGE_OK) return "ok";
     if (code == HIP_BRIDGE_EINVAL) return "invalid argument (op not launched)";
     if (code == HIP_BRIDGE_EUNSUPPORTED) return "unsupported type or shape (op not launched)";
+    if (code == HIP_BRIDGE_ESCRATCH)
+        return "call needs more scratch than the no-allocation entry point's static maximum (op not launched)";
     return hipGetErrorString((hipError_t)code);
 }
 

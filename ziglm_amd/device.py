@@ -331,6 +331,17 @@ class HipDevice:
                                     sliding_window, _ptr(d_workspace), workspace_bytes, self.stream)
         self._done("attentionDecode")
 
+    def attentionDecodeNoalloc(self, kv_dtype, d_q, d_k_cache, d_v_cache, d_out, cache_rows, row_stride, d_row_base,
+                               row_base, d_pos, pos_base, max_len, batch, n_heads, n_kv_heads, head_dim, attn_scale,
+                               softcap, sliding_window):
+        """attentionDecode with the split partials in the library's static scratch (no
+        workspace, no allocation); calls whose workspace would exceed 32 MiB record ESCRATCH."""
+        self.b.hip_attention_decode_noalloc(int(kv_dtype), _ptr(d_q), _ptr(d_k_cache), _ptr(d_v_cache), _ptr(d_out),
+                                            cache_rows, row_stride, _ptr(d_row_base), row_base, _ptr(d_pos), pos_base,
+                                            max_len, batch, n_heads, n_kv_heads, head_dim, attn_scale, softcap,
+                                            sliding_window, self.stream)
+        self._done("attentionDecodeNoalloc")
+
     def attentionDecodeQk(self, kv_dtype, d_q, d_k, d_v, d_q_norm_w, d_k_norm_w, v_norm, d_k_cache, d_v_cache,
                           d_out, cache_rows, row_stride, d_row_base, row_base, d_pos, pos_base, max_len, batch,
                           n_heads, n_kv_heads, head_dim, rotary_dim, freq_base, freq_scale, eps, use_unit_offset,

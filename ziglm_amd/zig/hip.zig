@@ -125,6 +125,7 @@ pub extern "c" fn hip_attention_forward_ind(q: [*]const f32, k_cache: [*]const f
 pub extern "c" fn hip_attention_batched(q: [*]const f32, k_cache: [*]const f32, v_cache: [*]const f32, out: [*]f32, donor_layer: c_int, pos: c_int, batch_size: c_int, max_seq: c_int, n_heads: c_int, n_kv_heads: c_int, head_dim: c_int, max_kv_dim: c_int, attn_scale: f32, softcap: f32, sliding_window: c_int, stream: HipStream_t) void;
 pub extern "c" fn hip_attention_workspace_bytes(batch: c_int, n_heads: c_int, n_kv_heads: c_int, head_dim: c_int, max_len: c_int, sliding_window: c_int) usize;
 pub extern "c" fn hip_attention_decode(kv_dtype: c_int, q: [*]const f32, k_cache: ?*const anyopaque, v_cache: ?*const anyopaque, out: [*]f32, cache_rows: i64, row_stride: i64, d_row_base: ?[*]const i64, row_base: i64, d_pos: ?[*]const i32, pos_base: c_int, max_len: c_int, batch: c_int, n_heads: c_int, n_kv_heads: c_int, head_dim: c_int, attn_scale: f32, softcap: f32, sliding_window: c_int, workspace: ?*anyopaque, workspace_bytes: usize, stream: HipStream_t) void;
+pub extern "c" fn hip_attention_decode_noalloc(kv_dtype: c_int, q: [*]const f32, k_cache: ?*const anyopaque, v_cache: ?*const anyopaque, out: [*]f32, cache_rows: i64, row_stride: i64, d_row_base: ?[*]const i64, row_base: i64, d_pos: ?[*]const i32, pos_base: c_int, max_len: c_int, batch: c_int, n_heads: c_int, n_kv_heads: c_int, head_dim: c_int, attn_scale: f32, softcap: f32, sliding_window: c_int, stream: HipStream_t) void;
 pub extern "c" fn hip_attention_decode_qk(kv_dtype: c_int, q: [*]const f32, k: ?[*]const f32, v: ?[*]const f32, q_norm_w: ?[*]const f32, k_norm_w: ?[*]const f32, v_norm: c_int, k_cache: *anyopaque, v_cache: *anyopaque, out: [*]f32, cache_rows: i64, row_stride: i64, d_row_base: ?[*]const i64, row_base: i64, d_pos: ?[*]const i32, pos_base: c_int, max_len: c_int, batch: c_int, n_heads: c_int, n_kv_heads: c_int, head_dim: c_int, rotary_dim: c_int, freq_base: f32, freq_scale: f32, eps: f32, use_unit_offset: c_int, attn_scale: f32, softcap: f32, sliding_window: c_int, workspace: ?*anyopaque, workspace_bytes: usize, stream: HipStream_t) void;
 
 // greedy token selection
@@ -503,6 +504,13 @@ pub const HipDevice = struct {
         const ws_ptr: ?*anyopaque = if (workspace) |w| w.ptr else null;
         const ws_len: usize = if (workspace) |w| w.size_bytes else 0;
         hip_attention_decode(kv_dtype, d_q, d_k_cache, d_v_cache, d_out, @intCast(cache_rows), @intCast(row_stride), d_row_base, @intCast(row_base), d_pos, int(pos_base), int(max_len), int(batch), int(n_heads), int(n_kv_heads), int(head_dim), attn_scale, softcap, int(sliding_window), ws_ptr, ws_len, self.stream);
+    }
+
+    /// attentionDecode for callers that cannot allocate (graph capture, serving loops): the
+    /// split partials live in the library's static 32 MiB device scratch; a call needing more
+    /// is not launched (lastError() = -3). Calls overlapping in time on one GPU race.
+    pub fn attentionDecodeNoalloc(self: *const HipDevice, kv_dtype: c_int, d_q: [*]const f32, d_k_cache: ?*const anyopaque, d_v_cache: ?*const anyopaque, d_out: [*]f32, cache_rows: usize, row_stride: usize, d_row_base: ?[*]const i64, row_base: usize, d_pos: ?[*]const i32, pos_base: usize, max_len: usize, batch: usize, n_heads: usize, n_kv_heads: usize, head_dim: usize, attn_scale: f32, softcap: f32, sliding_window: usize) void {
+        hip_attention_decode_noalloc(kv_dtype, d_q, d_k_cache, d_v_cache, d_out, @intCast(cache_rows), @intCast(row_stride), d_row_base, @intCast(row_base), d_pos, int(pos_base), int(max_len), int(batch), int(n_heads), int(n_kv_heads), int(head_dim), attn_scale, softcap, int(sliding_window), self.stream);
     }
 
     /// attentionDecode with the QK-norm, RoPE and KV append of the token's own row folded in
