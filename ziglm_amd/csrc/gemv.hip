@@ -750,7 +750,9 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(QT
     // compiler wait for it where the branch ends, i.e. before the step that needs it.)
     const int n = (G + kWave - 1) / kWave;
     // x is staged once per workgroup in LDS and read there at each step (it is not held in
-    // registers across a step, which keeps the kernel at 8 waves per SIMD for Q4_0).
+    // registers across a step, which keeps the kernel's VGPRs at 8 waves per SIMD for Q4_0;
+    // the cols * 4 bytes of LDS per 4-wave workgroup allow 8 waves per SIMD up to 5120
+    // columns of the CU's 160 KB, 4 up to 10240).
     extern __shared__ __attribute__((aligned(16))) float s_xw[];
     auto fetch = [&](int k, WGroup<QT> (&w)[RW][NM]) {
         const int g = min(lane + kWave * k, G - 1);
@@ -937,7 +939,10 @@ static void launch_vec(const GemvArgs& a, hipStream_t s) {
         constexpr bool blockq = QT != HIP_BRIDGE_F16 && QT != HIP_BRIDGE_BF16 && QT != HIP_BRIDGE_F32;
         if constexpr (F < 0 && blockq) {
             constexpr int RW = std::max(1, -F / H);
-            k_gemv_w<QT, RW, MODE><<<(unsigned)cdiv(a.total_rows, (int64_t)RW * kGemvWaves), kGemvThreads, (size_t)a.cols * 4, s>>>(a);
+            if (a.cols <= kGemvWaveColsMax)  // x in LDS: at most 64 KB
+                k_gemv_w<QT, RW, MODE><<<(unsigned)cdiv(a.total_rows, (int64_t)RW * kGemvWaves), kGemvThreads, (size_t)a.cols * 4, s>>>(a);
+            else
+                k_gemv<QT, 2 / H, 1, MODE><<<g2, kGemvThreads, 0, s>>>(a);
         } else {
             constexpr int RP = F > 0 ? std::max(1, F / H) : 2 / H;
             k_gemv<QT, RP, 1, MODE><<<(unsigned)cdiv(a.total_rows, RP), kGemvThreads, 0, s>>>(a);
