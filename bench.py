@@ -25,6 +25,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
 """
 import argparse
 import ctypes
+import dataclasses
 import json
 import math
 import os
@@ -82,6 +83,32 @@ def time_launches_us(dev, fn, sets, n_launch, warm=1):
     return ms * 1000.0 / n_launch
 
 
+def stream_ceiling(dev, n_in, n_out, nbytes, min_total=3 * MALL_BYTES, n_launch=40):
+    """Practical ceiling of a byte mix: the fastest launch shape of the library's reference
+    streaming kernel (hip_stream_ref: n_in reads and n_out writes of nbytes each, nothing
+    else) over buffer sets that together exceed the Infinity Cache. Returns (us, shape)."""
+    per = (n_in + n_out) * nbytes
+    nsets = int(min(8, max(2, math.ceil(min_total / per))))
+    sets = [[dev.alloc(nbytes) for _ in range(n_in + n_out)] for _ in range(nsets)]
+    for st in sets:
+        for buf in st:
+            buf.fill(0x3C)
+    best = (float("inf"), -1)
+    for shp in range(dev.b.hip_stream_ref_shapes()):
+        def fn(d, st, shp=shp):
+            i1 = st[1].ptr if n_in == 2 else None
+            o1 = st[n_in + 1].ptr if n_out == 2 else None
+            rc = d.b.hip_stream_ref(n_in, n_out, st[0].ptr, i1, st[n_in].ptr, o1, nbytes, shp, d.stream)
+            if rc != 0:
+                raise RuntimeError(f"hip_stream_ref: {rc}")
+        us = time_launches_us(dev, fn, sets, max(n_launch, 4 * nsets))
+        best = min(best, (us, shp))
+    for st in sets:
+        for buf in st:
+            buf.deinit()
+    return best
+
+
 # ---------------------------------------------------------------------------------------
 # data
 # ---------------------------------------------------------------------------------------
@@ -111,11 +138,14 @@ def fill_tiled(buf, src):
         done += c
 
 
-def make_sets(dev, shape, T, dtype, min_total=3 * MALL_BYTES, max_sets=8, cache_rows=None, pos0=0):
-    """Buffer sets for the rotation; set 0 seeded, others copies."""
+def make_sets(dev, shape, T, dtype, min_total=3 * MALL_BYTES, max_sets=8, cache_rows=None, pos0=0, thetas=None):
+    """Buffer sets for the rotation; set 0 seeded, others copies. thetas: RoPE bases the
+    sets cycle through (set i takes thetas[i % len]; the number of sets is then a multiple)."""
     L0 = LY.LayerBuffers(dev, shape, T, dtype, cache_rows=cache_rows)
     per = sum(b.size_bytes for b in (L0.x, L0.xb, L0.ao, L0.fo, L0.q, L0.k, L0.v, L0.gate, L0.up, L0.act))
     nsets = int(min(max_sets, max(2, math.ceil(min_total / per))))
+    if thetas:
+        nsets = max(len(thetas), nsets - nsets % len(thetas))
     p = pool(dtype)
     for name in ("x", "xb", "ao", "fo", "q", "k", "v", "gate", "up", "act"):
         fill_tiled(getattr(L0, name), p)
@@ -127,12 +157,15 @@ def make_sets(dev, shape, T, dtype, min_total=3 * MALL_BYTES, max_sets=8, cache_
     L0.kc.fill(0)
     L0.vc.fill(0)
     sets = [L0]
-    for _ in range(nsets - 1):
-        L = LY.LayerBuffers(dev, shape, T, dtype, cache_rows=cache_rows)
+    for i in range(1, nsets):
+        sh = dataclasses.replace(shape, theta=thetas[i % len(thetas)]) if thetas else shape
+        L = LY.LayerBuffers(dev, sh, T, dtype, cache_rows=cache_rows)
         L.copy_from(L0)
         L.kc.fill(0)
         L.vc.fill(0)
         sets.append(L)
+    if thetas:
+        L0.shape = dataclasses.replace(shape, theta=thetas[0])
     dev.sync()
     return sets, per
 
@@ -151,18 +184,51 @@ def free_sets(sets):
 # prefill chain configs (c2, c4)
 # ---------------------------------------------------------------------------------------
 
-def bench_prefill(dev, shape, T, dtype, steps, warmup, ops_launches=40):
+def op_mix(shape, T, es):
+    """(reads, writes, bytes per stream) of each op's activation traffic: the byte mix its
+    same-size streaming ceiling moves (the few KB of norm weights and positions aside)."""
+    H, I = shape.H, shape.I
+    qkv = T * (shape.nh + 2 * shape.nkv) * shape.D * es  # Q, K, V in; Q, K row, V row out
+    return {"input_norm": (1, 1, T * H * es), "add_rmsnorm": (2, 2, T * H * es),
+            "qk_norm_rope_kv": (1, 1, qkv), "norm_add_norm": (2, 2, T * H * es), "geglu": (2, 1, T * I * es),
+            "norm_add": (2, 1, T * H * es), "norm_add_norm_next": (2, 2, T * H * es)}
+
+
+def bench_prefill(dev, shape, T, dtype, steps, warmup, ops_launches=40, thetas=None):
+    """thetas: RoPE bases the buffer sets alternate (c4: local 1e4 and global 1e6 layers),
+    so consecutive chain steps and QK launches take both; the QK op is also timed at each
+    base alone."""
     es = 4 if dtype == B.F32 else 2
-    sets, per = make_sets(dev, shape, T, dtype)
-    log(f"{shape.name} T={T}: {len(sets)} buffer sets x {per / 1e6:.0f} MB")
+    sets, per = make_sets(dev, shape, T, dtype, thetas=thetas)
+    log(f"{shape.name} T={T}: {len(sets)} buffer sets x {per / 1e6:.0f} MB"
+        + (f", RoPE bases {thetas} alternating" if thetas else ""))
     nb = LY.op_bytes(shape, T, es)
+    mix = op_mix(shape, T, es)
+    ceilings = {}
     ops = {}
     for name in ("input_norm", "add_rmsnorm", "qk_norm_rope_kv", "norm_add_norm", "geglu", "norm_add",
                  "norm_add_norm_next"):
         us = time_launches_us(dev, LY.OPS[name], sets, max(ops_launches, len(sets) * 4))
+        if mix[name] not in ceilings:
+            ceilings[mix[name]] = stream_ceiling(dev, *mix[name])
+        cu, cshape = ceilings[mix[name]]
         ops[name] = {"us": round(us, 3), "bytes": nb[name], "GBps": round(nb[name] / us / 1e3, 1),
-                     "frac_peak": round(nb[name] / us / 1e3 / PEAK_HBM_GBS, 4)}
-        log(f"  {name:20s} {us:9.2f} us  {nb[name] / us / 1e3:8.1f} GB/s")
+                     "frac_peak": round(nb[name] / us / 1e3 / PEAK_HBM_GBS, 4),
+                     "ceiling": {"us": round(cu, 3), "reads": mix[name][0], "writes": mix[name][1],
+                                 "bytes_per_stream": mix[name][2], "shape": cshape,
+                                 "GBps": round((mix[name][0] + mix[name][1]) * mix[name][2] / cu / 1e3, 1),
+                                 "frac_of_ceiling": round(cu / us, 4)}}
+        log(f"  {name:20s} {us:9.2f} us  {nb[name] / us / 1e3:8.1f} GB/s  (same-size stream {cu:.2f} us, "
+            f"{cu / us:.1%} of it)")
+    if thetas:
+        for th in thetas:
+            own = [L for L in sets if L.shape.theta == th]
+            us = time_launches_us(dev, LY.OPS["qk_norm_rope_kv"], own, max(ops_launches, len(own) * 4))
+            b_ = nb["qk_norm_rope_kv"]
+            ops[f"qk_norm_rope_kv_theta_{th:g}"] = {"us": round(us, 3), "bytes": b_,
+                                                    "GBps": round(b_ / us / 1e3, 1),
+                                                    "frac_peak": round(b_ / us / 1e3 / PEAK_HBM_GBS, 4)}
+            log(f"  qk at theta {th:g}: {us:.2f} us")
 
     def steps_graph(n):
         def body():
@@ -199,6 +265,8 @@ def bench_prefill(dev, shape, T, dtype, steps, warmup, ops_launches=40):
         "ops": ops,
         "buffer_sets": len(sets),
     }
+    if thetas:
+        res["rope_bases"] = list(thetas)
     free_sets(sets)
     return res
 
@@ -253,17 +321,29 @@ def bench_decode(dev, B_, pos_seed=4, n_launch=200):
     us_fnorm = time_launches_us(dev, LY.op_input_norm, [L], n_launch)
     for bb in bufs:
         bb.deinit()
-    # decode attention over each sequence's cache (positions as above, f32 cache, split)
+    # decode attention over each sequence's cache (positions as above, f32 cache, split).
+    # The rows one call reads (attn_bytes) are rotated over enough cache sets that together
+    # they exceed the Infinity Cache three times, so every call streams from HBM.
     row_base = dev.from_numpy(np.arange(B_, dtype=np.int64) * max_seq)
     ws_bytes = dev.attentionWorkspaceBytes(B_, s.nh, s.nkv, s.D, max_seq)
     d_ws = dev.alloc(max(ws_bytes, 16))
     d_ao = dev.alloc(B_ * s.nh * s.D * 4)
-
-    def attn(d, L_):
-        d.attentionDecode(B.F32, L_.q, L_.kc, L_.vc, d_ao, L_.cache_rows, s.nkv * s.D, row_base, 0, L_.pos, 0,
-                          max_seq, B_, s.nh, s.nkv, s.D, 1.0, 0.0, 0, d_ws, ws_bytes)
-    us_attn = time_launches_us(dev, attn, [L], max(8, n_launch // 10))
     attn_bytes = int((pos.astype(np.int64) + 1).sum()) * s.nkv * s.D * 4 * 2 + 2 * B_ * s.nh * s.D * 4
+    n_caches = int(min(8, max(1, math.ceil(3 * MALL_BYTES / attn_bytes))))
+    caches = [(L.kc, L.vc)]
+    for _ in range(n_caches - 1):
+        kc2, vc2 = dev.alloc(L.kc.size_bytes), dev.alloc(L.vc.size_bytes)
+        kc2.fill(0)
+        vc2.fill(0)
+        caches.append((kc2, vc2))
+
+    def attn(d, kv):
+        d.attentionDecode(B.F32, L.q, kv[0], kv[1], d_ao, L.cache_rows, s.nkv * s.D, row_base, 0, L.pos, 0,
+                          max_seq, B_, s.nh, s.nkv, s.D, 1.0, 0.0, 0, d_ws, ws_bytes)
+    us_attn = time_launches_us(dev, attn, caches, max(8, n_launch // 10, 4 * n_caches))
+    for kc2, vc2 in caches[1:]:
+        kc2.deinit()
+        vc2.deinit()
     for bb in (row_base, d_ws, d_ao):
         bb.deinit()
     free_sets([L])
@@ -271,7 +351,8 @@ def bench_decode(dev, B_, pos_seed=4, n_launch=200):
     return {"B": B_, "us_per_layer": round(chain_us, 2), "us_per_layer_fused_4op": round(fused_us, 2), "ops": ops,
             "final_norm_us": round(us_fnorm, 3),
             "attention": {"us": round(us_attn, 2), "bytes": attn_bytes, "GBps": round(attn_bytes / us_attn / 1e3, 1),
-                          "frac_peak": round(attn_bytes / us_attn / 1e3 / PEAK_HBM_GBS, 4)},
+                          "frac_peak": round(attn_bytes / us_attn / 1e3 / PEAK_HBM_GBS, 4),
+                          "cache_sets": n_caches},
             "softcap": {"us": round(us_cap, 2), "bytes": cap_bytes,
                         "GBps": round(cap_bytes / us_cap / 1e3, 1),
                         "frac_peak": round(cap_bytes / us_cap / 1e3 / PEAK_HBM_GBS, 4)}}
@@ -512,63 +593,81 @@ def pool_threads(cpus):
     return cpus // 2 if cpus >= 16 else 8 if cpus > 8 else max(1, cpus)
 
 
-def cpu_baseline(shape, T, target_s=10.0, parallel_s=3.0):
-    """The oracle's SIMD build timed on the host over the c2 chain: the whole 2048-token chain
-    repeated for about `target_s` seconds on one thread (ziglm's CPU ops are single-threaded,
-    one token at a time), plus a token-parallel run over ziglm's default pool size as an upper
-    bound."""
+def cpu_baseline(shape, T, iters=21, parallel_s=3.0):
+    """The oracle's SIMD build (-O3 -march=x86-64-v3, restating ziglm's CPU path) timed on the
+    host over the c2 workload, one thread (ziglm's CPU ops are single-threaded, one token at a
+    time): each op of the chain over all T tokens, median of `iters` runs after one warm-up,
+    the runs alternating between two seeded input sets; the chain time is the sum of the
+    per-op medians. A token-parallel run over ziglm's default pool size is an upper bound."""
     from concurrent.futures import ThreadPoolExecutor
     from oracle import oracle as O
     o = O.get(simd=True)
     s = shape
-    x = synth.normal_bf16(1, "x", (T, s.H))
-    ao = synth.normal_bf16(1, "ao", (T, s.H))
-    fo = synth.normal_bf16(1, "fo", (T, s.H))
-    q = synth.normal_bf16(1, "q", (T, s.nh, s.D))
-    k = synth.normal_bf16(1, "k", (T, s.nkv, s.D))
-    v = synth.normal_bf16(1, "v", (T, s.nkv, s.D))
-    gate = synth.normal_bf16(1, "gate", (T, s.I))
-    up = synth.normal_bf16(1, "up", (T, s.I))
-    w = {k_: synth.normal_f32(1, "w_" + k_, (s.H,), 0, 0.1) for k_ in ("in", "post_attn", "pre_ffn", "post_ffn")}
+    wts = {k_: synth.normal_f32(1, "w_" + k_, (s.H,), 0, 0.1) for k_ in ("in", "post_attn", "pre_ffn", "post_ffn")}
     wq = synth.normal_f32(1, "wq", (s.D,), 0, 0.1)
     wk = synth.normal_f32(1, "wk", (s.D,), 0, 0.1)
-    kc = np.zeros((s.max_seq, s.nkv * s.D), np.uint16)
-    vc = np.zeros_like(kc)
+
+    def inputs(seed):
+        return {"x": synth.normal_bf16(seed, "x", (T, s.H)), "ao": synth.normal_bf16(seed, "ao", (T, s.H)),
+                "fo": synth.normal_bf16(seed, "fo", (T, s.H)), "q": synth.normal_bf16(seed, "q", (T, s.nh, s.D)),
+                "k": synth.normal_bf16(seed, "k", (T, s.nkv, s.D)), "v": synth.normal_bf16(seed, "v", (T, s.nkv, s.D)),
+                "gate": synth.normal_bf16(seed, "gate", (T, s.I)), "up": synth.normal_bf16(seed, "up", (T, s.I)),
+                "kc": np.zeros((s.max_seq, s.nkv * s.D), np.uint16), "vc": np.zeros((s.max_seq, s.nkv * s.D), np.uint16)}
+    sets = [inputs(1), inputs(101)]
     pos = np.arange(T, dtype=np.int32)
+    eps = np.float32(s.eps)
 
-    def chain(a, b):
-        o.rms_norm_bf16(x[a:b], w["in"], s.eps, True)
-        o.qk_norm_rope_kv(q[a:b], k[a:b], v[a:b], wq, wk, kc, vc, max_seq=s.max_seq,
-                          max_kv_dim=s.nkv * s.D, pos=pos[a:b], n_heads=s.nh, n_kv_heads=s.nkv,
-                          head_dim=s.D, base=s.theta, eps=s.eps)
-        x2, _ = o.rms_norm_add_rms_norm(x[a:b], ao[a:b], w["post_attn"], w["pre_ffn"], s.eps, True)
-        o.geglu(gate[a:b], up[a:b])
-        o.rms_norm_add(x2, fo[a:b], w["post_ffn"], s.eps, True)
+    def op(name, h, a=0, b=T):
+        if name == "input_norm":
+            o.rms_norm_bf16(h["x"][a:b], wts["in"], eps, True)
+        elif name == "qk_norm_rope_kv":
+            o.qk_norm_rope_kv(h["q"][a:b], h["k"][a:b], h["v"][a:b], wq, wk, h["kc"], h["vc"], max_seq=s.max_seq,
+                              max_kv_dim=s.nkv * s.D, pos=pos[a:b], n_heads=s.nh, n_kv_heads=s.nkv, head_dim=s.D,
+                              base=s.theta, eps=eps)
+        elif name == "norm_add_norm":
+            o.rms_norm_add_rms_norm(h["x"][a:b], h["ao"][a:b], wts["post_attn"], wts["pre_ffn"], eps, True)
+        elif name == "geglu":
+            o.geglu(h["gate"][a:b], h["up"][a:b])
+        else:  # norm_add
+            o.rms_norm_add(h["x"][a:b], h["fo"][a:b], wts["post_ffn"], eps, True)
 
-    def timed(fn, budget):
-        reps, t0 = 0, time.perf_counter()
-        while True:
-            fn()
-            reps += 1
-            t = time.perf_counter() - t0
-            if t >= budget:
-                return reps, t
-
+    nb = LY.op_bytes(shape, T, 2)
+    ops = {}
+    t_all = time.perf_counter()
+    for name in LY.CHAIN:
+        op(name, sets[1])
+        runs = []
+        for i in range(iters):
+            t0 = time.perf_counter()
+            op(name, sets[i % 2])
+            runs.append(time.perf_counter() - t0)
+        us = float(np.median(runs)) * 1e6
+        ops[name] = {"us": round(us, 1), "GBps": round(nb[name] / us / 1e3, 4), "runs": iters}
+    t_all = time.perf_counter() - t_all
+    chain_us = sum(v["us"] for v in ops.values())
     nbytes = LY.chain_bytes(shape, T, 2)
-    reps, t = timed(lambda: chain(0, T), target_s)
     cpus = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
     nt = pool_threads(cpus)
     edges = [T * i // nt for i in range(nt + 1)]
+
+    def chain(a, b):
+        for name in LY.CHAIN:
+            op(name, sets[0], a, b)
     with ThreadPoolExecutor(nt) as ex:
         def par():
             for f in [ex.submit(chain, edges[i], edges[i + 1]) for i in range(nt)]:
                 f.result()
         par()
-        preps, pt = timed(par, parallel_s)
-    return {"value": round(reps * nbytes / t / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"c2 per-layer chain, all {T} tokens, repeated {reps}x ({t:.1f} s), "
-                      f"oracle -O3 -march=x86-64-v3, one thread",
-            "us_per_token": round(t / (reps * T) * 1e6, 1),
+        preps, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < parallel_s:
+            par()
+            preps += 1
+        pt = time.perf_counter() - t0
+    return {"value": round(nbytes / chain_us / 1e3, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"c2 per-layer chain over all {T} tokens, each op the median of {iters} runs after a warm-up "
+                      f"(two input sets alternating; {t_all:.1f} s in all), oracle -O3 -march=x86-64-v3, one thread; "
+                      f"chain = sum of the op medians",
+            "us_per_layer": round(chain_us, 1), "us_per_token": round(chain_us / T, 2), "ops": ops,
             "token_parallel_upper_bound": {
                 "value": round(preps * nbytes / pt / 1e9, 4), "unit": "GB/s", "threads": nt,
                 "sample": f"same chain split over {nt} threads by token ({preps}x, {pt:.1f} s)"}}
@@ -577,14 +676,26 @@ def cpu_baseline(shape, T, target_s=10.0, parallel_s=3.0):
 # ---------------------------------------------------------------------------------------
 
 def host_cpu():
+    """The host CPU as /proc/cpuinfo describes it: model name, family / model / stepping,
+    clock, the SIMD extensions the timed build can use, and the CPUs this process may run on."""
+    info = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                if ":" not in line:
+                    if info:
+                        break
+                    continue
+                k_, v_ = (t.strip() for t in line.split(":", 1))
+                info.setdefault(k_, v_)
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    flags = set(info.get("flags", "").split())
+    simd = [f for f in ("avx2", "fma", "avx512f", "avx512bw", "avx512vl", "avx512_bf16") if f in flags]
+    cpus = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    return (f"{info.get('model name', 'unknown')} (vendor {info.get('vendor_id', '?')}, family "
+            f"{info.get('cpu family', '?')}, model {info.get('model', '?')}, stepping {info.get('stepping', '?')}, "
+            f"{info.get('cpu MHz', '?')} MHz, {' '.join(simd)}; {cpus} CPUs available)")
 
 
 def load_traffic():
@@ -704,9 +815,9 @@ def main():
             if f"gather_{k}_c3" in tr:
                 v["traffic"] = tr[f"gather_{k}_c3"]
         log("c4 27B prefill")
-        c4 = bench_prefill(dev, LY.GEMMA_27B, 8192, B.BF16, max(4, a.steps // 4), 2)
+        c4 = bench_prefill(dev, LY.GEMMA_27B, 8192, B.BF16, max(4, a.steps // 4), 2, thetas=(1e4, 1e6))
         cfgs["c4_prefill"] = {k: c4[k] for k in ("us_per_layer", "us_per_layer_isolated_sum",
-                                                 "us_per_layer_fused_4op", "chain_GBps", "ops")}
+                                                 "us_per_layer_fused_4op", "chain_GBps", "ops", "rope_bases")}
         cfgs["c4_prefill"]["chain_GBps"] = round(cfgs["c4_prefill"]["chain_GBps"], 1)
         log("gemv (decode projections)")
         cfgs["gemv_decode"] = bench_gemv(dev)

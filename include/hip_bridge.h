@@ -388,6 +388,17 @@ void hip_ple_gate_gelu(const float* ple_gate_in, const float* ple_slice, float* 
 void hip_ple_ctx_fuse(float* ctx_ple_buf, const float* ctx_scratch, int n, int add_token_embd,
                       HipStream_t stream);                                   /* cuda_bridge.h:172 */
 
+/* ---------------------------------------------------------------------------------- */
+/* new, measurement only (no counterpart in the reference): the practical HBM ceiling of  */
+/* an op's byte mix. Reads n_in (1 or 2) streams and writes n_out (1 or 2) streams of      */
+/* `bytes` each (a multiple of 16, 16-byte aligned buffers) with launch shape `shape` in   */
+/* [0, hip_stream_ref_shapes()); returns 0 or an error code. The fastest shape at a given  */
+/* size and mix is the ceiling a fused op of that mix is compared with.                    */
+/* ---------------------------------------------------------------------------------- */
+int hip_stream_ref_shapes(void);
+int hip_stream_ref(int n_in, int n_out, const void* in0, const void* in1, void* out0, void* out1,
+                   int64_t bytes, int shape, HipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -146,6 +146,10 @@ pub extern "c" fn hip_swiglu_ex(dtype: c_int, gate: *const anyopaque, up: *const
 pub extern "c" fn hip_ple_gate_gelu(ple_gate_in: [*]const f32, ple_slice: [*]const f32, ple_buf_out: [*]f32, ple_dim: c_int, stream: HipStream_t) void;
 pub extern "c" fn hip_ple_ctx_fuse(ctx_ple_buf: [*]f32, ctx_scratch: [*]const f32, n: c_int, add_token_embd: c_int, stream: HipStream_t) void;
 
+// measurement: the streaming ceiling of a byte mix
+pub extern "c" fn hip_stream_ref_shapes() c_int;
+pub extern "c" fn hip_stream_ref(n_in: c_int, n_out: c_int, in0: ?*const anyopaque, in1: ?*const anyopaque, out0: ?*anyopaque, out1: ?*anyopaque, bytes: i64, shape: c_int, stream: HipStream_t) c_int;
+
 // ---------------------------------------------------------------------------------------
 // Reference names (cuda.zig:5-181): what cuda_model.zig, engine.zig, backend.zig and
 // root.zig refer to.
