@@ -20,8 +20,10 @@
  * Numerics follow ziglm's CPU path (src/math.zig, src/quant.zig), not its CUDA kernels:
  *   - gathers are bit-exact: out = (f32(q) * d) * scale, one rounding;
  *   - RMSNorm: inv = 1/sqrt(mean + eps) (IEEE sqrt and divide), out = (x*inv)*(1+w);
- *   - RoPE angles: theta = f32(pos)*freq_scale / D_i with D_i = f32(pow(base, f32(2i)/f32(r)))
- *     evaluated on the host in double precision, cos/sin evaluated in double precision;
+ *   - RoPE angles: theta = f32(pos)*freq_scale / D_i (IEEE f32 division) with
+ *     D_i = f32(pow(base, f32(2i)/f32(r))) evaluated in double precision; cos/sin within
+ *     1.3 ulp of the correctly rounded values (an exact double-precision reduction by pi/2,
+ *     then fitted f32 polynomials);
  *   - bf16 activations: upconvert, compute in f32, round to nearest even once.
  */
 #ifndef HIP_BRIDGE_H

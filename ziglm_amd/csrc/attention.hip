@@ -195,10 +195,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
         // cos / sin of the token's position for the rotary pairs, while the q loads fly
         if (a.qk_half > 0 && tid < a.qk_half && end > 0) {
             const float theta = ((float)last * a.qk_freq_scale) / rope_denom(tid, 2 * a.qk_half, a.qk_log2_base);
-            double sn, cs;
-            sincos((double)theta, &sn, &cs);
-            s_cos[tid] = (float)cs;
-            s_sin[tid] = (float)sn;
+            rope_sincos(theta, &s_sin[tid], &s_cos[tid]);
         }
     }
     float q[G][8];
