@@ -81,7 +81,9 @@ class Oracle:
 
     def __init__(self, simd=False):
         name = "liboracle_simd.so" if simd else "liboracle.so"
-        path = os.path.join(_HERE, name)
+        # ZIGLM_ORACLE_LIB: another build of the same sources (the sanitizer build of
+        # tests/asan) for both roles
+        path = os.environ.get("ZIGLM_ORACLE_LIB") or os.path.join(_HERE, name)
         if not os.path.exists(path):
             raise FileNotFoundError(f"{path} missing: run `make -C oracle` (or __graft_entry__.build())")
         self.lib = ctypes.CDLL(path)
