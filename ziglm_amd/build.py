@@ -25,8 +25,8 @@ BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libhip_bridge.so")
 ORACLE_DIR = os.path.join(ROOT, "oracle")
 
-SOURCES = ["runtime.hip", "embed.hip", "norm.hip", "rope_kv.hip", "elementwise.hip", "gemv.hip", "attention.hip", "argmax.hip",
-           "stream.hip", "gguf.cpp"]
+SOURCES = ["runtime.hip", "embed.hip", "norm.hip", "rope_kv.hip", "elementwise.hip", "gemv.hip", "gemm.hip",
+           "attention.hip", "argmax.hip", "stream.hip", "gguf.cpp"]
 
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 

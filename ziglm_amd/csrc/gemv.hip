@@ -1071,6 +1071,10 @@ extern "C" {
 void hip_gemm(int qtype, const void* weights, const float* x, float* y, int batch_size, int rows,
               int cols, HipStream_t stream) {
     if (batch_size <= 0 || rows <= 0 || cols <= 0) return;
+    if (batch_size >= kGemmMfmaMinBatch && weights && x) {
+        const int64_t rb = gemv_row_bytes(qtype, cols);
+        if (rb > 0 && launch_gemm_mfma(qtype, weights, rb, x, y, rows, cols, batch_size, stream_of(stream))) return;
+    }
     GemvArgs a = one_matrix(weights, x, y, rows, cols, batch_size);
     launch_gemv<GV_PLAIN>(qtype, a, stream_of(stream));
 }

@@ -24,4 +24,11 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Matrix-core GEMM (gemm.hip) for batches of at least kGemmMfmaMinBatch tokens: launches and
+// returns true when the type, shape (cols % 32 == 0) and alignment suit it, else launches
+// nothing and returns false (the caller takes the vector path).
+constexpr int kGemmMfmaMinBatch = 32;
+bool launch_gemm_mfma(int qtype, const void* w, int64_t row_bytes, const float* x, float* y, int rows, int cols,
+                      int batch, hipStream_t s);
+
 }  // namespace zl
