@@ -20,6 +20,7 @@
 // Fused forms: GeGLU pairs each gate row with its up row and writes gelu(g) * u (the
 // elementwise kernels' gelu_fast); QKV treats the three matrices as one row space.
 #include <algorithm>
+#include <type_traits>
 
 #include "zl_common.h"
 #include "zl_host.h"
@@ -817,6 +818,202 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(QT
     }
 }
 
+// Batch-1 Q4_0 products, one 32-column block per lane and step: the loops above issue two
+// loads per 8-column group (the 16-bit scale and 4 quant bytes, every other one 2-byte
+// aligned), and at decode sizes that instruction stream, not HBM, sets the rate (measured
+// with the arithmetic removed: 262144 x 2560 in 97 us against 82 us with every quant load
+// 4-byte aligned). Here a lane takes the whole 18-byte block with two dword-aligned loads
+// (16 + 4 bytes: the 20-byte window at 18b for even b, at 18b - 2 for odd b, so with an even
+// block count per row both ends stay inside the row) and picks the scale and the 16 quant
+// bytes out of the window with byte permutes.
+//
+// Layout: LPR lanes per row (16, 32 or 64) and 64 / LPR row sets of RW rows per wave; lane i
+// of a set takes blocks i, i + LPR, ... (bpl <= kQ4bMaxB of them) of each of its rows, every
+// weight load of the wave issued before any arithmetic (one memory round trip per wave).
+// x is staged once per workgroup in LDS, 36 floats per 32-column block (the padding keeps
+// the 16 lanes of a set, which read consecutive blocks, on distinct banks); each lane reads
+// its blocks' x there once and applies them to all its rows. Row sums: LPR-lane butterfly.
+constexpr int kQ4bMaxB = 6;
+constexpr int kQ4bXStride = 36;
+constexpr int kQ4bXMax = 12;  // x float4 per thread: cols <= 12288
+#ifndef ZL_GEMV_Q4B
+#define ZL_GEMV_Q4B 1
+#endif
+#ifndef ZL_GEMV_Q4B_WAVES
+#define ZL_GEMV_Q4B_WAVES 1024
+#endif
+typedef u32x4 u32x4_a4 __attribute__((aligned(4)));
+typedef uint32_t u32_a4 __attribute__((aligned(4)));
+
+struct Q4Win {
+    u32x4 a;     // window bytes 0..15
+    uint32_t e;  // window bytes 16..19
+};
+
+// sum over the block's 32 columns of q_j * x_j (q_j the stored nibble), x the block's 32
+// values from LDS (xs: 36-float stride slot), and the block's f32 scale; returns
+// d * (sum - 8 * sum x) (math.zig:304-305).
+__device__ __forceinline__ float q4b_dot(const Q4Win& w, bool odd, const f32x4 (&xl)[4], const f32x4 (&xh)[4],
+                                         float sx) {
+    const uint32_t sel = odd ? 0x07060504u : 0x05040302u;  // quant bytes 4..19 / 2..17
+    const uint32_t q0 = __builtin_amdgcn_perm(w.a.y, w.a.x, sel);
+    const uint32_t q1 = __builtin_amdgcn_perm(w.a.z, w.a.y, sel);
+    const uint32_t q2 = __builtin_amdgcn_perm(w.a.w, w.a.z, sel);
+    const uint32_t q3 = __builtin_amdgcn_perm(w.e, w.a.w, sel);
+    const uint32_t d16 = __builtin_amdgcn_perm(0u, w.a.x, odd ? 0x0c0c0302u : 0x0c0c0100u);
+    const uint32_t q[4] = {q0, q1, q2, q3};
+    float t = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t lo = mask_bytes(q[i], 0x0f0f0f0fu);       // columns 4i .. 4i+3
+        const uint32_t hi = mask_bytes(q[i] >> 4, 0x0f0f0f0fu);  // columns 16+4i .. 16+4i+3
+        t = i == 0 ? (float)(lo & 0xff) * xl[0].x : fmaf((float)(lo & 0xff), xl[i].x, t);
+        t = fmaf((float)((lo >> 8) & 0xff), xl[i].y, t);
+        t = fmaf((float)((lo >> 16) & 0xff), xl[i].z, t);
+        t = fmaf((float)(lo >> 24), xl[i].w, t);
+        t = fmaf((float)(hi & 0xff), xh[i].x, t);
+        t = fmaf((float)((hi >> 8) & 0xff), xh[i].y, t);
+        t = fmaf((float)((hi >> 16) & 0xff), xh[i].z, t);
+        t = fmaf((float)(hi >> 24), xh[i].w, t);
+    }
+    return h2f(d16) * fmaf(-8.0f, sx, t);
+}
+
+template <int MODE, int LPR, int RW, int BPL>
+__global__ __launch_bounds__(kGemvThreads) void k_gemv_q4b(GemvArgs a) {
+    constexpr int NM = MODE == GV_GEGLU ? 2 : 1;
+    constexpr int SETS = kWave / LPR;
+    extern __shared__ __attribute__((aligned(16))) float s_xq[];
+    const int lane = threadIdx.x & 63;
+    const int wv = threadIdx.x >> 6;
+    const int li = lane % LPR, set = lane / LPR;
+    const int row0 = ((blockIdx.x * kGemvWaves + wv) * SETS + set) * RW;
+    // x first (its loads complete before the weights' do): up to kQ4bXMax float4 per thread
+    const int n4 = a.cols / 4;
+    f32x4 xv[kQ4bXMax];
+#pragma unroll
+    for (int k = 0; k < kQ4bXMax; ++k) {
+        const int i = (int)threadIdx.x + k * kGemvThreads;
+        if (i < n4) xv[k] = ldf4(a.x + 4 * i);
+    }
+    // Row pointers: the segment of each row by selects over the (uniform) segment fields, so
+    // no per-lane indexed read of the arguments.
+    const unsigned char* wrow[RW][NM];
+    float* yrow[RW];
+    const int r0 = a.seg[0].rows, r1 = a.nseg > 1 ? a.seg[1].rows : 0;
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+        const bool ok = row0 + r < a.total_rows;
+        const int R = ok ? row0 + r : a.total_rows - 1;  // past the end: the last row, not written
+        const bool s0 = R < r0, s1 = !s0 && R - r0 < r1;
+        const int Rs = s0 ? R : s1 ? R - r0 : R - r0 - r1;
+        const unsigned char* wb = s0 ? a.seg[0].w : s1 ? a.seg[1].w : a.seg[2].w;
+        float* yb = s0 ? a.seg[0].y : s1 ? a.seg[1].y : a.seg[2].y;
+        wrow[r][0] = wb + (int64_t)Rs * a.row_bytes;
+        if constexpr (NM == 2) wrow[r][1] = a.w_up + (int64_t)Rs * a.row_bytes;
+        yrow[r] = ok ? yb + Rs : nullptr;
+    }
+    Q4Win w[BPL][RW][NM];
+#pragma unroll
+    for (int j = 0; j < BPL; ++j) {
+        const uint32_t off = ((uint32_t)(li + LPR * j) * 18u) & ~3u;
+#pragma unroll
+        for (int r = 0; r < RW; ++r)
+#pragma unroll
+            for (int m = 0; m < NM; ++m) {
+                w[j][r][m].a = *reinterpret_cast<const u32x4_a4*>(wrow[r][m] + off);
+                w[j][r][m].e = *reinterpret_cast<const u32_a4*>(wrow[r][m] + off + 16u);
+            }
+    }
+    // x into LDS: float4 i of block i / 8 at slot offset 4 * (i % 8)
+#pragma unroll
+    for (int k = 0; k < kQ4bXMax; ++k) {
+        const int i = (int)threadIdx.x + k * kGemvThreads;
+        if (i < n4) *reinterpret_cast<f32x4*>(s_xq + (i >> 3) * kQ4bXStride + 4 * (i & 7)) = xv[k];
+    }
+    __syncthreads();
+    float acc[RW][NM];
+#pragma unroll
+    for (int r = 0; r < RW; ++r)
+#pragma unroll
+        for (int m = 0; m < NM; ++m) acc[r][m] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < BPL; ++j) {
+        const int b = li + LPR * j;
+        const float* xs = s_xq + b * kQ4bXStride;
+        f32x4 xl[4], xh[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            xl[i] = *reinterpret_cast<const f32x4*>(xs + 4 * i);
+            xh[i] = *reinterpret_cast<const f32x4*>(xs + 16 + 4 * i);
+        }
+        float sx = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sx += ((xl[i].x + xl[i].y) + (xl[i].z + xl[i].w)) + ((xh[i].x + xh[i].y) + (xh[i].z + xh[i].w));
+        const bool odd = b & 1;
+#pragma unroll
+        for (int r = 0; r < RW; ++r)
+#pragma unroll
+            for (int m = 0; m < NM; ++m) acc[r][m] += q4b_dot(w[j][r][m], odd, xl, xh, sx);
+    }
+#pragma unroll
+    for (int r = 0; r < RW; ++r)
+#pragma unroll
+        for (int m = 0; m < NM; ++m) acc[r][m] = group_sum<LPR>(acc[r][m]);
+    if (li == 0) {
+#pragma unroll
+        for (int r = 0; r < RW; ++r) {
+            if (!yrow[r]) continue;
+            float out = acc[r][0];
+            if constexpr (MODE == GV_GEGLU) out = gelu_fast(acc[r][0]) * acc[r][1];
+            *yrow[r] = out;
+        }
+    }
+}
+
+// Launches k_gemv_q4b when the product suits it (batch 1, Q4_0, blocks per row a multiple of
+// 16 with at most kQ4bMaxB per lane at 64 lanes per row, x within 64 KB of LDS); returns
+// false otherwise. LPR: the fewest lanes per row that take every block in kQ4bMaxB steps,
+// more while the grid has fewer than ZL_GEMV_Q4B_WAVES waves; RW = 2 rows per set from
+// 4 * ZL_GEMV_Q4B_WAVES waves.
+template <int QT, int MODE>
+static bool launch_q4b(const GemvArgs& a, hipStream_t s) {
+    if (!ZL_GEMV_Q4B || QT != HIP_BRIDGE_Q4_0 || a.batch != 1) return false;
+    const int nblk = a.cols / 32;
+    if (a.cols % 512 != 0) return false;
+    const size_t lds = (size_t)nblk * kQ4bXStride * sizeof(float);
+    if (a.cols > 4 * kQ4bXMax * kGemvThreads || lds > 65536) return false;
+    int lpr = 0;
+    for (int l : {16, 32, 64})
+        if (nblk % l == 0 && nblk / l <= kQ4bMaxB) {
+            lpr = l;
+            break;
+        }
+    if (!lpr) return false;
+    auto waves = [&](int l, int rw) { return cdiv(a.total_rows, (int64_t)(kWave / l) * rw); };
+    while (lpr < 64 && waves(lpr, 1) < ZL_GEMV_Q4B_WAVES && nblk % (2 * lpr) == 0) lpr *= 2;
+    const int rw = waves(lpr, 2) >= 4 * ZL_GEMV_Q4B_WAVES ? 2 : 1;
+    const int bpl = nblk / lpr;
+    const unsigned grid = (unsigned)cdiv(waves(lpr, rw), (int64_t)kGemvWaves);
+    auto go = [&](auto lpr_c, auto rw_c) {
+        constexpr int L = decltype(lpr_c)::value, RW = decltype(rw_c)::value;
+        switch (bpl) {
+            case 1: k_gemv_q4b<MODE, L, RW, 1><<<grid, kGemvThreads, lds, s>>>(a); break;
+            case 2: k_gemv_q4b<MODE, L, RW, 2><<<grid, kGemvThreads, lds, s>>>(a); break;
+            case 3: k_gemv_q4b<MODE, L, RW, 3><<<grid, kGemvThreads, lds, s>>>(a); break;
+            case 4: k_gemv_q4b<MODE, L, RW, 4><<<grid, kGemvThreads, lds, s>>>(a); break;
+            case 5: k_gemv_q4b<MODE, L, RW, 5><<<grid, kGemvThreads, lds, s>>>(a); break;
+            default: k_gemv_q4b<MODE, L, RW, 6><<<grid, kGemvThreads, lds, s>>>(a); break;
+        }
+    };
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    if (lpr == 16) rw == 2 ? go(std::integral_constant<int, 16>{}, I2{}) : go(std::integral_constant<int, 16>{}, I1{});
+    else if (lpr == 32) rw == 2 ? go(std::integral_constant<int, 32>{}, I2{}) : go(std::integral_constant<int, 32>{}, I1{});
+    else rw == 2 ? go(std::integral_constant<int, 64>{}, I2{}) : go(std::integral_constant<int, 64>{}, I1{});
+    return true;
+}
+
 // Any alignment / column count: one workgroup per row, scalar dequantisation per element.
 template <int QT>
 __device__ __forceinline__ float w_elem(const unsigned char* row, int c) {
@@ -947,6 +1144,8 @@ static void launch_vec(const GemvArgs& a, hipStream_t s) {
             constexpr int RP = F > 0 ? std::max(1, F / H) : 2 / H;
             k_gemv<QT, RP, 1, MODE><<<(unsigned)cdiv(a.total_rows, RP), kGemvThreads, 0, s>>>(a);
         }
+    } else if (launch_q4b<QT, MODE>(a, s)) {
+        // launched: batch-1 Q4_0 with 512-column multiples
     } else if (MODE == GV_PLAIN && a.batch == 1 && a.total_rows >= kGemvWaveRowsMin && a.cols <= kGemvWaveColsMax &&
                QT != HIP_BRIDGE_F16 && QT != HIP_BRIDGE_BF16 && QT != HIP_BRIDGE_F32) {
         // (k_gemv_w is instantiated for these cases only)

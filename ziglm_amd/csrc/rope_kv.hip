@@ -143,15 +143,10 @@ __global__ __launch_bounds__(256) void k_qk_fused(QkArgs a) {
         return a.v != nullptr && row >= 0;
     };
 
-    // Issue the first head row's HBM loads and the weights, then evaluate the token's
-    // cos/sin table (no memory operands) while they are in flight.
+    // Issue the weight loads (L2 hits after the first tokens: the barrier below waits on
+    // them) and then the first head row's HBM loads, and evaluate the token's cos/sin table
+    // (no memory operands) while they are in flight.
     const int ti = threadIdx.x;
-    u32x4 ra = {0, 0, 0, 0}, rb = {0, 0, 0, 0};
-    if (gslot < HR && active(gslot)) {
-        const T* src = src_of(gslot);
-        ra = lds16(src + c0 * E);
-        rb = lds16(src + c1 * E);
-    }
     // The norm weights go to LDS (read there per head, not held in registers): one f32x4
     // per thread (threads [0, D/4) stage wq, [D/4, D/2) stage wk; D <= 256 fits 256 threads).
     const bool has_wq = a.wq != nullptr, has_wk = a.wk != nullptr;
@@ -159,6 +154,12 @@ __global__ __launch_bounds__(256) void k_qk_fused(QkArgs a) {
     const int wi = ti < D / 4 ? ti : ti - D / 4;  // thread -> float4 index in its vector
     const bool stage_q = ti < D / 4, stage_k = ti >= D / 4 && ti < D / 2;
     if ((stage_q && has_wq) || (stage_k && has_wk)) wstage = ldf4((stage_q ? a.wq : a.wk) + 4 * wi);
+    u32x4 ra = {0, 0, 0, 0}, rb = {0, 0, 0, 0};
+    if (gslot < HR && active(gslot)) {
+        const T* src = src_of(gslot);
+        ra = lds16(src + c0 * E);
+        rb = lds16(src + c1 * E);
+    }
     if (a.do_rope && ti < a.half) {
         const float theta = ((float)p * a.freq_scale) / rope_denom(ti, 2 * a.half, a.log2_base);
         rope_sincos(theta, &s_sin[ti], &s_cos[ti]);
