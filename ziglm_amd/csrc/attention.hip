@@ -29,7 +29,11 @@
 
 namespace zl {
 
-constexpr int kAttnThreads = 256;
+#ifndef ZL_ATTN_THREADS
+#define ZL_ATTN_THREADS 256
+#endif
+constexpr int kAttnThreads = ZL_ATTN_THREADS;  // k_attn workgroup
+constexpr int kMergeThreads = 256;             // k_attn_merge workgroup
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct AttnArgs {
@@ -78,13 +82,9 @@ __device__ __forceinline__ void attn_range(const AttnArgs& a, int b, int& start,
 // Positions per split for a sequence of `len` positions: the sequence's own length is cut
 // into nsplit equal chunks (the host sized nsplit for the longest possible sequence), no
 // chunk shorter than kChunkMin, so a short context spreads over fewer splits and the rest
-// stay empty. Returns the number of non-empty splits in `used`. Measured on MI355X (us per
-// call with the merge; floor 32 / 64 / 128 / 256): Gemma-4B heads (8/4 x 256), one token at
-// position 27259 of a 32768-row cache: 47.6 / 45.7 / 50.0 / 43.6; the same at position 100:
-// 9.8 / 11.2 / 17.9 / 13.2; 8/1 x 512 at position 1234 of 4096: 12.2 / 13.1 / 15.1 / 22.3;
-// 8/1 x 256, window 512: 8.0 / 8.3 / 10.0 / 13.5.
+// stay empty. Returns the number of non-empty splits in `used`.
 #ifndef ZL_ATTN_CHUNK_MIN
-#define ZL_ATTN_CHUNK_MIN 32
+#define ZL_ATTN_CHUNK_MIN 8
 #endif
 constexpr int kChunkMin = ZL_ATTN_CHUNK_MIN;
 __device__ __forceinline__ int split_chunk(const AttnArgs& a, int len, int& used) {
@@ -190,6 +190,18 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
         }
     };
     if (nstep > 0) load_step(t0 + slot);
+    // QK mode: the split holding the token's own position requests the raw K / V rows that
+    // position is formed from now (used after the loop), not after the loop.
+    const bool own_here = own && t0 <= last && last < t1;  // block-uniform
+    f32x4 rk0{}, rk1{}, rv0{}, rv1{};
+    if (own_here) {
+        const float* kr = a.qk_k + ((int64_t)b * a.nkv + kvh) * D + li * 8;
+        const float* vr = a.qk_v + ((int64_t)b * a.nkv + kvh) * D + li * 8;
+        rk0 = ldf4(kr);
+        rk1 = ldf4(kr + 4);
+        rv0 = ldf4(vr);
+        rv1 = ldf4(vr + 4);
+    }
 
     if constexpr (QK) {
         // cos / sin of the token's position for the rotary pairs, while the q loads fly
@@ -267,14 +279,11 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
         }
     }
     if constexpr (QK) {
-        if (own && t0 <= last && last < t1) {  // block-uniform: the split holding the token
+        if (own_here) {  // block-uniform: the split holding the token
             // Every lane group forms the row (uniform code); slot 0 folds it in and, in the
             // first head group's workgroup, writes it to the cache.
-            const float* kr = a.qk_k + ((int64_t)b * a.nkv + kvh) * D + li * 8;
-            const float* vr = a.qk_v + ((int64_t)b * a.nkv + kvh) * D + li * 8;
-            const f32x4 k0 = ldf4(kr), k1 = ldf4(kr + 4), v0 = ldf4(vr), v1 = ldf4(vr + 4);
-            float kn[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
-            float vn[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+            float kn[8] = {rk0.x, rk0.y, rk0.z, rk0.w, rk1.x, rk1.y, rk1.z, rk1.w};
+            float vn[8] = {rv0.x, rv0.y, rv0.z, rv0.w, rv1.x, rv1.y, rv1.z, rv1.w};
             float fk[8];
             norm_factors(a.qk_wk, fk);
             if (a.qk_wk) qk_norm8<LT>(kn, D, a.qk_eps, fk);
@@ -365,9 +374,9 @@ constexpr int kMergePre = 8;
 __device__ __forceinline__ float bldf(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
 }
-__global__ __launch_bounds__(kAttnThreads) void k_attn_merge(AttnArgs a) {
-    constexpr int NW = kAttnThreads / kWave;
-    constexpr int PER = kMaxSplit / kAttnThreads;  // (m, l) pairs per thread
+__global__ __launch_bounds__(kMergeThreads) void k_attn_merge(AttnArgs a) {
+    constexpr int NW = kMergeThreads / kWave;
+    constexpr int PER = kMaxSplit / kMergeThreads;  // (m, l) pairs per thread
     __shared__ float s_c[kMaxSplit];
     __shared__ float s_red[NW];
     __shared__ float s_part[NW][kMergeCols];
@@ -390,7 +399,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_merge(AttnArgs a) {
     float mv[PER], lv[PER], pre[kMergePre];
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
-        const uint32_t o = (uint32_t)(tid + k * kAttnThreads) * rowb;
+        const uint32_t o = (uint32_t)(tid + k * kMergeThreads) * rowb;
         mv[k] = bldf(rs, o);
         lv[k] = bldf(rs, o + 4u);
     }
@@ -399,7 +408,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_merge(AttnArgs a) {
     float mx = -INFINITY;
 #pragma unroll
     for (int k = 0; k < PER; ++k)
-        if (tid + k * kAttnThreads < used) mx = fmaxf(mx, mv[k]);
+        if (tid + k * kMergeThreads < used) mx = fmaxf(mx, mv[k]);
 #pragma unroll
     for (int o = 1; o < kWave; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
     if (lane == 0) s_red[wv] = mx;
@@ -409,7 +418,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_merge(AttnArgs a) {
     float lsum = 0.0f;
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
-        const int sp = tid + k * kAttnThreads;
+        const int sp = tid + k * kMergeThreads;
         if (sp < used) {
             const float c = M == -INFINITY ? 0.0f : exp2f((mv[k] - M) * kLog2e);
             s_c[sp] = c;
@@ -477,15 +486,24 @@ static void choose_heads(AttnArgs& a, int es) {
     a.hg = a.gq / gw;
 }
 
-// Splits per sequence: enough that batch * n_kv_heads * head groups * splits fills the chip
-// (~2048 workgroups) and no split exceeds 1024 positions of the longest possible sequence
-// (sequences of a batch differ in length: short splits keep the long ones from leaving a
-// tail), at most one per kChunkMin positions, at most kMaxSplit. The actual lengths are on
-// the device: each sequence cuts its own length into that many chunks (split_chunk).
+// Splits per sequence: enough that batch * n_kv_heads * head groups * splits reaches
+// ZL_ATTN_TARGET_WG workgroups and no split exceeds 1024 positions of the longest possible
+// sequence (sequences of a batch differ in length: short splits keep the long ones from
+// leaving a tail), at most one per kChunkMin positions, at most kMaxSplit. The actual lengths
+// are on the device: each sequence cuts its own length into that many chunks (split_chunk).
+// A decode workgroup is latency-bound (its K/V rows, a few tens of KB, arrive at the rate one
+// CU sustains with 4 waves), so more, shorter splits help until the merge's share grows.
+// Measured on MI355X, Gemma-4B heads (8/4 x 256, f32 cache of 4096 rows), one token, the
+// QK-fused call with its merge, K/V cold (34 layers' caches in rotation), us per call at
+// positions 200 / 1250 / 4000: 2048 workgroups, 32-position floor 10.8 / 14.1 / 18.0; 512
+// and 16: 9.9 / 13.0 / 14.7; 512 and 8: 9.0 / 13.0 / 14.7; 1024 and 16: 11.7 / 14.4 / 17.8.
+#ifndef ZL_ATTN_TARGET_WG
+#define ZL_ATTN_TARGET_WG 512
+#endif
 static void choose_split(AttnArgs& a, size_t ws_bytes) {
     const int len = a.window > 0 ? std::min(a.window, a.max_len) : a.max_len;
     const int64_t groups = (int64_t)a.batch * a.nkv * a.hg;
-    const int64_t want = std::max<int64_t>(cdiv(2048, groups), cdiv(len, 1024));
+    const int64_t want = std::max<int64_t>(cdiv(ZL_ATTN_TARGET_WG, groups), cdiv(len, 1024));
     int nsplit = (int)std::max<int64_t>(1, std::min<int64_t>({cdiv(len, kChunkMin), want, (int64_t)kMaxSplit}));
     const size_t need = (size_t)a.batch * a.nh * nsplit * (a.D + 2) * sizeof(float);
     if (!a.ws || need > ws_bytes) nsplit = 1;
@@ -538,7 +556,7 @@ static void launch_attn(int kv_dtype, AttnArgs& a, size_t ws_bytes, hipStream_t 
         else launch_g<uint16_t, 512>(a, qk, s);
     }
     if (a.nsplit > 1)
-        k_attn_merge<<<dim3((unsigned)((int64_t)a.batch * a.nh), (unsigned)(a.D / kMergeCols)), kAttnThreads, 0, s>>>(a);
+        k_attn_merge<<<dim3((unsigned)((int64_t)a.batch * a.nh), (unsigned)(a.D / kMergeCols)), kMergeThreads, 0, s>>>(a);
     check_launch();
 }
 

@@ -19,6 +19,15 @@
 // sums are reduced within the wave (DPP / permlane) and across the 4 waves through LDS.
 // Fused forms: GeGLU pairs each gate row with its up row and writes gelu(g) * u (the
 // elementwise kernels' gelu_fast); QKV treats the three matrices as one row space.
+// Batch-1 Q4_0 products with 512-column multiples take k_gemv_q4b instead (one 18-byte
+// block per lane from two dword-aligned loads, every weight load of a wave issued at once,
+// x staged in LDS; with or without the input prologue); the loops above serve every other
+// type, shape and batch. Measured at the Gemma-4B decode shapes (us, weights cold): QKV
+// 4096 x 2560 5.4 -> 4.5, O 2560 x 2048 3.5 -> 3.4, gate.up 2 x 10240 x 2560 11.8 -> 10.0,
+// down 2560 x 10240 8.4 -> 7.3, LM head 262144 x 2560 110 -> 94; the same-size read-only
+// streams take 2.3, 1.9, 6.0, 3.7 and 58 us. Without the dequantisation arithmetic the block
+// kernel takes 3.6, 2.9, 7.8, 5.5 and 62 us: at Q4_0's 2.5 VALU instructions per weight
+// the larger products are issue-bound as much as memory-bound.
 #include <algorithm>
 #include <type_traits>
 
@@ -836,6 +845,7 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(QT
 constexpr int kQ4bMaxB = 6;
 constexpr int kQ4bXStride = 36;
 constexpr int kQ4bXMax = 12;  // x float4 per thread: cols <= 12288
+constexpr int kQ4bProChunks = 4;  // PRO operands: cols <= 4096
 #ifndef ZL_GEMV_Q4B
 #define ZL_GEMV_Q4B 1
 #endif
@@ -879,22 +889,100 @@ __device__ __forceinline__ float q4b_dot(const Q4Win& w, bool odd, const f32x4 (
     return h2f(d16) * fmaf(-8.0f, sx, t);
 }
 
-template <int MODE, int LPR, int RW, int BPL>
+// PRO prologue of the block kernel, in two phases around the weight loads: q4b_pro_load
+// issues the operand loads (x, r, r's weights, the norm weights: K float4 each per thread,
+// range-checked), q4b_pro_finish forms the input vector in registers with the arithmetic of
+// gemv_prologue (workgroup 0 writes x1 and the input when asked).
+template <int K>
+__device__ __forceinline__ void q4b_pro_load(const GemvArgs& a, f32x4 (&xv)[K], f32x4 (&rv)[K], f32x4 (&rwv)[K],
+                                             f32x4 (&wv)[K]) {
+    const GemvPro& p = a.pro;
+    const uint32_t nb = (uint32_t)a.cols * 4u;
+    const auto rs_x = buf_rsrc(a.x, nb);
+    const auto rs_r = buf_rsrc(p.r, p.r ? nb : 0u);
+    const auto rs_rw = buf_rsrc(p.r_w, p.mode == GP_NORM && p.r && p.r_w ? nb : 0u);
+    const auto rs_w = buf_rsrc(p.w, p.mode == GP_NORM && p.w ? nb : 0u);
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const uint32_t o = (uint32_t)(threadIdx.x + k * kGemvThreads) * 16u;
+        xv[k] = bldf4(rs_x, o);
+        rv[k] = bldf4(rs_r, o);
+        rwv[k] = bldf4(rs_rw, o);
+        wv[k] = bldf4(rs_w, o);
+    }
+}
+template <int K>
+__device__ __forceinline__ void q4b_pro_finish(const GemvArgs& a, f32x4 (&xv)[K], const f32x4 (&rv)[K],
+                                               const f32x4 (&rwv)[K], const f32x4 (&wv)[K], float* s_red) {
+    const GemvPro& p = a.pro;
+    const int n4 = a.cols / 4;
+    const int tid = threadIdx.x;
+    if (p.mode == GP_GEGLU) {
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            xv[k].x = gelu_fast(xv[k].x) * rv[k].x;
+            xv[k].y = gelu_fast(xv[k].y) * rv[k].y;
+            xv[k].z = gelu_fast(xv[k].z) * rv[k].z;
+            xv[k].w = gelu_fast(xv[k].w) * rv[k].w;
+        }
+    } else {
+        const bool wr = p.x_out && blockIdx.x == 0;
+        float inv1 = 0.0f;
+        if (p.r && p.r_w) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int k = 0; k < K; ++k)
+                if (tid + k * kGemvThreads < n4) ss = sumsq4(rv[k], ss);
+            inv1 = rms_inv(gemv_block_sum(ss, s_red), a.cols, p.eps);
+        }
+        float ss = 0.0f;
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            const int c = tid + k * kGemvThreads;
+            if (c < n4) {
+                xv[k] = pro_x1(p, xv[k], rv[k], rwv[k], inv1);
+                if (wr) *reinterpret_cast<f32x4*>(p.x_out + 4 * c) = xv[k];
+                ss = sumsq4(xv[k], ss);
+            }
+        }
+        if (p.w) {
+            const float inv2 = rms_inv(gemv_block_sum(ss, s_red), a.cols, p.eps);
+#pragma unroll
+            for (int k = 0; k < K; ++k) xv[k] = norm_w4(xv[k], inv2, wv[k], p.uo);
+        }
+    }
+    if (p.xb_out && blockIdx.x == 0) {
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            const int c = tid + k * kGemvThreads;
+            if (c < n4) *reinterpret_cast<f32x4*>(p.xb_out + 4 * c) = xv[k];
+        }
+    }
+}
+
+template <int MODE, int LPR, int RW, int BPL, bool PRO>
 __global__ __launch_bounds__(kGemvThreads) void k_gemv_q4b(GemvArgs a) {
     constexpr int NM = MODE == GV_GEGLU ? 2 : 1;
     constexpr int SETS = kWave / LPR;
+    constexpr int XK = PRO ? kQ4bProChunks : kQ4bXMax;  // x float4 per thread
     extern __shared__ __attribute__((aligned(16))) float s_xq[];
+    __shared__ float s_red[kGemvWaves];
     const int lane = threadIdx.x & 63;
     const int wv = threadIdx.x >> 6;
     const int li = lane % LPR, set = lane / LPR;
     const int row0 = ((blockIdx.x * kGemvWaves + wv) * SETS + set) * RW;
-    // x first (its loads complete before the weights' do): up to kQ4bXMax float4 per thread
+    // x (PRO: the prologue's operands) first: its loads complete before the weights' do, so
+    // staging it waits on it alone
     const int n4 = a.cols / 4;
-    f32x4 xv[kQ4bXMax];
+    f32x4 xv[XK], rv[PRO ? XK : 1], rwv[PRO ? XK : 1], wnv[PRO ? XK : 1];
+    if constexpr (PRO) {
+        q4b_pro_load<XK>(a, xv, rv, rwv, wnv);
+    } else {
 #pragma unroll
-    for (int k = 0; k < kQ4bXMax; ++k) {
-        const int i = (int)threadIdx.x + k * kGemvThreads;
-        if (i < n4) xv[k] = ldf4(a.x + 4 * i);
+        for (int k = 0; k < XK; ++k) {
+            const int i = (int)threadIdx.x + k * kGemvThreads;
+            if (i < n4) xv[k] = ldf4(a.x + 4 * i);
+        }
     }
     // Row pointers: the segment of each row by selects over the (uniform) segment fields, so
     // no per-lane indexed read of the arguments.
@@ -925,9 +1013,10 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_q4b(GemvArgs a) {
                 w[j][r][m].e = *reinterpret_cast<const u32_a4*>(wrow[r][m] + off + 16u);
             }
     }
-    // x into LDS: float4 i of block i / 8 at slot offset 4 * (i % 8)
+    // the input into LDS: float4 i of block i / 8 at slot offset 4 * (i % 8)
+    if constexpr (PRO) q4b_pro_finish<XK>(a, xv, rv, rwv, wnv, s_red);
 #pragma unroll
-    for (int k = 0; k < kQ4bXMax; ++k) {
+    for (int k = 0; k < XK; ++k) {
         const int i = (int)threadIdx.x + k * kGemvThreads;
         if (i < n4) *reinterpret_cast<f32x4*>(s_xq + (i >> 3) * kQ4bXStride + 4 * (i & 7)) = xv[k];
     }
@@ -976,13 +1065,13 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_q4b(GemvArgs a) {
 // false otherwise. LPR: the fewest lanes per row that take every block in kQ4bMaxB steps,
 // more while the grid has fewer than ZL_GEMV_Q4B_WAVES waves; RW = 2 rows per set from
 // 4 * ZL_GEMV_Q4B_WAVES waves.
-template <int QT, int MODE>
+template <int QT, int MODE, bool PRO>
 static bool launch_q4b(const GemvArgs& a, hipStream_t s) {
     if (!ZL_GEMV_Q4B || QT != HIP_BRIDGE_Q4_0 || a.batch != 1) return false;
     const int nblk = a.cols / 32;
     if (a.cols % 512 != 0) return false;
     const size_t lds = (size_t)nblk * kQ4bXStride * sizeof(float);
-    if (a.cols > 4 * kQ4bXMax * kGemvThreads || lds > 65536) return false;
+    if (a.cols > 4 * (PRO ? kQ4bProChunks : kQ4bXMax) * kGemvThreads || lds > 65536) return false;
     int lpr = 0;
     for (int l : {16, 32, 64})
         if (nblk % l == 0 && nblk / l <= kQ4bMaxB) {
@@ -998,12 +1087,12 @@ static bool launch_q4b(const GemvArgs& a, hipStream_t s) {
     auto go = [&](auto lpr_c, auto rw_c) {
         constexpr int L = decltype(lpr_c)::value, RW = decltype(rw_c)::value;
         switch (bpl) {
-            case 1: k_gemv_q4b<MODE, L, RW, 1><<<grid, kGemvThreads, lds, s>>>(a); break;
-            case 2: k_gemv_q4b<MODE, L, RW, 2><<<grid, kGemvThreads, lds, s>>>(a); break;
-            case 3: k_gemv_q4b<MODE, L, RW, 3><<<grid, kGemvThreads, lds, s>>>(a); break;
-            case 4: k_gemv_q4b<MODE, L, RW, 4><<<grid, kGemvThreads, lds, s>>>(a); break;
-            case 5: k_gemv_q4b<MODE, L, RW, 5><<<grid, kGemvThreads, lds, s>>>(a); break;
-            default: k_gemv_q4b<MODE, L, RW, 6><<<grid, kGemvThreads, lds, s>>>(a); break;
+            case 1: k_gemv_q4b<MODE, L, RW, 1, PRO><<<grid, kGemvThreads, lds, s>>>(a); break;
+            case 2: k_gemv_q4b<MODE, L, RW, 2, PRO><<<grid, kGemvThreads, lds, s>>>(a); break;
+            case 3: k_gemv_q4b<MODE, L, RW, 3, PRO><<<grid, kGemvThreads, lds, s>>>(a); break;
+            case 4: k_gemv_q4b<MODE, L, RW, 4, PRO><<<grid, kGemvThreads, lds, s>>>(a); break;
+            case 5: k_gemv_q4b<MODE, L, RW, 5, PRO><<<grid, kGemvThreads, lds, s>>>(a); break;
+            default: k_gemv_q4b<MODE, L, RW, 6, PRO><<<grid, kGemvThreads, lds, s>>>(a); break;
         }
     };
     using I1 = std::integral_constant<int, 1>;
@@ -1122,7 +1211,9 @@ static void launch_vec(const GemvArgs& a, hipStream_t s) {
     constexpr int H = MODE == GV_GEGLU ? 2 : 1;
     const unsigned g8 = (unsigned)cdiv(a.total_rows, 8 / H), g4 = (unsigned)cdiv(a.total_rows, 4 / H),
                    g2 = (unsigned)cdiv(a.total_rows, 2 / H);
-    if (PRO) {  // batch 1; the input vector in dynamic LDS; at most kGemvProGrid workgroups
+    if (PRO && launch_q4b<QT, MODE, true>(a, s)) {
+        // launched: batch-1 Q4_0 block kernel with the prologue
+    } else if (PRO) {  // batch 1; the input vector in dynamic LDS; at most kGemvProGrid workgroups
         const size_t lds = (size_t)a.cols * sizeof(float);
         const unsigned cap = kGemvProGrid;
         if (QT == HIP_BRIDGE_Q4_0 && a.total_rows >= 16384)
@@ -1144,7 +1235,7 @@ static void launch_vec(const GemvArgs& a, hipStream_t s) {
             constexpr int RP = F > 0 ? std::max(1, F / H) : 2 / H;
             k_gemv<QT, RP, 1, MODE><<<(unsigned)cdiv(a.total_rows, RP), kGemvThreads, 0, s>>>(a);
         }
-    } else if (launch_q4b<QT, MODE>(a, s)) {
+    } else if (launch_q4b<QT, MODE, false>(a, s)) {
         // launched: batch-1 Q4_0 with 512-column multiples
     } else if (MODE == GV_PLAIN && a.batch == 1 && a.total_rows >= kGemvWaveRowsMin && a.cols <= kGemvWaveColsMax &&
                QT != HIP_BRIDGE_F16 && QT != HIP_BRIDGE_BF16 && QT != HIP_BRIDGE_F32) {

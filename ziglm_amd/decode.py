@@ -316,15 +316,17 @@ def qk_attention_ok(ly):
 
 def default_fuse(model):
     """Products that take their norms in a prologue by default. Every workgroup of a
-    prologue product recomputes the input (norm statistics included), so the prologue pays
-    only where the product has few workgroups: the per-layer-embedding gate (256 rows) and
-    projection (whose prologue is gelu(gate) * ple, no statistics). "attn" puts the QK-norm /
-    RoPE / KV append inside the attention launch (one launch fewer per layer). Measured,
-    graph decode step, us per token (E2B-shaped 35 x 1536 / Gemma-4B-shaped 34 x 2560), with
-    "attn" in every set: PLE 1737 / -; + QKV 1754 / 1886-1892; + gate.up 1867 / 2017-2025;
-    + LM head 1806-1812 / 1904-1909; + all three 1939-1942 / -; none of the three
-    - / 1849-1850. Before "attn": no prologues 2103 / 2071, PLE 2065 / -."""
-    return {"ple", "attn"}
+    prologue product recomputes the input (norm statistics included) from x, the pending
+    branch and both norm weights: worth it where that replaces a launch and the product's
+    workgroups are few against its weight stream -- the QKV product (the previous layer's
+    post-FFN norm + add and this layer's input norm), the per-layer-embedding gate (256
+    rows) and projection (whose prologue is gelu(gate) * ple, no statistics). "attn" puts
+    the QK-norm / RoPE / KV append inside the attention launch (one launch fewer per layer).
+    Measured, graph decode step of the Gemma-4B-shaped model (34 x 2560, Q4_0), us per token,
+    with "ple" and "attn": 1588-1610 alone; + QKV 1520-1534; + gate.up 1598-1610; + QKV and
+    gate.up 1557; + those and the LM head 1582 (the gate.up product has 640 workgroups, each
+    reading 40 KB of prologue operands beside its 46 KB of weights)."""
+    return {"ple", "attn", "qkv"}
 
 
 def cache_bytes(model, max_seq):
