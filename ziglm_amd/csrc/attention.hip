@@ -52,6 +52,7 @@ struct AttnArgs {
     int batch, nh, nkv, D;
     int window;
     int nsplit;               // splits per sequence (split_chunk)
+    int chunk_min;            // shortest split (split_chunk)
     int gq;                   // query heads per kv head (nh / nkv)
     int hg;                   // workgroups per (token, kv head, split): each takes gq / hg heads
     float scale, softcap, inv_cap;
@@ -81,14 +82,13 @@ __device__ __forceinline__ void attn_range(const AttnArgs& a, int b, int& start,
 
 // Positions per split for a sequence of `len` positions: the sequence's own length is cut
 // into nsplit equal chunks (the host sized nsplit for the longest possible sequence), no
-// chunk shorter than kChunkMin, so a short context spreads over fewer splits and the rest
+// chunk shorter than a.chunk_min, so a short context spreads over fewer splits and the rest
 // stay empty. Returns the number of non-empty splits in `used`.
 #ifndef ZL_ATTN_CHUNK_MIN
 #define ZL_ATTN_CHUNK_MIN 8
 #endif
-constexpr int kChunkMin = ZL_ATTN_CHUNK_MIN;
 __device__ __forceinline__ int split_chunk(const AttnArgs& a, int len, int& used) {
-    const int chunk = max((len + a.nsplit - 1) / a.nsplit, kChunkMin);
+    const int chunk = max((len + a.nsplit - 1) / a.nsplit, a.chunk_min);
     used = len > 0 ? min(a.nsplit, (len + chunk - 1) / chunk) : 0;
     return chunk;
 }
@@ -489,14 +489,15 @@ static void choose_heads(AttnArgs& a, int es) {
 // Splits per sequence: enough that batch * n_kv_heads * head groups * splits reaches
 // ZL_ATTN_TARGET_WG workgroups and no split exceeds 1024 positions of the longest possible
 // sequence (sequences of a batch differ in length: short splits keep the long ones from
-// leaving a tail), at most one per kChunkMin positions, at most kMaxSplit. The actual lengths
+// leaving a tail), at most one per chunk_min positions, at most kMaxSplit. The actual lengths
 // are on the device: each sequence cuts its own length into that many chunks (split_chunk).
-// A decode workgroup is latency-bound (its K/V rows, a few tens of KB, arrive at the rate one
-// CU sustains with 4 waves), so more, shorter splits help until the merge's share grows.
-// Measured on MI355X, Gemma-4B heads (8/4 x 256, f32 cache of 4096 rows), one token, the
-// QK-fused call with its merge, K/V cold (34 layers' caches in rotation), us per call at
-// positions 200 / 1250 / 4000: 2048 workgroups, 32-position floor 10.8 / 14.1 / 18.0; 512
-// and 16: 9.9 / 13.0 / 14.7; 512 and 8: 9.0 / 13.0 / 14.7; 1024 and 16: 11.7 / 14.4 / 17.8.
+// A decode workgroup is latency-bound (its K/V rows arrive at the rate one CU sustains with
+// 4 waves), and every split adds to the merge. Measured on MI355X with K/V cold (caches
+// rotated past the Infinity Cache), Gemma-4B heads (8/4 x 256), one token, us per call with
+// the merge: f32 cache of 4096 rows, QK-fused call, positions 200 / 1250 / 4000: 2048
+// workgroups with a 32-position floor 10.8 / 14.1 / 18.0; 512 and 16: 9.9 / 13.0 / 14.7; 512
+// and 8: 9.0 / 13.0 / 14.7; 1024 and 16: 11.7 / 14.4 / 17.8. 32768-row cache, positions
+// ~U[0, 32767]: 60.8 us with 2048 workgroups, 53.5 with 512.
 #ifndef ZL_ATTN_TARGET_WG
 #define ZL_ATTN_TARGET_WG 512
 #endif
@@ -504,7 +505,9 @@ static void choose_split(AttnArgs& a, size_t ws_bytes) {
     const int len = a.window > 0 ? std::min(a.window, a.max_len) : a.max_len;
     const int64_t groups = (int64_t)a.batch * a.nkv * a.hg;
     const int64_t want = std::max<int64_t>(cdiv(ZL_ATTN_TARGET_WG, groups), cdiv(len, 1024));
-    int nsplit = (int)std::max<int64_t>(1, std::min<int64_t>({cdiv(len, kChunkMin), want, (int64_t)kMaxSplit}));
+    // shortest split: 8 positions in caches of up to 4096 rows, growing to 32 from 16384 rows
+    a.chunk_min = (int)std::min<int64_t>(std::max<int64_t>(len / 512, ZL_ATTN_CHUNK_MIN), 32);
+    int nsplit = (int)std::max<int64_t>(1, std::min<int64_t>({cdiv(len, a.chunk_min), want, (int64_t)kMaxSplit}));
     const size_t need = (size_t)a.batch * a.nh * nsplit * (a.D + 2) * sizeof(float);
     if (!a.ws || need > ws_bytes) nsplit = 1;
     a.nsplit = nsplit;
