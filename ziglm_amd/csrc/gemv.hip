@@ -844,8 +844,11 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(QT
 // its blocks' x there once and applies them to all its rows. Row sums: LPR-lane butterfly.
 constexpr int kQ4bMaxB = 6;
 constexpr int kQ4bXStride = 36;
-constexpr int kQ4bXMax = 12;  // x float4 per thread: cols <= 12288
-constexpr int kQ4bProChunks = 4;  // PRO operands: cols <= 4096
+constexpr int kQ4bMaxCols = 12288;    // x staged through registers: 12 float4 per thread at 256
+constexpr int kQ4bProMaxCols = 4096;  // PRO operands: 4 float4 each per thread at 256
+#ifndef ZL_GEMV_Q4B_PRO_WAVES
+#define ZL_GEMV_Q4B_PRO_WAVES 4
+#endif
 #ifndef ZL_GEMV_Q4B
 #define ZL_GEMV_Q4B 1
 #endif
@@ -893,7 +896,7 @@ __device__ __forceinline__ float q4b_dot(const Q4Win& w, bool odd, const f32x4 (
 // issues the operand loads (x, r, r's weights, the norm weights: K float4 each per thread,
 // range-checked), q4b_pro_finish forms the input vector in registers with the arithmetic of
 // gemv_prologue (workgroup 0 writes x1 and the input when asked).
-template <int K>
+template <int K, int T>
 __device__ __forceinline__ void q4b_pro_load(const GemvArgs& a, f32x4 (&xv)[K], f32x4 (&rv)[K], f32x4 (&rwv)[K],
                                              f32x4 (&wv)[K]) {
     const GemvPro& p = a.pro;
@@ -904,14 +907,27 @@ __device__ __forceinline__ void q4b_pro_load(const GemvArgs& a, f32x4 (&xv)[K], 
     const auto rs_w = buf_rsrc(p.w, p.mode == GP_NORM && p.w ? nb : 0u);
 #pragma unroll
     for (int k = 0; k < K; ++k) {
-        const uint32_t o = (uint32_t)(threadIdx.x + k * kGemvThreads) * 16u;
+        const uint32_t o = (uint32_t)(threadIdx.x + k * T) * 16u;
         xv[k] = bldf4(rs_x, o);
         rv[k] = bldf4(rs_r, o);
         rwv[k] = bldf4(rs_rw, o);
         wv[k] = bldf4(rs_w, o);
     }
 }
-template <int K>
+// Sum over a workgroup of T threads (wave sums, then the wave values in wave order); s_red
+// holds T / 64 floats.
+template <int T>
+__device__ __forceinline__ float q4b_block_sum(float v, float* s_red) {
+    v = group_sum<kWave>(v);
+    if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float t = s_red[0];
+#pragma unroll
+    for (int w = 1; w < T / kWave; ++w) t += s_red[w];
+    __syncthreads();  // s_red is reused by the next reduction
+    return t;
+}
+template <int K, int T>
 __device__ __forceinline__ void q4b_pro_finish(const GemvArgs& a, f32x4 (&xv)[K], const f32x4 (&rv)[K],
                                                const f32x4 (&rwv)[K], const f32x4 (&wv)[K], float* s_red) {
     const GemvPro& p = a.pro;
@@ -932,13 +948,13 @@ __device__ __forceinline__ void q4b_pro_finish(const GemvArgs& a, f32x4 (&xv)[K]
             float ss = 0.0f;
 #pragma unroll
             for (int k = 0; k < K; ++k)
-                if (tid + k * kGemvThreads < n4) ss = sumsq4(rv[k], ss);
-            inv1 = rms_inv(gemv_block_sum(ss, s_red), a.cols, p.eps);
+                if (tid + k * T < n4) ss = sumsq4(rv[k], ss);
+            inv1 = rms_inv(q4b_block_sum<T>(ss, s_red), a.cols, p.eps);
         }
         float ss = 0.0f;
 #pragma unroll
         for (int k = 0; k < K; ++k) {
-            const int c = tid + k * kGemvThreads;
+            const int c = tid + k * T;
             if (c < n4) {
                 xv[k] = pro_x1(p, xv[k], rv[k], rwv[k], inv1);
                 if (wr) *reinterpret_cast<f32x4*>(p.x_out + 4 * c) = xv[k];
@@ -946,7 +962,7 @@ __device__ __forceinline__ void q4b_pro_finish(const GemvArgs& a, f32x4 (&xv)[K]
             }
         }
         if (p.w) {
-            const float inv2 = rms_inv(gemv_block_sum(ss, s_red), a.cols, p.eps);
+            const float inv2 = rms_inv(q4b_block_sum<T>(ss, s_red), a.cols, p.eps);
 #pragma unroll
             for (int k = 0; k < K; ++k) xv[k] = norm_w4(xv[k], inv2, wv[k], p.uo);
         }
@@ -954,33 +970,34 @@ __device__ __forceinline__ void q4b_pro_finish(const GemvArgs& a, f32x4 (&xv)[K]
     if (p.xb_out && blockIdx.x == 0) {
 #pragma unroll
         for (int k = 0; k < K; ++k) {
-            const int c = tid + k * kGemvThreads;
+            const int c = tid + k * T;
             if (c < n4) *reinterpret_cast<f32x4*>(p.xb_out + 4 * c) = xv[k];
         }
     }
 }
 
-template <int MODE, int LPR, int RW, int BPL, bool PRO>
-__global__ __launch_bounds__(kGemvThreads) void k_gemv_q4b(GemvArgs a) {
+template <int MODE, int LPR, int RW, int BPL, bool PRO, int NW>
+__global__ __launch_bounds__(NW * kWave) void k_gemv_q4b(GemvArgs a) {
+    constexpr int T = NW * kWave;
     constexpr int NM = MODE == GV_GEGLU ? 2 : 1;
     constexpr int SETS = kWave / LPR;
-    constexpr int XK = PRO ? kQ4bProChunks : kQ4bXMax;  // x float4 per thread
+    constexpr int XK = (PRO ? kQ4bProMaxCols : kQ4bMaxCols) / 4 / T;  // x float4 per thread
     extern __shared__ __attribute__((aligned(16))) float s_xq[];
-    __shared__ float s_red[kGemvWaves];
+    __shared__ float s_red[NW];
     const int lane = threadIdx.x & 63;
     const int wv = threadIdx.x >> 6;
     const int li = lane % LPR, set = lane / LPR;
-    const int row0 = ((blockIdx.x * kGemvWaves + wv) * SETS + set) * RW;
+    const int row0 = ((blockIdx.x * NW + wv) * SETS + set) * RW;
     // x (PRO: the prologue's operands) first: its loads complete before the weights' do, so
     // staging it waits on it alone
     const int n4 = a.cols / 4;
     f32x4 xv[XK], rv[PRO ? XK : 1], rwv[PRO ? XK : 1], wnv[PRO ? XK : 1];
     if constexpr (PRO) {
-        q4b_pro_load<XK>(a, xv, rv, rwv, wnv);
+        q4b_pro_load<XK, T>(a, xv, rv, rwv, wnv);
     } else {
 #pragma unroll
         for (int k = 0; k < XK; ++k) {
-            const int i = (int)threadIdx.x + k * kGemvThreads;
+            const int i = (int)threadIdx.x + k * T;
             if (i < n4) xv[k] = ldf4(a.x + 4 * i);
         }
     }
@@ -1014,10 +1031,10 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_q4b(GemvArgs a) {
             }
     }
     // the input into LDS: float4 i of block i / 8 at slot offset 4 * (i % 8)
-    if constexpr (PRO) q4b_pro_finish<XK>(a, xv, rv, rwv, wnv, s_red);
+    if constexpr (PRO) q4b_pro_finish<XK, T>(a, xv, rv, rwv, wnv, s_red);
 #pragma unroll
     for (int k = 0; k < XK; ++k) {
-        const int i = (int)threadIdx.x + k * kGemvThreads;
+        const int i = (int)threadIdx.x + k * T;
         if (i < n4) *reinterpret_cast<f32x4*>(s_xq + (i >> 3) * kQ4bXStride + 4 * (i & 7)) = xv[k];
     }
     __syncthreads();
@@ -1071,7 +1088,9 @@ static bool launch_q4b(const GemvArgs& a, hipStream_t s) {
     const int nblk = a.cols / 32;
     if (a.cols % 512 != 0) return false;
     const size_t lds = (size_t)nblk * kQ4bXStride * sizeof(float);
-    if (a.cols > 4 * (PRO ? kQ4bProChunks : kQ4bXMax) * kGemvThreads || lds > 65536) return false;
+    if (a.cols > (PRO ? kQ4bProMaxCols : kQ4bMaxCols) || lds > 65536) return false;
+    // waves per workgroup: a prologue is paid once per workgroup, so its kernels take more
+    constexpr int NW = PRO ? ZL_GEMV_Q4B_PRO_WAVES : kGemvWaves;
     int lpr = 0;
     for (int l : {16, 32, 64})
         if (nblk % l == 0 && nblk / l <= kQ4bMaxB) {
@@ -1083,16 +1102,16 @@ static bool launch_q4b(const GemvArgs& a, hipStream_t s) {
     while (lpr < 64 && waves(lpr, 1) < ZL_GEMV_Q4B_WAVES && nblk % (2 * lpr) == 0) lpr *= 2;
     const int rw = waves(lpr, 2) >= 4 * ZL_GEMV_Q4B_WAVES ? 2 : 1;
     const int bpl = nblk / lpr;
-    const unsigned grid = (unsigned)cdiv(waves(lpr, rw), (int64_t)kGemvWaves);
+    const unsigned grid = (unsigned)cdiv(waves(lpr, rw), (int64_t)NW);
     auto go = [&](auto lpr_c, auto rw_c) {
         constexpr int L = decltype(lpr_c)::value, RW = decltype(rw_c)::value;
         switch (bpl) {
-            case 1: k_gemv_q4b<MODE, L, RW, 1, PRO><<<grid, kGemvThreads, lds, s>>>(a); break;
-            case 2: k_gemv_q4b<MODE, L, RW, 2, PRO><<<grid, kGemvThreads, lds, s>>>(a); break;
-            case 3: k_gemv_q4b<MODE, L, RW, 3, PRO><<<grid, kGemvThreads, lds, s>>>(a); break;
-            case 4: k_gemv_q4b<MODE, L, RW, 4, PRO><<<grid, kGemvThreads, lds, s>>>(a); break;
-            case 5: k_gemv_q4b<MODE, L, RW, 5, PRO><<<grid, kGemvThreads, lds, s>>>(a); break;
-            default: k_gemv_q4b<MODE, L, RW, 6, PRO><<<grid, kGemvThreads, lds, s>>>(a); break;
+            case 1: k_gemv_q4b<MODE, L, RW, 1, PRO, NW><<<grid, NW * kWave, lds, s>>>(a); break;
+            case 2: k_gemv_q4b<MODE, L, RW, 2, PRO, NW><<<grid, NW * kWave, lds, s>>>(a); break;
+            case 3: k_gemv_q4b<MODE, L, RW, 3, PRO, NW><<<grid, NW * kWave, lds, s>>>(a); break;
+            case 4: k_gemv_q4b<MODE, L, RW, 4, PRO, NW><<<grid, NW * kWave, lds, s>>>(a); break;
+            case 5: k_gemv_q4b<MODE, L, RW, 5, PRO, NW><<<grid, NW * kWave, lds, s>>>(a); break;
+            default: k_gemv_q4b<MODE, L, RW, 6, PRO, NW><<<grid, NW * kWave, lds, s>>>(a); break;
         }
     };
     using I1 = std::integral_constant<int, 1>;
