@@ -370,7 +370,10 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
 // split order, and the four waves' sums are added in wave order.
 constexpr int kMaxSplit = 1024;
 constexpr int kMergeCols = kWave;
-constexpr int kMergePre = 8;
+#ifndef ZL_ATTN_MERGE_PRE
+#define ZL_ATTN_MERGE_PRE 16
+#endif
+constexpr int kMergePre = ZL_ATTN_MERGE_PRE;
 __device__ __forceinline__ float bldf(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
 }
