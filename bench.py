@@ -44,6 +44,7 @@ from ziglm_amd import synth  # noqa: E402
 from ziglm_amd.device import HipDevice  # noqa: E402
 
 PEAK_HBM_GBS = 8000.0  # MI355X HBM3E peak
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 matrix peak
 MALL_BYTES = 256 << 20
 METRIC = "fused-op HBM GB/s (% of MI355X peak) + µs per Gemma layer, decode & 2k prefill"
 
@@ -479,6 +480,26 @@ def bench_gemv(dev):
     return out
 
 
+def bench_gemm_prefill(dev, T=2048):
+    """Prefill products on the matrix cores (hip_gemm, 2048 tokens, f32 activations): us and
+    algorithmic TFLOP/s (2 * rows * cols * tokens / t). The kernel runs three bf16 terms of
+    every activation (and one to three of every weight) through v_mfma_f32_32x32x16_bf16, so
+    its ceiling is a third of the 2.5 PFLOP/s dense bf16 peak for Q4_0 / Q8_0 / BF16."""
+    s = LY.GEMMA_4B
+    H, I = s.H, s.I
+    cases = [("gate_q4_0", B.Q4_0, I, H), ("down_q4_0", B.Q4_0, H, I), ("qkv_q4_0", B.Q4_0, (s.nh + 2 * s.nkv) * s.D, H),
+             ("gate_q8_0", B.Q8_0, I, H), ("gate_bf16", B.BF16, I, H)]
+    out = {}
+    for name, qt, rows, cols in cases:
+        r = gemv_case(dev, name, qt, [(rows, cols)],
+                      lambda d, m, x, ys, qt=qt, rows=rows, cols=cols: d.gemm(qt, m[0], x, ys[0], T, rows, cols), T)
+        tf = 2.0 * rows * cols * T / r["us"] / 1e6
+        out[name] = {"us": r["us"], "rows": rows, "cols": cols, "tokens": T, "TFLOPs": round(tf, 1),
+                     "frac_of_3term_bound": round(tf / (PEAK_BF16_TFLOPS / 3), 4)}
+        log(f"  gemm {name:12s} {r['us']:9.2f} us {tf:7.1f} TFLOP/s")
+    return out
+
+
 # ---------------------------------------------------------------------------------------
 # Full decode step (34-layer Gemma-4B-shaped Q4_0 model, graph replay per token)
 # ---------------------------------------------------------------------------------------
@@ -714,7 +735,7 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline config only")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default=None, help="run one op only (profiling): a chain op, "
-                    "gather_q8_0 / gather_q4_0 / gather_bf16 (c3), gemv, decode_step, gguf_decode, "
+                    "gather_q8_0 / gather_q4_0 / gather_bf16 (c3), gemv, gemm, decode_step, gguf_decode, "
                     "or 'copy' = hipMemcpy device-to-device of the GeGLU output size (counter calibration)")
     ap.add_argument("--eager", action="store_true", help="with --only: launch eagerly, no graph")
     ap.add_argument("--config", default="c2", choices=["c2", "c4"])
@@ -742,6 +763,10 @@ def main():
         elif a.only == "gemv":
             log("gemv (decode projections)")
             print(json.dumps(bench_gemv(dev)))
+            return
+        elif a.only == "gemm":
+            log("gemm (prefill projections, matrix cores)")
+            print(json.dumps(bench_gemm_prefill(dev)))
             return
         elif a.only == "copy":
             sets, _ = make_sets(dev, shape, T, B.BF16)
@@ -821,6 +846,8 @@ def main():
         cfgs["c4_prefill"]["chain_GBps"] = round(cfgs["c4_prefill"]["chain_GBps"], 1)
         log("gemv (decode projections)")
         cfgs["gemv_decode"] = bench_gemv(dev)
+        log("gemm (prefill projections, matrix cores)")
+        cfgs["gemm_prefill"] = bench_gemm_prefill(dev)
         log("decode step (34 layers, graph)")
         cfgs["decode_step"] = bench_decode_step(dev)
         log("GGUF load + E2B-shaped decode")
