@@ -1,6 +1,6 @@
 """The batch-1 Q4_0 block kernel (gemv.hip k_gemv_q4b) over its selection rules, through the
-C-ABI: every column count it takes (multiples of 512 up to 12288 columns: 16 to 384 blocks
-per row, so 16, 32 or 64 lanes per row and 1 to 6 blocks per lane), row counts that leave the
+C-ABI: every column count it takes (multiples of 256 up to 12288 columns: 8 to 384 blocks
+per row, so 8, 16, 32 or 64 lanes per row and 1 to 6 blocks per lane), row counts that leave the
 last row set partly empty, enough rows for two rows per set, the fused GeGLU and QKV forms and
 the 20-byte block windows at both ends of a row (first block even, last block odd).
 
@@ -18,7 +18,7 @@ from ziglm_amd import synth
 
 pytestmark = pytest.mark.gpu
 
-COLS = [512, 1024, 1536, 2048, 2560, 3072, 4096, 5120, 6144, 10240, 12288]
+COLS = [256, 512, 768, 1024, 1280, 1536, 2048, 2560, 3072, 4096, 5120, 6144, 10240, 12288]
 
 
 def int_x(seed, cols):
@@ -53,7 +53,7 @@ def test_q4b_two_rows_per_set(dev, rows, cols):
                                   err_msg=f"{rows} x {cols}")
 
 
-@pytest.mark.parametrize("rows,cols", [(77, 1536), (5003, 2560), (300, 6144), (64, 10240)])
+@pytest.mark.parametrize("rows,cols", [(77, 1536), (5003, 2560), (300, 6144), (64, 10240), (1536, 256)])
 def test_q4b_geglu_equals_unfused(dev, rows, cols):
     gw, _ = int_matrix(B.Q4_0, rows, cols, seed=1 + rows, scale_pow=-3)
     uw, _ = int_matrix(B.Q4_0, rows, cols, seed=2 + rows, scale_pow=-3)

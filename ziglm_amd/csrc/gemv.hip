@@ -836,7 +836,7 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(QT
 // block count per row both ends stay inside the row) and picks the scale and the 16 quant
 // bytes out of the window with byte permutes.
 //
-// Layout: LPR lanes per row (16, 32 or 64) and 64 / LPR row sets of RW rows per wave; lane i
+// Layout: LPR lanes per row (8, 16, 32 or 64) and 64 / LPR row sets of RW rows per wave; lane i
 // of a set takes blocks i, i + LPR, ... (bpl <= kQ4bMaxB of them) of each of its rows, every
 // weight load of the wave issued before any arithmetic (one memory round trip per wave).
 // x is staged once per workgroup in LDS, 36 floats per 32-column block (the padding keeps
@@ -1078,7 +1078,7 @@ __global__ __launch_bounds__(NW * kWave) void k_gemv_q4b(GemvArgs a) {
 }
 
 // Launches k_gemv_q4b when the product suits it (batch 1, Q4_0, blocks per row a multiple of
-// 16 with at most kQ4bMaxB per lane at 64 lanes per row, x within 64 KB of LDS); returns
+// 8 with at most kQ4bMaxB per lane at 8 to 64 lanes per row, x within 64 KB of LDS); returns
 // false otherwise. LPR: the fewest lanes per row that take every block in kQ4bMaxB steps,
 // more while the grid has fewer than ZL_GEMV_Q4B_WAVES waves; RW = 2 rows per set from
 // 4 * ZL_GEMV_Q4B_WAVES waves.
@@ -1086,14 +1086,16 @@ template <int QT, int MODE, bool PRO>
 static bool launch_q4b(const GemvArgs& a, hipStream_t s) {
     if (!ZL_GEMV_Q4B || QT != HIP_BRIDGE_Q4_0 || a.batch != 1) return false;
     const int nblk = a.cols / 32;
-    if (a.cols % 512 != 0) return false;
+    if (a.cols % 256 != 0) return false;
     const size_t lds = (size_t)nblk * kQ4bXStride * sizeof(float);
     if (a.cols > (PRO ? kQ4bProMaxCols : kQ4bMaxCols) || lds > 65536) return false;
     // waves per workgroup: a prologue is paid once per workgroup, so its kernels take more
     constexpr int NW = PRO ? ZL_GEMV_Q4B_PRO_WAVES : kGemvWaves;
-    int lpr = 0;
+    // 8 lanes per row only for block counts that 16 does not divide (8, 24, 40: e.g. the
+    // per-layer-embedding projection's 256 columns)
+    int lpr = nblk % 16 != 0 && nblk / 8 <= kQ4bMaxB ? 8 : 0;
     for (int l : {16, 32, 64})
-        if (nblk % l == 0 && nblk / l <= kQ4bMaxB) {
+        if (!lpr && nblk % l == 0 && nblk / l <= kQ4bMaxB) {
             lpr = l;
             break;
         }
@@ -1116,7 +1118,15 @@ static bool launch_q4b(const GemvArgs& a, hipStream_t s) {
     };
     using I1 = std::integral_constant<int, 1>;
     using I2 = std::integral_constant<int, 2>;
-    if (lpr == 16) rw == 2 ? go(std::integral_constant<int, 16>{}, I2{}) : go(std::integral_constant<int, 16>{}, I1{});
+    if (lpr == 8) {  // odd block counts per lane only
+        auto go8 = [&](auto rw_c) {
+            constexpr int RW = decltype(rw_c)::value;
+            if (bpl == 1) k_gemv_q4b<MODE, 8, RW, 1, PRO, NW><<<grid, NW * kWave, lds, s>>>(a);
+            else if (bpl == 3) k_gemv_q4b<MODE, 8, RW, 3, PRO, NW><<<grid, NW * kWave, lds, s>>>(a);
+            else k_gemv_q4b<MODE, 8, RW, 5, PRO, NW><<<grid, NW * kWave, lds, s>>>(a);
+        };
+        rw == 2 ? go8(I2{}) : go8(I1{});
+    } else if (lpr == 16) rw == 2 ? go(std::integral_constant<int, 16>{}, I2{}) : go(std::integral_constant<int, 16>{}, I1{});
     else if (lpr == 32) rw == 2 ? go(std::integral_constant<int, 32>{}, I2{}) : go(std::integral_constant<int, 32>{}, I1{});
     else rw == 2 ? go(std::integral_constant<int, 64>{}, I2{}) : go(std::integral_constant<int, 64>{}, I1{});
     return true;
@@ -1255,7 +1265,7 @@ static void launch_vec(const GemvArgs& a, hipStream_t s) {
             k_gemv<QT, RP, 1, MODE><<<(unsigned)cdiv(a.total_rows, RP), kGemvThreads, 0, s>>>(a);
         }
     } else if (launch_q4b<QT, MODE, false>(a, s)) {
-        // launched: batch-1 Q4_0 with 512-column multiples
+        // launched: batch-1 Q4_0 with 256-column multiples
     } else if (MODE == GV_PLAIN && a.batch == 1 && a.total_rows >= kGemvWaveRowsMin && a.cols <= kGemvWaveColsMax &&
                QT != HIP_BRIDGE_F16 && QT != HIP_BRIDGE_BF16 && QT != HIP_BRIDGE_F32) {
         // (k_gemv_w is instantiated for these cases only)
