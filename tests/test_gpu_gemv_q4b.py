@@ -1,4 +1,4 @@
-"""The batch-1 Q4_0 block kernel (gemv.hip k_gemv_q4b) over its selection rules, through the
+"""The batch-1 block kernel (gemv.hip k_gemv_q4b, Q4_0 and Q8_0) over its selection rules, through the
 C-ABI: every column count it takes (multiples of 256 up to 12288 columns: 8 to 384 blocks
 per row, so 8, 16, 32 or 64 lanes per row and 1 to 6 blocks per lane), row counts that leave the
 last row set partly empty, enough rows for two rows per set, the fused GeGLU and QKV forms and
@@ -25,32 +25,34 @@ def int_x(seed, cols):
     return np.random.default_rng(seed).integers(-3, 4, cols).astype(np.float32)
 
 
-def gemv(dev, raw, x, rows, cols):
+def gemv(dev, raw, x, rows, cols, qtype=B.Q4_0):
     d_y = dev.alloc(rows * 4)
     d_y.fill(0xAB)
-    dev.gemv(B.Q4_0, dev.from_numpy(np.ascontiguousarray(raw).reshape(-1)), dev.from_numpy(x), d_y, rows, cols)
+    dev.gemv(qtype, dev.from_numpy(np.ascontiguousarray(raw).reshape(-1)), dev.from_numpy(x), d_y, rows, cols)
     return d_y.to_numpy((rows,), np.float32)
 
 
+@pytest.mark.parametrize("qtype", [B.Q4_0, B.Q8_0])
 @pytest.mark.parametrize("cols", COLS)
 @pytest.mark.parametrize("rows", [1, 37, 4099])
-def test_q4b_integer_bitexact(dev, rows, cols):
-    raw, wd = int_matrix(B.Q4_0, rows, cols, seed=rows + cols, scale_pow=-1)
+def test_q4b_integer_bitexact(dev, qtype, rows, cols):
+    raw, wd = int_matrix(qtype, rows, cols, seed=rows + cols + qtype, scale_pow=-1)
     x = int_x(cols, cols)
     exact = wd @ x.astype(np.float64)
     assert np.all(np.abs(exact) < 2 ** 24)
-    np.testing.assert_array_equal(gemv(dev, raw, x, rows, cols), exact.astype(np.float32),
-                                  err_msg=f"{rows} x {cols}")
+    np.testing.assert_array_equal(gemv(dev, raw, x, rows, cols, qtype), exact.astype(np.float32),
+                                  err_msg=f"qtype {qtype} {rows} x {cols}")
 
 
+@pytest.mark.parametrize("qtype", [B.Q4_0, B.Q8_0])
 @pytest.mark.parametrize("rows,cols", [(40000, 2560), (33001, 512), (16389, 5120)])
-def test_q4b_two_rows_per_set(dev, rows, cols):
+def test_q4b_two_rows_per_set(dev, qtype, rows, cols):
     """Row counts that take two rows per row set (the LM-head shape class), ragged at the end."""
-    raw, wd = int_matrix(B.Q4_0, rows, cols, seed=rows, scale_pow=-2)
+    raw, wd = int_matrix(qtype, rows, cols, seed=rows + qtype, scale_pow=-2)
     x = int_x(rows, cols)
     exact = wd @ x.astype(np.float64)
-    np.testing.assert_array_equal(gemv(dev, raw, x, rows, cols), exact.astype(np.float32),
-                                  err_msg=f"{rows} x {cols}")
+    np.testing.assert_array_equal(gemv(dev, raw, x, rows, cols, qtype), exact.astype(np.float32),
+                                  err_msg=f"qtype {qtype} {rows} x {cols}")
 
 
 @pytest.mark.parametrize("rows,cols", [(77, 1536), (5003, 2560), (300, 6144), (64, 10240), (1536, 256)])
@@ -86,11 +88,12 @@ def test_q4b_qkv_segments(dev, q_rows, k_rows, v_rows, cols):
                                       err_msg=f"matrix {i}")
 
 
+@pytest.mark.parametrize("qtype", [B.Q4_0, B.Q8_0])
 @pytest.mark.parametrize("rows,cols", [(300, 2560), (4096, 10240), (2000, 3072)])
-def test_q4b_random_vs_f64(dev, rows, cols):
-    raw, wd = random_matrix(B.Q4_0, rows, cols, seed=rows + 7)
+def test_q4b_random_vs_f64(dev, qtype, rows, cols):
+    raw, wd = random_matrix(qtype, rows, cols, seed=rows + 7)
     x = synth.normal_f32(rows, "x", (cols,), 0, 2)
     exact = wd @ x.astype(np.float64)
-    got = gemv(dev, raw, x, rows, cols).astype(np.float64)
+    got = gemv(dev, raw, x, rows, cols, qtype).astype(np.float64)
     bd = bound(wd, x)
     assert np.all(np.abs(got - exact) <= bd), float(np.max(np.abs(got - exact) / bd))

@@ -827,14 +827,13 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(QT
     }
 }
 
-// Batch-1 Q4_0 products, one 32-column block per lane and step: the loops above issue two
-// loads per 8-column group (the 16-bit scale and 4 quant bytes, every other one 2-byte
-// aligned), and at decode sizes that instruction stream, not HBM, sets the rate (measured
-// with the arithmetic removed: 262144 x 2560 in 97 us against 82 us with every quant load
-// 4-byte aligned). Here a lane takes the whole 18-byte block with two dword-aligned loads
-// (16 + 4 bytes: the 20-byte window at 18b for even b, at 18b - 2 for odd b, so with an even
-// block count per row both ends stay inside the row) and picks the scale and the 16 quant
-// bytes out of the window with byte permutes.
+// Batch-1 Q4_0 / Q8_0 products, one 32-column block per lane and step: the loops above issue
+// two or three loads per 8-column group (the 16-bit scale and 4 or 8 quant bytes, every other
+// one 2-byte aligned), and at decode sizes that instruction stream, not HBM, sets the rate
+// (measured with the arithmetic removed: Q4_0 262144 x 2560 in 97 us against 82 us with every
+// quant load 4-byte aligned). Here a lane takes the whole block with dword-aligned loads
+// (BlkWin: 20 bytes for Q4_0, 36 for Q8_0) and picks the scale and the quant bytes out of the
+// window with byte permutes (Q8_0 262144 x 2560: 164 -> 128 us).
 //
 // Layout: LPR lanes per row (8, 16, 32 or 64) and 64 / LPR row sets of RW rows per wave; lane i
 // of a set takes blocks i, i + LPR, ... (bpl <= kQ4bMaxB of them) of each of its rows, every
@@ -858,39 +857,76 @@ constexpr int kQ4bProMaxCols = 4096;  // PRO operands: 4 float4 each per thread 
 typedef u32x4 u32x4_a4 __attribute__((aligned(4)));
 typedef uint32_t u32_a4 __attribute__((aligned(4)));
 
-struct Q4Win {
+// The dword-aligned window holding block b of a Q4_0 (18-byte) or Q8_0 (34-byte) row: it
+// starts at BB*b rounded down to 4 bytes, so the scale sits at window byte 0 (even b) or 2
+// (odd b) and the quants follow it; an even block count per row keeps both ends of every
+// window inside the row. Quant dword i is the window's bytes 2 + 4i .. 5 + 4i (even) or
+// 4 + 4i .. 7 + 4i (odd), one v_perm_b32 of two window dwords either way.
+template <int QT>
+struct BlkWin;
+template <>
+struct BlkWin<HIP_BRIDGE_Q4_0> {
+    static constexpr uint32_t BB = 18;
     u32x4 a;     // window bytes 0..15
     uint32_t e;  // window bytes 16..19
-};
-
-// sum over the block's 32 columns of q_j * x_j (q_j the stored nibble), x the block's 32
-// values from LDS (xs: 36-float stride slot), and the block's f32 scale; returns
-// d * (sum - 8 * sum x) (math.zig:304-305).
-__device__ __forceinline__ float q4b_dot(const Q4Win& w, bool odd, const f32x4 (&xl)[4], const f32x4 (&xh)[4],
-                                         float sx) {
-    const uint32_t sel = odd ? 0x07060504u : 0x05040302u;  // quant bytes 4..19 / 2..17
-    const uint32_t q0 = __builtin_amdgcn_perm(w.a.y, w.a.x, sel);
-    const uint32_t q1 = __builtin_amdgcn_perm(w.a.z, w.a.y, sel);
-    const uint32_t q2 = __builtin_amdgcn_perm(w.a.w, w.a.z, sel);
-    const uint32_t q3 = __builtin_amdgcn_perm(w.e, w.a.w, sel);
-    const uint32_t d16 = __builtin_amdgcn_perm(0u, w.a.x, odd ? 0x0c0c0302u : 0x0c0c0100u);
-    const uint32_t q[4] = {q0, q1, q2, q3};
-    float t = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t lo = mask_bytes(q[i], 0x0f0f0f0fu);       // columns 4i .. 4i+3
-        const uint32_t hi = mask_bytes(q[i] >> 4, 0x0f0f0f0fu);  // columns 16+4i .. 16+4i+3
-        t = i == 0 ? (float)(lo & 0xff) * xl[0].x : fmaf((float)(lo & 0xff), xl[i].x, t);
-        t = fmaf((float)((lo >> 8) & 0xff), xl[i].y, t);
-        t = fmaf((float)((lo >> 16) & 0xff), xl[i].z, t);
-        t = fmaf((float)(lo >> 24), xl[i].w, t);
-        t = fmaf((float)(hi & 0xff), xh[i].x, t);
-        t = fmaf((float)((hi >> 8) & 0xff), xh[i].y, t);
-        t = fmaf((float)((hi >> 16) & 0xff), xh[i].z, t);
-        t = fmaf((float)(hi >> 24), xh[i].w, t);
+    __device__ __forceinline__ void load(const unsigned char* p) {
+        a = *reinterpret_cast<const u32x4_a4*>(p);
+        e = *reinterpret_cast<const u32_a4*>(p + 16);
     }
-    return h2f(d16) * fmaf(-8.0f, sx, t);
-}
+    // d * (sum_j u_j x_j - 8 * sum x) over the block (math.zig:304-305): u_j the stored nibble,
+    // low nibbles columns 0..15, high nibbles 16..31; xl / xh: the block's x, columns 0..15
+    // and 16..31; sx their sum.
+    __device__ __forceinline__ float dot(bool odd, const f32x4 (&xl)[4], const f32x4 (&xh)[4], float sx) const {
+        const uint32_t sel = odd ? 0x07060504u : 0x05040302u;
+        const uint32_t q[4] = {__builtin_amdgcn_perm(a.y, a.x, sel), __builtin_amdgcn_perm(a.z, a.y, sel),
+                               __builtin_amdgcn_perm(a.w, a.z, sel), __builtin_amdgcn_perm(e, a.w, sel)};
+        const uint32_t d16 = __builtin_amdgcn_perm(0u, a.x, odd ? 0x0c0c0302u : 0x0c0c0100u);
+        float t = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t lo = mask_bytes(q[i], 0x0f0f0f0fu);       // columns 4i .. 4i+3
+            const uint32_t hi = mask_bytes(q[i] >> 4, 0x0f0f0f0fu);  // columns 16+4i .. 16+4i+3
+            t = i == 0 ? (float)(lo & 0xff) * xl[0].x : fmaf((float)(lo & 0xff), xl[i].x, t);
+            t = fmaf((float)((lo >> 8) & 0xff), xl[i].y, t);
+            t = fmaf((float)((lo >> 16) & 0xff), xl[i].z, t);
+            t = fmaf((float)(lo >> 24), xl[i].w, t);
+            t = fmaf((float)(hi & 0xff), xh[i].x, t);
+            t = fmaf((float)((hi >> 8) & 0xff), xh[i].y, t);
+            t = fmaf((float)((hi >> 16) & 0xff), xh[i].z, t);
+            t = fmaf((float)(hi >> 24), xh[i].w, t);
+        }
+        return h2f(d16) * fmaf(-8.0f, sx, t);
+    }
+};
+template <>
+struct BlkWin<HIP_BRIDGE_Q8_0> {
+    static constexpr uint32_t BB = 34;
+    u32x4 a, b;  // window bytes 0..31
+    uint32_t e;  // window bytes 32..35
+    __device__ __forceinline__ void load(const unsigned char* p) {
+        a = *reinterpret_cast<const u32x4_a4*>(p);
+        b = *reinterpret_cast<const u32x4_a4*>(p + 16);
+        e = *reinterpret_cast<const u32_a4*>(p + 32);
+    }
+    // d * (sum_j u_j x_j - 128 * sum x): the int8 quants read as u = q ^ 0x80 (columns 4i ..
+    // 4i+3 in quant dword i), as the group kernels do.
+    __device__ __forceinline__ float dot(bool odd, const f32x4 (&xl)[4], const f32x4 (&xh)[4], float sx) const {
+        const uint32_t sel = odd ? 0x07060504u : 0x05040302u;
+        const uint32_t D[9] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, e};
+        const uint32_t d16 = __builtin_amdgcn_perm(0u, a.x, odd ? 0x0c0c0302u : 0x0c0c0100u);
+        float t = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t u = __builtin_amdgcn_perm(D[i + 1], D[i], sel) ^ 0x80808080u;
+            const f32x4 xv = i < 4 ? xl[i] : xh[i - 4];
+            t = i == 0 ? (float)(u & 0xff) * xv.x : fmaf((float)(u & 0xff), xv.x, t);
+            t = fmaf((float)((u >> 8) & 0xff), xv.y, t);
+            t = fmaf((float)((u >> 16) & 0xff), xv.z, t);
+            t = fmaf((float)(u >> 24), xv.w, t);
+        }
+        return h2f(d16) * fmaf(-128.0f, sx, t);
+    }
+};
 
 // PRO prologue of the block kernel, in two phases around the weight loads: q4b_pro_load
 // issues the operand loads (x, r, r's weights, the norm weights: K float4 each per thread,
@@ -976,7 +1012,7 @@ __device__ __forceinline__ void q4b_pro_finish(const GemvArgs& a, f32x4 (&xv)[K]
     }
 }
 
-template <int MODE, int LPR, int RW, int BPL, bool PRO, int NW>
+template <int QT, int MODE, int LPR, int RW, int BPL, bool PRO, int NW>
 __global__ __launch_bounds__(NW * kWave) void k_gemv_q4b(GemvArgs a) {
     constexpr int T = NW * kWave;
     constexpr int NM = MODE == GV_GEGLU ? 2 : 1;
@@ -1018,17 +1054,14 @@ __global__ __launch_bounds__(NW * kWave) void k_gemv_q4b(GemvArgs a) {
         if constexpr (NM == 2) wrow[r][1] = a.w_up + (int64_t)Rs * a.row_bytes;
         yrow[r] = ok ? yb + Rs : nullptr;
     }
-    Q4Win w[BPL][RW][NM];
+    BlkWin<QT> w[BPL][RW][NM];
 #pragma unroll
     for (int j = 0; j < BPL; ++j) {
-        const uint32_t off = ((uint32_t)(li + LPR * j) * 18u) & ~3u;
+        const uint32_t off = ((uint32_t)(li + LPR * j) * BlkWin<QT>::BB) & ~3u;
 #pragma unroll
         for (int r = 0; r < RW; ++r)
 #pragma unroll
-            for (int m = 0; m < NM; ++m) {
-                w[j][r][m].a = *reinterpret_cast<const u32x4_a4*>(wrow[r][m] + off);
-                w[j][r][m].e = *reinterpret_cast<const u32_a4*>(wrow[r][m] + off + 16u);
-            }
+            for (int m = 0; m < NM; ++m) w[j][r][m].load(wrow[r][m] + off);
     }
     // the input into LDS: float4 i of block i / 8 at slot offset 4 * (i % 8)
     if constexpr (PRO) q4b_pro_finish<XK, T>(a, xv, rv, rwv, wnv, s_red);
@@ -1060,7 +1093,7 @@ __global__ __launch_bounds__(NW * kWave) void k_gemv_q4b(GemvArgs a) {
 #pragma unroll
         for (int r = 0; r < RW; ++r)
 #pragma unroll
-            for (int m = 0; m < NM; ++m) acc[r][m] += q4b_dot(w[j][r][m], odd, xl, xh, sx);
+            for (int m = 0; m < NM; ++m) acc[r][m] += w[j][r][m].dot(odd, xl, xh, sx);
     }
 #pragma unroll
     for (int r = 0; r < RW; ++r)
@@ -1084,7 +1117,10 @@ __global__ __launch_bounds__(NW * kWave) void k_gemv_q4b(GemvArgs a) {
 // 4 * ZL_GEMV_Q4B_WAVES waves.
 template <int QT, int MODE, bool PRO>
 static bool launch_q4b(const GemvArgs& a, hipStream_t s) {
-    if (!ZL_GEMV_Q4B || QT != HIP_BRIDGE_Q4_0 || a.batch != 1) return false;
+    if constexpr (QT != HIP_BRIDGE_Q4_0 && QT != HIP_BRIDGE_Q8_0) {
+        return false;
+    } else {
+    if (!ZL_GEMV_Q4B || a.batch != 1) return false;
     const int nblk = a.cols / 32;
     if (a.cols % 256 != 0) return false;
     const size_t lds = (size_t)nblk * kQ4bXStride * sizeof(float);
@@ -1108,12 +1144,12 @@ static bool launch_q4b(const GemvArgs& a, hipStream_t s) {
     auto go = [&](auto lpr_c, auto rw_c) {
         constexpr int L = decltype(lpr_c)::value, RW = decltype(rw_c)::value;
         switch (bpl) {
-            case 1: k_gemv_q4b<MODE, L, RW, 1, PRO, NW><<<grid, NW * kWave, lds, s>>>(a); break;
-            case 2: k_gemv_q4b<MODE, L, RW, 2, PRO, NW><<<grid, NW * kWave, lds, s>>>(a); break;
-            case 3: k_gemv_q4b<MODE, L, RW, 3, PRO, NW><<<grid, NW * kWave, lds, s>>>(a); break;
-            case 4: k_gemv_q4b<MODE, L, RW, 4, PRO, NW><<<grid, NW * kWave, lds, s>>>(a); break;
-            case 5: k_gemv_q4b<MODE, L, RW, 5, PRO, NW><<<grid, NW * kWave, lds, s>>>(a); break;
-            default: k_gemv_q4b<MODE, L, RW, 6, PRO, NW><<<grid, NW * kWave, lds, s>>>(a); break;
+            case 1: k_gemv_q4b<QT, MODE, L, RW, 1, PRO, NW><<<grid, NW * kWave, lds, s>>>(a); break;
+            case 2: k_gemv_q4b<QT, MODE, L, RW, 2, PRO, NW><<<grid, NW * kWave, lds, s>>>(a); break;
+            case 3: k_gemv_q4b<QT, MODE, L, RW, 3, PRO, NW><<<grid, NW * kWave, lds, s>>>(a); break;
+            case 4: k_gemv_q4b<QT, MODE, L, RW, 4, PRO, NW><<<grid, NW * kWave, lds, s>>>(a); break;
+            case 5: k_gemv_q4b<QT, MODE, L, RW, 5, PRO, NW><<<grid, NW * kWave, lds, s>>>(a); break;
+            default: k_gemv_q4b<QT, MODE, L, RW, 6, PRO, NW><<<grid, NW * kWave, lds, s>>>(a); break;
         }
     };
     using I1 = std::integral_constant<int, 1>;
@@ -1121,15 +1157,16 @@ static bool launch_q4b(const GemvArgs& a, hipStream_t s) {
     if (lpr == 8) {  // odd block counts per lane only
         auto go8 = [&](auto rw_c) {
             constexpr int RW = decltype(rw_c)::value;
-            if (bpl == 1) k_gemv_q4b<MODE, 8, RW, 1, PRO, NW><<<grid, NW * kWave, lds, s>>>(a);
-            else if (bpl == 3) k_gemv_q4b<MODE, 8, RW, 3, PRO, NW><<<grid, NW * kWave, lds, s>>>(a);
-            else k_gemv_q4b<MODE, 8, RW, 5, PRO, NW><<<grid, NW * kWave, lds, s>>>(a);
+            if (bpl == 1) k_gemv_q4b<QT, MODE, 8, RW, 1, PRO, NW><<<grid, NW * kWave, lds, s>>>(a);
+            else if (bpl == 3) k_gemv_q4b<QT, MODE, 8, RW, 3, PRO, NW><<<grid, NW * kWave, lds, s>>>(a);
+            else k_gemv_q4b<QT, MODE, 8, RW, 5, PRO, NW><<<grid, NW * kWave, lds, s>>>(a);
         };
         rw == 2 ? go8(I2{}) : go8(I1{});
     } else if (lpr == 16) rw == 2 ? go(std::integral_constant<int, 16>{}, I2{}) : go(std::integral_constant<int, 16>{}, I1{});
     else if (lpr == 32) rw == 2 ? go(std::integral_constant<int, 32>{}, I2{}) : go(std::integral_constant<int, 32>{}, I1{});
     else rw == 2 ? go(std::integral_constant<int, 64>{}, I2{}) : go(std::integral_constant<int, 64>{}, I1{});
     return true;
+    }
 }
 
 // Any alignment / column count: one workgroup per row, scalar dequantisation per element.
