@@ -97,3 +97,17 @@ def test_q4b_random_vs_f64(dev, qtype, rows, cols):
     got = gemv(dev, raw, x, rows, cols, qtype).astype(np.float64)
     bd = bound(wd, x)
     assert np.all(np.abs(got - exact) <= bd), float(np.max(np.abs(got - exact) / bd))
+
+
+@pytest.mark.parametrize("qtype", [B.Q4_0, B.Q8_0])
+def test_q4b_two_byte_aligned_weights_take_the_group_kernel(dev, qtype):
+    """Block rows are only 2-byte aligned in GGUF files; a matrix whose base is not 4-byte
+    aligned is left to the group-wise kernel (16-bit loads) and is as exact."""
+    rows, cols = 37, 2560
+    raw, wd = int_matrix(qtype, rows, cols, seed=5 + qtype, scale_pow=-1)
+    x = int_x(6, cols)
+    d_w = dev.alloc(raw.nbytes + 16)
+    d_w.at(2).upload(np.ascontiguousarray(raw).reshape(-1))
+    d_y = dev.alloc(rows * 4)
+    dev.gemv(qtype, d_w.at(2), dev.from_numpy(x), d_y, rows, cols)
+    np.testing.assert_array_equal(d_y.to_numpy((rows,), np.float32), (wd @ x.astype(np.float64)).astype(np.float32))

@@ -1121,6 +1121,12 @@ static bool launch_q4b(const GemvArgs& a, hipStream_t s) {
         return false;
     } else {
     if (!ZL_GEMV_Q4B || a.batch != 1) return false;
+    // the windows are dword loads from the row base: every matrix 4-byte aligned (rows are a
+    // whole number of block pairs, 36 / 68 bytes, so each row is too)
+    auto a4 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; };
+    for (int i = 0; i < a.nseg; ++i)
+        if (a.seg[i].rows > 0 && !a4(a.seg[i].w)) return false;
+    if (MODE == GV_GEGLU && !a4(a.w_up)) return false;
     const int nblk = a.cols / 32;
     if (a.cols % 256 != 0) return false;
     const size_t lds = (size_t)nblk * kQ4bXStride * sizeof(float);
