@@ -29,6 +29,7 @@ import dataclasses
 import json
 import math
 import os
+import statistics
 import sys
 import time
 
@@ -69,9 +70,10 @@ def time_graph_ms(dev, g, reps=1):
     return ms
 
 
-def time_launches_us(dev, fn, sets, n_launch, warm=1):
-    """Average microseconds per launch of fn(dev, set) over a graph of n_launch launches
-    cycling through `sets`."""
+def time_launches_us(dev, fn, sets, n_launch, warm=1, reps=5):
+    """Microseconds per launch of fn(dev, set) over a graph of n_launch launches cycling
+    through `sets`: the median over `reps` timed replays of the graph (each bracketed by HIP
+    events on the library's stream)."""
     def body():
         for i in range(n_launch):
             fn(dev, sets[i % len(sets)])
@@ -79,12 +81,12 @@ def time_launches_us(dev, fn, sets, n_launch, warm=1):
     for _ in range(warm):
         g.launch()
     dev.sync()
-    ms = time_graph_ms(dev, g)
+    ms = statistics.median(time_graph_ms(dev, g) for _ in range(reps))
     g.destroy()
     return ms * 1000.0 / n_launch
 
 
-def stream_ceiling(dev, n_in, n_out, nbytes, min_total=3 * MALL_BYTES, n_launch=40):
+def stream_ceiling(dev, n_in, n_out, nbytes, min_total=3 * MALL_BYTES, n_launch=100):
     """Practical ceiling of a byte mix: the fastest launch shape of the library's reference
     streaming kernel (hip_stream_ref: n_in reads and n_out writes of nbytes each, nothing
     else) over buffer sets that together exceed the Infinity Cache. Returns (us, shape)."""
@@ -195,7 +197,7 @@ def op_mix(shape, T, es):
             "norm_add": (2, 1, T * H * es), "norm_add_norm_next": (2, 2, T * H * es)}
 
 
-def bench_prefill(dev, shape, T, dtype, steps, warmup, ops_launches=40, thetas=None):
+def bench_prefill(dev, shape, T, dtype, steps, warmup, ops_launches=100, thetas=None):
     """thetas: RoPE bases the buffer sets alternate (c4: local 1e4 and global 1e6 layers),
     so consecutive chain steps and QK launches take both; the QK op is also timed at each
     base alone."""

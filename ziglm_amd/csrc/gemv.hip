@@ -838,9 +838,12 @@ __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(QT
 // Layout: LPR lanes per row (8, 16, 32 or 64) and 64 / LPR row sets of RW rows per wave; lane i
 // of a set takes blocks i, i + LPR, ... (bpl <= kQ4bMaxB of them) of each of its rows, every
 // weight load of the wave issued before any arithmetic (one memory round trip per wave).
-// x is staged once per workgroup in LDS, 36 floats per 32-column block (the padding keeps
-// the 16 lanes of a set, which read consecutive blocks, on distinct banks); each lane reads
-// its blocks' x there once and applies them to all its rows. Row sums: LPR-lane butterfly.
+// x is staged once per workgroup in LDS, 36 floats per 32-column block: the block's 32 values
+// and, at slot 32, their sum (the padding keeps the 16 lanes of a set, which read consecutive
+// blocks, on distinct banks); each lane reads its blocks' x there once and applies them to
+// all its rows. The sum is formed at staging, once per workgroup and block, not by each lane
+// for each of its blocks (31 additions per block, a quarter of a plain product's VALU work).
+// Row sums: LPR-lane butterfly.
 constexpr int kQ4bMaxB = 6;
 constexpr int kQ4bXStride = 36;
 constexpr int kQ4bMaxCols = 12288;    // x staged through registers: 12 float4 per thread at 256
@@ -853,6 +856,9 @@ constexpr int kQ4bProMaxCols = 4096;  // PRO operands: 4 float4 each per thread 
 #endif
 #ifndef ZL_GEMV_Q4B_WAVES
 #define ZL_GEMV_Q4B_WAVES 1024
+#endif
+#ifndef ZL_GEMV_Q4B_NW
+#define ZL_GEMV_Q4B_NW 4
 #endif
 typedef u32x4 u32x4_a4 __attribute__((aligned(4)));
 typedef uint32_t u32_a4 __attribute__((aligned(4)));
@@ -1063,14 +1069,40 @@ __global__ __launch_bounds__(NW * kWave) void k_gemv_q4b(GemvArgs a) {
 #pragma unroll
             for (int m = 0; m < NM; ++m) w[j][r][m].load(wrow[r][m] + off);
     }
-    // the input into LDS: float4 i of block i / 8 at slot offset 4 * (i % 8)
+    // the input into LDS: float4 i of block i / 8 at slot offset 4 * (i % 8), the block's sum
+    // at slot 32. Lanes 8j .. 8j+7 hold one block's float4s (T and 8 divide k * T), all in
+    // range or all out (n4 is a multiple of 64). The sum is ((v0 + v1) + v2) + v3, v_i the sum
+    // of float4s i and i + 4 (columns 4i.. and 16+4i..), each ((x + y) + (z + w)): DPP row
+    // shifts within the 8 lanes (v_i lands in lane 4 + i, the running sum moves up one lane a
+    // step and ends in lane 7; every lane read lies in the same 8-lane group).
     if constexpr (PRO) q4b_pro_finish<XK, T>(a, xv, rv, rwv, wnv, s_red);
+    // Staged block sums where a lane has few blocks of x to stage: at 64 lanes per row (more
+    // than 6144 columns) each thread stages 6+ float4s and the staging, which every wave waits
+    // for at the barrier, outlasts the additions it saves (2560 x 10240: 7.25 -> 7.55 us).
+    constexpr bool ssum = LPR < 64;
 #pragma unroll
     for (int k = 0; k < XK; ++k) {
         const int i = (int)threadIdx.x + k * T;
-        if (i < n4) *reinterpret_cast<f32x4*>(s_xq + (i >> 3) * kQ4bXStride + 4 * (i & 7)) = xv[k];
+        if (k * T >= n4) break;  // uniform
+        float bs = 0.0f;
+        if constexpr (ssum) {
+            const float s4 = i < n4 ? (xv[k].x + xv[k].y) + (xv[k].z + xv[k].w) : 0.0f;
+            const float v = s4 + dpp<0x114>(s4);  // row_shr:4
+            bs = v + dpp<0x111>(v);               // row_shr:1
+            bs = v + dpp<0x111>(bs);
+            bs = v + dpp<0x111>(bs);
+        }
+        if (i < n4) {
+            float* xs = s_xq + (i >> 3) * kQ4bXStride;
+            *reinterpret_cast<f32x4*>(xs + 4 * (i & 7)) = xv[k];
+            if (ssum && (i & 7) == 7) xs[32] = bs;
+        }
     }
     __syncthreads();
+    // nothing below moves above the barrier: the scheduler would otherwise start the first
+    // block's byte permutes there, and each wave would wait for its first weights before it
+    // arrives (and reads x) instead of after
+    __builtin_amdgcn_sched_barrier(0);
     float acc[RW][NM];
 #pragma unroll
     for (int r = 0; r < RW; ++r)
@@ -1087,8 +1119,13 @@ __global__ __launch_bounds__(NW * kWave) void k_gemv_q4b(GemvArgs a) {
             xh[i] = *reinterpret_cast<const f32x4*>(xs + 16 + 4 * i);
         }
         float sx = 0.0f;
+        if constexpr (ssum) {
+            sx = xs[32];
+        } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sx += ((xl[i].x + xl[i].y) + (xl[i].z + xl[i].w)) + ((xh[i].x + xh[i].y) + (xh[i].z + xh[i].w));
+            for (int i = 0; i < 4; ++i)
+                sx += ((xl[i].x + xl[i].y) + (xl[i].z + xl[i].w)) + ((xh[i].x + xh[i].y) + (xh[i].z + xh[i].w));
+        }
         const bool odd = b & 1;
 #pragma unroll
         for (int r = 0; r < RW; ++r)
@@ -1132,7 +1169,7 @@ static bool launch_q4b(const GemvArgs& a, hipStream_t s) {
     const size_t lds = (size_t)nblk * kQ4bXStride * sizeof(float);
     if (a.cols > (PRO ? kQ4bProMaxCols : kQ4bMaxCols) || lds > 65536) return false;
     // waves per workgroup: a prologue is paid once per workgroup, so its kernels take more
-    constexpr int NW = PRO ? ZL_GEMV_Q4B_PRO_WAVES : kGemvWaves;
+    constexpr int NW = PRO ? ZL_GEMV_Q4B_PRO_WAVES : ZL_GEMV_Q4B_NW;
     // 8 lanes per row only for block counts that 16 does not divide (8, 24, 40: e.g. the
     // per-layer-embedding projection's 256 columns)
     int lpr = nblk % 16 != 0 && nblk / 8 <= kQ4bMaxB ? 8 : 0;

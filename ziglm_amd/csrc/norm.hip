@@ -339,12 +339,15 @@ static void launch_wl(const NormArgs& a, int per_lane, int R, bool late, hipStre
 // per lane (3 for NORM_ADD_NORM, which also holds the second weight vector), so a row lives
 // in registers with few cross-wave reductions and every row of a 2048-token prefill is
 // resident at once; rows longer than that at 4 waves take up to 16 chunks per lane.
-// ZL_NORM_WAVES_PER_ROW and ZL_NORM_ROWS_PER_GROUP force values.
+// ZL_NORM_WAVES_PER_ROW, ZL_NORM_ROWS_PER_GROUP and ZL_NORM_LATE (0 / 1) force values.
 #ifndef ZL_NORM_WAVES_PER_ROW
 #define ZL_NORM_WAVES_PER_ROW 0
 #endif
 #ifndef ZL_NORM_ROWS_PER_GROUP
 #define ZL_NORM_ROWS_PER_GROUP 0
+#endif
+#ifndef ZL_NORM_LATE
+#define ZL_NORM_LATE -1
 #endif
 template <typename T, int MODE>
 static void launch_t(const NormArgs& a, hipStream_t s) {
@@ -364,10 +367,9 @@ static void launch_t(const NormArgs& a, hipStream_t s) {
     const int64_t waves = a.rows * W;
     const int R = ZL_NORM_ROWS_PER_GROUP ? ZL_NORM_ROWS_PER_GROUP
                   : waves >= 8192 || (MODE != M_NORM && waves >= 2048) ? 2 : 1;
-    // weights after the first row's activations (k_norm_rows), except for NORM_ADD, whose
-    // single weight vector measured faster with the activations (2048 x 2560 bf16: 7.15
-    // against 7.45 us)
-    const bool late = waves >= 1024 && MODE != M_NORM_ADD;
+    // weights after the first row's activations (k_norm_rows; NORM_ADD at 2048 x 2560 bf16,
+    // interleaved in-process rounds: 6.68 against 6.77 us with the activations)
+    const bool late = ZL_NORM_LATE >= 0 ? ZL_NORM_LATE != 0 : waves >= 1024;
     const bool vec = a.n % E == 0 && aligned16(a.x) && (MODE == M_NORM || aligned16(a.r)) &&
                      (MODE == M_NORM_ADD || aligned16(a.out)) && aligned16(a.w1) &&
                      (MODE != M_NORM_ADD_NORM || aligned16(a.w2)) && per_lane <= (W == 4 ? 16 : 8);
