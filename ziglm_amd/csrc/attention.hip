@@ -35,6 +35,8 @@ namespace zl {
 constexpr int kAttnThreads = ZL_ATTN_THREADS;  // k_attn workgroup
 constexpr int kMergeThreads = 256;             // k_attn_merge workgroup
 constexpr float kLog2e = 1.4426950408889634f;
+// A head row of zeros (head_dim <= 512) that loads with nothing to read point at.
+__device__ __attribute__((aligned(16))) float g_attn_pad_row[512];
 
 struct AttnArgs {
     const float* q;           // [batch][n_heads][D]
@@ -155,6 +157,28 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
     const int b = bk / a.nkv;
     const int h0 = kvh * a.gq + hgi * G;       // first query head of this workgroup
 
+    // The query rows (and in QK mode their norm factors) do not depend on the token's
+    // position: they go out first, ahead of the position read and of the K/V rows, so that
+    // the query is normalised and rotated while the K/V rows are in flight (waits count loads
+    // in issue order: issued after the K/V rows, the query would wait for all of them).
+    float q[G][8];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const float* qh = a.q + ((int64_t)b * a.nh + h0 + g) * D + li * 8;
+        const f32x4 x = ldf4(qh), y = ldf4(qh + 4);
+        q[g][0] = x.x; q[g][1] = x.y; q[g][2] = x.z; q[g][3] = x.w;
+        q[g][4] = y.x; q[g][5] = y.y; q[g][6] = y.z; q[g][7] = y.w;
+    }
+    // QK mode: the Q norm weights of this lane's slice
+    // (raw: the factors are formed where they are used, so nothing waits for these loads
+    // before the K/V rows are requested; a null weight reads as zeros through an empty range)
+    f32x4 wq0{}, wq1{};
+    if constexpr (QK) {
+        const auto rs = buf_rsrc(a.qk_wq, a.qk_wq ? (uint32_t)D * 4u : 0u);
+        wq0 = bldf4(rs, (uint32_t)li * 32u);
+        wq1 = bldf4(rs, (uint32_t)li * 32u + 16u);
+    }
+
     int start, end;
     int64_t rb;
     attn_range(a, b, start, end, rb);
@@ -177,63 +201,58 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
     // before any math, then folds them into its online softmax state in position order. A
     // position past the range loads the range's last row instead (in bounds, no per-lane
     // branch) and is not folded. The first step's rows are requested here, before the query
-    // is loaded and (QK mode) normalised and rotated, which does not need them.
+    // is (QK mode) normalised and rotated, which does not need them.
     constexpr int U = 4;
     const int nstep = t0 < tc ? (tc - t0 + U * SLOTS - 1) / (U * SLOTS) : 0;  // uniform
     float k[U][8], v[U][8];
+    // The first step's loads and the own-row loads below are issued on every path (no load
+    // under a branch): the compiler counts outstanding loads per path, and where paths with
+    // fewer loads join, its waits for the earlier loads (the query) become waits for all of
+    // them. With nothing to fold (nstep 0) the first step still loads, from row 0 of the
+    // sequence (or, for an invalid position, whose rows may lie outside the cache, from a
+    // zero row of this library): in bounds and never folded.
+    const bool rows_ok = end > 0;  // uniform
+    const KT* qsafe = (const KT*)g_attn_pad_row + li * 8;
     auto load_step = [&](int t) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int tu = min(t + u * SLOTS, tc - 1);
-            load8<KT>(kbase + (rb + tu) * a.row_stride, k[u]);
-            load8<KT>(vbase + (rb + tu) * a.row_stride, v[u]);
+            const int tu = max(min(t + u * SLOTS, tc - 1), 0);
+            load8<KT>(rows_ok ? kbase + (rb + tu) * a.row_stride : qsafe, k[u]);
+            load8<KT>(rows_ok ? vbase + (rb + tu) * a.row_stride : qsafe, v[u]);
         }
     };
-    if (nstep > 0) load_step(t0 + slot);
+    load_step(t0 + slot);
     // QK mode: the split holding the token's own position requests the raw K / V rows that
-    // position is formed from now (used after the loop), not after the loop.
+    // position is formed from (and the K norm factors) now, used after the loop; in the
+    // other splits the same loads read an empty range (zeros, no memory access).
     const bool own_here = own && t0 <= last && last < t1;  // block-uniform
-    f32x4 rk0{}, rk1{}, rv0{}, rv1{};
-    if (own_here) {
-        const float* kr = a.qk_k + ((int64_t)b * a.nkv + kvh) * D + li * 8;
-        const float* vr = a.qk_v + ((int64_t)b * a.nkv + kvh) * D + li * 8;
-        rk0 = ldf4(kr);
-        rk1 = ldf4(kr + 4);
-        rv0 = ldf4(vr);
-        rv1 = ldf4(vr + 4);
+    f32x4 rk0{}, rk1{}, rv0{}, rv1{}, wk0{}, wk1{};
+    if constexpr (QK) {
+        const uint32_t rowb = own_here ? (uint32_t)D * 4u : 0u;
+        const int64_t ro = ((int64_t)b * a.nkv + kvh) * D;
+        const auto rs_k = buf_rsrc(own_here ? a.qk_k + ro : a.q, rowb);
+        const auto rs_v = buf_rsrc(own_here ? a.qk_v + ro : a.q, rowb);
+        const auto rs_w = buf_rsrc(a.qk_wk ? a.qk_wk : a.q, a.qk_wk ? rowb : 0u);
+        const uint32_t o = (uint32_t)li * 32u;
+        rk0 = bldf4(rs_k, o);
+        rk1 = bldf4(rs_k, o + 16u);
+        rv0 = bldf4(rs_v, o);
+        rv1 = bldf4(rs_v, o + 16u);
+        wk0 = bldf4(rs_w, o);
+        wk1 = bldf4(rs_w, o + 16u);
     }
 
     if constexpr (QK) {
-        // cos / sin of the token's position for the rotary pairs, while the q loads fly
+        // cos / sin of the token's position for the rotary pairs, while the loads fly
         if (a.qk_half > 0 && tid < a.qk_half && end > 0) {
             const float theta = ((float)last * a.qk_freq_scale) / rope_denom(tid, 2 * a.qk_half, a.qk_log2_base);
             rope_sincos(theta, &s_sin[tid], &s_cos[tid]);
         }
-    }
-    float q[G][8];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        const float* qh = a.q + ((int64_t)b * a.nh + h0 + g) * D + li * 8;
-        const f32x4 x = ldf4(qh), y = ldf4(qh + 4);
-        q[g][0] = x.x; q[g][1] = x.y; q[g][2] = x.z; q[g][3] = x.w;
-        q[g][4] = y.x; q[g][5] = y.y; q[g][6] = y.z; q[g][7] = y.w;
-    }
-    // QK mode: per-element norm factors (1 + w), w or 1 of this lane's slice
-    auto norm_factors = [&](const float* w, float* f) {
-        if (w) {
-            const f32x4 x = ldf4(w + li * 8), y = ldf4(w + li * 8 + 4);
-            const float v[8] = {x.x, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
-#pragma unroll
-            for (int e = 0; e < 8; ++e) f[e] = a.qk_uo ? 1.0f + v[e] : v[e];
-        } else {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) f[e] = 1.0f;
-        }
-    };
-    if constexpr (QK) {
-        float fq[8];
-        norm_factors(a.qk_wq, fq);
         __syncthreads();  // the cos / sin table
+        const float wv[8] = {wq0.x, wq0.y, wq0.z, wq0.w, wq1.x, wq1.y, wq1.z, wq1.w};
+        float fq[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) fq[e] = a.qk_uo ? 1.0f + wv[e] : wv[e];
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             if (a.qk_wq) qk_norm8<LT>(q[g], D, a.qk_eps, fq);
@@ -284,8 +303,10 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
             // first head group's workgroup, writes it to the cache.
             float kn[8] = {rk0.x, rk0.y, rk0.z, rk0.w, rk1.x, rk1.y, rk1.z, rk1.w};
             float vn[8] = {rv0.x, rv0.y, rv0.z, rv0.w, rv1.x, rv1.y, rv1.z, rv1.w};
+            const float wv[8] = {wk0.x, wk0.y, wk0.z, wk0.w, wk1.x, wk1.y, wk1.z, wk1.w};
             float fk[8];
-            norm_factors(a.qk_wk, fk);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) fk[e] = a.qk_uo ? 1.0f + wv[e] : wv[e];
             if (a.qk_wk) qk_norm8<LT>(kn, D, a.qk_eps, fk);
             if (a.qk_vnorm) {
                 float one[8];
@@ -364,10 +385,10 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
 
 // Merge the splits of (token b, head h) over columns [64 y, 64 y + 64): one workgroup per
 // (b, h, y), over the sequence's non-empty splits. Every (m, l) pair and the first kMergePre
-// partials of each lane's column are loaded at once through range-checked loads (one memory
-// round trip before the first reduction); the per-split factors exp(m_s - M) and the total
-// L are formed in LDS, lane i of wave w sums column 64 y + i over splits w, w + 4, ... in
-// split order, and the four waves' sums are added in wave order.
+// partials of each lane's column are loaded at once through range-checked loads, with the
+// position read (one memory round trip before the first reduction); the per-split factors
+// exp(m_s - M) and the total L are formed in LDS, lane i of wave w sums column 64 y + i over
+// splits w, w + 4, ... in split order, and the four waves' sums are added in wave order.
 constexpr int kMaxSplit = 1024;
 constexpr int kMergeCols = kWave;
 #ifndef ZL_ATTN_MERGE_PRE
@@ -387,18 +408,11 @@ __global__ __launch_bounds__(kMergeThreads) void k_attn_merge(AttnArgs a) {
     const int tid = threadIdx.x;
     const int lane = tid % kWave, wv = tid / kWave;
     const int e = blockIdx.y * kMergeCols + lane;
-    int start, end, used;
-    int64_t rb;
-    attn_range(a, bh / a.nh, start, end, rb);
-    split_chunk(a, end - start, used);
-    float* out = a.out + (int64_t)bh * a.D;
-    if (used == 0) {
-        if (wv == 0) out[e] = 0.0f;
-        return;
-    }
+    // The loads go out before the position is read: over all nsplit splits of the workspace
+    // (reads past the last split give 0), the splits at or past `used` dropped below.
     const float* w = a.ws + (int64_t)bh * a.nsplit * (a.D + 2);
     const uint32_t rowb = (uint32_t)(a.D + 2) * 4u;
-    const auto rs = buf_rsrc(w, (uint32_t)used * rowb);  // reads past split used - 1 give 0
+    const auto rs = buf_rsrc(w, (uint32_t)a.nsplit * rowb);
     float mv[PER], lv[PER], pre[kMergePre];
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
@@ -408,6 +422,15 @@ __global__ __launch_bounds__(kMergeThreads) void k_attn_merge(AttnArgs a) {
     }
 #pragma unroll
     for (int k = 0; k < kMergePre; ++k) pre[k] = bldf(rs, (uint32_t)(wv + k * NW) * rowb + 8u + 4u * (uint32_t)e);
+    int start, end, used;
+    int64_t rb;
+    attn_range(a, bh / a.nh, start, end, rb);
+    split_chunk(a, end - start, used);
+    float* out = a.out + (int64_t)bh * a.D;
+    if (used == 0) {
+        if (wv == 0) out[e] = 0.0f;
+        return;
+    }
     float mx = -INFINITY;
 #pragma unroll
     for (int k = 0; k < PER; ++k)
