@@ -40,6 +40,9 @@
 namespace zl {
 
 constexpr int kMaxHalf = 256;  // head_dim <= 512
+// A head row of zeros that loads with nothing to read point at (k_qk_fused issues every
+// load of its first pass on every path).
+__device__ __attribute__((aligned(16))) float g_qk_pad_row[2 * kMaxHalf];
 
 struct RopeTab {
     float denom[kMaxHalf];
@@ -145,21 +148,22 @@ __global__ __launch_bounds__(256) void k_qk_fused(QkArgs a) {
 
     // Issue the weight loads (L2 hits after the first tokens: the barrier below waits on
     // them) and then the first head row's HBM loads, and evaluate the token's cos/sin table
-    // (no memory operands) while they are in flight.
+    // (no memory operands) while they are in flight. Every thread issues both (from an empty
+    // range or the zero row where there is nothing to read): the compiler counts outstanding
+    // loads per path, and were the head-row loads skipped on some path, the weights' wait
+    // before the barrier would wait for the head rows too.
     const int ti = threadIdx.x;
     // The norm weights go to LDS (read there per head, not held in registers): one f32x4
     // per thread (threads [0, D/4) stage wq, [D/4, D/2) stage wk; D <= 256 fits 256 threads).
     const bool has_wq = a.wq != nullptr, has_wk = a.wk != nullptr;
-    f32x4 wstage = {1.0f, 1.0f, 1.0f, 1.0f};
     const int wi = ti < D / 4 ? ti : ti - D / 4;  // thread -> float4 index in its vector
     const bool stage_q = ti < D / 4, stage_k = ti >= D / 4 && ti < D / 2;
-    if ((stage_q && has_wq) || (stage_k && has_wk)) wstage = ldf4((stage_q ? a.wq : a.wk) + 4 * wi);
-    u32x4 ra = {0, 0, 0, 0}, rb = {0, 0, 0, 0};
-    if (gslot < HR && active(gslot)) {
-        const T* src = src_of(gslot);
-        ra = lds16(src + c0 * E);
-        rb = lds16(src + c1 * E);
-    }
+    const bool wload = (stage_q && has_wq) || (stage_k && has_wk);
+    const auto rs_w = buf_rsrc(wload ? (stage_q ? a.wq : a.wk) : g_qk_pad_row, wload ? (uint32_t)D * 4u : 0u);
+    const f32x4 wstage = bldf4(rs_w, (uint32_t)wi * 16u);  // zeros when absent (factor 1 below)
+    const bool row_ok = gslot < HR && active(gslot);
+    const T* src0 = row_ok ? src_of(gslot) : (const T*)g_qk_pad_row;
+    u32x4 ra = lds16(src0 + c0 * E), rb = lds16(src0 + c1 * E);
     if (a.do_rope && ti < a.half) {
         const float theta = ((float)p * a.freq_scale) / rope_denom(ti, 2 * a.half, a.log2_base);
         rope_sincos(theta, &s_sin[ti], &s_cos[ti]);
