@@ -70,15 +70,17 @@ def time_graph_ms(dev, g, reps=1):
     return ms
 
 
-def time_launches_us(dev, fn, sets, n_launch, warm=1, reps=5):
+def time_launches_us(dev, fn, sets, n_launch, warm_ms=20.0, reps=5):
     """Microseconds per launch of fn(dev, set) over a graph of n_launch launches cycling
     through `sets`: the median over `reps` timed replays of the graph (each bracketed by HIP
-    events on the library's stream)."""
+    events on the library's stream), after untimed replays covering about warm_ms of GPU
+    time (the GPU at its working clocks, as in a run of back-to-back layers)."""
     def body():
         for i in range(n_launch):
             fn(dev, sets[i % len(sets)])
     g = Graph(dev, body)
-    for _ in range(warm):
+    first = time_graph_ms(dev, g)
+    for _ in range(min(200, int(warm_ms / max(first, 1e-3)))):
         g.launch()
     dev.sync()
     ms = statistics.median(time_graph_ms(dev, g) for _ in range(reps))

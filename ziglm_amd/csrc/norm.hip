@@ -336,7 +336,9 @@ static void launch_wl(const NormArgs& a, int per_lane, int R, bool late, hipStre
 }
 
 // Waves per row: the fewest (1, 2 or 4) that keep a row within 4 chunks (128-bit loads)
-// per lane (3 for NORM_ADD_NORM, which also holds the second weight vector), so a row lives
+// per lane (3 for NORM_ADD_NORM, which also holds the second weight vector; 6 for NORM_ADD,
+// whose one wave per row at 2048 x 2560 bf16 skips the cross-wave reduction: 6.57 -> 6.26 us,
+// 8192 x 5376 unchanged), so a row lives
 // in registers with few cross-wave reductions and every row of a 2048-token prefill is
 // resident at once; rows longer than that at 4 waves take up to 16 chunks per lane.
 // ZL_NORM_WAVES_PER_ROW, ZL_NORM_ROWS_PER_GROUP and ZL_NORM_LATE (0 / 1) force values.
@@ -345,6 +347,9 @@ static void launch_wl(const NormArgs& a, int per_lane, int R, bool late, hipStre
 #endif
 #ifndef ZL_NORM_ROWS_PER_GROUP
 #define ZL_NORM_ROWS_PER_GROUP 0
+#endif
+#ifndef ZL_NORM_FIT_ADD
+#define ZL_NORM_FIT_ADD 6
 #endif
 #ifndef ZL_NORM_LATE
 #define ZL_NORM_LATE -1
@@ -355,7 +360,7 @@ static void launch_t(const NormArgs& a, hipStream_t s) {
     const int nch = a.n / E;
     int W = ZL_NORM_WAVES_PER_ROW;
     if (W == 0) {
-        const int fit = MODE == M_NORM_ADD_NORM ? 3 : 4;
+        const int fit = MODE == M_NORM_ADD_NORM ? 3 : MODE == M_NORM_ADD ? ZL_NORM_FIT_ADD : 4;
         W = nch <= fit * kWave ? 1 : nch <= 2 * fit * kWave ? 2 : 4;
     }
     const int per_lane = (int)cdiv(nch, kWave * W);
