@@ -400,6 +400,16 @@ def test_qk_many_tokens_loop_over_head_rows(dev, oracle):
     qk_case(dev, oracle, B.F32, 80, 8, 1, 512, 128, 1e6, np.arange(10, 90), max_seq=1024)
 
 
+@pytest.mark.parametrize("dtype", [B.BF16, B.F32])
+def test_qk_two_tokens_per_workgroup_odd_count(dev, oracle, dtype):
+    """From 1024 tokens with every head row in one pass, a workgroup takes two tokens; an odd
+    token count leaves the last workgroup one token (its second slot reads and writes
+    nothing)."""
+    T = 1031
+    qk_case(dev, oracle, dtype, T, 8, 4, 256, 0, 10000.0, np.arange(3000, 3000 + T), max_seq=4096)
+    qk_case(dev, oracle, dtype, T, 8, 2, 256, 128, 1e6, np.arange(T)[::-1], max_seq=2048)
+
+
 def test_rope_mirrors(dev, oracle):
     nh, nkv, D = 8, 4, 256
     q = synth.normal_f32(9, "q", (nh, D))

@@ -44,6 +44,13 @@ constexpr int kMaxHalf = 256;  // head_dim <= 512
 // load of its first pass on every path).
 __device__ __attribute__((aligned(16))) float g_qk_pad_row[2 * kMaxHalf];
 
+#ifndef ZL_QK_TPW
+#define ZL_QK_TPW 2
+#endif
+#ifndef ZL_QK_TPW_MIN
+#define ZL_QK_TPW_MIN 1024
+#endif
+
 struct RopeTab {
     float denom[kMaxHalf];
 };
@@ -105,7 +112,7 @@ __host__ __device__ constexpr int qk_slots() {
     return 4 * (kWave / (D / 2 / Chunk<T>::E));
 }
 
-template <typename T, int D>
+template <typename T, int D, int TPW>
 __global__ __launch_bounds__(256) void k_qk_fused(QkArgs a) {
     using C = Chunk<T>;
     constexpr int E = C::E;
@@ -113,14 +120,15 @@ __global__ __launch_bounds__(256) void k_qk_fused(QkArgs a) {
     constexpr int LH = HALF / E;  // lanes per head
     constexpr int G = kWave / LH; // heads per wave
     static_assert(LH >= 1 && LH <= kWave && (LH & (LH - 1)) == 0, "bad head layout");
-    __shared__ float s_cos[HALF], s_sin[HALF];
+    __shared__ float s_cos[TPW][HALF], s_sin[TPW][HALF];
     __shared__ __attribute__((aligned(16))) float s_wq[D], s_wk[D];
 
-    const int t = blockIdx.x;
+    const int tb = blockIdx.x * TPW;  // the workgroup's first token (TPW tokens each)
     const int lane = threadIdx.x & 63;
     const int hl = lane & (LH - 1);
     constexpr int kSlots = qk_slots<T, D>();
-    // Workgroup (t, y) takes head rows y * kSlots + slot, + kSlots * gridDim.y, ...
+    // Workgroup (x, y) takes head rows y * kSlots + slot, + kSlots * gridDim.y, ... of each
+    // of its tokens.
     const int gslot = blockIdx.y * kSlots + (threadIdx.x >> 6) * G + lane / LH;
     const int hstep = kSlots * gridDim.y;
     // The lane's two chunks of a head row (E elements each): with rotary width r = 2 * half,
@@ -131,27 +139,35 @@ __global__ __launch_bounds__(256) void k_qk_fused(QkArgs a) {
     const int c1 = hl < R ? hl + R : c0 + 1;
     const int nq = a.q ? a.nh : 0;
     const int HR = a.nh + 2 * a.nkv;
-    const int p = token_pos(a, t);
-    const int64_t row = token_row(a, t, p);
+    int p[TPW];
+    int64_t row[TPW];
+    bool tok[TPW];
+#pragma unroll
+    for (int tt = 0; tt < TPW; ++tt) {
+        tok[tt] = tb + tt < a.n_tokens;  // uniform
+        p[tt] = tok[tt] ? token_pos(a, tb + tt) : 0;
+        row[tt] = tok[tt] ? token_row(a, tb + tt, p[tt]) : -1;
+    }
 
     // Head rows: [0, nh) Q, [nh, nh+nkv) K, [nh+nkv, nh+2nkv) V.
-    auto src_of = [&](int hr) -> const T* {
+    auto src_of = [&](int hr, int t) -> const T* {
         if (hr < a.nh) return (const T*)a.q + ((int64_t)t * a.nh + hr) * D;
         if (hr < a.nh + a.nkv) return (const T*)a.k + ((int64_t)t * a.nkv + (hr - a.nh)) * D;
         return (const T*)a.v + ((int64_t)t * a.nkv + (hr - a.nh - a.nkv)) * D;
     };
-    auto active = [&](int hr) -> bool {
+    auto active = [&](int hr, int tt) -> bool {
+        if (!tok[tt]) return false;
         if (hr < a.nh) return nq > 0;
-        if (hr < a.nh + a.nkv) return a.k != nullptr && row >= 0;
-        return a.v != nullptr && row >= 0;
+        if (hr < a.nh + a.nkv) return a.k != nullptr && row[tt] >= 0;
+        return a.v != nullptr && row[tt] >= 0;
     };
 
     // Issue the weight loads (L2 hits after the first tokens: the barrier below waits on
-    // them) and then the first head row's HBM loads, and evaluate the token's cos/sin table
-    // (no memory operands) while they are in flight. Every thread issues both (from an empty
-    // range or the zero row where there is nothing to read): the compiler counts outstanding
-    // loads per path, and were the head-row loads skipped on some path, the weights' wait
-    // before the barrier would wait for the head rows too.
+    // them) and then the first head row's HBM loads of every token, and evaluate the tokens'
+    // cos/sin tables (no memory operands) while they are in flight. Every thread issues all
+    // of them (from an empty range or the zero row where there is nothing to read): the
+    // compiler counts outstanding loads per path, and were the head-row loads skipped on
+    // some path, the weights' wait before the barrier would wait for the head rows too.
     const int ti = threadIdx.x;
     // The norm weights go to LDS (read there per head, not held in registers): one f32x4
     // per thread (threads [0, D/4) stage wq, [D/4, D/2) stage wk; D <= 256 fits 256 threads).
@@ -161,12 +177,20 @@ __global__ __launch_bounds__(256) void k_qk_fused(QkArgs a) {
     const bool wload = (stage_q && has_wq) || (stage_k && has_wk);
     const auto rs_w = buf_rsrc(wload ? (stage_q ? a.wq : a.wk) : g_qk_pad_row, wload ? (uint32_t)D * 4u : 0u);
     const f32x4 wstage = bldf4(rs_w, (uint32_t)wi * 16u);  // zeros when absent (factor 1 below)
-    const bool row_ok = gslot < HR && active(gslot);
-    const T* src0 = row_ok ? src_of(gslot) : (const T*)g_qk_pad_row;
-    u32x4 ra = lds16(src0 + c0 * E), rb = lds16(src0 + c1 * E);
-    if (a.do_rope && ti < a.half) {
-        const float theta = ((float)p * a.freq_scale) / rope_denom(ti, 2 * a.half, a.log2_base);
-        rope_sincos(theta, &s_sin[ti], &s_cos[ti]);
+    u32x4 ra[TPW], rb[TPW];
+#pragma unroll
+    for (int tt = 0; tt < TPW; ++tt) {
+        const bool row_ok = gslot < HR && active(gslot, tt);
+        const T* src0 = row_ok ? src_of(gslot, tb + tt) : (const T*)g_qk_pad_row;
+        ra[tt] = lds16(src0 + c0 * E);
+        rb[tt] = lds16(src0 + c1 * E);
+    }
+    if (a.do_rope) {
+        for (int i = ti; i < TPW * a.half; i += 256) {
+            const int tt = i / a.half, k = i - tt * a.half;
+            const float theta = ((float)p[tt] * a.freq_scale) / rope_denom(k, 2 * a.half, a.log2_base);
+            rope_sincos(theta, &s_sin[tt][k], &s_cos[tt][k]);
+        }
     }
     if (stage_q || stage_k) {
         const bool hw = stage_q ? has_wq : has_wk;
@@ -179,57 +203,62 @@ __global__ __launch_bounds__(256) void k_qk_fused(QkArgs a) {
     }
     __syncthreads();
 
-    for (int hr = gslot; hr < HR; hr += hstep) {
-        if (!active(hr)) continue;
-        if (hr != gslot) {
-            const T* src = src_of(hr);
-            ra = lds16(src + c0 * E);
-            rb = lds16(src + c1 * E);
-        }
-        const int kind = hr < a.nh ? 0 : hr < a.nh + a.nkv ? 1 : 2;  // Q, K, V
-        float x0[E], x1[E];
-        C::unpack(ra, x0);
-        C::unpack(rb, x1);
-        const bool norm = kind == 0 ? a.do_qnorm : kind == 1 ? a.do_knorm : a.v_norm;
-        if (norm) {
-            float ss = 0.0f;
 #pragma unroll
-            for (int j = 0; j < E; ++j) {
-                ss = fmaf(x0[j], x0[j], ss);
-                ss = fmaf(x1[j], x1[j], ss);
+    for (int tt = 0; tt < TPW; ++tt) {
+        const int t = tb + tt;
+        for (int hr = gslot; hr < HR; hr += hstep) {
+            if (!active(hr, tt)) continue;
+            u32x4 xa = ra[tt], xb = rb[tt];
+            if (hr != gslot) {
+                const T* src = src_of(hr, t);
+                xa = lds16(src + c0 * E);
+                xb = lds16(src + c1 * E);
             }
-            ss = group_sum<LH>(ss);
-            const float inv = rms_inv(ss, D, a.eps);
-            if (kind == 2) {  // Gemma-4 V: no-scale norm
+            const int kind = hr < a.nh ? 0 : hr < a.nh + a.nkv ? 1 : 2;  // Q, K, V
+            float x0[E], x1[E];
+            C::unpack(xa, x0);
+            C::unpack(xb, x1);
+            const bool norm = kind == 0 ? a.do_qnorm : kind == 1 ? a.do_knorm : a.v_norm;
+            if (norm) {
+                float ss = 0.0f;
 #pragma unroll
                 for (int j = 0; j < E; ++j) {
-                    x0[j] = x0[j] * inv;
-                    x1[j] = x1[j] * inv;
+                    ss = fmaf(x0[j], x0[j], ss);
+                    ss = fmaf(x1[j], x1[j], ss);
                 }
-            } else {
-                const float* sw = kind == 0 ? s_wq : s_wk;  // factors (1+w), w or 1
+                ss = group_sum<LH>(ss);
+                const float inv = rms_inv(ss, D, a.eps);
+                if (kind == 2) {  // Gemma-4 V: no-scale norm
+#pragma unroll
+                    for (int j = 0; j < E; ++j) {
+                        x0[j] = x0[j] * inv;
+                        x1[j] = x1[j] * inv;
+                    }
+                } else {
+                    const float* sw = kind == 0 ? s_wq : s_wk;  // factors (1+w), w or 1
+#pragma unroll
+                    for (int j = 0; j < E; ++j) {
+                        x0[j] = (x0[j] * inv) * sw[c0 * E + j];
+                        x1[j] = (x1[j] * inv) * sw[c1 * E + j];
+                    }
+                }
+            }
+            if (a.do_rope && kind != 2 && hl < R) {
 #pragma unroll
                 for (int j = 0; j < E; ++j) {
-                    x0[j] = (x0[j] * inv) * sw[c0 * E + j];
-                    x1[j] = (x1[j] * inv) * sw[c1 * E + j];
+                    const float c = s_cos[tt][hl * E + j], s = s_sin[tt][hl * E + j];
+                    const float v0 = x0[j], v1 = x1[j];
+                    x0[j] = v0 * c - v1 * s;
+                    x1[j] = v0 * s + v1 * c;
                 }
             }
+            T* dst;
+            if (kind == 0) dst = (T*)a.q + ((int64_t)t * a.nh + hr) * D;
+            else if (kind == 1) dst = (T*)a.kdst + row[tt] * a.row_stride + (int64_t)(hr - a.nh) * D;
+            else dst = (T*)a.vdst + row[tt] * a.row_stride + (int64_t)(hr - a.nh - a.nkv) * D;
+            sts16(dst + c0 * E, C::pack(x0));
+            sts16(dst + c1 * E, C::pack(x1));
         }
-        if (a.do_rope && kind != 2 && hl < R) {
-#pragma unroll
-            for (int j = 0; j < E; ++j) {
-                const float c = s_cos[hl * E + j], s = s_sin[hl * E + j];
-                const float v0 = x0[j], v1 = x1[j];
-                x0[j] = v0 * c - v1 * s;
-                x1[j] = v0 * s + v1 * c;
-            }
-        }
-        T* dst;
-        if (kind == 0) dst = (T*)a.q + ((int64_t)t * a.nh + hr) * D;
-        else if (kind == 1) dst = (T*)a.kdst + row * a.row_stride + (int64_t)(hr - a.nh) * D;
-        else dst = (T*)a.vdst + row * a.row_stride + (int64_t)(hr - a.nh - a.nkv) * D;
-        sts16(dst + c0 * E, C::pack(x0));
-        sts16(dst + c1 * E, C::pack(x1));
     }
 }
 
@@ -364,10 +393,21 @@ static void launch_qk_t(const QkArgs& a, const RopeTab& tab, hipStream_t s) {
         // (each pass would wait for its own loads); many tokens: the token's rows in turn.
         const int HR = a.nh + 2 * a.nkv;
         auto gy = [&](int slots) { return (unsigned)(a.n_tokens <= 64 ? std::max<int64_t>(1, cdiv(HR, slots)) : 1); };
-        if (a.D == 64) k_qk_fused<T, 64><<<dim3(grid, gy(qk_slots<T, 64>())), 256, 0, s>>>(a);
-        else if (a.D == 128) k_qk_fused<T, 128><<<dim3(grid, gy(qk_slots<T, 128>())), 256, 0, s>>>(a);
-        else if (a.D == 256) k_qk_fused<T, 256><<<dim3(grid, gy(qk_slots<T, 256>())), 256, 0, s>>>(a);
-        else k_qk_fused<T, 512><<<dim3(grid, gy(qk_slots<T, 512>())), 256, 0, s>>>(a);
+        // Two tokens per workgroup (the weight staging and the barrier shared by both) for
+        // launches with many tokens whose head rows fit one pass (Gemma-4B at 2048 tokens:
+        // 7.87 -> 7.76 us; with two passes per token the second token's passes follow the
+        // first's: Gemma-27B heads at 8192 tokens 43.8 -> 49.8 us, so one token there).
+        const unsigned grid2 = (unsigned)cdiv(a.n_tokens, 2);
+        auto go = [&](auto d_c) {
+            constexpr int DD = decltype(d_c)::value;
+            const bool two = ZL_QK_TPW == 2 && a.n_tokens >= ZL_QK_TPW_MIN && HR <= qk_slots<T, DD>();
+            if (two) k_qk_fused<T, DD, 2><<<dim3(grid2, gy(qk_slots<T, DD>())), 256, 0, s>>>(a);
+            else k_qk_fused<T, DD, 1><<<dim3(grid, gy(qk_slots<T, DD>())), 256, 0, s>>>(a);
+        };
+        if (a.D == 64) go(std::integral_constant<int, 64>{});
+        else if (a.D == 128) go(std::integral_constant<int, 128>{});
+        else if (a.D == 256) go(std::integral_constant<int, 256>{});
+        else go(std::integral_constant<int, 512>{});
     } else {
         const dim3 g2(grid, (unsigned)std::max<int64_t>(1, cdiv(a.nh + 2 * a.nkv, 4)));  // 4 head rows per workgroup
         k_qk_generic<T><<<g2, 256, 0, s>>>(a, tab);
