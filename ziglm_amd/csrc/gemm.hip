@@ -24,10 +24,16 @@
 // grid, each computing WT x WR tiles of 32 tokens x 32 rows with v_mfma_f32_32x32x16_bf16
 // (tokens on the A side, so a lane's accumulators are one weight row: the block scale is one
 // value per lane and tile, and stores of 32 lanes are 128 contiguous bytes of a token's output
-// row). The K loop takes one 32-column block per step: the workgroup loads the next block's X
-// (f32) and W (raw) into registers, converts the current one into bf16 terms in LDS
-// (rows padded to 80 bytes against bank conflicts), and runs the MFMAs; the global loads of
-// the next block are in flight meanwhile.
+// row). The K loop takes one 32-column block per step, software-pipelined: the LDS holds block
+// k as bf16 terms (rows padded to 80 bytes against bank conflicts) while registers hold block
+// k + 1's raw X (f32) and W; each wave reads all of block k's MFMA operands into registers, one
+// barrier frees the LDS, and block k's MFMAs then run from registers while the same waves
+// convert block k + 1 into the LDS and issue block k + 2's global loads, so the matrix cores
+// work during the conversion rather than after it. Loads take clamped (always valid) addresses
+// and select zeros afterwards, so the loop body has no branches and the compiler interleaves
+// the MFMAs with the conversion. Per 32-column block a 128 x 128 workgroup moves ~97 KB
+// through the LDS (80 KB of operand reads), about as many cycles at 128 bytes per clock as its
+// MFMAs take: LDS bandwidth bounds the kernel with the matrix cores.
 #include "zl_common.h"
 #include "zl_host.h"
 
@@ -112,22 +118,31 @@ __device__ __forceinline__ uint32_t ld_u32_unaligned(const unsigned char* p) {
     return *reinterpret_cast<const u32_a2*>(p);
 }
 
+// `blk` is always a valid block address (the caller clamps it); `ok` false gives zeros, selected
+// after the loads so that no load sits under a branch.
+__device__ __forceinline__ u32x4 sel4(bool ok, u32x4 v) { return ok ? v : u32x4{0, 0, 0, 0}; }
 template <int QT>
 __device__ __forceinline__ void load_w(const unsigned char* blk, int h, bool ok, WRaw<QT>& r) {
     if constexpr (QT == HIP_BRIDGE_Q4_0) {
-        r.d = ok ? *(const uint16_t*)blk : 0u;
-        r.q0 = ok ? ld_u32_unaligned(blk + 2 + 8 * h) : 0u;
-        r.q1 = ok ? ld_u32_unaligned(blk + 6 + 8 * h) : 0u;
+        const uint32_t d = *(const uint16_t*)blk, q0 = ld_u32_unaligned(blk + 2 + 8 * h),
+                       q1 = ld_u32_unaligned(blk + 6 + 8 * h);
+        r.d = ok ? d : 0u;
+        r.q0 = ok ? q0 : 0u;
+        r.q1 = ok ? q1 : 0u;
     } else if constexpr (QT == HIP_BRIDGE_Q8_0) {
-        r.d = ok ? *(const uint16_t*)blk : 0u;
+        const uint32_t d = *(const uint16_t*)blk;
+        r.d = ok ? d : 0u;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) r.q[i] = ok ? ld_u32_unaligned(blk + 2 + 16 * h + 4 * i) : 0u;
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t q = ld_u32_unaligned(blk + 2 + 16 * h + 4 * i);
+            r.q[i] = ok ? q : 0u;
+        }
     } else if constexpr (QT == HIP_BRIDGE_F32) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) r.v[i] = ok ? ld16(blk + 64 * h + 16 * i) : u32x4{0, 0, 0, 0};
+        for (int i = 0; i < 4; ++i) r.v[i] = sel4(ok, ld16(blk + 64 * h + 16 * i));
     } else {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) r.v[i] = ok ? ld16(blk + 32 * h + 16 * i) : u32x4{0, 0, 0, 0};
+        for (int i = 0; i < 2; ++i) r.v[i] = sel4(ok, ld16(blk + 32 * h + 16 * i));
     }
 }
 
@@ -140,7 +155,7 @@ template <int QT>
 __device__ __forceinline__ void store_w(const WRaw<QT>& r, int h, uint16_t* sw, int plane, int row, float* sd) {
     uint16_t* dst = sw + row * kLdsRow;
     if constexpr (QT == HIP_BRIDGE_Q4_0) {
-        if (h == 0) sd[row] = f16_bits_to_f32(r.d);
+        sd[row] = f16_bits_to_f32(r.d);  // both halves store the same value
         // byte j: low nibble = element j, high nibble = element j + 16 (value - 8)
         uint32_t lo[4], hi[4];
         const uint32_t q[2] = {r.q0, r.q1};
@@ -156,7 +171,7 @@ __device__ __forceinline__ void store_w(const WRaw<QT>& r, int h, uint16_t* sw, 
         *reinterpret_cast<u32x4*>(dst + 8 * h) = u32x4{lo[0], lo[1], lo[2], lo[3]};
         *reinterpret_cast<u32x4*>(dst + 16 + 8 * h) = u32x4{hi[0], hi[1], hi[2], hi[3]};
     } else if constexpr (QT == HIP_BRIDGE_Q8_0) {
-        if (h == 0) sd[row] = f16_bits_to_f32(r.d);
+        sd[row] = f16_bits_to_f32(r.d);  // both halves store the same value
         uint32_t p[8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -245,11 +260,12 @@ __global__ __launch_bounds__(kGemmThreads, 2) void k_gemm_mfma(GemmArgs a) {
     // X staging: chunk c = tid + 256 i (i < BT * 8 / 256) is token c / 8, columns 4 (c % 8) ...
     constexpr int XCH = BT * 8 / kGemmThreads;
     f32x4 xr[XCH];
-    auto load_x = [&](int kb) {
+    auto load_x = [&](int kb) {  // kb < nkb; tokens past the batch read the last token, then zeros
 #pragma unroll
         for (int i = 0; i < XCH; ++i) {
             const int c = tid + kGemmThreads * i, tok = b_base + c / 8;
-            xr[i] = tok < a.batch ? ldf4(a.x + (int64_t)tok * a.cols + kb * kKB + 4 * (c % 8)) : f32x4{0, 0, 0, 0};
+            const f32x4 v = ldf4(a.x + (int64_t)min(tok, a.batch - 1) * a.cols + kb * kKB + 4 * (c % 8));
+            xr[i] = tok < a.batch ? v : f32x4{0, 0, 0, 0};
         }
     };
     auto store_x = [&]() {
@@ -275,14 +291,14 @@ __global__ __launch_bounds__(kGemmThreads, 2) void k_gemm_mfma(GemmArgs a) {
             const int gr = r_base + row;
             const bool ok = hr < 2 * BR && gr < a.rows;
             const int64_t blk_bytes = QT == HIP_BRIDGE_Q4_0 ? 18 : QT == HIP_BRIDGE_Q8_0 ? 34 : QT == HIP_BRIDGE_F32 ? 128 : 64;
-            load_w<QT>(a.w + (int64_t)(ok ? gr : 0) * a.row_bytes + (int64_t)kb * blk_bytes, h, ok, wr[i]);
+            load_w<QT>(a.w + (int64_t)min(gr, a.rows - 1) * a.row_bytes + (int64_t)kb * blk_bytes, h, ok, wr[i]);
         }
     };
     auto store_wt = [&]() {
 #pragma unroll
         for (int i = 0; i < WPASS; ++i) {
             const int hr = tid + kGemmThreads * i;
-            if (hr < 2 * BR) store_w<QT>(wr[i], hr & 1, sw, WPLANE, hr >> 1, sd);
+            if (2 * BR >= kGemmThreads || hr < 2 * BR) store_w<QT>(wr[i], hr & 1, sw, WPLANE, hr >> 1, sd);
         }
     };
 
@@ -295,38 +311,50 @@ __global__ __launch_bounds__(kGemmThreads, 2) void k_gemm_mfma(GemmArgs a) {
 #pragma unroll
         for (int j = 0; j < WR; ++j) acc[i][j] = f32x16{};
 
+    // Pipeline: LDS holds block kb while the raw registers hold block kb + 1. Each wave reads
+    // all of block kb's MFMA operands (and scales) from LDS into registers, one barrier frees
+    // the LDS, and then block kb's MFMAs run from registers while the same waves convert block
+    // kb + 1 into the LDS (and issue block kb + 2's loads): the MFMAs overlap the conversion's
+    // VALU and LDS work instead of following it.
+    constexpr int NP = TermPairs<NW>::n;
     load_x(0);
     load_wt(0);
+    store_x();
+    store_wt();
+    __syncthreads();
+    load_x(min(1, nkb - 1));
+    load_wt(min(1, nkb - 1));
     for (int kb = 0; kb < nkb; ++kb) {
-        store_x();
-        store_wt();
-        __syncthreads();
-        if (kb + 1 < nkb) {  // the next block's loads fly during this block's MFMAs
-            load_x(kb + 1);
-            load_wt(kb + 1);
-        }
-        constexpr int NP = TermPairs<NW>::n;
+        bf16x8 xa[2][WT][3], wb[2][WR][NW];
+        float dv[WR];
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {  // two K = 16 halves of the block
             const int ko = 16 * ks + 8 * (lane >> 5);
-            bf16x8 xa[WT][3], wb[WR][NW];
 #pragma unroll
             for (int i = 0; i < WT; ++i)
 #pragma unroll
                 for (int u = 0; u < 3; ++u)
-                    xa[i][u] = *reinterpret_cast<const bf16x8*>(sx + u * XPLANE + (wt0 + 32 * i + (lane & 31)) * kLdsRow + ko);
+                    xa[ks][i][u] = *reinterpret_cast<const bf16x8*>(sx + u * XPLANE + (wt0 + 32 * i + (lane & 31)) * kLdsRow + ko);
 #pragma unroll
             for (int j = 0; j < WR; ++j)
 #pragma unroll
                 for (int u = 0; u < NW; ++u)
-                    wb[j][u] = *reinterpret_cast<const bf16x8*>(sw + u * WPLANE + (wr0 + 32 * j + (lane & 31)) * kLdsRow + ko);
+                    wb[ks][j][u] = *reinterpret_cast<const bf16x8*>(sw + u * WPLANE + (wr0 + 32 * j + (lane & 31)) * kLdsRow + ko);
+        }
+        if constexpr (SCALED) {
+#pragma unroll
+            for (int j = 0; j < WR; ++j) dv[j] = sd[wr0 + 32 * j + (lane & 31)];
+        }
+        __syncthreads();  // every wave holds block kb's operands: the LDS is free
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
             for (int i = 0; i < WT; ++i)
 #pragma unroll
                 for (int j = 0; j < WR; ++j)
 #pragma unroll
                     for (int p = 0; p < NP; ++p) {
-                        const bf16x8 A = xa[i][TermPairs<NW>::xt[p]], Bv = wb[j][TermPairs<NW>::wt[p]];
+                        const bf16x8 A = xa[ks][i][TermPairs<NW>::xt[p]], Bv = wb[ks][j][TermPairs<NW>::wt[p]];
                         if constexpr (SCALED) {
                             part[i][j] = (ks == 0 && p == 0)
                                              ? __builtin_amdgcn_mfma_f32_32x32x16_bf16(A, Bv, f32x16{}, 0, 0, 0)
@@ -335,18 +363,21 @@ __global__ __launch_bounds__(kGemmThreads, 2) void k_gemm_mfma(GemmArgs a) {
                             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A, Bv, acc[i][j], 0, 0, 0);
                         }
                     }
-        }
+        // block kb + 1 into the LDS (after the last block: a copy nobody reads), block kb + 2's
+        // loads in flight (past the end: the last block again, unused)
+        store_x();
+        store_wt();
+        load_x(min(kb + 2, nkb - 1));
+        load_wt(min(kb + 2, nkb - 1));
         if constexpr (SCALED) {
 #pragma unroll
-            for (int j = 0; j < WR; ++j) {
-                const float d = sd[wr0 + 32 * j + (lane & 31)];
+            for (int j = 0; j < WR; ++j)
 #pragma unroll
                 for (int i = 0; i < WT; ++i)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) acc[i][j][r] = fmaf(d, part[i][j][r], acc[i][j][r]);
-            }
+                    for (int r = 0; r < 16; ++r) acc[i][j][r] = fmaf(dv[j], part[i][j][r], acc[i][j][r]);
         }
-        __syncthreads();
+        __syncthreads();  // block kb + 1 is in the LDS
     }
 
     // Epilogue: lane (l, r) of tile (i, j) holds token 8 (r / 4) + 4 (l / 32) + r % 4 and row l % 32.
