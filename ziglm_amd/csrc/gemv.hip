@@ -1212,6 +1212,213 @@ static bool launch_q4b(const GemvArgs& a, hipStream_t s) {
     }
 }
 
+// Batch-1 Q4_K products, the block kernel's scheme over 64-column chunks. A Q4_K super-block
+// (144 bytes, 256 columns: f16 d, f16 dmin, 12 bytes of packed 6-bit scales and mins, 128 quant
+// bytes; types.zig:170-175) holds four chunks; chunk jj is sub-blocks 2jj (the low nibbles of
+// quant bytes 32jj .. 32jj+31, columns 64jj ..) and 2jj+1 (their high nibbles, columns
+// 64jj+32 ..). A lane takes whole chunks with three 16-byte loads (the super-block's 16-byte
+// header and the chunk's 32 quant bytes; rows are 144n bytes, so 16-byte aligned with the
+// matrix): the group-wise loops issue five 32-bit loads per 8 columns. x is staged per
+// workgroup at 72 floats per chunk, its two sub-block sums at slots 64 and 65 (the padding puts
+// the 8 lanes of a set, which read consecutive chunks, on distinct banks). Arithmetic as the
+// group kernels: (d sc_j) sum(q x) - (dmin m_j) sum(x) per sub-block (math.zig:440-496).
+constexpr int kQ4kbXStride = 72;
+struct KChunk {
+    u32x4 h;       // d | dmin << 16, scale bytes 0..3, 4..7, 8..11
+    u32x4 q0, q1;  // the chunk's quant bytes 0..15, 16..31
+    __device__ __forceinline__ void load(const unsigned char* sb, uint32_t jj) {
+        h = *reinterpret_cast<const u32x4*>(sb);
+        q0 = *reinterpret_cast<const u32x4*>(sb + 16u + 32u * jj);
+        q1 = *reinterpret_cast<const u32x4*>(sb + 32u + 32u * jj);
+    }
+    // xs: the chunk's x in LDS (columns 0..31 / 32..63, sub-blocks 2jj / 2jj+1, at slots 0 / 32,
+    // their sums at 64 / 65), read one sub-block at a time.
+    __device__ __forceinline__ float dot(uint32_t jj, const float* xs) const {
+        // 6-bit scale / min of sub-blocks 2jj and 2jj+1 (quant.zig:285-290): bytes t, t+1
+        // (t = 2 (jj & 1)) of the three scale words
+        // (selects rather than a branch: jj differs between lanes)
+        const uint32_t sft = (jj & 1u) * 16u;
+        const uint32_t A = h.y >> sft, Bw = h.z >> sft, C = h.w >> sft;
+        const bool lo = jj < 2;
+        const uint32_t sc0 = lo ? A & 63u : (C & 15u) | (((A >> 6) & 3u) << 4);
+        const uint32_t sc1 = lo ? (A >> 8) & 63u : ((C >> 8) & 15u) | (((A >> 14) & 3u) << 4);
+        const uint32_t m0 = lo ? Bw & 63u : ((C >> 4) & 15u) | (((Bw >> 6) & 3u) << 4);
+        const uint32_t m1 = lo ? (Bw >> 8) & 63u : ((C >> 12) & 15u) | (((Bw >> 14) & 3u) << 4);
+        const uint32_t q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+        float t[2];
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {  // low nibbles: columns 4i.., high: 32+4i..
+            f32x4 xv[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) xv[i] = *reinterpret_cast<const f32x4*>(xs + 32 * hf + 4 * i);
+            float acc = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t u = mask_bytes(hf ? q[i] >> 4 : q[i], 0x0f0f0f0fu);
+                acc = i == 0 ? (float)(u & 0xff) * xv[0].x : fmaf((float)(u & 0xff), xv[i].x, acc);
+                acc = fmaf((float)((u >> 8) & 0xff), xv[i].y, acc);
+                acc = fmaf((float)((u >> 16) & 0xff), xv[i].z, acc);
+                acc = fmaf((float)(u >> 24), xv[i].w, acc);
+            }
+            t[hf] = acc;
+        }
+        const float d = h2f(h.x & 0xffffu), dmin = h2f(h.x >> 16);
+        const float d0 = d * (float)sc0, d1 = d * (float)sc1;
+        const float n0 = dmin * (float)m0, n1 = dmin * (float)m1;
+        return fmaf(d0, t[0], -(n0 * xs[64])) + fmaf(d1, t[1], -(n1 * xs[65]));
+    }
+};
+
+// (3 waves per SIMD: up to 168 registers, which five chunks of weights, a chunk of x and the
+// prologue's operands take without spilling)
+template <int MODE, int LPR, int RW, int BPL, bool PRO, int NW>
+__global__ __launch_bounds__(NW * kWave, 12 / NW) void k_gemv_q4kb(GemvArgs a) {
+    constexpr int T = NW * kWave;
+    constexpr int NM = MODE == GV_GEGLU ? 2 : 1;
+    constexpr int SETS = kWave / LPR;
+    constexpr int XK = (PRO ? kQ4bProMaxCols : kQ4bMaxCols) / 4 / T;  // x float4 per thread
+    extern __shared__ __attribute__((aligned(16))) float s_xq[];
+    __shared__ float s_red[NW];
+    const int lane = threadIdx.x & 63;
+    const int wv = threadIdx.x >> 6;
+    const int li = lane % LPR, set = lane / LPR;
+    const int row0 = ((blockIdx.x * NW + wv) * SETS + set) * RW;
+    const int n4 = a.cols / 4;
+    f32x4 xv[XK], rv[PRO ? XK : 1], rwv[PRO ? XK : 1], wnv[PRO ? XK : 1];
+    if constexpr (PRO) {
+        q4b_pro_load<XK, T>(a, xv, rv, rwv, wnv);
+    } else {
+#pragma unroll
+        for (int k = 0; k < XK; ++k) {
+            const int i = (int)threadIdx.x + k * T;
+            if (i < n4) xv[k] = ldf4(a.x + 4 * i);
+        }
+    }
+    const unsigned char* wrow[RW][NM];
+    float* yrow[RW];
+    const int r0 = a.seg[0].rows, r1 = a.nseg > 1 ? a.seg[1].rows : 0;
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+        const bool ok = row0 + r < a.total_rows;
+        const int R = ok ? row0 + r : a.total_rows - 1;  // past the end: the last row, not written
+        const bool s0 = R < r0, s1 = !s0 && R - r0 < r1;
+        const int Rs = s0 ? R : s1 ? R - r0 : R - r0 - r1;
+        const unsigned char* wb = s0 ? a.seg[0].w : s1 ? a.seg[1].w : a.seg[2].w;
+        float* yb = s0 ? a.seg[0].y : s1 ? a.seg[1].y : a.seg[2].y;
+        wrow[r][0] = wb + (int64_t)Rs * a.row_bytes;
+        if constexpr (NM == 2) wrow[r][1] = a.w_up + (int64_t)Rs * a.row_bytes;
+        yrow[r] = ok ? yb + Rs : nullptr;
+    }
+    KChunk w[BPL][RW][NM];
+#pragma unroll
+    for (int j = 0; j < BPL; ++j) {
+        const uint32_t c = (uint32_t)(li + LPR * j);
+        const uint32_t off = (c >> 2) * 144u;
+#pragma unroll
+        for (int r = 0; r < RW; ++r)
+#pragma unroll
+            for (int m = 0; m < NM; ++m) w[j][r][m].load(wrow[r][m] + off, c & 3u);
+    }
+    if constexpr (PRO) q4b_pro_finish<XK, T>(a, xv, rv, rwv, wnv, s_red);
+    // x into LDS: float4 i at chunk i / 16, slot 4 (i % 16); the sum of each sub-block's 8
+    // float4s (lanes 8j .. 8j+7) at slot 64 + (i / 8) % 2, formed by DPP row shifts as in the
+    // Q4_0 kernel: ((v0 + v1) + v2) + v3, v_i the sum of float4s i and i + 4 of the sub-block.
+#pragma unroll
+    for (int k = 0; k < XK; ++k) {
+        const int i = (int)threadIdx.x + k * T;
+        if (k * T >= n4) break;  // uniform
+        const float s4 = i < n4 ? (xv[k].x + xv[k].y) + (xv[k].z + xv[k].w) : 0.0f;
+        const float v = s4 + dpp<0x114>(s4);  // row_shr:4
+        float bs = v + dpp<0x111>(v);         // row_shr:1
+        bs = v + dpp<0x111>(bs);
+        bs = v + dpp<0x111>(bs);
+        if (i < n4) {
+            float* xs = s_xq + (i >> 4) * kQ4kbXStride;
+            *reinterpret_cast<f32x4*>(xs + 4 * (i & 15)) = xv[k];
+            if ((i & 7) == 7) xs[64 + ((i >> 3) & 1)] = bs;
+        }
+    }
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+    float acc[RW][NM];
+#pragma unroll
+    for (int r = 0; r < RW; ++r)
+#pragma unroll
+        for (int m = 0; m < NM; ++m) acc[r][m] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < BPL; ++j) {
+        const uint32_t c = (uint32_t)(li + LPR * j);
+        const float* xs = s_xq + c * kQ4kbXStride;
+#pragma unroll
+        for (int r = 0; r < RW; ++r)
+#pragma unroll
+            for (int m = 0; m < NM; ++m) acc[r][m] += w[j][r][m].dot(c & 3u, xs);
+    }
+#pragma unroll
+    for (int r = 0; r < RW; ++r)
+#pragma unroll
+        for (int m = 0; m < NM; ++m) acc[r][m] = group_sum<LPR>(acc[r][m]);
+    if (li == 0) {
+#pragma unroll
+        for (int r = 0; r < RW; ++r) {
+            if (!yrow[r]) continue;
+            float out = acc[r][0];
+            if constexpr (MODE == GV_GEGLU) out = gelu_fast(acc[r][0]) * acc[r][1];
+            *yrow[r] = out;
+        }
+    }
+}
+
+#ifndef ZL_GEMV_Q4KB
+#define ZL_GEMV_Q4KB 1
+#endif
+// Launches k_gemv_q4kb for batch-1 Q4_K products with a whole number of 8-chunk groups per row
+// (cols % 512 == 0), at most kQ4bMaxB chunks per lane at 8 to 64 lanes per row, 16-byte
+// aligned matrices and x within the LDS; returns false otherwise. Lanes per row as the Q4_0
+// kernel's (the fewest that take every chunk in kQ4bMaxB steps, more while the grid has under
+// ZL_GEMV_Q4B_WAVES waves); one row per set.
+template <int QT, int MODE, bool PRO>
+static bool launch_q4kb(const GemvArgs& a, hipStream_t s) {
+    // (not the GeGLU pair: holding both matrices' chunks, the compiler converts every quant of
+    // a chunk to f32 ahead of the arithmetic and runs out of registers)
+    if constexpr (QT != HIP_BRIDGE_Q4_K || MODE == GV_GEGLU) {
+        return false;
+    } else {
+    if (!ZL_GEMV_Q4KB || a.batch != 1 || a.cols % 512 != 0) return false;
+    for (int i = 0; i < a.nseg; ++i)
+        if (a.seg[i].rows > 0 && !aligned16(a.seg[i].w)) return false;
+    if (MODE == GV_GEGLU && !aligned16(a.w_up)) return false;
+    const int nch = a.cols / 64;
+    const size_t lds = (size_t)nch * kQ4kbXStride * sizeof(float);
+    if (a.cols > (PRO ? kQ4bProMaxCols : kQ4bMaxCols) || lds > 65536) return false;
+    constexpr int NW = PRO ? ZL_GEMV_Q4B_PRO_WAVES : ZL_GEMV_Q4B_NW;
+    int lpr = 0;
+    for (int l : {8, 16, 32, 64})
+        if (!lpr && nch % l == 0 && nch / l <= kQ4bMaxB) lpr = l;
+    if (!lpr) return false;
+    auto waves = [&](int l) { return cdiv(a.total_rows, (int64_t)(kWave / l)); };
+    while (lpr < 64 && waves(lpr) < ZL_GEMV_Q4B_WAVES && nch % (2 * lpr) == 0) lpr *= 2;
+    const int bpl = nch / lpr;
+    const unsigned grid = (unsigned)cdiv(waves(lpr), (int64_t)NW);
+    auto go = [&](auto lpr_c) {
+        constexpr int L = decltype(lpr_c)::value;
+        switch (bpl) {
+            case 1: k_gemv_q4kb<MODE, L, 1, 1, PRO, NW><<<grid, NW * kWave, lds, s>>>(a); break;
+            case 2: k_gemv_q4kb<MODE, L, 1, 2, PRO, NW><<<grid, NW * kWave, lds, s>>>(a); break;
+            case 3: k_gemv_q4kb<MODE, L, 1, 3, PRO, NW><<<grid, NW * kWave, lds, s>>>(a); break;
+            case 4: k_gemv_q4kb<MODE, L, 1, 4, PRO, NW><<<grid, NW * kWave, lds, s>>>(a); break;
+            case 5: k_gemv_q4kb<MODE, L, 1, 5, PRO, NW><<<grid, NW * kWave, lds, s>>>(a); break;
+            default: k_gemv_q4kb<MODE, L, 1, 6, PRO, NW><<<grid, NW * kWave, lds, s>>>(a); break;
+        }
+    };
+    if (lpr == 8) go(std::integral_constant<int, 8>{});
+    else if (lpr == 16) go(std::integral_constant<int, 16>{});
+    else if (lpr == 32) go(std::integral_constant<int, 32>{});
+    else go(std::integral_constant<int, 64>{});
+    return true;
+    }
+}
+
 // Any alignment / column count: one workgroup per row, scalar dequantisation per element.
 template <int QT>
 __device__ __forceinline__ float w_elem(const unsigned char* row, int c) {
@@ -1320,8 +1527,8 @@ static void launch_vec(const GemvArgs& a, hipStream_t s) {
     constexpr int H = MODE == GV_GEGLU ? 2 : 1;
     const unsigned g8 = (unsigned)cdiv(a.total_rows, 8 / H), g4 = (unsigned)cdiv(a.total_rows, 4 / H),
                    g2 = (unsigned)cdiv(a.total_rows, 2 / H);
-    if (PRO && launch_q4b<QT, MODE, true>(a, s)) {
-        // launched: batch-1 Q4_0 block kernel with the prologue
+    if (PRO && (launch_q4b<QT, MODE, true>(a, s) || launch_q4kb<QT, MODE, true>(a, s))) {
+        // launched: batch-1 Q4_0 / Q8_0 / Q4_K block kernel with the prologue
     } else if (PRO) {  // batch 1; the input vector in dynamic LDS; at most kGemvProGrid workgroups
         const size_t lds = (size_t)a.cols * sizeof(float);
         const unsigned cap = kGemvProGrid;
@@ -1344,8 +1551,8 @@ static void launch_vec(const GemvArgs& a, hipStream_t s) {
             constexpr int RP = F > 0 ? std::max(1, F / H) : 2 / H;
             k_gemv<QT, RP, 1, MODE><<<(unsigned)cdiv(a.total_rows, RP), kGemvThreads, 0, s>>>(a);
         }
-    } else if (launch_q4b<QT, MODE, false>(a, s)) {
-        // launched: batch-1 Q4_0 with 256-column multiples
+    } else if (launch_q4b<QT, MODE, false>(a, s) || launch_q4kb<QT, MODE, false>(a, s)) {
+        // launched: batch-1 Q4_0 / Q8_0 with 256-column multiples, Q4_K with 512
     } else if (MODE == GV_PLAIN && a.batch == 1 && a.total_rows >= kGemvWaveRowsMin && a.cols <= kGemvWaveColsMax &&
                QT != HIP_BRIDGE_F16 && QT != HIP_BRIDGE_BF16 && QT != HIP_BRIDGE_F32) {
         // (k_gemv_w is instantiated for these cases only)
