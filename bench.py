@@ -47,6 +47,10 @@ from ziglm_amd.device import HipDevice  # noqa: E402
 PEAK_HBM_GBS = 8000.0  # MI355X HBM3E peak
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 matrix peak
 MALL_BYTES = 256 << 20
+# --eager: op timings launch from the host between events instead of replaying graphs (for
+# kernel traces: rocprofv3 --kernel-trace faults inside its graph-launch interception after
+# many replays)
+EAGER = False
 METRIC = "fused-op HBM GB/s (% of MI355X peak) + µs per Gemma layer, decode & 2k prefill"
 
 
@@ -74,7 +78,22 @@ def time_launches_us(dev, fn, sets, n_launch, warm_ms=20.0, reps=5):
     """Microseconds per launch of fn(dev, set) over a graph of n_launch launches cycling
     through `sets`: the median over `reps` timed replays of the graph (each bracketed by HIP
     events on the library's stream), after untimed replays covering about warm_ms of GPU
-    time (the GPU at its working clocks, as in a run of back-to-back layers)."""
+    time (the GPU at its working clocks, as in a run of back-to-back layers). With EAGER, the
+    n_launch launches are made from the host between two events, after one warm-up pass."""
+    if EAGER:
+        for st in sets:
+            fn(dev, st)
+        dev.sync()
+        e0, e1 = dev.event(), dev.event()
+        dev.record(e0)
+        for i in range(n_launch):
+            fn(dev, sets[i % len(sets)])
+        dev.record(e1)
+        ms = dev.elapsed_ms(e0, e1)
+        dev.b.hip_event_destroy(e0)
+        dev.b.hip_event_destroy(e1)
+        return ms * 1000.0 / n_launch
+
     def body():
         for i in range(n_launch):
             fn(dev, sets[i % len(sets)])
@@ -741,7 +760,7 @@ def main():
     ap.add_argument("--only", default=None, help="run one op only (profiling): a chain op, "
                     "gather_q8_0 / gather_q4_0 / gather_bf16 (c3), gemv, gemm, decode_step, gguf_decode, "
                     "or 'copy' = hipMemcpy device-to-device of the GeGLU output size (counter calibration)")
-    ap.add_argument("--eager", action="store_true", help="with --only: launch eagerly, no graph")
+    ap.add_argument("--eager", action="store_true", help="with --only: launch eagerly, no graph (kernel traces)")
     ap.add_argument("--config", default="c2", choices=["c2", "c4"])
     a = ap.parse_args()
     if a.gpus != 1:
@@ -751,6 +770,8 @@ def main():
               file=sys.stderr)
         sys.exit(2)
 
+    global EAGER
+    EAGER = bool(a.only and a.eager)
     dev = HipDevice()
     log(f"device {dev.name} {dev.total_vram_bytes / 2**30:.0f} GiB, {dev.b.version()}")
     shape, T = (LY.GEMMA_4B, 2048) if a.config == "c2" else (LY.GEMMA_27B, 8192)
