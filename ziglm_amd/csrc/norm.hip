@@ -325,6 +325,7 @@ static void launch_w(const NormArgs& a, int per_lane, int R, hipStream_t s) {
     else if (per_lane <= 2) k_norm_rows<T, 2, MODE, W, 1, WL><<<grid1, NT, 0, s>>>(a);
     else if (per_lane <= 3) k_norm_rows<T, 3, MODE, W, 1, WL><<<grid1, NT, 0, s>>>(a);
     else if (per_lane <= 4) k_norm_rows<T, 4, MODE, W, 1, WL><<<grid1, NT, 0, s>>>(a);
+    else if (per_lane <= 5 && MODE == M_NORM_ADD) k_norm_rows<T, 5, MODE, W, 1, WL><<<grid1, NT, 0, s>>>(a);
     else if (per_lane <= 6) k_norm_rows<T, 6, MODE, W, 1, WL><<<grid1, NT, 0, s>>>(a);
     else if (per_lane <= 8) k_norm_rows<T, 8, MODE, W, 1, WL><<<grid1, NT, 0, s>>>(a);
     else if constexpr (W == 4) k_norm_rows<T, 16, MODE, W, 1, WL><<<grid1, NT, 0, s>>>(a);
@@ -338,7 +339,7 @@ static void launch_wl(const NormArgs& a, int per_lane, int R, bool late, hipStre
 // Waves per row: the fewest (1, 2 or 4) that keep a row within 4 chunks (128-bit loads)
 // per lane (3 for NORM_ADD_NORM, which also holds the second weight vector; 6 for NORM_ADD,
 // whose one wave per row at 2048 x 2560 bf16 skips the cross-wave reduction: 6.57 -> 6.26 us,
-// 8192 x 5376 unchanged), so a row lives
+// 8192 x 5376 unchanged; with exactly 5 chunks per lane there, 6.49 -> 6.32 us against 6), so a row lives
 // in registers with few cross-wave reductions and every row of a 2048-token prefill is
 // resident at once; rows longer than that at 4 waves take up to 16 chunks per lane.
 // ZL_NORM_WAVES_PER_ROW, ZL_NORM_ROWS_PER_GROUP and ZL_NORM_LATE (0 / 1) force values.
