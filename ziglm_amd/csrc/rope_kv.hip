@@ -5,7 +5,8 @@
 // five extra HBM round trips of Q and K.
 //
 // Numerics follow ziglm's CPU path:
-//   norm  math.zig:850-988 (inv = 1.0/sqrt(mean + eps), (x*inv)*(1+w));
+//   norm  math.zig:850-988 ((x*inv)*(1+w); inv = 1.0/sqrt(mean + eps), in the fused kernel
+//         by the hardware reciprocal square root, within 1 ulp of it);
 //   RoPE  math.zig:1019-1078 .normal: pairs (i, i + r/2); theta = (f32(pos)*freq_scale)/D_i
 //         (IEEE f32 division); D_i = f32(pow(base, f32(2i)/f32(r))), the oracle's value (in
 //         the fused kernel evaluated per lane in double precision, rope_denom; in the generic
@@ -227,7 +228,11 @@ __global__ __launch_bounds__(256) void k_qk_fused(QkArgs a) {
                     ss = fmaf(x1[j], x1[j], ss);
                 }
                 ss = group_sum<LH>(ss);
-                const float inv = rms_inv(ss, D, a.eps);
+                // 1 / sqrt(mean + eps) by the hardware reciprocal square root (within 1 ulp
+                // of the reference's IEEE sqrt and divide, and ~20 instructions shorter per
+                // row: this kernel's arithmetic is exposed, c2 7.89 -> 7.72 us); D is a power
+                // of two, so the mean is exact
+                const float inv = __builtin_amdgcn_rsqf(ss * (1.0f / (float)D) + a.eps);
                 if (kind == 2) {  // Gemma-4 V: no-scale norm
 #pragma unroll
                     for (int j = 0; j < E; ++j) {
