@@ -1,6 +1,9 @@
 // RMSNorm family (replaces cuda_bridge.cu:1451-1553, 1942-2068) with ziglm's CPU numerics
-// (math.zig:850-988): sum of squares in f32, mean = sum/n, inv = 1.0/sqrt(mean + eps) with
-// IEEE sqrt and divide, out = (x*inv)*(1+w) | (x*inv)*w | x*inv (weight NULL).
+// (math.zig:850-988): sum of squares in f32, mean = sum/n (IEEE divide), inv = 1/sqrt(mean +
+// eps), out = (x*inv)*(1+w) | (x*inv)*w | x*inv (weight NULL). The register-row kernels take
+// 1/sqrt from the hardware reciprocal square root (within 1 ulp of the reference's IEEE sqrt
+// and divide; 2048 x 2560 bf16: input norm 4.28 -> 4.19 us, norm + add + norm 8.15 -> 7.92);
+// the generic kernel keeps the IEEE form.
 //
 // Modes (one kernel family):
 //   NORM           out = norm(x)                                   (rmsNorm, rmsNormBatched)
@@ -168,7 +171,7 @@ __global__ __launch_bounds__(256) void k_norm_rows(NormArgs a) {
             if (r == 0) load_weights();
         }
         ss = row_sum<W>(ss, slot1);
-        const float inv = rms_inv(ss, n, a.eps);
+        const float inv = rms_inv_hw(ss, n, a.eps);
 
         if constexpr (MODE == M_NORM || MODE == M_ADD_NORM) {
 #pragma unroll
@@ -210,7 +213,7 @@ __global__ __launch_bounds__(256) void k_norm_rows(NormArgs a) {
                 }
             }
             ss2 = row_sum<W>(ss2, slot2);
-            const float inv2 = rms_inv(ss2, n, a.eps);
+            const float inv2 = rms_inv_hw(ss2, n, a.eps);
 #pragma unroll
             for (int c = 0; c < NC; ++c) {
                 const int idx = g + c * STRIDE;
