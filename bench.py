@@ -758,7 +758,8 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline config only")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default=None, help="run one op only (profiling): a chain op, "
-                    "gather_q8_0 / gather_q4_0 / gather_bf16 (c3), gemv, gemm, decode_step, gguf_decode, "
+                    "gather_q8_0 / gather_q4_0 / gather_bf16 (c3), c5 (batched decode ops), gemv, gemm, decode_step, "
+                    "gguf_decode, "
                     "or 'copy' = hipMemcpy device-to-device of the GeGLU output size (counter calibration)")
     ap.add_argument("--eager", action="store_true", help="with --only: launch eagerly, no graph (kernel traces)")
     ap.add_argument("--config", default="c2", choices=["c2", "c4"])
@@ -784,6 +785,9 @@ def main():
             return
         elif a.only == "gguf_decode":
             print(json.dumps(bench_gguf_decode(dev, graph=not a.eager)))
+            return
+        elif a.only == "c5":
+            print(json.dumps({f"B{b_}": bench_decode(dev, b_) for b_ in (1, 8, 64, 256)}))
             return
         elif a.only == "gemv":
             log("gemv (decode projections)")

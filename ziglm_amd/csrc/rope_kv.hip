@@ -25,10 +25,12 @@
 // table (rotary_dim/2 entries) is computed once in LDS while the first head's loads are in
 // flight; its denominators are evaluated per lane (rope_denom) and its cos/sin by
 // rope_sincos, so that phase has no memory operand to wait for. Measured at c2 (2048 tokens,
-// 8/4 heads x 256, bf16): 7.9-8.2 us, against 7.1 us for the same kernel reduced to a copy
-// (no norm, RoPE, weights or barrier) and 6.3-6.8 us for a plain stream of the same bytes.
-// A variant without the workgroup barrier (each wave computing its own angles and staging
-// its own weights in LDS) measured 8.6-9.0 us.
+// 8/4 heads x 256, bf16): 6.7 us, against 6.6 us for a plain stream of the same bytes. Not
+// taken: a variant without the workgroup barrier (each wave computing its own angles and
+// staging its own weights in LDS, 8.6-9.0 us when the kernel took 7.9); each lane loading
+// the norm weights of its own chunks into registers instead of the LDS staging (7.3 us, the
+// weight loads as many load instructions as the rows'); one or four tokens per workgroup
+// (8.9 / 8.7 us).
 // Generic path (other head sizes up to 512, any alignment): one wave per head row (Q, K or V
 // head), head staged in LDS, four rows per workgroup.
 #include <math.h>
@@ -140,6 +142,55 @@ __global__ __launch_bounds__(256) void k_qk_fused(QkArgs a) {
     const int c1 = hl < R ? hl + R : c0 + 1;
     const int nq = a.q ? a.nh : 0;
     const int HR = a.nh + 2 * a.nkv;
+    const bool has_wq = a.wq != nullptr, has_wk = a.wk != nullptr;
+    // The base pointers as register values: a per-lane choice among them is then a select,
+    // not a per-lane load of the chosen argument (which the compiler otherwise emits, with a
+    // wait for it ahead of the row loads), nor, for the weights, a loop over the distinct
+    // buffer resources of a wave.
+    const T* const qb = sreg((const T*)a.q);
+    const T* const kb = sreg((const T*)a.k);
+    const T* const vb = sreg((const T*)a.v);
+    const float* const wqb = sreg(a.wq);
+    const float* const wkb = sreg(a.wk);
+
+    // Head rows: [0, nh) Q, [nh, nh+nkv) K, [nh+nkv, nh+2nkv) V.
+    auto src_of = [&](int hr, int t) -> const T* {
+        if (hr < a.nh) return qb + ((int64_t)t * a.nh + hr) * D;
+        if (hr < a.nh + a.nkv) return kb + ((int64_t)t * a.nkv + (hr - a.nh)) * D;
+        return vb + ((int64_t)t * a.nkv + (hr - a.nh - a.nkv)) * D;
+    };
+    // Source rows exist for every token of the launch (whether a K / V row is then written
+    // depends on its destination, known only after the position and slot reads below).
+    auto readable = [&](int hr, int t) -> bool {
+        if (t >= a.n_tokens) return false;
+        if (hr < a.nh) return nq > 0;
+        if (hr < a.nh + a.nkv) return a.k != nullptr;
+        return a.v != nullptr;
+    };
+    // Issue order. First the norm weights, staged once per workgroup in LDS as factors (1+w),
+    // w or 1 (threads [0, D/4) stage wq, [D/4, D/2) wk, one f32x4 each; L2 hits after the
+    // first workgroups): the barrier below waits for them, and loads complete in issue order.
+    // Then the first head row of every token (HBM), and only then the position / slot reads
+    // and the tokens' cos/sin tables (no memory operand but the angles' positions), which run
+    // while the rows are in flight (position reads issued ahead of the rows delay every row
+    // request by their latency: c2 7.75 -> 6.69 us with this order and the register selects
+    // above). Every thread issues all of these loads (from the zero row where there is nothing
+    // to read): the compiler counts outstanding loads per path, and were some skipped on one
+    // path, a wait for the earliest would become a wait for all of them.
+    const int ti = threadIdx.x;
+    const int wi = ti < D / 4 ? ti : ti - D / 4;
+    const bool stage_q = ti < D / 4, stage_k = ti >= D / 4 && ti < D / 2;
+    const float* ws = stage_q && has_wq ? wqb : stage_k && has_wk ? wkb : g_qk_pad_row;
+    const f32x4 wstage = ldf4(ws + (stage_q || stage_k ? 4 * wi : 0));
+    u32x4 ra[TPW], rb[TPW];
+#pragma unroll
+    for (int tt = 0; tt < TPW; ++tt) {
+        const bool row_ok = gslot < HR && readable(gslot, tb + tt);
+        const T* src0 = row_ok ? src_of(gslot, tb + tt) : (const T*)g_qk_pad_row;
+        ra[tt] = lds16(src0 + c0 * E);
+        rb[tt] = lds16(src0 + c1 * E);
+    }
+
     int p[TPW];
     int64_t row[TPW];
     bool tok[TPW];
@@ -149,43 +200,12 @@ __global__ __launch_bounds__(256) void k_qk_fused(QkArgs a) {
         p[tt] = tok[tt] ? token_pos(a, tb + tt) : 0;
         row[tt] = tok[tt] ? token_row(a, tb + tt, p[tt]) : -1;
     }
-
-    // Head rows: [0, nh) Q, [nh, nh+nkv) K, [nh+nkv, nh+2nkv) V.
-    auto src_of = [&](int hr, int t) -> const T* {
-        if (hr < a.nh) return (const T*)a.q + ((int64_t)t * a.nh + hr) * D;
-        if (hr < a.nh + a.nkv) return (const T*)a.k + ((int64_t)t * a.nkv + (hr - a.nh)) * D;
-        return (const T*)a.v + ((int64_t)t * a.nkv + (hr - a.nh - a.nkv)) * D;
-    };
     auto active = [&](int hr, int tt) -> bool {
         if (!tok[tt]) return false;
         if (hr < a.nh) return nq > 0;
         if (hr < a.nh + a.nkv) return a.k != nullptr && row[tt] >= 0;
         return a.v != nullptr && row[tt] >= 0;
     };
-
-    // Issue the weight loads (L2 hits after the first tokens: the barrier below waits on
-    // them) and then the first head row's HBM loads of every token, and evaluate the tokens'
-    // cos/sin tables (no memory operands) while they are in flight. Every thread issues all
-    // of them (from an empty range or the zero row where there is nothing to read): the
-    // compiler counts outstanding loads per path, and were the head-row loads skipped on
-    // some path, the weights' wait before the barrier would wait for the head rows too.
-    const int ti = threadIdx.x;
-    // The norm weights go to LDS (read there per head, not held in registers): one f32x4
-    // per thread (threads [0, D/4) stage wq, [D/4, D/2) stage wk; D <= 256 fits 256 threads).
-    const bool has_wq = a.wq != nullptr, has_wk = a.wk != nullptr;
-    const int wi = ti < D / 4 ? ti : ti - D / 4;  // thread -> float4 index in its vector
-    const bool stage_q = ti < D / 4, stage_k = ti >= D / 4 && ti < D / 2;
-    const bool wload = (stage_q && has_wq) || (stage_k && has_wk);
-    const auto rs_w = buf_rsrc(wload ? (stage_q ? a.wq : a.wk) : g_qk_pad_row, wload ? (uint32_t)D * 4u : 0u);
-    const f32x4 wstage = bldf4(rs_w, (uint32_t)wi * 16u);  // zeros when absent (factor 1 below)
-    u32x4 ra[TPW], rb[TPW];
-#pragma unroll
-    for (int tt = 0; tt < TPW; ++tt) {
-        const bool row_ok = gslot < HR && active(gslot, tt);
-        const T* src0 = row_ok ? src_of(gslot, tb + tt) : (const T*)g_qk_pad_row;
-        ra[tt] = lds16(src0 + c0 * E);
-        rb[tt] = lds16(src0 + c1 * E);
-    }
     if (a.do_rope) {
         for (int i = ti; i < TPW * a.half; i += 256) {
             const int tt = i / a.half, k = i - tt * a.half;
@@ -402,12 +422,14 @@ static void launch_qk_t(const QkArgs& a, const RopeTab& tab, hipStream_t s) {
         // launches with many tokens whose head rows fit one pass (Gemma-4B at 2048 tokens:
         // 7.87 -> 7.76 us; with two passes per token the second token's passes follow the
         // first's: Gemma-27B heads at 8192 tokens 43.8 -> 49.8 us, so one token there).
-        const unsigned grid2 = (unsigned)cdiv(a.n_tokens, 2);
+        constexpr int TP = ZL_QK_TPW;
+        const unsigned gridm = (unsigned)cdiv(a.n_tokens, TP);
         auto go = [&](auto d_c) {
             constexpr int DD = decltype(d_c)::value;
-            const bool two = ZL_QK_TPW == 2 && a.n_tokens >= ZL_QK_TPW_MIN && HR <= qk_slots<T, DD>();
-            if (two) k_qk_fused<T, DD, 2><<<dim3(grid2, gy(qk_slots<T, DD>())), 256, 0, s>>>(a);
-            else k_qk_fused<T, DD, 1><<<dim3(grid, gy(qk_slots<T, DD>())), 256, 0, s>>>(a);
+            constexpr int SL = qk_slots<T, DD>();
+            const bool multi = TP > 1 && a.n_tokens >= ZL_QK_TPW_MIN && HR <= SL;
+            if (multi) k_qk_fused<T, DD, TP><<<dim3(gridm, gy(SL)), 256, 0, s>>>(a);
+            else k_qk_fused<T, DD, 1><<<dim3(grid, gy(SL)), 256, 0, s>>>(a);
         };
         if (a.D == 64) go(std::integral_constant<int, 64>{});
         else if (a.D == 128) go(std::integral_constant<int, 128>{});

@@ -98,6 +98,16 @@ __device__ __forceinline__ void sts16(void* p, const u32x4& v) {
 #endif
 }
 __device__ __forceinline__ f32x4 ldf4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
+// A wave-uniform global pointer held in scalar registers and opaque to the optimiser, so
+// that a per-lane choice among several such pointers stays a register select (the asm is
+// not volatile and touches no memory, so loads around it keep their scalar / global forms).
+template <typename P>
+__device__ __forceinline__ P* sreg(P* p) {
+    typedef __attribute__((address_space(1))) P* GP;
+    uint64_t v = (uint64_t)p;
+    asm("" : "+s"(v));
+    return (P*)(GP)v;
+}
 
 // Range-checked loads through a buffer resource over [base, base + bytes): a raw buffer load
 // at a byte offset past the end returns zeros and makes no memory access (CDNA buffer range
