@@ -21,8 +21,9 @@
 // elementwise kernels' gelu_fast); QKV treats the three matrices as one row space.
 // Batch-1 Q4_0 products with 512-column multiples take k_gemv_q4b instead (one 18-byte
 // block per lane from two dword-aligned loads, every weight load of a wave issued at once,
-// x staged in LDS; with or without the input prologue); the loops above serve every other
-// type, shape and batch. Measured at the Gemma-4B decode shapes (us, weights cold): QKV
+// x staged in LDS; with or without the input prologue), Q4_K and Q6_K products the same
+// scheme over 64-column pieces of their super-blocks (k_gemv_q4kb, k_gemv_q6kb); the loops
+// above serve every other type, shape and batch. Measured at the Gemma-4B decode shapes (us, weights cold): QKV
 // 4096 x 2560 5.4 -> 4.5, O 2560 x 2048 3.5 -> 3.4, gate.up 2 x 10240 x 2560 11.8 -> 10.0,
 // down 2560 x 10240 8.4 -> 7.3, LM head 262144 x 2560 110 -> 94; the same-size read-only
 // streams take 2.3, 1.9, 6.0, 3.7 and 58 us. Without the dequantisation arithmetic the block
@@ -110,6 +111,12 @@ __device__ __forceinline__ uint32_t ldw16(const unsigned char* p) {
 typedef uint32_t u32_align2 __attribute__((aligned(2)));
 __device__ __forceinline__ uint32_t ldw32_a2(const unsigned char* p) {
     return *reinterpret_cast<const u32_align2*>(p);
+}
+// (v & m) | c in one instruction, opaque to the optimiser like mask_bytes.
+__device__ __forceinline__ uint32_t and_or(uint32_t v, uint32_t m, uint32_t c) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(v), "s"(m), "v"(c));
+    return r;
 }
 // v, opaque to the optimiser: a lane offset it would otherwise split into separately
 // zero-extended terms (64-bit address adds per row) stays one 32-bit offset register.
@@ -1419,6 +1426,188 @@ static bool launch_q4kb(const GemvArgs& a, hipStream_t s) {
     }
 }
 
+// Batch-1 Q6_K products, the same scheme over 64-column quarter chunks. A Q6_K super-block
+// (210 bytes, 256 columns: ql[128] low nibbles, qh[64] two high bits each, int8 scales[16],
+// f16 d; types.zig:187-192) holds four quarters (n, p), n the 128-column half, p the 16-column
+// half of each of its four 32-column quadrants qd: quarter (n, p) is columns 128n + 32qd + 16p
+// + i (i < 16), whose 6-bit values take their low nibbles from ql bytes 64n + 16p + i (qd 0
+// low, qd 2 high) and 64n + 32 + 16p + i (qd 1 low, qd 3 high) and their high bits from qh
+// byte 32n + 16p + i (bits 2qd, 2qd + 1), with scale 8n + 2qd + p (quant.zig:357-385,
+// math.zig:556-616). A lane takes a whole quarter with three 16-byte loads and an 8-byte one
+// (super-blocks are 210 bytes, so every other one starts 2 bytes past a dword: these are
+// unaligned vector loads, which gfx950 serves from 2-byte aligned addresses) and the f16 d.
+// x is staged per workgroup at 68 floats per quarter in the quarter's column order, its four
+// 16-column sums at slots 64-67 (68 = 4 mod 32 puts the 8 lanes of a set, which read
+// consecutive quarters, on distinct banks). Arithmetic as the group kernels:
+// d * sum_qd sc_qd * (sum u x - 32 sum x) over each 16-column group.
+constexpr int kQ6kbXStride = 68;
+typedef u32x4 u32x4_a2 __attribute__((aligned(2)));
+typedef u32x2 u32x2_a2 __attribute__((aligned(2)));
+struct Q6Chunk {
+    u32x4 a, b, h;  // ql bytes 64n+16p .. +16, 64n+32+16p .. +16; qh bytes 32n+16p .. +16
+    u32x2 s;        // scale bytes 8n .. 8n+7
+    uint32_t d;     // f16 d
+    __device__ __forceinline__ void load(const unsigned char* sb, uint32_t n, uint32_t p) {
+        a = *reinterpret_cast<const u32x4_a2*>(sb + 64u * n + 16u * p);
+        b = *reinterpret_cast<const u32x4_a2*>(sb + 64u * n + 32u + 16u * p);
+        h = *reinterpret_cast<const u32x4_a2*>(sb + 128u + 32u * n + 16u * p);
+        s = *reinterpret_cast<const u32x2_a2*>(sb + 192u + 8u * n);
+        d = *reinterpret_cast<const uint16_t*>(sb + 208u);
+    }
+    // xs: the quarter's x in LDS (quadrant qd at slots 16 qd .., its sum at 64 + qd).
+    __device__ __forceinline__ float dot(uint32_t p, const float* xs) const {
+        const uint32_t A[4] = {a.x, a.y, a.z, a.w}, Bq[4] = {b.x, b.y, b.z, b.w}, H[4] = {h.x, h.y, h.z, h.w};
+        float r = 0.0f;
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) {
+            f32x4 xv[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) xv[i] = *reinterpret_cast<const f32x4*>(xs + 16 * qd + 4 * i);
+            float t = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                // 6-bit values of columns 4i .. 4i+3 of quadrant qd (the high bits masked, then
+                // one and-or with the low nibbles)
+                const uint32_t lo = qd == 0 ? A[i] : qd == 1 ? Bq[i] : qd == 2 ? A[i] >> 4 : Bq[i] >> 4;
+                const uint32_t hi = qd == 0 ? H[i] << 4 : qd == 1 ? H[i] << 2 : qd == 2 ? H[i] : H[i] >> 2;
+                const uint32_t u = and_or(lo, 0x0f0f0f0fu, mask_bytes(hi, 0x30303030u));
+                t = i == 0 ? (float)(u & 0xff) * xv[0].x : fmaf((float)(u & 0xff), xv[i].x, t);
+                t = fmaf((float)((u >> 8) & 0xff), xv[i].y, t);
+                t = fmaf((float)((u >> 16) & 0xff), xv[i].z, t);
+                t = fmaf((float)(u >> 24), xv[i].w, t);
+            }
+            // scale byte 2 qd + p of the half's eight
+            const uint32_t w = qd < 2 ? s.x : s.y;
+            const float sc = (float)(int32_t)__builtin_amdgcn_sbfe((int32_t)w, 16u * (qd & 1) + 8u * p, 8u);
+            const float g = fmaf(-32.0f, xs[64 + qd], t);
+            r = qd == 0 ? sc * g : fmaf(sc, g, r);
+        }
+        return h2f(d & 0xffffu) * r;
+    }
+};
+
+// (4 waves per SIMD, up to 128 registers, where x takes at most 4 float4 per thread and no
+// prologue: six quarters of weights and a quadrant of x fit without spilling; otherwise 3)
+template <int MODE, int LPR, int BPL, bool PRO, int NW, int MAXC>
+__global__ __launch_bounds__(NW * kWave, (PRO || MAXC > kQ4bProMaxCols ? 3 : 4) * 4 / NW) void k_gemv_q6kb(GemvArgs a) {
+    constexpr int T = NW * kWave;
+    constexpr int SETS = kWave / LPR;
+    constexpr int XK = MAXC / 4 / T;  // x float4 per thread (MAXC: the most columns taken)
+    extern __shared__ __attribute__((aligned(16))) float s_xq[];
+    __shared__ float s_red[NW];
+    const int lane = threadIdx.x & 63;
+    const int wv = threadIdx.x >> 6;
+    const int li = lane % LPR, set = lane / LPR;
+    const int row0 = (blockIdx.x * NW + wv) * SETS + set;
+    const int n4 = a.cols / 4;
+    f32x4 xv[XK], rv[PRO ? XK : 1], rwv[PRO ? XK : 1], wnv[PRO ? XK : 1];
+    if constexpr (PRO) {
+        q4b_pro_load<XK, T>(a, xv, rv, rwv, wnv);
+    } else {
+#pragma unroll
+        for (int k = 0; k < XK; ++k) {
+            const int i = (int)threadIdx.x + k * T;
+            if (i < n4) xv[k] = ldf4(a.x + 4 * i);
+        }
+    }
+    const int r0 = a.seg[0].rows, r1 = a.nseg > 1 ? a.seg[1].rows : 0;
+    const bool ok = row0 < a.total_rows;
+    const int R = ok ? row0 : a.total_rows - 1;  // past the end: the last row, not written
+    const bool s0 = R < r0, s1 = !s0 && R - r0 < r1;
+    const int Rs = s0 ? R : s1 ? R - r0 : R - r0 - r1;
+    const unsigned char* wrow = (s0 ? a.seg[0].w : s1 ? a.seg[1].w : a.seg[2].w) + (int64_t)Rs * a.row_bytes;
+    float* yrow = ok ? (s0 ? a.seg[0].y : s1 ? a.seg[1].y : a.seg[2].y) + Rs : nullptr;
+    Q6Chunk w[BPL];
+#pragma unroll
+    for (int j = 0; j < BPL; ++j) {
+        const uint32_t c = (uint32_t)(li + LPR * j);
+        w[j].load(wrow + (c >> 2) * 210u, (c >> 1) & 1u, c & 1u);
+    }
+    if constexpr (PRO) q4b_pro_finish<XK, T>(a, xv, rv, rwv, wnv, s_red);
+    // x into LDS: float4 i (columns 4i ..) of super-block i / 64 goes to quarter
+    // (n, p) = (bit 5, bit 2 of i), quadrant qd = bits 3-4, slot 16 qd + 4 (i & 3); the sum of
+    // each 16-column group (4 consecutive float4s, lanes 4k .. 4k+3) by two DPP row shifts.
+#pragma unroll
+    for (int k = 0; k < XK; ++k) {
+        const int i = (int)threadIdx.x + k * T;
+        if (k * T >= n4) break;  // uniform
+        const float s4 = i < n4 ? (xv[k].x + xv[k].y) + (xv[k].z + xv[k].w) : 0.0f;
+        const float v = s4 + dpp<0x111>(s4);  // row_shr:1
+        const float gs = v + dpp<0x112>(v);   // row_shr:2
+        if (i < n4) {
+            const int c = ((i >> 6) << 2) | (((i >> 5) & 1) << 1) | ((i >> 2) & 1);
+            const int qd = (i >> 3) & 3;
+            float* xs = s_xq + c * kQ6kbXStride;
+            *reinterpret_cast<f32x4*>(xs + 16 * qd + 4 * (i & 3)) = xv[k];
+            if ((i & 3) == 3) xs[64 + qd] = gs;
+        }
+    }
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < BPL; ++j) {
+        const uint32_t c = (uint32_t)(li + LPR * j);
+        acc += w[j].dot(c & 1u, s_xq + c * kQ6kbXStride);
+    }
+    acc = group_sum<LPR>(acc);
+    if (li == 0 && yrow) *yrow = acc;
+}
+
+#ifndef ZL_GEMV_Q6KB
+#define ZL_GEMV_Q6KB 1
+#endif
+// Launches k_gemv_q6kb for batch-1 Q6_K products with a whole number of 8-quarter groups per
+// row (cols % 512 == 0), at most kQ4bMaxB quarters per lane at 8 to 64 lanes per row and x
+// within the LDS; returns false otherwise. Lanes per row as the Q4_K kernel's; one row per
+// set. (Not the GeGLU pair: two matrices' quarters do not fit the registers.)
+template <int QT, int MODE, bool PRO>
+static bool launch_q6kb(const GemvArgs& a, hipStream_t s) {
+    if constexpr (QT != HIP_BRIDGE_Q6_K || MODE == GV_GEGLU) {
+        return false;
+    } else {
+    if (!ZL_GEMV_Q6KB || a.batch != 1 || a.cols % 512 != 0) return false;
+    const int nch = a.cols / 64;
+    const size_t lds = (size_t)nch * kQ6kbXStride * sizeof(float);
+    if (a.cols > (PRO ? kQ4bProMaxCols : kQ4bMaxCols) || lds > 65536) return false;
+    constexpr int NW = PRO ? ZL_GEMV_Q4B_PRO_WAVES : ZL_GEMV_Q4B_NW;
+    // (with the prologue at most 5 quarters per lane: 6 spill)
+    const int maxb = PRO ? 5 : kQ4bMaxB;
+    int lpr = 0;
+    for (int l : {8, 16, 32, 64})
+        if (!lpr && nch % l == 0 && nch / l <= maxb) lpr = l;
+    if (!lpr) return false;
+    auto waves = [&](int l) { return cdiv(a.total_rows, (int64_t)(kWave / l)); };
+    while (lpr < 64 && waves(lpr) < ZL_GEMV_Q4B_WAVES && nch % (2 * lpr) == 0) lpr *= 2;
+    const int bpl = nch / lpr;
+    const unsigned grid = (unsigned)cdiv(waves(lpr), (int64_t)NW);
+    // x staged through registers: kQ4bProMaxCols columns' worth per thread for products up
+    // to that width (fewer registers held beside the weights), kQ4bMaxCols' above
+    const bool narrow = PRO || a.cols <= kQ4bProMaxCols;
+    auto go = [&](auto lpr_c) {
+        constexpr int L = decltype(lpr_c)::value;
+        auto go2 = [&](auto c_c) {
+            constexpr int MC = decltype(c_c)::value;
+            switch (bpl) {
+                case 1: k_gemv_q6kb<MODE, L, 1, PRO, NW, MC><<<grid, NW * kWave, lds, s>>>(a); break;
+                case 2: k_gemv_q6kb<MODE, L, 2, PRO, NW, MC><<<grid, NW * kWave, lds, s>>>(a); break;
+                case 3: k_gemv_q6kb<MODE, L, 3, PRO, NW, MC><<<grid, NW * kWave, lds, s>>>(a); break;
+                case 4: k_gemv_q6kb<MODE, L, 4, PRO, NW, MC><<<grid, NW * kWave, lds, s>>>(a); break;
+                case 5: k_gemv_q6kb<MODE, L, 5, PRO, NW, MC><<<grid, NW * kWave, lds, s>>>(a); break;
+                default: k_gemv_q6kb<MODE, L, PRO ? 5 : 6, PRO, NW, MC><<<grid, NW * kWave, lds, s>>>(a); break;
+            }
+        };
+        if (narrow) go2(std::integral_constant<int, kQ4bProMaxCols>{});
+        else if constexpr (!PRO) go2(std::integral_constant<int, kQ4bMaxCols>{});
+    };
+    if (lpr == 8) go(std::integral_constant<int, 8>{});
+    else if (lpr == 16) go(std::integral_constant<int, 16>{});
+    else if (lpr == 32) go(std::integral_constant<int, 32>{});
+    else go(std::integral_constant<int, 64>{});
+    return true;
+    }
+}
+
 // Any alignment / column count: one workgroup per row, scalar dequantisation per element.
 template <int QT>
 __device__ __forceinline__ float w_elem(const unsigned char* row, int c) {
@@ -1527,8 +1716,9 @@ static void launch_vec(const GemvArgs& a, hipStream_t s) {
     constexpr int H = MODE == GV_GEGLU ? 2 : 1;
     const unsigned g8 = (unsigned)cdiv(a.total_rows, 8 / H), g4 = (unsigned)cdiv(a.total_rows, 4 / H),
                    g2 = (unsigned)cdiv(a.total_rows, 2 / H);
-    if (PRO && (launch_q4b<QT, MODE, true>(a, s) || launch_q4kb<QT, MODE, true>(a, s))) {
-        // launched: batch-1 Q4_0 / Q8_0 / Q4_K block kernel with the prologue
+    if (PRO && (launch_q4b<QT, MODE, true>(a, s) || launch_q4kb<QT, MODE, true>(a, s) ||
+                launch_q6kb<QT, MODE, true>(a, s))) {
+        // launched: batch-1 Q4_0 / Q8_0 / Q4_K / Q6_K block kernel with the prologue
     } else if (PRO) {  // batch 1; the input vector in dynamic LDS; at most kGemvProGrid workgroups
         const size_t lds = (size_t)a.cols * sizeof(float);
         const unsigned cap = kGemvProGrid;
@@ -1551,8 +1741,9 @@ static void launch_vec(const GemvArgs& a, hipStream_t s) {
             constexpr int RP = F > 0 ? std::max(1, F / H) : 2 / H;
             k_gemv<QT, RP, 1, MODE><<<(unsigned)cdiv(a.total_rows, RP), kGemvThreads, 0, s>>>(a);
         }
-    } else if (launch_q4b<QT, MODE, false>(a, s) || launch_q4kb<QT, MODE, false>(a, s)) {
-        // launched: batch-1 Q4_0 / Q8_0 with 256-column multiples, Q4_K with 512
+    } else if (launch_q4b<QT, MODE, false>(a, s) || launch_q4kb<QT, MODE, false>(a, s) ||
+               launch_q6kb<QT, MODE, false>(a, s)) {
+        // launched: batch-1 Q4_0 / Q8_0 with 256-column multiples, Q4_K / Q6_K with 512
     } else if (MODE == GV_PLAIN && a.batch == 1 && a.total_rows >= kGemvWaveRowsMin && a.cols <= kGemvWaveColsMax &&
                QT != HIP_BRIDGE_F16 && QT != HIP_BRIDGE_BF16 && QT != HIP_BRIDGE_F32) {
         // (k_gemv_w is instantiated for these cases only)
