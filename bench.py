@@ -495,6 +495,7 @@ def bench_gemv(dev):
         ("lm_head_q4_k", B.Q4_K, [(V, H)], plain(B.Q4_K, V, H), 1),
         ("lm_head_q6_k", B.Q6_K, [(V, H)], plain(B.Q6_K, V, H), 1),
         ("down_q4_k", B.Q4_K, [(H, I)], plain(B.Q4_K, H, I), 1),
+        ("down_q6_k", B.Q6_K, [(H, I)], plain(B.Q6_K, H, I), 1),
         ("gate_q4_0_b8", B.Q4_0, [(I, H)], plain(B.Q4_0, I, H, 8), 8),
     ]
     for name, qt, shapes, fn, batch in cases:
