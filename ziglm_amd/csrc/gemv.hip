@@ -1848,6 +1848,217 @@ static void launch_gemv(int qtype, GemvArgs& a, hipStream_t s) {
     check_launch();
 }
 
+// ---- small batches on the matrix cores ------------------------------------------------------
+// Products of 2 to kGemmMfmaMinBatch - 1 tokens (hip_gemm below the prefill GEMM) with Q4_0,
+// Q8_0 or BF16 weights: v_mfma_f32_16x16x32_bf16 over tiles of 16 tokens x 16 rows x one
+// 32-column block, tokens on the A side (each x as three bf16 terms h + m + l, as the prefill
+// GEMM: exact to the f32 value's 24 bits), rows on the B side. Block quants enter as their
+// unsigned codes u (Q4_0 nibbles 0..15, Q8_0 q ^ 0x80: exact in bf16) and a block's sum is
+// d * (sum u x - c * sum x), c = 8 / 128, the batch-1 kernels' arithmetic; sum x per token and
+// block comes from three more MFMAs against a ones operand. A wave takes NT 16-row tiles over
+// a 1/KS share of the blocks and converts each block's x once for its NT tiles; the KS waves
+// of a workgroup cover the whole width and are added in wave order through LDS. Layouts
+// (16x16x32): lane l supplies A row (token) l % 16 and B column (weight row) l % 16, each over
+// the block's columns 8 (l / 16) .. + 8, and holds D[4 (l / 16) + r][l % 16], r < 4.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+constexpr int kMbTok = 16;  // tokens per tile
+
+// x0, x1 -> three packed bf16 pairs (h, m, l) with x = h + m + l (each term RNE of the rest).
+__device__ __forceinline__ void mb_split3(float x0, float x1, uint32_t& h, uint32_t& m, uint32_t& l) {
+    h = pack_bf16x2(x0, x1);
+    x0 -= bf16_lo(h);
+    x1 -= bf16_hi(h);
+    m = pack_bf16x2(x0, x1);
+    x0 -= bf16_lo(m);
+    x1 -= bf16_hi(m);
+    l = pack_bf16x2(x0, x1);
+}
+// Four byte codes (0..255) -> two packed bf16 pairs (small integers: the f32's high half).
+__device__ __forceinline__ void mb_codes(uint32_t u, uint32_t& p0, uint32_t& p1) {
+    const float f0 = (float)(u & 0xffu), f1 = (float)((u >> 8) & 0xffu);
+    const float f2 = (float)((u >> 16) & 0xffu), f3 = (float)(u >> 24);
+    p0 = __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
+    p1 = __builtin_amdgcn_perm(__float_as_uint(f3), __float_as_uint(f2), 0x07060302u);
+}
+
+template <int QT, int NT, int KS>
+__global__ __launch_bounds__(KS * kWave) void k_gemv_mb(GemvArgs a) {
+    constexpr bool SC = QT != HIP_BRIDGE_BF16;
+    constexpr uint32_t BB = QT == HIP_BRIDGE_Q4_0 ? 18u : QT == HIP_BRIDGE_Q8_0 ? 34u : 64u;  // bytes / block
+    constexpr float C = QT == HIP_BRIDGE_Q4_0 ? 8.0f : 128.0f;
+    __shared__ f32x4 s_red[KS][NT][kWave];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int mn = lane & 15, g = lane >> 4;
+    const int t0 = blockIdx.y * kMbTok;
+    const int r0 = blockIdx.x * 16 * NT;
+    const int nblk = a.cols / 32;
+    const int kb0 = (int)((int64_t)nblk * wv / KS), kb1 = (int)((int64_t)nblk * (wv + 1) / KS);
+    // the x row of token t0 + mn (past the batch: token 0's, zeroed), columns 8g .. of a block
+    const bool tok_ok = t0 + mn < a.batch;
+    const float* xr = a.x + (int64_t)(tok_ok ? t0 + mn : 0) * a.cols + 8 * g;
+    // the weight row of tile j (past the last row: the last row, not stored)
+    const unsigned char* wrow[NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+        const int row = min(r0 + 16 * j + mn, a.total_rows - 1);
+        wrow[j] = a.seg[0].w + (int64_t)row * a.row_bytes;
+    }
+    // the lane's quant bytes in a block: Q4_0 columns 8g .. are the low (g < 2) / high nibbles
+    // of bytes 8 (g & 1) ..; Q8_0 bytes 8g ..; BF16 elements 8g ..
+    const uint32_t qoff = QT == HIP_BRIDGE_Q4_0 ? 2u + 8u * (g & 1) : QT == HIP_BRIDGE_Q8_0 ? 2u + 8u * g : 16u * g;
+    const uint32_t nsh = QT == HIP_BRIDGE_Q4_0 ? 4u * (g >> 1) : 0u;
+    bf16x8 ones;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ones[e] = (__bf16)1.0f;
+    f32x4 acc[NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) acc[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    // One block at a time (measured: issuing 2-6 blocks' loads before their arithmetic was
+    // slower at every shape, 20.0 -> 22.5-25.3 us for 10240 x 2560 at 8 tokens).
+    for (int kb = kb0; kb < kb1; ++kb) {
+        const f32x4 xa = ldf4(xr + 32 * kb), xb = ldf4(xr + 32 * kb + 4);
+        u32x4 wq[NT];
+        uint32_t dd[NT];
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+            const unsigned char* blk = wrow[j] + BB * (uint32_t)kb;
+            if constexpr (QT == HIP_BRIDGE_BF16) {
+                wq[j] = *reinterpret_cast<const u32x4*>(blk + qoff);
+                dd[j] = 0;
+            } else {
+                const u32x2 v = *reinterpret_cast<const u32x2_a2*>(blk + qoff);
+                wq[j] = u32x4{v.x, v.y, 0u, 0u};
+                dd[j] = ldw16(blk);
+            }
+        }
+        {
+            const float xs[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+            u32x4 th, tm, tl;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                uint32_t h, m, l;
+                mb_split3(tok_ok ? xs[2 * e] : 0.0f, tok_ok ? xs[2 * e + 1] : 0.0f, h, m, l);
+                th[e] = h;
+                tm[e] = m;
+                tl[e] = l;
+            }
+            const bf16x8 Ah = __builtin_bit_cast(bf16x8, th), Am = __builtin_bit_cast(bf16x8, tm),
+                         Al = __builtin_bit_cast(bf16x8, tl);
+            f32x4 sx{};
+            if constexpr (SC) {
+                sx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Ah, ones, f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                sx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Am, ones, sx, 0, 0, 0);
+                sx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Al, ones, sx, 0, 0, 0);
+            }
+#pragma unroll
+            for (int j = 0; j < NT; ++j) {
+                u32x4 bw;
+                if constexpr (QT == HIP_BRIDGE_BF16) {
+                    bw = wq[j];
+                } else {
+                    uint32_t u0 = wq[j].x, u1 = wq[j].y;
+                    if constexpr (QT == HIP_BRIDGE_Q4_0) {
+                        u0 = mask_bytes(u0 >> nsh, 0x0f0f0f0fu);
+                        u1 = mask_bytes(u1 >> nsh, 0x0f0f0f0fu);
+                    } else {
+                        u0 ^= 0x80808080u;
+                        u1 ^= 0x80808080u;
+                    }
+                    uint32_t p0, p1, p2, p3;
+                    mb_codes(u0, p0, p1);
+                    mb_codes(u1, p2, p3);
+                    bw = u32x4{p0, p1, p2, p3};
+                }
+                const bf16x8 Bw = __builtin_bit_cast(bf16x8, bw);
+                if constexpr (SC) {
+                    f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Ah, Bw, f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                    p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Am, Bw, p, 0, 0, 0);
+                    p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Al, Bw, p, 0, 0, 0);
+                    const float d = h2f(dd[j]);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[j][r] = fmaf(d, fmaf(-C, sx[r], p[r]), acc[j][r]);
+                } else {
+                    acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Ah, Bw, acc[j], 0, 0, 0);
+                    acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Am, Bw, acc[j], 0, 0, 0);
+                    acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Al, Bw, acc[j], 0, 0, 0);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < NT; ++j) s_red[wv][j][lane] = acc[j];
+    __syncthreads();
+    if (wv == 0) {
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+            f32x4 t = s_red[0][j][lane];
+#pragma unroll
+            for (int w = 1; w < KS; ++w) t += s_red[w][j][lane];
+            const int row = r0 + 16 * j + mn;
+            if (row >= a.total_rows) continue;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int tok = t0 + 4 * g + r;
+                if (tok < a.batch) a.seg[0].y[(int64_t)tok * a.total_rows + row] = t[r];
+            }
+        }
+    }
+}
+
+#ifndef ZL_GEMV_MB
+#define ZL_GEMV_MB 1
+#endif
+#ifndef ZL_GEMV_MB_WAVES
+#define ZL_GEMV_MB_WAVES 1024
+#endif
+// Launches k_gemv_mb for a batch of 2 to kGemmMfmaMinBatch - 1 tokens (Q4_0 / Q8_0 with
+// 2-byte aligned rows, BF16 with 16-byte aligned ones; cols % 32 == 0, at most 160 blocks;
+// x 16-byte aligned); returns false otherwise (the vector kernels take the product).
+template <int QT>
+static bool launch_mb_t(const GemvArgs& a, hipStream_t s) {
+    const int nblk = a.cols / 32;
+    const int64_t tiles = cdiv(a.total_rows, 16), ttiles = cdiv(a.batch, kMbTok);
+    // the fewest waves per workgroup that leave each at most 10 blocks (a wave's blocks are a
+    // serial chain of memory round trips: longer rows keep the vector kernels, 2560 x 10240
+    // at 8 tokens 22.7 us there against 35.5), then the widest row tiles that still give the
+    // grid ZL_GEMV_MB_WAVES waves
+    int ks = 0;
+    for (int k : {4, 8, 16})
+        if (!ks && cdiv(nblk, k) <= 10) ks = k;
+    if (!ks) return false;
+    int nt = 1;
+    for (int n : {4, 2})
+        if (nt == 1 && cdiv(tiles, n) * ttiles * ks >= ZL_GEMV_MB_WAVES) nt = n;
+    const dim3 grid((unsigned)cdiv(tiles, nt), (unsigned)ttiles);
+    auto go = [&](auto n_c) {
+        constexpr int N = decltype(n_c)::value;
+        if (ks == 4) k_gemv_mb<QT, N, 4><<<grid, 4 * kWave, 0, s>>>(a);
+        else if (ks == 8) k_gemv_mb<QT, N, 8><<<grid, 8 * kWave, 0, s>>>(a);
+        else k_gemv_mb<QT, N, 16><<<grid, 16 * kWave, 0, s>>>(a);
+    };
+    if (nt == 4) go(std::integral_constant<int, 4>{});
+    else if (nt == 2) go(std::integral_constant<int, 2>{});
+    else go(std::integral_constant<int, 1>{});
+    return true;
+}
+static bool launch_gemv_mb(int qtype, GemvArgs& a, hipStream_t s) {
+    if (!ZL_GEMV_MB || a.batch < 2 || a.batch >= kGemmMfmaMinBatch || a.cols % 32 != 0 || a.nseg != 1 ||
+        !a.seg[0].w || !a.seg[0].y || !a.x || !aligned16(a.x))
+        return false;
+    const uintptr_t wa = reinterpret_cast<uintptr_t>(a.seg[0].w);
+    a.row_bytes = gemv_row_bytes(qtype, a.cols);
+    switch (qtype) {
+        case HIP_BRIDGE_Q4_0:
+            return wa % 2 == 0 && launch_mb_t<HIP_BRIDGE_Q4_0>(a, s);
+        case HIP_BRIDGE_Q8_0:
+            return wa % 2 == 0 && launch_mb_t<HIP_BRIDGE_Q8_0>(a, s);
+        case HIP_BRIDGE_BF16:
+            return wa % 16 == 0 && a.row_bytes % 16 == 0 && launch_mb_t<HIP_BRIDGE_BF16>(a, s);
+        default:
+            return false;
+    }
+}
+
 static GemvArgs one_matrix(const void* w, const float* x, float* y, int rows, int cols, int batch) {
     GemvArgs a{};
     a.seg[0] = GemvSeg{(const unsigned char*)w, y, rows};
@@ -1873,6 +2084,10 @@ void hip_gemm(int qtype, const void* weights, const float* x, float* y, int batc
         if (rb > 0 && launch_gemm_mfma(qtype, weights, rb, x, y, rows, cols, batch_size, stream_of(stream))) return;
     }
     GemvArgs a = one_matrix(weights, x, y, rows, cols, batch_size);
+    if (launch_gemv_mb(qtype, a, stream_of(stream))) {
+        check_launch();
+        return;
+    }
     launch_gemv<GV_PLAIN>(qtype, a, stream_of(stream));
 }
 
