@@ -147,6 +147,53 @@ def test_attention_unsupported_group_is_noop(dev):
     assert np.all(d_out.to_numpy((32 * 64 * 4,), np.uint8) == 0x11)
 
 
+@pytest.mark.parametrize("kv_dtype", [B.F32, B.BF16])
+@pytest.mark.parametrize("qk", [False, True], ids=["plain", "qk"])
+def test_attention_decode_long_splits(dev, oracle, kv_dtype, qk):
+    """Splits of up to 1024 positions (8 sequences x 2 kv heads of a 32768-row cache: the
+    double-buffered step loop), plain and QK mode (q normalised and rotated in the kernel, the
+    cache only read), positions at both ends of the cache and in between."""
+    B_, nh, nkv, d, cap = 8, 8, 2, 128, 32768
+    positions = np.array([32767, 0, 1, 31, 1024, 20000, 32766, 777], np.int32)
+    rows = B_ * cap
+    kc = synth.normal_f32(13, "kc", (rows, nkv * d))
+    vc = synth.normal_f32(13, "vc", (rows, nkv * d))
+    if kv_dtype == B.BF16:
+        kc_dev, vc_dev = oracle.f32_to_bf16(kc), oracle.f32_to_bf16(vc)
+        kc, vc = oracle.bf16_to_f32(kc_dev), oracle.bf16_to_f32(vc_dev)
+    else:
+        kc_dev, vc_dev = kc, vc
+    q = synth.normal_f32(13, "q", (B_, nh * d), 0, 0.3 if not qk else 1.0)
+    scale = float(np.float32(1.0 / np.sqrt(d)))
+    row_base = np.arange(B_, dtype=np.int64) * cap
+    ws = dev.attentionWorkspaceBytes(B_, nh, nkv, d, cap)
+    d_out = dev.alloc(B_ * nh * d * 4)
+    keep = [dev.from_numpy(a) for a in (q, kc_dev, vc_dev, row_base, positions)]
+    d_q, d_kc, d_vc, d_rb, d_pos = keep
+    if qk:
+        wq = synth.normal_f32(13, "wq", (d,), 0, 0.1)
+        eps = np.float32(1e-6)
+        kc_ref, vc_ref = kc.copy(), vc.copy()
+        q_att = oracle.qk_norm_rope_kv(q.reshape(B_, nh, d), np.zeros((B_, 0), np.float32),
+                                       np.zeros((B_, 0), np.float32), wq, None, kc_ref, vc_ref, v_norm=False,
+                                       max_seq=cap, max_kv_dim=nkv * d, pos=positions, slots=row_base + positions,
+                                       n_heads=nh, n_kv_heads=0, head_dim=d, rotary_dim=0, base=1e4, eps=eps,
+                                       unit_offset=True).reshape(B_, nh * d)
+        d_wq = dev.from_numpy(wq)
+        keep.append(d_wq)
+        dev.attentionDecodeQk(kv_dtype, d_q, None, None, d_wq, None, False, d_kc, d_vc, d_out, rows, nkv * d, d_rb,
+                              0, d_pos, 0, cap, B_, nh, nkv, d, 0, 1e4, 1.0, float(eps), True, scale, 0.0, 0,
+                              dev.alloc(ws), ws)
+    else:
+        q_att = q
+        dev.attentionDecode(kv_dtype, d_q, d_kc, d_vc, d_out, rows, nkv * d, d_rb, 0, d_pos, 0, cap, B_, nh, nkv, d,
+                            scale, 0.0, 0, dev.alloc(ws), ws)
+    got = d_out.to_numpy((B_, nh * d), np.float32)
+    for b in range(B_):
+        check(got[b], q_att[b], kc, vc, int(row_base[b]), int(positions[b]), nh, nkv, d, scale, 0.0, 0,
+              f"seq {b} pos {positions[b]}")
+
+
 QK_SHAPES = [(8, 4, 256, 0), (8, 1, 512, 128), (8, 1, 256, 0), (4, 2, 64, 0), (16, 4, 128, 64)]
 
 

@@ -136,7 +136,7 @@ __device__ __forceinline__ void qk_rope8(float* x, int li, int half, const float
     }
 }
 
-template <typename KT, int D, int G, bool QK>
+template <typename KT, int D, int G, bool QK, bool DB>
 __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
     constexpr int LT = D / 8;                  // lanes per position
     constexpr int SLOTS = kAttnThreads / LT;   // positions in flight per workgroup
@@ -213,15 +213,15 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
     // zero row of this library): in bounds and never folded.
     const bool rows_ok = end > 0;  // uniform
     const KT* qsafe = (const KT*)g_attn_pad_row + li * 8;
-    auto load_step = [&](int t) {
+    auto load_into = [&](float (&kk)[U][8], float (&vv)[U][8], int t) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int tu = max(min(t + u * SLOTS, tc - 1), 0);
-            load8<KT>(rows_ok ? kbase + (rb + tu) * a.row_stride : qsafe, k[u]);
-            load8<KT>(rows_ok ? vbase + (rb + tu) * a.row_stride : qsafe, v[u]);
+            load8<KT>(rows_ok ? kbase + (rb + tu) * a.row_stride : qsafe, kk[u]);
+            load8<KT>(rows_ok ? vbase + (rb + tu) * a.row_stride : qsafe, vv[u]);
         }
     };
-    load_step(t0 + slot);
+    load_into(k, v, t0 + slot);
     // QK mode: the split holding the token's own position requests the raw K / V rows that
     // position is formed from (and the K norm factors) now, used after the loop; in the
     // other splits the same loads read an empty range (zeros, no memory access).
@@ -288,13 +288,31 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
         }
     };
 
-    for (int st = 0; st < nstep; ++st) {
-        const int t = t0 + slot + st * U * SLOTS;
-        if (st > 0) load_step(t);
+    auto fold_step = [&](const float (&kk)[U][8], const float (&vv)[U][8], int t) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             if (t + u * SLOTS >= tc) break;  // uniform within a lane group
-            fold(k[u], v[u], true);
+            fold(kk[u], vv[u], true);
+        }
+    };
+    if constexpr (DB) {
+        // Two register sets in turn: the next step's rows are requested before the current
+        // step is folded, so each step's round trip overlaps the previous step's arithmetic
+        // (a step past the range loads the range's last row again and is not folded).
+        float k2[U][8], v2[U][8];
+        for (int st = 0; st < nstep; st += 2) {
+            const int t = t0 + slot + st * U * SLOTS;
+            load_into(k2, v2, t + U * SLOTS);
+            fold_step(k, v, t);
+            if (st + 1 >= nstep) break;  // uniform
+            load_into(k, v, t + 2 * U * SLOTS);
+            fold_step(k2, v2, t + U * SLOTS);
+        }
+    } else {
+        for (int st = 0; st < nstep; ++st) {
+            const int t = t0 + slot + st * U * SLOTS;
+            if (st > 0) load_into(k, v, t);
+            fold_step(k, v, t);
         }
     }
     if constexpr (QK) {
@@ -469,20 +487,35 @@ __global__ __launch_bounds__(kMergeThreads) void k_attn_merge(AttnArgs a) {
     }
 }
 
-template <typename KT, int D, bool QK>
+template <typename KT, int D, bool QK, bool DB>
 static void launch_gq(const AttnArgs& a, hipStream_t s) {
     const unsigned grid = (unsigned)((int64_t)a.batch * a.nkv * a.hg * a.nsplit);
     switch (a.gq / a.hg) {
-        case 1: k_attn<KT, D, 1, QK><<<grid, kAttnThreads, 0, s>>>(a); break;
-        case 2: k_attn<KT, D, 2, QK><<<grid, kAttnThreads, 0, s>>>(a); break;
-        case 4: k_attn<KT, D, 4, QK><<<grid, kAttnThreads, 0, s>>>(a); break;
-        default: k_attn<KT, D, 8, QK><<<grid, kAttnThreads, 0, s>>>(a); break;
+        case 1: k_attn<KT, D, 1, QK, DB><<<grid, kAttnThreads, 0, s>>>(a); break;
+        case 2: k_attn<KT, D, 2, QK, DB><<<grid, kAttnThreads, 0, s>>>(a); break;
+        case 4: k_attn<KT, D, 4, QK, DB><<<grid, kAttnThreads, 0, s>>>(a); break;
+        default: k_attn<KT, D, 8, QK, DB><<<grid, kAttnThreads, 0, s>>>(a); break;
     }
 }
+// Double-buffered K/V steps where a split can exceed ZL_ATTN_DB_MIN positions (long steps
+// chains; its extra registers cost more than it saves on short splits). Measured (us, Gemma-4B
+// heads, f32 caches, positions ~U[0, 32767]): B = 256 5638 -> 5397, B = 64 1638 -> 1606, B = 8
+// 253 -> 249; at B = 1 (256-position splits) 53.3 -> 55.9 and in the 4B decode step (short
+// splits) 1451 -> 1482 us per token, so those keep one set.
+#ifndef ZL_ATTN_DB_MIN
+#define ZL_ATTN_DB_MIN 512
+#endif
 template <typename KT, int D>
 static void launch_g(const AttnArgs& a, bool qk, hipStream_t s) {
-    if (qk) launch_gq<KT, D, true>(a, s);
-    else launch_gq<KT, D, false>(a, s);
+    const int len = a.window > 0 ? std::min(a.window, a.max_len) : a.max_len;
+    const bool db = cdiv((int64_t)len, (int64_t)a.nsplit) > ZL_ATTN_DB_MIN;
+    if (qk) {
+        if (db) launch_gq<KT, D, true, true>(a, s);
+        else launch_gq<KT, D, true, false>(a, s);
+    } else {
+        if (db) launch_gq<KT, D, false, true>(a, s);
+        else launch_gq<KT, D, false, false>(a, s);
+    }
 }
 
 // Query heads per workgroup. Each workgroup loads its positions' K/V rows once for all the
