@@ -557,13 +557,16 @@ static void choose_heads(AttnArgs& a, int es) {
 // workgroups with a 32-position floor 10.8 / 14.1 / 18.0; 512 and 16: 9.9 / 13.0 / 14.7; 512
 // and 8: 9.0 / 13.0 / 14.7; 1024 and 16: 11.7 / 14.4 / 17.8. 32768-row cache, positions
 // ~U[0, 32767]: 60.8 us with 2048 workgroups, 53.5 with 512.
+#ifndef ZL_ATTN_SPLIT_MAX
+#define ZL_ATTN_SPLIT_MAX 1024
+#endif
 #ifndef ZL_ATTN_TARGET_WG
 #define ZL_ATTN_TARGET_WG 512
 #endif
 static void choose_split(AttnArgs& a, size_t ws_bytes) {
     const int len = a.window > 0 ? std::min(a.window, a.max_len) : a.max_len;
     const int64_t groups = (int64_t)a.batch * a.nkv * a.hg;
-    const int64_t want = std::max<int64_t>(cdiv(ZL_ATTN_TARGET_WG, groups), cdiv(len, 1024));
+    const int64_t want = std::max<int64_t>(cdiv(ZL_ATTN_TARGET_WG, groups), cdiv(len, ZL_ATTN_SPLIT_MAX));
     // shortest split: 8 positions in caches of up to 4096 rows, growing to 32 from 16384 rows
     a.chunk_min = (int)std::min<int64_t>(std::max<int64_t>(len / 512, ZL_ATTN_CHUNK_MIN), 32);
     int nsplit = (int)std::max<int64_t>(1, std::min<int64_t>({cdiv(len, a.chunk_min), want, (int64_t)kMaxSplit}));
