@@ -864,6 +864,11 @@ constexpr int kQ4bProMaxCols = 4096;  // PRO operands: 4 float4 each per thread 
 #ifndef ZL_GEMV_Q4B_WAVES
 #define ZL_GEMV_Q4B_WAVES 1024
 #endif
+// GeGLU pairs over two row sets (k_gemv_q4b SPL); 0 keeps both rows of a pair in every lane
+// (tuning builds).
+#ifndef ZL_Q4B_GEGLU_SPLIT
+#define ZL_Q4B_GEGLU_SPLIT 1
+#endif
 #ifndef ZL_GEMV_Q4B_NW
 #define ZL_GEMV_Q4B_NW 4
 #endif
@@ -1025,18 +1030,23 @@ __device__ __forceinline__ void q4b_pro_finish(const GemvArgs& a, f32x4 (&xv)[K]
     }
 }
 
-template <int QT, int MODE, int LPR, int RW, int BPL, bool PRO, int NW>
+template <int QT, int MODE, int LPR, int RW, int BPL, bool PRO, int NW, bool SPLIT = false>
 __global__ __launch_bounds__(NW * kWave) void k_gemv_q4b(GemvArgs a) {
     constexpr int T = NW * kWave;
-    constexpr int NM = MODE == GV_GEGLU ? 2 : 1;
     constexpr int SETS = kWave / LPR;
+    // SPL (GeGLU): the gate and up rows of a pair in two neighbouring sets, combined across
+    // the wave at the end, instead of both in every lane (twice the waves, half the blocks each)
+    constexpr bool SPL = SPLIT && MODE == GV_GEGLU && SETS >= 2;
+    constexpr int NM = MODE == GV_GEGLU && !SPL ? 2 : 1;
     constexpr int XK = (PRO ? kQ4bProMaxCols : kQ4bMaxCols) / 4 / T;  // x float4 per thread
     extern __shared__ __attribute__((aligned(16))) float s_xq[];
     __shared__ float s_red[NW];
     const int lane = threadIdx.x & 63;
     const int wv = threadIdx.x >> 6;
     const int li = lane % LPR, set = lane / LPR;
-    const int row0 = ((blockIdx.x * NW + wv) * SETS + set) * RW;
+    const int gset = (blockIdx.x * NW + wv) * SETS + set;
+    const int mat = SPL ? (gset & 1) : 0;  // SPL: 0 gate, 1 up
+    const int row0 = (SPL ? gset >> 1 : gset) * RW;
     // x (PRO: the prologue's operands) first: its loads complete before the weights' do, so
     // staging it waits on it alone
     const int n4 = a.cols / 4;
@@ -1063,7 +1073,7 @@ __global__ __launch_bounds__(NW * kWave) void k_gemv_q4b(GemvArgs a) {
         const int Rs = s0 ? R : s1 ? R - r0 : R - r0 - r1;
         const unsigned char* wb = s0 ? a.seg[0].w : s1 ? a.seg[1].w : a.seg[2].w;
         float* yb = s0 ? a.seg[0].y : s1 ? a.seg[1].y : a.seg[2].y;
-        wrow[r][0] = wb + (int64_t)Rs * a.row_bytes;
+        wrow[r][0] = (SPL && mat ? a.w_up : wb) + (int64_t)Rs * a.row_bytes;
         if constexpr (NM == 2) wrow[r][1] = a.w_up + (int64_t)Rs * a.row_bytes;
         yrow[r] = ok ? yb + Rs : nullptr;
     }
@@ -1143,7 +1153,17 @@ __global__ __launch_bounds__(NW * kWave) void k_gemv_q4b(GemvArgs a) {
     for (int r = 0; r < RW; ++r)
 #pragma unroll
         for (int m = 0; m < NM; ++m) acc[r][m] = group_sum<LPR>(acc[r][m]);
-    if (li == 0) {
+    if constexpr (SPL) {
+        // the up set's sums to the gate set's lanes (LPR lanes further)
+        float up[RW];
+#pragma unroll
+        for (int r = 0; r < RW; ++r) up[r] = __shfl_down(acc[r][0], LPR);
+        if (li == 0 && mat == 0) {
+#pragma unroll
+            for (int r = 0; r < RW; ++r)
+                if (yrow[r]) *yrow[r] = gelu_fast(acc[r][0]) * up[r];
+        }
+    } else if (li == 0) {
 #pragma unroll
         for (int r = 0; r < RW; ++r) {
             if (!yrow[r]) continue;
@@ -1186,20 +1206,26 @@ static bool launch_q4b(const GemvArgs& a, hipStream_t s) {
             break;
         }
     if (!lpr) return false;
-    auto waves = [&](int l, int rw) { return cdiv(a.total_rows, (int64_t)(kWave / l) * rw); };
+    // GeGLU pairs split over two sets (SPL in the kernel) where lanes per row leave at least
+    // two sets per wave: the row space counts each pair twice
+    const bool spl = ZL_Q4B_GEGLU_SPLIT && MODE == GV_GEGLU && !PRO;
+    int64_t vrows = spl ? 2 * (int64_t)a.total_rows : a.total_rows;
+    auto waves = [&](int l, int rw) { return cdiv(vrows, (int64_t)(kWave / l) * rw); };
     while (lpr < 64 && waves(lpr, 1) < ZL_GEMV_Q4B_WAVES && nblk % (2 * lpr) == 0) lpr *= 2;
+    if (spl && lpr == 64) vrows = a.total_rows;  // one set per wave: the pairs stay whole
     const int rw = waves(lpr, 2) >= 4 * ZL_GEMV_Q4B_WAVES ? 2 : 1;
     const int bpl = nblk / lpr;
     const unsigned grid = (unsigned)cdiv(waves(lpr, rw), (int64_t)NW);
     auto go = [&](auto lpr_c, auto rw_c) {
         constexpr int L = decltype(lpr_c)::value, RW = decltype(rw_c)::value;
+        constexpr bool SP = ZL_Q4B_GEGLU_SPLIT && MODE == GV_GEGLU && !PRO && L < 64;
         switch (bpl) {
-            case 1: k_gemv_q4b<QT, MODE, L, RW, 1, PRO, NW><<<grid, NW * kWave, lds, s>>>(a); break;
-            case 2: k_gemv_q4b<QT, MODE, L, RW, 2, PRO, NW><<<grid, NW * kWave, lds, s>>>(a); break;
-            case 3: k_gemv_q4b<QT, MODE, L, RW, 3, PRO, NW><<<grid, NW * kWave, lds, s>>>(a); break;
-            case 4: k_gemv_q4b<QT, MODE, L, RW, 4, PRO, NW><<<grid, NW * kWave, lds, s>>>(a); break;
-            case 5: k_gemv_q4b<QT, MODE, L, RW, 5, PRO, NW><<<grid, NW * kWave, lds, s>>>(a); break;
-            default: k_gemv_q4b<QT, MODE, L, RW, 6, PRO, NW><<<grid, NW * kWave, lds, s>>>(a); break;
+            case 1: k_gemv_q4b<QT, MODE, L, RW, 1, PRO, NW, SP><<<grid, NW * kWave, lds, s>>>(a); break;
+            case 2: k_gemv_q4b<QT, MODE, L, RW, 2, PRO, NW, SP><<<grid, NW * kWave, lds, s>>>(a); break;
+            case 3: k_gemv_q4b<QT, MODE, L, RW, 3, PRO, NW, SP><<<grid, NW * kWave, lds, s>>>(a); break;
+            case 4: k_gemv_q4b<QT, MODE, L, RW, 4, PRO, NW, SP><<<grid, NW * kWave, lds, s>>>(a); break;
+            case 5: k_gemv_q4b<QT, MODE, L, RW, 5, PRO, NW, SP><<<grid, NW * kWave, lds, s>>>(a); break;
+            default: k_gemv_q4b<QT, MODE, L, RW, 6, PRO, NW, SP><<<grid, NW * kWave, lds, s>>>(a); break;
         }
     };
     using I1 = std::integral_constant<int, 1>;
@@ -1207,9 +1233,10 @@ static bool launch_q4b(const GemvArgs& a, hipStream_t s) {
     if (lpr == 8) {  // odd block counts per lane only
         auto go8 = [&](auto rw_c) {
             constexpr int RW = decltype(rw_c)::value;
-            if (bpl == 1) k_gemv_q4b<QT, MODE, 8, RW, 1, PRO, NW><<<grid, NW * kWave, lds, s>>>(a);
-            else if (bpl == 3) k_gemv_q4b<QT, MODE, 8, RW, 3, PRO, NW><<<grid, NW * kWave, lds, s>>>(a);
-            else k_gemv_q4b<QT, MODE, 8, RW, 5, PRO, NW><<<grid, NW * kWave, lds, s>>>(a);
+            constexpr bool SP = ZL_Q4B_GEGLU_SPLIT && MODE == GV_GEGLU && !PRO;
+            if (bpl == 1) k_gemv_q4b<QT, MODE, 8, RW, 1, PRO, NW, SP><<<grid, NW * kWave, lds, s>>>(a);
+            else if (bpl == 3) k_gemv_q4b<QT, MODE, 8, RW, 3, PRO, NW, SP><<<grid, NW * kWave, lds, s>>>(a);
+            else k_gemv_q4b<QT, MODE, 8, RW, 5, PRO, NW, SP><<<grid, NW * kWave, lds, s>>>(a);
         };
         rw == 2 ? go8(I2{}) : go8(I1{});
     } else if (lpr == 16) rw == 2 ? go(std::integral_constant<int, 16>{}, I2{}) : go(std::integral_constant<int, 16>{}, I1{});
