@@ -127,6 +127,27 @@ def test_gemv_qkv_equals_three_gemvs(dev, q_rows, k_rows, v_rows):
         np.testing.assert_array_equal(fused[i], d_y.to_numpy((m.shape[0],), np.float32), err_msg=f"matrix {i}")
 
 
+@pytest.mark.parametrize("qtype", [B.Q4_0, B.Q8_0])
+@pytest.mark.parametrize("rows,cols", [(77, 256), (1001, 2560), (10240, 2560), (333, 4096), (65, 12288),
+                                       (20001, 512), (6144, 1536)])
+def test_gemv_geglu_pairs_bitexact(dev, qtype, rows, cols):
+    """The fused gate.up product (pairs over two row sets of a wave where its lanes per row
+    leave several sets; both rows in every lane at 64 lanes per row) equals gelu(g) * u of
+    the two single products bit for bit on integer operands (every sum exact in f32)."""
+    gw, _ = int_matrix(qtype, rows, cols, seed=rows + 1, scale_pow=-3)
+    uw, _ = int_matrix(qtype, rows, cols, seed=rows + 2, scale_pow=-3)
+    x = np.random.default_rng(cols).integers(-3, 4, cols).astype(np.float32)
+    d_gw, d_uw, d_x = dev.from_numpy(gw.reshape(-1)), dev.from_numpy(uw.reshape(-1)), dev.from_numpy(x)
+    d_act, d_g, d_u = dev.alloc(rows * 4), dev.alloc(rows * 4), dev.alloc(rows * 4)
+    d_act.fill(0xAB)
+    dev.gemvPro(qtype, d_gw, d_uw, d_x, d_act, rows, cols, None)
+    dev.gemv(qtype, d_gw, d_x, d_g, rows, cols)
+    dev.gemv(qtype, d_uw, d_x, d_u, rows, cols)
+    dev.geglu(d_g, d_u, d_g, rows)
+    assert_bitexact(d_act.to_numpy((rows,), np.float32), d_g.to_numpy((rows,), np.float32),
+                    f"geglu pair {rows} x {cols}")
+
+
 @pytest.mark.parametrize("rows", [10240, 77])
 def test_gemv_geglu_q4_0(dev, oracle, rows):
     cols = 2560
