@@ -50,6 +50,9 @@ __device__ __attribute__((aligned(16))) float g_qk_pad_row[2 * kMaxHalf];
 #ifndef ZL_QK_TPW
 #define ZL_QK_TPW 2
 #endif
+#ifndef ZL_QK_NP2
+#define ZL_QK_NP2 0
+#endif
 #ifndef ZL_QK_TPW_MIN
 #define ZL_QK_TPW_MIN 1024
 #endif
@@ -115,7 +118,7 @@ __host__ __device__ constexpr int qk_slots() {
     return 4 * (kWave / (D / 2 / Chunk<T>::E));
 }
 
-template <typename T, int D, int TPW>
+template <typename T, int D, int TPW, int NP = 1>
 __global__ __launch_bounds__(256) void k_qk_fused(QkArgs a) {
     using C = Chunk<T>;
     constexpr int E = C::E;
@@ -182,14 +185,18 @@ __global__ __launch_bounds__(256) void k_qk_fused(QkArgs a) {
     const bool stage_q = ti < D / 4, stage_k = ti >= D / 4 && ti < D / 2;
     const float* ws = stage_q && has_wq ? wqb : stage_k && has_wk ? wkb : g_qk_pad_row;
     const f32x4 wstage = ldf4(ws + (stage_q || stage_k ? 4 * wi : 0));
-    u32x4 ra[TPW], rb[TPW];
+    // (NP > 1: the head rows of the token's first NP passes, all requested here)
+    u32x4 ra[TPW][NP], rb[TPW][NP];
 #pragma unroll
-    for (int tt = 0; tt < TPW; ++tt) {
-        const bool row_ok = gslot < HR && readable(gslot, tb + tt);
-        const T* src0 = row_ok ? src_of(gslot, tb + tt) : (const T*)g_qk_pad_row;
-        ra[tt] = lds16(src0 + c0 * E);
-        rb[tt] = lds16(src0 + c1 * E);
-    }
+    for (int tt = 0; tt < TPW; ++tt)
+#pragma unroll
+        for (int q = 0; q < NP; ++q) {
+            const int hr = gslot + q * hstep;
+            const bool row_ok = hr < HR && readable(hr, tb + tt);
+            const T* src0 = row_ok ? src_of(hr, tb + tt) : (const T*)g_qk_pad_row;
+            ra[tt][q] = lds16(src0 + c0 * E);
+            rb[tt][q] = lds16(src0 + c1 * E);
+        }
 
     int p[TPW];
     int64_t row[TPW];
@@ -224,65 +231,70 @@ __global__ __launch_bounds__(256) void k_qk_fused(QkArgs a) {
     }
     __syncthreads();
 
+    // One head row of token tb + tt: norm, RoPE, store.
+    auto process = [&](int hr, int tt, u32x4 xa, u32x4 xb) {
+        const int t = tb + tt;
+        const int kind = hr < a.nh ? 0 : hr < a.nh + a.nkv ? 1 : 2;  // Q, K, V
+        float x0[E], x1[E];
+        C::unpack(xa, x0);
+        C::unpack(xb, x1);
+        const bool norm = kind == 0 ? a.do_qnorm : kind == 1 ? a.do_knorm : a.v_norm;
+        if (norm) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int j = 0; j < E; ++j) {
+                ss = fmaf(x0[j], x0[j], ss);
+                ss = fmaf(x1[j], x1[j], ss);
+            }
+            ss = group_sum<LH>(ss);
+            // 1 / sqrt(mean + eps) by the hardware reciprocal square root (within 1 ulp
+            // of the reference's IEEE sqrt and divide, and ~20 instructions shorter per
+            // row: this kernel's arithmetic is exposed, c2 7.89 -> 7.72 us); D is a power
+            // of two, so the mean is exact
+            const float inv = __builtin_amdgcn_rsqf(ss * (1.0f / (float)D) + a.eps);
+            if (kind == 2) {  // Gemma-4 V: no-scale norm
+#pragma unroll
+                for (int j = 0; j < E; ++j) {
+                    x0[j] = x0[j] * inv;
+                    x1[j] = x1[j] * inv;
+                }
+            } else {
+                const float* sw = kind == 0 ? s_wq : s_wk;  // factors (1+w), w or 1
+#pragma unroll
+                for (int j = 0; j < E; ++j) {
+                    x0[j] = (x0[j] * inv) * sw[c0 * E + j];
+                    x1[j] = (x1[j] * inv) * sw[c1 * E + j];
+                }
+            }
+        }
+        if (a.do_rope && kind != 2 && hl < R) {
+#pragma unroll
+            for (int j = 0; j < E; ++j) {
+                const float c = s_cos[tt][hl * E + j], s = s_sin[tt][hl * E + j];
+                const float v0 = x0[j], v1 = x1[j];
+                x0[j] = v0 * c - v1 * s;
+                x1[j] = v0 * s + v1 * c;
+            }
+        }
+        T* dst;
+        if (kind == 0) dst = (T*)a.q + ((int64_t)t * a.nh + hr) * D;
+        else if (kind == 1) dst = (T*)a.kdst + row[tt] * a.row_stride + (int64_t)(hr - a.nh) * D;
+        else dst = (T*)a.vdst + row[tt] * a.row_stride + (int64_t)(hr - a.nh - a.nkv) * D;
+        sts16(dst + c0 * E, C::pack(x0));
+        sts16(dst + c1 * E, C::pack(x1));
+    };
 #pragma unroll
     for (int tt = 0; tt < TPW; ++tt) {
-        const int t = tb + tt;
-        for (int hr = gslot; hr < HR; hr += hstep) {
+#pragma unroll
+        for (int q = 0; q < NP; ++q) {
+            const int hr = gslot + q * hstep;
+            if (hr < HR && active(hr, tt)) process(hr, tt, ra[tt][q], rb[tt][q]);
+        }
+        // passes past the preloaded ones: their rows requested in turn
+        for (int hr = gslot + NP * hstep; hr < HR; hr += hstep) {
             if (!active(hr, tt)) continue;
-            u32x4 xa = ra[tt], xb = rb[tt];
-            if (hr != gslot) {
-                const T* src = src_of(hr, t);
-                xa = lds16(src + c0 * E);
-                xb = lds16(src + c1 * E);
-            }
-            const int kind = hr < a.nh ? 0 : hr < a.nh + a.nkv ? 1 : 2;  // Q, K, V
-            float x0[E], x1[E];
-            C::unpack(xa, x0);
-            C::unpack(xb, x1);
-            const bool norm = kind == 0 ? a.do_qnorm : kind == 1 ? a.do_knorm : a.v_norm;
-            if (norm) {
-                float ss = 0.0f;
-#pragma unroll
-                for (int j = 0; j < E; ++j) {
-                    ss = fmaf(x0[j], x0[j], ss);
-                    ss = fmaf(x1[j], x1[j], ss);
-                }
-                ss = group_sum<LH>(ss);
-                // 1 / sqrt(mean + eps) by the hardware reciprocal square root (within 1 ulp
-                // of the reference's IEEE sqrt and divide, and ~20 instructions shorter per
-                // row: this kernel's arithmetic is exposed, c2 7.89 -> 7.72 us); D is a power
-                // of two, so the mean is exact
-                const float inv = __builtin_amdgcn_rsqf(ss * (1.0f / (float)D) + a.eps);
-                if (kind == 2) {  // Gemma-4 V: no-scale norm
-#pragma unroll
-                    for (int j = 0; j < E; ++j) {
-                        x0[j] = x0[j] * inv;
-                        x1[j] = x1[j] * inv;
-                    }
-                } else {
-                    const float* sw = kind == 0 ? s_wq : s_wk;  // factors (1+w), w or 1
-#pragma unroll
-                    for (int j = 0; j < E; ++j) {
-                        x0[j] = (x0[j] * inv) * sw[c0 * E + j];
-                        x1[j] = (x1[j] * inv) * sw[c1 * E + j];
-                    }
-                }
-            }
-            if (a.do_rope && kind != 2 && hl < R) {
-#pragma unroll
-                for (int j = 0; j < E; ++j) {
-                    const float c = s_cos[tt][hl * E + j], s = s_sin[tt][hl * E + j];
-                    const float v0 = x0[j], v1 = x1[j];
-                    x0[j] = v0 * c - v1 * s;
-                    x1[j] = v0 * s + v1 * c;
-                }
-            }
-            T* dst;
-            if (kind == 0) dst = (T*)a.q + ((int64_t)t * a.nh + hr) * D;
-            else if (kind == 1) dst = (T*)a.kdst + row[tt] * a.row_stride + (int64_t)(hr - a.nh) * D;
-            else dst = (T*)a.vdst + row[tt] * a.row_stride + (int64_t)(hr - a.nh - a.nkv) * D;
-            sts16(dst + c0 * E, C::pack(x0));
-            sts16(dst + c1 * E, C::pack(x1));
+            const T* src = src_of(hr, tb + tt);
+            process(hr, tt, lds16(src + c0 * E), lds16(src + c1 * E));
         }
     }
 }
@@ -428,7 +440,11 @@ static void launch_qk_t(const QkArgs& a, const RopeTab& tab, hipStream_t s) {
             constexpr int DD = decltype(d_c)::value;
             constexpr int SL = qk_slots<T, DD>();
             const bool multi = TP > 1 && a.n_tokens >= ZL_QK_TPW_MIN && HR <= SL;
+            // ZL_QK_NP2: a token's two passes of head rows requested at once (NP = 2); measured
+            // slower for Gemma-27B heads at 8192 tokens (42.9 -> 45.0 us), so off by default
+            const bool two_pass = ZL_QK_NP2 && !multi && cdiv(HR, SL * (int)gy(SL)) == 2;
             if (multi) k_qk_fused<T, DD, TP><<<dim3(gridm, gy(SL)), 256, 0, s>>>(a);
+            else if (two_pass) k_qk_fused<T, DD, 1, 2><<<dim3(grid, gy(SL)), 256, 0, s>>>(a);
             else k_qk_fused<T, DD, 1><<<dim3(grid, gy(SL)), 256, 0, s>>>(a);
         };
         if (a.D == 64) go(std::integral_constant<int, 64>{});
