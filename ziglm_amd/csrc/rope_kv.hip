@@ -50,6 +50,11 @@ __device__ __attribute__((aligned(16))) float g_qk_pad_row[2 * kMaxHalf];
 #ifndef ZL_QK_TPW
 #define ZL_QK_TPW 2
 #endif
+// launches of at most this many tokens take a workgroup per token and pass of head rows (for
+// all token counts: Gemma-27B heads at 8192 tokens 43.9 -> 46.3 us, so not for prefill)
+#ifndef ZL_QK_GY_TOKENS
+#define ZL_QK_GY_TOKENS 64
+#endif
 #ifndef ZL_QK_NP2
 #define ZL_QK_NP2 0
 #endif
@@ -429,7 +434,9 @@ static void launch_qk_t(const QkArgs& a, const RopeTab& tab, hipStream_t s) {
         // Few tokens (decode): one workgroup per pass of head rows, so no workgroup loops
         // (each pass would wait for its own loads); many tokens: the token's rows in turn.
         const int HR = a.nh + 2 * a.nkv;
-        auto gy = [&](int slots) { return (unsigned)(a.n_tokens <= 64 ? std::max<int64_t>(1, cdiv(HR, slots)) : 1); };
+        auto gy = [&](int slots) {
+            return (unsigned)(a.n_tokens <= ZL_QK_GY_TOKENS ? std::max<int64_t>(1, cdiv(HR, slots)) : 1);
+        };
         // Two tokens per workgroup (the weight staging and the barrier shared by both) for
         // launches with many tokens whose head rows fit one pass (Gemma-4B at 2048 tokens:
         // 7.87 -> 7.76 us; with two passes per token the second token's passes follow the
