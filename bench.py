@@ -48,9 +48,20 @@ PEAK_HBM_GBS = 8000.0  # MI355X HBM3E peak
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 matrix peak
 MALL_BYTES = 256 << 20
 # --eager: op timings launch from the host between events instead of replaying graphs (for
-# kernel traces: rocprofv3 --kernel-trace faults inside its graph-launch interception after
-# many replays)
+# kernel traces: rocprofv3 --kernel-trace has faulted (SIGSEGV, faulting PC inside its
+# preloaded library) inside hipGraphLaunch after many replays, twice). Under a profiler
+# (profiler_attached) every timing is eager whatever the flags: graphs are never launched.
 EAGER = False
+
+
+def profiler_attached(env=None):
+    """True when a ROCm profiler's library is preloaded into this process (rocprofv3 sets
+    LD_PRELOAD to its tool library and exports ROCPROF_* / ROCP_* settings). Read from the
+    environment only, before any GPU call."""
+    env = os.environ if env is None else env
+    if "rocprof" in env.get("LD_PRELOAD", "").lower():
+        return True
+    return any(k.startswith(("ROCPROF", "ROCP_")) for k in env)
 METRIC = "fused-op HBM GB/s (% of MI355X peak) + µs per Gemma layer, decode & 2k prefill"
 
 
@@ -107,26 +118,31 @@ def time_launches_us(dev, fn, sets, n_launch, warm_ms=20.0, reps=5):
     return ms * 1000.0 / n_launch
 
 
-def stream_ceiling(dev, n_in, n_out, nbytes, min_total=3 * MALL_BYTES, n_launch=100):
-    """Practical ceiling of a byte mix: the fastest launch shape of the library's reference
-    streaming kernel (hip_stream_ref: n_in reads and n_out writes of nbytes each, nothing
-    else) over buffer sets that together exceed the Infinity Cache. Returns (us, shape)."""
+def stream_ceiling(dev, n_in, n_out, nbytes, inplace=False, min_total=3 * MALL_BYTES, n_launch=100):
+    """Practical ceiling of a byte mix: the fastest launch shape (workgroup size, chunks per
+    thread, load / store cache policy) of the library's reference streaming kernel
+    (hip_stream_ref: n_in reads and n_out writes of nbytes each, nothing else) over buffer
+    sets that together exceed the Infinity Cache. inplace: the mix of an op that rewrites its
+    first input (x += ...): the fastest of that in-place form (output 0 = input 0) and the
+    form with separate outputs. Returns (us, shape, "inplace" | "separate")."""
     per = (n_in + n_out) * nbytes
-    nsets = int(min(8, max(2, math.ceil(min_total / per))))
+    nsets = int(min(64, max(2, math.ceil(min_total / per))))
     sets = [[dev.alloc(nbytes) for _ in range(n_in + n_out)] for _ in range(nsets)]
     for st in sets:
         for buf in st:
             buf.fill(0x3C)
-    best = (float("inf"), -1)
-    for shp in range(dev.b.hip_stream_ref_shapes()):
-        def fn(d, st, shp=shp):
-            i1 = st[1].ptr if n_in == 2 else None
-            o1 = st[n_in + 1].ptr if n_out == 2 else None
-            rc = d.b.hip_stream_ref(n_in, n_out, st[0].ptr, i1, st[n_in].ptr, o1, nbytes, shp, d.stream)
-            if rc != 0:
-                raise RuntimeError(f"hip_stream_ref: {rc}")
-        us = time_launches_us(dev, fn, sets, max(n_launch, 4 * nsets))
-        best = min(best, (us, shp))
+    best = (float("inf"), -1, "separate")
+    for form in (("separate", "inplace") if inplace else ("separate",)):
+        for shp in range(dev.b.hip_stream_ref_shapes()):
+            def fn(d, st, shp=shp, form=form):
+                i1 = st[1].ptr if n_in == 2 else None
+                o0 = st[0].ptr if form == "inplace" else st[n_in].ptr
+                o1 = st[n_in + 1].ptr if n_out == 2 else None
+                rc = d.b.hip_stream_ref(n_in, n_out, st[0].ptr, i1, o0, o1, nbytes, shp, d.stream)
+                if rc != 0:
+                    raise RuntimeError(f"hip_stream_ref: {rc}")
+            us = time_launches_us(dev, fn, sets, max(n_launch, 4 * nsets))
+            best = min(best, (us, shp, form))
     for st in sets:
         for buf in st:
             buf.deinit()
@@ -162,14 +178,20 @@ def fill_tiled(buf, src):
         done += c
 
 
-def make_sets(dev, shape, T, dtype, min_total=3 * MALL_BYTES, max_sets=8, cache_rows=None, pos0=0, thetas=None):
-    """Buffer sets for the rotation; set 0 seeded, others copies. thetas: RoPE bases the
-    sets cycle through (set i takes thetas[i % len]; the number of sets is then a multiple)."""
+def make_sets(dev, shape, T, dtype, min_total=3 * MALL_BYTES, max_sets=64, cache_rows=None, pos0=0, thetas=None):
+    """Buffer sets for the rotation; set 0 seeded, others copies. Every op timed over them
+    touches only its own tensors of each set, so the number of sets is chosen for the op
+    with the fewest bytes: cycling through the sets, each op still moves at least
+    `min_total` (3x the Infinity Cache) before it returns to a set, and so streams from HBM.
+    thetas: RoPE bases the sets cycle through (set i takes thetas[i % len]; the number of
+    sets is then a multiple)."""
     L0 = LY.LayerBuffers(dev, shape, T, dtype, cache_rows=cache_rows)
     per = sum(b.size_bytes for b in (L0.x, L0.xb, L0.ao, L0.fo, L0.q, L0.k, L0.v, L0.gate, L0.up, L0.act))
-    nsets = int(min(max_sets, max(2, math.ceil(min_total / per))))
+    es = 4 if dtype == B.F32 else 2
+    least = min(LY.op_bytes(shape, T, es).values())
+    nsets = int(min(max_sets, max(2, math.ceil(min_total / least))))
     if thetas:
-        nsets = max(len(thetas), nsets - nsets % len(thetas))
+        nsets += (-nsets) % len(thetas)
     p = pool(dtype)
     for name in ("x", "xb", "ao", "fo", "q", "k", "v", "gate", "up", "act"):
         fill_tiled(getattr(L0, name), p)
@@ -209,13 +231,16 @@ def free_sets(sets):
 # ---------------------------------------------------------------------------------------
 
 def op_mix(shape, T, es):
-    """(reads, writes, bytes per stream) of each op's activation traffic: the byte mix its
-    same-size streaming ceiling moves (the few KB of norm weights and positions aside)."""
+    """(reads, writes, bytes per stream, in place) of each op's activation traffic: the byte
+    mix its same-size streaming ceiling moves (the few KB of norm weights and positions
+    aside)."""
     H, I = shape.H, shape.I
     qkv = T * (shape.nh + 2 * shape.nkv) * shape.D * es  # Q, K, V in; Q, K row, V row out
-    return {"input_norm": (1, 1, T * H * es), "add_rmsnorm": (2, 2, T * H * es),
-            "qk_norm_rope_kv": (1, 1, qkv), "norm_add_norm": (2, 2, T * H * es), "geglu": (2, 1, T * I * es),
-            "norm_add": (2, 1, T * H * es), "norm_add_norm_next": (2, 2, T * H * es)}
+    # the 4th field: the op rewrites its first input in place (x += ...)
+    return {"input_norm": (1, 1, T * H * es, False), "add_rmsnorm": (2, 2, T * H * es, True),
+            "qk_norm_rope_kv": (1, 1, qkv, False), "norm_add_norm": (2, 2, T * H * es, True),
+            "geglu": (2, 1, T * I * es, False), "norm_add": (2, 1, T * H * es, True),
+            "norm_add_norm_next": (2, 2, T * H * es, True)}
 
 
 def bench_prefill(dev, shape, T, dtype, steps, warmup, ops_launches=100, thetas=None):
@@ -235,11 +260,11 @@ def bench_prefill(dev, shape, T, dtype, steps, warmup, ops_launches=100, thetas=
         us = time_launches_us(dev, LY.OPS[name], sets, max(ops_launches, len(sets) * 4))
         if mix[name] not in ceilings:
             ceilings[mix[name]] = stream_ceiling(dev, *mix[name])
-        cu, cshape = ceilings[mix[name]]
+        cu, cshape, cform = ceilings[mix[name]]
         ops[name] = {"us": round(us, 3), "bytes": nb[name], "GBps": round(nb[name] / us / 1e3, 1),
                      "frac_peak": round(nb[name] / us / 1e3 / PEAK_HBM_GBS, 4),
                      "ceiling": {"us": round(cu, 3), "reads": mix[name][0], "writes": mix[name][1],
-                                 "bytes_per_stream": mix[name][2], "shape": cshape,
+                                 "bytes_per_stream": mix[name][2], "shape": cshape, "form": cform,
                                  "GBps": round((mix[name][0] + mix[name][1]) * mix[name][2] / cu / 1e3, 1),
                                  "frac_of_ceiling": round(cu / us, 4)}}
         log(f"  {name:20s} {us:9.2f} us  {nb[name] / us / 1e3:8.1f} GB/s  (same-size stream {cu:.2f} us, "
@@ -254,28 +279,38 @@ def bench_prefill(dev, shape, T, dtype, steps, warmup, ops_launches=100, thetas=
                                                     "frac_peak": round(b_ / us / 1e3 / PEAK_HBM_GBS, 4)}
             log(f"  qk at theta {th:g}: {us:.2f} us")
 
-    def steps_graph(n):
-        def body():
-            for i in range(n):
-                LY.run_chain(dev, sets[i % len(sets)])
-        return Graph(dev, body)
+    def chain_ms(n, fused, warm):
+        """ms for exactly n chain passes between two events: one graph replay (after `warm`
+        untimed passes), or with EAGER the same passes launched from the host."""
+        def body(k):
+            for i in range(k):
+                LY.run_chain(dev, sets[i % len(sets)], fused=fused)
+        if EAGER:
+            body(max(1, warm))
+            dev.sync()
+            e0, e1 = dev.event(), dev.event()
+            dev.record(e0)
+            body(n)
+            dev.record(e1)
+            ms_ = dev.elapsed_ms(e0, e1)
+            dev.b.hip_event_destroy(e0)
+            dev.b.hip_event_destroy(e1)
+            return ms_
+        gw = Graph(dev, lambda: body(max(1, warm)))
+        gw.launch()
+        dev.sync()
+        gw.destroy()
+        g = Graph(dev, lambda: body(n))
+        g.launch()  # untimed first replay
+        dev.sync()
+        ms_ = time_graph_ms(dev, g)
+        g.destroy()
+        return ms_
 
-    gw = steps_graph(max(1, warmup))
-    gw.launch()
-    dev.sync()
-    gw.destroy()
-    g = steps_graph(steps)
-    dev.sync()
-    ms = time_graph_ms(dev, g)  # exactly `steps` chain passes between the two events
-    g.destroy()
+    ms = chain_ms(steps, False, warmup)
     chain_b = LY.chain_bytes(shape, T, es)
     fused_b = LY.chain_bytes(shape, T, es, fused=True)
-
-    gf = Graph(dev, lambda: [LY.run_chain(dev, sets[i % len(sets)], fused=True) for i in range(steps)])
-    gf.launch()
-    dev.sync()
-    ms_f = time_graph_ms(dev, gf)
-    gf.destroy()
+    ms_f = chain_ms(steps, True, steps)
     isolated = sum(ops[k]["us"] for k in LY.CHAIN)
     res = {
         "T": T, "shape": shape.name, "io_dtype": "bf16" if dtype == B.BF16 else "f32",
@@ -389,11 +424,15 @@ def bench_decode(dev, B_, pos_seed=4, n_launch=200):
 GATHER_QTYPES = {"q8_0": B.Q8_0, "q4_0": B.Q4_0, "bf16": B.BF16}
 
 
-def gather_case(dev, name, vocab=262144, dim=2560, n_tok=4096, n_rep=64, nsets=8):
+def gather_case(dev, name, vocab=262144, dim=2560, n_tok=4096, n_rep=64, nsets=None):
     """c3: a [vocab x dim] table of `name` rows, `nsets` id lists (4032 uniform + 64 repeated
-    ids) and f32 outputs; returns (launch fn, sets, algorithmic bytes, buffers to free)."""
+    ids, each list its own seed) and f32 outputs; by default enough lists that one cycle
+    through them moves 3x the Infinity Cache (table rows and outputs), so a table row read
+    again has left that cache. Returns (launch fn, sets, algorithmic bytes, buffers to free)."""
     qt = GATHER_QTYPES[name]
     rb = {"q8_0": dim // 32 * 34, "q4_0": dim // 32 * 18, "bf16": dim * 2}[name]
+    if nsets is None:
+        nsets = int(min(64, max(2, math.ceil(3 * MALL_BYTES / (n_tok * (rb + dim * 4))))))
     scale = np.float32(np.sqrt(np.float32(dim)))
     id_sets = [dev.from_numpy(synth.gather_ids(2 + i, n_tok, vocab, n_repeat=n_rep)) for i in range(nsets)]
     outs = [dev.alloc(n_tok * dim * 4) for _ in range(nsets)]
@@ -776,6 +815,12 @@ def main():
 
     global EAGER
     EAGER = bool(a.only and a.eager)
+    if profiler_attached():
+        # never replay graphs under a profiler's preloaded library (see EAGER above)
+        if not EAGER:
+            log("profiler library preloaded: every timing below is eager (host launches between "
+                "events); no graph is captured or launched")
+        EAGER = True
     dev = HipDevice()
     log(f"device {dev.name} {dev.total_vram_bytes / 2**30:.0f} GiB, {dev.b.version()}")
     shape, T = (LY.GEMMA_4B, 2048) if a.config == "c2" else (LY.GEMMA_27B, 8192)
@@ -784,10 +829,10 @@ def main():
         if a.only.startswith("gather_"):
             fn, sets, traffic, _ = gather_case(dev, a.only[len("gather_"):])
         elif a.only == "decode_step":
-            print(json.dumps(bench_decode_step(dev, graph=not a.eager)))
+            print(json.dumps(bench_decode_step(dev, graph=not EAGER)))
             return
         elif a.only == "gguf_decode":
-            print(json.dumps(bench_gguf_decode(dev, graph=not a.eager)))
+            print(json.dumps(bench_gguf_decode(dev, graph=not EAGER)))
             return
         elif a.only == "c5":
             print(json.dumps({f"B{b_}": bench_decode(dev, b_) for b_ in (1, 8, 64, 256)}))
@@ -811,7 +856,7 @@ def main():
             sets, _ = make_sets(dev, shape, T, B.BF16)
             fn = LY.OPS[a.only]
             traffic = LY.op_bytes(shape, T, 2)[a.only]
-        if a.eager:
+        if EAGER:
             e0, e1 = dev.event(), dev.event()
             for i in range(len(sets)):
                 fn(dev, sets[i])
@@ -824,7 +869,7 @@ def main():
         else:
             us = time_launches_us(dev, fn, sets, a.steps)
         print(json.dumps({"op": a.only, "config": a.config, "us": us, "bytes": traffic, "GBps": traffic / us / 1e3,
-                          "eager": a.eager}))
+                          "eager": EAGER}))
         return
 
     t_start = time.time()
@@ -881,9 +926,9 @@ def main():
         log("gemm (prefill projections, matrix cores)")
         cfgs["gemm_prefill"] = bench_gemm_prefill(dev)
         log("decode step (34 layers, graph)")
-        cfgs["decode_step"] = bench_decode_step(dev)
+        cfgs["decode_step"] = bench_decode_step(dev, graph=not EAGER)
         log("GGUF load + E2B-shaped decode")
-        cfgs["gguf_e2b_decode"] = bench_gguf_decode(dev)
+        cfgs["gguf_e2b_decode"] = bench_gguf_decode(dev, graph=not EAGER)
         log("c1/c5 decode")
         cfgs["c5_decode"] = {}
         for b_ in (1, 8, 64, 256):

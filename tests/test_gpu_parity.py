@@ -233,6 +233,40 @@ def test_rmsnorm_add_rmsnorm(dev, oracle, dtype, n, rows):
         assert_bf16(go, out_ref, 1, floor=floor_o, what="bf16 norm2(x)")
 
 
+@pytest.mark.parametrize("dtype,n,rows", [(B.F32, 2560, 64), (B.BF16, 2560, 2048), (B.BF16, 5376, 64)])
+def test_rmsnorm_add_rmsnorm_cancellation(dev, oracle, dtype, n, rows):
+    """post-attn norm + add + pre-FFN norm where the residual stream nearly cancels the
+    normalised branch: x = -norm1(xb) + delta * noise, delta in {0, 1e-4, 1e-2, 1} by row
+    (s = x + norm1(xb) is ~delta, so the second statistic is a sum of cancelled terms), with
+    the same tolerances as test_rmsnorm_add_rmsnorm."""
+    f = O.get().bf16_to_f32
+    bf = dtype == B.BF16
+    xb = synth.normal_bf16(6, "xb", (rows, n)) if bf else synth.normal_f32(6, "xb", (rows, n))
+    w1 = synth.normal_f32(6, "w1", (n,), 0, 0.1)
+    w2 = synth.normal_f32(6, "w2", (n,), 0, 0.1)
+    a32 = oracle.rms_norm(f(xb) if bf else xb, w1, EPS, True)
+    delta = np.array([0.0, 1e-4, 1e-2, 1.0], np.float32)[np.arange(rows) % 4][:, None]
+    x32 = (-a32 + delta * synth.normal_f32(6, "noise", (rows, n))).astype(np.float32)
+    x = O.get().f32_to_bf16(x32) if bf else x32
+    x_ref, out_ref = oracle.rms_norm_add_rms_norm(x, xb, w1, w2, EPS, True)
+    d_x, d_o = dev.from_numpy(x), dev.alloc(x.nbytes)
+    dev.rmsNormAddRmsNorm(dtype, d_x, dev.from_numpy(xb), dev.from_numpy(w1), dev.from_numpy(w2), d_o, rows, n,
+                          EPS, True)
+    gx, go = d_x.to_numpy(x.shape, x.dtype), d_o.to_numpy(x.shape, x.dtype)
+    xf = (f(x) if bf else x).astype(np.float64)
+    a = a32.astype(np.float64)
+    s = xf + a
+    inv2 = 1.0 / np.sqrt(np.mean(s * s, axis=-1, keepdims=True) + float(EPS))
+    floor_x = 1e-5 * (np.abs(xf) + np.abs(a))
+    floor_o = 1e-5 * (np.abs(xf) + np.abs(a)) * inv2 * np.abs(1.0 + w2.astype(np.float64))
+    if bf:
+        assert_bf16(gx, x_ref, 1, floor=floor_x, what="bf16 x + norm1(xb), cancelling")
+        assert_bf16(go, out_ref, 1, floor=floor_o, what="bf16 norm2(x), cancelling")
+    else:
+        assert_rel(gx, x_ref, 1e-5, floor=floor_x, what="x + norm1(xb), cancelling")
+        assert_rel(go, out_ref, 1e-5, floor=floor_o, what="norm2(x), cancelling")
+
+
 @pytest.mark.parametrize("dtype,n,rows", [(B.BF16, 2560, 4097), (B.BF16, 5376, 2049), (B.F32, 2560, 2049),
                                           (B.BF16, 1024, 777), (B.F32, 5376, 512)])
 def test_norm_modes_many_rows(dev, oracle, dtype, n, rows):

@@ -26,8 +26,15 @@ namespace zl {
 #ifndef ZL_EW_UNROLL
 #define ZL_EW_UNROLL 1
 #endif
+#ifndef ZL_EW_LP
+#define ZL_EW_LP POL_NT
+#endif
+#ifndef ZL_EW_SP
+#define ZL_EW_SP POL_NT
+#endif
 constexpr int kEwThreads = ZL_EW_THREADS;
 constexpr int kEwUnroll = ZL_EW_UNROLL;
+constexpr int kEwLP = ZL_EW_LP, kEwSP = ZL_EW_SP;  // load / store cache policy (zl_common.h POL_*)
 
 enum EwOp { EW_GEGLU = 0, EW_SOFTCAP = 1, EW_ADD = 2, EW_SCALE = 3, EW_SWIGLU = 4, EW_PLE_FUSE = 5 };
 
@@ -62,26 +69,29 @@ __global__ __launch_bounds__(kEwThreads) void k_ew(EwArgs args) {
     const T* A = (const T*)args.a;
     const T* B = (const T*)args.b;
     T* O = (T*)args.out;
+    // The workgroup's chunks through range-checked buffer resources (chunks past the end read
+    // zeros and are not stored), with the streaming cache policies.
+    const int64_t c0 = (int64_t)blockIdx.x * kEwUnroll * kEwThreads;
+    const int64_t left = nch - c0;
+    const uint32_t bytes = (uint32_t)(left < kEwUnroll * kEwThreads ? left : kEwUnroll * kEwThreads) * 16u;
+    const auto rsa = buf_rsrc(A + c0 * E, bytes);
+    const auto rsb = buf_rsrc(kTwo ? B + c0 * E : A, kTwo ? bytes : 0u);
+    const auto rso = buf_rsrc(O + c0 * E, bytes);
     u32x4 ra[kEwUnroll], rb[kEwUnroll];
-    int64_t idx[kEwUnroll];
 #pragma unroll
     for (int u = 0; u < kEwUnroll; ++u) {
-        idx[u] = ((int64_t)blockIdx.x * kEwUnroll + u) * kEwThreads + threadIdx.x;
-        if (idx[u] < nch) {
-            ra[u] = lds16(A + idx[u] * E);
-            if constexpr (kTwo) rb[u] = lds16(B + idx[u] * E);
-        }
+        const uint32_t off = (uint32_t)(u * kEwThreads + threadIdx.x) * 16u;
+        ra[u] = bldp<kEwLP>(rsa, off);
+        if constexpr (kTwo) rb[u] = bldp<kEwLP>(rsb, off);
     }
 #pragma unroll
     for (int u = 0; u < kEwUnroll; ++u) {
-        if (idx[u] < nch) {
-            float x[E], y[E];
-            C::unpack(ra[u], x);
-            if constexpr (kTwo) C::unpack(rb[u], y);
+        float x[E], y[E];
+        C::unpack(ra[u], x);
+        if constexpr (kTwo) C::unpack(rb[u], y);
 #pragma unroll
-            for (int j = 0; j < E; ++j) x[j] = ew1<OP>(x[j], kTwo ? y[j] : 0.0f, args);
-            sts16(O + idx[u] * E, C::pack(x));
-        }
+        for (int j = 0; j < E; ++j) x[j] = ew1<OP>(x[j], kTwo ? y[j] : 0.0f, args);
+        bstp<kEwSP>(rso, (uint32_t)(u * kEwThreads + threadIdx.x) * 16u, C::pack(x));
     }
     // scalar tail
     const int64_t tail0 = nch * E;

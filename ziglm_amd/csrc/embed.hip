@@ -5,13 +5,14 @@
 // output is one IEEE rounding and the result is bit-exact; Q6_K keeps the CPU's
 // ((d * scale_j) * q) * scale order and Q4_K its (q * (d * sc_j) - dmin * m_j) * scale.
 //
-// Layout: one wave per segment of 512 consecutive outputs of one row (2048 for K-quants), four
-// independent waves per workgroup (no block barrier): a 4096-token gather is ~20k waves.
-// Every lane produces 16 bytes of output per step (4 f32 or 8 bf16), so each store
-// instruction of a wave writes 1 KB of whole, contiguous cache lines.
+// Layout: one wave per segment of consecutive outputs of one row (K * 64 16-byte chunks for
+// Q8_0 / Q4_0 / dense types, 2048 outputs for K-quants), four independent waves per
+// workgroup (no block barrier). Every lane produces 16 bytes of output per step (4 f32 or 8
+// bf16), so each store instruction of a wave writes 1 KB of whole, contiguous cache lines.
 // Q8_0 / Q4_0 (34 / 18 B blocks, 2-byte aligned): each lane loads the f16 scale and the
-// quant bytes behind its outputs straight from global memory with 16-bit loads; the lanes of a wave read a contiguous span of the row, so the
-// loads coalesce into that span's cache lines (measured on MI355X at 4096 x 2560: 9.4 us
+// quant bytes behind its outputs straight from global memory (a 16-bit load and 32-bit loads
+// from 2-byte aligned addresses); the lanes of a wave read a contiguous span of the row, so
+// the loads coalesce into that span's cache lines (measured on MI355X at 4096 x 2560: 9.4 us
 // against 12.9 us for staging the row through LDS first).
 // Q6_K / Q4_K (210 / 144 B super-blocks): the segment (8 super-blocks) is staged in LDS, then
 // decoded.
@@ -44,6 +45,15 @@ __host__ __device__ constexpr int out_epl() {
 template <typename OutT>
 __device__ __forceinline__ void store16(OutT* p, const float* v) {
     sts16(p, Chunk<OutT>::pack(v));
+}
+// Output stores of the Q8_0 / Q4_0 / dense gathers: cache policy ZL_GATHER_SP (zl_common.h
+// POL_*), through a resource `r` over the output row at byte offset `off` (p = row + off).
+#ifndef ZL_GATHER_SP
+#define ZL_GATHER_SP POL_NT
+#endif
+template <typename OutT>
+__device__ __forceinline__ void store16p(OutT* p, __amdgpu_buffer_rsrc_t r, uint32_t off, const float* v) {
+    strow16<ZL_GATHER_SP>(p - off / sizeof(OutT), r, off, Chunk<OutT>::pack(v));
 }
 
 // Dequantise elements [e, e+N) (N = 4 or 8, e a multiple of N) of a block row staged at
@@ -140,69 +150,84 @@ __host__ __device__ constexpr int seg_elems() {
 }
 
 
-// Q8_0 / Q4_0: one wave per 512 outputs, direct 16-bit global loads (the table only needs
-// 2-byte alignment: blocks are 34 / 18 B).
-template <int QT, typename OutT>
+// Steps per wave of the Q8_0 / Q4_0 (K_Q) and dense (K_D) gathers: a wave takes K * 64
+// consecutive 16-byte output chunks of one row (K * 256 f32 or K * 512 bf16 outputs) and
+// reads its row's id once. Measured at 4096 x 2560 -> f32 (us, K = 2 / 3 / 5 / 10): Q8_0
+// 10.2 / 10.5 / 11.0 / 12.2, Q4_0 8.66 / 8.83 / 9.2 / 8.95, BF16 12.3 / 12.3 / 12.1 / 12.2.
+#ifndef ZL_GATHER_STEPS
+#define ZL_GATHER_STEPS 2
+#endif
+#ifndef ZL_GATHER_STEPS_DENSE
+#define ZL_GATHER_STEPS_DENSE 5
+#endif
+constexpr int kGatherSteps = ZL_GATHER_STEPS;
+constexpr int kGatherStepsDense = ZL_GATHER_STEPS_DENSE;
+
+typedef uint32_t u32_a2 __attribute__((aligned(2)));
+// 32-bit load from a 2-byte aligned address (one global_load_dword; gfx950 serves it
+// unaligned).
+__device__ __forceinline__ uint32_t ld32_a2(const unsigned char* p) {
+    return *reinterpret_cast<const u32_a2*>(p);
+}
+
+// Q8_0 / Q4_0: per 16-byte output chunk (N = 4 f32 or 8 bf16 outputs of one block) a lane
+// loads the block's f16 scale (16-bit) and the quant bytes behind its outputs as 32-bit
+// words from 2-byte aligned addresses (Q8_0: N bytes; Q4_0: 4 bytes for N = 4, 8 for N = 8,
+// low nibbles for elements 0..15 of the block, high for 16..31). Every address is clamped
+// into the table (id 0, element 0 for lanes past the row or an invalid id) and the values
+// are dropped afterwards, so no load sits under a branch and all 2K of a lane's loads are in
+// flight before its first store.
+template <int QT, typename OutT, int K>
 __global__ __launch_bounds__(256) void k_gather_q(const unsigned char* __restrict__ table,
                                                   const int32_t* __restrict__ ids,
                                                   OutT* __restrict__ out, int64_t n_rows,
                                                   int64_t n_tokens, int dim, float scale, int nseg,
                                                   int64_t single_id) {
     constexpr int N = out_epl<OutT>();  // outputs per lane per step
-    constexpr int K = 512 / (kWave * N);  // steps per wave
+    constexpr int S = K * kWave * N;    // outputs per wave
     constexpr int BB = (int)block_bytes<QT>();
-    const int wave = threadIdx.x >> 6;
+    constexpr int NW = N / 4;  // quant words per chunk: one byte per output (Q4_0: a nibble of it)
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int64_t wg = (int64_t)blockIdx.x * kGatherWaves + wave;
     const int64_t t = wg / nseg;
     if (t >= n_tokens) return;
-    const int e0 = (int)(wg - t * nseg) * 512;
-    const int64_t id = ids ? (int64_t)ids[t] : single_id;
+    const int e0 = (int)(wg - t * nseg) * S;
+    const int64_t id = ids ? (int64_t)ids[t] : single_id;  // wave-uniform: a scalar load
     const bool valid = id >= 0 && id < n_rows;
-    // (Plain loads under the bounds condition: the range-checked form of these 16-bit loads
-    // measured slower here, Q4_0 at 4096 x 2560 9.4 against 9.9 us.)
     const unsigned char* grow = table + (valid ? id : 0) * (int64_t)(dim / 32) * BB;
-    uint32_t dq[K], w[K][N / 2];
+    uint32_t dq[K], w[K][NW];
 #pragma unroll
     for (int k = 0; k < K; ++k) {
-        const int e = e0 + lane * N + kWave * N * k;
-        if (valid && e < dim) {
-            const unsigned char* blk = grow + (e >> 5) * BB;
-            dq[k] = lds_u16(blk);
-            // Q8_0: bytes 2 + (e & 31) ..; Q4_0: nibble bytes 2 + (e & 15) .. (low nibbles
-            // hold elements 0..15 of the block, high nibbles 16..31)
-            const unsigned char* qs = blk + 2 + (QT == HIP_BRIDGE_Q8_0 ? (e & 31) : (e & 15));
+        const int e = e0 + kWave * N * k + lane * N;
+        const int ec = e < dim ? e : 0;
+        const unsigned char* blk = grow + (ec >> 5) * BB;
+        dq[k] = lds_u16(blk);
+        const unsigned char* qs = blk + 2 + (QT == HIP_BRIDGE_Q8_0 ? (ec & 31) : (ec & 15));
 #pragma unroll
-            for (int j = 0; j < N / 2; ++j) w[k][j] = lds_u16(qs + 2 * j);
-        }
+        for (int j = 0; j < NW; ++j) w[k][j] = ld32_a2(qs + 4 * j);
     }
     OutT* orow = out + t * (int64_t)dim;
+    const auto ro = buf_rsrc(orow, (uint32_t)dim * sizeof(OutT));
 #pragma unroll
     for (int k = 0; k < K; ++k) {
-        const int e = e0 + lane * N + kWave * N * k;
+        const int e = e0 + kWave * N * k + lane * N;
         if (e >= dim) break;
         float v[N];
-        if (valid) {
-            const float d = f16_bits_to_f32(dq[k]);
-            const int shift = (e & 31) < 16 ? 0 : 4;
+        const float d = f16_bits_to_f32(dq[k]);
+        const int shift = (e & 31) < 16 ? 0 : 4;  // Q4_0: low or high nibbles of the block
 #pragma unroll
-            for (int j = 0; j < N / 2; ++j) {
-                int q0, q1;
-                if constexpr (QT == HIP_BRIDGE_Q8_0) {
-                    q0 = (int8_t)(w[k][j] & 0xff);
-                    q1 = (int8_t)(w[k][j] >> 8);
-                } else {
-                    q0 = (int)((w[k][j] >> shift) & 0xf) - 8;
-                    q1 = (int)((w[k][j] >> (8 + shift)) & 0xf) - 8;
-                }
-                v[2 * j] = ((float)q0 * d) * scale;
-                v[2 * j + 1] = ((float)q1 * d) * scale;
-            }
-        } else {
+        for (int j = 0; j < N; ++j) {
+            // element j of the chunk: byte j of the lane's quant span
+            const uint32_t byte = w[k][j >> 2] >> (8 * (j & 3));
+            const int q = QT == HIP_BRIDGE_Q8_0 ? (int)(int8_t)(byte & 0xff) : (int)((byte >> shift) & 0xf) - 8;
+            v[j] = ((float)q * d) * scale;
+        }
+        if (!valid) {
 #pragma unroll
             for (int j = 0; j < N; ++j) v[j] = 0.0f;
         }
-        store16<OutT>(orow + e, v);
+        store16p<OutT>(orow + e, ro, (uint32_t)e * sizeof(OutT), v);
     }
 }
 
@@ -321,22 +346,21 @@ struct DenseIn {
     }
 };
 
-template <int QT, typename OutT>
+template <int QT, typename OutT, int K>
 __global__ __launch_bounds__(256) void k_gather_dense(const unsigned char* __restrict__ table,
                                                       const int32_t* __restrict__ ids,
                                                       OutT* __restrict__ out, int64_t n_rows,
                                                       int64_t n_tokens, int dim, float scale,
                                                       int nseg, int64_t single_id) {
     constexpr int N = out_epl<OutT>();
-    constexpr int K = 512 / (kWave * N);
     using In = DenseIn<QT, N>;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int64_t wg = (int64_t)blockIdx.x * kGatherWaves + wave;
     const int64_t t = wg / nseg;
     if (t >= n_tokens) return;
-    const int e0 = (int)(wg - t * nseg) * 512;
-    const int64_t id = ids ? (int64_t)ids[t] : single_id;
+    const int e0 = (int)(wg - t * nseg) * (K * kWave * N);
+    const int64_t id = ids ? (int64_t)ids[t] : single_id;  // wave-uniform: a scalar load
     const bool valid = id >= 0 && id < n_rows;
     const int64_t rbytes = (int64_t)dim * In::ES;
     const auto rs = buf_rsrc(table + (valid ? id : 0) * rbytes, valid ? (uint32_t)rbytes : 0u);
@@ -344,6 +368,7 @@ __global__ __launch_bounds__(256) void k_gather_dense(const unsigned char* __res
 #pragma unroll
     for (int k = 0; k < K; ++k) in[k].load(rs, (uint32_t)(e0 + lane * N + kWave * N * k) * In::ES);
     OutT* orow = out + t * (int64_t)dim;
+    const auto ro = buf_rsrc(orow, (uint32_t)dim * sizeof(OutT));
 #pragma unroll
     for (int k = 0; k < K; ++k) {
         const int e = e0 + lane * N + kWave * N * k;
@@ -355,7 +380,7 @@ __global__ __launch_bounds__(256) void k_gather_dense(const unsigned char* __res
 #pragma unroll
             for (int j = 0; j < N; ++j) v[j] = 0.0f;
         }
-        store16<OutT>(orow + e, v);
+        store16p<OutT>(orow + e, ro, (uint32_t)e * sizeof(OutT), v);
     }
 }
 
@@ -423,14 +448,15 @@ static void launch_blocks(const void* table, const int32_t* ids, int64_t single_
 template <int QT, typename OutT>
 static void launch_q(const void* table, const int32_t* ids, int64_t single_id, void* out,
                      int64_t n_rows, int64_t n_tokens, int dim, float scale, hipStream_t s) {
-    const int nseg = (int)cdiv(dim, 512);
+    constexpr int S = kGatherSteps * kWave * out_epl<OutT>();
+    const int nseg = (int)cdiv(dim, S);
     const int64_t grid = cdiv(n_tokens * nseg, kGatherWaves);
     if (grid > INT32_MAX) {
         set_error(HIP_BRIDGE_EUNSUPPORTED);
         return;
     }
-    k_gather_q<QT, OutT><<<(unsigned)grid, 256, 0, s>>>((const unsigned char*)table, ids, (OutT*)out,
-                                                        n_rows, n_tokens, dim, scale, nseg, single_id);
+    k_gather_q<QT, OutT, kGatherSteps><<<(unsigned)grid, 256, 0, s>>>(
+        (const unsigned char*)table, ids, (OutT*)out, n_rows, n_tokens, dim, scale, nseg, single_id);
     check_launch();
 }
 
@@ -439,13 +465,13 @@ static void launch_dense(const void* table, const int32_t* ids, int64_t single_i
                          int64_t n_rows, int64_t n_tokens, int dim, float scale, hipStream_t s) {
     const bool vec = dim % 8 == 0 && aligned16(table) && aligned16(out);
     if (vec) {
-        const int nseg = (int)cdiv(dim, 512);
+        const int nseg = (int)cdiv(dim, kGatherStepsDense * kWave * out_epl<OutT>());
         const int64_t grid = cdiv(n_tokens * nseg, kGatherWaves);
         if (grid > INT32_MAX) {
             set_error(HIP_BRIDGE_EUNSUPPORTED);
             return;
         }
-        k_gather_dense<QT, OutT><<<(unsigned)grid, 256, 0, s>>>(
+        k_gather_dense<QT, OutT, kGatherStepsDense><<<(unsigned)grid, 256, 0, s>>>(
             (const unsigned char*)table, ids, (OutT*)out, n_rows, n_tokens, dim, scale, nseg,
             single_id);
     } else {

@@ -82,10 +82,19 @@ __host__ __device__ constexpr int norm_gpb() {
     return ZL_NORM_GROUPS_PER_BLOCK ? ZL_NORM_GROUPS_PER_BLOCK : 4 / W;
 }
 
+// Cache policy of the row loads and stores (zl_common.h POL_*; tuning builds set others).
+#ifndef ZL_NORM_LP
+#define ZL_NORM_LP POL_NT
+#endif
+#ifndef ZL_NORM_SP
+#define ZL_NORM_SP POL_NT
+#endif
+
 template <typename T, int NC, int MODE, int W, int R, bool WL>
 __global__ __launch_bounds__(256) void k_norm_rows(NormArgs a) {
     using C = Chunk<T>;
     constexpr int E = C::E;
+    constexpr int LP = ZL_NORM_LP, SP = ZL_NORM_SP;
     constexpr int GPB = norm_gpb<W>();  // row groups per block
     constexpr int STRIDE = kWave * W;
     // one slot set per (row, reduction): no slot is rewritten while a wave may still read it
@@ -112,8 +121,8 @@ __global__ __launch_bounds__(256) void k_norm_rows(NormArgs a) {
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
             const uint32_t off = (uint32_t)(g + c * STRIDE) * 16u;
-            rx[r][c] = bld16(rsx, off);
-            if constexpr (MODE != M_NORM) rr[r][c] = bld16(rsr, off);
+            rx[r][c] = bldp<LP>(rsx, off);
+            if constexpr (MODE != M_NORM) rr[r][c] = bldp<LP>(rsr, off);
         }
     }
     // Weights: with the activations (WL false: latency-bound launches, one round trip in
@@ -140,8 +149,11 @@ __global__ __launch_bounds__(256) void k_norm_rows(NormArgs a) {
     for (int r = 0; r < R; ++r) {
         const int64_t row = row0 + r;
         const bool row_ok = row < a.rows;
-        T* xrow = (T*)a.x + row * n;
-        T* orow = (T*)a.out + row * n;
+        const uint32_t row_bytes = row_ok ? (uint32_t)n * sizeof(T) : 0u;
+        T* const xrow = (T*)a.x + row * n;
+        T* const orow = (T*)a.out + row * n;
+        const auto wsx = buf_rsrc(xrow, MODE != M_NORM ? row_bytes : 0u);
+        const auto wso = buf_rsrc(orow, MODE != M_NORM_ADD ? row_bytes : 0u);
         float* slot1 = s_red[2 * r] + rib * W;
         float* slot2 = s_red[2 * r + 1] + rib * W;
 
@@ -181,8 +193,8 @@ __global__ __launch_bounds__(256) void k_norm_rows(NormArgs a) {
                     float y[E];
 #pragma unroll
                     for (int j = 0; j < E; ++j) y[j] = (v[c][j] * inv) * w_factor(f1[c][j], has_w1, a.uo);
-                    if constexpr (MODE == M_ADD_NORM) sts16(xrow + (int64_t)idx * E, C::pack(v[c]));
-                    sts16(orow + (int64_t)idx * E, C::pack(y));
+                    if constexpr (MODE == M_ADD_NORM) strow16<SP>(xrow, wsx, (uint32_t)idx * 16u, C::pack(v[c]));
+                    strow16<SP>(orow, wso, (uint32_t)idx * 16u, C::pack(y));
                 }
             }
         } else if constexpr (MODE == M_NORM_ADD) {
@@ -194,7 +206,7 @@ __global__ __launch_bounds__(256) void k_norm_rows(NormArgs a) {
                     C::unpack(rx[r][c], xv);
 #pragma unroll
                     for (int j = 0; j < E; ++j) xv[j] = xv[j] + (v[c][j] * inv) * w_factor(f1[c][j], has_w1, a.uo);
-                    sts16(xrow + (int64_t)idx * E, C::pack(xv));
+                    strow16<SP>(xrow, wsx, (uint32_t)idx * 16u, C::pack(xv));
                 }
             }
         } else {  // M_NORM_ADD_NORM
@@ -221,8 +233,8 @@ __global__ __launch_bounds__(256) void k_norm_rows(NormArgs a) {
                     float y[E];
 #pragma unroll
                     for (int j = 0; j < E; ++j) y[j] = (v[c][j] * inv2) * w_factor(f2[c][j], has_w2, a.uo);
-                    sts16(xrow + (int64_t)idx * E, C::pack(v[c]));
-                    sts16(orow + (int64_t)idx * E, C::pack(y));
+                    strow16<SP>(xrow, wsx, (uint32_t)idx * 16u, C::pack(v[c]));
+                    strow16<SP>(orow, wso, (uint32_t)idx * 16u, C::pack(y));
                 }
             }
         }
@@ -355,6 +367,9 @@ static void launch_wl(const NormArgs& a, int per_lane, int R, bool late, hipStre
 #ifndef ZL_NORM_FIT_ADD
 #define ZL_NORM_FIT_ADD 6
 #endif
+#ifndef ZL_NORM_FIT_NAN
+#define ZL_NORM_FIT_NAN 3
+#endif
 #ifndef ZL_NORM_LATE
 #define ZL_NORM_LATE -1
 #endif
@@ -364,7 +379,7 @@ static void launch_t(const NormArgs& a, hipStream_t s) {
     const int nch = a.n / E;
     int W = ZL_NORM_WAVES_PER_ROW;
     if (W == 0) {
-        const int fit = MODE == M_NORM_ADD_NORM ? 3 : MODE == M_NORM_ADD ? ZL_NORM_FIT_ADD : 4;
+        const int fit = MODE == M_NORM_ADD_NORM ? ZL_NORM_FIT_NAN : MODE == M_NORM_ADD ? ZL_NORM_FIT_ADD : 4;
         W = nch <= fit * kWave ? 1 : nch <= 2 * fit * kWave ? 2 : 4;
     }
     const int per_lane = (int)cdiv(nch, kWave * W);

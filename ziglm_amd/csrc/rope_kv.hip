@@ -117,6 +117,16 @@ __device__ __forceinline__ void fill_cos_sin(const RopeTab& tab, float pos_f, in
     }
 }
 
+// Cache policy of the head-row loads and stores (nt or the default; the rows are addressed
+// per lane, so the buffer-only policies do not apply).
+#ifndef ZL_QK_LD_NT
+#define ZL_QK_LD_NT 1
+#endif
+#ifndef ZL_QK_ST_NT
+#define ZL_QK_ST_NT 1
+#endif
+constexpr bool kQkLdNt = ZL_QK_LD_NT, kQkStNt = ZL_QK_ST_NT;
+
 // Head rows one pass of a k_qk_fused workgroup takes (4 waves of 64 / LH heads).
 template <typename T, int D>
 __host__ __device__ constexpr int qk_slots() {
@@ -199,8 +209,8 @@ __global__ __launch_bounds__(256) void k_qk_fused(QkArgs a) {
             const int hr = gslot + q * hstep;
             const bool row_ok = hr < HR && readable(hr, tb + tt);
             const T* src0 = row_ok ? src_of(hr, tb + tt) : (const T*)g_qk_pad_row;
-            ra[tt][q] = lds16(src0 + c0 * E);
-            rb[tt][q] = lds16(src0 + c1 * E);
+            ra[tt][q] = ldg16<kQkLdNt>(src0 + c0 * E);
+            rb[tt][q] = ldg16<kQkLdNt>(src0 + c1 * E);
         }
 
     int p[TPW];
@@ -285,8 +295,8 @@ __global__ __launch_bounds__(256) void k_qk_fused(QkArgs a) {
         if (kind == 0) dst = (T*)a.q + ((int64_t)t * a.nh + hr) * D;
         else if (kind == 1) dst = (T*)a.kdst + row[tt] * a.row_stride + (int64_t)(hr - a.nh) * D;
         else dst = (T*)a.vdst + row[tt] * a.row_stride + (int64_t)(hr - a.nh - a.nkv) * D;
-        sts16(dst + c0 * E, C::pack(x0));
-        sts16(dst + c1 * E, C::pack(x1));
+        stg16<kQkStNt>(dst + c0 * E, C::pack(x0));
+        stg16<kQkStNt>(dst + c1 * E, C::pack(x1));
     };
 #pragma unroll
     for (int tt = 0; tt < TPW; ++tt) {
@@ -299,7 +309,7 @@ __global__ __launch_bounds__(256) void k_qk_fused(QkArgs a) {
         for (int hr = gslot + NP * hstep; hr < HR; hr += hstep) {
             if (!active(hr, tt)) continue;
             const T* src = src_of(hr, tb + tt);
-            process(hr, tt, lds16(src + c0 * E), lds16(src + c1 * E));
+            process(hr, tt, ldg16<kQkLdNt>(src + c0 * E), ldg16<kQkLdNt>(src + c1 * E));
         }
     }
 }

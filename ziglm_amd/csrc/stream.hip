@@ -1,71 +1,87 @@
 // Reference streaming kernel: the practical HBM ceiling of an op's byte mix. It reads n_in
 // streams and writes n_out streams of `bytes` each (out_j[i] = in0[i] ^ in1[i], or in0[i]),
 // so an op that reads R tensors and writes W tensors of one size can be set beside a kernel
-// that moves exactly the same bytes and does nothing else. Several launch shapes are built;
-// the benchmark times each and takes the fastest as the ceiling of that size and mix.
+// that moves exactly the same bytes and does nothing else. out0 may be in0 (a read-modify-
+// write of one tensor in place, as the residual-stream updates x += ... do). Launch shapes
+// combine threads per workgroup, 128-bit chunks per thread and the load / store cache
+// policies the ops choose among (zl_common.h POL_*); the benchmark times each and takes the
+// fastest as the ceiling of that size and mix.
 //
-// Every shape issues all of a thread's 128-bit loads before its first store, with the same
-// nontemporal policy the ops use for single-use activations (zl_common.h lds16 / sts16).
+// Every shape issues all of a thread's loads before its first store; accesses go through
+// range-checked buffer resources over the workgroup's span.
 #include "zl_common.h"
 #include "zl_host.h"
 
 namespace zl {
 
 struct StreamArgs {
-    const u32x4* in0;
-    const u32x4* in1;
-    u32x4* out0;
-    u32x4* out1;
+    const uint8_t* in0;
+    const uint8_t* in1;
+    uint8_t* out0;
+    uint8_t* out1;
     int64_t nch;  // 16-byte chunks per stream
 };
 
 // U chunks per thread, consecutive by workgroup: chunk (block * U + u) * THREADS + thread.
-template <int NIN, int NOUT, int THREADS, int U>
+template <int NIN, int NOUT, int THREADS, int U, int LP, int SP>
 __global__ __launch_bounds__(THREADS) void k_stream(StreamArgs a) {
-    u32x4 r0[U], r1[U];
-    int64_t idx[U];
+    const int64_t c0 = (int64_t)blockIdx.x * U * THREADS;
+    const int64_t left = a.nch - c0;
+    const uint32_t bytes = (uint32_t)(left < U * THREADS ? left : U * THREADS) * 16u;
+    const auto r0 = buf_rsrc(a.in0 + c0 * 16, bytes);
+    const auto r1 = buf_rsrc(NIN == 2 ? a.in1 + c0 * 16 : a.in0, NIN == 2 ? bytes : 0u);
+    const auto w0 = buf_rsrc(a.out0 + c0 * 16, bytes);
+    const auto w1 = buf_rsrc(NOUT == 2 ? a.out1 + c0 * 16 : a.out0, NOUT == 2 ? bytes : 0u);
+    u32x4 x[U], y[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        idx[u] = ((int64_t)blockIdx.x * U + u) * THREADS + threadIdx.x;
-        if (idx[u] < a.nch) {
-            r0[u] = lds16(a.in0 + idx[u]);
-            if constexpr (NIN == 2) r1[u] = lds16(a.in1 + idx[u]);
-        }
+        const uint32_t off = (uint32_t)(u * THREADS + threadIdx.x) * 16u;
+        x[u] = bldp<LP>(r0, off);
+        if constexpr (NIN == 2) y[u] = bldp<LP>(r1, off);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        if (idx[u] < a.nch) {
-            const u32x4 v = NIN == 2 ? (r0[u] ^ r1[u]) : r0[u];
-            sts16(a.out0 + idx[u], v);
-            if constexpr (NOUT == 2) sts16(a.out1 + idx[u], v);
-        }
+        const uint32_t off = (uint32_t)(u * THREADS + threadIdx.x) * 16u;
+        const u32x4 v = NIN == 2 ? (x[u] ^ y[u]) : x[u];
+        bstp<SP>(w0, off, v);
+        if constexpr (NOUT == 2) bstp<SP>(w1, off, v);
     }
 }
 
+// The launch shapes the ceiling is the best of: {threads, chunks per thread} x load policy
+// {default, nt} x store policy {nt, sc1}.
 struct Shape {
     int threads, unroll;
 };
-// The launch shapes the ceiling is the best of.
-constexpr Shape kShapes[] = {{64, 1}, {128, 1}, {256, 1}, {256, 2}, {256, 4}, {512, 1}, {1024, 1}, {64, 4}};
-constexpr int kNumShapes = sizeof(kShapes) / sizeof(kShapes[0]);
+constexpr Shape kGeo[] = {{64, 1}, {256, 1}, {256, 2}, {256, 4}, {512, 2}};
+constexpr int kNumGeo = sizeof(kGeo) / sizeof(kGeo[0]);
+constexpr int kNumShapes = kNumGeo * 4;
 
-template <int NIN, int NOUT, int THREADS, int U>
+template <int NIN, int NOUT, int THREADS, int U, int LP, int SP>
 static void launch_one(const StreamArgs& a, hipStream_t s) {
     const int64_t grid = cdiv(a.nch, (int64_t)THREADS * U);
-    k_stream<NIN, NOUT, THREADS, U><<<(unsigned)grid, THREADS, 0, s>>>(a);
+    k_stream<NIN, NOUT, THREADS, U, LP, SP><<<(unsigned)grid, THREADS, 0, s>>>(a);
+}
+
+template <int NIN, int NOUT, int LP, int SP>
+static void launch_geo(int geo, const StreamArgs& a, hipStream_t s) {
+    switch (geo) {
+        case 0: launch_one<NIN, NOUT, 64, 1, LP, SP>(a, s); break;
+        case 1: launch_one<NIN, NOUT, 256, 1, LP, SP>(a, s); break;
+        case 2: launch_one<NIN, NOUT, 256, 2, LP, SP>(a, s); break;
+        case 3: launch_one<NIN, NOUT, 256, 4, LP, SP>(a, s); break;
+        default: launch_one<NIN, NOUT, 512, 2, LP, SP>(a, s); break;
+    }
 }
 
 template <int NIN, int NOUT>
 static void launch_shape(int shape, const StreamArgs& a, hipStream_t s) {
-    switch (shape) {
-        case 0: launch_one<NIN, NOUT, 64, 1>(a, s); break;
-        case 1: launch_one<NIN, NOUT, 128, 1>(a, s); break;
-        case 2: launch_one<NIN, NOUT, 256, 1>(a, s); break;
-        case 3: launch_one<NIN, NOUT, 256, 2>(a, s); break;
-        case 4: launch_one<NIN, NOUT, 256, 4>(a, s); break;
-        case 5: launch_one<NIN, NOUT, 512, 1>(a, s); break;
-        case 6: launch_one<NIN, NOUT, 1024, 1>(a, s); break;
-        default: launch_one<NIN, NOUT, 64, 4>(a, s); break;
+    const int geo = shape % kNumGeo, pol = shape / kNumGeo;
+    switch (pol) {
+        case 0: launch_geo<NIN, NOUT, POL_NT, POL_NT>(geo, a, s); break;
+        case 1: launch_geo<NIN, NOUT, POL_DEFAULT, POL_NT>(geo, a, s); break;
+        case 2: launch_geo<NIN, NOUT, POL_NT, POL_SC1>(geo, a, s); break;
+        default: launch_geo<NIN, NOUT, POL_DEFAULT, POL_SC1>(geo, a, s); break;
     }
 }
 
@@ -84,7 +100,8 @@ int hip_stream_ref(int n_in, int n_out, const void* in0, const void* in1, void* 
         !in0 || !out0 || (n_in == 2 && !in1) || (n_out == 2 && !out1) || !aligned16(in0) || !aligned16(out0) ||
         (n_in == 2 && !aligned16(in1)) || (n_out == 2 && !aligned16(out1)))
         return HIP_BRIDGE_EINVAL;
-    const StreamArgs a{(const u32x4*)in0, (const u32x4*)in1, (u32x4*)out0, (u32x4*)out1, bytes / 16};
+    if (bytes / 16 > 0xffffffffLL) return HIP_BRIDGE_EUNSUPPORTED;
+    const StreamArgs a{(const uint8_t*)in0, (const uint8_t*)in1, (uint8_t*)out0, (uint8_t*)out1, bytes / 16};
     const hipStream_t s = stream_of(stream);
     if (n_in == 1 && n_out == 1) launch_shape<1, 1>(shape, a, s);
     else if (n_in == 2 && n_out == 1) launch_shape<2, 1>(shape, a, s);

@@ -126,6 +126,45 @@ __device__ __forceinline__ f32x4 bldf4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
 
+// Cache policy of a buffer access (the instruction's cache-policy bits on gfx950): bit 0 sc0,
+// bit 1 nt (streaming: not retained), bit 4 sc1 (for stores, sc1 alone is device scope). The
+// streaming kernels take their load / store policy as compile-time constants; measured on
+// MI355X with every op's inputs rotated past the Infinity Cache, nt loads and nt stores are
+// the fastest for each of them (2048 x 2560 bf16: norm + add with default-policy loads 6.55
+// -> 8.8 us; 4096 x 2560 gathers with sc1 or default-policy stores 8.7 -> 15.0-15.4 us for
+// Q4_0). The reference streaming kernel (stream.hip), whose best shape defines an op's
+// ceiling, also tries default-policy loads and sc1 stores, which a plain stream of some
+// byte mixes prefers.
+enum : int { POL_DEFAULT = 0, POL_SC0 = 1, POL_NT = 2, POL_SC1 = 16 };
+template <int POL>
+__device__ __forceinline__ u32x4 bldp(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, POL));
+}
+template <int POL>
+__device__ __forceinline__ void bstp(__amdgpu_buffer_rsrc_t r, uint32_t off, const u32x4& v) {
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, POL);
+}
+// A 128-bit store at byte offset `off` of a row (base `p`, range-checked resource `r` over
+// the same row) with policy POL: POL_NT as a global nontemporal store (measured faster than
+// the buffer form for the norm kernels: 2048 x 2560 bf16 norm + add + norm 8.60 -> 8.26 us),
+// other policies as buffer stores.
+template <int POL>
+__device__ __forceinline__ void strow16(void* p, __amdgpu_buffer_rsrc_t r, uint32_t off, const u32x4& v) {
+    if constexpr (POL == POL_NT) sts16((uint8_t*)p + off, v);
+    else bstp<POL>(r, off, v);
+}
+// Global (per-lane address) 128-bit accesses with the nt policy or the default one.
+template <bool NT>
+__device__ __forceinline__ u32x4 ldg16(const void* p) {
+    if constexpr (NT) return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    else return *reinterpret_cast<const u32x4*>(p);
+}
+template <bool NT>
+__device__ __forceinline__ void stg16(void* p, const u32x4& v) {
+    if constexpr (NT) __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+    else *reinterpret_cast<u32x4*>(p) = v;
+}
+
 // ---- lane-group reductions -----------------------------------------------------------
 // Sum over aligned groups of G lanes (G a power of two <= 64); every lane of a group gets
 // the bit-identical group total (each step adds a pair in the same order on both sides).
