@@ -16,10 +16,15 @@
  *     without launching when a size is <= 0;
  *   - unsupported qtype / dtype / shape: no launch (the reference silently no-ops); the
  *     reason is recorded for hip_bridge_last_error();
- *   - in-place aliasing is allowed where the reference relies on it (noted per op).
+ *   - in-place aliasing is allowed where the reference relies on it (noted per op);
+ *   - a pointer parameter marked NULL may be NULL (its meaning is stated per op); every
+ *     other pointer must point to a buffer of the stated size.
  * Numerics follow ziglm's CPU path (src/math.zig, src/quant.zig), not its CUDA kernels:
  *   - gathers are bit-exact: out = (f32(q) * d) * scale, one rounding;
- *   - RMSNorm: inv = 1/sqrt(mean + eps) (IEEE sqrt and divide), out = (x*inv)*(1+w);
+ *   - RMSNorm: inv = 1/sqrt(mean + eps), out = (x*inv)*(1+w); the register-row kernels
+ *     (rows of up to 16 16-byte chunks per lane, 16-byte aligned) take 1/sqrt from the
+ *     hardware reciprocal square root, within 1 ulp of the reference's IEEE sqrt and
+ *     divide; other rows take the IEEE form;
  *   - RoPE angles: theta = f32(pos)*freq_scale / D_i (IEEE f32 division) with
  *     D_i = f32(pow(base, f32(2i)/f32(r))) evaluated in double precision; cos/sin within
  *     1.3 ulp of the correctly rounded values (an exact double-precision reduction by pi/2,
@@ -62,9 +67,9 @@ typedef void* HipEvent_t;     /* new: event handle for stream timing */
 /* ---------------------------------------------------------------------------------- */
 int hip_device_get_info(int device_id, char* name, size_t name_len, size_t* total_vram_bytes); /* cuda_bridge.h:15 */
 int hip_malloc(void** ptr, size_t bytes);                                            /* cuda_bridge.h:16 */
-int hip_free(void* ptr);                                                             /* cuda_bridge.h:17 */
+int hip_free(void* ptr /*NULL*/);                                                    /* cuda_bridge.h:17 */
 int hip_malloc_host(void** ptr, size_t bytes);                                       /* cuda_bridge.h:18 */
-int hip_free_host(void* ptr);                                                        /* cuda_bridge.h:19 */
+int hip_free_host(void* ptr /*NULL*/);                                               /* cuda_bridge.h:19 */
 int hip_memcpy_h2d(void* dst, const void* src, size_t bytes, HipStream_t stream);    /* cuda_bridge.h:20 */
 int hip_memcpy_d2h(void* dst, const void* src, size_t bytes, HipStream_t stream);    /* cuda_bridge.h:21 */
 int hip_memcpy_d2d(void* dst, const void* src, size_t bytes, HipStream_t stream);    /* cuda_bridge.h:22 */
@@ -119,49 +124,49 @@ void hip_embed_gather(const void* table, int qtype, int64_t n_rows, const int32_
 /* RMSNorm family, f32 (replaces cuda_bridge.h:55-58, cuda_bridge.cu:2058)             */
 /* weight may be NULL (scale 1, reference's no-scale norm); use_unit_offset: (1+w).     */
 /* ---------------------------------------------------------------------------------- */
-void hip_rmsnorm(const float* x, const float* weight, float* out, int n, float eps,
+void hip_rmsnorm(const float* x, const float* weight /*NULL*/, float* out, int n, float eps,
                  int use_unit_offset, HipStream_t stream);                   /* cuda_bridge.h:55 */
 /* count rows of head_dim; weight shared by all rows; x == out allowed. */
-void hip_rmsnorm_batched(float* x, const float* weight, float* out, int head_dim, int count,
+void hip_rmsnorm_batched(float* x, const float* weight /*NULL*/, float* out, int head_dim, int count,
                          float eps, int use_unit_offset, HipStream_t stream); /* cuda_bridge.h:56 */
 /* x += residual (written back), out = norm(x); out may alias residual. */
-void hip_add_rmsnorm(float* x, const float* residual, const float* weight, float* out, int n,
+void hip_add_rmsnorm(float* x, const float* residual, const float* weight /*NULL*/, float* out, int n,
                      float eps, int use_unit_offset, HipStream_t stream);     /* cuda_bridge.h:57 */
-void hip_add_rmsnorm_batched(float* x, const float* residual, const float* weight, float* out,
+void hip_add_rmsnorm_batched(float* x, const float* residual, const float* weight /*NULL*/, float* out,
                              int n, int batch_size, float eps, int use_unit_offset,
                              HipStream_t stream);                            /* cuda_bridge.h:58 */
 /* x += norm(in). */
-void hip_rmsnorm_add(float* x, const float* in, const float* weight, int n, float eps,
+void hip_rmsnorm_add(float* x, const float* in, const float* weight /*NULL*/, int n, float eps,
                      int use_unit_offset, HipStream_t stream); /* cuda_bridge.cu:2058, cuda.zig:49 */
 
 /* new: dtype-generic row variants (dtype HIP_BRIDGE_F32 or HIP_BRIDGE_BF16 for x, residual,
  * out; weights always f32), `rows` rows of n. Semantics as the f32 ops above. */
-void hip_rmsnorm_rows(int dtype, const void* x, const float* weight, void* out, int64_t rows,
+void hip_rmsnorm_rows(int dtype, const void* x, const float* weight /*NULL*/, void* out, int64_t rows,
                       int n, float eps, int use_unit_offset, HipStream_t stream);
-void hip_add_rmsnorm_rows(int dtype, void* x, const void* residual, const float* weight,
+void hip_add_rmsnorm_rows(int dtype, void* x, const void* residual, const float* weight /*NULL*/,
                           void* out, int64_t rows, int n, float eps, int use_unit_offset,
                           HipStream_t stream);
-void hip_rmsnorm_add_rows(int dtype, void* x, const void* in, const float* weight,
+void hip_rmsnorm_add_rows(int dtype, void* x, const void* in, const float* weight /*NULL*/,
                           int64_t rows, int n, float eps, int use_unit_offset,
                           HipStream_t stream);
 /* new, fused: xb' = norm(xb; w1); x += xb'; out = norm(x; w2). This is the reference's
  * post-attention norm + addRmsNorm pair (cuda_model.zig:930-942) and also the post-FFN
  * rmsnormAdd followed by the next layer's input norm (cuda_model.zig:962-967, 840-845).
  * out may alias xb. */
-void hip_rmsnorm_add_rmsnorm(int dtype, void* x, const void* xb, const float* w1,
-                             const float* w2, void* out, int64_t rows, int n, float eps,
+void hip_rmsnorm_add_rmsnorm(int dtype, void* x, const void* xb, const float* w1 /*NULL*/,
+                             const float* w2 /*NULL*/, void* out, int64_t rows, int n, float eps,
                              int use_unit_offset, HipStream_t stream);
 
 /* ---------------------------------------------------------------------------------- */
 /* RoPE, half-split (ziglm RoPEType.normal), f32, in place (replaces cuda_bridge.h:59-61) */
 /* q or k may be NULL. rotary_dim 0 or > head_dim means head_dim.                       */
 /* ---------------------------------------------------------------------------------- */
-void hip_rope(float* q, float* k, int pos, int num_heads, int num_kv_heads, int head_dim,
+void hip_rope(float* q /*NULL*/, float* k /*NULL*/, int pos, int num_heads, int num_kv_heads, int head_dim,
               int rotary_dim, float freq_base, HipStream_t stream);          /* cuda_bridge.h:59 */
-void hip_rope_ind(float* q, float* k, const int* d_pos, int num_heads, int num_kv_heads,
+void hip_rope_ind(float* q /*NULL*/, float* k /*NULL*/, const int* d_pos, int num_heads, int num_kv_heads,
                   int head_dim, int rotary_dim, float freq_base, HipStream_t stream); /* cuda_bridge.h:60 */
 /* token b of batch_size at position pos + b */
-void hip_rope_batched(float* q, float* k, int pos, int batch_size, int num_heads,
+void hip_rope_batched(float* q /*NULL*/, float* k /*NULL*/, int pos, int batch_size, int num_heads,
                       int num_kv_heads, int head_dim, int rotary_dim, float freq_base,
                       HipStream_t stream);                                   /* cuda_bridge.h:61 */
 
@@ -189,16 +194,18 @@ void hip_kv_cache_put_batched(float* k_cache, float* v_cache, const float* k, co
 /*   q: [n_tokens][num_heads][head_dim], k, v: [n_tokens][num_kv_heads][head_dim],      */
 /*   dtype HIP_BRIDGE_F32 or HIP_BRIDGE_BF16 (activations and caches);                  */
 /*   q_norm_w / k_norm_w: f32[head_dim] or NULL (no norm); q may be NULL (K/V only);     */
+/*   k or v NULL: that cache is not written (its cache pointer is then unused; given k   */
+/*   or v, k_cache or v_cache must not be NULL: EINVAL, no launch);                     */
 /*   position of token t: d_pos ? d_pos[t] : pos_base + t;                              */
 /*   cache row of token t: d_slot ? d_slot[t] : layer_idx*max_seq + position;           */
 /*   rows outside [0, cache_rows) are not written; element (t, h, j) of K goes to        */
 /*   k_cache[row*max_kv_dim + h*head_dim + j].                                          */
 /* ---------------------------------------------------------------------------------- */
-void hip_qk_norm_rope_kv(int dtype, void* q, const void* k, const void* v,
-                         const float* q_norm_w, const float* k_norm_w, int v_norm,
+void hip_qk_norm_rope_kv(int dtype, void* q /*NULL*/, const void* k /*NULL*/, const void* v /*NULL*/,
+                         const float* q_norm_w /*NULL*/, const float* k_norm_w /*NULL*/, int v_norm,
                          void* k_cache, void* v_cache, int64_t cache_rows, int layer_idx,
-                         int max_seq, int max_kv_dim, const int32_t* d_pos, int pos_base,
-                         const int64_t* d_slot, int n_tokens, int num_heads, int num_kv_heads,
+                         int max_seq, int max_kv_dim, const int32_t* d_pos /*NULL*/, int pos_base,
+                         const int64_t* d_slot /*NULL*/, int n_tokens, int num_heads, int num_kv_heads,
                          int head_dim, int rotary_dim, float freq_base, float freq_scale,
                          float eps, int use_unit_offset, HipStream_t stream);
 
@@ -260,7 +267,7 @@ typedef struct {
     float* xb_out;
 } HipGemvPrologue;
 /* y = W . v, or with up_weights: y[r] = gelu_tanh(W_r . v) * (U_r . v); any GEMV qtype. */
-void hip_gemv_pro(int qtype, const void* weights, const void* up_weights, const float* x, float* y,
+void hip_gemv_pro(int qtype, const void* weights, const void* up_weights /*NULL*/, const float* x, float* y,
                   int rows, int cols, const HipGemvPrologue* pro, HipStream_t stream);
 /* Q, K, V of one qtype over one v in one launch (hip_gemv_qkv_q4_0 for any qtype). */
 void hip_gemv_qkv_pro(int qtype, const void* q_w, const void* k_w, const void* v_w, const float* x,
@@ -309,10 +316,10 @@ size_t hip_attention_workspace_bytes(int batch, int n_heads, int n_kv_heads, int
                                      int max_len, int sliding_window);
 void hip_attention_decode(int kv_dtype, const float* q, const void* k_cache, const void* v_cache,
                           float* out, int64_t cache_rows, int64_t row_stride,
-                          const int64_t* d_row_base, int64_t row_base, const int32_t* d_pos,
+                          const int64_t* d_row_base /*NULL*/, int64_t row_base, const int32_t* d_pos /*NULL*/,
                           int pos_base, int max_len, int batch, int n_heads, int n_kv_heads,
                           int head_dim, float attn_scale, float softcap, int sliding_window,
-                          void* workspace, size_t workspace_bytes, HipStream_t stream);
+                          void* workspace /*NULL*/, size_t workspace_bytes, HipStream_t stream);
 /* new, no counterpart in the reference: hip_attention_decode for callers that cannot
  * allocate (code under hipGraph capture, tight serving loops, harnesses that forbid
  * hipMalloc). The split partials live in a static 32 MiB device array of the library, one per
@@ -322,11 +329,11 @@ void hip_attention_decode(int kv_dtype, const float* q, const void* k_cache, con
  * sequences of Gemma-4B heads over 32768 positions need 68 MB: use hip_attention_decode).
  * Every call on one GPU shares that GPU's array: calls that overlap in time on one GPU
  * (different streams, or host threads) race. Nothing in the array needs to start at zero
- * (every partial the merge reads is written by the same call). The first call on a device
+ * (every partial the merge uses is written by the same call). The first call on a device
  * looks up the array's device address (hipGetSymbolAddress); make it outside stream capture. */
 void hip_attention_decode_noalloc(int kv_dtype, const float* q, const void* k_cache, const void* v_cache,
                                   float* out, int64_t cache_rows, int64_t row_stride,
-                                  const int64_t* d_row_base, int64_t row_base, const int32_t* d_pos,
+                                  const int64_t* d_row_base /*NULL*/, int64_t row_base, const int32_t* d_pos /*NULL*/,
                                   int pos_base, int max_len, int batch, int n_heads, int n_kv_heads,
                                   int head_dim, float attn_scale, float softcap, int sliding_window,
                                   HipStream_t stream);
@@ -335,20 +342,22 @@ void hip_attention_decode_noalloc(int kv_dtype, const float* q, const void* k_ca
  * launches before attention): q holds the raw query heads (read only; not rewritten), and
  * each token's own K / V row is formed from the raw k, v [batch][n_kv_heads][head_dim]
  * (norm with k_norm_w, RoPE, v no-scale norm when v_norm) and written to its cache row
- * (row base + position), exactly what hip_qk_norm_rope_kv would write, while attention uses
- * it directly. k = v = NULL: the layer reads rows written earlier (KV-shared layers); only
+ * (row base + position), the same computation as hip_qk_norm_rope_kv's except for the order
+ * of the per-head sum of squares and the inverse square root (IEEE sqrt and divide here, the
+ * hardware reciprocal square root there, within 1 ulp of each other): the rows agree within
+ * the oracle's tolerance, not bit for bit. Attention uses the row directly. k = v = NULL: the layer reads rows written earlier (KV-shared layers); only
  * q is normalised and rotated. Norm weights may be NULL (no norm). rotary_dim / 2 must be a
  * multiple of 8 with rotary_dim / 16 a power of two (or rotary_dim 0 = head_dim such);
  * other shapes report HIP_BRIDGE_EUNSUPPORTED. Same workspace rule as hip_attention_decode. */
-void hip_attention_decode_qk(int kv_dtype, const float* q, const float* k, const float* v,
-                             const float* q_norm_w, const float* k_norm_w, int v_norm,
+void hip_attention_decode_qk(int kv_dtype, const float* q, const float* k /*NULL*/, const float* v /*NULL*/,
+                             const float* q_norm_w /*NULL*/, const float* k_norm_w /*NULL*/, int v_norm,
                              void* k_cache, void* v_cache, float* out, int64_t cache_rows,
-                             int64_t row_stride, const int64_t* d_row_base, int64_t row_base,
-                             const int32_t* d_pos, int pos_base, int max_len, int batch,
+                             int64_t row_stride, const int64_t* d_row_base /*NULL*/, int64_t row_base,
+                             const int32_t* d_pos /*NULL*/, int pos_base, int max_len, int batch,
                              int n_heads, int n_kv_heads, int head_dim, int rotary_dim,
                              float freq_base, float freq_scale, float eps, int use_unit_offset,
                              float attn_scale, float softcap, int sliding_window,
-                             void* workspace, size_t workspace_bytes, HipStream_t stream);
+                             void* workspace /*NULL*/, size_t workspace_bytes, HipStream_t stream);
 
 /* ---------------------------------------------------------------------------------- */
 /* Greedy token selection (replaces cuda_bridge.h:175) with ziglm's CPU definition      */
@@ -400,7 +409,7 @@ void hip_ple_ctx_fuse(float* ctx_ple_buf, const float* ctx_scratch, int n, int a
 /* and mix is the ceiling a fused op of that mix is compared with.                         */
 /* ---------------------------------------------------------------------------------- */
 int hip_stream_ref_shapes(void);
-int hip_stream_ref(int n_in, int n_out, const void* in0, const void* in1, void* out0, void* out1,
+int hip_stream_ref(int n_in, int n_out, const void* in0, const void* in1 /*NULL*/, void* out0, void* out1 /*NULL*/,
                    int64_t bytes, int shape, HipStream_t stream);
 
 #ifdef __cplusplus

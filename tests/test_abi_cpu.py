@@ -8,6 +8,7 @@ device."""
 import os
 import re
 import subprocess
+import sys
 
 import pytest
 
@@ -135,3 +136,137 @@ def test_zig_binding_has_every_cuda_device_method():
         assert re.search(r"pub const " + alias + r"\b", text), alias
     for n in REFERENCE_ABI:
         assert re.search(r"pub const " + n + r" = hip_", text), n
+
+
+# ---- parameter types of hip.zig's externs against include/hip_bridge.h ---------------------
+
+_C_BASE = {"int": "c_int", "unsigned int": "c_uint", "int64_t": "i64", "int32_t": "i32", "size_t": "usize",
+           "float": "f32", "double": "f64", "unsigned char": "u8", "char": "u8", "uint32_t": "u32",
+           "void": "anyopaque", "HipStream_t": "HipStream_t", "HipGraph_t": "HipGraph_t",
+           "HipGraphExec_t": "HipGraphExec_t", "HipEvent_t": "HipEvent_t",
+           "HipGemvPrologue": "HipGemvPrologue"}
+# handle typedefs: void* in C, an optional opaque pointer in Zig (as cuda.zig's CudaStream_t)
+_HANDLES = {"HipStream_t", "HipGraph_t", "HipGraphExec_t", "HipEvent_t"}
+# Zig parameters that keep cuda.zig's declared type where the C definition is more specific
+# (the same pointer in the ABI): cuda.zig:39 binds cuda_gemv_f32's const float* weights
+# (cuda_bridge.cu:1151) as ?*const anyopaque.
+_ZIG_AS_REFERENCE = {("hip_gemv_f32", "weights"): "?*const anyopaque"}
+
+
+def _c_type(decl):
+    """'const float* w' -> (pointer levels, const pointee, Zig name of the base type)."""
+    t = decl.strip()
+    t = t[: len(t) - len(re.search(r"\w+$", t).group(0))].strip()  # drop the parameter name
+    parts = [p.strip() for p in t.split("*")]
+    words = parts[0].split()
+    base = " ".join(w for w in words if w != "const")
+    return len(parts) - 1, "const" in words, _C_BASE[base]
+
+
+def _c_params():
+    text = open(os.path.join(ROOT, "include", "hip_bridge.h")).read()
+    out = {}
+    for m in re.finditer(r"\b(int|void|size_t|const char\*)\s+(hip_\w+)\s*\(([^;{]*?)\)\s*;", text, flags=re.S):
+        ret, name, args = m.group(1), m.group(2), m.group(3)
+        params = []
+        raw = [a for a in args.split(",")] if args.strip() not in ("", "void") else []
+        for a in raw:
+            nullable = "/*NULL*/" in a
+            a = re.sub(r"/\*.*?\*/", "", a, flags=re.S).strip()
+            levels, cbase, base = _c_type(a)
+            params.append((a.split()[-1].lstrip("*"), levels, cbase, base, nullable))
+        out[name] = (ret, params)
+    return out
+
+
+def _zig_type(t):
+    """'?[*]const f32' -> (optional, levels, const pointee at the innermost level, base)."""
+    t = t.strip()
+    opt = t.startswith("?")
+    t = t.lstrip("?")
+    levels = 0
+    inner_opt = False
+    const = False
+    while True:
+        m = re.match(r"^(\[\*c\]|\[\*:0\]|\[\*\]|\*)(const\s+)?(\?)?", t)
+        if not m:
+            break
+        levels += 1
+        const = bool(m.group(2))
+        inner_opt = inner_opt or bool(m.group(3))
+        t = t[m.end():].strip()
+    return opt, levels, const, t, inner_opt
+
+
+def _zig_params():
+    text = open(HIP_ZIG).read()
+    out = {}
+    for m in re.finditer(r"pub extern \"c\" fn (hip_\w+)\((.*?)\)\s*([^;(]+);", text):
+        args = [a for a in m.group(2).split(",") if a.strip()]
+        params = []
+        for a in args:
+            nm, ty = a.split(":", 1)
+            params.append((nm.strip(), ty.strip()))
+        out[m.group(1)] = (m.group(3).strip(), params)
+    return out
+
+
+def test_zig_binding_parameter_types_match_header():
+    """Every extern of hip.zig against its C declaration, parameter by parameter: pointer
+    depth, constness of the pointee, the scalar type (c_int / i64 / i32 / usize / f32 / u8),
+    and optionality: a parameter the header marks NULL is optional (?) in Zig. The header's
+    plain pointers may also be optional in Zig (device buffers pass as CudaBuffer.ptr, an
+    optional pointer, as in cuda.zig). Handle typedefs (HipStream_t, ...) are pointer types
+    in both."""
+    c, z = _c_params(), _zig_params()
+    assert set(c) == set(z), (sorted(set(c) - set(z)), sorted(set(z) - set(c)))
+    ret_map = {"int": "c_int", "void": "void", "size_t": "usize", "const char*": "[*:0]const u8"}
+    problems = []
+    for name, (cret, cps) in c.items():
+        zret, zps = z[name]
+        if ret_map[cret] != zret:
+            problems.append((name, "return", cret, zret))
+        if len(cps) != len(zps):
+            problems.append((name, "arity", len(cps), len(zps)))
+            continue
+        for (cn, lv, cconst, base, nullable), (zn, zt) in zip(cps, zps):
+            opt, zlv, zconst, zbase, _ = _zig_type(zt)
+            where = (name, cn, zt)
+            if (name, cn) in _ZIG_AS_REFERENCE:
+                if zt != _ZIG_AS_REFERENCE[(name, cn)]:
+                    problems.append(where + ("cuda.zig form",))
+                continue
+            if base in _HANDLES:
+                if lv == 0 and zbase != base or lv == 1 and not (zlv == 1 and zbase == base):
+                    problems.append(where + ("handle",))
+                continue
+            if zlv != lv or zbase != base:
+                problems.append(where + (f"C {lv}x* {base}",))
+            elif lv == 1 and zconst != cconst:
+                problems.append(where + ("const" if cconst else "mutable",))
+            elif lv == 0 and opt:
+                problems.append(where + ("optional scalar",))
+            if nullable and not opt:
+                problems.append(where + ("NULL allowed in C, not optional in Zig",))
+    assert not problems, problems
+
+
+def test_zig_type_check_catches_planted_mistakes(tmp_path, monkeypatch):
+    """The check above against copies of hip.zig with one planted mistake each: a const
+    pointee made mutable, an i64 narrowed to c_int, a NULL-able pointer made non-optional, a
+    pointer made a double pointer."""
+    src = open(HIP_ZIG).read()
+    mutations = [
+        ("hip_rmsnorm(x: [*]const f32", "hip_rmsnorm(x: [*]f32"),
+        ("n_rows: i64, ids: [*]const i32", "n_rows: c_int, ids: [*]const i32"),
+        ("hip_rmsnorm_add_rmsnorm(dtype: c_int, x: *anyopaque, xb: *const anyopaque, w1: ?[*]const f32",
+         "hip_rmsnorm_add_rmsnorm(dtype: c_int, x: *anyopaque, xb: *const anyopaque, w1: [*]const f32"),
+        ("hip_event_elapsed_ms(ms: *f32", "hip_event_elapsed_ms(ms: **f32"),
+    ]
+    for old, new in mutations:
+        assert src.count(old) == 1, old
+        p = tmp_path / "hip.zig"
+        p.write_text(src.replace(old, new))
+        monkeypatch.setattr(sys.modules[__name__], "HIP_ZIG", str(p))
+        with pytest.raises(AssertionError):
+            test_zig_binding_parameter_types_match_header()

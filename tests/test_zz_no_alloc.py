@@ -1,14 +1,17 @@
 """hip_attention_decode_noalloc (the no-allocation entry point) against hip_attention_decode
 with a caller workspace, through the C-ABI: two calls in a row, the second with a smaller
 input, each bit-identical to the workspace entry point (same kernels, same split count, same
-partials); and a call whose workspace would exceed the static scratch is refused with
-HIP_BRIDGE_ESCRATCH and leaves its output untouched."""
+partials); a call that needs no workspace (the unsplit path); the call captured in a
+hipGraph and replayed over the shared scratch with new positions; and a call whose workspace
+would exceed the static scratch is refused with HIP_BRIDGE_ESCRATCH and leaves its output
+untouched."""
 import numpy as np
 import pytest
 
 from ziglm_amd import bridge as B
 from ziglm_amd import synth
 from ziglm_amd.bridge import HipError
+from ziglm_amd.device import Graph
 
 pytestmark = pytest.mark.gpu
 
@@ -27,21 +30,33 @@ def _case(dev, seed, batch, n_heads, n_kv, D, max_len, window, kv_dtype):
                       kv_dtype=kv_dtype, rows=batch * max_len, kvd=kvd)
 
 
+def _noalloc(dev, bufs, c, out):
+    dev.attentionDecodeNoalloc(c["kv_dtype"], bufs["q"], bufs["kc"], bufs["vc"], out, c["rows"], c["kvd"], bufs["rb"],
+                               0, bufs["pos"], 0, c["max_len"], c["batch"], c["n_heads"], c["n_kv"], c["D"], 1.0, 30.0,
+                               c["window"])
+
+
+def _with_workspace(dev, bufs, c):
+    """hip_attention_decode with a caller workspace: (output, workspace bytes)."""
+    n = c["batch"] * c["n_heads"] * c["D"]
+    out_ws = dev.alloc(n * 4)
+    out_ws.fill(0xCD)
+    need = dev.attentionWorkspaceBytes(c["batch"], c["n_heads"], c["n_kv"], c["D"], c["max_len"], c["window"])
+    ws = dev.alloc(max(need, 16))
+    dev.attentionDecode(c["kv_dtype"], bufs["q"], bufs["kc"], bufs["vc"], out_ws, c["rows"], c["kvd"], bufs["rb"], 0,
+                        bufs["pos"], 0, c["max_len"], c["batch"], c["n_heads"], c["n_kv"], c["D"], 1.0, 30.0,
+                        c["window"], ws, need)
+    return out_ws.to_numpy((c["batch"], c["n_heads"] * c["D"]), np.float32), need
+
+
 def _run_pair(dev, bufs, c):
     """(no-alloc output, workspace output) of the same call."""
     n = c["batch"] * c["n_heads"] * c["D"]
-    out_na, out_ws = dev.alloc(n * 4), dev.alloc(n * 4)
+    out_na = dev.alloc(n * 4)
     out_na.fill(0xAB)
-    out_ws.fill(0xCD)
-    args = (bufs["kc"], bufs["vc"])
-    dev.attentionDecodeNoalloc(c["kv_dtype"], bufs["q"], *args, out_na, c["rows"], c["kvd"], bufs["rb"], 0, bufs["pos"],
-                               0, c["max_len"], c["batch"], c["n_heads"], c["n_kv"], c["D"], 1.0, 30.0, c["window"])
-    need = dev.attentionWorkspaceBytes(c["batch"], c["n_heads"], c["n_kv"], c["D"], c["max_len"], c["window"])
-    ws = dev.alloc(max(need, 16))
-    dev.attentionDecode(c["kv_dtype"], bufs["q"], *args, out_ws, c["rows"], c["kvd"], bufs["rb"], 0, bufs["pos"], 0,
-                        c["max_len"], c["batch"], c["n_heads"], c["n_kv"], c["D"], 1.0, 30.0, c["window"], ws, need)
-    shape = (c["batch"], c["n_heads"] * c["D"])
-    return out_na.to_numpy(shape, np.float32), out_ws.to_numpy(shape, np.float32), need
+    _noalloc(dev, bufs, c, out_na)
+    ref, need = _with_workspace(dev, bufs, c)
+    return out_na.to_numpy(ref.shape, np.float32), ref, need
 
 
 def test_noalloc_matches_workspace_entry_point_twice(dev):
@@ -74,3 +89,41 @@ def test_noalloc_refuses_calls_beyond_its_scratch(dev):
                                    1.0, 0.0, 0)
     assert f"{B.ESCRATCH} " in str(e.value)
     assert np.all(out.to_numpy((batch * nh * D * 4,), np.uint8) == 0x5A)
+
+
+def test_noalloc_unsplit_shape(dev):
+    """A call that needs no workspace (8-row caches: one split): the no-allocation entry point
+    takes the unsplit path and matches the workspace entry point bit for bit."""
+    bufs, c = _case(dev, 46, 3, 8, 4, 256, 8, 0, B.F32)
+    got, ref, need = _run_pair(dev, bufs, c)
+    assert need == 0
+    assert np.all(np.isfinite(ref))
+    np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_noalloc_captured_in_a_graph(dev):
+    """The use the entry point is for: one eager call (the scratch address is looked up
+    outside capture), then the call captured in a hipGraph and replayed twice over the
+    shared static scratch with new positions written into d_pos between the replays; each
+    replay bit-identical to hip_attention_decode with a workspace over the same positions."""
+    bufs, c = _case(dev, 43, 4, 8, 4, 256, 4096, 0, B.F32)
+    n = c["batch"] * c["n_heads"] * c["D"]
+    out_g = dev.alloc(n * 4)
+    _noalloc(dev, bufs, c, out_g)
+    dev.sync()
+    g = Graph(dev, lambda: _noalloc(dev, bufs, c, out_g))
+    try:
+        for seed in (44, 45):
+            pos = synth.uniform_int(seed, "pos", (c["batch"],), 0, c["max_len"] - 1).astype(np.int32)
+            bufs["pos"].upload(pos)
+            out_g.fill(0xAB)
+            dev.sync()
+            g.launch()
+            dev.sync()
+            got = out_g.to_numpy((c["batch"], c["n_heads"] * c["D"]), np.float32)
+            ref, need = _with_workspace(dev, bufs, c)
+            assert need > 0
+            assert np.all(np.isfinite(ref))
+            np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
+    finally:
+        g.destroy()

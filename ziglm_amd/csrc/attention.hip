@@ -427,7 +427,10 @@ __global__ __launch_bounds__(kMergeThreads) void k_attn_merge(AttnArgs a) {
     const int lane = tid % kWave, wv = tid / kWave;
     const int e = blockIdx.y * kMergeCols + lane;
     // The loads go out before the position is read: over all nsplit splits of the workspace
-    // (reads past the last split give 0), the splits at or past `used` dropped below.
+    // (reads past the last split give 0), the splits at or past `used` dropped below. Those
+    // slots hold whatever an earlier call left (the no-allocation scratch is never cleared):
+    // the `< used` masks on mv / lv / pre below are what keep such contents, NaN included,
+    // out of the result.
     const float* w = a.ws + (int64_t)bh * a.nsplit * (a.D + 2);
     const uint32_t rowb = (uint32_t)(a.D + 2) * 4u;
     const auto rs = buf_rsrc(w, (uint32_t)a.nsplit * rowb);

@@ -544,7 +544,7 @@ void hip_qk_norm_rope_kv(int dtype, void* q, const void* k, const void* v,
     a.uo = use_unit_offset;
     a.freq_scale = freq_scale;
     a.eps = eps;
-    if (max_kv_dim < num_kv_heads * head_dim) {
+    if (max_kv_dim < num_kv_heads * head_dim || (k && !k_cache) || (v && !v_cache)) {
         set_error(HIP_BRIDGE_EINVAL);
         return;
     }

@@ -49,11 +49,13 @@ __global__ __launch_bounds__(THREADS) void k_stream(StreamArgs a) {
 }
 
 // The launch shapes the ceiling is the best of: {threads, chunks per thread} x load policy
-// {default, nt} x store policy {nt, sc1}.
+// {default, nt} x store policy {nt, sc1}. The 3-, 5- and 6-chunk shapes follow the norm
+// kernels' layout (a 128- or 256-thread group over 3 chunks per lane of a row, two rows per
+// group).
 struct Shape {
     int threads, unroll;
 };
-constexpr Shape kGeo[] = {{64, 1}, {256, 1}, {256, 2}, {256, 4}, {512, 2}};
+constexpr Shape kGeo[] = {{64, 1}, {256, 1}, {256, 2}, {256, 4}, {512, 2}, {128, 3}, {256, 3}, {256, 5}, {256, 6}};
 constexpr int kNumGeo = sizeof(kGeo) / sizeof(kGeo[0]);
 constexpr int kNumShapes = kNumGeo * 4;
 
@@ -70,7 +72,11 @@ static void launch_geo(int geo, const StreamArgs& a, hipStream_t s) {
         case 1: launch_one<NIN, NOUT, 256, 1, LP, SP>(a, s); break;
         case 2: launch_one<NIN, NOUT, 256, 2, LP, SP>(a, s); break;
         case 3: launch_one<NIN, NOUT, 256, 4, LP, SP>(a, s); break;
-        default: launch_one<NIN, NOUT, 512, 2, LP, SP>(a, s); break;
+        case 4: launch_one<NIN, NOUT, 512, 2, LP, SP>(a, s); break;
+        case 5: launch_one<NIN, NOUT, 128, 3, LP, SP>(a, s); break;
+        case 6: launch_one<NIN, NOUT, 256, 3, LP, SP>(a, s); break;
+        case 7: launch_one<NIN, NOUT, 256, 5, LP, SP>(a, s); break;
+        default: launch_one<NIN, NOUT, 256, 6, LP, SP>(a, s); break;
     }
 }
 
