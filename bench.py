@@ -548,8 +548,9 @@ def bench_gemv(dev):
 def bench_gemm_prefill(dev, T=2048):
     """Prefill products on the matrix cores (hip_gemm, 2048 tokens, f32 activations): us and
     algorithmic TFLOP/s (2 * rows * cols * tokens / t). The kernel runs three bf16 terms of
-    every activation (and one to three of every weight) through v_mfma_f32_32x32x16_bf16, so
-    its ceiling is a third of the 2.5 PFLOP/s dense bf16 peak for Q4_0 / Q8_0 / BF16."""
+    every activation and one to three of every weight through v_mfma_f32_32x32x16_bf16
+    (frac_of_3term_bound: against a third of the 2.5 PFLOP/s dense bf16 peak); hip_gemm_ex
+    with bf16 activations takes one activation term (frac_of_bf16_peak)."""
     s = LY.GEMMA_4B
     H, I = s.H, s.I
     cases = [("gate_q4_0", B.Q4_0, I, H), ("down_q4_0", B.Q4_0, H, I), ("qkv_q4_0", B.Q4_0, (s.nh + 2 * s.nkv) * s.D, H),
@@ -562,6 +563,60 @@ def bench_gemm_prefill(dev, T=2048):
         out[name] = {"us": r["us"], "rows": rows, "cols": cols, "tokens": T, "TFLOPs": round(tf, 1),
                      "frac_of_3term_bound": round(tf / (PEAK_BF16_TFLOPS / 3), 4)}
         log(f"  gemm {name:12s} {r['us']:9.2f} us {tf:7.1f} TFLOP/s")
+    # f32 activations split once into three bf16 planes (hip_split_terms; shared by every
+    # product of one input, so the K loop converts weights only): the products alone.
+    x_planes = dev.alloc(3 * T * max(H, I) * 2)
+    for name, qt, rows, cols in [("gate_q4_0_terms", B.Q4_0, I, H), ("down_q4_0_terms", B.Q4_0, H, I)]:
+        def fn(d, m, x, ys, qt=qt, rows=rows, cols=cols):
+            d.gemmEx(qt, m[0], None, B.F32_TERMS, x_planes, B.F32, ys[0], T, rows, cols)
+        r = gemv_case(dev, name, qt, [(rows, cols)], fn, T)
+        tf = 2.0 * rows * cols * T / r["us"] / 1e6
+        out[name] = {"us": r["us"], "rows": rows, "cols": cols, "tokens": T, "TFLOPs": round(tf, 1), "x": "f32 as 3 planes",
+                     "frac_of_3term_bound": round(tf / (PEAK_BF16_TFLOPS / 3), 4)}
+        log(f"  gemm {name:22s} {r['us']:9.2f} us {tf:7.1f} TFLOP/s")
+    # the split itself (f32 [T x H] -> three planes), once per activation
+    xs = [dev.alloc(T * H * 4) for _ in range(8)]
+    us_split = time_launches_us(dev, lambda d, xb: d.splitTerms(xb, x_planes, T * H), xs, 64)
+    out["split_terms_2048x2560"] = {"us": round(us_split, 2), "bytes": T * H * (4 + 6),
+                                    "GBps": round(T * H * 10 / us_split / 1e3, 1)}
+    log(f"  split terms 2048 x 2560          {us_split:9.2f} us")
+    for b_ in xs + [x_planes]:
+        b_.deinit()
+    # bf16 activations (one exact term; the c2 chain's norm output feeds them directly) with
+    # bf16 output, and the gate.up pair with its GeGLU epilogue (two products, one launch).
+    # The activation buffer's bytes are read as bf16 (timing only).
+    ex_cases = [("gate_q4_0_bf16", B.Q4_0, I, H, False), ("down_q4_0_bf16", B.Q4_0, H, I, False),
+                ("gateup_geglu_q4_0_bf16", B.Q4_0, I, H, True)]
+    for name, qt, rows, cols, ge in ex_cases:
+        shapes = [(rows, cols)] * (2 if ge else 1)
+
+        def fn(d, m, x, ys, qt=qt, rows=rows, cols=cols, ge=ge):
+            d.gemmEx(qt, m[0], m[1] if ge else None, B.BF16, x, B.BF16, ys[0], T, rows, cols)
+        r = gemv_case(dev, name, qt, shapes, fn, T)
+        flops = 2.0 * rows * cols * T * (2 if ge else 1)
+        tf = flops / r["us"] / 1e6
+        out[name] = {"us": r["us"], "rows": rows, "cols": cols, "tokens": T, "TFLOPs": round(tf, 1),
+                     "x": "bf16", "y": "bf16", "geglu_pair": ge, "frac_of_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4)}
+        log(f"  gemm {name:22s} {r['us']:9.2f} us {tf:7.1f} TFLOP/s")
+    # The FFN half of a prefill layer with bf16 activations (gate.up -> GeGLU -> down, Q4_0):
+    # the reference's structure (two GEMMs writing gate and up, k_geglu reading them back,
+    # cuda_model.zig:1372-1387) against the fused pair, whose gate and up never reach HBM
+    # (3 * T * I * 2 bytes less traffic: 126 MB at T = 2048).
+    for name, fused in (("ffn_block_q4_0_bf16_unfused", False), ("ffn_block_q4_0_bf16_fused", True)):
+        def fn(d, m, x, ys, fused=fused):
+            half = T * I * 2  # ys[0] holds gate (bf16) then act; ys[1] up
+            gate, act, up = ys[0], ys[0].at(half), ys[1]
+            if fused:
+                d.gemmEx(B.Q4_0, m[0], m[1], B.BF16, x, B.BF16, act, T, I, H)
+            else:
+                d.gemmEx(B.Q4_0, m[0], None, B.BF16, x, B.BF16, gate, T, I, H)
+                d.gemmEx(B.Q4_0, m[1], None, B.BF16, x, B.BF16, up, T, I, H)
+                d.gegluEx(B.BF16, gate, up, act, T * I)
+            d.gemmEx(B.Q4_0, m[2], None, B.BF16, act, B.BF16, ys[2], T, H, I)
+        r = gemv_case(dev, name, B.Q4_0, [(I, H), (I, H), (H, I)], fn, T)
+        out[name] = {"us": r["us"], "tokens": T, "hidden": H, "intermediate": I,
+                     "TFLOPs": round(2.0 * 3 * I * H * T / r["us"] / 1e6, 1)}
+        log(f"  {name:30s} {r['us']:9.2f} us")
     return out
 
 

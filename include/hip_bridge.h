@@ -54,6 +54,9 @@ typedef void* HipEvent_t;     /* new: event handle for stream timing */
 #define HIP_BRIDGE_Q4_K 12
 #define HIP_BRIDGE_Q6_K 14
 #define HIP_BRIDGE_BF16 30
+/* new: f32 activations as three bf16 term planes (hip_split_terms), an input form of
+ * hip_gemm_ex only */
+#define HIP_BRIDGE_F32_TERMS 256
 
 /* hip_bridge_last_error() codes (positive values are hipError_t launch errors). */
 #define HIP_BRIDGE_OK 0
@@ -282,6 +285,24 @@ void hip_gemm_f16(const void* weights, const float* x, float* y, int batch_size,
                   int cols, HipStream_t stream);                            /* cuda_bridge.h:49 */
 void hip_gemm(int qtype, const void* weights, const float* x, float* y, int batch_size,
               int rows, int cols, HipStream_t stream);                      /* cuda_bridge.h:50 */
+/* new: the prefill product with f32, bf16 or split f32 (HIP_BRIDGE_F32_TERMS) activations
+ * (x_dtype) and f32 or bf16 output (y_dtype), and
+ * the gate.up GeGLU pair: with up_weights (same type and shape), y[b][r] =
+ * gelu_tanh(W_r . x_b) * (U_r . x_b), the reference's two prefill GEMMs and k_geglu
+ * (cuda_model.zig:1372-1387) in one launch. bf16 activations are exact matrix-core operands
+ * (one term), so a bf16 norm output feeds the product directly. Q4_0, Q8_0, F16, BF16, F32
+ * weights; cols % 32 == 0; x 16-byte aligned; 128 * cols * sizeof(x element) < 4 GiB; else
+ * EUNSUPPORTED. f32 x and y without up_weights is hip_gemm. */
+void hip_gemm_ex(int qtype, const void* weights, const void* up_weights /*NULL*/, int x_dtype,
+                 const void* x, int y_dtype, void* y, int batch_size, int rows, int cols,
+                 HipStream_t stream);
+/* new: f32 activations x[n] -> three bf16 planes planes[u][n] (u = 0, 1, 2: h = bf16(x),
+ * m = bf16(x - h), l = bf16(x - h - m); h + m + l carries x's 24 significant bits), the
+ * HIP_BRIDGE_F32_TERMS input of hip_gemm_ex: split once and shared by every product of the
+ * same activations (QKV, gate and up), the K loop then converts weights only. The products
+ * equal hip_gemm's on the f32 activations bit for bit. n % 4 == 0, x 16-byte and planes
+ * 8-byte aligned; else EUNSUPPORTED. */
+void hip_split_terms(const float* x, void* planes, int64_t n, HipStream_t stream);
 
 /* ---------------------------------------------------------------------------------- */
 /* Decode attention, f32 q/out (replaces cuda_bridge.h:115-168)                         */

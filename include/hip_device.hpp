@@ -101,6 +101,16 @@ public:
               size_t rows, size_t cols) const {
         hip_gemm((int)qtype, d_weights, d_x, d_y, (int)batch_size, (int)rows, (int)cols, stream);
     }
+    // new: f32 activations -> three bf16 term planes [3][n] (gemmEx's HIP_BRIDGE_F32_TERMS input)
+    void splitTerms(const float* d_x, void* d_planes, size_t n) const {
+        hip_split_terms(d_x, d_planes, (int64_t)n, stream);
+    }
+    // new: f32 / bf16 activations and output; with d_up_weights, y = gelu(W x) * (U x)
+    void gemmEx(GGMLType qtype, const void* d_weights, const void* d_up_weights, int x_dtype, const void* d_x,
+                int y_dtype, void* d_y, size_t batch_size, size_t rows, size_t cols) const {
+        hip_gemm_ex((int)qtype, d_weights, d_up_weights, x_dtype, d_x, y_dtype, d_y, (int)batch_size, (int)rows,
+                    (int)cols, stream);
+    }
     // new: products with an input prologue (norm / residual add / gelu(x) * r), batch 1
     void gemvPro(GGMLType qtype, const void* d_weights, const void* d_up_weights, const float* d_x, float* d_y,
                  size_t rows, size_t cols, const HipGemvPrologue* pro) const {

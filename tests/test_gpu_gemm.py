@@ -73,3 +73,149 @@ def test_gemm_mfma_extreme_activations(dev):
     exact = X.astype(np.float64) @ wd.T
     got = run(dev, B.BF16, raw, X, rows, cols).astype(np.float64)
     assert np.all(np.abs(got - exact) <= bound(wd, X))
+
+
+# ---- hip_gemm_ex: bf16 activations (one exact term), bf16 output, gate.up GeGLU ----------
+
+def bf16_bits(a):
+    return O.get().f32_to_bf16(np.ascontiguousarray(a, np.float32))
+
+
+def run_ex(dev, qtype, raw, X, rows, cols, x_dtype, y_dtype, raw_up=None):
+    batch = X.shape[0]
+    xb = bf16_bits(X) if x_dtype == B.BF16 else np.ascontiguousarray(X, np.float32)
+    d_w = dev.from_numpy(np.ascontiguousarray(raw).reshape(-1))
+    d_u = dev.from_numpy(np.ascontiguousarray(raw_up).reshape(-1)) if raw_up is not None else None
+    d_x = dev.from_numpy(xb.reshape(-1))
+    es = 2 if y_dtype == B.BF16 else 4
+    d_y = dev.alloc(batch * rows * es)
+    d_y.fill(0xAB)
+    dev.gemmEx(qtype, d_w, d_u, x_dtype, d_x, y_dtype, d_y, batch, rows, cols)
+    if y_dtype == B.BF16:
+        return d_y.to_numpy((batch, rows), np.uint16)
+    return d_y.to_numpy((batch, rows), np.float32)
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("rows,cols,batch", [(128, 64, 32), (200, 96, 37), (129, 2560, 5), (4100, 64, 2050),
+                                             (4096, 64, 1024), (77, 160, 300)])
+def test_gemm_ex_bf16_activations_integer_bitexact(dev, qtype, rows, cols, batch):
+    """Integer activations are exact in bf16, so the bf16-input product of integer operands is
+    the exact integer dot product (f32 output) and its bf16 rounding (bf16 output)."""
+    raw, wd = int_matrix(qtype, rows, cols, seed=rows * cols + qtype + batch + 1, scale_pow=-1)
+    X = np.random.default_rng(batch + 7).integers(-3, 4, (batch, cols)).astype(np.float32)
+    exact = (X.astype(np.float64) @ wd.T).astype(np.float32)
+    got = run_ex(dev, qtype, raw, X, rows, cols, B.BF16, B.F32)
+    np.testing.assert_array_equal(got, exact, err_msg=f"qtype={qtype} {rows}x{cols} b={batch}")
+    got16 = run_ex(dev, qtype, raw, X, rows, cols, B.BF16, B.BF16)
+    np.testing.assert_array_equal(got16, bf16_bits(exact))
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("rows,cols,batch", [(256, 2560, 128), (300, 1024, 77), (1024, 2560, 512), (4096, 512, 2048)])
+def test_gemm_ex_bf16_activations_vs_f64_and_oracle(dev, oracle, qtype, rows, cols, batch):
+    """bf16 activations against the float64 product of the same (bf16-valued) activations and
+    the oracle's math.gemm on them: within 2^-20 * sum |w_i x_i|."""
+    raw, wd = random_matrix(qtype, rows, cols, seed=rows + cols + batch + 3)
+    Xf = O.get().bf16_to_f32(bf16_bits(synth.normal_f32(rows + batch, "Xb", (batch, cols), 0, 2)))
+    exact = Xf.astype(np.float64) @ wd.T
+    bd = bound(wd, Xf)
+    got = run_ex(dev, qtype, raw, Xf, rows, cols, B.BF16, B.F32).astype(np.float64)
+    assert np.all(np.abs(got - exact) <= bd), float(np.max(np.abs(got - exact) / bd))
+    if rows * cols * batch <= 1 << 27:
+        ref = oracle.gemm(qtype, raw, Xf).astype(np.float64)
+        assert np.all(np.abs(ref - exact) <= bd)
+
+
+def _gelu64(g):
+    return 0.5 * g * (1.0 + np.tanh(0.7978845608 * (g + 0.044715 * g ** 3)))
+
+
+@pytest.mark.parametrize("qtype", [B.Q4_0, B.Q8_0, B.BF16])
+@pytest.mark.parametrize("x_dtype,y_dtype", [(B.BF16, B.BF16), (B.BF16, B.F32), (B.F32, B.F32)])
+@pytest.mark.parametrize("rows,cols,batch", [(320, 256, 96), (1000, 512, 200), (2560, 2560, 2048)])
+def test_gemm_ex_geglu_pair(dev, oracle, qtype, x_dtype, y_dtype, rows, cols, batch):
+    """y = gelu_tanh(W x) * (U x) in one launch against float64: g = W x and u = U x each lie
+    within the product bound bd_g / bd_u of their exact values, and gelu has |gelu'| < 1.13,
+    so |y - gelu(g64) u64| <= 1.13 bd_g |u64| + |gelu(g64)| bd_u + bd_g bd_u, plus the kernel's
+    own GELU and product rounding (a few ulp: 1e-5 relative and, for the reference's 1 + tanh(z)
+    cancellation, 2^-22 |g u|), plus one bf16 ulp for a bf16 output. Also against the oracle's
+    composition (math.gemm twice, then math.geglu) at the smallest size."""
+    raw_g, wg = random_matrix(qtype, rows, cols, seed=rows + batch + 11)
+    raw_u, wu = random_matrix(qtype, rows, cols, seed=rows + batch + 12)
+    X = synth.normal_f32(rows + batch + 13, "Xg", (batch, cols), 0, 1)
+    if x_dtype == B.BF16:
+        X = O.get().bf16_to_f32(bf16_bits(X))
+    g64, u64 = X.astype(np.float64) @ wg.T, X.astype(np.float64) @ wu.T
+    bd_g, bd_u = bound(wg, X), bound(wu, X)
+    ref = _gelu64(g64) * u64
+    tol = 1.13 * bd_g * np.abs(u64) + np.abs(_gelu64(g64)) * bd_u + bd_g * bd_u + 1e-5 * np.abs(ref) \
+        + 2.0 ** -22 * np.abs(g64 * u64)
+    got = run_ex(dev, qtype, raw_g, X, rows, cols, x_dtype, y_dtype, raw_up=raw_u)
+    if y_dtype == B.BF16:
+        got = O.get().bf16_to_f32(got)
+        tol = tol + np.spacing(np.abs(ref).astype(np.float32)).astype(np.float64) * 65536.0
+    got = got.astype(np.float64)
+    bad = np.abs(got - ref) > tol
+    assert not bad.any(), (int(bad.sum()), float(np.max(np.abs(got - ref) / tol)))
+    if rows == 320:
+        og = oracle.gemm(qtype, raw_g, X)
+        ou = oracle.gemm(qtype, raw_u, X)
+        oref = oracle.geglu(og, ou).astype(np.float64)
+        assert np.all(np.abs(oref - ref) <= tol)
+
+
+# ---- hip_split_terms and the F32_TERMS input ----------------------------------------------
+
+def split_terms_ref(x):
+    """h = bf16(x), m = bf16(x - h), l = bf16(x - h - m), RNE, float32 arithmetic (numpy)."""
+    o = O.get()
+    x = np.ascontiguousarray(x, np.float32)
+    h = o.f32_to_bf16(x)
+    r = (x - o.bf16_to_f32(h)).astype(np.float32)
+    m = o.f32_to_bf16(r)
+    r2 = (r - o.bf16_to_f32(m)).astype(np.float32)
+    return np.stack([h, m, o.f32_to_bf16(r2)])
+
+
+def test_split_terms_bitexact(dev):
+    rng = np.random.default_rng(31)
+    n = 4 * 40000
+    x = (rng.standard_normal(n) * 10.0 ** rng.integers(-30, 31, n)).astype(np.float32)
+    x[::97] = 0.0
+    x[1::101] = -0.0
+    d_p = dev.alloc(3 * n * 2)
+    dev.splitTerms(dev.from_numpy(x), d_p, n)
+    got = d_p.to_numpy((3, n), np.uint16)
+    assert_eq = np.testing.assert_array_equal
+    assert_eq(got, split_terms_ref(x))
+    o = O.get()
+    # h + m + l = x to 2^-24 relative; where x is below ~2^-110 the small terms are bf16
+    # subnormals, whose last place is 2^-133 (the absolute floor)
+    s = sum(o.bf16_to_f32(got[u]).astype(np.float64) for u in range(3))
+    assert np.all(np.abs(s - x) <= 2.0 ** -24 * np.abs(x) + 2.0 ** -133)
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("rows,cols,batch", [(256, 2560, 128), (300, 1024, 77), (4096, 512, 2048), (129, 160, 40)])
+def test_gemm_ex_split_terms_equal_f32_product(dev, qtype, rows, cols, batch):
+    """Activations split beforehand (hip_split_terms, F32_TERMS input) give hip_gemm's f32
+    product bit for bit: the kernel stages the same three terms it would form itself."""
+    raw, _ = random_matrix(qtype, rows, cols, seed=rows + cols + batch + 21)
+    X = synth.normal_f32(rows + batch + 22, "Xs", (batch, cols), 0, 3)
+    ref = run(dev, qtype, raw, X, rows, cols)
+    d_x = dev.from_numpy(X.reshape(-1))
+    d_p = dev.alloc(3 * batch * cols * 2)
+    dev.splitTerms(d_x, d_p, batch * cols)
+    d_w = dev.from_numpy(np.ascontiguousarray(raw).reshape(-1))
+    d_y = dev.alloc(batch * rows * 4)
+    d_y.fill(0xAB)
+    dev.gemmEx(qtype, d_w, None, B.F32_TERMS, d_p, B.F32, d_y, batch, rows, cols)
+    np.testing.assert_array_equal(d_y.to_numpy((batch, rows), np.float32), ref)
+    # the GeGLU pair on split activations against the pair on f32 activations
+    if qtype == B.Q4_0:
+        raw_u, _ = random_matrix(qtype, rows, cols, seed=rows + cols + batch + 23)
+        a = run_ex(dev, qtype, raw, X, rows, cols, B.F32, B.F32, raw_up=raw_u)
+        d_u = dev.from_numpy(np.ascontiguousarray(raw_u).reshape(-1))
+        dev.gemmEx(qtype, d_w, d_u, B.F32_TERMS, d_p, B.F32, d_y, batch, rows, cols)
+        np.testing.assert_array_equal(d_y.to_numpy((batch, rows), np.float32), a)

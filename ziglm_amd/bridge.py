@@ -13,6 +13,7 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("HIP_BRIDGE_LIB") or os.path.join(PKG, "libhip_bridge.so")
 
 F32, F16, Q4_0, Q8_0, Q4_K, Q6_K, BF16 = 0, 1, 2, 8, 12, 14, 30
+F32_TERMS = 256  # f32 activations as three bf16 term planes (hip_split_terms)
 OK, EINVAL, EUNSUPPORTED, ESCRATCH = 0, -1, -2, -3
 
 _v = ctypes.c_void_p
@@ -115,6 +116,8 @@ SIGNATURES = {
     "hip_gemm_q8_0": (None, [_v, _v, _v, _i, _i, _i, _v]),
     "hip_gemm_f16": (None, [_v, _v, _v, _i, _i, _i, _v]),
     "hip_gemm": (None, [_i, _v, _v, _v, _i, _i, _i, _v]),
+    "hip_gemm_ex": (None, [_i, _v, _v, _i, _v, _i, _v, _i, _i, _i, _v]),
+    "hip_split_terms": (None, [_v, _v, _i64, _v]),
     "hip_argmax": (None, [_v, _i, _v, _v]),
     # decode attention (cuda_bridge.h:115-168)
     "hip_attention_forward": (None, [_v, _v, _v, _v, _i, _i, _i, _i, _i, _i, _i, _f, _f, _i, _v]),

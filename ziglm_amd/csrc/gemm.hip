@@ -1,14 +1,19 @@
 // Prefill-sized GEMM on the matrix cores (gfx950 MFMA): Y[b][r] = sum_c W[r][c] * X[b][c] for
-// Q4_0, Q8_0, F16, BF16 and F32 weights and f32 activations (replaces cuda_bridge.cu:1179-1445,
-// k_gemm_q4_0 / k_gemm_q8_0 / k_gemm_f16, used by ziglm's batched prefill at
-// cuda_model.zig:1264-1383), with ziglm's CPU arithmetic (math.zig:440-616): weights dequantised
-// exactly, activations kept in f32, f32 sums.
+// Q4_0, Q8_0, F16, BF16 and F32 weights and f32 or bf16 activations (replaces
+// cuda_bridge.cu:1179-1445, k_gemm_q4_0 / k_gemm_q8_0 / k_gemm_f16, used by ziglm's batched
+// prefill at cuda_model.zig:1264-1383), with ziglm's CPU arithmetic (math.zig:440-616): weights
+// dequantised exactly, activations kept in full, f32 sums. Outputs are f32 or bf16, and the
+// gate.up pair of a GeGLU FFN runs as one launch that writes gelu(gate) * up (the reference's
+// two prefill GEMMs and k_geglu, cuda_model.zig:1372-1387, cuda_bridge.cu:2247-2269): the
+// workgroup's W tile holds its output rows of both matrices, the up half's accumulators pass
+// to the gate half's waves through LDS, and the gate and up outputs never reach HBM.
 //
 // Exact operands on a bf16 matrix core. The MFMA multiplies bf16 operands exactly into f32
 // accumulators, so every operand is written as a short sum of bf16 terms that is exact or
 // nearly so:
 //   x (f32) = h + m + l, h = bf16(x), m = bf16(x - h), l = bf16(x - h - m): the three terms
-//     carry x's 24 significant bits (the remainder is below 2^-24 |x|);
+//     carry x's 24 significant bits (the remainder is below 2^-24 |x|); bf16 activations are
+//     one exact term (a third of the MFMAs and no split);
 //   Q4_0 / Q8_0 quants (integers -8..7 / -127..127) are exact in bf16; the block's f16 scale d
 //     multiplies the block's f32 partial sum, sum_k q_k x_k, afterwards (the CPU's
 //     (q * d) * x products are all exact-integer-times-f16 values, so applying d after the sum
@@ -25,15 +30,16 @@
 // (tokens on the A side, so a lane's accumulators are one weight row: the block scale is one
 // value per lane and tile, and stores of 32 lanes are 128 contiguous bytes of a token's output
 // row). The K loop takes one 32-column block per step, software-pipelined: the LDS holds block
-// k as bf16 terms (rows padded to 80 bytes against bank conflicts) while registers hold block
-// k + 1's raw X (f32) and W; each wave reads all of block k's MFMA operands into registers, one
-// barrier frees the LDS, and block k's MFMAs then run from registers while the same waves
-// convert block k + 1 into the LDS and issue block k + 2's global loads, so the matrix cores
-// work during the conversion rather than after it. Loads take clamped (always valid) addresses
-// and select zeros afterwards, so the loop body has no branches and the compiler interleaves
-// the MFMAs with the conversion. Per 32-column block a 128 x 128 workgroup moves ~97 KB
-// through the LDS (80 KB of operand reads), about as many cycles at 128 bytes per clock as its
-// MFMAs take: LDS bandwidth bounds the kernel with the matrix cores.
+// k as bf16 terms (rows padded to 80 bytes against bank conflicts; a block scale sits in its
+// row's padding) while registers hold block k + 1's raw X and W, and block k's MFMAs run while
+// the same waves convert block k + 1 into the LDS and issue block k + 2's global loads, so the
+// matrix cores work during the conversion rather than after it. Where two operand buffers fit
+// two workgroups per CU (f32 or bf16 activations with one weight term: 80 KB) block k + 1 goes
+// to the other buffer and a step takes one barrier; otherwise every wave first reads all of
+// block k's operands into registers and a barrier frees the buffer. Activations load through a
+// range-checked resource (tokens past the batch read zeros) and weights from clamped rows with
+// zeros selected afterwards, so the loop body has no branches and the compiler interleaves the
+// MFMAs with the conversion.
 #include "zl_common.h"
 #include "zl_host.h"
 
@@ -46,6 +52,11 @@ constexpr int kGemmThreads = 256;
 constexpr int kKB = 32;       // columns per K step (one Q4_0 / Q8_0 block)
 constexpr int kLdsRow = 40;   // bf16 per LDS row: 32 + 8 padding (80 bytes)
 
+// Weight terms (bf16 planes) per type: Q4_0 / Q8_0 quants are exact in bf16 and their block
+// scale multiplies each 32-column partial sum; BF16 weights are exact; F16 weights are two
+// exact terms, F32 three. (Q4_0 products (u - 8) * d are also exact in two bf16 terms, which
+// saves the per-block scale products at twice the MFMAs: measured slower, with f32
+// activations 333 -> 438 us and with bf16 ones 191 -> 213 us for 10240 x 2560 x 2048.)
 template <int QT>
 constexpr int w_terms() {
     return QT == HIP_BRIDGE_F16 ? 2 : QT == HIP_BRIDGE_F32 ? 3 : 1;
@@ -81,8 +92,9 @@ __device__ __forceinline__ void split2(float x0, float x1, uint32_t* t) {
 
 struct GemmArgs {
     const unsigned char* w;
-    const float* x;
-    float* y;
+    const unsigned char* wu;  // GeGLU: the up matrix (same type and shape as w)
+    const void* x;            // f32 or bf16 [batch][cols]
+    void* y;                  // f32 or bf16 [batch][rows]
     int64_t row_bytes;
     int rows, cols, batch;
 };
@@ -150,28 +162,30 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }
 
-// Convert the thread's half row into bf16 terms: sw[t][row][...] (and the scale into sd[row]).
+// Convert the thread's half row into bf16 terms: sw[t][row][...]; a block scale goes into the
+// padding of the row's first plane (bf16 slots 32, 33: kScaleSlot).
+constexpr int kScaleSlot = 32;
 template <int QT>
-__device__ __forceinline__ void store_w(const WRaw<QT>& r, int h, uint16_t* sw, int plane, int row, float* sd) {
+__device__ __forceinline__ void store_w(const WRaw<QT>& r, int h, uint16_t* sw, int plane, int row) {
     uint16_t* dst = sw + row * kLdsRow;
     if constexpr (QT == HIP_BRIDGE_Q4_0) {
-        sd[row] = f16_bits_to_f32(r.d);  // both halves store the same value
-        // byte j: low nibble = element j, high nibble = element j + 16 (value - 8)
+        *reinterpret_cast<float*>(dst + kScaleSlot) = f16_bits_to_f32(r.d);  // both halves store it
+        // byte j: low nibble = element j, high nibble = element j + 16 (value u - 8, exact)
         uint32_t lo[4], hi[4];
         const uint32_t q[2] = {r.q0, r.q1};
 #pragma unroll
         for (int w = 0; w < 2; ++w) {
+            const uint32_t lo4 = q[w] & 0x0f0f0f0fu, hi4 = (q[w] >> 4) & 0x0f0f0f0fu;
 #pragma unroll
             for (int b = 0; b < 4; b += 2) {
-                const uint32_t b0 = (q[w] >> (8 * b)) & 0xffu, b1 = (q[w] >> (8 * b + 8)) & 0xffu;
-                lo[w * 2 + b / 2] = pack_bf16x2((float)(int)(b0 & 15u) - 8.0f, (float)(int)(b1 & 15u) - 8.0f);
-                hi[w * 2 + b / 2] = pack_bf16x2((float)(int)(b0 >> 4) - 8.0f, (float)(int)(b1 >> 4) - 8.0f);
+                lo[w * 2 + b / 2] = pack_bf16x2((float)((lo4 >> (8 * b)) & 0xffu) - 8.0f, (float)((lo4 >> (8 * b + 8)) & 0xffu) - 8.0f);
+                hi[w * 2 + b / 2] = pack_bf16x2((float)((hi4 >> (8 * b)) & 0xffu) - 8.0f, (float)((hi4 >> (8 * b + 8)) & 0xffu) - 8.0f);
             }
         }
         *reinterpret_cast<u32x4*>(dst + 8 * h) = u32x4{lo[0], lo[1], lo[2], lo[3]};
         *reinterpret_cast<u32x4*>(dst + 16 + 8 * h) = u32x4{hi[0], hi[1], hi[2], hi[3]};
     } else if constexpr (QT == HIP_BRIDGE_Q8_0) {
-        sd[row] = f16_bits_to_f32(r.d);  // both halves store the same value
+        *reinterpret_cast<float*>(dst + kScaleSlot) = f16_bits_to_f32(r.d);  // both halves store it
         uint32_t p[8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -222,88 +236,164 @@ __device__ __forceinline__ void store_w(const WRaw<QT>& r, int h, uint16_t* sw, 
     }
 }
 
-// The (x term, w term) products accumulated, largest first: down to relative size 2^-16.
-template <int NW>
+// The (x term, w term) products accumulated, largest first: down to relative size 2^-16
+// (x in XT terms: 3 for f32 activations, 1 for bf16 ones, which are exact).
+template <int XT, int NW>
 struct TermPairs;
 template <>
-struct TermPairs<1> {
+struct TermPairs<3, 1> {
     static constexpr int n = 3;
     static constexpr int xt[3] = {0, 1, 2}, wt[3] = {0, 0, 0};
 };
 template <>
-struct TermPairs<2> {
+struct TermPairs<3, 2> {
     static constexpr int n = 5;
     static constexpr int xt[5] = {0, 1, 0, 2, 1}, wt[5] = {0, 0, 1, 0, 1};
 };
 template <>
-struct TermPairs<3> {
+struct TermPairs<3, 3> {
     static constexpr int n = 6;
     static constexpr int xt[6] = {0, 1, 0, 2, 1, 0}, wt[6] = {0, 0, 1, 0, 1, 2};
 };
+template <int NW>
+struct TermPairs<1, NW> {
+    static constexpr int n = NW;
+    static constexpr int xt[3] = {0, 0, 0}, wt[3] = {0, 1, 2};
+};
 
-template <int QT, int WT, int WR>
-__global__ __launch_bounds__(kGemmThreads, 2) void k_gemm_mfma(GemmArgs a) {
+// Workgroup order. Workgroups are dispatched to the 8 XCDs in turn (linear id i on XCD i % 8),
+// and each XCD has its own L2. With ZL_GEMM_XCD the linear id is renumbered so that XCD k
+// takes the k-th eighth of the tiles in row-fastest order (the workgroups of one XCD then
+// share their token tile's activations in its L2). Measured neutral (within 2% either way
+// over the prefill products: the kernel is bound by its instruction issue, not by operand
+// fetches), so off by default.
+#ifndef ZL_GEMM_XCD
+#define ZL_GEMM_XCD 0
+#endif
+// Two operand buffers with f32 activations too (there the block-partial and total accumulators
+// leave too few registers and the loop spills a few).
+#ifndef ZL_GEMM_DB_F32X
+#define ZL_GEMM_DB_F32X 0
+#endif
+
+// XK: activation form (X_F32: f32, split into three terms while staging; X_BF16: bf16, one
+// term; X_TERMS: three bf16 planes split beforehand, staged as they are). GE: gate.up GeGLU
+// pairs (the W tile's first
+// half holds gate rows, its second half the same rows of the up matrix; out = gelu(g) * u).
+// YB: bf16 output (else f32).
+enum XKind { X_F32 = 0, X_BF16 = 1, X_TERMS = 2 };
+
+// Workgroups per CU the launch asks registers for: three (170 VGPRs a lane) for bf16
+// activations when the LDS holds three, so a third wave per SIMD has MFMAs ready while the
+// others read operands or wait at a barrier; two otherwise (the three-term activations' loop
+// needs more registers: held to 170 it spills).
+template <int QT, int XK, int WT, int WR>
+constexpr int gemm_wgs_per_cu() {
+    constexpr int bt = 64 * WT, br = 64 * WR;
+    constexpr int oper = (bt + w_terms<QT>() * br) * kLdsRow * 2;  // bf16 activations: one term
+    return XK == X_BF16 && 2 * oper * 3 <= 160 * 1024 ? 3 : 2;
+}
+
+template <int QT, int XK, int WT, int WR, bool GE, bool YB>
+__global__ __launch_bounds__(kGemmThreads, (gemm_wgs_per_cu<QT, XK, WT, WR>())) void k_gemm_mfma(GemmArgs a) {
+    constexpr int XT = XK == X_BF16 ? 1 : 3;  // activation terms
     constexpr int NW = w_terms<QT>();
     constexpr bool SCALED = w_scaled<QT>();
     constexpr int BT = 2 * 32 * WT;  // tokens per workgroup
-    constexpr int BR = 2 * 32 * WR;  // rows per workgroup
+    constexpr int BR = 2 * 32 * WR;  // W rows per workgroup (GE: BR / 2 gate + BR / 2 up rows)
+    constexpr int OR = GE ? BR / 2 : BR;  // output rows per workgroup
     constexpr int XPLANE = BT * kLdsRow, WPLANE = BR * kLdsRow;
-    __shared__ __attribute__((aligned(16))) uint16_t sx[3 * XPLANE];
-    __shared__ __attribute__((aligned(16))) uint16_t sw[NW * WPLANE];
-    __shared__ float sd[SCALED ? BR : 1];
+    constexpr int OPER_BYTES = (XT * XPLANE + NW * WPLANE) * 2;
+    // Two operand buffers (block kb read while block kb + 1 is written: one barrier per step)
+    // when they fit two workgroups per CU in the 160 KB of LDS; else one.
+    constexpr bool DB = 2 * OPER_BYTES <= 80 * 1024 && (XK != X_F32 || ZL_GEMM_DB_F32X);
+    constexpr int NBUF = DB ? 2 : 1;
+    constexpr int XCH_BYTES = GE ? 2 * WT * WR * 16 * kWave * 4 : 0;  // up accumulators, two waves
+    __shared__ __attribute__((aligned(16)))
+    unsigned char s_raw[NBUF * OPER_BYTES > XCH_BYTES ? NBUF * OPER_BYTES : XCH_BYTES];
+    auto sx_of = [&](int b) { return reinterpret_cast<uint16_t*>(s_raw + b * OPER_BYTES); };
+    auto sw_of = [&](int b) { return reinterpret_cast<uint16_t*>(s_raw + b * OPER_BYTES) + XT * XPLANE; };
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
-    const int r_base = blockIdx.x * BR, b_base = blockIdx.y * BT;
+    int tile = blockIdx.x;
+    const int gx = (a.rows + OR - 1) / OR, nwg = (int)gridDim.x;
+    if (ZL_GEMM_XCD && nwg % 8 == 0) tile = (tile % 8) * (nwg / 8) + tile / 8;
+    const int r_base = (tile % gx) * OR, b_base = (tile / gx) * BT;
     const int nkb = a.cols / kKB;
 
-    // X staging: chunk c = tid + 256 i (i < BT * 8 / 256) is token c / 8, columns 4 (c % 8) ...
-    constexpr int XCH = BT * 8 / kGemmThreads;
-    f32x4 xr[XCH];
-    auto load_x = [&](int kb) {  // kb < nkb; tokens past the batch read the last token, then zeros
+    // X staging. f32 x: chunk c = tid + 256 i is token c / 8, columns 4 (c % 8) .. (four
+    // floats); bf16 x: token c / 4, columns 8 (c % 4) .. (eight bf16); term planes: chunk c of
+    // plane c / (4 BT), as bf16 x within the plane. Loads through range-checked resources over
+    // the workgroup's tokens: tokens past the batch read zeros.
+    constexpr int XE = XK == X_F32 ? 4 : 8;          // elements per 16-byte chunk
+    constexpr int XCPT = kKB / XE;                  // chunks per token per block (per plane)
+    constexpr int XPL = XK == X_TERMS ? 3 : 1;      // planes loaded
+    constexpr int XCH = XPL * BT * XCPT / kGemmThreads;
+    const int xes = XK == X_F32 ? 4 : 2;
+    const int64_t tok_left = (int64_t)a.batch - b_base;
+    const int64_t xbytes = (tok_left < BT ? tok_left : BT) * (int64_t)a.cols * xes;
+    const uint32_t xrange = (uint32_t)(xbytes < 0xffffffffLL ? xbytes : 0xffffffffLL);
+    const int64_t plane_bytes = (int64_t)a.batch * a.cols * xes;
+    __amdgpu_buffer_rsrc_t rsx[XPL];
+#pragma unroll
+    for (int u = 0; u < XPL; ++u)
+        rsx[u] = buf_rsrc((const unsigned char*)a.x + u * plane_bytes + (int64_t)b_base * a.cols * xes, xrange);
+    u32x4 xr[XCH];
+    auto load_x = [&](int kb) {
 #pragma unroll
         for (int i = 0; i < XCH; ++i) {
-            const int c = tid + kGemmThreads * i, tok = b_base + c / 8;
-            const f32x4 v = ldf4(a.x + (int64_t)min(tok, a.batch - 1) * a.cols + kb * kKB + 4 * (c % 8));
-            xr[i] = tok < a.batch ? v : f32x4{0, 0, 0, 0};
+            const int c = tid + kGemmThreads * i, pl = c / (BT * XCPT), cc = c % (BT * XCPT), tok = cc / XCPT;
+            const uint32_t off = (uint32_t)(((int64_t)tok * a.cols + kb * kKB + XE * (cc % XCPT)) * xes);
+            xr[i] = bldp<POL_DEFAULT>(rsx[pl], off);
         }
     };
-    auto store_x = [&]() {
+    auto store_x = [&](int buf) {
+        uint16_t* const sx = sx_of(buf);
 #pragma unroll
         for (int i = 0; i < XCH; ++i) {
-            const int c = tid + kGemmThreads * i, tok = c / 8, k = 4 * (c % 8);
-            uint32_t t0[3], t1[3];
-            split3(xr[i].x, xr[i].y, t0);
-            split3(xr[i].z, xr[i].w, t1);
+            const int c = tid + kGemmThreads * i, pl = c / (BT * XCPT), cc = c % (BT * XCPT);
+            const int tok = cc / XCPT, k = XE * (cc % XCPT);
+            if constexpr (XK == X_F32) {
+                uint32_t t0[3], t1[3];
+                split3(__uint_as_float(xr[i].x), __uint_as_float(xr[i].y), t0);
+                split3(__uint_as_float(xr[i].z), __uint_as_float(xr[i].w), t1);
 #pragma unroll
-            for (int u = 0; u < 3; ++u)
-                *reinterpret_cast<u32x2*>(sx + u * XPLANE + tok * kLdsRow + k) = u32x2{t0[u], t1[u]};
+                for (int u = 0; u < 3; ++u)
+                    *reinterpret_cast<u32x2*>(sx + u * XPLANE + tok * kLdsRow + k) = u32x2{t0[u], t1[u]};
+            } else {
+                *reinterpret_cast<u32x4*>(sx + pl * XPLANE + tok * kLdsRow + k) = xr[i];
+            }
         }
     };
     // W staging: half rows (BR rows x 2 halves over 256 threads: BR / 128 passes, or the
-    // first 2 BR threads when BR < 128)
+    // first 2 BR threads when BR < 128). GE: tile rows [0, OR) are gate rows, [OR, BR) the
+    // same rows of the up matrix.
     constexpr int WPASS = BR * 2 >= kGemmThreads ? BR * 2 / kGemmThreads : 1;
+    constexpr int64_t blk_bytes = QT == HIP_BRIDGE_Q4_0 ? 18 : QT == HIP_BRIDGE_Q8_0 ? 34 : QT == HIP_BRIDGE_F32 ? 128 : 64;
     WRaw<QT> wr[WPASS];
     auto load_wt = [&](int kb) {
 #pragma unroll
         for (int i = 0; i < WPASS; ++i) {
             const int hr = tid + kGemmThreads * i, row = hr >> 1, h = hr & 1;
-            const int gr = r_base + row;
+            const bool up = GE && row >= OR;
+            const int gr = r_base + (up ? row - OR : row);
             const bool ok = hr < 2 * BR && gr < a.rows;
-            const int64_t blk_bytes = QT == HIP_BRIDGE_Q4_0 ? 18 : QT == HIP_BRIDGE_Q8_0 ? 34 : QT == HIP_BRIDGE_F32 ? 128 : 64;
-            load_w<QT>(a.w + (int64_t)min(gr, a.rows - 1) * a.row_bytes + (int64_t)kb * blk_bytes, h, ok, wr[i]);
+            const unsigned char* wm = up ? a.wu : a.w;
+            load_w<QT>(wm + (int64_t)min(gr, a.rows - 1) * a.row_bytes + (int64_t)kb * blk_bytes, h, ok, wr[i]);
         }
     };
-    auto store_wt = [&]() {
+    auto store_wt = [&](int buf) {
+        uint16_t* const swb = sw_of(buf);
 #pragma unroll
         for (int i = 0; i < WPASS; ++i) {
             const int hr = tid + kGemmThreads * i;
-            if (2 * BR >= kGemmThreads || hr < 2 * BR) store_w<QT>(wr[i], hr & 1, sw, WPLANE, hr >> 1, sd);
+            if (2 * BR >= kGemmThreads || hr < 2 * BR) store_w<QT>(wr[i], hr & 1, swb, WPLANE, hr >> 1);
         }
     };
 
     const int wt0 = (wave >> 1) * 32 * WT;  // the wave's first token (within the workgroup)
-    const int wr0 = (wave & 1) * 32 * WR;   // the wave's first row
+    const int wr0 = (wave & 1) * 32 * WR;   // the wave's first W row (GE: wave & 1 = up)
     f32x16 acc[WT][WR];
     f32x16 part[WT][WR];
 #pragma unroll
@@ -311,50 +401,41 @@ __global__ __launch_bounds__(kGemmThreads, 2) void k_gemm_mfma(GemmArgs a) {
 #pragma unroll
         for (int j = 0; j < WR; ++j) acc[i][j] = f32x16{};
 
-    // Pipeline: LDS holds block kb while the raw registers hold block kb + 1. Each wave reads
-    // all of block kb's MFMA operands (and scales) from LDS into registers, one barrier frees
-    // the LDS, and then block kb's MFMAs run from registers while the same waves convert block
-    // kb + 1 into the LDS (and issue block kb + 2's loads): the MFMAs overlap the conversion's
-    // VALU and LDS work instead of following it.
-    constexpr int NP = TermPairs<NW>::n;
-    load_x(0);
-    load_wt(0);
-    store_x();
-    store_wt();
-    __syncthreads();
-    load_x(min(1, nkb - 1));
-    load_wt(min(1, nkb - 1));
-    for (int kb = 0; kb < nkb; ++kb) {
-        bf16x8 xa[2][WT][3], wb[2][WR][NW];
+    using TP = TermPairs<XT, NW>;
+    constexpr int NP = TP::n;
+    // One K step: block kb's operands from LDS buffer `buf` into registers, its MFMAs (into the
+    // block partial when SCALED), then `convert` (block kb + 1 into the LDS and the loads of
+    // kb + 2), then the block scale products.
+    auto step = [&](int buf, bool single, auto convert) {
+        const uint16_t* const sx = sx_of(buf);
+        const uint16_t* const sw = sw_of(buf);
+        // with one buffer every wave holds all of block kb's operands before the barrier;
+        // with two, each K = 16 half's operands are read just before its MFMAs (half the
+        // registers)
+        constexpr int KH = DB ? 1 : 2;
+        bf16x8 xa[KH][WT][XT], wb[KH][WR][NW];
         float dv[WR];
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {  // two K = 16 halves of the block
+        auto read_ops = [&](int ks, int slot) {
             const int ko = 16 * ks + 8 * (lane >> 5);
 #pragma unroll
             for (int i = 0; i < WT; ++i)
 #pragma unroll
-                for (int u = 0; u < 3; ++u)
-                    xa[ks][i][u] = *reinterpret_cast<const bf16x8*>(sx + u * XPLANE + (wt0 + 32 * i + (lane & 31)) * kLdsRow + ko);
+                for (int u = 0; u < XT; ++u)
+                    xa[slot][i][u] = *reinterpret_cast<const bf16x8*>(sx + u * XPLANE + (wt0 + 32 * i + (lane & 31)) * kLdsRow + ko);
 #pragma unroll
             for (int j = 0; j < WR; ++j)
 #pragma unroll
                 for (int u = 0; u < NW; ++u)
-                    wb[ks][j][u] = *reinterpret_cast<const bf16x8*>(sw + u * WPLANE + (wr0 + 32 * j + (lane & 31)) * kLdsRow + ko);
-        }
-        if constexpr (SCALED) {
-#pragma unroll
-            for (int j = 0; j < WR; ++j) dv[j] = sd[wr0 + 32 * j + (lane & 31)];
-        }
-        __syncthreads();  // every wave holds block kb's operands: the LDS is free
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
+                    wb[slot][j][u] = *reinterpret_cast<const bf16x8*>(sw + u * WPLANE + (wr0 + 32 * j + (lane & 31)) * kLdsRow + ko);
+        };
+        auto mfmas = [&](int ks, int slot) {
 #pragma unroll
             for (int i = 0; i < WT; ++i)
 #pragma unroll
                 for (int j = 0; j < WR; ++j)
 #pragma unroll
                     for (int p = 0; p < NP; ++p) {
-                        const bf16x8 A = xa[ks][i][TermPairs<NW>::xt[p]], Bv = wb[ks][j][TermPairs<NW>::wt[p]];
+                        const bf16x8 A = xa[slot][i][TP::xt[p]], Bv = wb[slot][j][TP::wt[p]];
                         if constexpr (SCALED) {
                             part[i][j] = (ks == 0 && p == 0)
                                              ? __builtin_amdgcn_mfma_f32_32x32x16_bf16(A, Bv, f32x16{}, 0, 0, 0)
@@ -363,12 +444,26 @@ __global__ __launch_bounds__(kGemmThreads, 2) void k_gemm_mfma(GemmArgs a) {
                             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A, Bv, acc[i][j], 0, 0, 0);
                         }
                     }
-        // block kb + 1 into the LDS (after the last block: a copy nobody reads), block kb + 2's
-        // loads in flight (past the end: the last block again, unused)
-        store_x();
-        store_wt();
-        load_x(min(kb + 2, nkb - 1));
-        load_wt(min(kb + 2, nkb - 1));
+        };
+        if constexpr (SCALED) {
+#pragma unroll
+            for (int j = 0; j < WR; ++j)
+                dv[j] = *reinterpret_cast<const float*>(sw + (wr0 + 32 * j + (lane & 31)) * kLdsRow + kScaleSlot);
+        }
+        if constexpr (DB) {
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                read_ops(ks, 0);
+                mfmas(ks, 0);
+            }
+        } else {
+            read_ops(0, 0);
+            read_ops(1, 1);
+            if (single) __syncthreads();
+            mfmas(0, 0);
+            mfmas(1, 1);
+        }
+        convert();
         if constexpr (SCALED) {
 #pragma unroll
             for (int j = 0; j < WR; ++j)
@@ -377,59 +472,166 @@ __global__ __launch_bounds__(kGemmThreads, 2) void k_gemm_mfma(GemmArgs a) {
 #pragma unroll
                     for (int r = 0; r < 16; ++r) acc[i][j][r] = fmaf(dv[j], part[i][j][r], acc[i][j][r]);
         }
-        __syncthreads();  // block kb + 1 is in the LDS
+    };
+
+    // Pipeline. The raw registers hold block kb + 1 while the MFMAs of block kb run; they are
+    // converted into the LDS (the other buffer with DB, else the same one once every wave has
+    // read block kb's operands) and block kb + 2's loads are issued, so the matrix cores work
+    // during the conversion rather than after it. Past the end: the last block again, unused.
+    load_x(0);
+    load_wt(0);
+    store_x(0);
+    store_wt(0);
+    __syncthreads();
+    load_x(min(1, nkb - 1));
+    load_wt(min(1, nkb - 1));
+    for (int kb = 0; kb < nkb; ++kb) {
+        const int cur = DB ? (kb & 1) : 0, nxt = DB ? (cur ^ 1) : 0;
+        step(cur, !DB, [&]() {
+            store_x(nxt);
+            store_wt(nxt);
+            load_x(min(kb + 2, nkb - 1));
+            load_wt(min(kb + 2, nkb - 1));
+        });
+        __syncthreads();  // block kb + 1 is in the LDS (DB: and block kb's buffer is free)
     }
 
-    // Epilogue: lane (l, r) of tile (i, j) holds token 8 (r / 4) + 4 (l / 32) + r % 4 and row l % 32.
+    // Epilogue: lane (l, r) of tile (i, j) holds token 8 (r / 4) + 4 (l / 32) + r % 4 and row
+    // l % 32. GE: the up waves pass their accumulators through the (now free) LDS to the gate
+    // waves of the same tokens, which write gelu(g) * u.
+    if constexpr (GE) {
+        float* const xch = reinterpret_cast<float*>(s_raw) + (wave >> 1) * (WT * WR * 16 * kWave);
+        if (wave & 1) {
+#pragma unroll
+            for (int i = 0; i < WT; ++i)
+#pragma unroll
+                for (int j = 0; j < WR; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) xch[((i * WR + j) * 16 + r) * kWave + lane] = acc[i][j][r];
+        }
+        __syncthreads();
+        if (wave & 1) return;
+#pragma unroll
+        for (int i = 0; i < WT; ++i)
+#pragma unroll
+            for (int j = 0; j < WR; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    acc[i][j][r] = gelu_fast(acc[i][j][r]) * xch[((i * WR + j) * 16 + r) * kWave + lane];
+    }
 #pragma unroll
     for (int i = 0; i < WT; ++i)
 #pragma unroll
         for (int j = 0; j < WR; ++j) {
-            const int row = r_base + wr0 + 32 * j + (lane & 31);
+            const int row = r_base + (GE ? 0 : wr0) + 32 * j + (lane & 31);
             if (row >= a.rows) continue;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int tok = b_base + wt0 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (tok < a.batch) a.y[(int64_t)tok * a.rows + row] = acc[i][j][r];
+                if (tok < a.batch) {
+                    if constexpr (YB)
+                        ((uint16_t*)a.y)[(int64_t)tok * a.rows + row] = (uint16_t)(pack_bf16x2(acc[i][j][r], 0.0f) & 0xffffu);
+                    else
+                        ((float*)a.y)[(int64_t)tok * a.rows + row] = acc[i][j][r];
+                }
             }
         }
 }
 
-// Workgroup tile: the largest of 128 x 128, 64 x 128 and 64 x 64 (tokens x rows) that still
+// Workgroup tile: the largest of 128 x 128, 64 x 128 and 64 x 64 (tokens x W rows) that still
 // gives at least two workgroups per CU (bigger tiles convert each operand for more MFMAs;
 // smaller ones fill the chip at small batches).
-template <int QT>
+template <int QT, int XK, bool GE, bool YB>
 static void launch_qt(const GemmArgs& a, hipStream_t s) {
     constexpr int64_t kFill = 512;
-    auto wgs = [&](int bt, int br) { return cdiv(a.rows, br) * cdiv(a.batch, bt); };
+    auto wgs = [&](int bt, int br) { return cdiv(a.rows, GE ? br / 2 : br) * cdiv(a.batch, bt); };
     if (wgs(128, 128) >= kFill) {
-        k_gemm_mfma<QT, 2, 2><<<dim3((unsigned)cdiv(a.rows, 128), (unsigned)cdiv(a.batch, 128)), kGemmThreads, 0, s>>>(a);
+        k_gemm_mfma<QT, XK, 2, 2, GE, YB><<<(unsigned)wgs(128, 128), kGemmThreads, 0, s>>>(a);
     } else if (wgs(64, 128) >= kFill) {
-        k_gemm_mfma<QT, 1, 2><<<dim3((unsigned)cdiv(a.rows, 128), (unsigned)cdiv(a.batch, 64)), kGemmThreads, 0, s>>>(a);
+        k_gemm_mfma<QT, XK, 1, 2, GE, YB><<<(unsigned)wgs(64, 128), kGemmThreads, 0, s>>>(a);
     } else {
-        k_gemm_mfma<QT, 1, 1><<<dim3((unsigned)cdiv(a.rows, 64), (unsigned)cdiv(a.batch, 64)), kGemmThreads, 0, s>>>(a);
+        k_gemm_mfma<QT, XK, 1, 1, GE, YB><<<(unsigned)wgs(64, 64), kGemmThreads, 0, s>>>(a);
     }
+}
+
+template <int QT, int XK>
+static void launch_qx(const GemmArgs& a, bool ge, bool y_bf16, hipStream_t s) {
+    if (ge) y_bf16 ? launch_qt<QT, XK, true, true>(a, s) : launch_qt<QT, XK, true, false>(a, s);
+    else y_bf16 ? launch_qt<QT, XK, false, true>(a, s) : launch_qt<QT, XK, false, false>(a, s);
+}
+template <int QT>
+static void launch_q(const GemmArgs& a, int xk, bool ge, bool y_bf16, hipStream_t s) {
+    if (xk == X_F32) launch_qx<QT, X_F32>(a, ge, y_bf16, s);
+    else if (xk == X_BF16) launch_qx<QT, X_BF16>(a, ge, y_bf16, s);
+    else launch_qx<QT, X_TERMS>(a, ge, y_bf16, s);
+}
+
+// 0 = launched; otherwise why not (the caller decides between a fallback and an error).
+int launch_gemm_mfma_ex(int qtype, const void* w, const void* wu, int64_t row_bytes, int x_dtype, const void* x,
+                        int y_dtype, void* y, int rows, int cols, int batch, hipStream_t s) {
+    const bool types = qtype == HIP_BRIDGE_Q4_0 || qtype == HIP_BRIDGE_Q8_0 || qtype == HIP_BRIDGE_F16 ||
+                       qtype == HIP_BRIDGE_BF16 || qtype == HIP_BRIDGE_F32;
+    if (!types || (x_dtype != HIP_BRIDGE_F32 && x_dtype != HIP_BRIDGE_BF16 && x_dtype != HIP_BRIDGE_F32_TERMS) ||
+        (y_dtype != HIP_BRIDGE_F32 && y_dtype != HIP_BRIDGE_BF16))
+        return HIP_BRIDGE_EUNSUPPORTED;
+    // dense rows must be 16-byte aligned for the 128-bit loads; block rows need 2 bytes
+    const bool dense = qtype == HIP_BRIDGE_F16 || qtype == HIP_BRIDGE_BF16 || qtype == HIP_BRIDGE_F32;
+    auto w_ok = [&](const void* p) {
+        const uintptr_t wa = reinterpret_cast<uintptr_t>(p);
+        return dense ? (wa % 16 == 0 && row_bytes % 16 == 0) : (wa % 2 == 0);
+    };
+    if (cols % kKB != 0 || !aligned16(x) || !w_ok(w) || (wu && !w_ok(wu))) return HIP_BRIDGE_EUNSUPPORTED;
+    // 32-bit byte offsets within a token tile's activations (per plane)
+    if ((int64_t)128 * cols * (x_dtype == HIP_BRIDGE_F32 ? 4 : 2) > 0xffffffffLL) return HIP_BRIDGE_EUNSUPPORTED;
+    const GemmArgs a{(const unsigned char*)w, (const unsigned char*)wu, x, y, row_bytes, rows, cols, batch};
+    const int xk = x_dtype == HIP_BRIDGE_BF16 ? X_BF16 : x_dtype == HIP_BRIDGE_F32_TERMS ? X_TERMS : X_F32;
+    const bool ge = wu != nullptr, yb = y_dtype == HIP_BRIDGE_BF16;
+    switch (qtype) {
+        case HIP_BRIDGE_Q4_0: launch_q<HIP_BRIDGE_Q4_0>(a, xk, ge, yb, s); break;
+        case HIP_BRIDGE_Q8_0: launch_q<HIP_BRIDGE_Q8_0>(a, xk, ge, yb, s); break;
+        case HIP_BRIDGE_F16: launch_q<HIP_BRIDGE_F16>(a, xk, ge, yb, s); break;
+        case HIP_BRIDGE_BF16: launch_q<HIP_BRIDGE_BF16>(a, xk, ge, yb, s); break;
+        default: launch_q<HIP_BRIDGE_F32>(a, xk, ge, yb, s); break;
+    }
+    check_launch();
+    return 0;
+}
+
+// x (f32) -> three bf16 planes h, m, l (h = bf16(x), m = bf16(x - h), l = bf16(x - h - m)):
+// the activation form the K loop stages without converting. Four elements per thread.
+__global__ __launch_bounds__(256) void k_split_terms(const float* __restrict__ x, uint16_t* __restrict__ planes,
+                                                     int64_t n) {
+    const int64_t i4 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;  // n % 4 == 0
+    if (i4 >= n) return;
+    const u32x4 v = lds16(x + i4);
+    uint32_t t0[3], t1[3];
+    split3(__uint_as_float(v.x), __uint_as_float(v.y), t0);
+    split3(__uint_as_float(v.z), __uint_as_float(v.w), t1);
+#pragma unroll
+    for (int u = 0; u < 3; ++u) *reinterpret_cast<u32x2*>(planes + u * n + i4) = u32x2{t0[u], t1[u]};
 }
 
 bool launch_gemm_mfma(int qtype, const void* w, int64_t row_bytes, const float* x, float* y, int rows, int cols,
                       int batch, hipStream_t s) {
-    const bool types = qtype == HIP_BRIDGE_Q4_0 || qtype == HIP_BRIDGE_Q8_0 || qtype == HIP_BRIDGE_F16 ||
-                       qtype == HIP_BRIDGE_BF16 || qtype == HIP_BRIDGE_F32;
-    // dense rows must be 16-byte aligned for the 128-bit loads; block rows need 2 bytes
-    const uintptr_t wa = reinterpret_cast<uintptr_t>(w);
-    const bool dense = qtype == HIP_BRIDGE_F16 || qtype == HIP_BRIDGE_BF16 || qtype == HIP_BRIDGE_F32;
-    const bool aligned = aligned16(x) && (dense ? (wa % 16 == 0 && row_bytes % 16 == 0) : (wa % 2 == 0));
-    if (!types || cols % kKB != 0 || batch < kGemmMfmaMinBatch || !aligned || !y) return false;
-    const GemmArgs a{(const unsigned char*)w, x, y, row_bytes, rows, cols, batch};
-    switch (qtype) {
-        case HIP_BRIDGE_Q4_0: launch_qt<HIP_BRIDGE_Q4_0>(a, s); break;
-        case HIP_BRIDGE_Q8_0: launch_qt<HIP_BRIDGE_Q8_0>(a, s); break;
-        case HIP_BRIDGE_F16: launch_qt<HIP_BRIDGE_F16>(a, s); break;
-        case HIP_BRIDGE_BF16: launch_qt<HIP_BRIDGE_BF16>(a, s); break;
-        default: launch_qt<HIP_BRIDGE_F32>(a, s); break;
-    }
-    check_launch();
-    return true;
+    if (batch < kGemmMfmaMinBatch || !y) return false;
+    return launch_gemm_mfma_ex(qtype, w, nullptr, row_bytes, HIP_BRIDGE_F32, x, HIP_BRIDGE_F32, y, rows, cols, batch,
+                               s) == 0;
 }
 
 }  // namespace zl
+
+using namespace zl;
+
+extern "C" void hip_split_terms(const float* x, void* planes, int64_t n, HipStream_t stream) {
+    if (n <= 0) return;
+    if (!x || !planes) {
+        set_error(HIP_BRIDGE_EINVAL);
+        return;
+    }
+    if (!aligned16(x) || (reinterpret_cast<uintptr_t>(planes) & 7u) || n % 4) {
+        set_error(HIP_BRIDGE_EUNSUPPORTED);
+        return;
+    }
+    k_split_terms<<<(unsigned)cdiv(n, 1024), 256, 0, stream_of(stream)>>>(x, (uint16_t*)planes, n);
+    check_launch();
+}

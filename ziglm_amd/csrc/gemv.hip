@@ -2123,6 +2123,24 @@ void hip_gemv(int qtype, const void* weights, const float* x, float* y, int rows
     hip_gemm(qtype, weights, x, y, 1, rows, cols, stream);
 }
 
+void hip_gemm_ex(int qtype, const void* weights, const void* up_weights, int x_dtype, const void* x,
+                 int y_dtype, void* y, int batch_size, int rows, int cols, HipStream_t stream) {
+    if (batch_size <= 0 || rows <= 0 || cols <= 0) return;
+    if (!weights || !x || !y) {
+        set_error(HIP_BRIDGE_EINVAL);
+        return;
+    }
+    if (!up_weights && x_dtype == HIP_BRIDGE_F32 && y_dtype == HIP_BRIDGE_F32) {
+        hip_gemm(qtype, weights, (const float*)x, (float*)y, batch_size, rows, cols, stream);
+        return;
+    }
+    const int64_t rb = gemv_row_bytes(qtype, cols);
+    const int rc = rb > 0 ? launch_gemm_mfma_ex(qtype, weights, up_weights, rb, x_dtype, x, y_dtype, y, rows, cols,
+                                                batch_size, stream_of(stream))
+                          : HIP_BRIDGE_EUNSUPPORTED;
+    if (rc != 0) set_error(rc);
+}
+
 void hip_gemv_q4_0(const void* weights, const float* x, float* y, int rows, int cols, HipStream_t stream) {
     hip_gemm(HIP_BRIDGE_Q4_0, weights, x, y, 1, rows, cols, stream);
 }

@@ -30,5 +30,9 @@ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 constexpr int kGemmMfmaMinBatch = 32;
 bool launch_gemm_mfma(int qtype, const void* w, int64_t row_bytes, const float* x, float* y, int rows, int cols,
                       int batch, hipStream_t s);
+// The same for any batch with f32 or bf16 activations and output and an optional up matrix
+// (y = gelu(W x) * (U x)); returns 0 when launched, else a HIP_BRIDGE_* code (nothing launched).
+int launch_gemm_mfma_ex(int qtype, const void* w, const void* wu, int64_t row_bytes, int x_dtype, const void* x,
+                        int y_dtype, void* y, int rows, int cols, int batch, hipStream_t s);
 
 }  // namespace zl

@@ -291,6 +291,17 @@ class HipDevice:
         self.b.hip_gemm(int(qtype), _ptr(d_weights), _ptr(d_x), _ptr(d_y), batch_size, rows, cols, self.stream)
         self._done("gemm")
 
+    # new: f32 / bf16 activations and output; with d_up: y = gelu(W x) * (U x)
+    def gemmEx(self, qtype, d_weights, d_up, x_dtype, d_x, y_dtype, d_y, batch_size, rows, cols):
+        self.b.hip_gemm_ex(int(qtype), _ptr(d_weights), _ptr(d_up), int(x_dtype), _ptr(d_x), int(y_dtype), _ptr(d_y),
+                           batch_size, rows, cols, self.stream)
+        self._done("gemmEx")
+
+    # new: f32 activations -> three bf16 term planes [3][n] (hip_gemm_ex's F32_TERMS input)
+    def splitTerms(self, d_x, d_planes, n):
+        self.b.hip_split_terms(_ptr(d_x), _ptr(d_planes), n, self.stream)
+        self._done("splitTerms")
+
     # -- greedy token (cuda.zig:743-750) -------------------------------------------------
     def argmax(self, d_logits, n, d_out_idx):
         self.b.hip_argmax(_ptr(d_logits), n, _ptr(d_out_idx), self.stream)

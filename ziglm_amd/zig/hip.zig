@@ -29,6 +29,8 @@ pub const HipEvent_t = ?*anyopaque;
 /// Activation / table dtypes of the new entry points (GGML type ids, hip_bridge.h).
 pub const dtype_f32: c_int = 0;
 pub const dtype_bf16: c_int = 30;
+/// f32 activations as three bf16 term planes (splitTerms), an input form of gemmEx.
+pub const dtype_f32_terms: c_int = 256;
 
 // ---------------------------------------------------------------------------------------
 // C-ABI (include/hip_bridge.h)
@@ -118,6 +120,8 @@ pub extern "c" fn hip_gemm_q4_0(weights: ?*const anyopaque, x: [*]const f32, y: 
 pub extern "c" fn hip_gemm_q8_0(weights: ?*const anyopaque, x: [*]const f32, y: [*]f32, batch_size: c_int, rows: c_int, cols: c_int, stream: HipStream_t) void;
 pub extern "c" fn hip_gemm_f16(weights: ?*const anyopaque, x: [*]const f32, y: [*]f32, batch_size: c_int, rows: c_int, cols: c_int, stream: HipStream_t) void;
 pub extern "c" fn hip_gemm(qtype: c_int, weights: ?*const anyopaque, x: [*]const f32, y: [*]f32, batch_size: c_int, rows: c_int, cols: c_int, stream: HipStream_t) void;
+pub extern "c" fn hip_split_terms(x: [*]const f32, planes: ?*anyopaque, n: i64, stream: HipStream_t) void;
+pub extern "c" fn hip_gemm_ex(qtype: c_int, weights: ?*const anyopaque, up_weights: ?*const anyopaque, x_dtype: c_int, x: ?*const anyopaque, y_dtype: c_int, y: ?*anyopaque, batch_size: c_int, rows: c_int, cols: c_int, stream: HipStream_t) void;
 
 // decode attention
 pub extern "c" fn hip_attention_forward(q: [*]const f32, k_cache: [*]const f32, v_cache: [*]const f32, out: [*]f32, donor_layer: c_int, pos: c_int, max_seq: c_int, n_heads: c_int, n_kv_heads: c_int, head_dim: c_int, max_kv_dim: c_int, attn_scale: f32, softcap: f32, sliding_window: c_int, stream: HipStream_t) void;
@@ -339,6 +343,17 @@ pub const HipDevice = struct {
 
     pub fn gemm(self: *const HipDevice, qtype: GGMLType, d_weights: ?*const anyopaque, d_x: [*]const f32, d_y: [*]f32, batch_size: usize, rows: usize, cols: usize) void {
         hip_gemm(qt(qtype), d_weights, d_x, d_y, int(batch_size), int(rows), int(cols), self.stream);
+    }
+
+    /// New: the prefill product with f32 or bf16 activations (x_dtype) and output (y_dtype:
+    /// dtype_f32 / dtype_bf16); with d_up_weights, y = gelu(W x) * (U x) (gate.up GeGLU).
+    /// New: f32 activations -> three bf16 term planes [3][n], gemmEx's dtype_f32_terms input.
+    pub fn splitTerms(self: *const HipDevice, d_x: [*]const f32, d_planes: ?*anyopaque, n: usize) void {
+        hip_split_terms(d_x, d_planes, @intCast(n), self.stream);
+    }
+
+    pub fn gemmEx(self: *const HipDevice, qtype: GGMLType, d_weights: ?*const anyopaque, d_up_weights: ?*const anyopaque, x_dtype: c_int, d_x: ?*const anyopaque, y_dtype: c_int, d_y: ?*anyopaque, batch_size: usize, rows: usize, cols: usize) void {
+        hip_gemm_ex(qt(qtype), d_weights, d_up_weights, x_dtype, d_x, y_dtype, d_y, int(batch_size), int(rows), int(cols), self.stream);
     }
 
     // ---- embeddings (cuda.zig:358-380) --------------------------------------------------
