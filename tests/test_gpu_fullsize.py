@@ -152,10 +152,10 @@ class Case:
         _close(gk.reshape(T, s.nkv, s.D), kr, pair_floor(_f(kr), s.D, 0), "K cache")
         assert_bitexact(gv, vc, "V cache")
 
-    def check_chain(self, fused):
+    def check_chain(self, fused, theta=None):
         """The 5-op chain (or the 4-op chain with the next layer's input norm) against the
         oracle's composition: every output after a residual update inherits a one-ulp
-        difference of that update, hence the floors."""
+        difference of that update, hence the floors. theta: the RoPE base the chain ran at."""
         o, s, T, h, w, eps = O.get(), self.s, self.T, self.h, self.w, self.eps
         bf = self.dtype == B.BF16
         H = s.H
@@ -182,7 +182,7 @@ class Case:
             inv = 1.0 / np.sqrt(np.mean(s3 * s3, axis=-1, keepdims=True) + float(eps))
             _close(gxb, xb3, floor * inv * np.abs(1.0 + w["pre_ffn"].astype(np.float64)), "pre-FFN norm")
         self.check_op("geglu")
-        self.check_qk(s.theta)
+        self.check_qk(theta or s.theta)
 
 
 OPS_ALL = ["input_norm", "add_rmsnorm", "qk_norm_rope_kv", "norm_add_norm", "geglu", "norm_add",
@@ -271,6 +271,15 @@ def test_c4_op_full_size(c4, op, theta):
     c4.restore()
     c4.run(op, theta)
     c4.check_op(op, theta)
+
+
+@pytest.mark.parametrize("fused,theta", [(False, 1e4), (True, 1e6)], ids=["5op-local", "4op-global"])
+def test_c4_chain_full_size(c4, fused, theta):
+    """The whole c4 chain in sequence at a local (1e4) and a global (1e6) RoPE base."""
+    c4.restore()
+    for op in (LY.CHAIN_FUSED if fused else LY.CHAIN):
+        c4.run(op, theta if op == "qk_norm_rope_kv" else None)
+    c4.check_chain(fused, theta)
 
 
 # ---------------------------------------------------------------------------------------

@@ -268,11 +268,13 @@ def test_rmsnorm_add_rmsnorm_cancellation(dev, oracle, dtype, n, rows):
 
 
 @pytest.mark.parametrize("dtype,n,rows", [(B.BF16, 2560, 4097), (B.BF16, 5376, 2049), (B.F32, 2560, 2049),
-                                          (B.BF16, 1024, 777), (B.F32, 5376, 512)])
+                                          (B.BF16, 1024, 777), (B.F32, 5376, 512), (B.BF16, 5376, 4099),
+                                          (B.F32, 2560, 4101)])
 def test_norm_modes_many_rows(dev, oracle, dtype, n, rows):
     """Prefill-sized row counts. rows * waves-per-row >= 8192 takes two rows per lane group
-    (the odd counts leave the last group's second row out of range); the last two cases
-    take one row per group."""
+    (the odd counts leave the last group's second row out of range; 5376 x 4099 bf16 and
+    2560 x 4101 f32 at four waves a row); 1024 x 777 and 5376 x 512 f32 take one row per
+    group."""
     f = O.get().bf16_to_f32
     bf = dtype == B.BF16
     gen = synth.normal_bf16 if bf else synth.normal_f32
