@@ -855,7 +855,8 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline config only")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default=None, help="run one op only (profiling): a chain op, "
-                    "gather_q8_0 / gather_q4_0 / gather_bf16 (c3), c5 (batched decode ops), gemv, gemm, decode_step, "
+                    "gather_q8_0 / gather_q4_0 / gather_bf16 (c3), c3 (all three), prefill (every chain op and the "
+                    "chain at --config), c5 (batched decode ops), gemv, gemm, decode_step, "
                     "gguf_decode, "
                     "or 'copy' = hipMemcpy device-to-device of the GeGLU output size (counter calibration)")
     ap.add_argument("--eager", action="store_true", help="with --only: launch eagerly, no graph (kernel traces)")
@@ -891,6 +892,16 @@ def main():
             return
         elif a.only == "c5":
             print(json.dumps({f"B{b_}": bench_decode(dev, b_) for b_ in (1, 8, 64, 256)}))
+            return
+        elif a.only == "c3":
+            log("c3 gather")
+            print(json.dumps(bench_gather(dev)))
+            return
+        elif a.only == "prefill":
+            thetas = (1e4, 1e6) if a.config == "c4" else None
+            r = bench_prefill(dev, shape, T, B.BF16, max(4, a.steps // 4) if a.config == "c4" else a.steps, a.warmup,
+                              thetas=thetas)
+            print(json.dumps(r))
             return
         elif a.only == "gemv":
             log("gemv (decode projections)")

@@ -24,7 +24,10 @@
 
 namespace zl {
 
-constexpr int kGatherWaves = 4;  // rows per workgroup
+#ifndef ZL_GATHER_WAVES
+#define ZL_GATHER_WAVES 4
+#endif
+constexpr int kGatherWaves = ZL_GATHER_WAVES;  // independent waves (segments) per workgroup
 
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
@@ -178,7 +181,7 @@ __device__ __forceinline__ uint32_t ld32_a2(const unsigned char* p) {
 // are dropped afterwards, so no load sits under a branch and all 2K of a lane's loads are in
 // flight before its first store.
 template <int QT, typename OutT, int K>
-__global__ __launch_bounds__(256) void k_gather_q(const unsigned char* __restrict__ table,
+__global__ __launch_bounds__(64 * kGatherWaves) void k_gather_q(const unsigned char* __restrict__ table,
                                                   const int32_t* __restrict__ ids,
                                                   OutT* __restrict__ out, int64_t n_rows,
                                                   int64_t n_tokens, int dim, float scale, int nseg,
@@ -235,7 +238,7 @@ __global__ __launch_bounds__(256) void k_gather_q(const unsigned char* __restric
 // (128-bit loads when the row is 16-byte aligned, byte loads otherwise), then decoded.
 // Segments hold whole blocks and start at multiples of 16 bytes within the row.
 template <int QT, typename OutT>
-__global__ __launch_bounds__(256) void k_gather_blocks(const unsigned char* __restrict__ table,
+__global__ __launch_bounds__(64 * kGatherWaves) void k_gather_blocks(const unsigned char* __restrict__ table,
                                                        const int32_t* __restrict__ ids,
                                                        OutT* __restrict__ out, int64_t n_rows,
                                                        int64_t n_tokens, int dim, float scale,
@@ -347,7 +350,7 @@ struct DenseIn {
 };
 
 template <int QT, typename OutT, int K>
-__global__ __launch_bounds__(256) void k_gather_dense(const unsigned char* __restrict__ table,
+__global__ __launch_bounds__(64 * kGatherWaves) void k_gather_dense(const unsigned char* __restrict__ table,
                                                       const int32_t* __restrict__ ids,
                                                       OutT* __restrict__ out, int64_t n_rows,
                                                       int64_t n_tokens, int dim, float scale,
@@ -439,7 +442,7 @@ static void launch_blocks(const void* table, const int32_t* ids, int64_t single_
         set_error(HIP_BRIDGE_EUNSUPPORTED);
         return;
     }
-    k_gather_blocks<QT, OutT><<<(unsigned)grid, 256, 0, s>>>(
+    k_gather_blocks<QT, OutT><<<(unsigned)grid, 64 * kGatherWaves, 0, s>>>(
         (const unsigned char*)table, ids, (OutT*)out, n_rows, n_tokens, dim, scale, (int)rb,
         nseg, vec16, single_id);
     check_launch();
@@ -455,7 +458,7 @@ static void launch_q(const void* table, const int32_t* ids, int64_t single_id, v
         set_error(HIP_BRIDGE_EUNSUPPORTED);
         return;
     }
-    k_gather_q<QT, OutT, kGatherSteps><<<(unsigned)grid, 256, 0, s>>>(
+    k_gather_q<QT, OutT, kGatherSteps><<<(unsigned)grid, 64 * kGatherWaves, 0, s>>>(
         (const unsigned char*)table, ids, (OutT*)out, n_rows, n_tokens, dim, scale, nseg, single_id);
     check_launch();
 }
@@ -471,7 +474,7 @@ static void launch_dense(const void* table, const int32_t* ids, int64_t single_i
             set_error(HIP_BRIDGE_EUNSUPPORTED);
             return;
         }
-        k_gather_dense<QT, OutT, kGatherStepsDense><<<(unsigned)grid, 256, 0, s>>>(
+        k_gather_dense<QT, OutT, kGatherStepsDense><<<(unsigned)grid, 64 * kGatherWaves, 0, s>>>(
             (const unsigned char*)table, ids, (OutT*)out, n_rows, n_tokens, dim, scale, nseg,
             single_id);
     } else {
