@@ -449,14 +449,27 @@ def gather_case(dev, name, vocab=262144, dim=2560, n_tok=4096, n_rep=64, nsets=N
     return g, list(range(nsets)), nbytes, [tab] + outs + id_sets
 
 
-def bench_gather(dev):
+def bench_gather(dev, n_tok=4096, dim=2560):
+    """c3 gathers, each beside a practical ceiling: the rate of the reference streaming kernel
+    reading one and writing two streams of half the f32 output's bytes (the BF16 gather's
+    exact byte mix: 2-byte rows in, 4-byte values out), over buffer sets beyond the Infinity
+    Cache, applied to each gather's algorithmic bytes (Q8_0 / Q4_0 read fewer row bytes for
+    the same writes)."""
+    half = n_tok * dim * 2
+    c_us, c_shape, _ = stream_ceiling(dev, 1, 2, half)
+    c_rate = 3 * half / c_us / 1e3  # GB/s
     out = {}
     for name in GATHER_QTYPES:
-        g, sets, nbytes, bufs = gather_case(dev, name)
+        g, sets, nbytes, bufs = gather_case(dev, name, n_tok=n_tok, dim=dim)
         us = time_launches_us(dev, g, sets, 4 * len(sets))
+        cus = nbytes / c_rate / 1e3
         out[name] = {"us": round(us, 2), "bytes": nbytes, "GBps": round(nbytes / us / 1e3, 1),
-                     "frac_peak": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4)}
-        log(f"  gather {name}: {us:.2f} us {nbytes / us / 1e3:.0f} GB/s")
+                     "frac_peak": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4),
+                     "ceiling": {"us": round(cus, 2), "reads": 1, "writes": 2, "bytes_per_stream": half,
+                                 "shape": c_shape, "stream_us": round(c_us, 3), "GBps": round(c_rate, 1),
+                                 "frac_of_ceiling": round(cus / us, 4)}}
+        log(f"  gather {name}: {us:.2f} us {nbytes / us / 1e3:.0f} GB/s  (ceiling {cus:.2f} us at "
+            f"{c_rate:.0f} GB/s, {100 * cus / us:.1f}% of it)")
         for b_ in bufs:
             b_.deinit()
     return out
@@ -987,6 +1000,9 @@ def main():
         cfgs["c4_prefill"] = {k: c4[k] for k in ("us_per_layer", "us_per_layer_isolated_sum",
                                                  "us_per_layer_fused_4op", "chain_GBps", "ops", "rope_bases")}
         cfgs["c4_prefill"]["chain_GBps"] = round(cfgs["c4_prefill"]["chain_GBps"], 1)
+        for k, v in cfgs["c4_prefill"]["ops"].items():
+            if f"{k}_c4" in tr:
+                v["traffic"] = tr[f"{k}_c4"]
         log("gemv (decode projections)")
         cfgs["gemv_decode"] = bench_gemv(dev)
         log("gemm (prefill projections, matrix cores)")

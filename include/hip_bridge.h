@@ -426,8 +426,9 @@ void hip_ple_ctx_fuse(float* ctx_ple_buf, const float* ctx_scratch, int n, int a
 /* `bytes` each (a multiple of 16, 16-byte aligned buffers) with launch shape `shape` in   */
 /* [0, hip_stream_ref_shapes()); returns 0 or an error code. out0 may equal in0 (a read-   */
 /* modify-write in place, like the residual-stream updates). Shapes differ in workgroup    */
-/* size, chunks per thread and load/store cache policy. The fastest shape at a given size  */
-/* and mix is the ceiling a fused op of that mix is compared with.                         */
+/* size, chunks per thread, load/store cache policy and store form (buffer or global      */
+/* stores). The fastest shape at a given size and mix is the ceiling a fused op of that    */
+/* mix is compared with.                                                                   */
 /* ---------------------------------------------------------------------------------- */
 int hip_stream_ref_shapes(void);
 int hip_stream_ref(int n_in, int n_out, const void* in0, const void* in1 /*NULL*/, void* out0, void* out1 /*NULL*/,

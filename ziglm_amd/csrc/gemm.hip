@@ -275,6 +275,18 @@ struct TermPairs<1, NW> {
 #ifndef ZL_GEMM_DB_F32X
 #define ZL_GEMM_DB_F32X 0
 #endif
+// Wave priority raised while a wave issues its MFMAs (s_setprio 1 over the block's MFMAs, 0
+// for the conversion and the scale products): taken for three-plane activations at 64-token
+// tiles, where three workgroups share a CU (10240 x 2560 weights, 2048 tokens: 498 -> 407 us);
+// at 128-token tiles it slows the products (292 -> 363 us), and elsewhere it is neutral.
+// ZL_GEMM_PRIO=1 forces it everywhere. ZL_GEMM_SGB: a forced MFMA / VALU interleave (that
+// many VALU instructions after each MFMA; measured no better, off).
+#ifndef ZL_GEMM_PRIO
+#define ZL_GEMM_PRIO 0
+#endif
+#ifndef ZL_GEMM_SGB
+#define ZL_GEMM_SGB 0
+#endif
 
 // XK: activation form (X_F32: f32, split into three terms while staging; X_BF16: bf16, one
 // term; X_TERMS: three bf16 planes split beforehand, staged as they are). GE: gate.up GeGLU
@@ -340,10 +352,15 @@ __global__ __launch_bounds__(kGemmThreads, (gemm_wgs_per_cu<QT, XK, WT, WR>())) 
     for (int u = 0; u < XPL; ++u)
         rsx[u] = buf_rsrc((const unsigned char*)a.x + u * plane_bytes + (int64_t)b_base * a.cols * xes, xrange);
     u32x4 xr[XCH];
+    // A plane is a whole number of 256-chunk passes, so pass i's plane is a constant of the
+    // unrolled loop: the resource it selects stays in scalar registers (a plane index
+    // computed from tid would make each load a loop over the lanes' distinct resources).
+    static_assert((BT * XCPT) % kGemmThreads == 0, "X plane not a whole number of passes");
     auto load_x = [&](int kb) {
 #pragma unroll
         for (int i = 0; i < XCH; ++i) {
-            const int c = tid + kGemmThreads * i, pl = c / (BT * XCPT), cc = c % (BT * XCPT), tok = cc / XCPT;
+            constexpr int PC = BT * XCPT;  // chunks per plane
+            const int pl = kGemmThreads * i / PC, cc = tid + kGemmThreads * i % PC, tok = cc / XCPT;
             const uint32_t off = (uint32_t)(((int64_t)tok * a.cols + kb * kKB + XE * (cc % XCPT)) * xes);
             xr[i] = bldp<POL_DEFAULT>(rsx[pl], off);
         }
@@ -352,7 +369,8 @@ __global__ __launch_bounds__(kGemmThreads, (gemm_wgs_per_cu<QT, XK, WT, WR>())) 
         uint16_t* const sx = sx_of(buf);
 #pragma unroll
         for (int i = 0; i < XCH; ++i) {
-            const int c = tid + kGemmThreads * i, pl = c / (BT * XCPT), cc = c % (BT * XCPT);
+            constexpr int PC = BT * XCPT;
+            const int pl = kGemmThreads * i / PC, cc = tid + kGemmThreads * i % PC;
             const int tok = cc / XCPT, k = XE * (cc % XCPT);
             if constexpr (XK == X_F32) {
                 uint32_t t0[3], t1[3];
@@ -403,6 +421,7 @@ __global__ __launch_bounds__(kGemmThreads, (gemm_wgs_per_cu<QT, XK, WT, WR>())) 
 
     using TP = TermPairs<XT, NW>;
     constexpr int NP = TP::n;
+    constexpr bool PRIO = ZL_GEMM_PRIO || (XK == X_TERMS && WT == 1);
     // One K step: block kb's operands from LDS buffer `buf` into registers, its MFMAs (into the
     // block partial when SCALED), then `convert` (block kb + 1 into the LDS and the loads of
     // kb + 2), then the block scale products.
@@ -450,6 +469,7 @@ __global__ __launch_bounds__(kGemmThreads, (gemm_wgs_per_cu<QT, XK, WT, WR>())) 
             for (int j = 0; j < WR; ++j)
                 dv[j] = *reinterpret_cast<const float*>(sw + (wr0 + 32 * j + (lane & 31)) * kLdsRow + kScaleSlot);
         }
+        if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
         if constexpr (DB) {
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
@@ -463,6 +483,7 @@ __global__ __launch_bounds__(kGemmThreads, (gemm_wgs_per_cu<QT, XK, WT, WR>())) 
             mfmas(0, 0);
             mfmas(1, 1);
         }
+        if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
         convert();
         if constexpr (SCALED) {
 #pragma unroll
@@ -471,6 +492,14 @@ __global__ __launch_bounds__(kGemmThreads, (gemm_wgs_per_cu<QT, XK, WT, WR>())) 
                 for (int i = 0; i < WT; ++i)
 #pragma unroll
                     for (int r = 0; r < 16; ++r) acc[i][j][r] = fmaf(dv[j], part[i][j][r], acc[i][j][r]);
+        }
+        if (ZL_GEMM_SGB) {
+            // one MFMA, then ZL_GEMM_SGB VALU instructions, for each of the step's MFMAs
+#pragma unroll
+            for (int m = 0; m < 2 * WT * WR * NP; ++m) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, ZL_GEMM_SGB, 0);
+            }
         }
     };
 

@@ -67,6 +67,28 @@ __device__ __forceinline__ float row_sum(float v, float* slot) {
     }
 }
 
+// row_sum of R rows at once: slots[r] is row r's slot set; one barrier for all of them.
+template <int W, int R>
+__device__ __forceinline__ void row_sums(float (&v)[R], float* const (&slots)[R]) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) v[r] = group_sum<kWave>(v[r]);
+    if constexpr (W > 1) {
+        const int wave = (threadIdx.x >> 6) % W;
+        if ((threadIdx.x & 63) == 0) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) slots[r][wave] = v[r];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float t = slots[r][0];
+#pragma unroll
+            for (int i = 1; i < W; ++i) t += slots[r][i];
+            v[r] = t;
+        }
+    }
+}
+
 // W waves per row group (W in {1, 2, 4}), 256 threads per block, 4/W row groups per block,
 // R consecutive rows per group (R in {1, 2}). Lane g of a group (g in [0, 64W)) owns chunks
 // g, g + 64W, ... (NC of them at most) of each of its R rows, so it loads the weights of
@@ -90,10 +112,19 @@ __host__ __device__ constexpr int norm_gpb() {
 #define ZL_NORM_SP POL_NT
 #endif
 
+#ifndef ZL_NORM_STAGED
+#define ZL_NORM_STAGED 1
+#endif
 template <typename T, int NC, int MODE, int W, int R, bool WL>
 __global__ __launch_bounds__(256) void k_norm_rows(NormArgs a) {
     using C = Chunk<T>;
     constexpr int E = C::E;
+    // Rows reduced stage by stage (one barrier per reduction for all R rows instead of one
+    // per row and reduction), for the two-input modes at 4 waves per row: 8192 x 5376 bf16
+    // norm + add + norm 62.3 -> 61.2 us, add + norm 61.5 -> 60.9 us; slower at 2 waves per
+    // row (2048 x 2560: 8.32 -> 8.63 us, 7.55 -> 7.68 us) and for the plain norm (31.9 ->
+    // 32.3 us), which keep the row-by-row order. ZL_NORM_STAGED=0 turns it off.
+    constexpr bool STAGED = ZL_NORM_STAGED && W == 4 && R > 1 && MODE != M_NORM;
     constexpr int LP = ZL_NORM_LP, SP = ZL_NORM_SP;
     constexpr int GPB = norm_gpb<W>();  // row groups per block
     constexpr int STRIDE = kWave * W;
@@ -144,6 +175,106 @@ __global__ __launch_bounds__(256) void k_norm_rows(NormArgs a) {
         }
     };
     if constexpr (!WL) load_weights();
+
+    if constexpr (STAGED) {
+        // Stage by stage over the R rows: every row's first sums, one barrier for all of
+        // them; (NORM_ADD_NORM) every row's second sums, one barrier; then the stores.
+        float v[R][NC][E];
+        float ss[R];
+        float* s1[R];
+        float* s2[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const bool row_ok = row0 + r < a.rows;
+            s1[r] = s_red[2 * r] + rib * W;
+            s2[r] = s_red[2 * r + 1] + rib * W;
+            ss[r] = 0.0f;
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                const int idx = g + c * STRIDE;
+                if (row_ok && idx < nch) {
+                    if constexpr (MODE == M_NORM) {
+                        C::unpack(rx[r][c], v[r][c]);
+                    } else if constexpr (MODE == M_ADD_NORM) {
+                        float xv[E], rv[E];
+                        C::unpack(rx[r][c], xv);
+                        C::unpack(rr[r][c], rv);
+#pragma unroll
+                        for (int j = 0; j < E; ++j) v[r][c][j] = xv[j] + rv[j];
+                    } else {
+                        C::unpack(rr[r][c], v[r][c]);
+                    }
+#pragma unroll
+                    for (int j = 0; j < E; ++j) ss[r] = fmaf(v[r][c][j], v[r][c][j], ss[r]);
+                }
+            }
+            if constexpr (WL) {
+                if (r == 0) load_weights();
+            }
+        }
+        row_sums<W, R>(ss, s1);
+        float inv[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) inv[r] = rms_inv_hw(ss[r], n, a.eps);
+        if constexpr (MODE == M_NORM_ADD_NORM) {
+            float ss2[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const bool row_ok = row0 + r < a.rows;
+                ss2[r] = 0.0f;
+#pragma unroll
+                for (int c = 0; c < NC; ++c) {
+                    const int idx = g + c * STRIDE;
+                    if (row_ok && idx < nch) {
+                        float xv[E];
+                        C::unpack(rx[r][c], xv);
+#pragma unroll
+                        for (int j = 0; j < E; ++j) {
+                            v[r][c][j] = xv[j] + (v[r][c][j] * inv[r]) * w_factor(f1[c][j], has_w1, a.uo);
+                            ss2[r] = fmaf(v[r][c][j], v[r][c][j], ss2[r]);
+                        }
+                    }
+                }
+            }
+            row_sums<W, R>(ss2, s2);
+#pragma unroll
+            for (int r = 0; r < R; ++r) inv[r] = rms_inv_hw(ss2[r], n, a.eps);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int64_t row = row0 + r;
+            const bool row_ok = row < a.rows;
+            const uint32_t row_bytes = row_ok ? (uint32_t)n * sizeof(T) : 0u;
+            T* const xrow = (T*)a.x + row * n;
+            T* const orow = (T*)a.out + row * n;
+            const auto wsx = buf_rsrc(xrow, MODE != M_NORM ? row_bytes : 0u);
+            const auto wso = buf_rsrc(orow, MODE != M_NORM_ADD ? row_bytes : 0u);
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                const int idx = g + c * STRIDE;
+                if (!(row_ok && idx < nch)) continue;
+                if constexpr (MODE == M_NORM_ADD) {
+                    float xv[E];
+                    C::unpack(rx[r][c], xv);
+#pragma unroll
+                    for (int j = 0; j < E; ++j) xv[j] = xv[j] + (v[r][c][j] * inv[r]) * w_factor(f1[c][j], has_w1, a.uo);
+                    strow16<SP>(xrow, wsx, (uint32_t)idx * 16u, C::pack(xv));
+                } else {
+                    float y[E];
+                    if constexpr (MODE == M_NORM_ADD_NORM) {
+#pragma unroll
+                        for (int j = 0; j < E; ++j) y[j] = (v[r][c][j] * inv[r]) * w_factor(f2[c][j], has_w2, a.uo);
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < E; ++j) y[j] = (v[r][c][j] * inv[r]) * w_factor(f1[c][j], has_w1, a.uo);
+                    }
+                    if constexpr (MODE != M_NORM) strow16<SP>(xrow, wsx, (uint32_t)idx * 16u, C::pack(v[r][c]));
+                    strow16<SP>(orow, wso, (uint32_t)idx * 16u, C::pack(y));
+                }
+            }
+        }
+        return;
+    }
 
 #pragma unroll
     for (int r = 0; r < R; ++r) {

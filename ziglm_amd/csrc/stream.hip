@@ -22,6 +22,10 @@ struct StreamArgs {
     int64_t nch;  // 16-byte chunks per stream
 };
 
+// Store policy kGlobalNt: nt stores as global (per-lane address) stores, the form the norm
+// kernels use (buffer nt stores are the other nt form).
+constexpr int kGlobalNt = -1;
+
 // U chunks per thread, consecutive by workgroup: chunk (block * U + u) * THREADS + thread.
 template <int NIN, int NOUT, int THREADS, int U, int LP, int SP>
 __global__ __launch_bounds__(THREADS) void k_stream(StreamArgs a) {
@@ -43,13 +47,20 @@ __global__ __launch_bounds__(THREADS) void k_stream(StreamArgs a) {
     for (int u = 0; u < U; ++u) {
         const uint32_t off = (uint32_t)(u * THREADS + threadIdx.x) * 16u;
         const u32x4 v = NIN == 2 ? (x[u] ^ y[u]) : x[u];
-        bstp<SP>(w0, off, v);
-        if constexpr (NOUT == 2) bstp<SP>(w1, off, v);
+        if constexpr (SP == kGlobalNt) {
+            if (off < bytes) {
+                sts16(a.out0 + c0 * 16 + off, v);
+                if constexpr (NOUT == 2) sts16(a.out1 + c0 * 16 + off, v);
+            }
+        } else {
+            bstp<SP>(w0, off, v);
+            if constexpr (NOUT == 2) bstp<SP>(w1, off, v);
+        }
     }
 }
 
 // The launch shapes the ceiling is the best of: {threads, chunks per thread} x load policy
-// {default, nt} x store policy {nt, sc1}. The 3-, 5- and 6-chunk shapes follow the norm
+// {default, nt} x store policy {nt (buffer store), sc1}, and nt loads with nt global stores. The 3-, 5- and 6-chunk shapes follow the norm
 // kernels' layout (a 128- or 256-thread group over 3 chunks per lane of a row, two rows per
 // group).
 struct Shape {
@@ -57,7 +68,7 @@ struct Shape {
 };
 constexpr Shape kGeo[] = {{64, 1}, {256, 1}, {256, 2}, {256, 4}, {512, 2}, {128, 3}, {256, 3}, {256, 5}, {256, 6}};
 constexpr int kNumGeo = sizeof(kGeo) / sizeof(kGeo[0]);
-constexpr int kNumShapes = kNumGeo * 4;
+constexpr int kNumShapes = kNumGeo * 5;
 
 template <int NIN, int NOUT, int THREADS, int U, int LP, int SP>
 static void launch_one(const StreamArgs& a, hipStream_t s) {
@@ -87,7 +98,8 @@ static void launch_shape(int shape, const StreamArgs& a, hipStream_t s) {
         case 0: launch_geo<NIN, NOUT, POL_NT, POL_NT>(geo, a, s); break;
         case 1: launch_geo<NIN, NOUT, POL_DEFAULT, POL_NT>(geo, a, s); break;
         case 2: launch_geo<NIN, NOUT, POL_NT, POL_SC1>(geo, a, s); break;
-        default: launch_geo<NIN, NOUT, POL_DEFAULT, POL_SC1>(geo, a, s); break;
+        case 3: launch_geo<NIN, NOUT, POL_DEFAULT, POL_SC1>(geo, a, s); break;
+        default: launch_geo<NIN, NOUT, POL_NT, kGlobalNt>(geo, a, s); break;
     }
 }
 
