@@ -118,15 +118,16 @@ def time_launches_us(dev, fn, sets, n_launch, warm_ms=20.0, reps=5):
     return ms * 1000.0 / n_launch
 
 
-def stream_ceiling(dev, n_in, n_out, nbytes, inplace=False, min_total=3 * MALL_BYTES, n_launch=100):
+def stream_ceiling(dev, n_in, n_out, nbytes, inplace=False, min_total=3 * MALL_BYTES, n_launch=100, min_sets=2):
     """Practical ceiling of a byte mix: the fastest launch shape (workgroup size, chunks per
-    thread, load / store cache policy) of the library's reference streaming kernel
-    (hip_stream_ref: n_in reads and n_out writes of nbytes each, nothing else) over buffer
-    sets that together exceed the Infinity Cache. inplace: the mix of an op that rewrites its
-    first input (x += ...): the fastest of that in-place form (output 0 = input 0) and the
-    form with separate outputs. Returns (us, shape, "inplace" | "separate")."""
+    thread, load / store cache policy and store form) of the library's reference streaming
+    kernel (hip_stream_ref: n_in reads and n_out writes of nbytes each, nothing else) over
+    buffer sets of its own that together exceed the Infinity Cache (at least min_sets of
+    them). inplace: the mix of an op that rewrites its first input (x += ...): the fastest of
+    that in-place form (output 0 = input 0) and the form with separate outputs. Returns (us,
+    shape, "inplace" | "separate")."""
     per = (n_in + n_out) * nbytes
-    nsets = int(min(64, max(2, math.ceil(min_total / per))))
+    nsets = int(min(64, max(min_sets, math.ceil(min_total / per))))
     sets = [[dev.alloc(nbytes) for _ in range(n_in + n_out)] for _ in range(nsets)]
     for st in sets:
         for buf in st:
@@ -146,6 +147,36 @@ def stream_ceiling(dev, n_in, n_out, nbytes, inplace=False, min_total=3 * MALL_B
     for st in sets:
         for buf in st:
             buf.deinit()
+    return best
+
+
+def op_streams(name, L):
+    """(reads, writes, in0, in1, out0, out1) of an op's activation streams over its own buffers
+    (equal sizes: x, xb, ao, fo are [T x H], gate, up, act [T x I]); None where the op's
+    streams differ in size (QK: Q in place, K / V rows into the caches)."""
+    return {"input_norm": (1, 1, L.x, None, L.xb, None),
+            "add_rmsnorm": (2, 2, L.x, L.ao, L.x, L.xb),
+            "norm_add_norm": (2, 2, L.x, L.ao, L.x, L.xb),
+            "geglu": (2, 1, L.gate, L.up, L.act, None),
+            "norm_add": (2, 1, L.x, L.fo, L.x, None),
+            "norm_add_norm_next": (2, 2, L.x, L.fo, L.x, L.xb)}.get(name)
+
+
+def stream_ceiling_on(dev, sets, name, nbytes, n_launch=100):
+    """The op's ceiling over its own buffers: the fastest shape of the reference streaming
+    kernel reading and writing the very tensors the op reads and writes (same sets, same
+    rotation, same addresses and pages), in place where the op is. Returns (us, shape). The
+    streaming kernel overwrites those tensors, so this runs after the op's own timings."""
+    best = (float("inf"), -1)
+    for shp in range(dev.b.hip_stream_ref_shapes()):
+        def fn(d, L, shp=shp):
+            n_in, n_out, i0, i1, o0, o1 = op_streams(name, L)
+            rc = d.b.hip_stream_ref(n_in, n_out, i0.ptr, i1.ptr if i1 is not None else None, o0.ptr,
+                                    o1.ptr if o1 is not None else None, nbytes, shp, d.stream)
+            if rc != 0:
+                raise RuntimeError(f"hip_stream_ref: {rc}")
+        us = time_launches_us(dev, fn, sets, max(n_launch, 4 * len(sets)))
+        best = min(best, (us, shp))
     return best
 
 
@@ -253,22 +284,14 @@ def bench_prefill(dev, shape, T, dtype, steps, warmup, ops_launches=100, thetas=
         + (f", RoPE bases {thetas} alternating" if thetas else ""))
     nb = LY.op_bytes(shape, T, es)
     mix = op_mix(shape, T, es)
-    ceilings = {}
+    op_names = ("input_norm", "add_rmsnorm", "qk_norm_rope_kv", "norm_add_norm", "geglu", "norm_add",
+                "norm_add_norm_next")
     ops = {}
-    for name in ("input_norm", "add_rmsnorm", "qk_norm_rope_kv", "norm_add_norm", "geglu", "norm_add",
-                 "norm_add_norm_next"):
+    for name in op_names:
         us = time_launches_us(dev, LY.OPS[name], sets, max(ops_launches, len(sets) * 4))
-        if mix[name] not in ceilings:
-            ceilings[mix[name]] = stream_ceiling(dev, *mix[name])
-        cu, cshape, cform = ceilings[mix[name]]
         ops[name] = {"us": round(us, 3), "bytes": nb[name], "GBps": round(nb[name] / us / 1e3, 1),
-                     "frac_peak": round(nb[name] / us / 1e3 / PEAK_HBM_GBS, 4),
-                     "ceiling": {"us": round(cu, 3), "reads": mix[name][0], "writes": mix[name][1],
-                                 "bytes_per_stream": mix[name][2], "shape": cshape, "form": cform,
-                                 "GBps": round((mix[name][0] + mix[name][1]) * mix[name][2] / cu / 1e3, 1),
-                                 "frac_of_ceiling": round(cu / us, 4)}}
-        log(f"  {name:20s} {us:9.2f} us  {nb[name] / us / 1e3:8.1f} GB/s  (same-size stream {cu:.2f} us, "
-            f"{cu / us:.1%} of it)")
+                     "frac_peak": round(nb[name] / us / 1e3 / PEAK_HBM_GBS, 4)}
+        log(f"  {name:20s} {us:9.2f} us  {nb[name] / us / 1e3:8.1f} GB/s")
     if thetas:
         for th in thetas:
             own = [L for L in sets if L.shape.theta == th]
@@ -311,6 +334,33 @@ def bench_prefill(dev, shape, T, dtype, steps, warmup, ops_launches=100, thetas=
     chain_b = LY.chain_bytes(shape, T, es)
     fused_b = LY.chain_bytes(shape, T, es, fused=True)
     ms_f = chain_ms(steps, True, steps)
+
+    # Ceilings, after every timing above (the streaming kernel overwrites the op's tensors).
+    # ceiling: over the op's own buffers where its streams are equal-sized tensors, else (QK)
+    # over buffer sets of the streaming kernel's own, at least as many as the op rotates;
+    # ceiling_separate: always the latter, for comparison.
+    separate = {}
+    for name in op_names:
+        r_, w_, per_stream, inplace = mix[name]
+        if mix[name] not in separate:
+            separate[mix[name]] = stream_ceiling(dev, *mix[name], min_sets=len(sets))
+        su, sshape, sform = separate[mix[name]]
+        sep = {"us": round(su, 3), "reads": r_, "writes": w_, "bytes_per_stream": per_stream, "shape": sshape,
+               "form": sform, "GBps": round((r_ + w_) * per_stream / su / 1e3, 1)}
+        if op_streams(name, sets[0]) is not None:
+            cu, cshape = stream_ceiling_on(dev, sets, name, per_stream)
+            ceil = {"us": round(cu, 3), "reads": r_, "writes": w_, "bytes_per_stream": per_stream, "shape": cshape,
+                    "form": "op buffers" + (", in place" if inplace else ""),
+                    "GBps": round((r_ + w_) * per_stream / cu / 1e3, 1)}
+        else:
+            cu, ceil = su, dict(sep)
+        us = ops[name]["us"]
+        ceil["frac_of_ceiling"] = round(cu / us, 4)
+        sep["frac_of_ceiling"] = round(su / us, 4)
+        ops[name]["ceiling"] = ceil
+        ops[name]["ceiling_separate"] = sep
+        log(f"  {name:20s} {us:9.2f} us: ceiling {cu:.2f} us ({ceil['form']}), {cu / us:.1%} of it; "
+            f"separate buffers {su:.2f} us, {su / us:.1%}")
     isolated = sum(ops[k]["us"] for k in LY.CHAIN)
     res = {
         "T": T, "shape": shape.name, "io_dtype": "bf16" if dtype == B.BF16 else "f32",

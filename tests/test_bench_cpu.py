@@ -32,3 +32,26 @@ def test_in_place_mixes():
     mix = bench.op_mix(LY.GEMMA_4B, 2048, 2)
     assert mix["norm_add"][3] and mix["norm_add_norm"][3] and mix["add_rmsnorm"][3]
     assert not mix["input_norm"][3] and not mix["geglu"][3]
+
+
+def test_op_streams_match_mixes():
+    """The op-buffer ceiling reads and writes what op_mix says each op moves: the same number
+    of streams, in place exactly where the op rewrites its first input."""
+    class L:  # stand-in buffers: only identity matters
+        pass
+    lb = L()
+    for name in ("x", "xb", "ao", "fo", "gate", "up", "act"):
+        setattr(lb, name, object())
+    mix = bench.op_mix(LY.GEMMA_4B, 2048, 2)
+    covered = 0
+    for name, (r, w, _, inplace) in mix.items():
+        st = bench.op_streams(name, lb)
+        if st is None:
+            assert name == "qk_norm_rope_kv"
+            continue
+        covered += 1
+        n_in, n_out, i0, i1, o0, o1 = st
+        assert (n_in, n_out) == (r, w), name
+        assert (i1 is not None) == (n_in == 2) and (o1 is not None) == (n_out == 2), name
+        assert (o0 is i0) == inplace, name
+    assert covered == 6
