@@ -279,13 +279,9 @@ struct TermPairs<1, NW> {
 // for the conversion and the scale products): taken for three-plane activations at 64-token
 // tiles, where three workgroups share a CU (10240 x 2560 weights, 2048 tokens: 498 -> 407 us);
 // at 128-token tiles it slows the products (292 -> 363 us), and elsewhere it is neutral.
-// ZL_GEMM_PRIO=1 forces it everywhere. ZL_GEMM_SGB: a forced MFMA / VALU interleave (that
-// many VALU instructions after each MFMA; measured no better, off).
+// ZL_GEMM_PRIO=1 forces it everywhere.
 #ifndef ZL_GEMM_PRIO
 #define ZL_GEMM_PRIO 0
-#endif
-#ifndef ZL_GEMM_SGB
-#define ZL_GEMM_SGB 0
 #endif
 
 // XK: activation form (X_F32: f32, split into three terms while staging; X_BF16: bf16, one
@@ -492,14 +488,6 @@ __global__ __launch_bounds__(kGemmThreads, (gemm_wgs_per_cu<QT, XK, WT, WR>())) 
                 for (int i = 0; i < WT; ++i)
 #pragma unroll
                     for (int r = 0; r < 16; ++r) acc[i][j][r] = fmaf(dv[j], part[i][j][r], acc[i][j][r]);
-        }
-        if (ZL_GEMM_SGB) {
-            // one MFMA, then ZL_GEMM_SGB VALU instructions, for each of the step's MFMAs
-#pragma unroll
-            for (int m = 0; m < 2 * WT * WR * NP; ++m) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, ZL_GEMM_SGB, 0);
-            }
         }
     };
 
