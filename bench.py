@@ -131,7 +131,7 @@ def stream_ceiling(dev, n_in, n_out, nbytes, inplace=False, min_total=3 * MALL_B
     sets = [[dev.alloc(nbytes) for _ in range(n_in + n_out)] for _ in range(nsets)]
     for st in sets:
         for buf in st:
-            buf.fill(0x3C)
+            fill_tiled(buf, pool(B.BF16))  # data like the ops' (power, and so clocks, depend on it)
     best = (float("inf"), -1, "separate")
     for form in (("separate", "inplace") if inplace else ("separate",)):
         for shp in range(dev.b.hip_stream_ref_shapes()):
@@ -629,6 +629,10 @@ def bench_gemm_prefill(dev, T=2048):
     # f32 activations split once into three bf16 planes (hip_split_terms; shared by every
     # product of one input, so the K loop converts weights only): the products alone.
     x_planes = dev.alloc(3 * T * max(H, I) * 2)
+    x_src = dev.from_numpy(synth.normal_f32(5, "x", (T, max(H, I))))
+    dev.splitTerms(x_src, x_planes, T * max(H, I))  # the planes of real N(0,1) activations
+    dev.sync()
+    x_src.deinit()
     for name, qt, rows, cols in [("gate_q4_0_terms", B.Q4_0, I, H), ("down_q4_0_terms", B.Q4_0, H, I)]:
         def fn(d, m, x, ys, qt=qt, rows=rows, cols=cols):
             d.gemmEx(qt, m[0], None, B.F32_TERMS, x_planes, B.F32, ys[0], T, rows, cols)

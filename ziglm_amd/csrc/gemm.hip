@@ -279,7 +279,7 @@ struct TermPairs<1, NW> {
 // for the conversion and the scale products): taken for three-plane activations at 64-token
 // tiles, where three workgroups share a CU (10240 x 2560 weights, 2048 tokens: 498 -> 407 us);
 // at 128-token tiles it slows the products (292 -> 363 us), and elsewhere it is neutral.
-// ZL_GEMM_PRIO=1 forces it everywhere.
+// ZL_GEMM_PRIO=1 forces it everywhere, -1 turns it off.
 #ifndef ZL_GEMM_PRIO
 #define ZL_GEMM_PRIO 0
 #endif
@@ -417,7 +417,7 @@ __global__ __launch_bounds__(kGemmThreads, (gemm_wgs_per_cu<QT, XK, WT, WR>())) 
 
     using TP = TermPairs<XT, NW>;
     constexpr int NP = TP::n;
-    constexpr bool PRIO = ZL_GEMM_PRIO || (XK == X_TERMS && WT == 1);
+    constexpr bool PRIO = ZL_GEMM_PRIO > 0 || (ZL_GEMM_PRIO == 0 && XK == X_TERMS && WT == 1);
     // One K step: block kb's operands from LDS buffer `buf` into registers, its MFMAs (into the
     // block partial when SCALED), then `convert` (block kb + 1 into the LDS and the loads of
     // kb + 2), then the block scale products.
