@@ -392,8 +392,8 @@ def bench_decode(dev, B_, pos_seed=4, n_launch=200):
     max_seq = 32768
     L = LY.LayerBuffers(dev, s, B_, B.F32, cache_rows=B_ * max_seq)
     p = pool(B.F32)
-    for name in ("x", "xb", "ao", "fo", "q", "k", "v", "gate", "up", "act"):
-        fill_tiled(getattr(L, name), p)
+    for name in ("x", "xb", "ao", "fo", "q", "k", "v", "gate", "up", "act", "kc", "vc"):
+        fill_tiled(getattr(L, name), p)  # caches too: attention reads rows of N(0,1) data
     for k in L.w:
         L.w[k].upload(synth.normal_f32(4, "w_" + k, (s.H,), 0, 0.1))
     L.wq.upload(synth.normal_f32(4, "wq", (s.D,), 0, 0.1))
@@ -696,6 +696,9 @@ def bench_decode_step(dev, n_layers=34, pos0=1234, n_tokens=32, fused=True, grap
     from ziglm_amd.decode import DecodeModel
     m = DecodeModel.synthetic(dev, LY.GEMMA_4B, n_layers=n_layers, vocab=262144, max_seq=4096, fused=fused)
     try:
+        # cache rows before the timed positions hold N(0,1) data (as after a prefill), not zeros
+        fill_tiled(m.kc, pool(B.F32))
+        fill_tiled(m.vc, pool(B.F32))
         m.set_token(2)
         e0, e1 = dev.event(), dev.event()
         if graph:
@@ -759,6 +762,10 @@ def bench_gguf_decode(dev, pos0=1234, n_tokens=64, path=None, graph=True, fused=
             os.unlink(tmp)
     try:
         dm.reset(2)
+        # cache rows before the timed positions hold N(0,1) data (as after a prefill), not zeros
+        fill_tiled(dm.kc, pool(B.F32))
+        fill_tiled(dm.vc, pool(B.F32))
+        dev.sync()
         e0, e1 = dev.event(), dev.event()
         if graph:
             dm.capture()
