@@ -687,6 +687,39 @@ def bench_gemm_prefill(dev, T=2048):
     return out
 
 
+def bench_gemm_library(T=2048, n=100):
+    """Reference for the prefill GEMM: torch.matmul (hipBLASLt / rocBLAS) on the same shapes
+    with dense bf16 and f32 operands (N(0,1) data, 8 weight copies in turn): what the
+    platform's library reaches on the matrix cores at these sizes. Measurement only; the
+    library's products are not ziglm's (no quantised weights, no exact f32 split)."""
+    import torch
+    dev = torch.device("cuda:0")
+    s = LY.GEMMA_4B
+    out = {}
+    for name, rows, cols in (("gate", s.I, s.H), ("down", s.H, s.I)):
+        for dt, tag in ((torch.bfloat16, "bf16"), (torch.float32, "f32")):
+            g = torch.Generator(device=dev)
+            g.manual_seed(1)
+            x = torch.randn(T, cols, device=dev, dtype=dt, generator=g)
+            ws = [torch.randn(cols, rows, device=dev, dtype=dt, generator=g) for _ in range(8)]
+            y = torch.empty(T, rows, device=dev, dtype=dt)
+            for i in range(20):
+                torch.matmul(x, ws[i % 8], out=y)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for i in range(n):
+                torch.matmul(x, ws[i % 8], out=y)
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1000.0 / n
+            tf = 2.0 * rows * cols * T / us / 1e6
+            out[f"{name}_{tag}"] = {"us": round(us, 1), "rows": rows, "cols": cols, "tokens": T, "TFLOPs": round(tf, 1)}
+            log(f"  torch.matmul {name} {tag}: {us:.1f} us {tf:.1f} TFLOP/s")
+            del x, ws, y
+    return out
+
+
 # ---------------------------------------------------------------------------------------
 # Full decode step (34-layer Gemma-4B-shaped Q4_0 model, graph replay per token)
 # ---------------------------------------------------------------------------------------
@@ -931,7 +964,7 @@ def main():
     ap.add_argument("--only", default=None, help="run one op only (profiling): a chain op, "
                     "gather_q8_0 / gather_q4_0 / gather_bf16 (c3), c3 (all three), prefill (every chain op and the "
                     "chain at --config), c5 (batched decode ops), gemv, gemm, decode_step, "
-                    "gguf_decode, "
+                    "gguf_decode, gemm_lib (torch.matmul at the prefill shapes, reference only), "
                     "or 'copy' = hipMemcpy device-to-device of the GeGLU output size (counter calibration)")
     ap.add_argument("--eager", action="store_true", help="with --only: launch eagerly, no graph (kernel traces)")
     ap.add_argument("--config", default="c2", choices=["c2", "c4"])
@@ -942,6 +975,12 @@ def main():
               f"each run them on their own token or head shard)",
               file=sys.stderr)
         sys.exit(2)
+
+    if a.only == "gemm_lib":
+        # the platform's own GEMM (torch.matmul -> hipBLASLt / rocBLAS) at the prefill shapes,
+        # as a practical reference for the matrix cores; this mode never loads hip_bridge
+        print(json.dumps(bench_gemm_library()))
+        return
 
     global EAGER
     EAGER = bool(a.only and a.eager)
