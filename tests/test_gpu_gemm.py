@@ -33,11 +33,13 @@ def run(dev, qtype, raw, X, rows, cols):
 
 
 # Workgroup tiles (tokens x rows) by launch size: 128 x 128 from 512 such tiles (e.g. 4096 rows
-# x 2048 tokens), else 64 x 128 from 512 (4096 x 1024), else 64 x 64.
+# x 2048 tokens), else 64 x 128 from 512 (4096 x 1024; 2560 x 2048, 2500 x 1900 with a ragged
+# last tile), else 64 x 64.
 @pytest.mark.parametrize("qtype", TYPES)
 @pytest.mark.parametrize("rows,cols,batch", [(128, 64, 32), (200, 96, 37), (129, 2560, 128), (77, 160, 300),
                                              (256, 512, 64), (4096, 96, 2048), (4100, 64, 2050),
-                                             (4096, 64, 1024), (4097, 96, 1000)])
+                                             (4096, 64, 1024), (4097, 96, 1000), (2560, 256, 2048),
+                                             (2500, 96, 1900)])
 def test_gemm_mfma_integer_bitexact(dev, qtype, rows, cols, batch):
     raw, wd = int_matrix(qtype, rows, cols, seed=rows * cols + qtype + batch, scale_pow=-1)
     X = np.random.default_rng(batch).integers(-3, 4, (batch, cols)).astype(np.float32)
@@ -49,7 +51,8 @@ def test_gemm_mfma_integer_bitexact(dev, qtype, rows, cols, batch):
 
 @pytest.mark.parametrize("qtype", TYPES)
 @pytest.mark.parametrize("rows,cols,batch", [(256, 2560, 128), (300, 1024, 77), (1024, 2560, 512),
-                                             (128, 10240, 64), (4096, 512, 2048), (4096, 1024, 1024)])
+                                             (128, 10240, 64), (4096, 512, 2048), (4096, 1024, 1024),
+                                             (2560, 1024, 2048)])
 def test_gemm_mfma_vs_f64_and_oracle(dev, oracle, qtype, rows, cols, batch):
     raw, wd = random_matrix(qtype, rows, cols, seed=rows + cols + batch)
     X = synth.normal_f32(rows + batch, "X", (batch, cols), 0, 2)
@@ -98,7 +101,7 @@ def run_ex(dev, qtype, raw, X, rows, cols, x_dtype, y_dtype, raw_up=None):
 
 @pytest.mark.parametrize("qtype", TYPES)
 @pytest.mark.parametrize("rows,cols,batch", [(128, 64, 32), (200, 96, 37), (129, 2560, 5), (4100, 64, 2050),
-                                             (4096, 64, 1024), (77, 160, 300)])
+                                             (4096, 64, 1024), (77, 160, 300), (2560, 256, 2048), (2500, 96, 1900)])
 def test_gemm_ex_bf16_activations_integer_bitexact(dev, qtype, rows, cols, batch):
     """Integer activations are exact in bf16, so the bf16-input product of integer operands is
     the exact integer dot product (f32 output) and its bf16 rounding (bf16 output)."""
@@ -197,7 +200,8 @@ def test_split_terms_bitexact(dev):
 
 
 @pytest.mark.parametrize("qtype", TYPES)
-@pytest.mark.parametrize("rows,cols,batch", [(256, 2560, 128), (300, 1024, 77), (4096, 512, 2048), (129, 160, 40)])
+@pytest.mark.parametrize("rows,cols,batch", [(256, 2560, 128), (300, 1024, 77), (4096, 512, 2048), (129, 160, 40),
+                                             (2500, 96, 1900)])
 def test_gemm_ex_split_terms_equal_f32_product(dev, qtype, rows, cols, batch):
     """Activations split beforehand (hip_split_terms, F32_TERMS input) give hip_gemm's f32
     product bit for bit: the kernel stages the same three terms it would form itself."""
