@@ -474,17 +474,23 @@ def bench_decode(dev, B_, pos_seed=4, n_launch=200):
 GATHER_QTYPES = {"q8_0": B.Q8_0, "q4_0": B.Q4_0, "bf16": B.BF16}
 
 
-def gather_case(dev, name, vocab=262144, dim=2560, n_tok=4096, n_rep=64, nsets=None):
+def gather_case(dev, name, vocab=262144, dim=2560, n_tok=4096, n_rep=64, nsets=None, sequential=False):
     """c3: a [vocab x dim] table of `name` rows, `nsets` id lists (4032 uniform + 64 repeated
     ids, each list its own seed) and f32 outputs; by default enough lists that one cycle
     through them moves 3x the Infinity Cache (table rows and outputs), so a table row read
-    again has left that cache. Returns (launch fn, sets, algorithmic bytes, buffers to free)."""
+    again has left that cache. `sequential`: list i holds the consecutive ids i * n_tok + t
+    instead (contiguous table reads, for comparison). Returns (launch fn, sets, algorithmic
+    bytes, buffers to free)."""
     qt = GATHER_QTYPES[name]
     rb = {"q8_0": dim // 32 * 34, "q4_0": dim // 32 * 18, "bf16": dim * 2}[name]
     if nsets is None:
         nsets = int(min(64, max(2, math.ceil(3 * MALL_BYTES / (n_tok * (rb + dim * 4))))))
     scale = np.float32(np.sqrt(np.float32(dim)))
-    id_sets = [dev.from_numpy(synth.gather_ids(2 + i, n_tok, vocab, n_repeat=n_rep)) for i in range(nsets)]
+    if sequential:
+        lists = [((np.arange(n_tok) + i * n_tok) % vocab).astype(np.int32) for i in range(nsets)]
+    else:
+        lists = [synth.gather_ids(2 + i, n_tok, vocab, n_repeat=n_rep) for i in range(nsets)]
+    id_sets = [dev.from_numpy(ids) for ids in lists]
     outs = [dev.alloc(n_tok * dim * 4) for _ in range(nsets)]
     tab = dev.alloc(vocab * rb)
     if qt == B.BF16:
@@ -504,7 +510,8 @@ def bench_gather(dev, n_tok=4096, dim=2560):
     reading one and writing two streams of half the f32 output's bytes (the BF16 gather's
     exact byte mix: 2-byte rows in, 4-byte values out), over buffer sets beyond the Infinity
     Cache, applied to each gather's algorithmic bytes (Q8_0 / Q4_0 read fewer row bytes for
-    the same writes)."""
+    the same writes). `sequential_ids`: the same gather over consecutive ids (contiguous
+    table reads), which separates the cost of random row addresses from the kernel's."""
     half = n_tok * dim * 2
     c_us, c_shape, _ = stream_ceiling(dev, 1, 2, half)
     c_rate = 3 * half / c_us / 1e3  # GB/s
@@ -518,10 +525,17 @@ def bench_gather(dev, n_tok=4096, dim=2560):
                      "ceiling": {"us": round(cus, 2), "reads": 1, "writes": 2, "bytes_per_stream": half,
                                  "shape": c_shape, "stream_us": round(c_us, 3), "GBps": round(c_rate, 1),
                                  "frac_of_ceiling": round(cus / us, 4)}}
-        log(f"  gather {name}: {us:.2f} us {nbytes / us / 1e3:.0f} GB/s  (ceiling {cus:.2f} us at "
-            f"{c_rate:.0f} GB/s, {100 * cus / us:.1f}% of it)")
         for b_ in bufs:
             b_.deinit()
+        g, sets, _, bufs = gather_case(dev, name, n_tok=n_tok, dim=dim, sequential=True)
+        sus = time_launches_us(dev, g, sets, 4 * len(sets))
+        out[name]["sequential_ids"] = {"us": round(sus, 2), "GBps": round(nbytes / sus / 1e3, 1),
+                                       "frac_peak": round(nbytes / sus / 1e3 / PEAK_HBM_GBS, 4),
+                                       "frac_of_ceiling": round(cus / sus, 4)}
+        for b_ in bufs:
+            b_.deinit()
+        log(f"  gather {name}: {us:.2f} us {nbytes / us / 1e3:.0f} GB/s  (ceiling {cus:.2f} us at "
+            f"{c_rate:.0f} GB/s, {100 * cus / us:.1f}% of it; consecutive ids {sus:.2f} us)")
     return out
 
 

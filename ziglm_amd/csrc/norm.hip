@@ -115,6 +115,12 @@ __host__ __device__ constexpr int norm_gpb() {
 #ifndef ZL_NORM_STAGED
 #define ZL_NORM_STAGED 1
 #endif
+// NORM_ADD_NORM with late weights: the second norm's weights are requested after the first
+// reduction, not with the first norm's (2048 x 2560 bf16, four runs: 8.43 -> 8.29 us; 8192 x
+// 5376 unchanged). ZL_NORM_W2_LATE=0 loads both together.
+#ifndef ZL_NORM_W2_LATE
+#define ZL_NORM_W2_LATE 1
+#endif
 template <typename T, int NC, int MODE, int W, int R, bool WL>
 __global__ __launch_bounds__(256) void k_norm_rows(NormArgs a) {
     using C = Chunk<T>;
@@ -163,16 +169,20 @@ __global__ __launch_bounds__(256) void k_norm_rows(NormArgs a) {
     // 5.84 -> 4.62 us).
     float f1[NC][E];
     float f2[MODE == M_NORM_ADD_NORM ? NC : 1][E];
+    constexpr bool W2L = ZL_NORM_W2_LATE && WL && MODE == M_NORM_ADD_NORM;
+    auto load_w2 = [&]() {
+        if constexpr (MODE == M_NORM_ADD_NORM) {
+            const auto rsw2 = buf_rsrc(a.w2, has_w2 ? (uint32_t)n * 4u : 0u);
+#pragma unroll
+            for (int c = 0; c < NC; ++c) load_wb<E>(rsw2, (uint32_t)(g + c * STRIDE) * E * 4u, f2[c]);
+        }
+    };
     auto load_weights = [&]() {
         const uint32_t wbytes = (uint32_t)n * 4u;
         const auto rsw1 = buf_rsrc(a.w1, has_w1 ? wbytes : 0u);
 #pragma unroll
         for (int c = 0; c < NC; ++c) load_wb<E>(rsw1, (uint32_t)(g + c * STRIDE) * E * 4u, f1[c]);
-        if constexpr (MODE == M_NORM_ADD_NORM) {
-            const auto rsw2 = buf_rsrc(a.w2, has_w2 ? wbytes : 0u);
-#pragma unroll
-            for (int c = 0; c < NC; ++c) load_wb<E>(rsw2, (uint32_t)(g + c * STRIDE) * E * 4u, f2[c]);
-        }
+        if constexpr (!W2L) load_w2();
     };
     if constexpr (!WL) load_weights();
 
@@ -213,6 +223,7 @@ __global__ __launch_bounds__(256) void k_norm_rows(NormArgs a) {
             }
         }
         row_sums<W, R>(ss, s1);
+        if constexpr (W2L) load_w2();
         float inv[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) inv[r] = rms_inv_hw(ss[r], n, a.eps);
@@ -314,6 +325,9 @@ __global__ __launch_bounds__(256) void k_norm_rows(NormArgs a) {
             if (r == 0) load_weights();
         }
         ss = row_sum<W>(ss, slot1);
+        if constexpr (W2L) {
+            if (r == 0) load_w2();
+        }
         const float inv = rms_inv_hw(ss, n, a.eps);
 
         if constexpr (MODE == M_NORM || MODE == M_ADD_NORM) {
