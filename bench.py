@@ -162,6 +162,36 @@ def op_streams(name, L):
             "norm_add_norm_next": (2, 2, L.x, L.fo, L.x, L.xb)}.get(name)
 
 
+def op_copies(name, L):
+    """(source, destination, bytes) pairs of an op whose streams differ in size, over its own
+    buffers: the QK op reads Q, K and V and writes Q in place and K / V into the caches (rows
+    0 .. T-1 of layer 0, where the benchmark's op writes them). None for the other ops."""
+    if name != "qk_norm_rope_kv":
+        return None
+    s, es = L.shape, L.esize
+    qb, kb = L.T * s.nh * s.D * es, L.T * s.nkv * s.D * es
+    return [(L.q, L.q, qb), (L.k, L.kc, kb), (L.v, L.vc, kb)]
+
+
+def stream_copies_on(dev, sets, name, n_launch=100):
+    """op_copies' pairs copied by the reference streaming kernel's copies form (one launch;
+    every shape, pair by pair and interleaved), over the op's own buffer sets in the op's
+    rotation. Returns (us, shape, interleaved)."""
+    best = (float("inf"), -1, 0)
+    for ilv in (0, 1):
+        for shp in range(dev.b.hip_stream_ref_shapes()):
+            def fn(d, L, shp=shp, ilv=ilv):
+                args = []
+                for src, dst, nb in op_copies(name, L):
+                    args += [src.ptr, dst.ptr, nb]
+                rc = d.b.hip_stream_ref_copies(*args, ilv, shp, d.stream)
+                if rc != 0:
+                    raise RuntimeError(f"hip_stream_ref_copies: {rc}")
+            us = time_launches_us(dev, fn, sets, max(n_launch, 4 * len(sets)))
+            best = min(best, (us, shp, ilv))
+    return best
+
+
 def stream_ceiling_on(dev, sets, name, nbytes, n_launch=100):
     """The op's ceiling over its own buffers: the fastest shape of the reference streaming
     kernel reading and writing the very tensors the op reads and writes (same sets, same
@@ -336,9 +366,9 @@ def bench_prefill(dev, shape, T, dtype, steps, warmup, ops_launches=100, thetas=
     ms_f = chain_ms(steps, True, steps)
 
     # Ceilings, after every timing above (the streaming kernel overwrites the op's tensors).
-    # ceiling: over the op's own buffers where its streams are equal-sized tensors, else (QK)
-    # over buffer sets of the streaming kernel's own, at least as many as the op rotates;
-    # ceiling_separate: always the latter, for comparison.
+    # ceiling: over the op's own buffers (the QK op's three streams of different sizes by the
+    # streaming kernel's copies form); ceiling_separate: over buffer sets of the streaming
+    # kernel's own at the op's byte mix, at least as many as the op rotates, for comparison.
     separate = {}
     for name in op_names:
         r_, w_, per_stream, inplace = mix[name]
@@ -352,6 +382,12 @@ def bench_prefill(dev, shape, T, dtype, steps, warmup, ops_launches=100, thetas=
             ceil = {"us": round(cu, 3), "reads": r_, "writes": w_, "bytes_per_stream": per_stream, "shape": cshape,
                     "form": "op buffers" + (", in place" if inplace else ""),
                     "GBps": round((r_ + w_) * per_stream / cu / 1e3, 1)}
+        elif op_copies(name, sets[0]) is not None:
+            cu, cshape, ilv = stream_copies_on(dev, sets, name)
+            pairs = [nb for _, _, nb in op_copies(name, sets[0])]
+            ceil = {"us": round(cu, 3), "pairs_bytes": pairs, "shape": cshape,
+                    "form": "op buffers: Q in place, K / V into the caches" + (", interleaved" if ilv else ""),
+                    "GBps": round(2 * sum(pairs) / cu / 1e3, 1)}
         else:
             cu, ceil = su, dict(sep)
         us = ops[name]["us"]

@@ -433,6 +433,14 @@ void hip_ple_ctx_fuse(float* ctx_ple_buf, const float* ctx_scratch, int n, int a
 int hip_stream_ref_shapes(void);
 int hip_stream_ref(int n_in, int n_out, const void* in0, const void* in1 /*NULL*/, void* out0, void* out1 /*NULL*/,
                    int64_t bytes, int shape, HipStream_t stream);
+/* The same kernel copying up to three pairs in one launch, dst_p = src_p over bytes_p      */
+/* (a multiple of 16, 16-byte aligned buffers; bytes_p == 0: pair unused, pointers may be */
+/* NULL; dst_p may equal src_p), for byte mixes whose streams differ in size (the QK op:  */
+/* Q in place, K and V into the caches). interleave != 0: the pairs' workgroups are       */
+/* interleaved in proportion to their sizes, else pair by pair. Returns 0 or an error.    */
+int hip_stream_ref_copies(const void* src0, void* dst0, int64_t bytes0, const void* src1 /*NULL*/,
+                          void* dst1 /*NULL*/, int64_t bytes1, const void* src2 /*NULL*/, void* dst2 /*NULL*/,
+                          int64_t bytes2, int interleave, int shape, HipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -55,3 +55,21 @@ def test_op_streams_match_mixes():
         assert (i1 is not None) == (n_in == 2) and (o1 is not None) == (n_out == 2), name
         assert (o0 is i0) == inplace, name
     assert covered == 6
+
+
+def test_qk_copies_match_op_bytes():
+    """The QK ceiling's copies read and write the QK op's activation bytes (its algorithmic
+    bytes less the two norm-weight rows and the positions): Q in place, K / V to the caches."""
+    class L:
+        pass
+    s, T = LY.GEMMA_4B, 2048
+    lb = L()
+    lb.shape, lb.T, lb.esize = s, T, 2
+    for name in ("q", "k", "v", "kc", "vc"):
+        setattr(lb, name, object())
+    pairs = bench.op_copies("qk_norm_rope_kv", lb)
+    assert [(a is lb.q, b is lb.q) for a, b, _ in pairs][0] == (True, True)
+    assert pairs[1][0] is lb.k and pairs[1][1] is lb.kc and pairs[2][0] is lb.v and pairs[2][1] is lb.vc
+    algo = LY.op_bytes(s, T, 2, pos_array=True)["qk_norm_rope_kv"] - 2 * 4 * s.D - 4 * T
+    assert 2 * sum(nb for _, _, nb in pairs) == algo
+    assert bench.op_copies("geglu", lb) is None

@@ -137,6 +137,7 @@ SIGNATURES = {
     # measurement: streaming ceiling of a byte mix (new)
     "hip_stream_ref_shapes": (_i, []),
     "hip_stream_ref": (_i, [_i, _i, _v, _v, _v, _v, _i64, _i, _v]),
+    "hip_stream_ref_copies": (_i, [_v, _v, _i64, _v, _v, _i64, _v, _v, _i64, _i, _i, _v]),
     # per-layer embedding steps (cuda_bridge.h:171-172)
     "hip_ple_gate_gelu": (None, [_v, _v, _v, _i, _v]),
     "hip_ple_ctx_fuse": (None, [_v, _v, _i, _i, _v]),

@@ -153,6 +153,7 @@ pub extern "c" fn hip_ple_ctx_fuse(ctx_ple_buf: [*]f32, ctx_scratch: [*]const f3
 // measurement: the streaming ceiling of a byte mix
 pub extern "c" fn hip_stream_ref_shapes() c_int;
 pub extern "c" fn hip_stream_ref(n_in: c_int, n_out: c_int, in0: ?*const anyopaque, in1: ?*const anyopaque, out0: ?*anyopaque, out1: ?*anyopaque, bytes: i64, shape: c_int, stream: HipStream_t) c_int;
+pub extern "c" fn hip_stream_ref_copies(src0: ?*const anyopaque, dst0: ?*anyopaque, bytes0: i64, src1: ?*const anyopaque, dst1: ?*anyopaque, bytes1: i64, src2: ?*const anyopaque, dst2: ?*anyopaque, bytes2: i64, interleave: c_int, shape: c_int, stream: HipStream_t) c_int;
 
 // ---------------------------------------------------------------------------------------
 // Reference names (cuda.zig:5-181): what cuda_model.zig, engine.zig, backend.zig and
