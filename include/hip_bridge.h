@@ -291,8 +291,9 @@ void hip_gemm(int qtype, const void* weights, const float* x, float* y, int batc
  * gelu_tanh(W_r . x_b) * (U_r . x_b), the reference's two prefill GEMMs and k_geglu
  * (cuda_model.zig:1372-1387) in one launch. bf16 activations are exact matrix-core operands
  * (one term), so a bf16 norm output feeds the product directly. Q4_0, Q8_0, F16, BF16, F32
- * weights; cols % 32 == 0; x 16-byte aligned; 128 * cols * sizeof(x element) < 4 GiB; else
- * EUNSUPPORTED. f32 x and y without up_weights is hip_gemm. */
+ * weights with cols % 32 == 0, Q4_K and Q6_K with cols % 256 == 0; x 16-byte aligned;
+ * 128 * cols * sizeof(x element) < 4 GiB; else EUNSUPPORTED. f32 x and y without
+ * up_weights is hip_gemm (which takes the matrix cores from 32 tokens for these types). */
 void hip_gemm_ex(int qtype, const void* weights, const void* up_weights /*NULL*/, int x_dtype,
                  const void* x, int y_dtype, void* y, int batch_size, int rows, int cols,
                  HipStream_t stream);

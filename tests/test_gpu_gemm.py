@@ -1,8 +1,8 @@
 """Prefill-sized GEMM on the matrix cores (hip_gemm with batch >= 32: gemm.hip) against
 float64 and the oracle's math.gemm (math.zig:440-616), through the C-ABI.
 
-The activations are split into three bf16 terms and the weights into one (Q4_0, Q8_0, BF16),
-two (F16) or three (F32) exact bf16 terms, so
+The activations are split into three bf16 terms and the weights into one (Q4_0, Q8_0, BF16,
+Q4_K), two (F16, Q6_K) or three (F32) exact bf16 terms, so
   * integer-valued operands give the exact integer dot product, bit for bit (every term but
     the first is zero and every partial sum is exact): indexing, nibble order, block scales,
     ragged tiles in both dimensions, the two workgroup shapes;
@@ -134,7 +134,7 @@ def _gelu64(g):
     return 0.5 * g * (1.0 + np.tanh(0.7978845608 * (g + 0.044715 * g ** 3)))
 
 
-@pytest.mark.parametrize("qtype", [B.Q4_0, B.Q8_0, B.BF16])
+@pytest.mark.parametrize("qtype", [B.Q4_0, B.Q8_0, B.BF16, B.Q4_K, B.Q6_K])
 @pytest.mark.parametrize("x_dtype,y_dtype", [(B.BF16, B.BF16), (B.BF16, B.F32), (B.F32, B.F32)])
 @pytest.mark.parametrize("rows,cols,batch", [(320, 256, 96), (1000, 512, 200), (2560, 2560, 2048)])
 def test_gemm_ex_geglu_pair(dev, oracle, qtype, x_dtype, y_dtype, rows, cols, batch):
@@ -223,3 +223,133 @@ def test_gemm_ex_split_terms_equal_f32_product(dev, qtype, rows, cols, batch):
         d_u = dev.from_numpy(np.ascontiguousarray(raw_u).reshape(-1))
         dev.gemmEx(qtype, d_w, d_u, B.F32_TERMS, d_p, B.F32, d_y, batch, rows, cols)
         np.testing.assert_array_equal(d_y.to_numpy((batch, rows), np.float32), a)
+
+
+# ---- K-quant weights (Q4_K, Q6_K) on the matrix cores --------------------------------------
+# Q4_K: quants 0..15 exact in bf16, each 32-column sub-block's partial sum scaled by d * sc_j
+# and the min term dmin * m_j * sum(x) subtracted (the x sums formed while staging); Q6_K:
+# sc * (u - 32) as two exact bf16 terms, the super-block's d scaling each partial sum.
+
+KTYPES = [B.Q4_K, B.Q6_K]
+
+
+@pytest.mark.parametrize("qtype", KTYPES)
+@pytest.mark.parametrize("rows,cols,batch", [(128, 256, 32), (200, 512, 37), (129, 2560, 128), (77, 768, 300),
+                                             (4096, 256, 2048), (4100, 256, 2050), (4096, 256, 1024),
+                                             (2560, 512, 2048), (2500, 256, 1900)])
+def test_gemm_mfma_kquant_integer_bitexact(dev, qtype, rows, cols, batch):
+    """Integer-valued K-quant weights and activations: the exact integer dot product, f32 and
+    bf16 activations alike (every tile shape, ragged tiles, tokens and rows past the ends)."""
+    raw, wd = int_matrix(qtype, rows, cols, seed=rows * cols + qtype + batch, scale_pow=-1)
+    X = np.random.default_rng(batch).integers(-3, 4, (batch, cols)).astype(np.float32)
+    exact = X.astype(np.float64) @ wd.T
+    assert np.all(np.abs(exact) < 2 ** 24)
+    got = run(dev, qtype, raw, X, rows, cols)
+    np.testing.assert_array_equal(got, exact.astype(np.float32), err_msg=f"qtype={qtype} {rows}x{cols} b={batch}")
+    got_b = run_ex(dev, qtype, raw, X, rows, cols, B.BF16, B.F32)
+    np.testing.assert_array_equal(got_b, exact.astype(np.float32), err_msg="bf16 activations")
+
+
+def q6_k_full_scales(rng, rows, cols, d):
+    """Q6_K rows with int8 scales over their whole range (-128..127), so sc * (u - 32) spans
+    13 bits and needs both bf16 terms; packed by the format description: super-block {ql[128],
+    qh[64], scales[16], f16 d}, column c = 128 h + 32 k + l takes nibble k // 2 of
+    ql[64 h + 32 (k % 2) + l], bits 2k, 2k + 1 of qh[32 h + l] and scale c // 16."""
+    nsb = cols // 256
+    u = rng.integers(0, 64, (rows, nsb, 256))
+    sc = rng.integers(-128, 128, (rows, nsb, 16))
+    raw = np.zeros((rows, nsb, 210), np.uint8)
+    ql = np.zeros((rows, nsb, 128), np.int64)
+    qh = np.zeros((rows, nsb, 64), np.int64)
+    for c in range(256):
+        h, i = divmod(c, 128)
+        k, l = divmod(i, 32)
+        ql[..., 64 * h + 32 * (k % 2) + l] |= (u[..., c] & 15) << (4 * (k // 2))
+        qh[..., 32 * h + l] |= (u[..., c] >> 4) << (2 * k)
+    raw[..., 0:128] = ql.astype(np.uint8)
+    raw[..., 128:192] = qh.astype(np.uint8)
+    raw[..., 192:208] = sc.astype(np.int8).view(np.uint8)
+    raw[..., 208:210] = np.frombuffer(np.float16(d).tobytes(), np.uint8)
+    val = d * np.repeat(sc, 16, axis=-1) * (u - 32)
+    return raw.reshape(rows, -1), val.reshape(rows, cols).astype(np.float64)
+
+
+@pytest.mark.parametrize("rows,cols,batch", [(130, 512, 64), (300, 256, 257)])
+def test_gemm_mfma_q6_k_full_scale_range_exact(dev, rows, cols, batch):
+    """sc * (u - 32) up to 4096 in magnitude (13 bits) is carried exactly by its two bf16
+    terms: integer products with full-range scales are exact."""
+    raw, wd = q6_k_full_scales(np.random.default_rng(rows), rows, cols, 0.5)
+    X = np.random.default_rng(batch).integers(-1, 2, (batch, cols)).astype(np.float32)
+    exact = X.astype(np.float64) @ wd.T
+    assert np.all(np.abs(exact) < 2 ** 24) and np.max(np.abs(wd)) > 1000
+    np.testing.assert_array_equal(run(dev, B.Q6_K, raw, X, rows, cols), exact.astype(np.float32))
+    np.testing.assert_array_equal(run_ex(dev, B.Q6_K, raw, X, rows, cols, B.BF16, B.F32), exact.astype(np.float32))
+
+
+@pytest.mark.parametrize("qtype", KTYPES)
+@pytest.mark.parametrize("rows,cols,batch", [(256, 2560, 128), (300, 1024, 77), (1024, 2560, 512),
+                                             (128, 10240, 64), (4096, 512, 2048), (2560, 1024, 2048)])
+def test_gemm_mfma_kquant_vs_f64_and_oracle(dev, oracle, qtype, rows, cols, batch):
+    """Random K-quant weights and N(0, 2) activations: within 2^-20 * sum |w_i x_i| of the
+    float64 product of the dequantised weights, as is the oracle's math.gemm."""
+    raw, wd = random_matrix(qtype, rows, cols, seed=rows + cols + batch + 5)
+    X = synth.normal_f32(rows + batch + 5, "Xk", (batch, cols), 0, 2)
+    exact = X.astype(np.float64) @ wd.T
+    bd = bound(wd, X)
+    got = run(dev, qtype, raw, X, rows, cols).astype(np.float64)
+    assert np.all(np.abs(got - exact) <= bd), float(np.max(np.abs(got - exact) / bd))
+    if rows * cols * batch <= 1 << 27:
+        ref = oracle.gemm(qtype, raw, X).astype(np.float64)
+        assert np.all(np.abs(ref - exact) <= bd)
+
+
+@pytest.mark.parametrize("qtype", KTYPES)
+@pytest.mark.parametrize("rows,cols,batch", [(256, 2560, 128), (1024, 2560, 512), (4096, 512, 2048)])
+def test_gemm_ex_kquant_bf16_activations_vs_f64(dev, qtype, rows, cols, batch):
+    """bf16 activations (one exact term) with K-quant weights, f32 and bf16 output."""
+    raw, wd = random_matrix(qtype, rows, cols, seed=rows + cols + batch + 6)
+    Xf = O.get().bf16_to_f32(bf16_bits(synth.normal_f32(rows + batch + 6, "Xkb", (batch, cols), 0, 2)))
+    exact = Xf.astype(np.float64) @ wd.T
+    bd = bound(wd, Xf)
+    got = run_ex(dev, qtype, raw, Xf, rows, cols, B.BF16, B.F32).astype(np.float64)
+    assert np.all(np.abs(got - exact) <= bd), float(np.max(np.abs(got - exact) / bd))
+    got16 = O.get().bf16_to_f32(run_ex(dev, qtype, raw, Xf, rows, cols, B.BF16, B.BF16)).astype(np.float64)
+    tol16 = bd + np.spacing(np.abs(exact).astype(np.float32)).astype(np.float64) * 65536.0
+    assert np.all(np.abs(got16 - exact) <= tol16)
+
+
+@pytest.mark.parametrize("qtype", KTYPES)
+@pytest.mark.parametrize("rows,cols,batch", [(256, 2560, 128), (4096, 512, 2048), (129, 256, 40)])
+def test_gemm_ex_kquant_split_terms_and_geglu(dev, qtype, rows, cols, batch):
+    """Pre-split activations (F32_TERMS) give hip_gemm's f32 product bit for bit, and the
+    gate.up GeGLU pair on them equals the pair on the f32 activations."""
+    raw, _ = random_matrix(qtype, rows, cols, seed=rows + cols + batch + 7)
+    raw_u, _ = random_matrix(qtype, rows, cols, seed=rows + cols + batch + 8)
+    X = synth.normal_f32(rows + batch + 7, "Xks", (batch, cols), 0, 3)
+    ref = run(dev, qtype, raw, X, rows, cols)
+    d_p = dev.alloc(3 * batch * cols * 2)
+    dev.splitTerms(dev.from_numpy(X.reshape(-1)), d_p, batch * cols)
+    d_w = dev.from_numpy(np.ascontiguousarray(raw).reshape(-1))
+    d_u = dev.from_numpy(np.ascontiguousarray(raw_u).reshape(-1))
+    d_y = dev.alloc(batch * rows * 4)
+    d_y.fill(0xAB)
+    dev.gemmEx(qtype, d_w, None, B.F32_TERMS, d_p, B.F32, d_y, batch, rows, cols)
+    np.testing.assert_array_equal(d_y.to_numpy((batch, rows), np.float32), ref)
+    pair = run_ex(dev, qtype, raw, X, rows, cols, B.F32, B.F32, raw_up=raw_u)
+    dev.gemmEx(qtype, d_w, d_u, B.F32_TERMS, d_p, B.F32, d_y, batch, rows, cols)
+    np.testing.assert_array_equal(d_y.to_numpy((batch, rows), np.float32), pair)
+
+
+def test_gemm_kquant_refuses_partial_super_blocks(dev):
+    """K-quant rows that are not whole 256-column super-blocks are refused by hip_gemm_ex
+    (nothing written)."""
+    w, x, y = dev.alloc(1 << 16), dev.alloc(1 << 16), dev.alloc(64 * 64 * 4)
+    y.fill(0x11)
+    dev.strict = False
+    try:
+        for qt in KTYPES:
+            dev.gemmEx(qt, w, None, B.BF16, x, B.F32, y, 64, 64, 224)
+            assert dev.b.last_error() == B.EUNSUPPORTED
+    finally:
+        dev.strict = True
+    assert np.all(y.to_numpy((64 * 64 * 4,), np.uint8) == 0x11)

@@ -19,7 +19,15 @@
 //     (q * d) * x products are all exact-integer-times-f16 values, so applying d after the sum
 //     changes only the f32 rounding);
 //   BF16 weights are exact; F16 weights (11 significant bits) are hi + lo, both exact in bf16;
-//   F32 weights are split like x.
+//   F32 weights are split like x;
+//   Q4_K (math.zig:440-496): a 32-column block is one sub-block j of a 256-column
+//     super-block, value q * (d * sc_j) - dmin * m_j with q in 0..15 (exact in bf16): the
+//     block's partial sum_k q_k x_k is scaled by A_j = d * sc_j and the min term
+//     B_j * sum_k x_k subtracted, with the per-token sums of x formed while staging x (the
+//     decode GEMV's decomposition);
+//   Q6_K (math.zig:556-616): value d * sc * (u - 32) with an int8 scale per 16 columns;
+//     sc * (u - 32) (at most 13 significant bits) is hi + lo, both exact in bf16, and the
+//     super-block's d scales the block's partial sum.
 // The products of the terms are accumulated down to relative weight 2^-16 (h*w_hi, m*w_hi,
 // l*w_hi, and for F16 / F32 the cross terms of the same size); the dropped ones are below
 // 2^-24 of a product, so a dot product lies within the f32 rounding of the sum, like the
@@ -59,11 +67,16 @@ constexpr int kLdsRow = 40;   // bf16 per LDS row: 32 + 8 padding (80 bytes)
 // activations 333 -> 438 us and with bf16 ones 191 -> 213 us for 10240 x 2560 x 2048.)
 template <int QT>
 constexpr int w_terms() {
-    return QT == HIP_BRIDGE_F16 ? 2 : QT == HIP_BRIDGE_F32 ? 3 : 1;
+    return QT == HIP_BRIDGE_F16 || QT == HIP_BRIDGE_Q6_K ? 2 : QT == HIP_BRIDGE_F32 ? 3 : 1;
 }
 template <int QT>
 constexpr bool w_scaled() {
-    return QT == HIP_BRIDGE_Q4_0 || QT == HIP_BRIDGE_Q8_0;
+    return QT == HIP_BRIDGE_Q4_0 || QT == HIP_BRIDGE_Q8_0 || QT == HIP_BRIDGE_Q4_K || QT == HIP_BRIDGE_Q6_K;
+}
+// K-quant super-blocks: 8 K steps of 32 columns each
+template <int QT>
+constexpr bool k_quant() {
+    return QT == HIP_BRIDGE_Q4_K || QT == HIP_BRIDGE_Q6_K;
 }
 
 // bf16 (RNE) of two floats and the f32 values of the result.
@@ -122,6 +135,14 @@ template <>
 struct WRaw<HIP_BRIDGE_F32> {
     u32x4 v[4];
 };
+template <>
+struct WRaw<HIP_BRIDGE_Q4_K> {  // {d, dmin}, scales[12], qs bytes [16h, 16h + 16) of sub-block j's span
+    uint32_t dm, s[3], q[4], j;
+};
+template <>
+struct WRaw<HIP_BRIDGE_Q6_K> {  // ql / qh bytes of the half's 16 columns, its int8 scale, d
+    uint32_t ql[4], qh[4], sc, d, t;
+};
 
 // 32-bit load from a 2-byte aligned address (block quants sit at offset 2 of 18 / 34-byte
 // blocks): one global_load_dword, which gfx950 serves unaligned.
@@ -131,11 +152,51 @@ __device__ __forceinline__ uint32_t ld_u32_unaligned(const unsigned char* p) {
 }
 
 // `blk` is always a valid block address (the caller clamps it); `ok` false gives zeros, selected
-// after the loads so that no load sits under a branch.
+// after the loads so that no load sits under a branch. K-quants: `blk` is the super-block and
+// `sub` the K step within it (0..7).
 __device__ __forceinline__ u32x4 sel4(bool ok, u32x4 v) { return ok ? v : u32x4{0, 0, 0, 0}; }
 template <int QT>
-__device__ __forceinline__ void load_w(const unsigned char* blk, int h, bool ok, WRaw<QT>& r) {
-    if constexpr (QT == HIP_BRIDGE_Q4_0) {
+__device__ __forceinline__ void load_w(const unsigned char* blk, int sub, int h, bool ok, WRaw<QT>& r) {
+    if constexpr (QT == HIP_BRIDGE_Q4_K) {
+        // 144-byte super-block {f16 d, f16 dmin, scales[12], qs[128]} (types.zig:170-175);
+        // sub-block j's 32 values are the low (j even) or high (j odd) nibbles of
+        // qs[32 (j / 2) .. + 32)
+        uint32_t v[8];
+        v[0] = ld_u32_unaligned(blk);
+#pragma unroll
+        for (int i = 0; i < 3; ++i) v[1 + i] = ld_u32_unaligned(blk + 4 + 4 * i);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[4 + i] = ld_u32_unaligned(blk + 16 + 32 * (sub >> 1) + 16 * h + 4 * i);
+        r.dm = ok ? v[0] : 0u;
+#pragma unroll
+        for (int i = 0; i < 3; ++i) r.s[i] = ok ? v[1 + i] : 0u;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r.q[i] = ok ? v[4 + i] : 0u;
+        r.j = (uint32_t)sub;
+    } else if constexpr (QT == HIP_BRIDGE_Q6_K) {
+        // 210-byte super-block {ql[128], qh[64], int8 scales[16], f16 d} (types.zig:187-192).
+        // K step sub = 4 n + t covers values [128 n + 32 t, + 32): value l of it takes the
+        // low (t < 2) or high nibble of ql[64 n + 32 (t & 1) + l], bits 2t, 2t + 1 of
+        // qh[32 n + l] and scale sc[8 n + l / 16 + 2 t] (quant.zig:357-385); the half h is
+        // l in [16 h, 16 h + 16), one scale
+        const int n = sub >> 2, t = sub & 3;
+        uint32_t ql[4], qh[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            ql[i] = ld_u32_unaligned(blk + 64 * n + 32 * (t & 1) + 16 * h + 4 * i);
+            qh[i] = ld_u32_unaligned(blk + 128 + 32 * n + 16 * h + 4 * i);
+        }
+        const uint32_t scw = *(const uint16_t*)(blk + 192 + 8 * n + 2 * t);  // scales 8n+2t, +1
+        const uint32_t d = *(const uint16_t*)(blk + 208);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            r.ql[i] = ok ? ql[i] : 0u;
+            r.qh[i] = ok ? qh[i] : 0u;
+        }
+        r.sc = ok ? (scw >> (8 * h)) & 0xffu : 0u;
+        r.d = ok ? d : 0u;
+        r.t = (uint32_t)t;
+    } else if constexpr (QT == HIP_BRIDGE_Q4_0) {
         const uint32_t d = *(const uint16_t*)blk, q0 = ld_u32_unaligned(blk + 2 + 8 * h),
                        q1 = ld_u32_unaligned(blk + 6 + 8 * h);
         r.d = ok ? d : 0u;
@@ -165,10 +226,56 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
 // Convert the thread's half row into bf16 terms: sw[t][row][...]; a block scale goes into the
 // padding of the row's first plane (bf16 slots 32, 33: kScaleSlot).
 constexpr int kScaleSlot = 32;
+constexpr int kMinSlot = 34;  // Q4_K: the block's min factor B_j = dmin * m_j (bf16 slots 34, 35)
 template <int QT>
 __device__ __forceinline__ void store_w(const WRaw<QT>& r, int h, uint16_t* sw, int plane, int row) {
     uint16_t* dst = sw + row * kLdsRow;
-    if constexpr (QT == HIP_BRIDGE_Q4_0) {
+    if constexpr (QT == HIP_BRIDGE_Q4_K) {
+        // 6-bit scale and min of sub-block j (quant.zig:285-290): j < 4: scales[j] & 63 and
+        // scales[j + 4] & 63; else the low / high nibble of scales[j + 4] with the top two
+        // bits of scales[j - 4] / scales[j] above them
+        const uint32_t j = r.j, b = 8u * (j & 3u);
+        const uint32_t s0 = (r.s[0] >> b) & 0xffu, s1 = (r.s[1] >> b) & 0xffu, s2 = (r.s[2] >> b) & 0xffu;
+        const uint32_t sc = j < 4 ? (s0 & 63u) : ((s2 & 15u) | ((s0 >> 6) << 4));
+        const uint32_t m = j < 4 ? (s1 & 63u) : ((s2 >> 4) | ((s1 >> 6) << 4));
+        *reinterpret_cast<float*>(dst + kScaleSlot) = f16_bits_to_f32(r.dm & 0xffffu) * (float)sc;
+        *reinterpret_cast<float*>(dst + kMinSlot) = f16_bits_to_f32(r.dm >> 16) * (float)m;
+        const int sh = (int)(j & 1u) * 4;
+        uint32_t p[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t v = (r.q[i] >> sh) & 0x0f0f0f0fu;
+            p[2 * i] = pack_bf16x2((float)(v & 0xffu), (float)((v >> 8) & 0xffu));
+            p[2 * i + 1] = pack_bf16x2((float)((v >> 16) & 0xffu), (float)(v >> 24));
+        }
+        *reinterpret_cast<u32x4*>(dst + 16 * h) = u32x4{p[0], p[1], p[2], p[3]};
+        *reinterpret_cast<u32x4*>(dst + 16 * h + 8) = u32x4{p[4], p[5], p[6], p[7]};
+    } else if constexpr (QT == HIP_BRIDGE_Q6_K) {
+        *reinterpret_cast<float*>(dst + kScaleSlot) = f16_bits_to_f32(r.d);  // both halves store it
+        const float sc = (float)(int8_t)(uint8_t)r.sc;
+        const int nsh = r.t < 2 ? 0 : 4, hsh = 2 * (int)r.t;
+        uint32_t t[2][8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t u = ((r.ql[i] >> (8 * e + nsh)) & 15u) | (((r.qh[i] >> (8 * e + hsh)) & 3u) << 4);
+                v[e] = sc * (float)((int)u - 32);  // an integer of at most 13 bits: exact
+            }
+            uint32_t s2[2];
+            split2(v[0], v[1], s2);
+            t[0][2 * i] = s2[0], t[1][2 * i] = s2[1];
+            split2(v[2], v[3], s2);
+            t[0][2 * i + 1] = s2[0], t[1][2 * i + 1] = s2[1];
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            uint16_t* d = sw + u * plane + row * kLdsRow + 16 * h;
+            *reinterpret_cast<u32x4*>(d) = u32x4{t[u][0], t[u][1], t[u][2], t[u][3]};
+            *reinterpret_cast<u32x4*>(d + 8) = u32x4{t[u][4], t[u][5], t[u][6], t[u][7]};
+        }
+    } else if constexpr (QT == HIP_BRIDGE_Q4_0) {
         *reinterpret_cast<float*>(dst + kScaleSlot) = f16_bits_to_f32(r.d);  // both halves store it
         // byte j: low nibble = element j, high nibble = element j + 16 (value u - 8, exact)
         uint32_t lo[4], hi[4];
@@ -299,7 +406,8 @@ template <int QT, int XK, int WT, int WR>
 constexpr int gemm_wgs_per_cu() {
     constexpr int bt = 64 * WT, br = 64 * WR;
     constexpr int oper = (bt + w_terms<QT>() * br) * kLdsRow * 2;  // bf16 activations: one term
-    return XK == X_BF16 && 2 * oper * 3 <= 160 * 1024 ? 3 : 2;
+    // (Q4_K's min term needs the registers: held to 170 its loop spills)
+    return XK == X_BF16 && QT != HIP_BRIDGE_Q4_K && 2 * oper * 3 <= 160 * 1024 ? 3 : 2;
 }
 
 template <int QT, int XK, int WT, int WR, bool GE, bool YB>
@@ -313,14 +421,24 @@ __global__ __launch_bounds__(kGemmThreads, (gemm_wgs_per_cu<QT, XK, WT, WR>())) 
     constexpr int XPLANE = BT * kLdsRow, WPLANE = BR * kLdsRow;
     constexpr int OPER_BYTES = (XT * XPLANE + NW * WPLANE) * 2;
     // Two operand buffers (block kb read while block kb + 1 is written: one barrier per step)
-    // when they fit two workgroups per CU in the 160 KB of LDS; else one.
-    constexpr bool DB = 2 * OPER_BYTES <= 80 * 1024 && (XK != X_F32 || ZL_GEMM_DB_F32X);
+    // when they fit two workgroups per CU in the 160 KB of LDS; else one (also for Q4_K with
+    // three activation planes, whose two-buffer loop needs 284 registers: one wave per SIMD).
+    constexpr bool DB = 2 * OPER_BYTES <= 80 * 1024 && (XK != X_F32 || ZL_GEMM_DB_F32X) &&
+                        !(QT == HIP_BRIDGE_Q4_K && XK == X_TERMS);
     constexpr int NBUF = DB ? 2 : 1;
     constexpr int XCH_BYTES = GE ? 2 * WT * WR * 16 * kWave * 4 : 0;  // up accumulators, two waves
-    __shared__ __attribute__((aligned(16)))
-    unsigned char s_raw[NBUF * OPER_BYTES > XCH_BYTES ? NBUF * OPER_BYTES : XCH_BYTES];
+    // Q4_K: per-token sums of each K step's activations, one per activation term (f32 x:
+    // of its three terms h, m, l, summed in the same order as pre-split planes, so both forms
+    // give the same products bit for bit), in two slots by step parity: step kb + 1's sums are
+    // written while step kb's are read
+    constexpr bool MIN = QT == HIP_BRIDGE_Q4_K;
+    constexpr int XSP = XT;  // sum planes
+    constexpr int XS_FLOATS = MIN ? 2 * XSP * BT : 0;
+    constexpr int MAIN_BYTES = NBUF * OPER_BYTES > XCH_BYTES ? NBUF * OPER_BYTES : XCH_BYTES;
+    __shared__ __attribute__((aligned(16))) unsigned char s_raw[MAIN_BYTES + XS_FLOATS * 4];
     auto sx_of = [&](int b) { return reinterpret_cast<uint16_t*>(s_raw + b * OPER_BYTES); };
     auto sw_of = [&](int b) { return reinterpret_cast<uint16_t*>(s_raw + b * OPER_BYTES) + XT * XPLANE; };
+    float* const s_xs = reinterpret_cast<float*>(s_raw + MAIN_BYTES);  // [slot][plane][token]
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -361,22 +479,35 @@ __global__ __launch_bounds__(kGemmThreads, (gemm_wgs_per_cu<QT, XK, WT, WR>())) 
             xr[i] = bldp<POL_DEFAULT>(rsx[pl], off);
         }
     };
-    auto store_x = [&](int buf) {
+    auto store_x = [&](int buf, int slot) {
         uint16_t* const sx = sx_of(buf);
 #pragma unroll
         for (int i = 0; i < XCH; ++i) {
             constexpr int PC = BT * XCPT;
             const int pl = kGemmThreads * i / PC, cc = tid + kGemmThreads * i % PC;
             const int tok = cc / XCPT, k = XE * (cc % XCPT);
+            // (MIN) the token's sum over the step's 32 columns of one term: pairs, then the
+            // XCPT consecutive lanes holding its chunks (8 of 4 f32 or 4 of 8 bf16: the same
+            // tree over the 32 values)
+            auto put_sum = [&](float cs, int plane) {
+                cs = group_sum<XCPT>(cs);
+                if (cc % XCPT == 0) s_xs[(slot * XSP + plane) * BT + tok] = cs;
+            };
             if constexpr (XK == X_F32) {
                 uint32_t t0[3], t1[3];
                 split3(__uint_as_float(xr[i].x), __uint_as_float(xr[i].y), t0);
                 split3(__uint_as_float(xr[i].z), __uint_as_float(xr[i].w), t1);
 #pragma unroll
-                for (int u = 0; u < 3; ++u)
+                for (int u = 0; u < 3; ++u) {
                     *reinterpret_cast<u32x2*>(sx + u * XPLANE + tok * kLdsRow + k) = u32x2{t0[u], t1[u]};
+                    if constexpr (MIN) put_sum((bf16_lo(t0[u]) + bf16_hi(t0[u])) + (bf16_lo(t1[u]) + bf16_hi(t1[u])), u);
+                }
             } else {
                 *reinterpret_cast<u32x4*>(sx + pl * XPLANE + tok * kLdsRow + k) = xr[i];
+                if constexpr (MIN)
+                    put_sum(((bf16_lo(xr[i].x) + bf16_hi(xr[i].x)) + (bf16_lo(xr[i].y) + bf16_hi(xr[i].y))) +
+                                ((bf16_lo(xr[i].z) + bf16_hi(xr[i].z)) + (bf16_lo(xr[i].w) + bf16_hi(xr[i].w))),
+                            pl);
             }
         }
     };
@@ -384,9 +515,12 @@ __global__ __launch_bounds__(kGemmThreads, (gemm_wgs_per_cu<QT, XK, WT, WR>())) 
     // first 2 BR threads when BR < 128). GE: tile rows [0, OR) are gate rows, [OR, BR) the
     // same rows of the up matrix.
     constexpr int WPASS = BR * 2 >= kGemmThreads ? BR * 2 / kGemmThreads : 1;
-    constexpr int64_t blk_bytes = QT == HIP_BRIDGE_Q4_0 ? 18 : QT == HIP_BRIDGE_Q8_0 ? 34 : QT == HIP_BRIDGE_F32 ? 128 : 64;
+    // bytes per K step (K-quants: per super-block of 8 steps)
+    constexpr int64_t blk_bytes = QT == HIP_BRIDGE_Q4_0 ? 18 : QT == HIP_BRIDGE_Q8_0 ? 34 : QT == HIP_BRIDGE_F32 ? 128
+                                  : QT == HIP_BRIDGE_Q4_K ? 144 : QT == HIP_BRIDGE_Q6_K ? 210 : 64;
     WRaw<QT> wr[WPASS];
     auto load_wt = [&](int kb) {
+        const int64_t boff = k_quant<QT>() ? (int64_t)(kb >> 3) * blk_bytes : (int64_t)kb * blk_bytes;
 #pragma unroll
         for (int i = 0; i < WPASS; ++i) {
             const int hr = tid + kGemmThreads * i, row = hr >> 1, h = hr & 1;
@@ -394,7 +528,7 @@ __global__ __launch_bounds__(kGemmThreads, (gemm_wgs_per_cu<QT, XK, WT, WR>())) 
             const int gr = r_base + (up ? row - OR : row);
             const bool ok = hr < 2 * BR && gr < a.rows;
             const unsigned char* wm = up ? a.wu : a.w;
-            load_w<QT>(wm + (int64_t)min(gr, a.rows - 1) * a.row_bytes + (int64_t)kb * blk_bytes, h, ok, wr[i]);
+            load_w<QT>(wm + (int64_t)min(gr, a.rows - 1) * a.row_bytes + boff, kb & 7, h, ok, wr[i]);
         }
     };
     auto store_wt = [&](int buf) {
@@ -421,7 +555,7 @@ __global__ __launch_bounds__(kGemmThreads, (gemm_wgs_per_cu<QT, XK, WT, WR>())) 
     // One K step: block kb's operands from LDS buffer `buf` into registers, its MFMAs (into the
     // block partial when SCALED), then `convert` (block kb + 1 into the LDS and the loads of
     // kb + 2), then the block scale products.
-    auto step = [&](int buf, bool single, auto convert) {
+    auto step = [&](int buf, int slot, bool single, auto convert) {
         const uint16_t* const sx = sx_of(buf);
         const uint16_t* const sw = sw_of(buf);
         // with one buffer every wave holds all of block kb's operands before the barrier;
@@ -429,7 +563,7 @@ __global__ __launch_bounds__(kGemmThreads, (gemm_wgs_per_cu<QT, XK, WT, WR>())) 
         // registers)
         constexpr int KH = DB ? 1 : 2;
         bf16x8 xa[KH][WT][XT], wb[KH][WR][NW];
-        float dv[WR];
+        float dv[WR], bv[MIN ? WR : 1];
         auto read_ops = [&](int ks, int slot) {
             const int ko = 16 * ks + 8 * (lane >> 5);
 #pragma unroll
@@ -462,8 +596,11 @@ __global__ __launch_bounds__(kGemmThreads, (gemm_wgs_per_cu<QT, XK, WT, WR>())) 
         };
         if constexpr (SCALED) {
 #pragma unroll
-            for (int j = 0; j < WR; ++j)
+            for (int j = 0; j < WR; ++j) {
                 dv[j] = *reinterpret_cast<const float*>(sw + (wr0 + 32 * j + (lane & 31)) * kLdsRow + kScaleSlot);
+                if constexpr (MIN)
+                    bv[j] = *reinterpret_cast<const float*>(sw + (wr0 + 32 * j + (lane & 31)) * kLdsRow + kMinSlot);
+            }
         }
         if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
         if constexpr (DB) {
@@ -481,7 +618,31 @@ __global__ __launch_bounds__(kGemmThreads, (gemm_wgs_per_cu<QT, XK, WT, WR>())) 
         }
         if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
         convert();
-        if constexpr (SCALED) {
+        if constexpr (MIN) {
+            // acc += A_j * part - B_j * (sum of the token's x over the step: its terms' sums
+            // added in order); lane (l, r) of tile i holds token 32 i + 8 (r / 4) + 4 (l / 32) +
+            // r % 4: four runs of four
+#pragma unroll
+            for (int i = 0; i < WT; ++i)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int t0 = wt0 + 32 * i + 8 * q + 4 * (lane >> 5);
+                    f32x4 v = *reinterpret_cast<const f32x4*>(s_xs + slot * XSP * BT + t0);
+#pragma unroll
+                    for (int u = 1; u < XSP; ++u) {
+                        const f32x4 w = *reinterpret_cast<const f32x4*>(s_xs + (slot * XSP + u) * BT + t0);
+                        v.x += w.x, v.y += w.y, v.z += w.z, v.w += w.w;
+                    }
+                    const float xs[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                    for (int j = 0; j < WR; ++j)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int r = 4 * q + e;
+                            acc[i][j][r] = fmaf(dv[j], part[i][j][r], fmaf(-bv[j], xs[e], acc[i][j][r]));
+                        }
+                }
+        } else if constexpr (SCALED) {
 #pragma unroll
             for (int j = 0; j < WR; ++j)
 #pragma unroll
@@ -497,15 +658,15 @@ __global__ __launch_bounds__(kGemmThreads, (gemm_wgs_per_cu<QT, XK, WT, WR>())) 
     // during the conversion rather than after it. Past the end: the last block again, unused.
     load_x(0);
     load_wt(0);
-    store_x(0);
+    store_x(0, 0);
     store_wt(0);
     __syncthreads();
     load_x(min(1, nkb - 1));
     load_wt(min(1, nkb - 1));
     for (int kb = 0; kb < nkb; ++kb) {
         const int cur = DB ? (kb & 1) : 0, nxt = DB ? (cur ^ 1) : 0;
-        step(cur, !DB, [&]() {
-            store_x(nxt);
+        step(cur, kb & 1, !DB, [&]() {
+            store_x(nxt, (kb + 1) & 1);
             store_wt(nxt);
             load_x(min(kb + 2, nkb - 1));
             load_wt(min(kb + 2, nkb - 1));
@@ -586,8 +747,9 @@ static void launch_q(const GemmArgs& a, int xk, bool ge, bool y_bf16, hipStream_
 // 0 = launched; otherwise why not (the caller decides between a fallback and an error).
 int launch_gemm_mfma_ex(int qtype, const void* w, const void* wu, int64_t row_bytes, int x_dtype, const void* x,
                         int y_dtype, void* y, int rows, int cols, int batch, hipStream_t s) {
+    const bool kq = qtype == HIP_BRIDGE_Q4_K || qtype == HIP_BRIDGE_Q6_K;
     const bool types = qtype == HIP_BRIDGE_Q4_0 || qtype == HIP_BRIDGE_Q8_0 || qtype == HIP_BRIDGE_F16 ||
-                       qtype == HIP_BRIDGE_BF16 || qtype == HIP_BRIDGE_F32;
+                       qtype == HIP_BRIDGE_BF16 || qtype == HIP_BRIDGE_F32 || kq;
     if (!types || (x_dtype != HIP_BRIDGE_F32 && x_dtype != HIP_BRIDGE_BF16 && x_dtype != HIP_BRIDGE_F32_TERMS) ||
         (y_dtype != HIP_BRIDGE_F32 && y_dtype != HIP_BRIDGE_BF16))
         return HIP_BRIDGE_EUNSUPPORTED;
@@ -597,7 +759,7 @@ int launch_gemm_mfma_ex(int qtype, const void* w, const void* wu, int64_t row_by
         const uintptr_t wa = reinterpret_cast<uintptr_t>(p);
         return dense ? (wa % 16 == 0 && row_bytes % 16 == 0) : (wa % 2 == 0);
     };
-    if (cols % kKB != 0 || !aligned16(x) || !w_ok(w) || (wu && !w_ok(wu))) return HIP_BRIDGE_EUNSUPPORTED;
+    if (cols % (kq ? 256 : kKB) != 0 || !aligned16(x) || !w_ok(w) || (wu && !w_ok(wu))) return HIP_BRIDGE_EUNSUPPORTED;
     // 32-bit byte offsets within a token tile's activations (per plane)
     if ((int64_t)128 * cols * (x_dtype == HIP_BRIDGE_F32 ? 4 : 2) > 0xffffffffLL) return HIP_BRIDGE_EUNSUPPORTED;
     const GemmArgs a{(const unsigned char*)w, (const unsigned char*)wu, x, y, row_bytes, rows, cols, batch};
@@ -608,6 +770,8 @@ int launch_gemm_mfma_ex(int qtype, const void* w, const void* wu, int64_t row_by
         case HIP_BRIDGE_Q8_0: launch_q<HIP_BRIDGE_Q8_0>(a, xk, ge, yb, s); break;
         case HIP_BRIDGE_F16: launch_q<HIP_BRIDGE_F16>(a, xk, ge, yb, s); break;
         case HIP_BRIDGE_BF16: launch_q<HIP_BRIDGE_BF16>(a, xk, ge, yb, s); break;
+        case HIP_BRIDGE_Q4_K: launch_q<HIP_BRIDGE_Q4_K>(a, xk, ge, yb, s); break;
+        case HIP_BRIDGE_Q6_K: launch_q<HIP_BRIDGE_Q6_K>(a, xk, ge, yb, s); break;
         default: launch_q<HIP_BRIDGE_F32>(a, xk, ge, yb, s); break;
     }
     check_launch();
