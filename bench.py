@@ -667,9 +667,11 @@ def bench_gemm_prefill(dev, T=2048):
     s = LY.GEMMA_4B
     H, I = s.H, s.I
     cases = [("gate_q4_0", B.Q4_0, I, H), ("down_q4_0", B.Q4_0, H, I), ("qkv_q4_0", B.Q4_0, (s.nh + 2 * s.nkv) * s.D, H),
-             ("gate_q8_0", B.Q8_0, I, H), ("gate_bf16", B.BF16, I, H)]
+             ("gate_q8_0", B.Q8_0, I, H), ("gate_bf16", B.BF16, I, H),
+             ("gate_q4_k", B.Q4_K, I, H), ("down_q4_k", B.Q4_K, H, I), ("gate_q6_k", B.Q6_K, I, H),
+             ("down_q6_k", B.Q6_K, H, I)]
     out = {}
-    for name, qt, rows, cols in cases:
+    for name, qt, rows, cols in cases:  # every weight type here is one bf16 term
         r = gemv_case(dev, name, qt, [(rows, cols)],
                       lambda d, m, x, ys, qt=qt, rows=rows, cols=cols: d.gemm(qt, m[0], x, ys[0], T, rows, cols), T)
         tf = 2.0 * rows * cols * T / r["us"] / 1e6
@@ -703,7 +705,8 @@ def bench_gemm_prefill(dev, T=2048):
     # bf16 output, and the gate.up pair with its GeGLU epilogue (two products, one launch).
     # The activation buffer's bytes are read as bf16 (timing only).
     ex_cases = [("gate_q4_0_bf16", B.Q4_0, I, H, False), ("down_q4_0_bf16", B.Q4_0, H, I, False),
-                ("gateup_geglu_q4_0_bf16", B.Q4_0, I, H, True)]
+                ("gateup_geglu_q4_0_bf16", B.Q4_0, I, H, True), ("gate_q4_k_bf16", B.Q4_K, I, H, False),
+                ("gate_q6_k_bf16", B.Q6_K, I, H, False)]
     for name, qt, rows, cols, ge in ex_cases:
         shapes = [(rows, cols)] * (2 if ge else 1)
 

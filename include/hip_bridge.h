@@ -301,8 +301,9 @@ void hip_gemm_ex(int qtype, const void* weights, const void* up_weights /*NULL*/
  * m = bf16(x - h), l = bf16(x - h - m); h + m + l carries x's 24 significant bits), the
  * HIP_BRIDGE_F32_TERMS input of hip_gemm_ex: split once and shared by every product of the
  * same activations (QKV, gate and up), the K loop then converts weights only. The products
- * equal hip_gemm's on the f32 activations bit for bit. n % 4 == 0, x 16-byte and planes
- * 8-byte aligned; else EUNSUPPORTED. */
+ * equal hip_gemm's on the f32 activations bit for bit (Q4_K: within f32 rounding, its min
+ * term summing the planes rather than x). n % 4 == 0, x 16-byte and planes 8-byte aligned;
+ * else EUNSUPPORTED. */
 void hip_split_terms(const float* x, void* planes, int64_t n, HipStream_t stream);
 
 /* ---------------------------------------------------------------------------------- */

@@ -2,7 +2,7 @@
 float64 and the oracle's math.gemm (math.zig:440-616), through the C-ABI.
 
 The activations are split into three bf16 terms and the weights into one (Q4_0, Q8_0, BF16,
-Q4_K), two (F16, Q6_K) or three (F32) exact bf16 terms, so
+Q4_K, Q6_K), two (F16) or three (F32) exact bf16 terms, so
   * integer-valued operands give the exact integer dot product, bit for bit (every term but
     the first is zero and every partial sum is exact): indexing, nibble order, block scales,
     ragged tiles in both dimensions, the two workgroup shapes;
@@ -228,7 +228,7 @@ def test_gemm_ex_split_terms_equal_f32_product(dev, qtype, rows, cols, batch):
 # ---- K-quant weights (Q4_K, Q6_K) on the matrix cores --------------------------------------
 # Q4_K: quants 0..15 exact in bf16, each 32-column sub-block's partial sum scaled by d * sc_j
 # and the min term dmin * m_j * sum(x) subtracted (the x sums formed while staging); Q6_K:
-# sc * (u - 32) as two exact bf16 terms, the super-block's d scaling each partial sum.
+# u - 32 exact in bf16, each 16-column half's partial sum scaled by d * sc.
 
 KTYPES = [B.Q4_K, B.Q6_K]
 
@@ -251,8 +251,8 @@ def test_gemm_mfma_kquant_integer_bitexact(dev, qtype, rows, cols, batch):
 
 
 def q6_k_full_scales(rng, rows, cols, d):
-    """Q6_K rows with int8 scales over their whole range (-128..127), so sc * (u - 32) spans
-    13 bits and needs both bf16 terms; packed by the format description: super-block {ql[128],
+    """Q6_K rows with int8 scales over their whole range (-128..127), so values d * sc * (u -
+    32) span 13 bits; packed by the format description: super-block {ql[128],
     qh[64], scales[16], f16 d}, column c = 128 h + 32 k + l takes nibble k // 2 of
     ql[64 h + 32 (k % 2) + l], bits 2k, 2k + 1 of qh[32 h + l] and scale c // 16."""
     nsb = cols // 256
@@ -276,8 +276,8 @@ def q6_k_full_scales(rng, rows, cols, d):
 
 @pytest.mark.parametrize("rows,cols,batch", [(130, 512, 64), (300, 256, 257)])
 def test_gemm_mfma_q6_k_full_scale_range_exact(dev, rows, cols, batch):
-    """sc * (u - 32) up to 4096 in magnitude (13 bits) is carried exactly by its two bf16
-    terms: integer products with full-range scales are exact."""
+    """Full-range int8 scales (|sc * (u - 32)| up to 4096, 13 bits) and every half's own
+    scale: integer products are exact."""
     raw, wd = q6_k_full_scales(np.random.default_rng(rows), rows, cols, 0.5)
     X = np.random.default_rng(batch).integers(-1, 2, (batch, cols)).astype(np.float32)
     exact = X.astype(np.float64) @ wd.T
@@ -321,10 +321,12 @@ def test_gemm_ex_kquant_bf16_activations_vs_f64(dev, qtype, rows, cols, batch):
 @pytest.mark.parametrize("qtype", KTYPES)
 @pytest.mark.parametrize("rows,cols,batch", [(256, 2560, 128), (4096, 512, 2048), (129, 256, 40)])
 def test_gemm_ex_kquant_split_terms_and_geglu(dev, qtype, rows, cols, batch):
-    """Pre-split activations (F32_TERMS) give hip_gemm's f32 product bit for bit, and the
-    gate.up GeGLU pair on them equals the pair on the f32 activations."""
-    raw, _ = random_matrix(qtype, rows, cols, seed=rows + cols + batch + 7)
-    raw_u, _ = random_matrix(qtype, rows, cols, seed=rows + cols + batch + 8)
+    """Pre-split activations (F32_TERMS) give hip_gemm's f32 product bit for bit for Q6_K; for
+    Q4_K, whose min term sums each plane of the split activations instead of x itself, both
+    lie within the product bound of the float64 product. The gate.up GeGLU pair on the planes
+    equals (Q6_K) or matches within the bound (Q4_K) the pair on the f32 activations."""
+    raw, wd = random_matrix(qtype, rows, cols, seed=rows + cols + batch + 7)
+    raw_u, wu = random_matrix(qtype, rows, cols, seed=rows + cols + batch + 8)
     X = synth.normal_f32(rows + batch + 7, "Xks", (batch, cols), 0, 3)
     ref = run(dev, qtype, raw, X, rows, cols)
     d_p = dev.alloc(3 * batch * cols * 2)
@@ -334,10 +336,24 @@ def test_gemm_ex_kquant_split_terms_and_geglu(dev, qtype, rows, cols, batch):
     d_y = dev.alloc(batch * rows * 4)
     d_y.fill(0xAB)
     dev.gemmEx(qtype, d_w, None, B.F32_TERMS, d_p, B.F32, d_y, batch, rows, cols)
-    np.testing.assert_array_equal(d_y.to_numpy((batch, rows), np.float32), ref)
+    got = d_y.to_numpy((batch, rows), np.float32)
     pair = run_ex(dev, qtype, raw, X, rows, cols, B.F32, B.F32, raw_up=raw_u)
     dev.gemmEx(qtype, d_w, d_u, B.F32_TERMS, d_p, B.F32, d_y, batch, rows, cols)
-    np.testing.assert_array_equal(d_y.to_numpy((batch, rows), np.float32), pair)
+    got_pair = d_y.to_numpy((batch, rows), np.float32)
+    if qtype == B.Q6_K:
+        np.testing.assert_array_equal(got, ref)
+        np.testing.assert_array_equal(got_pair, pair)
+        return
+    g64, u64 = X.astype(np.float64) @ wd.T, X.astype(np.float64) @ wu.T
+    bd_g, bd_u = bound(wd, X), bound(wu, X)
+    assert np.all(np.abs(got.astype(np.float64) - g64) <= bd_g)
+    assert np.all(np.abs(ref.astype(np.float64) - g64) <= bd_g)
+    # the pair, both forms against float64 with test_gemm_ex_geglu_pair's tolerance
+    ref_pair = _gelu64(g64) * u64
+    tol = 1.13 * bd_g * np.abs(u64) + np.abs(_gelu64(g64)) * bd_u + bd_g * bd_u + 1e-5 * np.abs(ref_pair) \
+        + 2.0 ** -22 * np.abs(g64 * u64)
+    assert np.all(np.abs(got_pair.astype(np.float64) - ref_pair) <= tol)
+    assert np.all(np.abs(pair.astype(np.float64) - ref_pair) <= tol)
 
 
 def test_gemm_kquant_refuses_partial_super_blocks(dev):

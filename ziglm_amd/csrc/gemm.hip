@@ -26,8 +26,8 @@
 //     B_j * sum_k x_k subtracted, with the per-token sums of x formed while staging x (the
 //     decode GEMV's decomposition);
 //   Q6_K (math.zig:556-616): value d * sc * (u - 32) with an int8 scale per 16 columns;
-//     sc * (u - 32) (at most 13 significant bits) is hi + lo, both exact in bf16, and the
-//     super-block's d scales the block's partial sum.
+//     u - 32 is exact in bf16 and d * sc (exact in f32) scales each K = 16 half's partial
+//     sum.
 // The products of the terms are accumulated down to relative weight 2^-16 (h*w_hi, m*w_hi,
 // l*w_hi, and for F16 / F32 the cross terms of the same size); the dropped ones are below
 // 2^-24 of a product, so a dot product lies within the f32 rounding of the sum, like the
@@ -65,9 +65,16 @@ constexpr int kLdsRow = 40;   // bf16 per LDS row: 32 + 8 padding (80 bytes)
 // exact terms, F32 three. (Q4_0 products (u - 8) * d are also exact in two bf16 terms, which
 // saves the per-block scale products at twice the MFMAs: measured slower, with f32
 // activations 333 -> 438 us and with bf16 ones 191 -> 213 us for 10240 x 2560 x 2048.)
+// Q6_K: its scale per 16-column half multiplies each K = 16 MFMA half's partial sum, the
+// quants u - 32 one exact term. (sc * (u - 32) as two exact terms with one scale d per step
+// instead: 5 term products, 10240 x 2560 x 2048 with f32 activations 555 against 453 us.)
+template <int QT>
+constexpr bool w_halves() {
+    return QT == HIP_BRIDGE_Q6_K;
+}
 template <int QT>
 constexpr int w_terms() {
-    return QT == HIP_BRIDGE_F16 || QT == HIP_BRIDGE_Q6_K ? 2 : QT == HIP_BRIDGE_F32 ? 3 : 1;
+    return QT == HIP_BRIDGE_F16 ? 2 : QT == HIP_BRIDGE_F32 ? 3 : 1;
 }
 template <int QT>
 constexpr bool w_scaled() {
@@ -251,30 +258,23 @@ __device__ __forceinline__ void store_w(const WRaw<QT>& r, int h, uint16_t* sw, 
         *reinterpret_cast<u32x4*>(dst + 16 * h) = u32x4{p[0], p[1], p[2], p[3]};
         *reinterpret_cast<u32x4*>(dst + 16 * h + 8) = u32x4{p[4], p[5], p[6], p[7]};
     } else if constexpr (QT == HIP_BRIDGE_Q6_K) {
-        *reinterpret_cast<float*>(dst + kScaleSlot) = f16_bits_to_f32(r.d);  // both halves store it
-        const float sc = (float)(int8_t)(uint8_t)r.sc;
+        // the half's scale d * sc (exact) in slot 32 + 2h; quants u - 32, exact in bf16
+        *reinterpret_cast<float*>(dst + kScaleSlot + 2 * h) = f16_bits_to_f32(r.d) * (float)(int8_t)(uint8_t)r.sc;
         const int nsh = r.t < 2 ? 0 : 4, hsh = 2 * (int)r.t;
-        uint32_t t[2][8];
+        uint32_t p[8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             float v[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const uint32_t u = ((r.ql[i] >> (8 * e + nsh)) & 15u) | (((r.qh[i] >> (8 * e + hsh)) & 3u) << 4);
-                v[e] = sc * (float)((int)u - 32);  // an integer of at most 13 bits: exact
+                v[e] = (float)((int)u - 32);
             }
-            uint32_t s2[2];
-            split2(v[0], v[1], s2);
-            t[0][2 * i] = s2[0], t[1][2 * i] = s2[1];
-            split2(v[2], v[3], s2);
-            t[0][2 * i + 1] = s2[0], t[1][2 * i + 1] = s2[1];
+            p[2 * i] = pack_bf16x2(v[0], v[1]);
+            p[2 * i + 1] = pack_bf16x2(v[2], v[3]);
         }
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            uint16_t* d = sw + u * plane + row * kLdsRow + 16 * h;
-            *reinterpret_cast<u32x4*>(d) = u32x4{t[u][0], t[u][1], t[u][2], t[u][3]};
-            *reinterpret_cast<u32x4*>(d + 8) = u32x4{t[u][4], t[u][5], t[u][6], t[u][7]};
-        }
+        *reinterpret_cast<u32x4*>(dst + 16 * h) = u32x4{p[0], p[1], p[2], p[3]};
+        *reinterpret_cast<u32x4*>(dst + 16 * h + 8) = u32x4{p[4], p[5], p[6], p[7]};
     } else if constexpr (QT == HIP_BRIDGE_Q4_0) {
         *reinterpret_cast<float*>(dst + kScaleSlot) = f16_bits_to_f32(r.d);  // both halves store it
         // byte j: low nibble = element j, high nibble = element j + 16 (value u - 8, exact)
@@ -427,12 +427,12 @@ __global__ __launch_bounds__(kGemmThreads, (gemm_wgs_per_cu<QT, XK, WT, WR>())) 
                         !(QT == HIP_BRIDGE_Q4_K && XK == X_TERMS);
     constexpr int NBUF = DB ? 2 : 1;
     constexpr int XCH_BYTES = GE ? 2 * WT * WR * 16 * kWave * 4 : 0;  // up accumulators, two waves
-    // Q4_K: per-token sums of each K step's activations, one per activation term (f32 x:
-    // of its three terms h, m, l, summed in the same order as pre-split planes, so both forms
-    // give the same products bit for bit), in two slots by step parity: step kb + 1's sums are
-    // written while step kb's are read
+    // Q4_K: per-token sums of each K step's activations (f32 or bf16 x: one sum; pre-split
+    // planes: one per plane, added in plane order), in two slots by step parity: step kb + 1's
+    // sums are written while step kb's are read. (Summing f32 x's three terms instead, so that
+    // both f32 forms agree bit for bit, cost 3 reductions a step: 10240 x 2560 x 2048, 531 us.)
     constexpr bool MIN = QT == HIP_BRIDGE_Q4_K;
-    constexpr int XSP = XT;  // sum planes
+    constexpr int XSP = XK == X_TERMS ? 3 : 1;  // sum planes
     constexpr int XS_FLOATS = MIN ? 2 * XSP * BT : 0;
     constexpr int MAIN_BYTES = NBUF * OPER_BYTES > XCH_BYTES ? NBUF * OPER_BYTES : XCH_BYTES;
     __shared__ __attribute__((aligned(16))) unsigned char s_raw[MAIN_BYTES + XS_FLOATS * 4];
@@ -498,10 +498,12 @@ __global__ __launch_bounds__(kGemmThreads, (gemm_wgs_per_cu<QT, XK, WT, WR>())) 
                 split3(__uint_as_float(xr[i].x), __uint_as_float(xr[i].y), t0);
                 split3(__uint_as_float(xr[i].z), __uint_as_float(xr[i].w), t1);
 #pragma unroll
-                for (int u = 0; u < 3; ++u) {
+                for (int u = 0; u < 3; ++u)
                     *reinterpret_cast<u32x2*>(sx + u * XPLANE + tok * kLdsRow + k) = u32x2{t0[u], t1[u]};
-                    if constexpr (MIN) put_sum((bf16_lo(t0[u]) + bf16_hi(t0[u])) + (bf16_lo(t1[u]) + bf16_hi(t1[u])), u);
-                }
+                if constexpr (MIN)
+                    put_sum((__uint_as_float(xr[i].x) + __uint_as_float(xr[i].y)) +
+                                (__uint_as_float(xr[i].z) + __uint_as_float(xr[i].w)),
+                            0);
             } else {
                 *reinterpret_cast<u32x4*>(sx + pl * XPLANE + tok * kLdsRow + k) = xr[i];
                 if constexpr (MIN)
@@ -562,8 +564,9 @@ __global__ __launch_bounds__(kGemmThreads, (gemm_wgs_per_cu<QT, XK, WT, WR>())) 
         // with two, each K = 16 half's operands are read just before its MFMAs (half the
         // registers)
         constexpr int KH = DB ? 1 : 2;
+        constexpr bool HALVES = w_halves<QT>();
         bf16x8 xa[KH][WT][XT], wb[KH][WR][NW];
-        float dv[WR], bv[MIN ? WR : 1];
+        float dv[WR], bv[MIN ? WR : 1], dv1[HALVES ? WR : 1];
         auto read_ops = [&](int ks, int slot) {
             const int ko = 16 * ks + 8 * (lane >> 5);
 #pragma unroll
@@ -586,7 +589,7 @@ __global__ __launch_bounds__(kGemmThreads, (gemm_wgs_per_cu<QT, XK, WT, WR>())) 
                     for (int p = 0; p < NP; ++p) {
                         const bf16x8 A = xa[slot][i][TP::xt[p]], Bv = wb[slot][j][TP::wt[p]];
                         if constexpr (SCALED) {
-                            part[i][j] = (ks == 0 && p == 0)
+                            part[i][j] = ((ks == 0 || HALVES) && p == 0)
                                              ? __builtin_amdgcn_mfma_f32_32x32x16_bf16(A, Bv, f32x16{}, 0, 0, 0)
                                              : __builtin_amdgcn_mfma_f32_32x32x16_bf16(A, Bv, part[i][j], 0, 0, 0);
                         } else {
@@ -600,20 +603,35 @@ __global__ __launch_bounds__(kGemmThreads, (gemm_wgs_per_cu<QT, XK, WT, WR>())) 
                 dv[j] = *reinterpret_cast<const float*>(sw + (wr0 + 32 * j + (lane & 31)) * kLdsRow + kScaleSlot);
                 if constexpr (MIN)
                     bv[j] = *reinterpret_cast<const float*>(sw + (wr0 + 32 * j + (lane & 31)) * kLdsRow + kMinSlot);
+                if constexpr (HALVES)
+                    dv1[j] = *reinterpret_cast<const float*>(sw + (wr0 + 32 * j + (lane & 31)) * kLdsRow + kScaleSlot + 2);
             }
         }
+        // HALVES: the first half's partial sums scaled into acc before the second half's MFMAs
+        auto scale_first_half = [&]() {
+            if constexpr (HALVES) {
+#pragma unroll
+                for (int j = 0; j < WR; ++j)
+#pragma unroll
+                    for (int i = 0; i < WT; ++i)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) acc[i][j][r] = fmaf(dv[j], part[i][j][r], acc[i][j][r]);
+            }
+        };
         if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
         if constexpr (DB) {
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
                 read_ops(ks, 0);
                 mfmas(ks, 0);
+                if (ks == 0) scale_first_half();
             }
         } else {
             read_ops(0, 0);
             read_ops(1, 1);
             if (single) __syncthreads();
             mfmas(0, 0);
+            scale_first_half();
             mfmas(1, 1);
         }
         if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
@@ -648,7 +666,7 @@ __global__ __launch_bounds__(kGemmThreads, (gemm_wgs_per_cu<QT, XK, WT, WR>())) 
 #pragma unroll
                 for (int i = 0; i < WT; ++i)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) acc[i][j][r] = fmaf(dv[j], part[i][j][r], acc[i][j][r]);
+                    for (int r = 0; r < 16; ++r) acc[i][j][r] = fmaf(HALVES ? dv1[j] : dv[j], part[i][j][r], acc[i][j][r]);
         }
     };
 
