@@ -293,7 +293,8 @@ void hip_gemm(int qtype, const void* weights, const float* x, float* y, int batc
  * (one term), so a bf16 norm output feeds the product directly. Q4_0, Q8_0, F16, BF16, F32
  * weights with cols % 32 == 0, Q4_K and Q6_K with cols % 256 == 0; x 16-byte aligned;
  * 128 * cols * sizeof(x element) < 4 GiB; else EUNSUPPORTED. f32 x and y without
- * up_weights is hip_gemm (which takes the matrix cores from 32 tokens for these types). */
+ * up_weights is hip_gemm, which takes the matrix cores from 96 tokens (8192 rows or more;
+ * else 128; Q4_K 8 / 64, Q6_K 16 / 96) and the small-batch or vector kernels below. */
 void hip_gemm_ex(int qtype, const void* weights, const void* up_weights /*NULL*/, int x_dtype,
                  const void* x, int y_dtype, void* y, int batch_size, int rows, int cols,
                  HipStream_t stream);
@@ -301,9 +302,9 @@ void hip_gemm_ex(int qtype, const void* weights, const void* up_weights /*NULL*/
  * m = bf16(x - h), l = bf16(x - h - m); h + m + l carries x's 24 significant bits), the
  * HIP_BRIDGE_F32_TERMS input of hip_gemm_ex: split once and shared by every product of the
  * same activations (QKV, gate and up), the K loop then converts weights only. The products
- * equal hip_gemm's on the f32 activations bit for bit (Q4_K: within f32 rounding, its min
- * term summing the planes rather than x). n % 4 == 0, x 16-byte and planes 8-byte aligned;
- * else EUNSUPPORTED. */
+ * equal hip_gemm's on the f32 activations bit for bit where hip_gemm runs on the matrix cores
+ * (Q4_K: within f32 rounding, its min term summing the planes rather than x). n % 4 == 0, x
+ * 16-byte and planes 8-byte aligned; else EUNSUPPORTED. */
 void hip_split_terms(const float* x, void* planes, int64_t n, HipStream_t stream);
 
 /* ---------------------------------------------------------------------------------- */

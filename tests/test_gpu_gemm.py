@@ -1,4 +1,4 @@
-"""Prefill-sized GEMM on the matrix cores (hip_gemm with batch >= 32: gemm.hip) against
+"""Prefill-sized GEMM on the matrix cores (hip_gemm from its threshold, hip_gemm_ex: gemm.hip) against
 float64 and the oracle's math.gemm (math.zig:440-616), through the C-ABI.
 
 The activations are split into three bf16 terms and the weights into one (Q4_0, Q8_0, BF16,
@@ -200,11 +200,12 @@ def test_split_terms_bitexact(dev):
 
 
 @pytest.mark.parametrize("qtype", TYPES)
-@pytest.mark.parametrize("rows,cols,batch", [(256, 2560, 128), (300, 1024, 77), (4096, 512, 2048), (129, 160, 40),
+@pytest.mark.parametrize("rows,cols,batch", [(256, 2560, 128), (300, 1024, 130), (4096, 512, 2048), (129, 160, 140),
                                              (2500, 96, 1900)])
 def test_gemm_ex_split_terms_equal_f32_product(dev, qtype, rows, cols, batch):
     """Activations split beforehand (hip_split_terms, F32_TERMS input) give hip_gemm's f32
-    product bit for bit: the kernel stages the same three terms it would form itself."""
+    product bit for bit where hip_gemm runs on the matrix cores (128 tokens and more for
+    these row counts): the kernel stages the same three terms it would form itself."""
     raw, _ = random_matrix(qtype, rows, cols, seed=rows + cols + batch + 21)
     X = synth.normal_f32(rows + batch + 22, "Xs", (batch, cols), 0, 3)
     ref = run(dev, qtype, raw, X, rows, cols)
@@ -319,7 +320,7 @@ def test_gemm_ex_kquant_bf16_activations_vs_f64(dev, qtype, rows, cols, batch):
 
 
 @pytest.mark.parametrize("qtype", KTYPES)
-@pytest.mark.parametrize("rows,cols,batch", [(256, 2560, 128), (4096, 512, 2048), (129, 256, 40)])
+@pytest.mark.parametrize("rows,cols,batch", [(256, 2560, 128), (4096, 512, 2048), (129, 256, 100)])
 def test_gemm_ex_kquant_split_terms_and_geglu(dev, qtype, rows, cols, batch):
     """Pre-split activations (F32_TERMS) give hip_gemm's f32 product bit for bit for Q6_K; for
     Q4_K, whose min term sums each plane of the split activations instead of x itself, both

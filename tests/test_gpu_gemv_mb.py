@@ -1,5 +1,6 @@
-"""Small-batch products on the matrix cores (gemv.hip k_gemv_mb: 2 to 31 tokens, Q4_0 / Q8_0
-/ BF16 weights, hip_gemm below the prefill GEMM's 32 tokens) through the C-ABI, over its
+"""Small-batch products on the matrix cores (gemv.hip k_gemv_mb: from 2 tokens up to the
+prefill GEMM's threshold, 96 tokens for 8192 rows or more, else 128; Q4_0 / Q8_0 / BF16
+weights) through the C-ABI, over its
 launch choices: 1, 2 or 4 sixteen-row tiles per wave and 4, 8 or 16 waves splitting the
 blocks of a row (so row counts that leave tiles and tile groups partly empty, block counts
 that the waves split unevenly, one or two 16-token tiles, tokens that leave a tile partly
@@ -86,3 +87,19 @@ def test_mb_leaves_other_cases_to_the_vector_kernels(dev, qtype):
     exact = (X.astype(np.float64) @ wd.T).astype(np.float32)
     np.testing.assert_array_equal(gemm(dev, qtype, raw, X, rows, cols, batch, x_offset=4 if qtype == B.Q4_0 else 0),
                                   exact)
+
+
+@pytest.mark.parametrize("qtype,rows,cols,batch", [
+    (B.Q4_0, 10240, 2560, 95), (B.Q8_0, 8192, 1024, 64), (B.Q4_0, 2560, 10240, 100), (B.BF16, 4096, 1024, 127),
+    (B.Q4_K, 2560, 2560, 63), (B.Q6_K, 10240, 2560, 12), (B.Q6_K, 2048, 1024, 95), (B.F16, 1024, 512, 100),
+    (B.F32, 512, 512, 77), (B.Q4_K, 8192, 512, 7)])
+def test_below_matrix_core_threshold_vs_f64(dev, qtype, rows, cols, batch):
+    """Batches below the prefill GEMM's threshold for their type and row count (96 or 128
+    tokens; Q4_K 8 or 64, Q6_K 16 or 96) take the small-batch or the vector kernels: within
+    2^-20 * sum |w_i x_i| of float64."""
+    raw, wd = random_matrix(qtype, rows, cols, seed=rows + 5 * batch)
+    X = synth.normal_f32(rows + batch + 1, "Xt", (batch, cols), 0, 2)
+    exact = X.astype(np.float64) @ wd.T
+    got = gemm(dev, qtype, raw, X, rows, cols, batch).astype(np.float64)
+    bd = bound(wd, X)
+    assert np.all(np.abs(got - exact) <= bd), float(np.max(np.abs(got - exact) / bd))

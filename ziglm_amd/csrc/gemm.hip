@@ -812,7 +812,7 @@ __global__ __launch_bounds__(256) void k_split_terms(const float* __restrict__ x
 
 bool launch_gemm_mfma(int qtype, const void* w, int64_t row_bytes, const float* x, float* y, int rows, int cols,
                       int batch, hipStream_t s) {
-    if (batch < kGemmMfmaMinBatch || !y) return false;
+    if (batch < gemm_mfma_min_batch(qtype, rows) || !y) return false;
     return launch_gemm_mfma_ex(qtype, w, nullptr, row_bytes, HIP_BRIDGE_F32, x, HIP_BRIDGE_F32, y, rows, cols, batch,
                                s) == 0;
 }

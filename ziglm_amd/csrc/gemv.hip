@@ -1876,7 +1876,7 @@ static void launch_gemv(int qtype, GemvArgs& a, hipStream_t s) {
 }
 
 // ---- small batches on the matrix cores ------------------------------------------------------
-// Products of 2 to kGemmMfmaMinBatch - 1 tokens (hip_gemm below the prefill GEMM) with Q4_0,
+// Products of 2 to gemm_mfma_min_batch - 1 tokens (hip_gemm below the prefill GEMM) with Q4_0,
 // Q8_0 or BF16 weights: v_mfma_f32_16x16x32_bf16 over tiles of 16 tokens x 16 rows x one
 // 32-column block, tokens on the A side (each x as three bf16 terms h + m + l, as the prefill
 // GEMM: exact to the f32 value's 24 bits), rows on the B side. Block quants enter as their
@@ -2038,7 +2038,7 @@ __global__ __launch_bounds__(KS * kWave) void k_gemv_mb(GemvArgs a) {
 #ifndef ZL_GEMV_MB_WAVES
 #define ZL_GEMV_MB_WAVES 1024
 #endif
-// Launches k_gemv_mb for a batch of 2 to kGemmMfmaMinBatch - 1 tokens (Q4_0 / Q8_0 with
+// Launches k_gemv_mb for a batch of 2 to gemm_mfma_min_batch - 1 tokens (Q4_0 / Q8_0 with
 // 2-byte aligned rows, BF16 with 16-byte aligned ones; cols % 32 == 0, at most 160 blocks;
 // x 16-byte aligned); returns false otherwise (the vector kernels take the product).
 template <int QT>
@@ -2069,7 +2069,8 @@ static bool launch_mb_t(const GemvArgs& a, hipStream_t s) {
     return true;
 }
 static bool launch_gemv_mb(int qtype, GemvArgs& a, hipStream_t s) {
-    if (!ZL_GEMV_MB || a.batch < 2 || a.batch >= kGemmMfmaMinBatch || a.cols % 32 != 0 || a.nseg != 1 ||
+    if (!ZL_GEMV_MB || a.batch < 2 || a.batch >= gemm_mfma_min_batch(qtype, a.total_rows) || a.cols % 32 != 0 ||
+        a.nseg != 1 ||
         !a.seg[0].w || !a.seg[0].y || !a.x || !aligned16(a.x))
         return false;
     const uintptr_t wa = reinterpret_cast<uintptr_t>(a.seg[0].w);
@@ -2106,7 +2107,7 @@ extern "C" {
 void hip_gemm(int qtype, const void* weights, const float* x, float* y, int batch_size, int rows,
               int cols, HipStream_t stream) {
     if (batch_size <= 0 || rows <= 0 || cols <= 0) return;
-    if (batch_size >= kGemmMfmaMinBatch && weights && x) {
+    if (batch_size >= gemm_mfma_min_batch(qtype, rows) && weights && x) {
         const int64_t rb = gemv_row_bytes(qtype, cols);
         if (rb > 0 && launch_gemm_mfma(qtype, weights, rb, x, y, rows, cols, batch_size, stream_of(stream))) return;
     }
