@@ -497,11 +497,13 @@ static void launch_wl(const NormArgs& a, int per_lane, int R, bool late, hipStre
 }
 
 // Waves per row: the fewest (1, 2 or 4) that keep a row within 4 chunks (128-bit loads)
-// per lane (3 for NORM_ADD_NORM, which also holds the second weight vector; 6 for NORM_ADD,
-// whose one wave per row at 2048 x 2560 bf16 skips the cross-wave reduction: 6.57 -> 6.26 us,
-// 8192 x 5376 unchanged; with exactly 5 chunks per lane there, 6.49 -> 6.32 us against 6), so a row lives
-// in registers with few cross-wave reductions and every row of a 2048-token prefill is
-// resident at once; rows longer than that at 4 waves take up to 16 chunks per lane.
+// per lane (3 for NORM_ADD_NORM, which also holds the second weight vector; for NORM_ADD one
+// wave per row up to 6 chunks, which skips the cross-wave reduction: 2048 x 2560 bf16 6.57 ->
+// 6.26 us, with exactly 5 chunks per lane there 6.49 -> 6.32 us against 6; past one wave it
+// takes 4 chunks too, so 8192 x 5376 runs 4 waves of 3 chunks and two rows stage by stage
+// instead of 2 waves of 6: 45.7 -> 44.8 us), so a row lives in registers with few
+// cross-wave reductions and every row of a 2048-token prefill is resident at once; rows
+// longer than that at 4 waves take up to 16 chunks per lane.
 // ZL_NORM_WAVES_PER_ROW, ZL_NORM_ROWS_PER_GROUP and ZL_NORM_LATE (0 / 1) force values.
 #ifndef ZL_NORM_WAVES_PER_ROW
 #define ZL_NORM_WAVES_PER_ROW 0
@@ -524,8 +526,9 @@ static void launch_t(const NormArgs& a, hipStream_t s) {
     const int nch = a.n / E;
     int W = ZL_NORM_WAVES_PER_ROW;
     if (W == 0) {
-        const int fit = MODE == M_NORM_ADD_NORM ? ZL_NORM_FIT_NAN : MODE == M_NORM_ADD ? ZL_NORM_FIT_ADD : 4;
-        W = nch <= fit * kWave ? 1 : nch <= 2 * fit * kWave ? 2 : 4;
+        const int fit = MODE == M_NORM_ADD_NORM ? ZL_NORM_FIT_NAN : 4;
+        const int fit1 = MODE == M_NORM_ADD ? ZL_NORM_FIT_ADD : fit;  // one wave per row
+        W = nch <= fit1 * kWave ? 1 : nch <= 2 * fit * kWave ? 2 : 4;
     }
     const int per_lane = (int)cdiv(nch, kWave * W);
     // Two rows per lane group (the second row's loads in flight while the first is reduced
