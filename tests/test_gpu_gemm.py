@@ -370,3 +370,26 @@ def test_gemm_kquant_refuses_partial_super_blocks(dev):
     finally:
         dev.strict = True
     assert np.all(y.to_numpy((64 * 64 * 4,), np.uint8) == 0x11)
+
+
+# ---- two K halves (deep products, f32 output, fewer than two rounds of workgroups) -------------
+
+@pytest.mark.parametrize("qtype", [B.Q4_0, B.Q8_0, B.BF16, B.Q4_K, B.Q6_K])
+@pytest.mark.parametrize("rows,cols,batch", [(2560, 10240, 256), (300, 4352, 130), (77, 8192, 300)])
+def test_gemm_split_k_integer_bitexact_and_random(dev, qtype, rows, cols, batch):
+    """Deep products (cols >= 4096) whose tiles number fewer than two rounds run each tile as two
+    K halves added into zeroed y: integer operands give the exact product bit for bit, random
+    ones stay within 2^-20 * sum |w_i x_i| of float64, and a second call gives the same bits
+    (two addends: 0 + a + b in either order)."""
+    raw, wd = int_matrix(qtype, rows, cols, seed=rows + cols + batch + qtype, scale_pow=-3)
+    X = np.random.default_rng(rows + batch).integers(-2, 3, (batch, cols)).astype(np.float32)
+    exact = X.astype(np.float64) @ wd.T
+    assert np.all(np.abs(exact) < 2 ** 24)
+    np.testing.assert_array_equal(run(dev, qtype, raw, X, rows, cols), exact.astype(np.float32))
+    raw, wd = random_matrix(qtype, rows, cols, seed=rows + cols + batch + 31)
+    X = synth.normal_f32(rows + batch + 31, "Xsk", (batch, cols), 0, 2)
+    exact = X.astype(np.float64) @ wd.T
+    got = run(dev, qtype, raw, X, rows, cols)
+    bd = bound(wd, X)
+    assert np.all(np.abs(got.astype(np.float64) - exact) <= bd), float(np.max(np.abs(got - exact) / bd))
+    np.testing.assert_array_equal(run(dev, qtype, raw, X, rows, cols), got)

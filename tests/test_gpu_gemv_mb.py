@@ -1,6 +1,6 @@
 """Small-batch products on the matrix cores (gemv.hip k_gemv_mb: from 2 tokens up to the
-prefill GEMM's threshold, 96 tokens for 8192 rows or more, else 128; Q4_0 / Q8_0 / BF16
-weights) through the C-ABI, over its
+prefill GEMM's threshold, 96 tokens for 8192 rows or more, 64 for narrower products at
+least 4096 deep, else 128; Q4_0 / Q8_0 / BF16 weights) through the C-ABI, over its
 launch choices: 1, 2 or 4 sixteen-row tiles per wave and 4, 8 or 16 waves splitting the
 blocks of a row (so row counts that leave tiles and tile groups partly empty, block counts
 that the waves split unevenly, one or two 16-token tiles, tokens that leave a tile partly
@@ -90,12 +90,13 @@ def test_mb_leaves_other_cases_to_the_vector_kernels(dev, qtype):
 
 
 @pytest.mark.parametrize("qtype,rows,cols,batch", [
-    (B.Q4_0, 10240, 2560, 95), (B.Q8_0, 8192, 1024, 64), (B.Q4_0, 2560, 10240, 100), (B.BF16, 4096, 1024, 127),
+    (B.Q4_0, 10240, 2560, 95), (B.Q8_0, 8192, 1024, 64), (B.Q4_0, 2560, 10240, 60), (B.BF16, 4096, 1024, 127),
     (B.Q4_K, 2560, 2560, 63), (B.Q6_K, 10240, 2560, 12), (B.Q6_K, 2048, 1024, 95), (B.F16, 1024, 512, 100),
-    (B.F32, 512, 512, 77), (B.Q4_K, 8192, 512, 7)])
+    (B.F32, 512, 512, 77), (B.Q4_K, 8192, 512, 7), (B.Q4_K, 2560, 4096, 31), (B.Q6_K, 1024, 8192, 47)])
 def test_below_matrix_core_threshold_vs_f64(dev, qtype, rows, cols, batch):
-    """Batches below the prefill GEMM's threshold for their type and row count (96 or 128
-    tokens; Q4_K 8 or 64, Q6_K 16 or 96) take the small-batch or the vector kernels: within
+    """Batches below the prefill GEMM's threshold for their type and shape (8192 rows or more
+    / narrower but at least 4096 deep / the rest: Q4_0 and the dense types 96 / 64 / 128, Q4_K
+    8 / 32 / 64, Q6_K 16 / 48 / 96 tokens) take the small-batch or the vector kernels: within
     2^-20 * sum |w_i x_i| of float64."""
     raw, wd = random_matrix(qtype, rows, cols, seed=rows + 5 * batch)
     X = synth.normal_f32(rows + batch + 1, "Xt", (batch, cols), 0, 2)

@@ -446,7 +446,11 @@ __global__ __launch_bounds__(kGemmThreads, (gemm_wgs_per_cu<QT, XK, WT, WR>())) 
     const int gx = (a.rows + OR - 1) / OR, nwg = (int)gridDim.x;
     if (ZL_GEMM_XCD && nwg % 8 == 0) tile = (tile % 8) * (nwg / 8) + tile / 8;
     const int r_base = (tile % gx) * OR, b_base = (tile / gx) * BT;
-    const int nkb = a.cols / kKB;
+    // K steps [kbb, kbe): all of them, or with a split launch (gridDim.y = 2, f32 output,
+    // added into zeroed y) one half per workgroup row
+    const int nkb_all = a.cols / kKB;
+    const int kbb = (int)((int64_t)nkb_all * blockIdx.y / gridDim.y);
+    const int kbe = (int)((int64_t)nkb_all * (blockIdx.y + 1) / gridDim.y);
 
     // X staging. f32 x: chunk c = tid + 256 i is token c / 8, columns 4 (c % 8) .. (four
     // floats); bf16 x: token c / 4, columns 8 (c % 4) .. (eight bf16); term planes: chunk c of
@@ -674,20 +678,20 @@ __global__ __launch_bounds__(kGemmThreads, (gemm_wgs_per_cu<QT, XK, WT, WR>())) 
     // converted into the LDS (the other buffer with DB, else the same one once every wave has
     // read block kb's operands) and block kb + 2's loads are issued, so the matrix cores work
     // during the conversion rather than after it. Past the end: the last block again, unused.
-    load_x(0);
-    load_wt(0);
-    store_x(0, 0);
+    load_x(kbb);
+    load_wt(kbb);
+    store_x(0, kbb & 1);
     store_wt(0);
     __syncthreads();
-    load_x(min(1, nkb - 1));
-    load_wt(min(1, nkb - 1));
-    for (int kb = 0; kb < nkb; ++kb) {
-        const int cur = DB ? (kb & 1) : 0, nxt = DB ? (cur ^ 1) : 0;
+    load_x(min(kbb + 1, kbe - 1));
+    load_wt(min(kbb + 1, kbe - 1));
+    for (int kb = kbb; kb < kbe; ++kb) {
+        const int cur = DB ? ((kb - kbb) & 1) : 0, nxt = DB ? (cur ^ 1) : 0;
         step(cur, kb & 1, !DB, [&]() {
             store_x(nxt, (kb + 1) & 1);
             store_wt(nxt);
-            load_x(min(kb + 2, nkb - 1));
-            load_wt(min(kb + 2, nkb - 1));
+            load_x(min(kb + 2, kbe - 1));
+            load_wt(min(kb + 2, kbe - 1));
         });
         __syncthreads();  // block kb + 1 is in the LDS (DB: and block kb's buffer is free)
     }
@@ -727,6 +731,8 @@ __global__ __launch_bounds__(kGemmThreads, (gemm_wgs_per_cu<QT, XK, WT, WR>())) 
                 if (tok < a.batch) {
                     if constexpr (YB)
                         ((uint16_t*)a.y)[(int64_t)tok * a.rows + row] = (uint16_t)(pack_bf16x2(acc[i][j][r], 0.0f) & 0xffffu);
+                    else if (gridDim.y > 1)  // two K halves into zeroed y: 0 + a + b in either order
+                        unsafeAtomicAdd((float*)a.y + (int64_t)tok * a.rows + row, acc[i][j][r]);
                     else
                         ((float*)a.y)[(int64_t)tok * a.rows + row] = acc[i][j][r];
                 }
@@ -737,16 +743,36 @@ __global__ __launch_bounds__(kGemmThreads, (gemm_wgs_per_cu<QT, XK, WT, WR>())) 
 // Workgroup tile: the largest of 128 x 128, 64 x 128 and 64 x 64 (tokens x W rows) that still
 // gives at least two workgroups per CU (bigger tiles convert each operand for more MFMAs;
 // smaller ones fill the chip at small batches).
+// Split K (ZL_GEMM_SPLITK, zl_host.h: two halves of the K steps per output tile, summed into
+// zeroed y by float atomic adds; with exactly two addends the sum does not depend on their
+// order, so results stay bit-reproducible) for deep products with f32 output that give fewer
+// than two rounds of workgroups: 2560 x 10240 x 2048, 640 -> 1280 workgroups: Q4_0 435 -> 401
+// us, Q4_K 520 -> 479, Q6_K 634 -> 559; at 128 tokens Q4_0 250 -> 129 us.
+__global__ __launch_bounds__(256) void k_zero_f32(float* __restrict__ y, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) y[i] = 0.0f;
+}
 template <int QT, int XK, bool GE, bool YB>
 static void launch_qt(const GemmArgs& a, hipStream_t s) {
     constexpr int64_t kFill = 512;
     auto wgs = [&](int bt, int br) { return cdiv(a.rows, GE ? br / 2 : br) * cdiv(a.batch, bt); };
+    const int64_t n = wgs(128, 128) >= kFill ? wgs(128, 128) : wgs(64, 128) >= kFill ? wgs(64, 128) : wgs(64, 64);
+    // Deep products with f32 output and fewer than two rounds of workgroups: two K halves per
+    // tile, added into zeroed y
+    unsigned ky = 1;
+    if constexpr (!GE && !YB) {
+        if (ZL_GEMM_SPLITK && n < 2 * kFill && a.cols >= ZL_GEMM_SPLITK_MIN_COLS) {
+            ky = 2;
+            const int64_t ny = (int64_t)a.batch * a.rows;
+            k_zero_f32<<<(unsigned)std::min<int64_t>(cdiv(ny, 256), 8192), 256, 0, s>>>((float*)a.y, ny);
+        }
+    }
+    const dim3 grid((unsigned)n, ky);
     if (wgs(128, 128) >= kFill) {
-        k_gemm_mfma<QT, XK, 2, 2, GE, YB><<<(unsigned)wgs(128, 128), kGemmThreads, 0, s>>>(a);
+        k_gemm_mfma<QT, XK, 2, 2, GE, YB><<<grid, kGemmThreads, 0, s>>>(a);
     } else if (wgs(64, 128) >= kFill) {
-        k_gemm_mfma<QT, XK, 1, 2, GE, YB><<<(unsigned)wgs(64, 128), kGemmThreads, 0, s>>>(a);
+        k_gemm_mfma<QT, XK, 1, 2, GE, YB><<<grid, kGemmThreads, 0, s>>>(a);
     } else {
-        k_gemm_mfma<QT, XK, 1, 1, GE, YB><<<(unsigned)wgs(64, 64), kGemmThreads, 0, s>>>(a);
+        k_gemm_mfma<QT, XK, 1, 1, GE, YB><<<grid, kGemmThreads, 0, s>>>(a);
     }
 }
 
@@ -812,7 +838,7 @@ __global__ __launch_bounds__(256) void k_split_terms(const float* __restrict__ x
 
 bool launch_gemm_mfma(int qtype, const void* w, int64_t row_bytes, const float* x, float* y, int rows, int cols,
                       int batch, hipStream_t s) {
-    if (batch < gemm_mfma_min_batch(qtype, rows) || !y) return false;
+    if (batch < gemm_mfma_min_batch(qtype, rows, cols) || !y) return false;
     return launch_gemm_mfma_ex(qtype, w, nullptr, row_bytes, HIP_BRIDGE_F32, x, HIP_BRIDGE_F32, y, rows, cols, batch,
                                s) == 0;
 }

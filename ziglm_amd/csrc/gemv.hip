@@ -2069,8 +2069,8 @@ static bool launch_mb_t(const GemvArgs& a, hipStream_t s) {
     return true;
 }
 static bool launch_gemv_mb(int qtype, GemvArgs& a, hipStream_t s) {
-    if (!ZL_GEMV_MB || a.batch < 2 || a.batch >= gemm_mfma_min_batch(qtype, a.total_rows) || a.cols % 32 != 0 ||
-        a.nseg != 1 ||
+    if (!ZL_GEMV_MB || a.batch < 2 || a.batch >= gemm_mfma_min_batch(qtype, a.total_rows, a.cols) ||
+        a.cols % 32 != 0 || a.nseg != 1 ||
         !a.seg[0].w || !a.seg[0].y || !a.x || !aligned16(a.x))
         return false;
     const uintptr_t wa = reinterpret_cast<uintptr_t>(a.seg[0].w);
@@ -2107,7 +2107,7 @@ extern "C" {
 void hip_gemm(int qtype, const void* weights, const float* x, float* y, int batch_size, int rows,
               int cols, HipStream_t stream) {
     if (batch_size <= 0 || rows <= 0 || cols <= 0) return;
-    if (batch_size >= gemm_mfma_min_batch(qtype, rows) && weights && x) {
+    if (batch_size >= gemm_mfma_min_batch(qtype, rows, cols) && weights && x) {
         const int64_t rb = gemv_row_bytes(qtype, cols);
         if (rb > 0 && launch_gemm_mfma(qtype, weights, rb, x, y, rows, cols, batch_size, stream_of(stream))) return;
     }

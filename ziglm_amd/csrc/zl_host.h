@@ -24,24 +24,35 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-// Matrix-core GEMM (gemm.hip) for batches of at least gemm_mfma_min_batch(qtype, rows) tokens:
+// Matrix-core GEMM (gemm.hip) for batches of at least gemm_mfma_min_batch(qtype, rows, cols) tokens:
 // launches and returns true when the type, shape (cols % 32 == 0, K-quants % 256) and
 // alignment suit it, else launches nothing and returns false (the caller takes the vector
 // path).
-// The matrix-core kernel's smallest workgroup tile is 64 tokens x 64 rows over the whole of
-// K, so below a few hundred tiles it leaves most of the chip idle (2560 x 10240 at up to 128
-// tokens: 40-80 workgroups, ~250 us whatever the batch), while the vector kernels' time grows
-// with the batch. The batch from which it wins, measured per type on 10240 x 2560 (160 row
-// tiles) and 2560 x 10240 (40) products: Q4_0 / Q8_0 96 / 128, Q4_K 8 / 64, Q6_K 16 / 96.
+// Split K in the matrix-core kernel (gemm.hip launch_qt): products at least this deep with
+// f32 output run each tile as two K halves when their tiles number fewer than two rounds.
+#ifndef ZL_GEMM_SPLITK
+#define ZL_GEMM_SPLITK 1
+#endif
+#ifndef ZL_GEMM_SPLITK_MIN_COLS
+#define ZL_GEMM_SPLITK_MIN_COLS 4096
+#endif
+// The matrix-core kernel's smallest workgroup tile is 64 tokens x 64 rows, so below a few
+// hundred tiles it leaves most of the chip idle (2560 x 10240 at up to 128 tokens: 40-80
+// workgroups; split in two K halves ~130 us for Q4_0 whatever the batch), while the vector
+// kernels' time grows with the batch. The batch from which it wins, measured per type on
+// 10240 x 2560 (160 row tiles: "wide") and 2560 x 10240 (40, deep enough to split) products:
+// Q4_0 / Q8_0 96 / 64, Q4_K 8 / 32, Q6_K 16 / 48; narrow products too shallow to split keep
+// the unsplit crossovers (128, 64, 96).
 #ifndef ZL_GEMM_MIN_BATCH
 #define ZL_GEMM_MIN_BATCH 0
 #endif
-inline int gemm_mfma_min_batch(int qtype, int rows) {
+inline int gemm_mfma_min_batch(int qtype, int rows, int cols) {
     if (ZL_GEMM_MIN_BATCH) return ZL_GEMM_MIN_BATCH;
     const bool wide = rows >= 128 * 64;  // enough row tiles to fill half the chip's workgroup slots
-    if (qtype == HIP_BRIDGE_Q4_K) return wide ? 8 : 64;
-    if (qtype == HIP_BRIDGE_Q6_K) return wide ? 16 : 96;
-    return wide ? 96 : 128;
+    const bool deep = ZL_GEMM_SPLITK && cols >= ZL_GEMM_SPLITK_MIN_COLS;
+    if (qtype == HIP_BRIDGE_Q4_K) return wide ? 8 : deep ? 32 : 64;
+    if (qtype == HIP_BRIDGE_Q6_K) return wide ? 16 : deep ? 48 : 96;
+    return wide ? 96 : deep ? 64 : 128;
 }
 bool launch_gemm_mfma(int qtype, const void* w, int64_t row_bytes, const float* x, float* y, int rows, int cols,
                       int batch, hipStream_t s);
