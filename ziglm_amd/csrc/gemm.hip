@@ -685,8 +685,9 @@ __global__ __launch_bounds__(kGemmThreads, (gemm_wgs_per_cu<QT, XK, WT, WR>())) 
     __syncthreads();
     load_x(min(kbb + 1, kbe - 1));
     load_wt(min(kbb + 1, kbe - 1));
-    for (int kb = kbb; kb < kbe; ++kb) {
-        const int cur = DB ? ((kb - kbb) & 1) : 0, nxt = DB ? (cur ^ 1) : 0;
+    for (int it = 0; it < kbe - kbb; ++it) {
+        const int kb = kbb + it;
+        const int cur = DB ? (it & 1) : 0, nxt = DB ? (cur ^ 1) : 0;
         step(cur, kb & 1, !DB, [&]() {
             store_x(nxt, (kb + 1) & 1);
             store_wt(nxt);
