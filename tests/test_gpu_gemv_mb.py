@@ -2,7 +2,7 @@
 prefill GEMM's threshold, 96 tokens for 8192 rows or more, 64 for narrower products at
 least 4096 deep, else 128; Q4_0 / Q8_0 / BF16 weights) through the C-ABI, over its
 launch choices: 1, 2 or 4 sixteen-row tiles per wave and 4, 8 or 16 waves splitting the
-blocks of a row (so row counts that leave tiles and tile groups partly empty, block counts
+blocks of a row, rows too long for that in two halves added into zeroed y (so row counts that leave tiles and tile groups partly empty, block counts
 that the waves split unevenly, one or two 16-token tiles, tokens that leave a tile partly
 empty), and the shapes it leaves to the vector kernels (x not 16-byte aligned, other types,
 a column count that is not a whole number of blocks).
@@ -42,7 +42,8 @@ def gemm(dev, qtype, raw, X, rows, cols, batch, x_offset=0):
 @pytest.mark.parametrize("qtype", MB_TYPES)
 @pytest.mark.parametrize("rows,cols,batch", [
     (10240, 2560, 8),   # 4 tiles per wave, 8 waves per workgroup
-    (2560, 10240, 8),   # 1 tile per wave, 16 waves
+    (2560, 10240, 8),   # rows too long for 16 waves of 10 blocks: the vector kernels below 12 tokens,
+    (2500, 10240, 40), (130, 6144, 20), (2560, 10240, 12),  # two halves added into y from 12
     (4096, 2560, 2), (1000, 2560, 16), (37, 2560, 17), (300, 1536, 31), (19, 96, 3),
     (5, 32, 2), (64, 160, 9), (777, 4096, 24), (100, 64, 5)])
 def test_mb_integer_bitexact(dev, qtype, rows, cols, batch):

@@ -752,6 +752,9 @@ __global__ __launch_bounds__(kGemmThreads, (gemm_wgs_per_cu<QT, XK, WT, WR>())) 
 __global__ __launch_bounds__(256) void k_zero_f32(float* __restrict__ y, int64_t n) {
     for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) y[i] = 0.0f;
 }
+void launch_zero_f32(float* y, int64_t n, hipStream_t s) {
+    k_zero_f32<<<(unsigned)std::min<int64_t>(cdiv(n, 256), 8192), 256, 0, s>>>(y, n);
+}
 template <int QT, int XK, bool GE, bool YB>
 static void launch_qt(const GemmArgs& a, hipStream_t s) {
     constexpr int64_t kFill = 512;
@@ -763,8 +766,7 @@ static void launch_qt(const GemmArgs& a, hipStream_t s) {
     if constexpr (!GE && !YB) {
         if (ZL_GEMM_SPLITK && n < 2 * kFill && a.cols >= ZL_GEMM_SPLITK_MIN_COLS) {
             ky = 2;
-            const int64_t ny = (int64_t)a.batch * a.rows;
-            k_zero_f32<<<(unsigned)std::min<int64_t>(cdiv(ny, 256), 8192), 256, 0, s>>>((float*)a.y, ny);
+            launch_zero_f32((float*)a.y, (int64_t)a.batch * a.rows, s);
         }
     }
     const dim3 grid((unsigned)n, ky);

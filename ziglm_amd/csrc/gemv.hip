@@ -1919,7 +1919,9 @@ __global__ __launch_bounds__(KS * kWave) void k_gemv_mb(GemvArgs a) {
     const int t0 = blockIdx.y * kMbTok;
     const int r0 = blockIdx.x * 16 * NT;
     const int nblk = a.cols / 32;
-    const int kb0 = (int)((int64_t)nblk * wv / KS), kb1 = (int)((int64_t)nblk * (wv + 1) / KS);
+    // the workgroup's blocks: all, or with gridDim.z = 2 one half (added into zeroed y)
+    const int kbs = (int)((int64_t)nblk * blockIdx.z / gridDim.z), kbn = (int)((int64_t)nblk * (blockIdx.z + 1) / gridDim.z) - kbs;
+    const int kb0 = kbs + (int)((int64_t)kbn * wv / KS), kb1 = kbs + (int)((int64_t)kbn * (wv + 1) / KS);
     // the x row of token t0 + mn (past the batch: token 0's, zeroed), columns 8g .. of a block
     const bool tok_ok = t0 + mn < a.batch;
     const float* xr = a.x + (int64_t)(tok_ok ? t0 + mn : 0) * a.cols + 8 * g;
@@ -2026,7 +2028,10 @@ __global__ __launch_bounds__(KS * kWave) void k_gemv_mb(GemvArgs a) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int tok = t0 + 4 * g + r;
-                if (tok < a.batch) a.seg[0].y[(int64_t)tok * a.total_rows + row] = t[r];
+                if (tok >= a.batch) continue;
+                float* const yp = a.seg[0].y + (int64_t)tok * a.total_rows + row;
+                if (gridDim.z > 1) unsafeAtomicAdd(yp, t[r]);  // two halves: 0 + a + b in either order
+                else *yp = t[r];
             }
         }
     }
@@ -2034,6 +2039,12 @@ __global__ __launch_bounds__(KS * kWave) void k_gemv_mb(GemvArgs a) {
 
 #ifndef ZL_GEMV_MB
 #define ZL_GEMV_MB 1
+#endif
+#ifndef ZL_GEMV_MB_SPLIT
+#define ZL_GEMV_MB_SPLIT 1
+#endif
+#ifndef ZL_GEMV_MB_SPLIT_NT
+#define ZL_GEMV_MB_SPLIT_NT 2
 #endif
 #ifndef ZL_GEMV_MB_WAVES
 #define ZL_GEMV_MB_WAVES 1024
@@ -2052,11 +2063,21 @@ static bool launch_mb_t(const GemvArgs& a, hipStream_t s) {
     int ks = 0;
     for (int k : {4, 8, 16})
         if (!ks && cdiv(nblk, k) <= 10) ks = k;
+    // Rows too long for 16 waves of 10 blocks: from 12 tokens, two halves of the blocks per
+    // row tile added into zeroed y, at most 2 row tiles per wave (Q4_0 2560 x 10240 at 16 / 32 /
+    // 48 / 63 tokens: 36 / 67 / 68 / 99 us against the vector kernel's 39 / 73 / 105 / ~137;
+    // at 8 tokens 33 against 23, so fewer tokens keep the vector kernel).
+    unsigned kz = 1;
+    if (!ks && ZL_GEMV_MB_SPLIT && a.batch >= 12 && cdiv(nblk, 2 * 16) <= 10) {
+        ks = 16;
+        kz = 2;
+    }
     if (!ks) return false;
     int nt = 1;
     for (int n : {4, 2})
-        if (nt == 1 && cdiv(tiles, n) * ttiles * ks >= ZL_GEMV_MB_WAVES) nt = n;
-    const dim3 grid((unsigned)cdiv(tiles, nt), (unsigned)ttiles);
+        if (nt == 1 && cdiv(tiles, n) * ttiles * ks * kz >= ZL_GEMV_MB_WAVES && (kz == 1 || n <= ZL_GEMV_MB_SPLIT_NT)) nt = n;
+    const dim3 grid((unsigned)cdiv(tiles, nt), (unsigned)ttiles, kz);
+    if (kz > 1) launch_zero_f32(a.seg[0].y, (int64_t)a.batch * a.total_rows, s);
     auto go = [&](auto n_c) {
         constexpr int N = decltype(n_c)::value;
         if (ks == 4) k_gemv_mb<QT, N, 4><<<grid, 4 * kWave, 0, s>>>(a);

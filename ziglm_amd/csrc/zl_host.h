@@ -43,6 +43,9 @@ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // 10240 x 2560 (160 row tiles: "wide") and 2560 x 10240 (40, deep enough to split) products:
 // Q4_0 / Q8_0 96 / 64, Q4_K 8 / 32, Q6_K 16 / 48; narrow products too shallow to split keep
 // the unsplit crossovers (128, 64, 96).
+// y[0, n) = 0 (a kernel, not hipMemsetAsync, so that graph captures of the products that
+// add into y replay correctly)
+void launch_zero_f32(float* y, int64_t n, hipStream_t s);
 #ifndef ZL_GEMM_MIN_BATCH
 #define ZL_GEMM_MIN_BATCH 0
 #endif
