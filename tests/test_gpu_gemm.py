@@ -393,3 +393,31 @@ def test_gemm_split_k_integer_bitexact_and_random(dev, qtype, rows, cols, batch)
     bd = bound(wd, X)
     assert np.all(np.abs(got.astype(np.float64) - exact) <= bd), float(np.max(np.abs(got - exact) / bd))
     np.testing.assert_array_equal(run(dev, qtype, raw, X, rows, cols), got)
+
+
+@pytest.mark.parametrize("qtype,rows,cols,batch", [(B.Q4_0, 2560, 10240, 256), (B.Q4_0, 2560, 10240, 40),
+                                                   (B.Q4_K, 2560, 4096, 200)])
+def test_split_products_replay_in_a_graph(dev, qtype, rows, cols, batch):
+    """The split products (a zero-fill kernel, then two halves added into y) captured in a
+    hipGraph: three replays, with eager products on other buffers between them, each equal
+    to the eager result bit for bit."""
+    from ziglm_amd.device import Graph
+    raw, _ = random_matrix(qtype, rows, cols, seed=rows + batch + 41)
+    X = synth.normal_f32(rows + batch + 41, "Xg", (batch, cols), 0, 2)
+    d_w = dev.from_numpy(np.ascontiguousarray(raw).reshape(-1))
+    d_x = dev.from_numpy(np.ascontiguousarray(X).reshape(-1))
+    d_y = dev.alloc(batch * rows * 4)
+    dev.gemm(qtype, d_w, d_x, d_y, batch, rows, cols)
+    ref = d_y.to_numpy((batch, rows), np.float32)
+    g = Graph(dev, lambda: dev.gemm(qtype, d_w, d_x, d_y, batch, rows, cols))
+    d_o = dev.alloc(batch * rows * 4)
+    for i in range(3):
+        d_y.fill(0x7F)
+        dev.sync()
+        g.launch()
+        dev.sync()
+        np.testing.assert_array_equal(d_y.to_numpy((batch, rows), np.float32), ref, err_msg=f"replay {i}")
+        dev.gemm(qtype, d_w, d_x, d_o, batch, rows, cols)  # eager work between replays
+        dev.sync()
+        np.testing.assert_array_equal(d_o.to_numpy((batch, rows), np.float32), ref)
+    g.destroy()
