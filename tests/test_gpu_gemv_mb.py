@@ -97,11 +97,31 @@ def test_mb_leaves_other_cases_to_the_vector_kernels(dev, qtype):
 def test_below_matrix_core_threshold_vs_f64(dev, qtype, rows, cols, batch):
     """Batches below the prefill GEMM's threshold for their type and shape (8192 rows or more
     / narrower but at least 4096 deep / the rest: Q4_0 and the dense types 96 / 64 / 128, Q4_K
-    8 / 32 / 64, Q6_K 16 / 48 / 96 tokens) take the small-batch or the vector kernels: within
+    128 / 96 / 96, Q6_K 16 / 48 / 96 tokens) take the small-batch or the vector kernels: within
     2^-20 * sum |w_i x_i| of float64."""
     raw, wd = random_matrix(qtype, rows, cols, seed=rows + 5 * batch)
     X = synth.normal_f32(rows + batch + 1, "Xt", (batch, cols), 0, 2)
     exact = X.astype(np.float64) @ wd.T
     got = gemm(dev, qtype, raw, X, rows, cols, batch).astype(np.float64)
+    bd = bound(wd, X)
+    assert np.all(np.abs(got - exact) <= bd), float(np.max(np.abs(got - exact) / bd))
+
+
+@pytest.mark.parametrize("rows,cols,batch", [(10240, 2560, 8), (2560, 10240, 16), (1000, 2560, 3), (37, 2048, 31),
+                                             (300, 1536, 17), (2500, 10240, 40), (64, 256, 2)])
+def test_mb_q4_k_integer_bitexact_and_random(dev, rows, cols, batch):
+    """Q4_K on the small-batch kernel: each 32-column block is one sub-block of a 256-column
+    super-block, scaled by d * sc_j with dmin * m_j * sum x subtracted (per-sub-block scale and
+    min decoded from the 12 packed bytes): integer operands exact, random ones within the
+    bound."""
+    raw, wd = int_matrix(B.Q4_K, rows, cols, seed=rows + cols + batch, scale_pow=-2)
+    X = np.random.default_rng(rows + batch).integers(-3, 4, (batch, cols)).astype(np.float32)
+    exact = X.astype(np.float64) @ wd.T
+    assert np.all(np.abs(exact) < 2 ** 24)
+    np.testing.assert_array_equal(gemm(dev, B.Q4_K, raw, X, rows, cols, batch), exact.astype(np.float32))
+    raw, wd = random_matrix(B.Q4_K, rows, cols, seed=rows + 3 * batch)
+    X = synth.normal_f32(rows + batch + 2, "Xk", (batch, cols), 0, 2)
+    exact = X.astype(np.float64) @ wd.T
+    got = gemm(dev, B.Q4_K, raw, X, rows, cols, batch).astype(np.float64)
     bd = bound(wd, X)
     assert np.all(np.abs(got - exact) <= bd), float(np.max(np.abs(got - exact) / bd))

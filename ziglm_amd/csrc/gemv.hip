@@ -1877,7 +1877,7 @@ static void launch_gemv(int qtype, GemvArgs& a, hipStream_t s) {
 
 // ---- small batches on the matrix cores ------------------------------------------------------
 // Products of 2 to gemm_mfma_min_batch - 1 tokens (hip_gemm below the prefill GEMM) with Q4_0,
-// Q8_0 or BF16 weights: v_mfma_f32_16x16x32_bf16 over tiles of 16 tokens x 16 rows x one
+// Q8_0, Q4_K or BF16 weights: v_mfma_f32_16x16x32_bf16 over tiles of 16 tokens x 16 rows x one
 // 32-column block, tokens on the A side (each x as three bf16 terms h + m + l, as the prefill
 // GEMM: exact to the f32 value's 24 bits), rows on the B side. Block quants enter as their
 // unsigned codes u (Q4_0 nibbles 0..15, Q8_0 q ^ 0x80: exact in bf16) and a block's sum is
@@ -1911,7 +1911,11 @@ __device__ __forceinline__ void mb_codes(uint32_t u, uint32_t& p0, uint32_t& p1)
 template <int QT, int NT, int KS>
 __global__ __launch_bounds__(KS * kWave) void k_gemv_mb(GemvArgs a) {
     constexpr bool SC = QT != HIP_BRIDGE_BF16;
-    constexpr uint32_t BB = QT == HIP_BRIDGE_Q4_0 ? 18u : QT == HIP_BRIDGE_Q8_0 ? 34u : 64u;  // bytes / block
+    // Q4_K: a 32-column block is sub-block j = kb % 8 of super-block kb / 8 (144 bytes:
+    // {f16 d, f16 dmin, scales[12], qs[128]}); its codes are the low (j even) or high nibbles
+    // of qs[32 (j / 2) ..], and its sum is (d sc_j) sum u x - (dmin m_j) sum x
+    constexpr bool KQ = QT == HIP_BRIDGE_Q4_K;
+    constexpr uint32_t BB = QT == HIP_BRIDGE_Q4_0 ? 18u : QT == HIP_BRIDGE_Q8_0 ? 34u : KQ ? 144u : 64u;  // bytes / block
     constexpr float C = QT == HIP_BRIDGE_Q4_0 ? 8.0f : 128.0f;
     __shared__ f32x4 s_red[KS][NT][kWave];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -1934,7 +1938,7 @@ __global__ __launch_bounds__(KS * kWave) void k_gemv_mb(GemvArgs a) {
     }
     // the lane's quant bytes in a block: Q4_0 columns 8g .. are the low (g < 2) / high nibbles
     // of bytes 8 (g & 1) ..; Q8_0 bytes 8g ..; BF16 elements 8g ..
-    const uint32_t qoff = QT == HIP_BRIDGE_Q4_0 ? 2u + 8u * (g & 1) : QT == HIP_BRIDGE_Q8_0 ? 2u + 8u * g : 16u * g;
+    const uint32_t qoff = QT == HIP_BRIDGE_Q4_0 ? 2u + 8u * (g & 1) : QT == HIP_BRIDGE_Q8_0 ? 2u + 8u * g : KQ ? 16u + 8u * g : 16u * g;
     const uint32_t nsh = QT == HIP_BRIDGE_Q4_0 ? 4u * (g >> 1) : 0u;
     bf16x8 ones;
 #pragma unroll
@@ -1948,10 +1952,18 @@ __global__ __launch_bounds__(KS * kWave) void k_gemv_mb(GemvArgs a) {
         const f32x4 xa = ldf4(xr + 32 * kb), xb = ldf4(xr + 32 * kb + 4);
         u32x4 wq[NT];
         uint32_t dd[NT];
+        uint32_t ks3[KQ ? NT : 1][3];  // Q4_K: scales[12] of the super-block
 #pragma unroll
         for (int j = 0; j < NT; ++j) {
             const unsigned char* blk = wrow[j] + BB * (uint32_t)kb;
-            if constexpr (QT == HIP_BRIDGE_BF16) {
+            if constexpr (KQ) {
+                const unsigned char* sb = wrow[j] + BB * (uint32_t)(kb >> 3);
+                const u32x2 v = *reinterpret_cast<const u32x2_a2*>(sb + qoff + 32u * ((uint32_t)(kb & 7) >> 1));
+                wq[j] = u32x4{v.x, v.y, 0u, 0u};
+                dd[j] = ldw32_a2(sb);
+#pragma unroll
+                for (int i = 0; i < 3; ++i) ks3[j][i] = ldw32_a2(sb + 4u + 4u * i);
+            } else if constexpr (QT == HIP_BRIDGE_BF16) {
                 wq[j] = *reinterpret_cast<const u32x4*>(blk + qoff);
                 dd[j] = 0;
             } else {
@@ -1986,7 +1998,11 @@ __global__ __launch_bounds__(KS * kWave) void k_gemv_mb(GemvArgs a) {
                     bw = wq[j];
                 } else {
                     uint32_t u0 = wq[j].x, u1 = wq[j].y;
-                    if constexpr (QT == HIP_BRIDGE_Q4_0) {
+                    if constexpr (KQ) {
+                        const uint32_t ksh = 4u * ((uint32_t)kb & 1u);
+                        u0 = mask_bytes(u0 >> ksh, 0x0f0f0f0fu);
+                        u1 = mask_bytes(u1 >> ksh, 0x0f0f0f0fu);
+                    } else if constexpr (QT == HIP_BRIDGE_Q4_0) {
                         u0 = mask_bytes(u0 >> nsh, 0x0f0f0f0fu);
                         u1 = mask_bytes(u1 >> nsh, 0x0f0f0f0fu);
                     } else {
@@ -2003,9 +2019,21 @@ __global__ __launch_bounds__(KS * kWave) void k_gemv_mb(GemvArgs a) {
                     f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Ah, Bw, f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
                     p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Am, Bw, p, 0, 0, 0);
                     p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Al, Bw, p, 0, 0, 0);
-                    const float d = h2f(dd[j]);
+                    if constexpr (KQ) {
+                        // 6-bit scale and min of sub-block sj (quant.zig:285-290), as the prefill GEMM
+                        const uint32_t sj = (uint32_t)kb & 7u, b = 8u * (sj & 3u);
+                        const uint32_t s0 = (ks3[j][0] >> b) & 0xffu, s1 = (ks3[j][1] >> b) & 0xffu,
+                                       s2 = (ks3[j][2] >> b) & 0xffu;
+                        const uint32_t sc = sj < 4 ? (s0 & 63u) : ((s2 & 15u) | ((s0 >> 6) << 4));
+                        const uint32_t mq = sj < 4 ? (s1 & 63u) : ((s2 >> 4) | ((s1 >> 6) << 4));
+                        const float A = h2f(dd[j] & 0xffffu) * (float)sc, Bm = h2f(dd[j] >> 16) * (float)mq;
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) acc[j][r] = fmaf(d, fmaf(-C, sx[r], p[r]), acc[j][r]);
+                        for (int r = 0; r < 4; ++r) acc[j][r] = fmaf(A, p[r], fmaf(-Bm, sx[r], acc[j][r]));
+                    } else {
+                        const float d = h2f(dd[j]);
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) acc[j][r] = fmaf(d, fmaf(-C, sx[r], p[r]), acc[j][r]);
+                    }
                 } else {
                     acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Ah, Bw, acc[j], 0, 0, 0);
                     acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Am, Bw, acc[j], 0, 0, 0);
@@ -2049,9 +2077,10 @@ __global__ __launch_bounds__(KS * kWave) void k_gemv_mb(GemvArgs a) {
 #ifndef ZL_GEMV_MB_WAVES
 #define ZL_GEMV_MB_WAVES 1024
 #endif
-// Launches k_gemv_mb for a batch of 2 to gemm_mfma_min_batch - 1 tokens (Q4_0 / Q8_0 with
-// 2-byte aligned rows, BF16 with 16-byte aligned ones; cols % 32 == 0, at most 160 blocks;
-// x 16-byte aligned); returns false otherwise (the vector kernels take the product).
+// Launches k_gemv_mb for a batch of 2 to gemm_mfma_min_batch - 1 tokens (Q4_0 / Q8_0 / Q4_K
+// with 2-byte aligned rows, BF16 with 16-byte aligned ones; cols % 32 == 0, Q4_K % 256; at most
+// 160 blocks, or 320 from 12 tokens; x 16-byte aligned); returns false otherwise (the vector
+// kernels take the product).
 template <int QT>
 static bool launch_mb_t(const GemvArgs& a, hipStream_t s) {
     const int nblk = a.cols / 32;
@@ -2063,12 +2092,13 @@ static bool launch_mb_t(const GemvArgs& a, hipStream_t s) {
     int ks = 0;
     for (int k : {4, 8, 16})
         if (!ks && cdiv(nblk, k) <= 10) ks = k;
-    // Rows too long for 16 waves of 10 blocks: from 12 tokens, two halves of the blocks per
-    // row tile added into zeroed y, at most 2 row tiles per wave (Q4_0 2560 x 10240 at 16 / 32 /
-    // 48 / 63 tokens: 36 / 67 / 68 / 99 us against the vector kernel's 39 / 73 / 105 / ~137;
-    // at 8 tokens 33 against 23, so fewer tokens keep the vector kernel).
+    // Rows too long for 16 waves of 10 blocks: from 12 tokens (Q4_K 8), two halves of the blocks
+    // per row tile added into zeroed y, at most 2 row tiles per wave (Q4_0 2560 x 10240 at 16 /
+    // 32 / 48 / 63 tokens: 36 / 67 / 68 / 99 us against the vector kernel's 39 / 73 / 105 / ~137;
+    // at 8 tokens 33 against 23, so fewer tokens keep the vector kernel; Q4_K's is slower: 46
+    // us at 8 tokens).
     unsigned kz = 1;
-    if (!ks && ZL_GEMV_MB_SPLIT && a.batch >= 12 && cdiv(nblk, 2 * 16) <= 10) {
+    if (!ks && ZL_GEMV_MB_SPLIT && a.batch >= (QT == HIP_BRIDGE_Q4_K ? 8 : 12) && cdiv(nblk, 2 * 16) <= 10) {
         ks = 16;
         kz = 2;
     }
@@ -2101,6 +2131,8 @@ static bool launch_gemv_mb(int qtype, GemvArgs& a, hipStream_t s) {
             return wa % 2 == 0 && launch_mb_t<HIP_BRIDGE_Q4_0>(a, s);
         case HIP_BRIDGE_Q8_0:
             return wa % 2 == 0 && launch_mb_t<HIP_BRIDGE_Q8_0>(a, s);
+        case HIP_BRIDGE_Q4_K:
+            return a.cols % 256 == 0 && wa % 2 == 0 && launch_mb_t<HIP_BRIDGE_Q4_K>(a, s);
         case HIP_BRIDGE_BF16:
             return wa % 16 == 0 && a.row_bytes % 16 == 0 && launch_mb_t<HIP_BRIDGE_BF16>(a, s);
         default:
