@@ -651,6 +651,9 @@ def bench_gemv(dev):
         ("gate_q4_0_b8", B.Q4_0, [(I, H)], plain(B.Q4_0, I, H, 8), 8),
         ("down_q4_0_b8", B.Q4_0, [(H, I)], plain(B.Q4_0, H, I, 8), 8),
         ("gate_q8_0_b16", B.Q8_0, [(I, H)], plain(B.Q8_0, I, H, 16), 16),
+        ("down_q4_0_b32", B.Q4_0, [(H, I)], plain(B.Q4_0, H, I, 32), 32),
+        ("gate_q4_k_b8", B.Q4_K, [(I, H)], plain(B.Q4_K, I, H, 8), 8),
+        ("down_q4_k_b16", B.Q4_K, [(H, I)], plain(B.Q4_K, H, I, 16), 16),
     ]
     for name, qt, shapes, fn, batch in cases:
         out[name] = gemv_case(dev, name, qt, shapes, fn, batch)
