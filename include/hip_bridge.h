@@ -294,7 +294,7 @@ void hip_gemm(int qtype, const void* weights, const float* x, float* y, int batc
  * weights with cols % 32 == 0, Q4_K and Q6_K with cols % 256 == 0; x 16-byte aligned;
  * 128 * cols * sizeof(x element) < 4 GiB; else EUNSUPPORTED. f32 x and y without
  * up_weights is hip_gemm, which takes the matrix cores from 96 tokens for 8192 rows or more,
- * 64 for fewer rows at least 4096 deep, else 128 (Q4_K 128 / 96 / 96, Q6_K 16 / 48 / 96), and
+ * 64 for fewer rows at least 4096 deep, else 128 (Q4_K 128 / 96 / 96, Q6_K 64 / 96 / 96), and
  * the small-batch or vector kernels below. */
 void hip_gemm_ex(int qtype, const void* weights, const void* up_weights /*NULL*/, int x_dtype,
                  const void* x, int y_dtype, void* y, int batch_size, int rows, int cols,

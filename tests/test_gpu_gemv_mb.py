@@ -97,7 +97,7 @@ def test_mb_leaves_other_cases_to_the_vector_kernels(dev, qtype):
 def test_below_matrix_core_threshold_vs_f64(dev, qtype, rows, cols, batch):
     """Batches below the prefill GEMM's threshold for their type and shape (8192 rows or more
     / narrower but at least 4096 deep / the rest: Q4_0 and the dense types 96 / 64 / 128, Q4_K
-    128 / 96 / 96, Q6_K 16 / 48 / 96 tokens) take the small-batch or the vector kernels: within
+    128 / 96 / 96, Q6_K 64 / 96 / 96 tokens) take the small-batch or the vector kernels: within
     2^-20 * sum |w_i x_i| of float64."""
     raw, wd = random_matrix(qtype, rows, cols, seed=rows + 5 * batch)
     X = synth.normal_f32(rows + batch + 1, "Xt", (batch, cols), 0, 2)
@@ -107,21 +107,34 @@ def test_below_matrix_core_threshold_vs_f64(dev, qtype, rows, cols, batch):
     assert np.all(np.abs(got - exact) <= bd), float(np.max(np.abs(got - exact) / bd))
 
 
+@pytest.mark.parametrize("qtype", [B.Q4_K, B.Q6_K])
 @pytest.mark.parametrize("rows,cols,batch", [(10240, 2560, 8), (2560, 10240, 16), (1000, 2560, 3), (37, 2048, 31),
                                              (300, 1536, 17), (2500, 10240, 40), (64, 256, 2)])
-def test_mb_q4_k_integer_bitexact_and_random(dev, rows, cols, batch):
-    """Q4_K on the small-batch kernel: each 32-column block is one sub-block of a 256-column
-    super-block, scaled by d * sc_j with dmin * m_j * sum x subtracted (per-sub-block scale and
-    min decoded from the 12 packed bytes): integer operands exact, random ones within the
-    bound."""
-    raw, wd = int_matrix(B.Q4_K, rows, cols, seed=rows + cols + batch, scale_pow=-2)
+def test_mb_kquant_integer_bitexact_and_random(dev, qtype, rows, cols, batch):
+    """K-quants on the small-batch kernel. Q4_K: each 32-column block is one sub-block of a
+    256-column super-block, scaled by d * sc_j with dmin * m_j * sum x subtracted (scale and min
+    decoded from the 12 packed bytes); Q6_K: sc * (u - 32) per 16 columns as two exact bf16
+    terms, d per super-block. Integer operands exact, random ones within the bound."""
+    raw, wd = int_matrix(qtype, rows, cols, seed=rows + cols + batch, scale_pow=-2)
     X = np.random.default_rng(rows + batch).integers(-3, 4, (batch, cols)).astype(np.float32)
     exact = X.astype(np.float64) @ wd.T
     assert np.all(np.abs(exact) < 2 ** 24)
-    np.testing.assert_array_equal(gemm(dev, B.Q4_K, raw, X, rows, cols, batch), exact.astype(np.float32))
-    raw, wd = random_matrix(B.Q4_K, rows, cols, seed=rows + 3 * batch)
+    np.testing.assert_array_equal(gemm(dev, qtype, raw, X, rows, cols, batch), exact.astype(np.float32))
+    raw, wd = random_matrix(qtype, rows, cols, seed=rows + 3 * batch)
     X = synth.normal_f32(rows + batch + 2, "Xk", (batch, cols), 0, 2)
     exact = X.astype(np.float64) @ wd.T
-    got = gemm(dev, B.Q4_K, raw, X, rows, cols, batch).astype(np.float64)
+    got = gemm(dev, qtype, raw, X, rows, cols, batch).astype(np.float64)
     bd = bound(wd, X)
     assert np.all(np.abs(got - exact) <= bd), float(np.max(np.abs(got - exact) / bd))
+
+
+@pytest.mark.parametrize("rows,cols,batch", [(130, 512, 9), (77, 1024, 20)])
+def test_mb_q6_k_full_scale_range_exact(dev, rows, cols, batch):
+    """Q6_K int8 scales over their whole range (|sc * (u - 32)| up to 4096): both bf16 terms
+    carry it exactly, integer products bit for bit."""
+    from test_gpu_gemm import q6_k_full_scales
+    raw, wd = q6_k_full_scales(np.random.default_rng(rows + batch), rows, cols, 0.5)
+    X = np.random.default_rng(batch).integers(-1, 2, (batch, cols)).astype(np.float32)
+    exact = X.astype(np.float64) @ wd.T
+    assert np.all(np.abs(exact) < 2 ** 24) and np.max(np.abs(wd)) > 1000
+    np.testing.assert_array_equal(gemm(dev, B.Q6_K, raw, X, rows, cols, batch), exact.astype(np.float32))

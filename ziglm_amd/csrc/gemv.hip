@@ -1877,7 +1877,7 @@ static void launch_gemv(int qtype, GemvArgs& a, hipStream_t s) {
 
 // ---- small batches on the matrix cores ------------------------------------------------------
 // Products of 2 to gemm_mfma_min_batch - 1 tokens (hip_gemm below the prefill GEMM) with Q4_0,
-// Q8_0, Q4_K or BF16 weights: v_mfma_f32_16x16x32_bf16 over tiles of 16 tokens x 16 rows x one
+// Q8_0, Q4_K, Q6_K or BF16 weights: v_mfma_f32_16x16x32_bf16 over tiles of 16 tokens x 16 rows x one
 // 32-column block, tokens on the A side (each x as three bf16 terms h + m + l, as the prefill
 // GEMM: exact to the f32 value's 24 bits), rows on the B side. Block quants enter as their
 // unsigned codes u (Q4_0 nibbles 0..15, Q8_0 q ^ 0x80: exact in bf16) and a block's sum is
@@ -1915,7 +1915,13 @@ __global__ __launch_bounds__(KS * kWave) void k_gemv_mb(GemvArgs a) {
     // {f16 d, f16 dmin, scales[12], qs[128]}); its codes are the low (j even) or high nibbles
     // of qs[32 (j / 2) ..], and its sum is (d sc_j) sum u x - (dmin m_j) sum x
     constexpr bool KQ = QT == HIP_BRIDGE_Q4_K;
-    constexpr uint32_t BB = QT == HIP_BRIDGE_Q4_0 ? 18u : QT == HIP_BRIDGE_Q8_0 ? 34u : KQ ? 144u : 64u;  // bytes / block
+    // Q6_K: a 32-column block is quadrant t of half n (kb % 8 = 4 n + t) of super-block kb / 8
+    // (210 bytes: {ql[128], qh[64], int8 scales[16], f16 d}); lane group g's 8 values take the
+    // low (t < 2) or high nibbles of ql[64 n + 32 (t & 1) + 8 g ..], bits 2t, 2t + 1 of
+    // qh[32 n + 8 g ..] and scale sc[8 n + g / 2 + 2 t]; sc * (u - 32) (at most 13 bits) enters
+    // as two exact bf16 terms, and the super-block's d scales the block's sum
+    constexpr bool Q6 = QT == HIP_BRIDGE_Q6_K;
+    constexpr uint32_t BB = QT == HIP_BRIDGE_Q4_0 ? 18u : QT == HIP_BRIDGE_Q8_0 ? 34u : KQ ? 144u : Q6 ? 210u : 64u;  // bytes / block
     constexpr float C = QT == HIP_BRIDGE_Q4_0 ? 8.0f : 128.0f;
     __shared__ f32x4 s_red[KS][NT][kWave];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -1956,7 +1962,15 @@ __global__ __launch_bounds__(KS * kWave) void k_gemv_mb(GemvArgs a) {
 #pragma unroll
         for (int j = 0; j < NT; ++j) {
             const unsigned char* blk = wrow[j] + BB * (uint32_t)kb;
-            if constexpr (KQ) {
+            if constexpr (Q6) {
+                const unsigned char* sb = wrow[j] + BB * (uint32_t)(kb >> 3);
+                const uint32_t n6 = ((uint32_t)kb >> 2) & 1u, t6 = (uint32_t)kb & 3u;
+                const u32x2 ql = *reinterpret_cast<const u32x2_a2*>(sb + 64u * n6 + 32u * (t6 & 1u) + 8u * g);
+                const u32x2 qh = *reinterpret_cast<const u32x2_a2*>(sb + 128u + 32u * n6 + 8u * g);
+                wq[j] = u32x4{ql.x, ql.y, qh.x, qh.y};
+                const uint32_t scw = ldw16(sb + 192u + 8u * n6 + 2u * t6);  // scales 8n+2t, 8n+2t+1
+                dd[j] = ldw16(sb + 208u) | (((scw >> (8u * ((uint32_t)g >> 1))) & 0xffu) << 16);
+            } else if constexpr (KQ) {
                 const unsigned char* sb = wrow[j] + BB * (uint32_t)(kb >> 3);
                 const u32x2 v = *reinterpret_cast<const u32x2_a2*>(sb + qoff + 32u * ((uint32_t)(kb & 7) >> 1));
                 wq[j] = u32x4{v.x, v.y, 0u, 0u};
@@ -1986,13 +2000,42 @@ __global__ __launch_bounds__(KS * kWave) void k_gemv_mb(GemvArgs a) {
             const bf16x8 Ah = __builtin_bit_cast(bf16x8, th), Am = __builtin_bit_cast(bf16x8, tm),
                          Al = __builtin_bit_cast(bf16x8, tl);
             f32x4 sx{};
-            if constexpr (SC) {
+            if constexpr (SC && !Q6) {
                 sx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Ah, ones, f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
                 sx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Am, ones, sx, 0, 0, 0);
                 sx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Al, ones, sx, 0, 0, 0);
             }
 #pragma unroll
             for (int j = 0; j < NT; ++j) {
+                if constexpr (Q6) {
+                    const uint32_t t6 = (uint32_t)kb & 3u, nsh6 = t6 < 2 ? 0u : 4u, hsh = 2u * t6;
+                    const float sc = (float)(int8_t)(uint8_t)(dd[j] >> 16);
+                    const uint32_t qlw[2] = {wq[j].x, wq[j].y}, qhw[2] = {wq[j].z, wq[j].w};
+                    u32x4 hw, lw;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        float v[2];
+#pragma unroll
+                        for (int k = 0; k < 2; ++k) {
+                            const uint32_t b = 8u * (uint32_t)((2 * e + k) & 3), w = (uint32_t)(2 * e + k) >> 2;
+                            const uint32_t u = ((qlw[w] >> (b + nsh6)) & 15u) | (((qhw[w] >> (b + hsh)) & 3u) << 4);
+                            v[k] = sc * (float)((int)u - 32);  // an integer of at most 13 bits: exact
+                        }
+                        const uint32_t hi = pack_bf16x2(v[0], v[1]);
+                        hw[e] = hi;
+                        lw[e] = pack_bf16x2(v[0] - bf16_lo(hi), v[1] - bf16_hi(hi));
+                    }
+                    const bf16x8 Wh = __builtin_bit_cast(bf16x8, hw), Wl = __builtin_bit_cast(bf16x8, lw);
+                    f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Ah, Wh, f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                    p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Am, Wh, p, 0, 0, 0);
+                    p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Ah, Wl, p, 0, 0, 0);
+                    p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Al, Wh, p, 0, 0, 0);
+                    p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Am, Wl, p, 0, 0, 0);
+                    const float d = h2f(dd[j] & 0xffffu);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[j][r] = fmaf(d, p[r], acc[j][r]);
+                    continue;
+                }
                 u32x4 bw;
                 if constexpr (QT == HIP_BRIDGE_BF16) {
                     bw = wq[j];
@@ -2077,8 +2120,9 @@ __global__ __launch_bounds__(KS * kWave) void k_gemv_mb(GemvArgs a) {
 #ifndef ZL_GEMV_MB_WAVES
 #define ZL_GEMV_MB_WAVES 1024
 #endif
-// Launches k_gemv_mb for a batch of 2 to gemm_mfma_min_batch - 1 tokens (Q4_0 / Q8_0 / Q4_K
-// with 2-byte aligned rows, BF16 with 16-byte aligned ones; cols % 32 == 0, Q4_K % 256; at most
+// Launches k_gemv_mb for a batch of 2 (Q6_K 8) to gemm_mfma_min_batch - 1 tokens (Q4_0 / Q8_0 /
+// Q4_K / Q6_K with 2-byte aligned rows, BF16 with 16-byte aligned ones; cols % 32 == 0, K-quants
+// % 256; at most
 // 160 blocks, or 320 from 12 tokens; x 16-byte aligned); returns false otherwise (the vector
 // kernels take the product).
 template <int QT>
@@ -2133,6 +2177,8 @@ static bool launch_gemv_mb(int qtype, GemvArgs& a, hipStream_t s) {
             return wa % 2 == 0 && launch_mb_t<HIP_BRIDGE_Q8_0>(a, s);
         case HIP_BRIDGE_Q4_K:
             return a.cols % 256 == 0 && wa % 2 == 0 && launch_mb_t<HIP_BRIDGE_Q4_K>(a, s);
+        case HIP_BRIDGE_Q6_K:  // (below 8 tokens the vector kernel: 10240 x 2560 at 4, 24 against 38 us)
+            return a.batch >= 8 && a.cols % 256 == 0 && wa % 2 == 0 && launch_mb_t<HIP_BRIDGE_Q6_K>(a, s);
         case HIP_BRIDGE_BF16:
             return wa % 16 == 0 && a.row_bytes % 16 == 0 && launch_mb_t<HIP_BRIDGE_BF16>(a, s);
         default:

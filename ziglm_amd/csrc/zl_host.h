@@ -42,8 +42,9 @@ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // kernels' time grows with the batch. The batch from which it wins, measured per type on
 // 10240 x 2560 (160 row tiles: "wide") and 2560 x 10240 (40, deep enough to split) products:
 // Q4_0 / Q8_0 96 / 64, Q4_K 128 / 96 (against the small-batch kernel: 44 / 86 us at 64 tokens,
-// the matrix cores 73 / 136), Q6_K 16 / 48; narrow products too shallow to split keep the
-// unsplit crossovers (128, 96, 96).
+// the matrix cores 73 / 136), Q6_K 64 / 96 (small-batch kernel at 48 tokens 73 / 80 us, matrix
+// cores 86 / 173); narrow products too shallow to split keep the unsplit crossovers (128, 96,
+// 96).
 // y[0, n) = 0 (a kernel, not hipMemsetAsync, so that graph captures of the products that
 // add into y replay correctly)
 void launch_zero_f32(float* y, int64_t n, hipStream_t s);
@@ -55,7 +56,7 @@ inline int gemm_mfma_min_batch(int qtype, int rows, int cols) {
     const bool wide = rows >= 128 * 64;  // enough row tiles to fill half the chip's workgroup slots
     const bool deep = ZL_GEMM_SPLITK && cols >= ZL_GEMM_SPLITK_MIN_COLS;
     if (qtype == HIP_BRIDGE_Q4_K) return wide ? 128 : 96;
-    if (qtype == HIP_BRIDGE_Q6_K) return wide ? 16 : deep ? 48 : 96;
+    if (qtype == HIP_BRIDGE_Q6_K) return wide ? 64 : 96;
     return wide ? 96 : deep ? 64 : 128;
 }
 bool launch_gemm_mfma(int qtype, const void* w, int64_t row_bytes, const float* x, float* y, int rows, int cols,
