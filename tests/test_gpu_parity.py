@@ -319,6 +319,55 @@ def test_norm_modes_many_rows(dev, oracle, dtype, n, rows):
           floor * inv2 * np.abs(1.0 + w2.astype(np.float64)))
 
 
+@pytest.mark.parametrize("dtype,n", [(B.BF16, 5376), (B.BF16, 4104), (B.BF16, 8192), (B.F32, 2560)])
+@pytest.mark.parametrize("weighted", [True, False])
+def test_norm_pipelined_rows_equal_row_kernel(dev, oracle, dtype, n, weighted):
+    """Launches of 16384 or more waves at four waves a row (4099 rows here) take the
+    persistent, pipelined row kernel for the norm, add + norm and norm + add modes, whose
+    workgroups walk several rows each (an odd count for some); the same rows in two launches
+    under that size take the one-shot row kernel. Both do the same arithmetic in the same
+    order, so every output is bit-equal between the two; the norm is also checked against the
+    oracle. 4104 leaves part of each row's last chunk column empty, 8192 fills four chunks per
+    lane; no weight, and plain (not unit-offset) weights, take the other factor forms. add +
+    norm writes its output over the residual, as the reference's decode step does."""
+    rows, split = 4099, 2050
+    bf = dtype == B.BF16
+    gen = synth.normal_bf16 if bf else synth.normal_f32
+    npdt = np.uint16 if bf else np.float32
+    es = 2 if bf else 4
+    x = gen(21, "x", (rows, n))
+    r = gen(21, "r", (rows, n))
+    w = synth.normal_f32(21, "w", (n,), 0, 0.1) if weighted else None
+    uo = weighted  # weighted: (1 + w); otherwise no weight at all
+    d_w = dev.from_numpy(w) if weighted else None
+
+    def both(run):
+        """run(x_view, r_view, out_view, rows) over all rows at once, then in two launches."""
+        outs = []
+        for parts in ([(0, rows)], [(0, split), (split, rows - split)]):
+            d_x, d_r, d_o = dev.from_numpy(x), dev.from_numpy(r), dev.alloc(x.nbytes)
+            d_o.fill(0)  # the modes that write no separate output leave it zero in both runs
+            for r0, cnt in parts:
+                off = r0 * n * es
+                run(d_x.at(off), d_r.at(off), d_o.at(off), cnt)
+            dev.sync()
+            outs.append(tuple(b.to_numpy(x.shape, npdt) for b in (d_x, d_r, d_o)))
+            for b in (d_x, d_r, d_o):
+                b.deinit()
+        for k, what in enumerate(("x", "r", "out")):
+            assert_bitexact(outs[0][k], outs[1][k], what)
+        return outs[0]
+
+    _, _, o = both(lambda dx, dr, do, cnt: dev.rmsNormRows(dtype, dx, d_w, do, cnt, n, EPS, uo))
+    if bf:  # the bf16 oracle is the f32 one between exact widening and RNE narrowing
+        ref = oracle.f32_to_bf16(oracle.rms_norm(O.get().bf16_to_f32(x), w, EPS, uo))
+        assert_bf16(o, ref, 1, what="norm")
+    else:
+        assert_rel(o, oracle.rms_norm(x, w, EPS, uo), 1e-5, what="norm")
+    both(lambda dx, dr, do, cnt: dev.addRmsNormRows(dtype, dx, dr, d_w, dr, cnt, n, EPS, uo))
+    both(lambda dx, dr, do, cnt: dev.rmsnormAddRows(dtype, dx, dr, d_w, cnt, n, EPS, uo))
+
+
 # ---------------------------------------------------------------------------------------
 # QK-norm + RoPE + KV append
 # ---------------------------------------------------------------------------------------

@@ -24,6 +24,10 @@
 #include "zl_common.h"
 #include "zl_host.h"
 
+#include <algorithm>
+#include <atomic>
+#include <type_traits>
+
 namespace zl {
 
 enum NormMode { M_NORM = 0, M_ADD_NORM = 1, M_NORM_ADD = 2, M_NORM_ADD_NORM = 3 };
@@ -386,6 +390,166 @@ __global__ __launch_bounds__(256) void k_norm_rows(NormArgs a) {
     }
 }
 
+// Persistent, software-pipelined form for launches of several rounds of 4-wave rows: as many
+// workgroups as stay resident, each walking rows blockIdx.x, blockIdx.x + gridDim.x, ...,
+// with the next row's loads issued before the current row is reduced and stored, so a
+// workgroup keeps a row in flight from its first load to its last store instead of
+// alternating between a load phase and a reduce / store phase; the norm factors are loaded
+// once per workgroup. Same arithmetic, in the same order, as k_norm_rows at 4 waves per row.
+// The loop is unrolled by two so that both register buffers have compile-time indices; the
+// reduction slots alternate with them (a wave that runs ahead into the next row writes the
+// other slot set, and cannot reach the row after it before every wave has passed the next
+// row's barrier). Rows go round-robin over the workgroups, so the rows in flight at any time
+// are neighbours. Measured at 8192 x 5376 bf16 and not taken (us, input norm / add + norm /
+// norm + add, against 29.7 / 58.5 / 42.9): a contiguous range of rows per workgroup 35.5 /
+// 67.3 / 50.3; default-policy loads 31.7 / 62.4 / 49.8; three row buffers (two rows in
+// flight) at the same workgroup counts 31.6 / 59.2 / 45.3, at one workgroup per CU 31.7 /
+// 59.6 / 42.8.
+template <typename T, int NC, int MODE>
+__global__ __launch_bounds__(256) void k_norm_pipe(NormArgs a) {
+    using C = Chunk<T>;
+    constexpr int E = C::E;
+    constexpr int W = 4;
+    constexpr int STRIDE = kWave * W;
+    constexpr int LP = ZL_NORM_LP, SP = ZL_NORM_SP;
+    __shared__ float s_red[2][2][W];  // [buffer][reduction][wave]
+    const int g = threadIdx.x;
+    const int n = a.n;
+    const int nch = n / E;
+    const uint32_t row_bytes = (uint32_t)n * sizeof(T);
+    const bool has_w1 = a.w1 != nullptr;
+    const bool has_w2 = a.w2 != nullptr;
+    const int64_t end = a.rows;
+    const int64_t step = gridDim.x;
+
+    u32x4 bx[2][NC], br[2][NC];
+    // every load of a row through range-checked resources (rows past the tensor read zeros)
+    auto issue = [&](auto B, int64_t row) {
+        constexpr int b = decltype(B)::value;
+        const bool ok = row < end;
+        const int64_t rr = ok ? row : 0;
+        const auto rsx = buf_rsrc((const T*)a.x + rr * n, ok ? row_bytes : 0u);
+        const auto rsr = buf_rsrc((const T*)a.r + rr * n, ok && MODE != M_NORM ? row_bytes : 0u);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const uint32_t off = (uint32_t)(g + c * STRIDE) * 16u;
+            bx[b][c] = bldp<LP>(rsx, off);
+            if constexpr (MODE != M_NORM) br[b][c] = bldp<LP>(rsr, off);
+        }
+    };
+    float f1[NC][E];
+    float f2[MODE == M_NORM_ADD_NORM ? NC : 1][E];
+
+    // one row (row < a.rows, block-uniform) from buffer B
+    auto process = [&](auto B, int64_t row) {
+        constexpr int b = decltype(B)::value;
+        T* const xrow = (T*)a.x + row * n;
+        T* const orow = (T*)a.out + row * n;
+        const auto wsx = buf_rsrc(xrow, MODE != M_NORM ? row_bytes : 0u);
+        const auto wso = buf_rsrc(orow, MODE != M_NORM_ADD ? row_bytes : 0u);
+        float v[NC][E];
+        float ss = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            if (g + c * STRIDE < nch) {
+                if constexpr (MODE == M_NORM) {
+                    C::unpack(bx[b][c], v[c]);
+                } else if constexpr (MODE == M_ADD_NORM) {
+                    float xv[E], rv[E];
+                    C::unpack(bx[b][c], xv);
+                    C::unpack(br[b][c], rv);
+#pragma unroll
+                    for (int j = 0; j < E; ++j) v[c][j] = xv[j] + rv[j];
+                } else {
+                    C::unpack(br[b][c], v[c]);
+                }
+#pragma unroll
+                for (int j = 0; j < E; ++j) ss = fmaf(v[c][j], v[c][j], ss);
+            }
+        }
+        ss = row_sum<W>(ss, s_red[b][0]);
+        const float inv = rms_inv_hw(ss, n, a.eps);
+        if constexpr (MODE == M_NORM || MODE == M_ADD_NORM) {
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                const int idx = g + c * STRIDE;
+                if (idx < nch) {
+                    float y[E];
+#pragma unroll
+                    for (int j = 0; j < E; ++j) y[j] = (v[c][j] * inv) * w_factor(f1[c][j], has_w1, a.uo);
+                    if constexpr (MODE == M_ADD_NORM) strow16<SP>(xrow, wsx, (uint32_t)idx * 16u, C::pack(v[c]));
+                    strow16<SP>(orow, wso, (uint32_t)idx * 16u, C::pack(y));
+                }
+            }
+        } else if constexpr (MODE == M_NORM_ADD) {
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                const int idx = g + c * STRIDE;
+                if (idx < nch) {
+                    float xv[E];
+                    C::unpack(bx[b][c], xv);
+#pragma unroll
+                    for (int j = 0; j < E; ++j) xv[j] = xv[j] + (v[c][j] * inv) * w_factor(f1[c][j], has_w1, a.uo);
+                    strow16<SP>(xrow, wsx, (uint32_t)idx * 16u, C::pack(xv));
+                }
+            }
+        } else {  // M_NORM_ADD_NORM
+            float ss2 = 0.0f;
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                if (g + c * STRIDE < nch) {
+                    float xv[E];
+                    C::unpack(bx[b][c], xv);
+#pragma unroll
+                    for (int j = 0; j < E; ++j) {
+                        v[c][j] = xv[j] + (v[c][j] * inv) * w_factor(f1[c][j], has_w1, a.uo);
+                        ss2 = fmaf(v[c][j], v[c][j], ss2);
+                    }
+                }
+            }
+            ss2 = row_sum<W>(ss2, s_red[b][1]);
+            const float inv2 = rms_inv_hw(ss2, n, a.eps);
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                const int idx = g + c * STRIDE;
+                if (idx < nch) {
+                    float y[E];
+#pragma unroll
+                    for (int j = 0; j < E; ++j) y[j] = (v[c][j] * inv2) * w_factor(f2[c][j], has_w2, a.uo);
+                    strow16<SP>(xrow, wsx, (uint32_t)idx * 16u, C::pack(v[c]));
+                    strow16<SP>(orow, wso, (uint32_t)idx * 16u, C::pack(y));
+                }
+            }
+        }
+    };
+
+    constexpr std::integral_constant<int, 0> B0{};
+    constexpr std::integral_constant<int, 1> B1{};
+    int64_t row = blockIdx.x;
+    issue(B0, row);
+    // the weights once, behind the first row's loads
+    {
+        const auto rsw1 = buf_rsrc(a.w1, has_w1 ? (uint32_t)n * 4u : 0u);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) load_wb<E>(rsw1, (uint32_t)(g + c * STRIDE) * E * 4u, f1[c]);
+        if constexpr (MODE == M_NORM_ADD_NORM) {
+            const auto rsw2 = buf_rsrc(a.w2, has_w2 ? (uint32_t)n * 4u : 0u);
+#pragma unroll
+            for (int c = 0; c < NC; ++c) load_wb<E>(rsw2, (uint32_t)(g + c * STRIDE) * E * 4u, f2[c]);
+        }
+    }
+    // one row in flight while another is reduced and stored
+    while (row < end) {
+        issue(B1, row + step);
+        process(B0, row);
+        row += step;
+        if (row >= end) break;
+        issue(B0, row + step);
+        process(B1, row);
+        row += step;
+    }
+}
+
 // ---- block-per-row fallback: any n, any alignment ------------------------------------------
 
 template <typename T>
@@ -490,6 +654,60 @@ static void launch_w(const NormArgs& a, int per_lane, int R, hipStream_t s) {
     else if (per_lane <= 8) k_norm_rows<T, 8, MODE, W, 1, WL><<<grid1, NT, 0, s>>>(a);
     else if constexpr (W == 4) k_norm_rows<T, 16, MODE, W, 1, WL><<<grid1, NT, 0, s>>>(a);
 }
+// Launches of at least this many waves (rows x waves per row, at 4 waves per row) take
+// k_norm_pipe (0: never) with pipe_wgs_per_cu<MODE>() workgroups per CU. Measured on MI355X
+// at 8192 x 5376 bf16 (us; k_norm_rows with two rows per group and 4096 workgroups, then
+// k_norm_pipe at 1 / 2 / 3 / 4 workgroups per CU and at its occupancy limit of 4-7, two
+// runs each, within 0.3%):
+//   input norm         31.6 -> 37.3 / 30.5 / 29.7 / 30.8 / 31.7
+//   add + norm         60.9 -> 58.4 / 60.3 / 63.5 / 64.0 / 63.3
+//   norm + add         44.9 -> 45.1 / 42.9 / 45.4 / 45.8 / 45.8
+//   norm + add + norm  61.3 -> 65.0 / 61.9 / 65.7 / 65.5 / 65.1 (keeps k_norm_rows)
+// Each mode has its own best count of rows in flight per CU; more or fewer are slower.
+#ifndef ZL_NORM_PIPE_WAVES
+#define ZL_NORM_PIPE_WAVES 16384
+#endif
+// Nonzero: workgroups per CU of every mode's k_norm_pipe launch (tuning builds).
+#ifndef ZL_NORM_PIPE_WG
+#define ZL_NORM_PIPE_WG 0
+#endif
+template <int MODE>
+constexpr int pipe_wgs_per_cu() {
+    return ZL_NORM_PIPE_WG ? ZL_NORM_PIPE_WG
+           : MODE == M_NORM ? 3
+           : MODE == M_ADD_NORM ? 1
+           : MODE == M_NORM_ADD ? 2
+                                : 0;
+}
+// Compute units of the current device (looked up once).
+static int device_cus() {
+    static std::atomic<int> cus{0};
+    int c = cus.load(std::memory_order_relaxed);
+    if (c == 0) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0)
+            c = 256;
+        cus.store(c, std::memory_order_relaxed);
+    }
+    return c;
+}
+// false: this mode keeps k_norm_rows
+template <typename T, int MODE>
+static bool launch_pipe(const NormArgs& a, int per_lane, hipStream_t s) {
+    constexpr int wg = pipe_wgs_per_cu<MODE>();
+    if constexpr (wg == 0) {
+        return false;
+    } else {
+        const unsigned grid = (unsigned)std::min<int64_t>(a.rows, (int64_t)device_cus() * wg);
+        if (per_lane <= 1) k_norm_pipe<T, 1, MODE><<<grid, 256, 0, s>>>(a);
+        else if (per_lane <= 2) k_norm_pipe<T, 2, MODE><<<grid, 256, 0, s>>>(a);
+        else if (per_lane <= 3) k_norm_pipe<T, 3, MODE><<<grid, 256, 0, s>>>(a);
+        else k_norm_pipe<T, 4, MODE><<<grid, 256, 0, s>>>(a);
+        return true;
+    }
+}
+
 template <typename T, int MODE, int W>
 static void launch_wl(const NormArgs& a, int per_lane, int R, bool late, hipStream_t s) {
     if (late) launch_w<T, MODE, W, true>(a, per_lane, R, s);
@@ -545,7 +763,10 @@ static void launch_t(const NormArgs& a, hipStream_t s) {
     const bool vec = a.n % E == 0 && aligned16(a.x) && (MODE == M_NORM || aligned16(a.r)) &&
                      (MODE == M_NORM_ADD || aligned16(a.out)) && aligned16(a.w1) &&
                      (MODE != M_NORM_ADD_NORM || aligned16(a.w2)) && per_lane <= (W == 4 ? 16 : 8);
-    if (vec) {
+    const bool pipe = vec && W == 4 && per_lane <= 4 && ZL_NORM_PIPE_WAVES > 0 && waves >= ZL_NORM_PIPE_WAVES;
+    if (pipe && launch_pipe<T, MODE>(a, per_lane, s)) {
+        // launched: persistent, pipelined rows
+    } else if (vec) {
         if (W == 4) launch_wl<T, MODE, 4>(a, per_lane, R, late, s);
         else if (W == 2) launch_wl<T, MODE, 2>(a, per_lane, R, late, s);
         else launch_wl<T, MODE, 1>(a, per_lane, R, late, s);
