@@ -471,6 +471,57 @@ def test_qk_partial_rotary(dev, oracle, D, rot):
     qk_case(dev, oracle, B.BF16, 3, 4, 2, D, rot, 1e6, [3, 900, 4095])
 
 
+@pytest.mark.parametrize("dtype,nh,nkv,D,rot,v_norm", [
+    (B.BF16, 32, 16, 128, 0, False),  # Gemma-27B heads (the c4 shape)
+    (B.F32, 8, 4, 256, 0, False),
+    (B.BF16, 16, 4, 256, 128, False),  # partial rotary
+    (B.BF16, 64, 16, 64, 0, True),  # Gemma-4 V no-scale norm
+])
+def test_qk_many_tokens_equal_split_launches(dev, oracle, dtype, nh, nkv, D, rot, v_norm):
+    """A launch of 4100 tokens whose head rows take two passes of a workgroup, against the same
+    tokens in two launches (views into the same buffers and position array): Q and both
+    caches bit-equal, so a token's result depends on nothing but its own rows and position.
+    Positions come from a device array, all distinct, some at or past max_seq (those tokens'
+    K / V rows are not written). The whole launch is also checked against the oracle at
+    in-range positions."""
+    T, split, max_seq = 4100, 2050, 8192
+    bf = dtype == B.BF16
+    gen = synth.normal_bf16 if bf else synth.normal_f32
+    cdt = np.uint16 if bf else np.float32
+    es = 2 if bf else 4
+    q = gen(31, "q", (T, nh, D))
+    k = gen(31, "k", (T, nkv, D))
+    v = gen(31, "v", (T, nkv, D))
+    d_wq = dev.from_numpy(synth.normal_f32(31, "wq", (D,), 0, 0.1))
+    d_wk = dev.from_numpy(synth.normal_f32(31, "wk", (D,), 0, 0.1))
+    rng = np.random.default_rng(31)
+    pos = rng.permutation(max_seq + 64)[:T].astype(np.int32)
+    assert np.any(pos >= max_seq)
+
+    def run(parts):
+        d_q, d_k, d_v, d_pos = dev.from_numpy(q), dev.from_numpy(k), dev.from_numpy(v), dev.from_numpy(pos)
+        d_kc, d_vc = dev.alloc(max_seq * nkv * D * es), dev.alloc(max_seq * nkv * D * es)
+        d_kc.fill(0)
+        d_vc.fill(0)
+        for t0, cnt in parts:
+            dev.qkNormRopeKv(dtype, d_q.at(t0 * nh * D * es), d_k.at(t0 * nkv * D * es),
+                             d_v.at(t0 * nkv * D * es), d_wq, d_wk, v_norm, d_kc, d_vc, max_seq, 0,
+                             max_seq, nkv * D, d_pos.at(t0 * 4), 0, None, cnt, nh, nkv, D, rot, 10000.0,
+                             1.0, EPS, True)
+        dev.sync()
+        out = (d_q.to_numpy(q.shape, cdt), d_kc.to_numpy((max_seq, nkv * D), cdt),
+               d_vc.to_numpy((max_seq, nkv * D), cdt))
+        for b in (d_q, d_k, d_v, d_pos, d_kc, d_vc):
+            b.deinit()
+        return out
+
+    whole, halves = run([(0, T)]), run([(0, split), (split, T - split)])
+    for got, ref, what in zip(whole, halves, ("Q", "K cache", "V cache")):
+        assert_bitexact(got, ref, what)
+    qk_case(dev, oracle, dtype, T, nh, nkv, D, rot, 10000.0, rng.permutation(max_seq)[:T], v_norm=v_norm,
+            max_seq=max_seq, seed=32)
+
+
 @pytest.mark.parametrize("D,rot", [(96, 0), (128, 24)])
 def test_qk_generic_path(dev, oracle, D, rot):
     """Generic path: head_dim outside the fused set, or (bf16) a rotary half that is not a

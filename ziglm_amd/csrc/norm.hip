@@ -25,7 +25,6 @@
 #include "zl_host.h"
 
 #include <algorithm>
-#include <atomic>
 #include <type_traits>
 
 namespace zl {
@@ -678,19 +677,6 @@ constexpr int pipe_wgs_per_cu() {
            : MODE == M_ADD_NORM ? 1
            : MODE == M_NORM_ADD ? 2
                                 : 0;
-}
-// Compute units of the current device (looked up once).
-static int device_cus() {
-    static std::atomic<int> cus{0};
-    int c = cus.load(std::memory_order_relaxed);
-    if (c == 0) {
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0)
-            c = 256;
-        cus.store(c, std::memory_order_relaxed);
-    }
-    return c;
 }
 // false: this mode keeps k_norm_rows
 template <typename T, int MODE>

@@ -30,7 +30,10 @@
 // staging its own weights in LDS, 8.6-9.0 us when the kernel took 7.9); each lane loading
 // the norm weights of its own chunks into registers instead of the LDS staging (7.3 us, the
 // weight loads as many load instructions as the rows'); one or four tokens per workgroup
-// (8.9 / 8.7 us).
+// (8.9 / 8.7 us); a persistent form whose workgroups walk the tokens with the next token's
+// head rows in flight (as the row norms do at 8192 rows), bit-equal to this one: Gemma-27B
+// heads at 8192 tokens 44.8 -> 48.7 us at its best grid (3-4 workgroups per CU; 2, 6 and 8
+// were slower still).
 // Generic path (other head sizes up to 512, any alignment): one wave per head row (Q, K or V
 // head), head staged in LDS, four rows per workgroup.
 #include <math.h>

@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 #include "../../include/hip_bridge.h"
 
 namespace zl {
@@ -23,6 +25,23 @@ inline hipStream_t stream_of(HipStream_t s) { return reinterpret_cast<hipStream_
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Compute units of the current device, looked up once (the persistent kernels size their
+// grids by it); 256 if the query fails.
+inline int device_cus() {
+    static std::atomic<int> cus{0};
+    int c = cus.load(std::memory_order_relaxed);
+    if (c == 0) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) {
+            (void)hipGetLastError();  // the failed query's error is not an op's
+            c = 256;
+        }
+        cus.store(c, std::memory_order_relaxed);
+    }
+    return c;
+}
 
 // Matrix-core GEMM (gemm.hip) for batches of at least gemm_mfma_min_batch(qtype, rows, cols) tokens:
 // launches and returns true when the type, shape (cols % 32 == 0, K-quants % 256) and
