@@ -661,7 +661,8 @@ static void launch_w(const NormArgs& a, int per_lane, int R, hipStream_t s) {
 //   input norm         31.6 -> 37.3 / 30.5 / 29.7 / 30.8 / 31.7
 //   add + norm         60.9 -> 58.4 / 60.3 / 63.5 / 64.0 / 63.3
 //   norm + add         44.9 -> 45.1 / 42.9 / 45.4 / 45.8 / 45.8
-//   norm + add + norm  61.3 -> 65.0 / 61.9 / 65.7 / 65.5 / 65.1 (keeps k_norm_rows)
+//   norm + add + norm  61.3 -> 65.0 / 61.9 / 65.7 / 65.5 / 65.1 (keeps k_norm_rows; with
+//                      two rows per step reduced stage by stage, 61.9 / 64.5 at 1 / 2)
 // Each mode has its own best count of rows in flight per CU; more or fewer are slower.
 #ifndef ZL_NORM_PIPE_WAVES
 #define ZL_NORM_PIPE_WAVES 16384
