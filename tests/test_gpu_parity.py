@@ -74,6 +74,34 @@ def test_embed_gather_bitexact(dev, oracle, qtype, dim, out_dtype):
         assert_bitexact(got, oracle.f32_to_bf16(ref), f"gather bf16-out qtype={qtype} dim={dim}")
 
 
+@pytest.mark.parametrize("out_dtype", [B.F32, B.BF16])
+@pytest.mark.parametrize("qtype", [B.Q8_0, B.Q4_0])
+@pytest.mark.parametrize("dim", [5376, 2560])
+def test_embed_gather_many_segments_bitexact(dev, oracle, qtype, dim, out_dtype):
+    """Prefill-sized gathers (4100 ids; a row of 5376 is 11 segments of f32 output, the last
+    partial, or 6 of bf16; one of 2560 is 5 or 3) over several rounds of waves, out-of-range
+    ids among them giving zero rows. Bit-exact against the oracle."""
+    vocab = 700
+    table = make_table(qtype, 4, vocab, dim)
+    ids = synth.gather_ids(4, 4096, vocab, n_repeat=64)
+    bad = np.array([-1, vocab, vocab + 77, -5], np.int32)
+    all_ids = np.concatenate([ids[:1000], bad, ids[1000:]])
+    ok = (all_ids >= 0) & (all_ids < vocab)
+    scale = np.float32(np.sqrt(np.float32(dim)))
+    ref = np.zeros((all_ids.size, dim), np.float32)
+    ref[ok] = oracle.embed_gather(table, qtype, all_ids[ok], dim, scale)
+    d_tab, d_ids = dev.from_numpy(table), dev.from_numpy(all_ids)
+    es = 4 if out_dtype == B.F32 else 2
+    d_out = dev.alloc(all_ids.size * dim * es)
+    d_out.fill(0xAB)
+    dev.embedGather(d_tab, qtype, vocab, d_ids, out_dtype, d_out, all_ids.size, dim, scale)
+    if out_dtype == B.F32:
+        assert_bitexact(d_out.to_numpy((all_ids.size, dim), np.float32), ref, f"gather qtype={qtype}")
+    else:
+        assert_bitexact(d_out.to_numpy((all_ids.size, dim), np.uint16), oracle.f32_to_bf16(ref),
+                        f"gather bf16-out qtype={qtype}")
+
+
 @pytest.mark.parametrize("qtype,offset", [(B.Q8_0, 1), (B.Q4_0, 1), (B.Q8_0, 2), (B.Q4_0, 6),
                                           (B.BF16, 2), (B.F16, 6), (B.F32, 4), (B.Q6_K, 8), (B.Q4_K, 1)])
 @pytest.mark.parametrize("out_dtype", [B.F32, B.BF16])

@@ -160,6 +160,9 @@ __host__ __device__ constexpr int seg_elems() {
 // consecutive 16-byte output chunks of one row (K * 256 f32 or K * 512 bf16 outputs) and
 // reads its row's id once. Measured at 4096 x 2560 -> f32 (us, K = 2 / 3 / 5 / 10): Q8_0
 // 10.2 / 10.5 / 11.0 / 12.2, Q4_0 8.66 / 8.83 / 9.2 / 8.95, BF16 12.3 / 12.3 / 12.1 / 12.2.
+// Not taken: a persistent grid whose waves walk segments with the next segment's table loads
+// and the id after it in flight (bit-equal): Q8_0 / Q4_0 10.28 / 8.71 -> 10.45 / 9.14 us at 8
+// workgroups per CU (2, 4, 6: slower still).
 #ifndef ZL_GATHER_STEPS
 #define ZL_GATHER_STEPS 2
 #endif
