@@ -8,7 +8,9 @@
 // covers 1 KiB of contiguous memory; all loads of a thread are issued before any math.
 // Elements that do not fill a whole chunk (n % E) are done by a scalar tail in block 0.
 // Launch shape measured on MI355X for bf16 GeGLU (2048 x 10240 / 8192 x 21504): 64 threads
-// and U = 1 take 20.2 / 155 us, against 22.1 / 169 us for 256 threads and U = 2.
+// and U = 1 take 20.2 / 155 us, against 22.1 / 169 us for 256 threads and U = 2, and against
+// 21.2-23.7 / 166-187 us for a persistent grid of one-wave workgroups walking blocks of 64 or
+// more chunks with the next block's loads in flight (4-32 waves per CU, 1-4 chunks per thread).
 //
 // GeGLU: out = gelu_tanh(gate) * up (math.zig:1119-1130) with the logistic form of GELU
 // (zl_common.h gelu_fast). SwiGLU: out = silu(gate) * up (math.zig:1108-1117, silu_fast).
