@@ -276,7 +276,10 @@ void hip_gemv_pro(int qtype, const void* weights, const void* up_weights /*NULL*
 void hip_gemv_qkv_pro(int qtype, const void* q_w, const void* k_w, const void* v_w, const float* x,
                       float* q_out, float* k_out, float* v_out, int q_rows, int k_rows, int v_rows,
                       int cols, const HipGemvPrologue* pro, HipStream_t stream);
-/* Y[b*rows + r] = W[r] . X[b*cols ...], b < batch_size (batch 1 is the GEMV). */
+/* Y[b*rows + r] = W[r] . X[b*cols ...], b < batch_size (batch 1 is the GEMV). y must not
+ * overlap x or the weights: deep products and small batches of long rows clear y and add two
+ * halves of each dot product into it (0 + a + b, the same bits in either order) while other
+ * workgroups still read x; y in device memory (float atomics). */
 void hip_gemm_q4_0(const void* weights, const float* x, float* y, int batch_size, int rows,
                    int cols, HipStream_t stream);                           /* cuda_bridge.h:47 */
 void hip_gemm_q8_0(const void* weights, const float* x, float* y, int batch_size, int rows,
