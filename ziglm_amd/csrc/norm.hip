@@ -403,7 +403,8 @@ __global__ __launch_bounds__(256) void k_norm_rows(NormArgs a) {
 // norm + add, against 29.7 / 58.5 / 42.9): a contiguous range of rows per workgroup 35.5 /
 // 67.3 / 50.3; default-policy loads 31.7 / 62.4 / 49.8; three row buffers (two rows in
 // flight) at the same workgroup counts 31.6 / 59.2 / 45.3, at one workgroup per CU 31.7 /
-// 59.6 / 42.8.
+// 59.6 / 42.8; two rows per step reduced stage by stage (one barrier per reduction for both)
+// 30.1 / 59.8 / 43.3 at the best of 1, 2 and the default workgroups per CU.
 template <typename T, int NC, int MODE>
 __global__ __launch_bounds__(256) void k_norm_pipe(NormArgs a) {
     using C = Chunk<T>;
