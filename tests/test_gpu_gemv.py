@@ -38,13 +38,14 @@ def run_gemm(dev, qtype, raw, X, rows, cols, batch):
     return d_y.to_numpy((batch, rows), np.float32)
 
 
-@pytest.mark.parametrize("qtype", QTYPES)
-@pytest.mark.parametrize("rows,cols,batch", [(37, 2560, 1), (16, 96, 1), (9, 10240, 1), (11, 512, 2),
-                                             (13, 2560, 3), (6, 256, 7), (65601, 256, 1), (65601, 768, 1),
-                                             (65537, 1280, 1)])
+_INT_SHAPES = [(37, 2560, 1), (16, 96, 1), (9, 10240, 1), (11, 512, 2), (13, 2560, 3), (6, 256, 7),
+               (65601, 256, 1), (65601, 768, 1), (65537, 1280, 1)]
+
+
+# super-block types take whole 256-column super-blocks (the 96-column shape is for the others)
+@pytest.mark.parametrize("qtype,rows,cols,batch", [(q, *sh) for q in QTYPES for sh in _INT_SHAPES
+                                                   if q not in K_QUANTS or sh[1] % 256 == 0])
 def test_gemv_integer_bitexact(dev, qtype, rows, cols, batch):
-    if qtype in K_QUANTS and cols % 256:
-        pytest.skip("super-block types need cols % 256 == 0")
     raw, wd = int_matrix(qtype, rows, cols, seed=rows * cols + qtype, scale_pow=-1)
     X = np.random.default_rng(rows).integers(-3, 4, (batch, cols)).astype(np.float32)
     exact = X.astype(np.float64) @ wd.T

@@ -148,13 +148,18 @@ def bound(wd, x):
     return np.abs(x).astype(np.float64) @ np.abs(wd).T * 2.0 ** -20
 
 
-@pytest.mark.parametrize("qtype", QTYPES)
-@pytest.mark.parametrize("cols", [32, 64, 96, 2560, 264])
+def _valid_cols(qtype, cols):
+    """Block types take whole 32-column blocks, super-block types whole 256-column ones."""
+    if qtype in (O.Q4_0, O.Q8_0):
+        return cols % 32 == 0
+    if qtype in (O.Q4_K, O.Q6_K):
+        return cols % 256 == 0
+    return True
+
+
+@pytest.mark.parametrize("qtype,cols", [(q, c) for q in QTYPES for c in (32, 64, 96, 2560, 264)
+                                        if _valid_cols(q, c)])
 def test_dot_integer_closed_form(o, qtype, cols):
-    if qtype in (O.Q4_0, O.Q8_0) and cols % 32:
-        pytest.skip("block types need cols % 32 == 0")
-    if qtype in (O.Q4_K, O.Q6_K) and cols % 256:
-        pytest.skip("super-block types need cols % 256 == 0")
     for p in (0, -1, 3):
         raw, wd = int_matrix(qtype, 5, cols, seed=cols + p + 100 * qtype, scale_pow=p)
         x = np.random.default_rng(cols).integers(-3, 4, cols).astype(np.float32)
