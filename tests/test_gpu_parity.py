@@ -351,13 +351,13 @@ def test_norm_modes_many_rows(dev, oracle, dtype, n, rows):
 @pytest.mark.parametrize("weighted", [True, False])
 def test_norm_pipelined_rows_equal_row_kernel(dev, oracle, dtype, n, weighted):
     """Launches of 16384 or more waves at four waves a row (4099 rows here) take the
-    persistent, pipelined row kernel for the norm, add + norm and norm + add modes, whose
+    persistent, pipelined row kernels (norm + add + norm its one-barrier-per-row form), whose
     workgroups walk several rows each (an odd count for some); the same rows in two launches
     under that size take the one-shot row kernel. Both do the same arithmetic in the same
     order, so every output is bit-equal between the two; the norm is also checked against the
     oracle. 4104 leaves part of each row's last chunk column empty, 8192 fills four chunks per
-    lane; no weight, and plain (not unit-offset) weights, take the other factor forms. add +
-    norm writes its output over the residual, as the reference's decode step does."""
+    lane; no weight takes the other factor form. add + norm writes its output over the
+    residual, as the reference's decode step does."""
     rows, split = 4099, 2050
     bf = dtype == B.BF16
     gen = synth.normal_bf16 if bf else synth.normal_f32
@@ -368,6 +368,7 @@ def test_norm_pipelined_rows_equal_row_kernel(dev, oracle, dtype, n, weighted):
     w = synth.normal_f32(21, "w", (n,), 0, 0.1) if weighted else None
     uo = weighted  # weighted: (1 + w); otherwise no weight at all
     d_w = dev.from_numpy(w) if weighted else None
+    d_w2 = dev.from_numpy(synth.normal_f32(21, "w2", (n,), 0, 0.1)) if weighted else None
 
     def both(run):
         """run(x_view, r_view, out_view, rows) over all rows at once, then in two launches."""
@@ -394,6 +395,9 @@ def test_norm_pipelined_rows_equal_row_kernel(dev, oracle, dtype, n, weighted):
         assert_rel(o, oracle.rms_norm(x, w, EPS, uo), 1e-5, what="norm")
     both(lambda dx, dr, do, cnt: dev.addRmsNormRows(dtype, dx, dr, d_w, dr, cnt, n, EPS, uo))
     both(lambda dx, dr, do, cnt: dev.rmsnormAddRows(dtype, dx, dr, d_w, cnt, n, EPS, uo))
+    # norm + add + norm, its output over its input r (the reference's fused call does that)
+    both(lambda dx, dr, do, cnt: dev.rmsNormAddRmsNorm(dtype, dx, dr, d_w, d_w2, dr, cnt, n, EPS, uo))
+    both(lambda dx, dr, do, cnt: dev.rmsNormAddRmsNorm(dtype, dx, dr, d_w, d_w2, do, cnt, n, EPS, uo))
 
 
 # ---------------------------------------------------------------------------------------

@@ -550,6 +550,148 @@ __global__ __launch_bounds__(256) void k_norm_pipe(NormArgs a) {
     }
 }
 
+// NORM_ADD_NORM in the persistent, pipelined form with one barrier per row: row q's first
+// statistic and the pending row p's second statistic (p the row before q in this
+// workgroup's walk) are exchanged behind the same barrier, then p is stored and q's sum s =
+// x + norm1(r) formed, whose second statistic waits for the next row. Same arithmetic, in
+// the same order, as k_norm_rows.
+template <typename T, int NC>
+__global__ __launch_bounds__(256) void k_norm_pipe_nan(NormArgs a) {
+    using C = Chunk<T>;
+    constexpr int E = C::E;
+    constexpr int W = 4;
+    constexpr int STRIDE = kWave * W;
+    constexpr int LP = ZL_NORM_LP, SP = ZL_NORM_SP;
+    __shared__ float s_red[2][2][W];  // [parity][row p / row q][wave]
+    const int g = threadIdx.x;
+    const int n = a.n;
+    const int nch = n / E;
+    const uint32_t row_bytes = (uint32_t)n * sizeof(T);
+    const bool has_w1 = a.w1 != nullptr;
+    const bool has_w2 = a.w2 != nullptr;
+    const int64_t end = a.rows;
+    const int64_t step = gridDim.x;
+
+    u32x4 bx[2][NC], br[2][NC];
+    auto issue = [&](auto B, int64_t row) {
+        constexpr int b = decltype(B)::value;
+        const bool ok = row < end;
+        const int64_t rr = ok ? row : 0;
+        const auto rsx = buf_rsrc((const T*)a.x + rr * n, ok ? row_bytes : 0u);
+        const auto rsr = buf_rsrc((const T*)a.r + rr * n, ok ? row_bytes : 0u);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const uint32_t off = (uint32_t)(g + c * STRIDE) * 16u;
+            bx[b][c] = bldp<LP>(rsx, off);
+            br[b][c] = bldp<LP>(rsr, off);
+        }
+    };
+    float f1[NC][E], f2[NC][E];
+    float sv[NC][E];  // s = x + norm1(r) of the pending row
+    float ss2 = 0.0f;  // its second statistic, this lane's part
+    // this lane's part of row q's first statistic (buffer B)
+    auto first_sum = [&](auto B) -> float {
+        constexpr int b = decltype(B)::value;
+        float ss = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            if (g + c * STRIDE < nch) {
+                float v[E];
+                C::unpack(br[b][c], v);
+#pragma unroll
+                for (int j = 0; j < E; ++j) ss = fmaf(v[j], v[j], ss);
+            }
+        }
+        return ss;
+    };
+    // s of row q (buffer B) with inv1, and this lane's part of its second statistic
+    auto form_s = [&](auto B, float inv) {
+        constexpr int b = decltype(B)::value;
+        ss2 = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            if (g + c * STRIDE < nch) {
+                float xv[E], v[E];
+                C::unpack(bx[b][c], xv);
+                C::unpack(br[b][c], v);
+#pragma unroll
+                for (int j = 0; j < E; ++j) {
+                    sv[c][j] = xv[j] + (v[j] * inv) * w_factor(f1[c][j], has_w1, a.uo);
+                    ss2 = fmaf(sv[c][j], sv[c][j], ss2);
+                }
+            }
+        }
+    };
+    auto store_p = [&](int64_t row, float inv2) {
+        T* const xrow = (T*)a.x + row * n;
+        T* const orow = (T*)a.out + row * n;
+        const auto wsx = buf_rsrc(xrow, row_bytes);
+        const auto wso = buf_rsrc(orow, row_bytes);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const int idx = g + c * STRIDE;
+            if (idx < nch) {
+                float y[E];
+#pragma unroll
+                for (int j = 0; j < E; ++j) y[j] = (sv[c][j] * inv2) * w_factor(f2[c][j], has_w2, a.uo);
+                strow16<SP>(xrow, wsx, (uint32_t)idx * 16u, C::pack(sv[c]));
+                strow16<SP>(orow, wso, (uint32_t)idx * 16u, C::pack(y));
+            }
+        }
+    };
+    // one iteration: pending row p (sv, ss2), row q = p + step in buffer B, the other
+    // buffer free; slots of parity P
+    auto iter = [&](auto B, auto Bo, int64_t p, int P) {
+        constexpr int b = decltype(B)::value;
+        const int64_t q = p + step;
+        issue(Bo, q + step);
+        float two[2] = {ss2, first_sum(B)};
+        float* const slots[2] = {s_red[P][0], s_red[P][1]};
+        row_sums<W, 2>(two, slots);
+        const float inv2 = rms_inv_hw(two[0], n, a.eps);
+        const float inv1 = rms_inv_hw(two[1], n, a.eps);
+        store_p(p, inv2);
+        form_s(B, inv1);
+        (void)b;
+    };
+
+    constexpr std::integral_constant<int, 0> B0{};
+    constexpr std::integral_constant<int, 1> B1{};
+    int64_t p = blockIdx.x;
+    if (p >= end) return;  // block-uniform
+    issue(B0, p);
+    {
+        const auto rsw1 = buf_rsrc(a.w1, has_w1 ? (uint32_t)n * 4u : 0u);
+        const auto rsw2 = buf_rsrc(a.w2, has_w2 ? (uint32_t)n * 4u : 0u);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) load_wb<E>(rsw1, (uint32_t)(g + c * STRIDE) * E * 4u, f1[c]);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) load_wb<E>(rsw2, (uint32_t)(g + c * STRIDE) * E * 4u, f2[c]);
+    }
+    issue(B1, p + step);
+    // the first row's first statistic alone
+    {
+        float one = first_sum(B0);
+        one = row_sum<W>(one, s_red[1][0]);
+        form_s(B0, rms_inv_hw(one, n, a.eps));
+    }
+    // pending p; row p + step in B1, B0 free
+    int P = 0;
+    while (true) {
+        if (p + step >= end) break;
+        iter(B1, B0, p, P);
+        p += step;
+        P ^= 1;
+        if (p + step >= end) break;
+        iter(B0, B1, p, P);
+        p += step;
+        P ^= 1;
+    }
+    // the last pending row's second statistic alone
+    const float last = row_sum<W>(ss2, s_red[P][0]);
+    store_p(p, rms_inv_hw(last, n, a.eps));
+}
+
 // ---- block-per-row fallback: any n, any alignment ------------------------------------------
 
 template <typename T>
@@ -662,8 +804,10 @@ static void launch_w(const NormArgs& a, int per_lane, int R, hipStream_t s) {
 //   input norm         31.6 -> 37.3 / 30.5 / 29.7 / 30.8 / 31.7
 //   add + norm         60.9 -> 58.4 / 60.3 / 63.5 / 64.0 / 63.3
 //   norm + add         44.9 -> 45.1 / 42.9 / 45.4 / 45.8 / 45.8
-//   norm + add + norm  61.3 -> 65.0 / 61.9 / 65.7 / 65.5 / 65.1 (keeps k_norm_rows; with
-//                      two rows per step reduced stage by stage, 61.9 / 64.5 at 1 / 2)
+//   norm + add + norm  61.3 -> 65.0 / 61.9 / 65.7 / 65.5 / 65.1 (two barriers per row; with
+//                      two rows per step reduced stage by stage, 61.9 / 64.5 at 1 / 2);
+//                      k_norm_pipe_nan (one barrier per row) 61.1-61.4 -> 59.9-60.2 / 63.1-63.7
+//                      at 1 / 2, so one workgroup per CU
 // Each mode has its own best count of rows in flight per CU; more or fewer are slower.
 #ifndef ZL_NORM_PIPE_WAVES
 #define ZL_NORM_PIPE_WAVES 16384
@@ -672,13 +816,16 @@ static void launch_w(const NormArgs& a, int per_lane, int R, hipStream_t s) {
 #ifndef ZL_NORM_PIPE_WG
 #define ZL_NORM_PIPE_WG 0
 #endif
+#ifndef ZL_NORM_PIPE_NAN_WG
+#define ZL_NORM_PIPE_NAN_WG 1
+#endif
 template <int MODE>
 constexpr int pipe_wgs_per_cu() {
     return ZL_NORM_PIPE_WG ? ZL_NORM_PIPE_WG
            : MODE == M_NORM ? 3
            : MODE == M_ADD_NORM ? 1
            : MODE == M_NORM_ADD ? 2
-                                : 0;
+                                : ZL_NORM_PIPE_NAN_WG;
 }
 // false: this mode keeps k_norm_rows
 template <typename T, int MODE>
@@ -688,6 +835,13 @@ static bool launch_pipe(const NormArgs& a, int per_lane, hipStream_t s) {
         return false;
     } else {
         const unsigned grid = (unsigned)std::min<int64_t>(a.rows, (int64_t)device_cus() * wg);
+        if constexpr (MODE == M_NORM_ADD_NORM) {
+            if (per_lane <= 1) k_norm_pipe_nan<T, 1><<<grid, 256, 0, s>>>(a);
+            else if (per_lane <= 2) k_norm_pipe_nan<T, 2><<<grid, 256, 0, s>>>(a);
+            else if (per_lane <= 3) k_norm_pipe_nan<T, 3><<<grid, 256, 0, s>>>(a);
+            else k_norm_pipe_nan<T, 4><<<grid, 256, 0, s>>>(a);
+            return true;
+        }
         if (per_lane <= 1) k_norm_pipe<T, 1, MODE><<<grid, 256, 0, s>>>(a);
         else if (per_lane <= 2) k_norm_pipe<T, 2, MODE><<<grid, 256, 0, s>>>(a);
         else if (per_lane <= 3) k_norm_pipe<T, 3, MODE><<<grid, 256, 0, s>>>(a);
