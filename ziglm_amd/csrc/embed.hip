@@ -159,7 +159,8 @@ __host__ __device__ constexpr int seg_elems() {
 // Steps per wave of the Q8_0 / Q4_0 (K_Q) and dense (K_D) gathers: a wave takes K * 64
 // consecutive 16-byte output chunks of one row (K * 256 f32 or K * 512 bf16 outputs) and
 // reads its row's id once. Measured at 4096 x 2560 -> f32 (us, K = 2 / 3 / 5 / 10): Q8_0
-// 10.2 / 10.5 / 11.0 / 12.2, Q4_0 8.66 / 8.83 / 9.2 / 8.95, BF16 12.3 / 12.3 / 12.1 / 12.2.
+// 10.2 / 10.5 / 11.0 / 12.2, Q4_0 8.66 / 8.83 / 9.2 / 8.95, BF16 12.3 / 12.3 / 12.1 / 12.2;
+// K = 1 and 4 retaken later against 10.3 / 8.7 for K = 2: Q8_0 17.5 / 11.1, Q4_0 16.6 / 8.9.
 // Not taken: a persistent grid whose waves walk segments with the next segment's table loads
 // and the id after it in flight (bit-equal): Q8_0 / Q4_0 10.28 / 8.71 -> 10.45 / 9.14 us at 8
 // workgroups per CU (2, 4, 6: slower still).
