@@ -18,7 +18,9 @@
 // shared by all rows, L2-resident) are loaded as 128-bit vectors up front and turned into
 // per-element factors (1+w), w or 1. Rows that are not 16-byte aligned, or longer than 16
 // chunks per lane (f32 > 16384, bf16 > 32768 elements), use a block-per-row kernel that
-// re-reads the row from L2.
+// re-reads the row from L2. Launches of many rounds of 4-wave rows (prefill at 8192 tokens)
+// run persistent workgroups that walk the rows with the next row's loads in flight
+// (k_norm_pipe; k_norm_pipe_nan for NORM_ADD_NORM), with the same arithmetic.
 // Aliasing: out may alias r (the reference calls addRmsNorm(x, xb, w, out=xb)) or x in
 // NORM mode; every lane reads its chunks before writing the same chunks.
 #include "zl_common.h"
